@@ -1,0 +1,200 @@
+"""Benchmark of libtempest_hip on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+The headline workload is config 2 of BASELINE.json, the one the metric's
+"GB/s fused reduce" is quoted on: two compiled programs over X, G of
+32768 x 8192 fp32 (the reference's 8192 x 32768 column-major arrays):
+sum(softmax_columns(X) .* G) and sum(layernorm(X) .* G), each with its
+gradient w.r.t. X.  A step replays both programs' captured graphs once.
+``value`` = algorithmic bytes per step (read X, read G, write dX for each
+program: 6 x 2^30 bytes) / seconds per step, inputs resident in HBM.
+
+The same JSON line carries the roofline of the dominant kernel (timed with
+events on the stream it runs on, inside the timed region), the CPU baseline
+(the oracle's single-threaded Float32 floor on a stated sample of rows) and
+the other configs' figures measured in the same run.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "tempest.jl_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+BF16_PEAK = 2.5e15         # MI355X dense bf16 MFMA, flop/s
+ROWS, N = 32768, 8192
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def config2(target, steps: int, warmup: int):
+    import torch
+    import tempest_hip as th
+
+    gen = torch.Generator(device="cuda").manual_seed(20261201)
+    x = torch.randn(ROWS, N, device="cuda", generator=gen)
+    g = torch.randn(ROWS, N, device="cuda", generator=gen)
+    cs = th.compile(th.programs.softmax_columns(ROWS, N), target, x, g)
+    cl = th.compile(th.programs.layernorm(ROWS, N), target, x, g)
+    es, el = cs.executable, cl.executable
+    for _ in range(warmup):
+        es.replay()
+        el.replay()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e in ev:
+        e[0].record()
+        es.replay()
+        e[1].record()
+        el.replay()
+        e[2].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    s_soft = sum(e[0].elapsed_time(e[1]) for e in ev) / steps * 1e-3
+    s_ln = sum(e[1].elapsed_time(e[2]) for e in ev) / steps * 1e-3
+    step_s = (t1 - t0) / steps
+    bytes_soft, _ = es.work()
+    bytes_ln, _ = el.work()
+    # Algorithmic bytes: X, G read and dX written per program (the loss's
+    # per-row partials are 1/8192 of that and counted in work() too).
+    alg = 3.0 * 4 * ROWS * N
+    # A quick parity check on sampled rows (outside the timed region).
+    parity = {}
+    try:
+        from oracle import interpret
+        from oracle.data import relative
+        idx = torch.tensor([0, 777, 16384, ROWS - 1], device="cuda")
+        xs, gs = x.index_select(0, idx).cpu().numpy(), g.index_select(0, idx).cpu().numpy()
+        for name, ex, f in (("softmax", es, interpret.softmax_grad), ("layernorm", el, interpret.layernorm_grad)):
+            _, dx = ex.outputs()
+            parity[name] = relative(dx.index_select(0, idx).cpu().numpy(), f(xs, gs)[1])
+    except Exception as err:  # the bench's number stands without it
+        parity["error"] = repr(err)
+    return dict(x=x, g=g, step_s=step_s, s_soft=s_soft, s_ln=s_ln, alg=alg, bytes_soft=bytes_soft,
+                bytes_ln=bytes_ln, parity=parity, describe=es.explain() + "\n" + el.explain())
+
+
+def cpu_baseline(x, g, budget_s: float = 10.0):
+    """The oracle's Float32 floor (oracle/floor.c, one thread) on the first
+    rows of the same X, G, 1024 rows at a time, both programs, until the
+    budget is spent or 16384 rows are done."""
+    import numpy as np
+    from oracle import floor
+
+    done = 0
+    spent = 0.0
+    chunk = 1024
+    while spent < budget_s and done < 16384:
+        xs = x[done:done + chunk].cpu().numpy()
+        gs = g[done:done + chunk].cpu().numpy()
+        t = time.perf_counter()
+        floor.softmax_grad(xs, gs)
+        floor.layernorm_grad(xs, gs)
+        spent += time.perf_counter() - t
+        done += chunk
+    rate = 2 * 3.0 * 4 * done * N / spent / 1e9
+    return {"value": rate, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/floor.c (the reference's CPU floor restated in C, -O2, 1 thread): both programs "
+                      f"on the first {done} of {ROWS} rows ({spent:.1f} s)",
+            "seconds_full_step_extrapolated": spent * ROWS / done}
+
+
+def config1(target):
+    import torch
+    import tempest_hip as th
+
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    w = torch.randn(64, 32, device="cuda", generator=gen)   # Julia w 32 x 64
+    b = torch.randn(64, device="cuda", generator=gen)
+    x = torch.randn(16, 32, device="cuda", generator=gen)   # Julia x 32 x 16
+    comp = th.compile(th.programs.tanh_layer(), target, w, b, x)
+    ex = comp.executable
+    graph_s = target.time_graph(ex.graph, warmup=20, reps=2000)
+    launch = ex.launches[0]
+    execute_s = target.time_run(launch, warmup=20, reps=2000)
+    for _ in range(50):
+        comp(w, b, x)
+    torch.cuda.synchronize()
+    n = 500
+    t = time.perf_counter()
+    for _ in range(n):
+        comp(w, b, x)  # point, replay, copy dw/db/dx, read the loss
+    call_s = (time.perf_counter() - t) / n
+    return {"us_per_step_graph": graph_s * 1e6, "us_per_step_execute": execute_s * 1e6,
+            "us_per_compiled_call_host": call_s * 1e6,
+            "note": "graph/execute: device time per step from events around 2000 back-to-back replays/runs; "
+                    "compiled call: host wall time of c(w, b, x) incl. result copies and the loss read"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
+              "the per-GPU share shards by rows with no exchange.", file=sys.stderr)
+        return 2
+    import torch
+    import tempest_hip as th
+
+    target = th.HIPTarget()
+    log("device:", target.device_name())
+    c2 = config2(target, a.steps, a.warmup)
+    log(c2["describe"])
+    step_s = c2["step_s"]
+    value = 2 * c2["alg"] / step_s / 1e9
+    dominant = ("softmax_grad_resident", c2["s_soft"]) if c2["s_soft"] >= c2["s_ln"] else \
+        ("layernorm_grad_resident", c2["s_ln"])
+    achieved = c2["alg"] / dominant[1]
+    traffic = None
+    tf = ROOT / "profiles" / "traffic_config2.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get(dominant[0])
+    roofline = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK, "traffic": traffic, "kernel": dominant[0],
+                "kernel_us": dominant[1] * 1e6,
+                "per_kernel": {"softmax_grad": {"us": c2["s_soft"] * 1e6, "GB/s": c2["alg"] / c2["s_soft"] / 1e9},
+                               "layernorm_grad": {"us": c2["s_ln"] * 1e6, "GB/s": c2["alg"] / c2["s_ln"] / 1e9}},
+                "note": "per-program events bracket the fused row kernel and the loss's one-block sum"}
+    configs = {"config2_parity_rel": c2["parity"]}
+    try:
+        configs["config1_tanh_layer"] = config1(target)
+    except Exception as err:
+        configs["config1_tanh_layer"] = {"error": repr(err)}
+    cpu = None
+    if not a.no_cpu:
+        try:
+            cpu = cpu_baseline(c2["x"], c2["g"])
+        except Exception as err:
+            cpu = {"error": repr(err)}
+    line = {
+        "metric": "GB/s fused reduce (config 2: softmax and LayerNorm fwd+grad over X 32768x8192 fp32)",
+        "value": value, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (torch Philox N(0,1) on device, seed 20261201)",
+        "config": {"workload": "config2: sum(softmax_columns(X).*G) and sum(layernorm(X).*G), withgradient, "
+                               "X,G 8192x32768 column-major fp32", "rows": ROWS, "n": N,
+                   "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu, "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,227 @@
+/*
+ * libtempest_hip — the C ABI of Tempest's MI355X (gfx950) execution backend.
+ *
+ * One process drives one GPU.  Every entry point returns an int status:
+ * TH_OK (0) on success, otherwise a TH_E_* code or a positive hipError_t;
+ * th_last_error() then holds a message for the calling thread.  Pointers are
+ * device addresses unless the name says host.  Arrays are the reference's
+ * dense column-major layout (first axis fastest, src/Compiler/IR/layout.jl:1-3);
+ * "rows" below are therefore the reference's columns: a reduction over
+ * `dims = 1` of an n x rows array is a reduction over contiguous runs of n.
+ *
+ * Each declaration names the reference interface it replaces (paths are
+ * relative to the Tempest.jl source tree).  A Julia extension binds these by
+ * `ccall`; the host mirror in tempest.jl_amd/tempest_hip binds them by ctypes.
+ */
+#ifndef TEMPEST_HIP_H
+#define TEMPEST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TH_OK = 0,
+  TH_E_ARGUMENT = -1,     /* shapes, strides or alignment a kernel cannot take */
+  TH_E_STATE = -2,        /* no th_init, or a handle used after release        */
+  TH_E_UNSUPPORTED = -3,  /* a case this build does not implement              */
+  TH_E_MEMORY = -4        /* an allocation failed                              */
+};
+
+typedef struct th_launch th_launch; /* one claim's built launch: kernels + arguments */
+typedef struct th_graph th_graph;   /* a captured run of launches                   */
+typedef struct th_arena th_arena;   /* the slot arena: one device slab              */
+
+/* Device rates as the cover prices them.
+ * Replaces device_rates(::CUDATarget), ext/CUDAExt.jl:913-921. */
+typedef struct th_rates {
+  double launch;    /* seconds between launches inside a replayed graph      */
+  double cached;    /* bytes/s for a launch whose data the caches hold       */
+  double bandwidth; /* bytes/s from HBM (memory clock x bus width)           */
+  double cache;     /* bytes of last-level cache (L2 + MALL)                 */
+  double blocks;    /* workgroups that fill the device (CUs)                 */
+} th_rates;
+
+/* Algorithmic work of one launch, as Implement.Work states it
+ * (src/Compiler/Implement/Implement.jl:61-82): the bytes a launch must move
+ * and the flops it must do, whatever its tiling. */
+typedef struct th_work {
+  double bytes;
+  double flops;
+  int64_t blocks;    /* workgroups launched by the dominant kernel */
+  int32_t kernels;   /* kernels in the launch                      */
+  int32_t values;    /* repointable values (see th_launch_repoint) */
+} th_work;
+
+/* ---- errors, device, streams ------------------------------------------- */
+
+/* The last failure's message on this thread; "" when none. */
+const char* th_last_error(void);
+
+/* Make `device` current and create the library's stream on it.
+ * Replaces task_state/on_device(::CUDATarget), ext/CUDAExt.jl:18-22,44-48. */
+int th_init(int device);
+
+/* Wait for the device and release the library's stream and helpers. */
+int th_shutdown(void);
+
+/* The device's marketing name and gfx arch, e.g. "AMD Instinct MI355X (gfx950)".
+ * Replaces device_name(target), src/Compiler/runtime/target.jl:583-584. */
+int th_device_name(char* host_out, size_t capacity);
+
+/* "hip=<runtime version>;clang=<compiler>;arch=gfx950".
+ * Replaces toolchain(target), src/Compiler/runtime/target.jl:594. */
+int th_toolchain(char* host_out, size_t capacity);
+
+/* Replaces device_rates(::CUDATarget), ext/CUDAExt.jl:906-921. */
+int th_device_rates(th_rates* host_out);
+
+/* Run the library's launches on `stream`, a hipStream_t (NULL is the null
+ * stream).  th_init starts on a non-blocking stream of the library's own,
+ * which th_get_stream returns until another is set.
+ * Replaces stream/task_stream(::CUDATarget), ext/CUDAExt.jl:326-337. */
+int th_set_stream(void* stream);
+int th_get_stream(void** host_out);
+
+/* Wait until the stream has run everything launched on it.
+ * Replaces quiesce(target[, stream]), src/Compiler/runtime/target.jl:493,617. */
+int th_quiesce(void);
+
+/* ---- storage --------------------------------------------------------------- */
+
+/* A device buffer of `bytes`, 256-byte aligned.
+ * Replaces allocate(::CUDATarget, T, n), ext/CUDAExt.jl:23. */
+int th_alloc(size_t bytes, void** host_out);
+int th_free(void* ptr);
+
+/* Host -> device, device -> host and device -> device copies on the stream;
+ * th_download waits for its copy.  Replace upload!/download!
+ * (src/Compiler/runtime/target.jl:258,267; ext/CUDAExt.jl:31-34) and the
+ * runtime's Copy (src/Compiler/runtime/runtime.jl:47-64). */
+int th_upload(void* dst, const void* host_src, size_t bytes);
+int th_download(void* host_dst, const void* src, size_t bytes);
+int th_copy(void* dst, const void* src, size_t bytes);
+
+/* The slot arena: `n` slots of `sizes[i]` bytes laid out in one hipMalloc
+ * slab, each at a multiple of `align` (>= 256, a power of two).  Replaces the
+ * per-slot allocate of `planned`, src/Compiler/runtime/runtime.jl:415, fed by
+ * the planner's Storage.sizes (src/Compiler/plan/storage.jl:37-46). */
+int th_arena_create(const uint64_t* host_sizes, int n, uint64_t align, th_arena** host_out);
+int th_arena_slot(th_arena* arena, int slot, void** host_out);
+int th_arena_bytes(th_arena* arena, uint64_t* host_out);
+int th_arena_destroy(th_arena* arena);
+
+/* ---- launches ---------------------------------------------------------- */
+
+/* Run a launch's kernels on the stream, in order: a step of `execute!`.
+ * Replaces (l::FloorLaunch)(), ext/CUDAExt.jl:1092-1098, and the claims'
+ * launch calls (src/Compiler/runtime/schedule.jl:131-136). */
+int th_launch_run(th_launch* launch);
+
+/* Point value `value` of a launch at `ptr`, as its builder numbered the
+ * values.  Replaces Implement.repoint!(launch, value, buffer),
+ * src/Compiler/Implement/Implement.jl (repoint!), ext/CUDAExt.jl:1086-1090. */
+int th_launch_repoint(th_launch* launch, int value, void* ptr);
+
+/* The launch's algorithmic work.  Feeds Implement.estimate,
+ * src/Compiler/Implement/Implement.jl:61-82. */
+int th_launch_work(th_launch* launch, th_work* host_out);
+
+/* A one-line description (kernel names and grids), as build_claim's
+ * description string (src/Compiler/Implement/Implement.jl, build_claim). */
+int th_launch_describe(th_launch* launch, char* host_out, size_t capacity);
+
+int th_launch_destroy(th_launch* launch);
+
+/* ---- graphs ------------------------------------------------------------ */
+
+/* Record `n` launches, in order, as one graph of kernel nodes.
+ * Replaces capture(::CUDATarget, steps, keep), ext/CUDAExt.jl:515-572. */
+int th_graph_capture(th_launch* const* host_steps, int n, th_graph** host_out);
+
+/* Launch the graph on the stream.  Replaces replay(::CUDATarget, graph),
+ * ext/CUDAExt.jl:739. */
+int th_graph_replay(th_graph* graph);
+
+/* Make the graph read what step `step`'s launch now reads, after
+ * th_launch_repoint moved its values: the step's kernel nodes take the
+ * launch's current arguments in place.  Replaces retarget!(::CUDATarget,
+ * graph, steps, moves, repoint) and patch!, ext/CUDAExt.jl:604-668. */
+int th_graph_retarget(th_graph* graph, int step);
+
+/* Replaces release(::CUDATarget, graph), ext/CUDAExt.jl:743. */
+int th_graph_release(th_graph* graph);
+
+/* ---- measuring --------------------------------------------------------- */
+
+/* Device seconds of one run of `launch` replayed alone as a graph after the
+ * caches are cleared (a read of 2 x (L2 + MALL)), the minimum over `samples`
+ * (0 = chosen as the reference does), less what replaying one graph adds.
+ * Replaces time_launch/timed_launch/cleared/replay_overhead,
+ * ext/CUDAExt.jl:760-882. */
+int th_time_launch(th_launch* launch, int samples, double* host_seconds);
+
+/* Mean device seconds of one replay of `graph`, `reps` replays back to back
+ * between two events (warm caches), after `warmup` replays.  Replaces
+ * batched(target, launch), ext/CUDAExt.jl:886-898. */
+int th_time_graph(th_graph* graph, int warmup, int reps, double* host_seconds);
+
+/* Mean device seconds of one run of `launch` (warm), as th_time_graph. */
+int th_time_run(th_launch* launch, int warmup, int reps, double* host_seconds);
+
+/* ---- op class (a): fused pointwise + reductions -------------------------- */
+
+/* Softmax over each contiguous run of n (a column of the reference's n x rows
+ * array) and its gradient, one program:
+ *   y = exp.(x .- logsumexp(x; dims = 1)),  loss = sum(y .* g),
+ *   dx = y .* (g .- sum(y .* g; dims = 1)).
+ * Inputs x, g (rows x ld floats, ld >= n); outputs dx (same layout) and
+ * loss (one float).  The fold is the reference's online softmax
+ * (Relative{Exponential}, src/Compiler/IR/folds.jl:119-222) run resident in
+ * registers, as the cuTile resident sketch (ext/cuTileExt/build.jl:138,
+ * ext/cuTileExt/cuTileExt.jl:638-672).  Values: 0 x, 1 g, 2 dx, 3 loss.
+ * The program is test/fixtures/programs.jl:8,74 differentiated. */
+int th_build_softmax_grad(int64_t rows, int32_t n, int64_t ld,
+                          const float* x, const float* g, float* dx, float* loss,
+                          th_launch** host_out);
+
+/* LayerNorm (weight 1, bias 0) over each contiguous run of n and its
+ * gradient: y = (x .- m) ./ sqrt.(v .+ eps) with m, v the run's mean and
+ * mean square deviation (two passes, test/fixtures/programs.jl:13-17),
+ * loss = sum(y .* g), dx = r .* (g .- mean(g) .- y .* mean(g .* y)),
+ * r = 1/sqrt(v + eps).  Values: 0 x, 1 g, 2 dx, 3 loss. */
+int th_build_layernorm_grad(int64_t rows, int32_t n, int64_t ld, float eps,
+                            const float* x, const float* g, float* dx, float* loss,
+                            th_launch** host_out);
+
+/* Forward only: y = softmax(x; dims = 1) (values 0 x, 1 y) and
+ * y = layernorm(x) (values 0 x, 1 y), over rows runs of n at stride ld. */
+int th_build_softmax_fwd(int64_t rows, int32_t n, int64_t ld, const float* x, float* y,
+                         th_launch** host_out);
+int th_build_layernorm_fwd(int64_t rows, int32_t n, int64_t ld, float eps, const float* x,
+                           float* y, th_launch** host_out);
+
+/* The sum of `count` floats into one (a full reduction, the cuTile `:full`
+ * sketch, ext/cuTileExt/cuTileExt.jl:638-641): values 0 x, 1 out. */
+int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out);
+
+/* ---- the small program of config 1 -------------------------------------- */
+
+/* loss(w, b, x) = sum(abs2, tanh.(w' * x .+ b)) and its gradient, one fused
+ * kernel in one workgroup: w is d x h, b h, x d x c (Float32, column-major);
+ * outputs loss (1), dw (d x h), db (h), dx (d x c).  d*h + d*c + 2*h*c
+ * floats must fit the workgroup's 64 KiB of LDS (with 16 floats of its own).
+ * Values: 0 w, 1 b, 2 x, 3 loss, 4 dw, 5 db, 6 dx. */
+int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c,
+                             const float* w, const float* b, const float* x,
+                             float* loss, float* dw, float* db, float* dx,
+                             th_launch** host_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEMPEST_HIP_H */

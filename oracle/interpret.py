@@ -1,0 +1,84 @@
+"""TEST INFRASTRUCTURE ONLY: Float64 meaning of the hot path's programs.
+
+Restates what src/Compiler/program/interpret.jl computes for each program
+when fed Float64 (plan-free, products by matrix multiply, half factors
+widened and the result rounded once, interpret.jl:58-63).  Arrays are numpy
+in the memory order the kernels see.  For the row programs an array of
+shape (rows, n), C order, is the reference's n x rows column-major array:
+each numpy row is one of the reference's columns, the axis dims = 1 folds.
+
+Pinning (tests/test_oracle_*.py):
+- softmax_grad, layernorm_grad, softmax_fwd, layernorm_fwd: central finite
+  differences of the loss in float64, torch CPU autograd (a library
+  routine), invariants (a softmax column sums to 1; its gradient's column
+  sums are 0; a LayerNorm column has mean 0, mean square v/(v+eps); its
+  gradient is orthogonal to 1 and to y).
+- tanh_layer_grad: closed form z = w'x + b (config 1), finite differences,
+  torch autograd, and the reference's own doctest sum(abs2, [1,2,3,4]) = 30.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def _f64(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float64)
+
+
+def logsumexp_rows(x: np.ndarray) -> np.ndarray:
+    """LOGSUMEXP over each row, shifted by lse_shift (folds.jl:194, 263)."""
+    x = _f64(x)
+    m = x.max(axis=1, keepdims=True)
+    sh = np.where(np.isfinite(m), m, 0.0)
+    with np.errstate(divide="ignore"):
+        return (sh + np.log(np.exp(x - sh).sum(axis=1, keepdims=True)))
+
+
+def softmax_fwd(x: np.ndarray) -> np.ndarray:
+    """softmax_columns(x) = exp.(x .- logsumexp(x; dims = 1)) (test/fixtures/programs.jl:8)."""
+    x = _f64(x)
+    return np.exp(x - logsumexp_rows(x))
+
+
+def softmax_grad(x: np.ndarray, g: np.ndarray):
+    """loss = sum(softmax_columns(x) .* g) and d loss / d x (programs.jl:74)."""
+    y = softmax_fwd(x)
+    g = _f64(g)
+    dot = (y * g).sum(axis=1, keepdims=True)
+    return float(dot.sum()), y * (g - dot)
+
+
+def layernorm_fwd(x: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """layernorm(x, 1) (test/fixtures/programs.jl:13-17): two passes, weight 1, bias 0."""
+    x = _f64(x)
+    n = x.shape[1]
+    m = x.sum(axis=1, keepdims=True) / n
+    v = ((x - m) ** 2).sum(axis=1, keepdims=True) / n
+    return (x - m) / np.sqrt(v + eps)
+
+
+def layernorm_grad(x: np.ndarray, g: np.ndarray, eps: float = 1e-5):
+    """loss = sum(layernorm(x) .* g) and d loss / d x."""
+    x = _f64(x)
+    g = _f64(g)
+    n = x.shape[1]
+    m = x.sum(axis=1, keepdims=True) / n
+    v = ((x - m) ** 2).sum(axis=1, keepdims=True) / n
+    r = 1.0 / np.sqrt(v + eps)
+    y = (x - m) * r
+    gy = (g * y).sum(axis=1, keepdims=True)
+    dx = r * (g - g.mean(axis=1, keepdims=True) - y * gy / n)
+    return float(gy.sum()), dx
+
+
+def tanh_layer_grad(w: np.ndarray, b: np.ndarray, x: np.ndarray):
+    """Config 1: loss(w, b, x) = sum(abs2, tanh.(w' * x .+ b)) and (dw, db, dx).
+
+    w is d x h, b h, x d x c as Julia matrices (numpy arrays indexed [i, j]
+    the way Julia indexes them; memory order does not matter here)."""
+    w, b, x = _f64(w), _f64(b), _f64(x)
+    z = w.T @ x + b[:, None]
+    y = np.tanh(z)
+    loss = float((y * y).sum())
+    dz = 2.0 * y * (1.0 - y * y)
+    return loss, x @ dz.T, dz.sum(axis=1), w @ dz

@@ -1,0 +1,583 @@
+// libtempest_hip runtime: errors, device and stream, storage (buffers and the
+// slot arena), launch objects, graphs and timing.  The Target protocol of the
+// reference (src/Compiler/runtime/target.jl) as a C ABI for one gfx950 GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "th_core.h"
+
+namespace th {
+
+// ---- errors ----------------------------------------------------------------
+
+static thread_local std::string g_error;
+
+void set_error(const std::string& message) { g_error = message; }
+
+int fail(int code, const std::string& message) {
+  g_error = message;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  return static_cast<int>(e);
+}
+
+// ---- context ---------------------------------------------------------------
+
+static Context g_ctx;
+static std::mutex g_timing;  // timings run one at a time (target.jl:619-628)
+
+Context& ctx() { return g_ctx; }
+
+int require_ready() {
+  if (!g_ctx.ready) return fail(TH_E_STATE, "libtempest_hip: th_init has not been called");
+  return TH_OK;
+}
+
+int device_alloc(size_t bytes, void** out) {
+  *out = nullptr;
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(out, bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(TH_E_MEMORY, std::string("hipMalloc of ") + std::to_string(bytes) +
+                                 " bytes failed: " + hipGetErrorString(e));
+  }
+  return TH_OK;
+}
+
+int launch_kernel(const Kernel& k, hipStream_t s) {
+  void* params[1] = {const_cast<unsigned char*>(k.args)};
+  hipError_t e = hipLaunchKernel(k.fn, k.grid, k.block, params, k.shmem, s);
+  if (e != hipSuccess) return hip_fail(e, k.name);
+  return TH_OK;
+}
+
+}  // namespace th
+
+using namespace th;
+
+// A kernel that does nothing: what a replay alone adds is timed with it.
+__global__ void th_blank_kernel(int) {}
+
+// Read `words` 32-bit words, keeping their xor only where zeros could not give
+// it, so that the reads stay: the cache clearing of a timing
+// (read_through, ext/CUDAExt.jl:837-850).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+struct ClearArgs {
+  const u32x4* a;
+  uint32_t* sink;
+  uint64_t n;
+};
+__global__ __launch_bounds__(256) void th_clear_kernel(ClearArgs c) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t s = 0;
+  for (; i < c.n; i += stride) {
+    u32x4 v = __builtin_nontemporal_load(c.a + i);
+    s ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (s == 0xffffffffu) c.sink[0] = s;
+}
+
+extern "C" {
+
+const char* th_last_error(void) { return g_error.c_str(); }
+
+int th_init(int device) {
+  Context& c = ctx();
+  if (c.ready) {
+    if (c.device == device) return TH_OK;
+    return fail(TH_E_STATE, "libtempest_hip drives one device per process; already on device " +
+                                std::to_string(c.device));
+  }
+  int count = 0;
+  TH_HIP(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count)
+    return fail(TH_E_ARGUMENT, "no device " + std::to_string(device) + " (" +
+                                   std::to_string(count) + " visible)");
+  TH_HIP(hipSetDevice(device));
+  TH_HIP(hipGetDeviceProperties(&c.prop, device));
+  TH_HIP(hipStreamCreateWithFlags(&c.own, hipStreamNonBlocking));
+  c.stream = c.own;
+  c.device = device;
+  c.ready = true;
+  return TH_OK;
+}
+
+int th_shutdown(void) {
+  Context& c = ctx();
+  if (!c.ready) return TH_OK;
+  TH_HIP(hipDeviceSynchronize());
+  if (c.clear_buf) TH_HIP(hipFree(c.clear_buf));
+  if (c.sink) TH_HIP(hipFree(c.sink));
+  if (c.own) TH_HIP(hipStreamDestroy(c.own));
+  c = Context{};
+  return TH_OK;
+}
+
+int th_device_name(char* out, size_t capacity) {
+  if (int r = require_ready()) return r;
+  const hipDeviceProp_t& p = ctx().prop;
+  std::snprintf(out, capacity, "%s (%s)", p.name, p.gcnArchName);
+  return TH_OK;
+}
+
+int th_toolchain(char* out, size_t capacity) {
+  int rt = 0;
+  (void)hipRuntimeGetVersion(&rt);
+  std::snprintf(out, capacity, "hip=%d;clang=%s;arch=gfx950", rt, __clang_version__);
+  return TH_OK;
+}
+
+int th_device_rates(th_rates* out) {
+  if (int r = require_ready()) return r;
+  const hipDeviceProp_t& p = ctx().prop;
+  int clock_khz = 0, bus_bits = 0;
+  TH_HIP(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeMemoryClockRate, ctx().device));
+  TH_HIP(hipDeviceGetAttribute(&bus_bits, hipDeviceAttributeMemoryBusWidth, ctx().device));
+  // HBM transfers twice a clock; bytes/s = 2 * clock * pins / 8.
+  double bandwidth = 2.0 * 1.0e3 * clock_khz * bus_bits / 8.0;
+  // CDNA4 has 256 MiB of MALL (Infinity Cache) behind the XCDs' L2.
+  double cache = (double)p.l2CacheSize + 256.0 * 1024 * 1024;
+  out->launch = 5.0e-7;
+  out->bandwidth = bandwidth;
+  out->cached = 2.0 * bandwidth;
+  out->cache = cache;
+  out->blocks = (double)p.multiProcessorCount;
+  return TH_OK;
+}
+
+int th_set_stream(void* stream) {
+  if (int r = require_ready()) return r;
+  ctx().stream = static_cast<hipStream_t>(stream);
+  return TH_OK;
+}
+
+int th_get_stream(void** out) {
+  if (int r = require_ready()) return r;
+  *out = ctx().stream;
+  return TH_OK;
+}
+
+int th_quiesce(void) {
+  if (int r = require_ready()) return r;
+  TH_HIP(hipStreamSynchronize(ctx().stream));
+  return TH_OK;
+}
+
+// ---- storage ---------------------------------------------------------------
+
+int th_alloc(size_t bytes, void** out) {
+  if (int r = require_ready()) return r;
+  return device_alloc(bytes, out);
+}
+
+int th_free(void* ptr) {
+  if (int r = require_ready()) return r;
+  if (ptr) TH_HIP(hipFree(ptr));
+  return TH_OK;
+}
+
+int th_upload(void* dst, const void* src, size_t bytes) {
+  if (int r = require_ready()) return r;
+  if (bytes == 0) return TH_OK;
+  TH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx().stream));
+  // The host array may be freed once the call returns.
+  TH_HIP(hipStreamSynchronize(ctx().stream));
+  return TH_OK;
+}
+
+int th_download(void* dst, const void* src, size_t bytes) {
+  if (int r = require_ready()) return r;
+  if (bytes == 0) return TH_OK;
+  TH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx().stream));
+  TH_HIP(hipStreamSynchronize(ctx().stream));
+  return TH_OK;
+}
+
+int th_copy(void* dst, const void* src, size_t bytes) {
+  if (int r = require_ready()) return r;
+  if (bytes == 0) return TH_OK;
+  TH_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx().stream));
+  return TH_OK;
+}
+
+}  // extern "C"
+
+struct th_arena {
+  void* base = nullptr;
+  uint64_t bytes = 0;
+  std::vector<uint64_t> offsets;
+};
+
+extern "C" {
+
+int th_arena_create(const uint64_t* sizes, int n, uint64_t align, th_arena** out) {
+  if (int r = require_ready()) return r;
+  *out = nullptr;
+  TH_REQUIRE(n >= 0, "th_arena_create: negative slot count");
+  if (align < 256) align = 256;
+  TH_REQUIRE((align & (align - 1)) == 0, "th_arena_create: alignment must be a power of two");
+  th_arena* a = new th_arena();
+  uint64_t at = 0;
+  for (int i = 0; i < n; ++i) {
+    at = (at + align - 1) & ~(align - 1);
+    a->offsets.push_back(at);
+    at += sizes[i];
+  }
+  a->bytes = (at + align - 1) & ~(align - 1);
+  if (int r = device_alloc(a->bytes, &a->base)) {
+    delete a;
+    return r;
+  }
+  *out = a;
+  return TH_OK;
+}
+
+int th_arena_slot(th_arena* a, int slot, void** out) {
+  TH_REQUIRE(a != nullptr, "th_arena_slot: null arena");
+  TH_REQUIRE(slot >= 0 && slot < (int)a->offsets.size(), "th_arena_slot: no such slot");
+  *out = static_cast<char*>(a->base) + a->offsets[slot];
+  return TH_OK;
+}
+
+int th_arena_bytes(th_arena* a, uint64_t* out) {
+  TH_REQUIRE(a != nullptr, "th_arena_bytes: null arena");
+  *out = a->bytes;
+  return TH_OK;
+}
+
+int th_arena_destroy(th_arena* a) {
+  if (!a) return TH_OK;
+  if (a->base) TH_HIP(hipFree(a->base));
+  delete a;
+  return TH_OK;
+}
+
+// ---- launches --------------------------------------------------------------
+
+int th_launch_run(th_launch* l) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(l != nullptr, "th_launch_run: null launch");
+  for (const Kernel& k : l->kernels)
+    if (int r = launch_kernel(k, ctx().stream)) return r;
+  return TH_OK;
+}
+
+int th_launch_repoint(th_launch* l, int value, void* ptr) {
+  TH_REQUIRE(l != nullptr, "th_launch_repoint: null launch");
+  TH_REQUIRE(value >= 0 && value < (int)l->values.size(),
+             "th_launch_repoint: " + l->name + " has no value " + std::to_string(value));
+  TH_REQUIRE(reinterpret_cast<uintptr_t>(ptr) % l->align[value] == 0,
+             "th_launch_repoint: " + l->name + " was built for value " + std::to_string(value) +
+                 " aligned to " + std::to_string(l->align[value]) + " bytes");
+  for (const Ref& r : l->values[value])
+    std::memcpy(l->kernels[r.kernel].args + r.offset, &ptr, sizeof(void*));
+  return TH_OK;
+}
+
+int th_launch_work(th_launch* l, th_work* out) {
+  TH_REQUIRE(l != nullptr, "th_launch_work: null launch");
+  *out = l->work;
+  return TH_OK;
+}
+
+int th_launch_describe(th_launch* l, char* out, size_t capacity) {
+  TH_REQUIRE(l != nullptr, "th_launch_describe: null launch");
+  std::string s = l->name + ":";
+  for (const Kernel& k : l->kernels) {
+    char buf[160];
+    std::snprintf(buf, sizeof buf, " %s<<<(%u,%u,%u),(%u,%u,%u),%u>>>", k.name, k.grid.x, k.grid.y,
+                  k.grid.z, k.block.x, k.block.y, k.block.z, k.shmem);
+    s += buf;
+  }
+  std::snprintf(out, capacity, "%s", s.c_str());
+  return TH_OK;
+}
+
+int th_launch_destroy(th_launch* l) {
+  if (!l) return TH_OK;
+  for (void* p : l->owned)
+    if (p) TH_HIP(hipFree(p));
+  delete l;
+  return TH_OK;
+}
+
+}  // extern "C"
+
+// ---- graphs ----------------------------------------------------------------
+
+struct th_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<th_launch*> steps;
+  std::vector<std::vector<hipGraphNode_t>> nodes;  // per step, per kernel
+};
+
+namespace th {
+
+static hipKernelNodeParams node_params(const Kernel& k, void** params) {
+  hipKernelNodeParams p{};
+  p.func = const_cast<void*>(k.fn);
+  p.gridDim = k.grid;
+  p.blockDim = k.block;
+  p.sharedMemBytes = k.shmem;
+  p.kernelParams = params;
+  p.extra = nullptr;
+  return p;
+}
+
+}  // namespace th
+
+extern "C" {
+
+int th_graph_capture(th_launch* const* steps, int n, th_graph** out) {
+  if (int r = require_ready()) return r;
+  *out = nullptr;
+  TH_REQUIRE(n >= 0, "th_graph_capture: negative step count");
+  th_graph* g = new th_graph();
+  hipError_t e = hipGraphCreate(&g->graph, 0);
+  if (e != hipSuccess) {
+    delete g;
+    return hip_fail(e, "hipGraphCreate");
+  }
+  hipGraphNode_t last = nullptr;
+  for (int i = 0; i < n; ++i) {
+    th_launch* l = steps[i];
+    g->steps.push_back(l);
+    g->nodes.emplace_back();
+    for (Kernel& k : l->kernels) {
+      void* params[1] = {k.args};
+      hipKernelNodeParams p = node_params(k, params);
+      hipGraphNode_t node;
+      e = hipGraphAddKernelNode(&node, g->graph, last ? &last : nullptr, last ? 1 : 0, &p);
+      if (e != hipSuccess) {
+        (void)hipGraphDestroy(g->graph);
+        delete g;
+        return hip_fail(e, "hipGraphAddKernelNode");
+      }
+      g->nodes.back().push_back(node);
+      last = node;
+    }
+  }
+  e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  *out = g;
+  return TH_OK;
+}
+
+int th_graph_replay(th_graph* g) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(g != nullptr, "th_graph_replay: null graph");
+  TH_HIP(hipGraphLaunch(g->exec, ctx().stream));
+  return TH_OK;
+}
+
+int th_graph_retarget(th_graph* g, int step) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(g != nullptr, "th_graph_retarget: null graph");
+  TH_REQUIRE(step >= 0 && step < (int)g->steps.size(), "th_graph_retarget: no such step");
+  th_launch* l = g->steps[step];
+  for (size_t j = 0; j < l->kernels.size(); ++j) {
+    Kernel& k = l->kernels[j];
+    void* params[1] = {k.args};
+    hipKernelNodeParams p = node_params(k, params);
+    TH_HIP(hipGraphExecKernelNodeSetParams(g->exec, g->nodes[step][j], &p));
+  }
+  return TH_OK;
+}
+
+int th_graph_release(th_graph* g) {
+  if (!g) return TH_OK;
+  if (g->exec) TH_HIP(hipGraphExecDestroy(g->exec));
+  if (g->graph) TH_HIP(hipGraphDestroy(g->graph));
+  delete g;
+  return TH_OK;
+}
+
+}  // extern "C"
+
+// ---- timing ----------------------------------------------------------------
+
+namespace th {
+
+static int ensure_clearing() {
+  Context& c = ctx();
+  if (c.clear_buf) return TH_OK;
+  double cache = (double)c.prop.l2CacheSize + 256.0 * 1024 * 1024;
+  size_t bytes = (size_t)(2.0 * cache);
+  bytes = (bytes + 4095) & ~(size_t)4095;
+  if (int r = device_alloc(bytes, &c.clear_buf)) return r;
+  TH_HIP(hipMemsetAsync(c.clear_buf, 0, bytes, c.stream));
+  if (int r = device_alloc(sizeof(uint32_t), (void**)&c.sink)) return r;
+  c.clear_bytes = bytes;
+  return TH_OK;
+}
+
+static int clear_cache() {
+  Context& c = ctx();
+  ClearArgs a{static_cast<const u32x4*>(c.clear_buf), c.sink, c.clear_bytes / 16};
+  int blocks = c.prop.multiProcessorCount * 8;
+  hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
+  TH_HIP(hipGetLastError());
+  return TH_OK;
+}
+
+// Minimum over `samples` of one replay of `g` after the caches are cleared
+// (cleared, ext/CUDAExt.jl:821-833).
+static int cleared(th_graph* g, int samples, double* out) {
+  Context& c = ctx();
+  std::vector<hipEvent_t> ev(2 * samples);
+  for (auto& e : ev) TH_HIP(hipEventCreate(&e));
+  for (int i = 0; i < samples; ++i) {
+    if (int r = clear_cache()) return r;
+    TH_HIP(hipEventRecord(ev[2 * i], c.stream));
+    TH_HIP(hipGraphLaunch(g->exec, c.stream));
+    TH_HIP(hipEventRecord(ev[2 * i + 1], c.stream));
+  }
+  TH_HIP(hipEventSynchronize(ev.back()));
+  float best = 1e30f;
+  for (int i = 0; i < samples; ++i) {
+    float ms = 0;
+    TH_HIP(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+    best = std::min(best, ms);
+  }
+  for (auto& e : ev) TH_HIP(hipEventDestroy(e));
+  *out = best * 1e-3;
+  return TH_OK;
+}
+
+static int mean_replay(th_graph* g, int warmup, int reps, double* out) {
+  Context& c = ctx();
+  for (int i = 0; i < warmup; ++i) TH_HIP(hipGraphLaunch(g->exec, c.stream));
+  hipEvent_t a, b;
+  TH_HIP(hipEventCreate(&a));
+  TH_HIP(hipEventCreate(&b));
+  TH_HIP(hipEventRecord(a, c.stream));
+  for (int i = 0; i < reps; ++i) TH_HIP(hipGraphLaunch(g->exec, c.stream));
+  TH_HIP(hipEventRecord(b, c.stream));
+  TH_HIP(hipEventSynchronize(b));
+  float ms = 0;
+  TH_HIP(hipEventElapsedTime(&ms, a, b));
+  TH_HIP(hipEventDestroy(a));
+  TH_HIP(hipEventDestroy(b));
+  *out = ms * 1e-3 / std::max(reps, 1);
+  return TH_OK;
+}
+
+// What replaying one graph alone adds: an empty kernel's graph timed alone,
+// less its time among a long graph of them (replay_overhead,
+// ext/CUDAExt.jl:874-884).
+static int replay_overhead(double* out) {
+  Context& c = ctx();
+  if (c.replay_overhead >= 0) {
+    *out = c.replay_overhead;
+    return TH_OK;
+  }
+  th_launch blank;
+  blank.name = "blank";
+  Kernel k;
+  k.fn = (const void*)th_blank_kernel;
+  k.name = "th_blank_kernel";
+  int zero = 0;
+  std::memcpy(k.args, &zero, sizeof zero);
+  k.args_size = sizeof zero;
+  blank.kernels.push_back(k);
+  th_launch* one[1] = {&blank};
+  th_graph* alone = nullptr;
+  if (int r = th_graph_capture(one, 1, &alone)) return r;
+  double t_alone = 0;
+  int r = cleared(alone, 20, &t_alone);
+  th_graph_release(alone);
+  if (r) return r;
+  std::vector<th_launch*> many(200, &blank);
+  th_graph* batch = nullptr;
+  if ((r = th_graph_capture(many.data(), (int)many.size(), &batch))) return r;
+  double t_batch = 0;
+  r = mean_replay(batch, 2, 5, &t_batch);
+  th_graph_release(batch);
+  if (r) return r;
+  c.replay_overhead = std::max(0.0, t_alone - t_batch / many.size());
+  *out = c.replay_overhead;
+  return TH_OK;
+}
+
+}  // namespace th
+
+extern "C" {
+
+int th_time_launch(th_launch* l, int samples, double* seconds) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(l != nullptr, "th_time_launch: null launch");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  TH_HIP(hipStreamSynchronize(c.stream));
+  if (int r = ensure_clearing()) return r;
+  double overhead = 0;
+  if (int r = replay_overhead(&overhead)) return r;
+  th_launch* one[1] = {l};
+  th_graph* g = nullptr;
+  if (int r = th_graph_capture(one, 1, &g)) return r;
+  if (samples <= 0) {
+    // As many samples as fit 10 ms of the launch, 3 to 20.
+    double once = 0;
+    int r = mean_replay(g, 1, 1, &once);
+    if (r) {
+      th_graph_release(g);
+      return r;
+    }
+    samples = (int)std::min(20.0, std::max(3.0, 1.0e-2 / std::max(once, 1.0e-6)));
+  }
+  double t = 0;
+  int r = cleared(g, samples, &t);
+  th_graph_release(g);
+  if (r) return r;
+  *seconds = std::max(0.0, t - overhead);
+  return TH_OK;
+}
+
+int th_time_graph(th_graph* g, int warmup, int reps, double* seconds) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(g != nullptr, "th_time_graph: null graph");
+  TH_REQUIRE(reps > 0 && warmup >= 0, "th_time_graph: reps must be positive");
+  std::lock_guard<std::mutex> lock(g_timing);
+  return mean_replay(g, warmup, reps, seconds);
+}
+
+int th_time_run(th_launch* l, int warmup, int reps, double* seconds) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(l != nullptr, "th_time_run: null launch");
+  TH_REQUIRE(reps > 0 && warmup >= 0, "th_time_run: reps must be positive");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  for (int i = 0; i < warmup; ++i)
+    if (int r = th_launch_run(l)) return r;
+  hipEvent_t a, b;
+  TH_HIP(hipEventCreate(&a));
+  TH_HIP(hipEventCreate(&b));
+  TH_HIP(hipEventRecord(a, c.stream));
+  for (int i = 0; i < reps; ++i)
+    if (int r = th_launch_run(l)) return r;
+  TH_HIP(hipEventRecord(b, c.stream));
+  TH_HIP(hipEventSynchronize(b));
+  float ms = 0;
+  TH_HIP(hipEventElapsedTime(&ms, a, b));
+  TH_HIP(hipEventDestroy(a));
+  TH_HIP(hipEventDestroy(b));
+  *seconds = ms * 1e-3 / reps;
+  return TH_OK;
+}
+
+}  // extern "C"

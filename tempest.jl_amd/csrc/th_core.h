@@ -1,0 +1,163 @@
+// Internal core of libtempest_hip: the launch object every builder returns,
+// error reporting, and the helpers kernels share.  Not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/tempest_hip.h"
+
+namespace th {
+
+// ---- errors --------------------------------------------------------------
+
+void set_error(const std::string& message);
+int fail(int code, const std::string& message);
+int hip_fail(hipError_t e, const char* what);
+
+#define TH_HIP(call)                                   \
+  do {                                                 \
+    hipError_t th_e_ = (call);                         \
+    if (th_e_ != hipSuccess) return ::th::hip_fail(th_e_, #call); \
+  } while (0)
+
+#define TH_REQUIRE(cond, msg)                                      \
+  do {                                                             \
+    if (!(cond)) return ::th::fail(TH_E_ARGUMENT, (msg));          \
+  } while (0)
+
+// ---- context ---------------------------------------------------------------
+
+struct Context {
+  bool ready = false;
+  int device = -1;
+  hipStream_t own = nullptr;     // the library's stream (default priority)
+  hipStream_t stream = nullptr;  // where launches go: `own` or the caller's
+  hipDeviceProp_t prop{};
+  // Cache clearing for timings: a buffer of 2 x (L2 + MALL) read through.
+  void* clear_buf = nullptr;
+  size_t clear_bytes = 0;
+  uint32_t* sink = nullptr;
+  double replay_overhead = -1.0;
+};
+
+Context& ctx();
+int require_ready();
+
+// ---- launches --------------------------------------------------------------
+
+// One kernel of a launch: the function, its grid, and its single by-value
+// argument struct, kept as bytes so that values can be repointed in place.
+struct Kernel {
+  const void* fn = nullptr;
+  const char* name = "";
+  dim3 grid{1, 1, 1};
+  dim3 block{1, 1, 1};
+  uint32_t shmem = 0;
+  alignas(16) unsigned char args[512];
+  uint32_t args_size = 0;
+};
+
+// Where a value's address lives: a kernel of the launch and a byte offset
+// into that kernel's argument struct.
+struct Ref {
+  int kernel;
+  uint32_t offset;
+};
+
+}  // namespace th
+
+struct th_launch {
+  std::string name;
+  std::vector<th::Kernel> kernels;
+  std::vector<std::vector<th::Ref>> values;  // per value: every place it is read
+  std::vector<uint32_t> align;               // per value: the alignment the build assumed
+  std::vector<void*> owned;                  // workspaces the launch owns
+  th_work work{};
+};
+
+namespace th {
+
+// A launch under construction: kernels added with their argument struct,
+// value references by member offset.
+class Builder {
+ public:
+  explicit Builder(const char* name, int values) {
+    l_ = new th_launch();
+    l_->name = name;
+    l_->values.resize(values);
+    l_->align.assign(values, 4);
+  }
+  ~Builder() { delete l_; }
+
+  template <class Args>
+  int kernel(const void* fn, const char* name, dim3 grid, dim3 block, uint32_t shmem,
+             const Args& a) {
+    static_assert(sizeof(Args) <= sizeof(Kernel::args), "kernel argument struct too large");
+    Kernel k;
+    k.fn = fn;
+    k.name = name;
+    k.grid = grid;
+    k.block = block;
+    k.shmem = shmem;
+    std::memcpy(k.args, &a, sizeof(Args));
+    k.args_size = sizeof(Args);
+    l_->kernels.push_back(k);
+    return static_cast<int>(l_->kernels.size()) - 1;
+  }
+  // Value `v` is the pointer at byte `offset` of kernel `k`'s arguments.
+  void ref(int v, int k, size_t offset) { l_->values[v].push_back(Ref{k, (uint32_t)offset}); }
+  // Value `v` must stay aligned to `bytes` when it is repointed.
+  void align(int v, uint32_t bytes) { l_->align[v] = std::max(l_->align[v], bytes); }
+  void own(void* p) { l_->owned.push_back(p); }
+  void work(double bytes, double flops, int64_t blocks) {
+    l_->work.bytes = bytes;
+    l_->work.flops = flops;
+    l_->work.blocks = blocks;
+  }
+  th_launch* release() {
+    l_->work.kernels = (int32_t)l_->kernels.size();
+    l_->work.values = (int32_t)l_->values.size();
+    th_launch* out = l_;
+    l_ = nullptr;
+    return out;
+  }
+
+ private:
+  th_launch* l_;
+};
+
+#define TH_OFFSET(Args, member) offsetof(Args, member)
+
+int launch_kernel(const Kernel& k, hipStream_t s);
+int device_alloc(size_t bytes, void** out);
+
+}  // namespace th
+
+// ---- device helpers shared by kernels ---------------------------------------
+
+namespace thd {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// The shift an exponential sum takes against maximum m: m itself when finite,
+// zero otherwise, so that an empty or all -Inf run sums to zero
+// (lse_shift, src/Compiler/IR/folds.jl:194).
+__device__ __forceinline__ float lse_shift(float m) { return isfinite(m) ? m : 0.0f; }
+
+}  // namespace thd

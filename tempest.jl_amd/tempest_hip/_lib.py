@@ -1,0 +1,120 @@
+"""ctypes binding of libtempest_hip.so (include/tempest_hip.h).
+
+The library is loaded from the package's parent directory, where
+tempest.jl_amd/build.py puts it.  There is no fallback: a missing library is
+an error, and every non-zero status raises ``HIPError`` with the library's
+message, as the reference turns a failed build into an exception that its
+cover catches (src/Compiler/cover/choose.jl:1014-1025).
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+LIBRARY = pathlib.Path(__file__).resolve().parent.parent / "libtempest_hip.so"
+
+c_void_p = ctypes.c_void_p
+c_int = ctypes.c_int
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_u64 = ctypes.c_uint64
+c_f32 = ctypes.c_float
+c_size = ctypes.c_size_t
+c_char_p = ctypes.c_char_p
+c_double = ctypes.c_double
+P = ctypes.POINTER
+
+
+class Rates(ctypes.Structure):
+    _fields_ = [("launch", c_double), ("cached", c_double), ("bandwidth", c_double),
+                ("cache", c_double), ("blocks", c_double)]
+
+
+class Work(ctypes.Structure):
+    _fields_ = [("bytes", c_double), ("flops", c_double), ("blocks", c_i64),
+                ("kernels", c_i32), ("values", c_i32)]
+
+
+class HIPError(RuntimeError):
+    """A libtempest_hip entry point returned a non-zero status."""
+
+    def __init__(self, name: str, code: int, message: str):
+        super().__init__(f"{name} failed ({code}): {message}")
+        self.code = code
+
+
+# name -> argtypes; every entry returns int.
+SIGNATURES: dict[str, list] = {
+    "th_init": [c_int],
+    "th_shutdown": [],
+    "th_device_name": [c_char_p, c_size],
+    "th_toolchain": [c_char_p, c_size],
+    "th_device_rates": [P(Rates)],
+    "th_set_stream": [c_void_p],
+    "th_get_stream": [P(c_void_p)],
+    "th_quiesce": [],
+    "th_alloc": [c_size, P(c_void_p)],
+    "th_free": [c_void_p],
+    "th_upload": [c_void_p, c_void_p, c_size],
+    "th_download": [c_void_p, c_void_p, c_size],
+    "th_copy": [c_void_p, c_void_p, c_size],
+    "th_arena_create": [P(c_u64), c_int, c_u64, P(c_void_p)],
+    "th_arena_slot": [c_void_p, c_int, P(c_void_p)],
+    "th_arena_bytes": [c_void_p, P(c_u64)],
+    "th_arena_destroy": [c_void_p],
+    "th_launch_run": [c_void_p],
+    "th_launch_repoint": [c_void_p, c_int, c_void_p],
+    "th_launch_work": [c_void_p, P(Work)],
+    "th_launch_describe": [c_void_p, c_char_p, c_size],
+    "th_launch_destroy": [c_void_p],
+    "th_graph_capture": [P(c_void_p), c_int, P(c_void_p)],
+    "th_graph_replay": [c_void_p],
+    "th_graph_retarget": [c_void_p, c_int],
+    "th_graph_release": [c_void_p],
+    "th_time_launch": [c_void_p, c_int, P(c_double)],
+    "th_time_graph": [c_void_p, c_int, c_int, P(c_double)],
+    "th_time_run": [c_void_p, c_int, c_int, P(c_double)],
+    "th_build_softmax_grad": [c_i64, c_i32, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_layernorm_grad": [c_i64, c_i32, c_i64, c_f32, c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_softmax_fwd": [c_i64, c_i32, c_i64, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_layernorm_fwd": [c_i64, c_i32, c_i64, c_f32, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_sum": [c_i64, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_void_p, c_void_p, P(c_void_p)],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The library, loaded once; raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIBRARY.exists():
+                raise FileNotFoundError(
+                    f"{LIBRARY} is missing: build it with `python tempest.jl_amd/build.py` "
+                    "(or __graft_entry__.build()); there is no fallback path")
+            lib = ctypes.CDLL(str(LIBRARY))
+            for name, args in SIGNATURES.items():
+                f = getattr(lib, name)
+                f.argtypes = args
+                f.restype = c_int
+            lib.th_last_error.argtypes = []
+            lib.th_last_error.restype = c_char_p
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call entry point ``name``; raise HIPError on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise HIPError(name, rc, lib.th_last_error().decode(errors="replace"))
+
+
+def out_ptr() -> c_void_p:
+    return c_void_p()

@@ -1,0 +1,96 @@
+"""Launches: what an implementation's build returns, owned on the host.
+
+A ``Launch`` wraps a ``th_launch*``: one claim's kernels with their
+arguments.  Calling it runs the kernels (a step of ``execute!``);
+``repoint`` is the reference's ``Implement.repoint!(launch, value, buffer)``
+(src/Compiler/Implement/Implement.jl; ext/CUDAExt.jl:1086-1090), by the value
+numbers its builder gave.  The builders below are the entry points of
+include/tempest_hip.h, one per op class and sketch.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+from ._lib import call
+
+
+class Launch:
+    def __init__(self, handle: ctypes.c_void_p, values: tuple[str, ...]):
+        self._h = handle
+        self.values = values  # value number -> the name the program gave it
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise RuntimeError("launch used after destroy")
+        return self._h
+
+    def __call__(self) -> None:
+        call("th_launch_run", self.handle)
+
+    def repoint(self, value: int | str, ptr: int) -> None:
+        if isinstance(value, str):
+            value = self.values.index(value)
+        call("th_launch_repoint", self.handle, value, ctypes.c_void_p(ptr))
+
+    def work(self) -> _lib.Work:
+        w = _lib.Work()
+        call("th_launch_work", self.handle, ctypes.byref(w))
+        return w
+
+    def describe(self) -> str:
+        buf = ctypes.create_string_buffer(2048)
+        call("th_launch_describe", self.handle, buf, len(buf))
+        return buf.value.decode()
+
+    def destroy(self) -> None:
+        if self._h is not None:
+            call("th_launch_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def _built(name: str, values: tuple[str, ...], *args) -> Launch:
+    out = ctypes.c_void_p()
+    call(name, *args, ctypes.byref(out))
+    return Launch(out, values)
+
+
+def _p(ptr: int) -> ctypes.c_void_p:
+    return ctypes.c_void_p(int(ptr))
+
+
+# ---- op class (a) -----------------------------------------------------------
+
+def softmax_grad(rows: int, n: int, ld: int, x: int, g: int, dx: int, loss: int) -> Launch:
+    return _built("th_build_softmax_grad", ("x", "g", "dx", "loss"), rows, n, ld, _p(x), _p(g), _p(dx), _p(loss))
+
+
+def layernorm_grad(rows: int, n: int, ld: int, eps: float, x: int, g: int, dx: int, loss: int) -> Launch:
+    return _built("th_build_layernorm_grad", ("x", "g", "dx", "loss"), rows, n, ld, eps, _p(x), _p(g), _p(dx),
+                  _p(loss))
+
+
+def softmax_fwd(rows: int, n: int, ld: int, x: int, y: int) -> Launch:
+    return _built("th_build_softmax_fwd", ("x", "y"), rows, n, ld, _p(x), _p(y))
+
+
+def layernorm_fwd(rows: int, n: int, ld: int, eps: float, x: int, y: int) -> Launch:
+    return _built("th_build_layernorm_fwd", ("x", "y"), rows, n, ld, eps, _p(x), _p(y))
+
+
+def full_sum(count: int, x: int, out: int) -> Launch:
+    return _built("th_build_sum", ("x", "out"), count, _p(x), _p(out))
+
+
+# ---- config 1 ---------------------------------------------------------------
+
+def tanh_layer_grad(d: int, h: int, c: int, w: int, b: int, x: int, loss: int, dw: int, db: int, dx: int) -> Launch:
+    return _built("th_build_tanh_layer_grad", ("w", "b", "x", "loss", "dw", "db", "dx"), d, h, c, _p(w), _p(b),
+                  _p(x), _p(loss), _p(dw), _p(db), _p(dx))
