@@ -144,7 +144,21 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only-config2", action="store_true",
+                    help="config 2 alone, no CPU baseline (for counter runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE counters to bytes")
     a = ap.parse_args()
+    if a.copy_calibration:
+        import torch
+        src = torch.ones(2**28, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 2**30, "copy_bytes_written": 2**30, "copies": 10}))
+        return 0
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {a.gpus}); "
               "the per-GPU share shards by rows with no exchange.", file=sys.stderr)
@@ -172,12 +186,13 @@ def main() -> int:
                                "layernorm_grad": {"us": c2["s_ln"] * 1e6, "GB/s": c2["alg"] / c2["s_ln"] / 1e9}},
                 "note": "per-program events bracket the fused row kernel and the loss's one-block sum"}
     configs = {"config2_parity_rel": c2["parity"]}
-    try:
-        configs["config1_tanh_layer"] = config1(target)
-    except Exception as err:
-        configs["config1_tanh_layer"] = {"error": repr(err)}
+    if not a.only_config2:
+        try:
+            configs["config1_tanh_layer"] = config1(target)
+        except Exception as err:
+            configs["config1_tanh_layer"] = {"error": repr(err)}
     cpu = None
-    if not a.no_cpu:
+    if not (a.no_cpu or a.only_config2):
         try:
             cpu = cpu_baseline(c2["x"], c2["g"])
         except Exception as err:

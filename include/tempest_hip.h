@@ -212,8 +212,8 @@ int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out
 
 /* loss(w, b, x) = sum(abs2, tanh.(w' * x .+ b)) and its gradient, one fused
  * kernel in one workgroup: w is d x h, b h, x d x c (Float32, column-major);
- * outputs loss (1), dw (d x h), db (h), dx (d x c).  d*h + d*c + 2*h*c
- * floats must fit the workgroup's 64 KiB of LDS (with 16 floats of its own).
+ * outputs loss (1), dw (d x h), db (h), dx (d x c).  p*(h + c) + h*c + 16
+ * floats, p = d rounded up to 4 plus 4, must fit the workgroup's 64 KiB of LDS.
  * Values: 0 w, 1 b, 2 x, 3 loss, 4 dw, 5 db, 6 dx. */
 int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c,
                              const float* w, const float* b, const float* x,

@@ -408,17 +408,30 @@ struct SumArgs {
   int64_t count;
 };
 
+// Each thread sums a contiguous share (16-byte loads where aligned), the
+// waves reduce by shuffles, and wave 0 folds the 16 wave sums in order.
 __global__ __launch_bounds__(1024) void sum_all(SumArgs a) {
-  __shared__ double lds[1024];
+  __shared__ double lds[16];
+  const int64_t per = (a.count + 1023) / 1024;
+  const int64_t lo = min<int64_t>(a.count, per * threadIdx.x);
+  const int64_t hi = min<int64_t>(a.count, lo + per);
   double s = 0.0;
-  for (int64_t i = threadIdx.x; i < a.count; i += 1024) s += (double)a.x[i];
-  lds[threadIdx.x] = s;
+  int64_t i = lo;
+  if ((reinterpret_cast<uintptr_t>(a.x + i) & 15) == 0)
+    for (; i + 4 <= hi; i += 4) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(a.x + i);
+      s += (double)v[0] + (double)v[1] + (double)v[2] + (double)v[3];
+    }
+  for (; i < hi; ++i) s += (double)a.x[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (threadIdx.x % 64 == 0) lds[threadIdx.x / 64] = s;
   __syncthreads();
-  for (int w = 512; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) lds[threadIdx.x] += lds[threadIdx.x + w];
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < 16; ++w) t += lds[w];
+    a.out[0] = (float)t;
   }
-  if (threadIdx.x == 0) a.out[0] = (float)lds[0];
 }
 
 // ---- dispatch --------------------------------------------------------------

@@ -34,22 +34,39 @@ struct TanhArgs {
   int32_t d, h, c;
 };
 
+// LDS rows are padded to a multiple of 4 floats plus 4, so that the lanes of
+// a wave reading neighbouring columns with 16-byte loads hit distinct banks.
+__device__ __forceinline__ int padded(int d) { return ((d + 3) / 4) * 4 + 4; }
+
 __global__ __launch_bounds__(kThreads) void tanh_layer_grad(TanhArgs a) {
   extern __shared__ float lds[];
   const int d = a.d, h = a.h, c = a.c;
-  float* w = lds;            // d x h
-  float* x = w + d * h;      // d x c
-  float* dz = x + d * c;     // h x c
+  const int pd = padded(d);
+  float* w = lds;            // h columns of d, stride pd
+  float* x = w + pd * h;     // c columns of d, stride pd
+  float* dz = x + pd * c;    // h x c
   float* red = dz + h * c;   // kThreads / 64 partial sums
   const int tid = threadIdx.x;
-  for (int i = tid; i < d * h; i += kThreads) w[i] = a.w[i];
-  for (int i = tid; i < d * c; i += kThreads) x[i] = a.x[i];
+  for (int i = tid; i < d * h; i += kThreads) w[(i / d) * pd + i % d] = a.w[i];
+  for (int i = tid; i < d * c; i += kThreads) x[(i / d) * pd + i % d] = a.x[i];
+  for (int i = tid; i < (pd - d) * (h + c); i += kThreads) {
+    const int col = i / (pd - d), k = d + i % (pd - d);
+    (col < h ? w + col * pd : x + (col - h) * pd)[k] = 0.0f;  // zero padding
+  }
   __syncthreads();
   float sq = 0.0f;
   for (int item = tid; item < h * c; item += kThreads) {
     const int j = item % h, col = item / h;
+    const float4* wj = reinterpret_cast<const float4*>(w + j * pd);
+    const float4* xc = reinterpret_cast<const float4*>(x + col * pd);
     float z = 0.0f;
-    for (int i = 0; i < d; ++i) z = fmaf(w[i + d * j], x[i + d * col], z);
+    for (int q = 0; q < pd / 4; ++q) {
+      const float4 u = wj[q], v = xc[q];
+      z = fmaf(u.x, v.x, z);
+      z = fmaf(u.y, v.y, z);
+      z = fmaf(u.z, v.z, z);
+      z = fmaf(u.w, v.w, z);
+    }
     z += a.b[j];
     const float y = tanhf(z);
     sq = fmaf(y, y, sq);
@@ -68,13 +85,13 @@ __global__ __launch_bounds__(kThreads) void tanh_layer_grad(TanhArgs a) {
   for (int item = tid; item < d * h; item += kThreads) {
     const int i = item % d, j = item / d;
     float s = 0.0f;
-    for (int col = 0; col < c; ++col) s = fmaf(x[i + d * col], dz[j + h * col], s);
+    for (int col = 0; col < c; ++col) s = fmaf(x[col * pd + i], dz[j + h * col], s);
     a.dw[item] = s;
   }
   for (int item = tid; item < d * c; item += kThreads) {
     const int i = item % d, col = item / d;
     float s = 0.0f;
-    for (int j = 0; j < h; ++j) s = fmaf(w[i + d * j], dz[j + h * col], s);
+    for (int j = 0; j < h; ++j) s = fmaf(w[j * pd + i], dz[j + h * col], s);
     a.dx[item] = s;
   }
   for (int j = tid; j < h; j += kThreads) {
@@ -92,9 +109,10 @@ extern "C" int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c, const f
   if (int r = th::require_ready()) return r;
   *out = nullptr;
   TH_REQUIRE(d >= 1 && h >= 1 && c >= 1, "th_build_tanh_layer_grad: sizes must be positive");
-  const int64_t floats = (int64_t)d * h + (int64_t)d * c + (int64_t)h * c + kThreads / 64;
+  const int64_t pd = ((d + 3) / 4) * 4 + 4;
+  const int64_t floats = pd * h + pd * c + (int64_t)h * c + kThreads / 64;
   TH_REQUIRE(floats <= kMaxLds,
-             "th_build_tanh_layer_grad: d*h + d*c + h*c must fit one workgroup's 64 KiB");
+             "th_build_tanh_layer_grad: (d+4)*(h+c) + h*c floats must fit one workgroup's 64 KiB");
   TH_REQUIRE(w && b && x && loss && dw && db && dx, "th_build_tanh_layer_grad: null pointer");
   th::Builder bld("tanh_layer_grad", 7);
   TanhArgs a{w, b, x, loss, dw, db, dx, d, h, c};
