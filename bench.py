@@ -138,6 +138,48 @@ def config1(target):
                     "compiled call: host wall time of c(w, b, x) incl. result copies and the loss read"}
 
 
+def config3(target, steps: int = 5, warmup: int = 2):
+    """The 2-layer MLP's gradient at 4096 / 16384 / 4096, batch 4096, bf16:
+    six products, 3.299e12 flops a step."""
+    import torch
+    import tempest_hip as th
+
+    batch, d_in, hidden, d_out = 4096, 4096, 16384, 4096
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    bf = torch.bfloat16
+    W1 = (torch.randn(d_in, hidden, device="cuda", generator=gen) / d_in ** 0.5).to(bf)
+    b1 = (torch.randn(hidden, device="cuda", generator=gen) / d_in ** 0.5).to(bf)
+    W2 = (torch.randn(hidden, d_out, device="cuda", generator=gen) / hidden ** 0.5).to(bf)
+    b2 = (torch.randn(d_out, device="cuda", generator=gen) / hidden ** 0.5).to(bf)
+    x = torch.randn(batch, d_in, device="cuda", generator=gen).to(bf)
+    comp = th.compile(th.programs.mlp(batch, d_in, hidden, d_out), target, W1, b1, W2, b2, x)
+    ex = comp.executable
+    flops = 6 * 2.0 * batch * hidden * d_in
+    for _ in range(warmup):
+        ex.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ex.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    step_s = e0.elapsed_time(e1) * 1e-3 / steps
+    per = {}
+    for g, l in zip(ex.program.groups, ex.launches):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        l()
+        evs[0].record()
+        for _ in range(3):
+            l()
+        evs[1].record()
+        torch.cuda.synchronize()
+        s = evs[0].elapsed_time(evs[1]) * 1e-3 / 3
+        per[g.name] = {"us": s * 1e6, "TFLOP/s": l.work().flops / s / 1e12}
+    return {"ms_per_step": step_s * 1e3, "TFLOP/s": flops / step_s / 1e12,
+            "frac_of_bf16_peak": flops / step_s / BF16_PEAK, "flops_per_step": flops, "per_launch": per}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +233,11 @@ def main() -> int:
             configs["config1_tanh_layer"] = config1(target)
         except Exception as err:
             configs["config1_tanh_layer"] = {"error": repr(err)}
+        try:
+            configs["config3_mlp"] = config3(target)
+        except Exception as err:
+            configs["config3_mlp"] = {"error": repr(err)}
+        log("config3:", json.dumps(configs["config3_mlp"]))
     cpu = None
     if not (a.no_cpu or a.only_config2):
         try:

@@ -220,6 +220,52 @@ int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c,
                              float* loss, float* dw, float* db, float* dx,
                              th_launch** host_out);
 
+/* ---- op class (b): bf16 products on the matrix cores --------------------- */
+
+enum { TH_F32 = 0, TH_BF16 = 1 };
+
+/* What the product's group fuses after it.  Every epilogue works on the fp32
+ * accumulator and rounds once to bf16 where it stores, except where noted.
+ *   TH_EPI_STORE          C = A*B (+ bias[i] if bias), bf16 or fp32.
+ *   TH_EPI_GELU           Z = round(A*B + bias[i]) to C, H = gelu(Z) to aux_out
+ *                         (tanh form, test/fixtures/programs.jl:19).
+ *   TH_EPI_SQUARE_LOSS    y = round(A*B + bias[i]); loss = sum(y .^ 2) (fp32,
+ *                         to *loss); C = dy = round(2y); row_sums[i] = the bf16
+ *                         rounding of sum over j of dy[i, j] (the bias gradient).
+ *   TH_EPI_GELU_BACKWARD  C = dz = round(round(A*B) .* gelu'(Z)), Z = aux
+ *                         (bf16, m x n, column-major at aux_ld); row_sums[i] =
+ *                         sum over j of dz[i, j], rounded to bf16. */
+enum { TH_EPI_STORE = 0, TH_EPI_GELU = 1, TH_EPI_SQUARE_LOSS = 2, TH_EPI_GELU_BACKWARD = 3 };
+
+/* C (m x n, column-major, leading dimension c_ld) = A (m x k) * B (k x n).
+ * A's element (i, l) is a[i*a_m + l*a_k], B's (l, j) is b[l*b_k + j*b_n]; one
+ * stride of each operand must be 1 (k-contiguous or m/n-contiguous), m, n, k
+ * and the other strides multiples of 8, operands 16-byte aligned.  A and B are
+ * bf16, products accumulate in fp32.
+ * Values: 0 a, 1 b, 2 c, 3 bias, 4 aux, 5 aux_out, 6 row_sums, 7 loss.
+ * Replaces the cuTile product sketch (ext/cuTileExt/contract.jl:32-206) and
+ * cuBLASProducts' gemm (ext/cuBLASExt.jl:247-259). */
+typedef struct th_gemm_desc {
+  int32_t m, n, k;
+  int32_t c_dtype;   /* TH_BF16 or TH_F32 (TH_F32 only with TH_EPI_STORE) */
+  int32_t epilogue;  /* TH_EPI_* */
+  int32_t reserved;
+  const void* a;
+  int64_t a_m, a_k;
+  const void* b;
+  int64_t b_k, b_n;
+  void* c;
+  int64_t c_ld;
+  const void* bias;  /* bf16, m */
+  const void* aux;   /* bf16 */
+  int64_t aux_ld;
+  void* aux_out;     /* bf16, C's layout */
+  void* row_sums;    /* bf16, m */
+  float* loss;       /* fp32, one */
+} th_gemm_desc;
+
+int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,3 +35,21 @@ def relative(a, b) -> float:
     b = np.asarray(b, dtype=np.float64)
     nb = np.linalg.norm(b.ravel())
     return float(np.linalg.norm((a - b).ravel()) / (nb if nb > 0 else 1.0))
+
+
+def bf16_bits(x) -> np.ndarray:
+    """Float32 values rounded to bfloat16 (nearest, ties to even), as uint16 bits:
+    BFloat16s' conversion (BFloat16s.jl 0.6.5, the reference's bf16 type)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_value(bits) -> np.ndarray:
+    """The float32 value of bfloat16 bits."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(x) -> np.ndarray:
+    return bf16_value(bf16_bits(x)).reshape(np.shape(x))

@@ -82,3 +82,37 @@ def tanh_layer_grad(w: np.ndarray, b: np.ndarray, x: np.ndarray):
     loss = float((y * y).sum())
     dz = 2.0 * y * (1.0 - y * y)
     return loss, x @ dz.T, dz.sum(axis=1), w @ dz
+
+
+GELU_C = 0.7978846
+GELU_A = 0.044715
+
+
+def gelu(x):
+    """gelu(x) = x/2 (1 + tanh(0.7978846 (x + 0.044715 x^3))) (test/fixtures/programs.jl:19)."""
+    return x / 2 * (1 + np.tanh(GELU_C * (x + GELU_A * x ** 3)))
+
+
+def gelu_grad(x):
+    t = np.tanh(GELU_C * (x + GELU_A * x ** 3))
+    return 0.5 * (1 + t) + 0.5 * x * (1 - t * t) * GELU_C * (1 + 3 * GELU_A * x * x)
+
+
+def mlp_grad(W1, b1, W2, b2, x):
+    """Config 3: loss = sum(abs2, W2 * gelu.(W1 * x .+ b1) .+ b2) and its gradient
+    w.r.t. (W1, b1, W2, b2, x), Julia matrices (W1 hidden x d_in, x d_in x batch,
+    W2 d_out x hidden) in float64: the program's meaning with products widened
+    and nothing rounded between (interpret.jl:58-63)."""
+    W1, b1, W2, b2, x = (np.asarray(a, dtype=np.float64) for a in (W1, b1, W2, b2, x))
+    z = W1 @ x + b1[:, None]
+    h = gelu(z)
+    y = W2 @ h + b2[:, None]
+    loss = float((y * y).sum())
+    dy = 2 * y
+    dW2 = dy @ h.T
+    db2 = dy.sum(axis=1)
+    dz = (W2.T @ dy) * gelu_grad(z)
+    dW1 = dz @ x.T
+    db1 = dz.sum(axis=1)
+    dx = W1.T @ dz
+    return loss, dW1, db1, dW2, db2, dx

@@ -1,0 +1,150 @@
+// th_build_gemm: the bf16 product's launch (gemm_kernel.h holds the kernel),
+// and the folds its epilogues leave: bias gradients and the loss.
+#include <hip/hip_runtime.h>
+
+#include "gemm_kernel.h"
+#include "th_core.h"
+
+namespace thg {
+namespace {
+
+struct RowSumArgs {
+  const float* partial;  // parts x m
+  uint16_t* out;         // m, bf16
+  int32_t m, parts;
+};
+
+// out[i] = sum over parts of partial[p, i], in part order.
+__global__ __launch_bounds__(256) void sum_parts(RowSumArgs a) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.m) return;
+  float s = 0.0f;
+  for (int p = 0; p < a.parts; ++p) s += a.partial[(int64_t)p * a.m + i];
+  a.out[i] = bf16_bits(s);
+}
+
+struct LossArgs {
+  const float* partial;
+  float* loss;
+  int32_t count;
+};
+
+__global__ __launch_bounds__(256) void sum_loss(LossArgs a) {
+  __shared__ double lds[4];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < a.count; i += 256) s += (double)a.partial[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (threadIdx.x % 64 == 0) lds[threadIdx.x / 64] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) a.loss[0] = (float)(lds[0] + lds[1] + lds[2] + lds[3]);
+}
+
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+}  // namespace
+}  // namespace thg
+
+using namespace thg;
+
+extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
+  if (int r = th::require_ready()) return r;
+  *out = nullptr;
+  TH_REQUIRE(d != nullptr, "th_build_gemm: null descriptor");
+  const int M = d->m, N = d->n, K = d->k;
+  TH_REQUIRE(M >= 1 && N >= 1 && K >= 1, "th_build_gemm: m, n, k must be positive");
+  TH_REQUIRE(M % 8 == 0 && N % 8 == 0 && K % 8 == 0,
+             "th_build_gemm: m, n and k must be multiples of 8 (16-byte rows)");
+  TH_REQUIRE(d->a && d->b && d->c, "th_build_gemm: null operand");
+  const int la = d->a_k == 1 ? kK : (d->a_m == 1 ? kMN : -1);
+  const int lb = d->b_k == 1 ? kK : (d->b_n == 1 ? kMN : -1);
+  TH_REQUIRE(la >= 0 && lb >= 0, "th_build_gemm: each operand needs a unit stride along k or along m/n");
+  const int64_t sa = la == kK ? d->a_m : d->a_k, sb = lb == kK ? d->b_n : d->b_k;
+  TH_REQUIRE(sa % 8 == 0 && sb % 8 == 0 && d->c_ld % 8 == 0 && d->c_ld >= M,
+             "th_build_gemm: leading dimensions must be multiples of 8 and c_ld >= m");
+  TH_REQUIRE(aligned(d->a, 16) && aligned(d->b, 16) && aligned(d->c, 16),
+             "th_build_gemm: operands must be 16-byte aligned");
+  const int epi = d->epilogue;
+  TH_REQUIRE(epi >= TH_EPI_STORE && epi <= TH_EPI_GELU_BACKWARD, "th_build_gemm: unknown epilogue");
+  TH_REQUIRE(d->c_dtype == TH_BF16 || (d->c_dtype == TH_F32 && epi == TH_EPI_STORE),
+             "th_build_gemm: fused epilogues write bf16");
+  TH_REQUIRE(!d->bias || aligned(d->bias, 8), "th_build_gemm: bias must be 8-byte aligned");
+  TH_REQUIRE(!(d->c_dtype == TH_F32 && d->bias), "th_build_gemm: an fp32 result takes no bias");
+  if (epi == TH_EPI_GELU)
+    TH_REQUIRE(d->aux_out && d->bias && aligned(d->aux_out, 8), "th_build_gemm: GELU needs bias and aux_out");
+  if (epi == TH_EPI_SQUARE_LOSS)
+    TH_REQUIRE(d->bias && d->loss && d->row_sums, "th_build_gemm: the square loss needs bias, loss, row_sums");
+  if (epi == TH_EPI_GELU_BACKWARD)
+    TH_REQUIRE(d->aux && d->row_sums && d->aux_ld >= M && d->aux_ld % 4 == 0 && aligned(d->aux, 8),
+               "th_build_gemm: the GELU backward needs aux (8-byte aligned, ld >= m, ld % 4 == 0) and row_sums");
+
+  const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+  const bool check = (M % kTile) || (N % kTile) || (K % kDepth);
+  const void* fn = nullptr;
+  const char* name = "";
+  switch (epi) {
+    case TH_EPI_STORE:
+      fn = d->c_dtype == TH_F32 ? gemm_store_f32(la, lb, check) : gemm_store(la, lb, check);
+      name = d->c_dtype == TH_F32 ? "gemm_bf16_store_f32" : "gemm_bf16_store";
+      break;
+    case TH_EPI_GELU: fn = gemm_gelu(la, lb, check), name = "gemm_bf16_gelu"; break;
+    case TH_EPI_SQUARE_LOSS: fn = gemm_square_loss(la, lb, check), name = "gemm_bf16_square_loss"; break;
+    default: fn = gemm_gelu_backward(la, lb, check), name = "gemm_bf16_gelu_backward"; break;
+  }
+  TH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds));
+
+  th::Builder b("gemm_bf16", 8);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(d->a);
+  g.b = static_cast<const uint16_t*>(d->b);
+  g.c = d->c;
+  g.bias = static_cast<const uint16_t*>(d->bias);
+  g.aux = static_cast<const uint16_t*>(d->aux);
+  g.aux_out = static_cast<uint16_t*>(d->aux_out);
+  g.a_o = la == kK ? d->a_m : 1;
+  g.a_k = la == kK ? 1 : d->a_k;
+  g.b_o = lb == kK ? d->b_n : 1;
+  g.b_k = lb == kK ? 1 : d->b_k;
+  g.ldc = d->c_ld;
+  g.aux_ld = d->aux_ld;
+  g.m = M;
+  g.n = N;
+  g.k = K;
+  g.tiles_m = tiles_m;
+  g.tiles_n = tiles_n;
+  const bool sums = epi == TH_EPI_SQUARE_LOSS || epi == TH_EPI_GELU_BACKWARD;
+  const int blocks = tiles_m * tiles_n;
+  if (sums) {
+    void* ws = nullptr;
+    const size_t floats = (size_t)2 * tiles_n * M + (size_t)4 * blocks;
+    if (int r = th::device_alloc(floats * sizeof(float), &ws)) return r;
+    b.own(ws);
+    g.partial = static_cast<float*>(ws);
+  }
+  int k = b.kernel(fn, name, dim3(blocks), dim3(kThreads), (uint32_t)kLds, g);
+  b.ref(0, k, TH_OFFSET(GemmArgs, a));
+  b.ref(1, k, TH_OFFSET(GemmArgs, b));
+  b.ref(2, k, TH_OFFSET(GemmArgs, c));
+  b.ref(3, k, TH_OFFSET(GemmArgs, bias));
+  b.ref(4, k, TH_OFFSET(GemmArgs, aux));
+  b.ref(5, k, TH_OFFSET(GemmArgs, aux_out));
+  for (int v : {0, 1, 2}) b.align(v, 16);
+  for (int v : {3, 4, 5}) b.align(v, 8);
+  if (sums) {
+    RowSumArgs rs{g.partial, static_cast<uint16_t*>(d->row_sums), M, 2 * tiles_n};
+    int k2 = b.kernel((const void*)sum_parts, "sum_parts", dim3((M + 255) / 256), dim3(256), 0, rs);
+    b.ref(6, k2, TH_OFFSET(RowSumArgs, out));
+  }
+  if (epi == TH_EPI_SQUARE_LOSS) {
+    LossArgs ls{g.partial + (size_t)2 * tiles_n * M, d->loss, 4 * blocks};
+    int k3 = b.kernel((const void*)sum_loss, "sum_loss", dim3(1), dim3(256), 0, ls);
+    b.ref(7, k3, TH_OFFSET(LossArgs, loss));
+  }
+  const double mm = M, nn = N, kk = K;
+  const double cbytes = d->c_dtype == TH_F32 ? 4 : 2;
+  double bytes = 2.0 * (mm * kk + kk * nn) + cbytes * mm * nn;
+  if (epi == TH_EPI_GELU || epi == TH_EPI_GELU_BACKWARD) bytes += 2.0 * mm * nn;
+  b.work(bytes, 2.0 * mm * nn * kk, blocks);
+  *out = b.release();
+  return TH_OK;
+}

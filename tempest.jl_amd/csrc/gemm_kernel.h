@@ -1,0 +1,365 @@
+// Op class (b): bf16 products on CDNA4 matrix cores, fp32 accumulation, with
+// the epilogues a planned group fuses after them.  The kernel template; each
+// gemm_*.hip instantiates one epilogue (they compile in parallel).
+//
+// C (m x n, column-major) = A (m x k) * B (k x n), each operand given by its
+// two strides, one of which is 1: "k-contiguous" or "mn-contiguous".  One
+// workgroup of four waves computes a 256 x 256 tile of C; each wave a
+// 128 x 128 quarter as 4 x 4 v_mfma_f32_32x32x16_bf16 blocks (256 fp32
+// accumulators per lane, in AGPRs).  K advances 64 at a time through two LDS
+// stages: while the waves multiply out of one stage, the next tile's global
+// loads are in flight into registers, and land in the other stage after.
+// LDS rows are k-contiguous, 64 bf16 plus 8 of padding (144 bytes), so the
+// 16-byte fragment reads of 16 lanes fall on 16 distinct bank quads.  An
+// mn-contiguous operand is transposed on its way into LDS: each thread loads
+// an 8 x 8 block (eight 16-byte rows along m or n, eight lanes along k side
+// by side so their LDS writes spread over the banks) and writes it back as
+// eight 16-byte rows along k.
+//
+// Workgroups are dealt to the eight XCDs round-robin; the tile order is
+// remapped so each XCD takes a contiguous range of tiles, grouped 8 tile-rows
+// high, and the tiles that share operands share an L2.
+//
+// Replaces the cuTile product sketch (ext/cuTileExt/contract.jl:32-206, MMA
+// step emit.jl:894-948, swizzle build.jl:35-45) and cuBLAS's
+// cublasGemmStridedBatchedEx (ext/cuBLASExt.jl:247-259).  Half factors are
+// widened to fp32 products and the result rounded once, as the reference's
+// interpreter evaluates a contraction (src/Compiler/program/interpret.jl:58-63).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+namespace thg {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kTile = 256;            // C tile, both sides
+constexpr int kDepth = 64;            // K per stage
+constexpr int kRow = 72;              // LDS row: 64 bf16 + 8 padding
+constexpr int kStage = kTile * kRow;  // bf16 per operand stage
+constexpr int kThreads = 256;
+constexpr size_t kLds = 4 * kStage * sizeof(uint16_t);  // A and B, two stages: 147456 bytes
+
+enum Layout { kK = 0, kMN = 1 };
+enum Epilogue { kStore = 0, kStoreF32 = 1, kGelu = 2, kSquareLoss = 3, kGeluBackward = 4 };
+
+struct GemmArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  void* c;
+  const uint16_t* bias;  // per-m, bf16 (kStore: optional)
+  const uint16_t* aux;   // kGeluBackward: Z, column-major, ld aux_ld
+  uint16_t* aux_out;     // kGelu: H, same layout as C
+  float* partial;        // row sums per (tile n, wave column) x m; then loss partials
+  int64_t a_o, a_k;      // A's strides along m and along k
+  int64_t b_o, b_k;      // B's strides along n and along k
+  int64_t ldc, aux_ld;
+  int32_t m, n, k;
+  int32_t tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ uint16_t bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                              // to nearest even
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ float half_of(uint32_t w, int r) { return bf16_float((uint16_t)(w >> (16 * r))); }
+
+__device__ __forceinline__ u32x2 pack4(const uint16_t (&h)[4]) {
+  return u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+}
+
+// GELU, tanh form (test/fixtures/programs.jl:19), and its derivative.
+__device__ __forceinline__ float gelu(float x) {
+  const float t = tanhf(0.7978846f * (x + 0.044715f * x * x * x));
+  return 0.5f * x * (1.0f + t);
+}
+__device__ __forceinline__ float gelu_grad(float x) {
+  const float t = tanhf(0.7978846f * (x + 0.044715f * x * x * x));
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * 0.7978846f * (1.0f + 3.0f * 0.044715f * x * x);
+}
+
+// ---- global -> registers -> LDS ----------------------------------------------
+
+// k-contiguous operand: thread takes the 16-byte chunk tid % 8 of rows
+// tid / 8 + 32 i (i = 0..7) of the tile's 256 rows.
+template <bool CHECK>
+__device__ __forceinline__ void load_k(const uint16_t* base, int64_t s_o, int o0, int k0, int O, int K,
+                                       u32x4 (&r)[8]) {
+  const int c = threadIdx.x % 8, row = threadIdx.x / 8;
+  const int k = k0 + 8 * c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int o = o0 + row + 32 * i;
+    if (!CHECK || (o < O && k < K))
+      r[i] = *reinterpret_cast<const u32x4*>(base + (int64_t)o * s_o + k);
+    else
+      r[i] = u32x4{0, 0, 0, 0};
+  }
+}
+
+__device__ __forceinline__ void store_k(uint16_t* lds, const u32x4 (&r)[8]) {
+  const int c = threadIdx.x % 8, row = threadIdx.x / 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(lds + (row + 32 * i) * kRow + 8 * c) = r[i];
+}
+
+// mn-contiguous operand: thread (kb = tid % 8, ob = tid / 8) takes the 8 x 8
+// block of rows k0 + 8 kb + (0..7), columns o0 + 8 ob + (0..7).
+template <bool CHECK>
+__device__ __forceinline__ void load_mn(const uint16_t* base, int64_t s_k, int o0, int k0, int O, int K,
+                                        u32x4 (&r)[8]) {
+  const int kb = threadIdx.x % 8, ob = threadIdx.x / 8;
+  const int o = o0 + 8 * ob;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int k = k0 + 8 * kb + i;
+    if (!CHECK || (o < O && k < K))
+      r[i] = *reinterpret_cast<const u32x4*>(base + o + (int64_t)k * s_k);
+    else
+      r[i] = u32x4{0, 0, 0, 0};
+  }
+}
+
+// Transpose the 8 x 8 block in registers and write it as 8 rows along k.
+__device__ __forceinline__ void store_mn(uint16_t* lds, const u32x4 (&r)[8]) {
+  const int kb = threadIdx.x % 8, ob = threadIdx.x / 8;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = r[2 * e][c / 2], hi = r[2 * e + 1][c / 2];
+      w[e] = (c % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+    }
+    *reinterpret_cast<u32x4*>(lds + (8 * ob + c) * kRow + 8 * kb) = w;
+  }
+}
+
+template <int L, bool CHECK>
+__device__ __forceinline__ void load_tile(const uint16_t* base, int64_t s_o, int64_t s_k, int o0, int k0, int O,
+                                          int K, u32x4 (&r)[8]) {
+  if constexpr (L == kK)
+    load_k<CHECK>(base, s_o, o0, k0, O, K, r);
+  else
+    load_mn<CHECK>(base, s_k, o0, k0, O, K, r);
+}
+
+template <int L>
+__device__ __forceinline__ void store_tile(uint16_t* lds, const u32x4 (&r)[8]) {
+  if constexpr (L == kK)
+    store_k(lds, r);
+  else
+    store_mn(lds, r);
+}
+
+// ---- the tile order ----------------------------------------------------------
+
+__device__ __forceinline__ void tile_of(int block, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int total = tiles_m * tiles_n;
+  int t = block;
+  if (total % 8 == 0) t = (block % 8) * (total / 8) + block / 8;  // XCD-contiguous ranges
+  const int group = 8;
+  const int per_group = group * tiles_n;
+  const int g = t / per_group;
+  const int first = g * group;
+  const int rows = min(tiles_m - first, group);
+  const int in = t % per_group;
+  *tm = first + in % rows;
+  *tn = in / rows;
+}
+
+// ---- the kernel --------------------------------------------------------------
+
+template <int LA, int LB, int EPI, bool CHECK>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1))) void gemm_bf16(
+    GemmArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  uint16_t* As = lds;
+  uint16_t* Bs = lds + 2 * kStage;
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int m0 = tm * kTile, n0 = tn * kTile;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int wm = wave / 2, wn = wave % 2;
+  const int lr = lane % 32, lh = lane / 32;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int KT = (p.k + kDepth - 1) / kDepth;
+  u32x4 ra[8], rb[8];
+  load_tile<LA, CHECK>(p.a, p.a_o, p.a_k, m0, 0, p.m, p.k, ra);
+  load_tile<LB, CHECK>(p.b, p.b_o, p.b_k, n0, 0, p.n, p.k, rb);
+  store_tile<LA>(As, ra);
+  store_tile<LB>(Bs, rb);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < KT;
+    if (more) {
+      load_tile<LA, CHECK>(p.a, p.a_o, p.a_k, m0, (kt + 1) * kDepth, p.m, p.k, ra);
+      load_tile<LB, CHECK>(p.b, p.b_o, p.b_k, n0, (kt + 1) * kDepth, p.n, p.k, rb);
+    }
+    const uint16_t* Ac = As + cur * kStage + (wm * 128 + lr) * kRow + 8 * lh;
+    const uint16_t* Bc = Bs + cur * kStage + (wn * 128 + lr) * kRow + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < kDepth / 16; ++kk) {
+      bf16x8 af[4], bf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(Ac + i * 32 * kRow + kk * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bc + j * 32 * kRow + kk * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      store_tile<LA>(As + (cur ^ 1) * kStage, ra);
+      store_tile<LB>(Bs + (cur ^ 1) * kStage, rb);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds C(m, n) for n = n_j + lane % 32 and
+  // m = m_i + 8 g + 4 (lane / 32) + (0..3), register 4 g + (0..3).
+  constexpr bool kSums = EPI == kSquareLoss || EPI == kGeluBackward;
+  float loss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int mi = m0 + wm * 128 + i * 32 + 4 * lh;
+    float rs[4][4];  // [g][r]: this lane's share of the row sums of block row i
+    float bias[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rs[g][r] = 0.0f, bias[g][r] = 0.0f;
+    if (EPI == kGelu || EPI == kSquareLoss || EPI == kStore) {
+      if (EPI != kStore || p.bias) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = mi + 8 * g;
+          if (!CHECK || m < p.m) {
+            const u32x2 bb = *reinterpret_cast<const u32x2*>(p.bias + m);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bias[g][r] = half_of(bb[r / 2], r % 2);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn * 128 + j * 32 + lr;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = mi + 8 * g;
+        const bool live = !CHECK || (m < p.m && n < p.n);
+        const int64_t at = (int64_t)m + (int64_t)n * p.ldc;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = acc[i][j][4 * g + r] + bias[g][r];
+        if constexpr (EPI == kStoreF32) {
+          if (live) *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + at) = f32x4{v[0], v[1], v[2], v[3]};
+          continue;
+        }
+        uint16_t out[4];
+        if constexpr (EPI == kGelu) {
+          uint16_t h[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            out[r] = bf16_bits(v[r]);
+            h[r] = bf16_bits(gelu(bf16_float(out[r])));
+          }
+          if (live) *reinterpret_cast<u32x2*>(p.aux_out + at) = pack4(h);
+        } else if constexpr (EPI == kSquareLoss) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float y = bf16_float(bf16_bits(v[r]));
+            out[r] = bf16_bits(2.0f * y);
+            if (live) {
+              loss = fmaf(y, y, loss);
+              rs[g][r] += bf16_float(out[r]);
+            }
+          }
+        } else if constexpr (EPI == kGeluBackward) {
+          u32x2 zz = u32x2{0, 0};
+          if (live) zz = *reinterpret_cast<const u32x2*>(p.aux + (int64_t)m + (int64_t)n * p.aux_ld);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float dh = bf16_float(bf16_bits(v[r]));
+            out[r] = bf16_bits(dh * gelu_grad(half_of(zz[r / 2], r % 2)));
+            if (live) rs[g][r] += bf16_float(out[r]);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) out[r] = bf16_bits(v[r]);
+        }
+        if (live) *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.c) + at) = pack4(out);
+      }
+    }
+    if constexpr (kSums) {
+      // Row sums over the wave's 128 columns: the 32 lanes of a half share rows.
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float s = rs[g][r];
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o, 64);
+          rs[g][r] = s;
+        }
+      if (lr == 0) {
+        float* part = p.partial + (int64_t)(tn * 2 + wn) * p.m;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = mi + 8 * g;
+          if (!CHECK || m < p.m) *reinterpret_cast<f32x4*>(part + m) = f32x4{rs[g][0], rs[g][1], rs[g][2], rs[g][3]};
+        }
+      }
+    }
+  }
+  if constexpr (EPI == kSquareLoss) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) loss += __shfl_xor(loss, o, 64);
+    if (lane == 0) p.partial[(int64_t)(2 * p.tiles_n) * p.m + blockIdx.x * 4 + wave] = loss;
+  }
+}
+
+template <int LA, int LB, int EPI>
+const void* kernel_for(bool check) {
+  return check ? (const void*)gemm_bf16<LA, LB, EPI, true> : (const void*)gemm_bf16<LA, LB, EPI, false>;
+}
+
+template <int EPI>
+const void* kernel_for(int la, int lb, bool check) {
+  if (la == kK && lb == kK) return kernel_for<kK, kK, EPI>(check);
+  if (la == kK && lb == kMN) return kernel_for<kK, kMN, EPI>(check);
+  if (la == kMN && lb == kK) return kernel_for<kMN, kK, EPI>(check);
+  return kernel_for<kMN, kMN, EPI>(check);
+}
+
+// One per epilogue, each defined in its own translation unit.
+const void* gemm_store(int la, int lb, bool check);
+const void* gemm_store_f32(int la, int lb, bool check);
+const void* gemm_gelu(int la, int lb, bool check);
+const void* gemm_square_loss(int la, int lb, bool check);
+const void* gemm_gelu_backward(int la, int lb, bool check);
+
+}  // namespace thg

@@ -36,6 +36,15 @@ class Work(ctypes.Structure):
                 ("kernels", c_i32), ("values", c_i32)]
 
 
+class GemmDesc(ctypes.Structure):
+    """th_gemm_desc (include/tempest_hip.h)."""
+    _fields_ = [("m", c_i32), ("n", c_i32), ("k", c_i32), ("c_dtype", c_i32), ("epilogue", c_i32),
+                ("reserved", c_i32), ("a", c_void_p), ("a_m", c_i64), ("a_k", c_i64), ("b", c_void_p),
+                ("b_k", c_i64), ("b_n", c_i64), ("c", c_void_p), ("c_ld", c_i64), ("bias", c_void_p),
+                ("aux", c_void_p), ("aux_ld", c_i64), ("aux_out", c_void_p), ("row_sums", c_void_p),
+                ("loss", c_void_p)]
+
+
 class HIPError(RuntimeError):
     """A libtempest_hip entry point returned a non-zero status."""
 
@@ -80,6 +89,7 @@ SIGNATURES: dict[str, list] = {
     "th_build_softmax_fwd": [c_i64, c_i32, c_i64, c_void_p, c_void_p, P(c_void_p)],
     "th_build_layernorm_fwd": [c_i64, c_i32, c_i64, c_f32, c_void_p, c_void_p, P(c_void_p)],
     "th_build_sum": [c_i64, c_void_p, c_void_p, P(c_void_p)],
+    "th_build_gemm": [P(GemmDesc), P(c_void_p)],
     "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, P(c_void_p)],
 }

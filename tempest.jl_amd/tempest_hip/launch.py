@@ -94,3 +94,21 @@ def full_sum(count: int, x: int, out: int) -> Launch:
 def tanh_layer_grad(d: int, h: int, c: int, w: int, b: int, x: int, loss: int, dw: int, db: int, dx: int) -> Launch:
     return _built("th_build_tanh_layer_grad", ("w", "b", "x", "loss", "dw", "db", "dx"), d, h, c, _p(w), _p(b),
                   _p(x), _p(loss), _p(dw), _p(db), _p(dx))
+
+
+# ---- op class (b) -----------------------------------------------------------
+
+F32, BF16 = 0, 1
+STORE, GELU, SQUARE_LOSS, GELU_BACKWARD = 0, 1, 2, 3
+
+
+def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b_n: int, c: int, c_ld: int,
+         c_dtype: int = BF16, epilogue: int = STORE, bias: int = 0, aux: int = 0, aux_ld: int = 0,
+         aux_out: int = 0, row_sums: int = 0, loss: int = 0) -> Launch:
+    """C (m x n, column-major at c_ld) = A (m x k) * B (k x n) on the matrix cores,
+    A(i, l) at a[i*a_m + l*a_k], B(l, j) at b[l*b_k + j*b_n], bf16 operands."""
+    d = _lib.GemmDesc(m=m, n=n, k=k, c_dtype=c_dtype, epilogue=epilogue, a=a, a_m=a_m, a_k=a_k, b=b, b_k=b_k,
+                      b_n=b_n, c=c, c_ld=c_ld, bias=bias or None, aux=aux or None, aux_ld=aux_ld,
+                      aux_out=aux_out or None, row_sums=row_sums or None, loss=loss or None)
+    return _built("th_build_gemm", ("a", "b", "c", "bias", "aux", "aux_out", "row_sums", "loss"),
+                  ctypes.byref(d))

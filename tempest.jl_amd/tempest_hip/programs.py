@@ -60,3 +60,51 @@ def layernorm(rows: int, n: int, eps: float = 1e-5) -> Program:
     """Config 2b: (x, g) -> sum(layernorm(x) .* g) and its gradient; x, g n x rows."""
     return _row_program("layernorm", rows, n,
                         lambda x, g, dx, loss: L.layernorm_grad(rows, n, n, eps, x, g, dx, loss))
+
+
+def mlp(batch: int = 4096, d_in: int = 4096, hidden: int = 16384, d_out: int = 4096) -> Program:
+    """Config 3: loss = sum(abs2, W2 * gelu.(W1 * x .+ b1) .+ b2) with withgradient
+    w.r.t. (W1, b1, W2, b2, x); bf16 arrays, fp32 accumulation.
+
+    Julia shapes: W1 hidden x d_in, b1 hidden, W2 d_out x hidden, b2 d_out,
+    x d_in x batch (column-major).  Plan: six product groups, each with the
+    pointwise work around it fused into its epilogue, and two stored values
+    between the forward and the backward (Z1 = W1 x + b1 and H = gelu(Z1));
+    dy = 2y and dZ1 = (W2' dy) .* gelu'(Z1) are stored for the weight
+    products that read them.  The biases' gradients and the loss are the
+    epilogues' row and full folds.
+    """
+    L_ = L
+    bf, f32 = torch.bfloat16, torch.float32
+    V = lambda name, dims, role, dt=bf: Value(name, dt, dims, role)  # noqa: E731
+    values = {v.name: v for v in [
+        V("W1", (hidden, d_in), "input"), V("b1", (hidden,), "input"),
+        V("W2", (d_out, hidden), "input"), V("b2", (d_out,), "input"),
+        V("x", (d_in, batch), "input"),
+        V("Z1", (hidden, batch), "stored"), V("H", (hidden, batch), "stored"),
+        V("dy", (d_out, batch), "stored"), V("dZ1", (hidden, batch), "stored"),
+        V("loss", (), "result", f32), V("dW1", (hidden, d_in), "result"), V("db1", (hidden,), "result"),
+        V("dW2", (d_out, hidden), "result"), V("db2", (d_out,), "result"), V("dx", (d_in, batch), "result"),
+    ]}
+    G = lambda name, vals, reads, writes, build: Group(name, vals, reads, writes, build)  # noqa: E731
+    groups = [
+        G("Z1 = W1 x .+ b1, H = gelu.(Z1)", ("W1", "x", "Z1", "b1", "", "H", "", ""), ("W1", "x", "b1"),
+          ("Z1", "H"),
+          lambda a: L_.gemm(hidden, batch, d_in, a["W1"], 1, hidden, a["x"], 1, d_in, a["Z1"], hidden,
+                            epilogue=L_.GELU, bias=a["b1"], aux_out=a["H"])),
+        G("y = W2 H .+ b2; loss = sum(y.^2); dy = 2y; db2 = sum(dy; dims=2)",
+          ("W2", "H", "dy", "b2", "", "", "db2", "loss"), ("W2", "H", "b2"), ("dy", "db2", "loss"),
+          lambda a: L_.gemm(d_out, batch, hidden, a["W2"], 1, d_out, a["H"], 1, hidden, a["dy"], d_out,
+                            epilogue=L_.SQUARE_LOSS, bias=a["b2"], row_sums=a["db2"], loss=a["loss"])),
+        G("dW2 = dy H'", ("dy", "H", "dW2", "", "", "", "", ""), ("dy", "H"), ("dW2",),
+          lambda a: L_.gemm(d_out, hidden, batch, a["dy"], 1, d_out, a["H"], hidden, 1, a["dW2"], d_out)),
+        G("dZ1 = (W2' dy) .* gelu'(Z1); db1 = sum(dZ1; dims=2)", ("W2", "dy", "dZ1", "", "Z1", "", "db1", ""),
+          ("W2", "dy", "Z1"), ("dZ1", "db1"),
+          lambda a: L_.gemm(hidden, batch, d_out, a["W2"], d_out, 1, a["dy"], 1, d_out, a["dZ1"], hidden,
+                            epilogue=L_.GELU_BACKWARD, aux=a["Z1"], aux_ld=hidden, row_sums=a["db1"])),
+        G("dW1 = dZ1 x'", ("dZ1", "x", "dW1", "", "", "", "", ""), ("dZ1", "x"), ("dW1",),
+          lambda a: L_.gemm(hidden, d_in, batch, a["dZ1"], 1, hidden, a["x"], d_in, 1, a["dW1"], hidden)),
+        G("dx = W1' dZ1", ("W1", "dZ1", "dx", "", "", "", "", ""), ("W1", "dZ1"), ("dx",),
+          lambda a: L_.gemm(d_in, batch, hidden, a["W1"], hidden, 1, a["dZ1"], 1, hidden, a["dx"], d_in)),
+    ]
+    return Program("mlp", values, groups, ["W1", "b1", "W2", "b2", "x"], ["loss", "dW1", "db1", "dW2", "db2", "dx"])

@@ -219,9 +219,10 @@ class Executable:
             after = self.addresses[name]
             if after != before:
                 for k, (g, l) in enumerate(zip(self.program.groups, self.launches)):
-                    if name in g.values:
-                        l.repoint(name, after)
-                        self._moved.add(k)
+                    for i, v in enumerate(g.values):
+                        if v == name:
+                            l.repoint(i, after)
+                            self._moved.add(k)
         return self
 
     # -- running --------------------------------------------------------------
