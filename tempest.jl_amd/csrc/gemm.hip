@@ -79,7 +79,11 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
                "th_build_gemm: the GELU backward needs aux (8-byte aligned, ld >= m, ld % 4 == 0) and row_sums");
 
   const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
-  const bool check = (M % kTile) || (N % kTile) || (K % kDepth);
+  // Interior tiles read through 32-bit buffer offsets: operands past 2 GiB
+  // take the bounds-checked kernel, which addresses with 64-bit pointers.
+  const int64_t a_bytes = 2 * (la == kK ? (int64_t)(M - 1) * d->a_m + K : (int64_t)(K - 1) * d->a_k + M);
+  const int64_t b_bytes = 2 * (lb == kK ? (int64_t)(N - 1) * d->b_n + K : (int64_t)(K - 1) * d->b_k + N);
+  const bool check = (M % kTile) || (N % kTile) || (K % kDepth) || a_bytes > 0x7fffffff || b_bytes > 0x7fffffff;
   const void* fn = nullptr;
   const char* name = "";
   switch (epi) {

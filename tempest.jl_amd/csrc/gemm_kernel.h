@@ -80,13 +80,18 @@ __device__ __forceinline__ u32x2 pack4(const uint16_t (&h)[4]) {
   return u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
 }
 
+// tanh(u) = 1 - 2 / (exp(2u) + 1): one exponential and one reciprocal, exact
+// at both ends (exp overflows to inf: 1; underflows to 0: -1); its few-ulp
+// error is far below the bf16 rounding every caller applies after.
+__device__ __forceinline__ float fast_tanh(float u) { return 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f); }
+
 // GELU, tanh form (test/fixtures/programs.jl:19), and its derivative.
 __device__ __forceinline__ float gelu(float x) {
-  const float t = tanhf(0.7978846f * (x + 0.044715f * x * x * x));
+  const float t = fast_tanh(0.7978846f * (x + 0.044715f * x * x * x));
   return 0.5f * x * (1.0f + t);
 }
 __device__ __forceinline__ float gelu_grad(float x) {
-  const float t = tanhf(0.7978846f * (x + 0.044715f * x * x * x));
+  const float t = fast_tanh(0.7978846f * (x + 0.044715f * x * x * x));
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * 0.7978846f * (1.0f + 3.0f * 0.044715f * x * x);
 }
 
@@ -164,6 +169,94 @@ __device__ __forceinline__ void store_tile(uint16_t* lds, const u32x4 (&r)[8]) {
     store_mn(lds, r);
 }
 
+// Interior tiles load through a buffer resource: the operand's base in
+// scalar registers, each of the thread's eight 16-byte loads a 32-bit byte
+// offset fixed for the whole sweep, and the K tile's advance a scalar offset.
+// Operands stay under 2 GiB on this path (the builder checks).
+template <int L>
+struct Sweep {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[8];
+  uint32_t step;
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int64_t s_k, int o0) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+    if constexpr (L == kK) {
+      const int c = threadIdx.x % 8, row = threadIdx.x / 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) off[i] = (uint32_t)(((int64_t)(o0 + row + 32 * i) * s_o + 8 * c) * 2);
+      step = kDepth * 2;
+    } else {
+      const int kb = threadIdx.x % 8, ob = threadIdx.x / 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) off[i] = (uint32_t)(((int64_t)(o0 + 8 * ob) + (int64_t)(8 * kb + i) * s_k) * 2);
+      step = (uint32_t)(kDepth * s_k * 2);
+    }
+  }
+
+  __device__ __forceinline__ void load(int kt, u32x4 (&r)[8]) const {
+    const int s = (int)(kt * step);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (u32x4)__builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off[i], s, 0);
+  }
+};
+
+// The products of one K tile out of LDS stage `stage`: the fragments of the
+// next 16-deep step are read while the 16 products of this one issue, and,
+// when `land`, the registers of the next tile go to the other stage during
+// the last two steps, each LDS access placed between products.
+template <int LA, int LB>
+__device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t* Bs, uint16_t* As_next,
+                                              uint16_t* Bs_next, bool land, const u32x4 (&ra)[8],
+                                              const u32x4 (&rb)[8], f32x16 (&acc)[4][4], int wm, int wn,
+                                              int lr, int lh) {
+  const uint16_t* Ac = As + (wm * 128 + lr) * kRow + 8 * lh;
+  const uint16_t* Bc = Bs + (wn * 128 + lr) * kRow + 8 * lh;
+  bf16x8 af[2][4], bf[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) af[0][i] = *reinterpret_cast<const bf16x8*>(Ac + i * 32 * kRow);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bf[0][j] = *reinterpret_cast<const bf16x8*>(Bc + j * 32 * kRow);
+#pragma unroll
+  for (int kk = 0; kk < kDepth / 16; ++kk) {
+    const int s = kk & 1;
+    if (kk + 1 < kDepth / 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[s ^ 1][i] = *reinterpret_cast<const bf16x8*>(Ac + i * 32 * kRow + (kk + 1) * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[s ^ 1][j] = *reinterpret_cast<const bf16x8*>(Bc + j * 32 * kRow + (kk + 1) * 16);
+    }
+    if (land && kk == 2) store_tile<LA>(As_next, ra);
+    if (land && kk == 3) store_tile<LB>(Bs_next, rb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
+    if (kk < 2) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two products
+      }
+    } else if (kk == 2) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a product
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // one LDS write
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a product
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // one LDS write
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two products
+      }
+    }
+  }
+}
+
 // ---- the tile order ----------------------------------------------------------
 
 __device__ __forceinline__ void tile_of(int block, int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -201,42 +294,46 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
+  // Two register sets keep two K tiles in flight: while the waves multiply
+  // tile kt out of one LDS stage, tile kt+1 (loaded during the step before)
+  // lands in the other stage and tile kt+2's loads are issued.
   const int KT = (p.k + kDepth - 1) / kDepth;
-  u32x4 ra[8], rb[8];
-  load_tile<LA, CHECK>(p.a, p.a_o, p.a_k, m0, 0, p.m, p.k, ra);
-  load_tile<LB, CHECK>(p.b, p.b_o, p.b_k, n0, 0, p.n, p.k, rb);
-  store_tile<LA>(As, ra);
-  store_tile<LB>(Bs, rb);
-  __syncthreads();
+  Sweep<LA> sa;
+  Sweep<LB> sb;
+  if (!CHECK) {
+    sa.init(p.a, p.a_o, p.a_k, m0);
+    sb.init(p.b, p.b_o, p.b_k, n0);
+  }
+  u32x4 ra0[8], rb0[8], ra1[8], rb1[8];
+#define TH_FETCH(kt, ra, rb)                                                    \
+  do {                                                                          \
+    if (CHECK) {                                                                \
+      load_tile<LA, true>(p.a, p.a_o, p.a_k, m0, (kt) * kDepth, p.m, p.k, ra); \
+      load_tile<LB, true>(p.b, p.b_o, p.b_k, n0, (kt) * kDepth, p.n, p.k, rb); \
+    } else {                                                                    \
+      sa.load(kt, ra);                                                          \
+      sb.load(kt, rb);                                                          \
+    }                                                                           \
+  } while (0)
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      load_tile<LA, CHECK>(p.a, p.a_o, p.a_k, m0, (kt + 1) * kDepth, p.m, p.k, ra);
-      load_tile<LB, CHECK>(p.b, p.b_o, p.b_k, n0, (kt + 1) * kDepth, p.n, p.k, rb);
-    }
-    const uint16_t* Ac = As + cur * kStage + (wm * 128 + lr) * kRow + 8 * lh;
-    const uint16_t* Bc = Bs + cur * kStage + (wn * 128 + lr) * kRow + 8 * lh;
-#pragma unroll
-    for (int kk = 0; kk < kDepth / 16; ++kk) {
-      bf16x8 af[4], bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8*>(Ac + i * 32 * kRow + kk * 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(Bc + j * 32 * kRow + kk * 16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      store_tile<LA>(As + (cur ^ 1) * kStage, ra);
-      store_tile<LB>(Bs + (cur ^ 1) * kStage, rb);
-    }
+  TH_FETCH(0, ra0, rb0);
+  store_tile<LA>(As, ra0);
+  store_tile<LB>(Bs, rb0);
+  if (KT > 1) TH_FETCH(1, ra1, rb1);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    // Stage 0 holds tile kt; set 1 brings tile kt+1, set 0 is free.
+    if (kt + 2 < KT) TH_FETCH(kt + 2, ra0, rb0);
+    multiply_tile<LA, LB>(As, Bs, As + kStage, Bs + kStage, true, ra1, rb1, acc, wm, wn, lr, lh);
+    __syncthreads();
+    // Stage 1 holds tile kt+1; set 0 brings tile kt+2, set 1 is free.
+    if (kt + 3 < KT) TH_FETCH(kt + 3, ra1, rb1);
+    multiply_tile<LA, LB>(As + kStage, Bs + kStage, As, Bs, kt + 2 < KT, ra0, rb0, acc, wm, wn, lr, lh);
     __syncthreads();
   }
+  if (kt < KT) multiply_tile<LA, LB>(As, Bs, As + kStage, Bs + kStage, false, ra1, rb1, acc, wm, wn, lr, lh);
+#undef TH_FETCH
 
   // ---- epilogue: lane holds C(m, n) for n = n_j + lane % 32 and
   // m = m_i + 8 g + 4 (lane / 32) + (0..3), register 4 g + (0..3).
