@@ -266,6 +266,46 @@ typedef struct th_gemm_desc {
 
 int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
 
+/* ---- op class (c): causal flash attention ------------------------------- */
+
+/* Attention over (features, heads, positions, batch) column-major bf16 arrays
+ * (test/fixtures/operations.jl:5-70): element (d, h, s, b) of q, o, dout, dq
+ * at d + h*q_strides[0] + s*q_strides[1] + b*q_strides[2], of k, v, dk, dv at
+ * d + h*k_strides[0] + s*k_strides[1] + b*k_strides[2].  head_dim 128, seq a
+ * multiple of 128; query head h reads key/value head h / (heads / kv_heads).
+ * lse is fp32, (1, heads, positions, batch): element (h, s, b) at
+ * h + heads*(s + seq*b), the natural log-sum-exp of each query's scaled scores.
+ * scale <= 0 means 1/sqrt(head_dim). */
+typedef struct th_attention_desc {
+  int32_t batch, heads, kv_heads, seq, head_dim;
+  int32_t causal;
+  float scale;
+  int32_t reserved;
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t q_strides[3]; /* along heads, positions, batch */
+  int64_t k_strides[3];
+} th_attention_desc;
+
+/* o = softmax(scale * k'q, masked causal) * v per head, and lse (if non-NULL).
+ * Values: 0 q, 1 k, 2 v, 3 o, 4 lse.  Replaces the cuTile online-softmax
+ * product sweep (ext/cuTileExt/build.jl:326-532) and cuDNNAttention's SDPA
+ * forward (ext/cuDNNExt.jl:38-55,116-210). */
+int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
+
+/* dq, dk, dv from q, k, v, o, lse (as the forward wrote them) and dout;
+ * deterministic (no atomics), kv_heads == heads.
+ * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 dout, 6 dq, 7 dk, 8 dv.  Replaces the
+ * cuTile transposed folds of the backward (ext/cuTileExt/transpose.jl:1-213). */
+int th_build_attention_bwd(const th_attention_desc* desc, th_launch** host_out);
+
 #ifdef __cplusplus
 }
 #endif

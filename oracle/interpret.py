@@ -116,3 +116,48 @@ def mlp_grad(W1, b1, W2, b2, x):
     db1 = dz.sum(axis=1)
     dx = W1.T @ dz
     return loss, dW1, db1, dW2, db2, dx
+
+
+def attention_fwd(q, k, v, causal=True, scale=None):
+    """attention(q, k, v; causal, scale) of test/fixtures/operations.jl:21-70 in
+    float64.  Arrays are numpy (batch, positions, heads, d): the memory of the
+    reference's (d, heads, positions, batch) column-major arrays.  Query head h
+    reads key/value head h // (heads // kv_heads).  Returns (o, lse), lse
+    (batch, positions, heads)."""
+    q, k, v = (np.asarray(a, dtype=np.float64) for a in (q, k, v))
+    B, S, H, D = q.shape
+    Hk = k.shape[2]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    kk = np.repeat(k, H // Hk, axis=2)
+    vv = np.repeat(v, H // Hk, axis=2)
+    s = np.einsum("bmhd,bnhd->bhmn", q, kk) * scale
+    if causal:
+        mask = np.arange(S)[None, :] > np.arange(S)[:, None]  # key n after query m
+        s = np.where(mask[None, None], -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    l = e.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhmn,bnhd->bmhd", e / l, vv)
+    lse = (m + np.log(l))[..., 0].transpose(0, 2, 1)
+    return o, lse
+
+
+def attention_bwd(q, k, v, dout, causal=True, scale=None):
+    """Gradients of sum(attention(q, k, v) .* dout) w.r.t. q, k, v in float64
+    (kv_heads == heads), same layout as attention_fwd."""
+    q, k, v, dout = (np.asarray(a, dtype=np.float64) for a in (q, k, v, dout))
+    B, S, H, D = q.shape
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    s = np.einsum("bmhd,bnhd->bhmn", q, k) * scale
+    if causal:
+        mask = np.arange(S)[None, :] > np.arange(S)[:, None]
+        s = np.where(mask[None, None], -np.inf, s)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    g = np.einsum("bmhd->bhmd", dout)
+    dv = np.einsum("bhmn,bhmd->bnhd", p, g)
+    dp = np.einsum("bhmd,bnhd->bhmn", g, v)
+    ds = p * (dp - (dp * p).sum(axis=-1, keepdims=True))
+    dq = np.einsum("bhmn,bnhd->bmhd", ds, k) * scale
+    dk = np.einsum("bhmn,bmhd->bnhd", ds, q) * scale
+    return dq, dk, dv

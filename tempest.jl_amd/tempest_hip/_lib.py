@@ -45,6 +45,14 @@ class GemmDesc(ctypes.Structure):
                 ("loss", c_void_p)]
 
 
+class AttentionDesc(ctypes.Structure):
+    """th_attention_desc (include/tempest_hip.h)."""
+    _fields_ = [("batch", c_i32), ("heads", c_i32), ("kv_heads", c_i32), ("seq", c_i32), ("head_dim", c_i32),
+                ("causal", c_i32), ("scale", c_f32), ("reserved", c_i32), ("q", c_void_p), ("k", c_void_p),
+                ("v", c_void_p), ("o", c_void_p), ("lse", c_void_p), ("dout", c_void_p), ("dq", c_void_p),
+                ("dk", c_void_p), ("dv", c_void_p), ("q_strides", c_i64 * 3), ("k_strides", c_i64 * 3)]
+
+
 class HIPError(RuntimeError):
     """A libtempest_hip entry point returned a non-zero status."""
 
@@ -90,6 +98,8 @@ SIGNATURES: dict[str, list] = {
     "th_build_layernorm_fwd": [c_i64, c_i32, c_i64, c_f32, c_void_p, c_void_p, P(c_void_p)],
     "th_build_sum": [c_i64, c_void_p, c_void_p, P(c_void_p)],
     "th_build_gemm": [P(GemmDesc), P(c_void_p)],
+    "th_build_attention_fwd": [P(AttentionDesc), P(c_void_p)],
+    "th_build_attention_bwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, P(c_void_p)],
 }

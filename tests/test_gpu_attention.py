@@ -1,0 +1,85 @@
+"""Op class (c) on the GPU: flash attention forward and backward against the
+oracle (float64 on the same bf16 inputs), causal and not, grouped heads, and
+config 4's full size on sampled heads."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import interpret
+from oracle.data import relative
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2  # bf16 attention: 2e-2 relative (norm-wise) of the fp64 reference
+
+
+def _rand(shape, gen):
+    return torch.randn(*shape, device="cuda", generator=gen).to(torch.bfloat16)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("B,H,Hk,S,causal", [(1, 2, 2, 128, True), (2, 3, 3, 384, True), (1, 2, 2, 256, False),
+                                             (1, 4, 2, 256, True), (1, 1, 1, 1024, True)])
+def test_forward_matches_oracle(target, B, H, Hk, S, causal):
+    import tempest_hip.launch as L
+    announce("attn fwd", B, H, Hk, S, causal)
+    gen = torch.Generator(device="cuda").manual_seed(S + H)
+    q, k, v = _rand((B, S, H, 128), gen), _rand((B, S, Hk, 128), gen), _rand((B, S, Hk, 128), gen)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, S, H, device="cuda")
+    l = L.attention_fwd(B, H, Hk, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                        causal=causal)
+    l()
+    torch.cuda.synchronize()
+    ro, rl = interpret.attention_fwd(_np(q), _np(k), _np(v), causal)
+    assert relative(_np(o), ro) < TOL
+    assert np.max(np.abs(lse.cpu().numpy() - rl)) < 1e-3 * max(1.0, np.abs(rl).max())
+
+
+@pytest.mark.parametrize("B,H,S,causal", [(1, 2, 128, True), (2, 2, 384, True), (1, 2, 256, False),
+                                          (1, 1, 1024, True)])
+def test_backward_matches_oracle(target, B, H, S, causal):
+    import tempest_hip as th
+    announce("attn bwd", B, H, S, causal)
+    gen = torch.Generator(device="cuda").manual_seed(7 * S + H)
+    q, k, v, g = (_rand((B, S, H, 128), gen) for _ in range(4))
+    comp = th.compile(th.programs.attention(B, H, S, causal=causal), target, q, k, v, g)
+    o, dq, dk, dv = comp(q, k, v, g)
+    ro, _ = interpret.attention_fwd(_np(q), _np(k), _np(v), causal)
+    rq, rk, rv = interpret.attention_bwd(_np(q), _np(k), _np(v), _np(g), causal)
+    assert relative(_np(o.view(B, S, H, 128)), ro) < TOL
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert relative(_np(got.view(B, S, H, 128)), ref) < TOL, name
+
+
+def test_refuses_other_head_dims(target):
+    import tempest_hip.launch as L
+    from tempest_hip import HIPError
+    t = torch.zeros(1, 128, 1, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(HIPError, match="head_dim"):
+        L.attention_fwd(1, 1, 1, 128, t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(), head_dim=64)
+    with pytest.raises(HIPError, match="multiple of 128"):
+        L.attention_fwd(1, 1, 1, 100, t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr())
+
+
+def test_config4_full_size_sampled_heads(target):
+    """B8 H16 S4096 D128 causal: every output computed on the GPU; sampled
+    (batch, head) pairs checked against the float64 oracle."""
+    import tempest_hip as th
+    announce("attn config4 full")
+    B, H, S = 8, 16, 4096
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v, g = (_rand((B, S, H, 128), gen) for _ in range(4))
+    comp = th.compile(th.programs.attention(B, H, S), target, q, k, v, g)
+    o, dq, dk, dv = comp(q, k, v, g)
+    for b, h in ((0, 0), (5, 11)):
+        sl = lambda t: _np(t.view(B, S, H, 128)[b:b + 1, :, h:h + 1])  # noqa: E731
+        ro, _ = interpret.attention_fwd(sl(q), sl(k), sl(v), True)
+        rq, rk, rv = interpret.attention_bwd(sl(q), sl(k), sl(v), sl(g), True)
+        assert relative(sl(o), ro) < TOL
+        for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            assert relative(sl(got), ref) < TOL, (b, h, name)

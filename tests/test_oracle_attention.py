@@ -1,0 +1,55 @@
+"""Config 4's oracle (attention forward and backward) against torch: the
+scaled-dot-product definition in float64 and autograd for the gradients."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import interpret
+from oracle.data import relative
+
+
+def _torch_attention(q, k, v, causal, scale):
+    # (b, s, h, d) -> (b, h, s, d)
+    qt, kt, vt = (x.permute(0, 2, 1, 3) for x in (q, k, v))
+    s = qt @ kt.transpose(-1, -2) * scale
+    if causal:
+        S = s.shape[-1]
+        s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    return (torch.softmax(s, dim=-1) @ vt).permute(0, 2, 1, 3), torch.logsumexp(s, dim=-1).permute(0, 2, 1)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_and_backward_match_torch(causal):
+    rng = np.random.default_rng(0)
+    B, S, H, D = 2, 9, 3, 8
+    q, k, v, g = (rng.normal(size=(B, S, H, D)) for _ in range(4))
+    o, lse = interpret.attention_fwd(q, k, v, causal)
+    t = [torch.tensor(a, requires_grad=True) for a in (q, k, v)]
+    ot, lt = _torch_attention(*t, causal, 1 / np.sqrt(D))
+    assert relative(o, ot.detach().numpy()) < 1e-13 and relative(lse, lt.detach().numpy()) < 1e-13
+    (ot * torch.tensor(g)).sum().backward()
+    dq, dk, dv = interpret.attention_bwd(q, k, v, g, causal)
+    for ours, tt in zip((dq, dk, dv), t):
+        assert relative(ours, tt.grad.numpy()) < 1e-12
+
+
+def test_grouped_heads_read_their_group():
+    rng = np.random.default_rng(1)
+    q = rng.normal(size=(1, 5, 4, 8))
+    k, v = rng.normal(size=(1, 5, 2, 8)), rng.normal(size=(1, 5, 2, 8))
+    o, _ = interpret.attention_fwd(q, k, v, True)
+    o2, _ = interpret.attention_fwd(q, np.repeat(k, 2, axis=2), np.repeat(v, 2, axis=2), True)
+    assert np.allclose(o, o2)
+    # Head 3 reads kv head 1: changing kv head 0 leaves it alone.
+    k2 = k.copy()
+    k2[:, :, 0] = rng.normal(size=k2[:, :, 0].shape)
+    o3, _ = interpret.attention_fwd(q, k2, v, True)
+    assert np.allclose(o3[:, :, 2:], o[:, :, 2:]) and not np.allclose(o3[:, :, :2], o[:, :, :2])
+
+
+def test_causal_first_query_reads_only_the_first_key():
+    rng = np.random.default_rng(2)
+    q, k, v = (rng.normal(size=(1, 4, 1, 8)) for _ in range(3))
+    o, lse = interpret.attention_fwd(q, k, v, True)
+    assert np.allclose(o[0, 0, 0], v[0, 0, 0])
+    assert np.isclose(lse[0, 0, 0], (q[0, 0, 0] @ k[0, 0, 0]) / np.sqrt(8))
