@@ -180,6 +180,43 @@ def config3(target, steps: int = 5, warmup: int = 2):
             "frac_of_bf16_peak": flops / step_s / BF16_PEAK, "flops_per_step": flops, "per_launch": per}
 
 
+def config4(target, steps: int = 3, warmup: int = 1):
+    """Causal attention fwd+bwd, B8 H16 S4096 D128 bf16: 1.924e12 flops a step
+    (forward 4 B H S^2 D / 2, backward 2.5x that)."""
+    import torch
+    import tempest_hip as th
+
+    B, H, S, D = 8, 16, 4096, 128
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v, g = (torch.randn(B, S, H, D, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
+    comp = th.compile(th.programs.attention(B, H, S), target, q, k, v, g)
+    ex = comp.executable
+    fwd, bwd = ex.launches
+    f_fwd, f_bwd = fwd.work().flops, bwd.work().flops
+    for _ in range(warmup):
+        ex.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    t_f = t_b = 0.0
+    for _ in range(steps):
+        ev[0].record()
+        fwd()
+        ev[1].record()
+        bwd()
+        ev[2].record()
+        torch.cuda.synchronize()
+        t_f += ev[0].elapsed_time(ev[1]) * 1e-3
+        t_b += ev[1].elapsed_time(ev[2]) * 1e-3
+    t_f /= steps
+    t_b /= steps
+    total = f_fwd + f_bwd
+    return {"ms_per_step": (t_f + t_b) * 1e3, "TFLOP/s": total / (t_f + t_b) / 1e12,
+            "frac_of_bf16_peak": total / (t_f + t_b) / BF16_PEAK, "flops_per_step": total,
+            "fwd": {"ms": t_f * 1e3, "TFLOP/s": f_fwd / t_f / 1e12},
+            "bwd": {"ms": t_b * 1e3, "TFLOP/s": f_bwd / t_b / 1e12,
+                    "note": "FA2 convention, 2.5x forward flops; the deterministic dQ sweep recomputes S and dP"}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +275,11 @@ def main() -> int:
         except Exception as err:
             configs["config3_mlp"] = {"error": repr(err)}
         log("config3:", json.dumps(configs["config3_mlp"]))
+        try:
+            configs["config4_attention"] = config4(target)
+        except Exception as err:
+            configs["config4_attention"] = {"error": repr(err)}
+        log("config4:", json.dumps(configs["config4_attention"]))
     cpu = None
     if not (a.no_cpu or a.only_config2):
         try:

@@ -65,12 +65,8 @@ struct AttnArgs {
   float scale;  // 1 / sqrt(d) unless given
 };
 
-__device__ __forceinline__ uint16_t bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// Round to bf16, nearest even (one v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);

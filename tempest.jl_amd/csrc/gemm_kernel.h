@@ -65,12 +65,8 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;
 };
 
-__device__ __forceinline__ uint16_t bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
-  u += 0x7fffu + ((u >> 16) & 1u);                                              // to nearest even
-  return (uint16_t)(u >> 16);
-}
+// Round to bf16, nearest even (one v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -83,7 +79,9 @@ __device__ __forceinline__ u32x2 pack4(const uint16_t (&h)[4]) {
 // tanh(u) = 1 - 2 / (exp(2u) + 1): one exponential and one reciprocal, exact
 // at both ends (exp overflows to inf: 1; underflows to 0: -1); its few-ulp
 // error is far below the bf16 rounding every caller applies after.
-__device__ __forceinline__ float fast_tanh(float u) { return 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f); }
+__device__ __forceinline__ float fast_tanh(float u) {
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * u) + 1.0f);
+}
 
 // GELU, tanh form (test/fixtures/programs.jl:19), and its derivative.
 __device__ __forceinline__ float gelu(float x) {
@@ -283,10 +281,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   uint16_t* Bs = lds + 2 * kStage;
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
-  const int m0 = tm * kTile, n0 = tn * kTile;
+  int m0 = tm * kTile, n0 = tn * kTile;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int wm = wave / 2, wn = wave % 2;
-  const int lr = lane % 32, lh = lane / 32;
+  int lr = lane % 32, lh = lane / 32;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -337,6 +335,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 
   // ---- epilogue: lane holds C(m, n) for n = n_j + lane % 32 and
   // m = m_i + 8 g + 4 (lane / 32) + (0..3), register 4 g + (0..3).
+  // The epilogue's indices are derived from opaque copies made here, so that
+  // none of its address arithmetic is hoisted above the main loop, where
+  // every register is taken.
+  {
+    int lane_e = lane, m0_e = m0, n0_e = n0;
+    asm volatile("" : "+v"(lane_e));
+    asm volatile("" : "+s"(m0_e), "+s"(n0_e));
+    lr = lane_e % 32, lh = lane_e / 32;
+    m0 = m0_e, n0 = n0_e;
+  }
   constexpr bool kSums = EPI == kSquareLoss || EPI == kGeluBackward;
   float loss = 0.0f;
 #pragma unroll
