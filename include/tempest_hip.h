@@ -306,6 +306,44 @@ int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
  * cuTile transposed folds of the backward (ext/cuTileExt/transpose.jl:1-213). */
 int th_build_attention_bwd(const th_attention_desc* desc, th_launch** host_out);
 
+/* ---- config 5: chunked gated DeltaNet (scan + recurrence) ---------------- */
+
+/* The gated delta rule per (batch, head) sequence, S (dk x dv) from zero:
+ *   S = exp(a_t) (I - beta_t k_t k_t') S + beta_t k_t v_t',  o_t = S' q_t
+ * (examples/deltanet.jl:89-101), computed in chunks of 64 positions as
+ * examples/deltanet.jl:58-86 writes it.  q, k, v, o, dout, dq, dk_out, dv_out
+ * are bf16 (d, heads, positions, batch): element (d, h, t, b) at
+ * d + h*strides[0] + t*strides[1] + b*strides[2]; a (the log-gates) and beta,
+ * da, dbeta are fp32 (heads, positions, batch) at gate_strides.  dk = dv =
+ * 128, chunk 64, seq a multiple of 64.  The gradient is of
+ * sum(o .* dout) with respect to q, k, v, a and beta.
+ * Values: 0 q, 1 k, 2 v, 3 a, 4 beta, 5 o, 6 dout, 7 dq, 8 dk, 9 dv, 10 da,
+ * 11 dbeta.  Replaces the scan and recurrence sketches (ext/cuTileExt/
+ * build.jl:715-839; codegen/scalar.jl:354-440; runtime/stepped.jl). */
+typedef struct th_deltanet_desc {
+  int32_t batch, heads, seq, dk, dv, chunk;
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* a;
+  const float* beta;
+  void* o;
+  const void* dout;
+  void* dq;
+  void* dk_out;
+  void* dv_out;
+  float* da;
+  float* dbeta;
+  int64_t strides[3];      /* along heads, positions, batch */
+  int64_t gate_strides[3]; /* along heads, positions, batch */
+} th_deltanet_desc;
+
+/* The forward alone (o). */
+int th_build_deltanet_fwd(const th_deltanet_desc* desc, th_launch** host_out);
+
+/* The forward and the gradient (o, dq, dk, dv, da, dbeta) in one launch. */
+int th_build_deltanet(const th_deltanet_desc* desc, th_launch** host_out);
+
 #ifdef __cplusplus
 }
 #endif

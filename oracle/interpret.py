@@ -161,3 +161,137 @@ def attention_bwd(q, k, v, dout, causal=True, scale=None):
     dq = np.einsum("bhmn,bnhd->bmhd", ds, k) * scale
     dk = np.einsum("bhmn,bmhd->bnhd", ds, q) * scale
     return dq, dk, dv
+
+
+# ---- config 5: gated DeltaNet -------------------------------------------------------
+# Arrays are numpy (batch, positions, heads, d) for q, k, v, o and (batch,
+# positions, heads) for the log-gates a and the strengths beta: the memory of
+# the program's (d, heads, positions, batch) and (heads, positions, batch)
+# column-major arrays.
+
+
+def deltanet_sequential(q, k, v, a, beta):
+    """The gated delta rule token by token (examples/deltanet.jl:89-101):
+    S = exp(a) (I - beta k k') S + beta k v', o = S' q, S starting at zero."""
+    q, k, v, a, beta = (np.asarray(x, dtype=np.float64) for x in (q, k, v, a, beta))
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    o = np.zeros((B, T, H, dv))
+    S = np.zeros((B, H, dk, dv))
+    for t in range(T):
+        kt, vt, qt = k[:, t], v[:, t], q[:, t]                      # (B, H, d)
+        bt, gt = beta[:, t][..., None, None], np.exp(a[:, t])[..., None, None]
+        kS = np.einsum("bhk,bhkv->bhv", kt, S)
+        S = gt * (S - bt * kt[..., :, None] * kS[..., None, :]) + bt * kt[..., :, None] * vt[..., None, :]
+        o[:, t] = np.einsum("bhkv,bhk->bhv", S, qt)
+    return o
+
+
+def _chunks(x, C):
+    """(B, T, H, ...) -> (B, H, N, C, ...)."""
+    B, T, H = x.shape[:3]
+    y = x.reshape((B, T // C, C, H) + x.shape[3:])
+    return np.moveaxis(y, 3, 1)
+
+
+def _unchunks(y):
+    """(B, H, N, C, ...) -> (B, T, H, ...)."""
+    B, H, N, C = y.shape[:4]
+    return np.moveaxis(y, 1, 3).reshape((B, N * C, H) + y.shape[4:])
+
+
+def _chunk_prep(q, k, v, a, beta, C):
+    """The chunk-local quantities of examples/deltanet.jl:58-86 (WY form)."""
+    Q, K, V = _chunks(q, C), _chunks(k, C), _chunks(v, C)          # (B, H, N, C, d)
+    A_, Bt = _chunks(a, C), _chunks(beta, C)                      # (B, H, N, C)
+    ca = np.cumsum(A_, axis=-1)
+    gam = np.exp(ca[..., :, None] - ca[..., None, :])            # Gamma[i, j] = exp(ca_i - ca_j)
+    strict = np.tril(np.ones((C, C)), -1)
+    lower = np.tril(np.ones((C, C)))
+    G = K @ np.swapaxes(K, -1, -2)
+    Am = Bt[..., :, None] * gam * G * strict
+    T_ = np.linalg.inv(np.eye(C) + Am)
+    X = (Bt * np.exp(ca))[..., None] * K
+    Y = Bt[..., None] * V
+    W, Ut = T_ @ X, T_ @ Y
+    QK = Q @ np.swapaxes(K, -1, -2)
+    P = gam * QK * lower
+    Qg = np.exp(ca)[..., None] * Q
+    Kd = np.exp(ca[..., -1:] - ca)[..., None] * K
+    g = np.exp(ca[..., -1])
+    return dict(Q=Q, K=K, V=V, Bt=Bt, ca=ca, gam=gam, G=G, T=T_, X=X, Y=Y, W=W, Ut=Ut, QK=QK, P=P, Qg=Qg, Kd=Kd,
+                g=g, strict=strict, lower=lower)
+
+
+def deltanet_chunked(q, k, v, a, beta, C=64, keep=False):
+    """The chunked form (examples/deltanet.jl:58-86): within a chunk products,
+    across chunks the state S carried: U = U~ - W S, O = Qg S + P U,
+    S <- g S + Kd' U."""
+    c = _chunk_prep(q, k, v, a, beta, C)
+    B, H, N = c["Q"].shape[:3]
+    dk, dv = c["K"].shape[-1], c["V"].shape[-1]
+    S = np.zeros((B, H, dk, dv))
+    O = np.zeros(c["V"].shape)
+    Ss, Us = [], []
+    for n in range(N):
+        Ss.append(S)
+        U = c["Ut"][:, :, n] - c["W"][:, :, n] @ S
+        Us.append(U)
+        O[:, :, n] = c["Qg"][:, :, n] @ S + c["P"][:, :, n] @ U
+        S = c["g"][:, :, n][..., None, None] * S + np.swapaxes(c["Kd"][:, :, n], -1, -2) @ U
+    o = _unchunks(O)
+    if keep:
+        c.update(S=np.stack(Ss, axis=2), U=np.stack(Us, axis=2))
+        return o, c
+    return o
+
+
+def deltanet_grad(q, k, v, a, beta, do, C=64):
+    """Gradients of sum(deltanet(q, k, v, a, beta) .* do) w.r.t. q, k, v, a
+    and beta, in float64: the reverse of the chunked form (state gradient
+    swept back over chunks, then each chunk's products, the WY inverse
+    T = (I + A)^-1 (dA = -T' dT T'), the decays exp(ca_i - ca_j) and the
+    within-chunk cumulative sum of a)."""
+    o, c = deltanet_chunked(q, k, v, a, beta, C, keep=True)
+    dO = _chunks(np.asarray(do, dtype=np.float64), C)
+    B, H, N = dO.shape[:3]
+    dk = c["K"].shape[-1]
+    dv = dO.shape[-1]
+    tr = lambda x: np.swapaxes(x, -1, -2)  # noqa: E731
+    dS = np.zeros((B, H, dk, dv))
+    dU = np.zeros_like(c["U"])
+    dSn = np.zeros_like(c["S"])  # gradient at each chunk's end state S_{n+1}
+    for n in reversed(range(N)):
+        dSn[:, :, n] = dS
+        du = tr(c["P"][:, :, n]) @ dO[:, :, n] + c["Kd"][:, :, n] @ dS
+        dU[:, :, n] = du
+        dS = tr(c["Qg"][:, :, n]) @ dO[:, :, n] + c["g"][:, :, n][..., None, None] * dS - tr(c["W"][:, :, n]) @ du
+    S, U = c["S"], c["U"]
+    dQg = dO @ tr(S)
+    dP = (dO @ tr(U)) * c["lower"]
+    dKd = U @ tr(dSn)
+    dg = np.einsum("bhnkv,bhnkv->bhn", S, dSn)
+    dW = -dU @ tr(S)
+    dUt = dU
+    T_ = c["T"]
+    dT = dW @ tr(c["X"]) + dUt @ tr(c["Y"])
+    dX = tr(T_) @ dW
+    dY = tr(T_) @ dUt
+    dA = -(tr(T_) @ dT @ tr(T_)) * c["strict"]
+    Bt, ca, gam, G, K, Q, V = c["Bt"], c["ca"], c["gam"], c["G"], c["K"], c["Q"], c["V"]
+    dG = dA * Bt[..., :, None] * gam
+    dQK = dP * gam
+    dQ = np.exp(ca)[..., None] * dQg + dQK @ K
+    dK = tr(dQK) @ Q + (dG + tr(dG)) @ K + (Bt * np.exp(ca))[..., None] * dX + np.exp(ca[..., -1:] - ca)[..., None] * dKd
+    dV = Bt[..., None] * dY
+    dBt = (dA * gam * G).sum(-1) + np.exp(ca) * (K * dX).sum(-1) + (V * dY).sum(-1)
+    dgam = dA * Bt[..., :, None] * G + dP * c["QK"]
+    w = dgam * gam
+    dca = w.sum(-1) - w.sum(-2)
+    dca += Bt * np.exp(ca) * (K * dX).sum(-1)
+    dca += np.exp(ca) * (Q * dQg).sum(-1)
+    kd = np.exp(ca[..., -1:] - ca) * (K * dKd).sum(-1)
+    dca -= kd
+    dca[..., -1] += kd.sum(-1) + dg * c["g"]
+    da = np.flip(np.cumsum(np.flip(dca, -1), -1), -1)
+    return _unchunks(dQ), _unchunks(dK), _unchunks(dV), _unchunks(da), _unchunks(dBt)

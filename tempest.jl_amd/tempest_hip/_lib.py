@@ -53,6 +53,14 @@ class AttentionDesc(ctypes.Structure):
                 ("dk", c_void_p), ("dv", c_void_p), ("q_strides", c_i64 * 3), ("k_strides", c_i64 * 3)]
 
 
+class DeltaNetDesc(ctypes.Structure):
+    """th_deltanet_desc (include/tempest_hip.h)."""
+    _fields_ = [("batch", c_i32), ("heads", c_i32), ("seq", c_i32), ("dk", c_i32), ("dv", c_i32), ("chunk", c_i32),
+                ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("a", c_void_p), ("beta", c_void_p),
+                ("o", c_void_p), ("dout", c_void_p), ("dq", c_void_p), ("dk_out", c_void_p), ("dv_out", c_void_p),
+                ("da", c_void_p), ("dbeta", c_void_p), ("strides", c_i64 * 3), ("gate_strides", c_i64 * 3)]
+
+
 class HIPError(RuntimeError):
     """A libtempest_hip entry point returned a non-zero status."""
 
@@ -100,6 +108,8 @@ SIGNATURES: dict[str, list] = {
     "th_build_gemm": [P(GemmDesc), P(c_void_p)],
     "th_build_attention_fwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_attention_bwd": [P(AttentionDesc), P(c_void_p)],
+    "th_build_deltanet_fwd": [P(DeltaNetDesc), P(c_void_p)],
+    "th_build_deltanet": [P(DeltaNetDesc), P(c_void_p)],
     "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, P(c_void_p)],
 }

@@ -141,3 +141,19 @@ def attention_bwd(batch: int, heads: int, seq: int, q: int, k: int, v: int, o: i
     d = _attention_desc(batch, heads, heads, seq, q, k, v, o, lse, dout, dq, dk, dv, causal=causal, scale=scale,
                         **strides)
     return _built("th_build_attention_bwd", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"), ctypes.byref(d))
+
+
+# ---- config 5 ---------------------------------------------------------------
+
+def deltanet(batch: int, heads: int, seq: int, q: int, k: int, v: int, a: int, beta: int, o: int, dout: int = 0,
+             dq: int = 0, dk: int = 0, dv: int = 0, da: int = 0, dbeta: int = 0, d: int = 128) -> Launch:
+    """Chunked gated DeltaNet over (d, heads, positions, batch) bf16 arrays and
+    (heads, positions, batch) fp32 gates; the gradient too when dout is given."""
+    desc = _lib.DeltaNetDesc(batch=batch, heads=heads, seq=seq, dk=d, dv=d, chunk=64, q=q, k=k, v=v, a=a, beta=beta,
+                             o=o, dout=dout or None, dq=dq or None, dk_out=dk or None, dv_out=dv or None,
+                             da=da or None, dbeta=dbeta or None)
+    desc.strides[:] = [d, heads * d, seq * heads * d]
+    desc.gate_strides[:] = [1, heads, seq * heads]
+    name = "th_build_deltanet" if dout else "th_build_deltanet_fwd"
+    return _built(name, ("q", "k", "v", "a", "beta", "o", "dout", "dq", "dk", "dv", "da", "dbeta"),
+                  ctypes.byref(desc))

@@ -135,3 +135,27 @@ def attention(batch: int = 8, heads: int = 16, seq: int = 4096, head_dim: int = 
                 lambda a: L.attention_bwd(batch, heads, seq, a["q"], a["k"], a["v"], a["o"], a["lse"], a["dout"],
                                           a["dq"], a["dk"], a["dv"], causal=causal))
     return Program("attention", values, [fwd, bwd], ["q", "k", "v", "dout"], ["o", "dq", "dk", "dv"])
+
+
+def deltanet(batch: int = 4, heads: int = 16, seq: int = 8192, d: int = 128) -> Program:
+    """Config 5: (q, k, v, a, beta, dout) -> o = gated DeltaNet (chunks of 64)
+    and the gradients of sum(o .* dout) w.r.t. q, k, v, a, beta.  q, k, v bf16
+    (d, heads, positions, batch); a (log-gates) and beta fp32 (heads,
+    positions, batch).  Plan: one group, its chunk-local products, the
+    recurrence across chunks and their gradients (examples/deltanet.jl:58-86)."""
+    bf, f32 = torch.bfloat16, torch.float32
+    dims, gdims = (d, heads, seq, batch), (heads, seq, batch)
+    values = {
+        "q": Value("q", bf, dims, "input"), "k": Value("k", bf, dims, "input"), "v": Value("v", bf, dims, "input"),
+        "a": Value("a", f32, gdims, "input"), "beta": Value("beta", f32, gdims, "input"),
+        "dout": Value("dout", bf, dims, "input"),
+        "o": Value("o", bf, dims, "result"), "dq": Value("dq", bf, dims, "result"),
+        "dk": Value("dk", bf, dims, "result"), "dv": Value("dv", bf, dims, "result"),
+        "da": Value("da", f32, gdims, "result"), "dbeta": Value("dbeta", f32, gdims, "result"),
+    }
+    names = ("q", "k", "v", "a", "beta", "o", "dout", "dq", "dk", "dv", "da", "dbeta")
+    group = Group("o = deltanet(q, k, v, a, beta) and its gradient", names,
+                  ("q", "k", "v", "a", "beta", "dout"), ("o", "dq", "dk", "dv", "da", "dbeta"),
+                  lambda x: L.deltanet(batch, heads, seq, *(x[n] for n in names), d=d))
+    return Program("deltanet", values, [group], ["q", "k", "v", "a", "beta", "dout"],
+                   ["o", "dq", "dk", "dv", "da", "dbeta"])
