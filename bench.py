@@ -217,6 +217,39 @@ def config4(target, steps: int = 3, warmup: int = 1):
                     "note": "FA2 convention, 2.5x forward flops; the deterministic dQ sweep recomputes S and dP"}}
 
 
+def config5(target, steps: int = 3, warmup: int = 1):
+    """Chunked gated DeltaNet forward + gradient, B4 H16 T8192, d 128, chunk 64."""
+    import torch
+    import tempest_hip as th
+
+    B, H, T = 4, 16, 8192
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    r = lambda *s: torch.randn(*s, device="cuda", generator=gen)  # noqa: E731
+    unit = lambda x: x / x.norm(dim=-1, keepdim=True)  # noqa: E731
+    q, k = unit(r(B, T, H, 128)).to(torch.bfloat16), unit(r(B, T, H, 128)).to(torch.bfloat16)
+    v, do = r(B, T, H, 128).to(torch.bfloat16), r(B, T, H, 128).to(torch.bfloat16)
+    a = (-torch.nn.functional.softplus(r(B, T, H))).contiguous()
+    beta = torch.sigmoid(r(B, T, H)).contiguous()
+    comp = th.compile(th.programs.deltanet(B, H, T), target, q, k, v, a, beta, do)
+    ex = comp.executable
+    (l,) = ex.launches
+    w = l.work()
+    for _ in range(warmup):
+        ex.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ex.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) * 1e-3 / steps
+    return {"ms_per_step": s * 1e3, "TFLOP/s": w.flops / s / 1e12, "GB/s": w.bytes / s / 1e9,
+            "flops_per_step": w.flops, "bytes_per_step": w.bytes,
+            "note": "fp32 FMA kernels (chunk prep, column-split state scan, outputs, reverse state-gradient "
+                    "scan, chunk-local backward); flops/bytes are the algorithmic estimates of th_launch_work"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +313,11 @@ def main() -> int:
         except Exception as err:
             configs["config4_attention"] = {"error": repr(err)}
         log("config4:", json.dumps(configs["config4_attention"]))
+        try:
+            configs["config5_deltanet"] = config5(target)
+        except Exception as err:
+            configs["config5_deltanet"] = {"error": repr(err)}
+        log("config5:", json.dumps(configs["config5_deltanet"]))
     cpu = None
     if not (a.no_cpu or a.only_config2):
         try:
