@@ -196,39 +196,44 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
       for (int j = 0; j < 2; ++j) s[j] = mfma(frag_rows(Ks(st), 32 * j, ks), qf[ks], s[j]);
-    // Scale, mask, and the running maximum of this lane's query.
+    // Mask (diagonal blocks only), and the running maximum of this lane's
+    // query in scaled units (the scale is positive, so max commutes with it).
     const int key0 = kb * kFwdK;
-    const bool diagonal = p.causal && key0 + kFwdK > q0;
+    if (p.causal && key0 + kFwdK > q0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = key0 + 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
+          if (key > query) s[j][i] = -INFINITY;
+        }
+    }
     float mb = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = s[j][i] * c;
-        if (diagonal) {
-          const int key = key0 + 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-          if (key > query) v = -INFINITY;
-        }
-        s[j][i] = v;
-        mb = fmaxf(mb, v);
-      }
-    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[j][i]);
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * c;
     const float mn = fmaxf(m, mb);
     const float shift = isfinite(mn) ? mn : 0.0f;
-    const float alpha = exp2f(m - shift);
     float ls = 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float w = exp2f(s[j][i] - shift);
+        const float w = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -shift));
         s[j][i] = w;
         ls += w;
       }
-    l = l * alpha + ls;
-    m = mn;
+    // Rescale only when some query's maximum grew.
+    if (__ballot(mn > m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - shift);
+      l *= alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      for (int i = 0; i < 4; ++i) o[i] *= alpha;
+    }
+    l += ls;
+    m = mn;
     // O' (128 d x 32 queries) += V' P', the weights rounded to bf16.
     bf16x8 pf[4] = {rows_operand(s[0], 0), rows_operand(s[0], 1), rows_operand(s[1], 0), rows_operand(s[1], 1)};
 #pragma unroll
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int qi = 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-        float pv = exp2f(s[j][i] * c - L[qi]);
+        float pv = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -L[qi]));
         if (diagonal && key > qq0 + qi) pv = 0.0f;
         s[j][i] = pv;                          // P
         dp[j][i] = pv * (dp[j][i] - Dl[qi]);   // dS
@@ -474,7 +479,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = key0 + 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-        float pv = exp2f(s[j][i] * c - lq);
+        float pv = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq));
         if (diagonal && key > query) pv = 0.0f;
         dp[j][i] = pv * (dp[j][i] - dq_delta);  // dS'
       }
