@@ -40,6 +40,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 128;        // head dimension
 constexpr int kRowN = kD + 8;  // LDS row of a [row][d] tile: 128 bf16 + 8 padding (272 bytes)
@@ -68,8 +70,9 @@ struct AttnArgs {
 // Round to bf16, nearest even (one v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// Two floats to a pair of bf16 (one v_cvt_pk_bf16_f32), a in the low half.
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -87,39 +90,84 @@ __device__ __forceinline__ bf16x8 rows_operand(const f32x16& acc, int part) {
 }
 
 // ---- 64-row tiles: global -> registers -> LDS ------------------------------
-// Thread t holds rows 4 (t / 16) + (0..3), columns 8 (t % 16) + (0..7).
+// Every load goes through a buffer resource at a uniform (scalar) base, with
+// per-thread 32-bit byte offsets fixed for the whole kernel; a 64-row tile
+// spans under 2 GiB (the builder checks the position stride).
 
-__device__ __forceinline__ void load_tile(const uint16_t* base, int64_t rs, u32x4 (&r)[4]) {
-  const int c = threadIdx.x % 16, g = threadIdx.x / 16;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const u32x4*>(base + (int64_t)(4 * g + i) * rs + 8 * c);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const uint16_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
-// [row][d], rows of kRowN.
+// Row-major staging: thread t holds rows 4 (t / 16) + i (i = 0..3), columns
+// 8 (t % 16) + (0..7), and writes them to [row][d] rows of kRowN: sixteen
+// lanes fill one row's 256 bytes, so the stores never share a bank.
+struct TileRows {
+  int32_t off;     // this thread's byte offset of its first row
+  int32_t stride;  // bytes between rows (uniform)
+  __device__ explicit TileRows(int64_t rs) : stride((int32_t)(rs * 2)) {
+    const int c = threadIdx.x % 16, g = threadIdx.x / 16;
+    off = (int32_t)((4 * g * rs + 8 * c) * 2);
+  }
+  __device__ void load(const uint16_t* base, u32x4 (&r)[4]) const {
+    const __amdgpu_buffer_rsrc_t rsrc = rsrc_of(base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (u32x4)__builtin_amdgcn_raw_buffer_load_b128(rsrc, off, i * stride, 0);
+  }
+};
+
 __device__ __forceinline__ void store_rows(uint16_t* lds, const u32x4 (&r)[4]) {
   const int c = threadIdx.x % 16, g = threadIdx.x / 16;
 #pragma unroll
   for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + (4 * g + i) * kRowN + 8 * c) = r[i];
 }
 
-// The slot of row `row` (0..63) in a transposed tile's row: within each 16,
-// rows 4h..4h+3 and 8+4h..8+4h+3 take slots 8h..8h+7.
-__device__ __forceinline__ int slot_of(int row) {
-  const int k16 = row % 16;
-  return (row / 16) * 16 + 8 * ((k16 % 8) / 4) + (k16 < 8 ? 0 : 4) + row % 4;
+// Transposed staging into [d][slot] rows of kRowT.  Slots permute the rows
+// so that a 32 x 32 accumulator's registers feed the next product directly:
+// within each 16 rows, rows 4h..4h+3 and 8+4h..8+4h+3 take slots 8h..8h+7.
+// Thread t owns slot chunk kb = t % 8 (slots 8 kb .. 8 kb + 7, i.e. rows
+// row_of_slot(8 kb + e)) and the four d columns 4 ob .. 4 ob + 3, loaded as
+// eight 8-byte pieces; it transposes them in registers and writes four
+// 16-byte pieces, one per d row.  Lanes 0..7 fill one d row's 128 bytes and
+// lanes 8..15 the row 8 further on (ob order 0, 2, 1, 3, 4, 6, 5, 7, ...),
+// which starts 32 banks away with rows of 36 words, so no two lanes of a
+// store share a bank.
+__device__ __forceinline__ int row_of_slot(int slot) {
+  const int chunk = slot / 8, e = slot % 8;
+  return 16 * (chunk / 2) + 4 * (chunk % 2) + 8 * (e / 4) + e % 4;
 }
 
-// [d][slot(row)], rows of kRowT: each thread writes, for each of its 8
-// columns, its 4 rows as 4 consecutive slots.
-__device__ __forceinline__ void store_transposed(uint16_t* lds, const u32x4 (&r)[4]) {
-  const int c = threadIdx.x % 16, g = threadIdx.x / 16;
-  const int slot = slot_of(4 * g);
+__device__ __forceinline__ int cols_ob() {
+  const int j = threadIdx.x / 8;
+  return 2 * (j & 1) + ((j >> 1) & 1) + 4 * (j >> 2);
+}
+
+struct TileCols {
+  int32_t off;     // byte offset of row_of_slot(8 kb), column 4 ob
+  int32_t stride;  // bytes between rows (uniform)
+  __device__ explicit TileCols(int64_t rs) : stride((int32_t)(rs * 2)) {
+    const int kb = threadIdx.x % 8, ob = cols_ob();
+    off = (int32_t)(((int64_t)row_of_slot(8 * kb) * rs + 4 * ob) * 2);
+  }
+  // Slot 8 kb + e is row row_of_slot(8 kb) + 8 (e / 4) + e % 4.
+  __device__ void load(const uint16_t* base, u32x2 (&r)[8]) const {
+    const __amdgpu_buffer_rsrc_t rsrc = rsrc_of(base);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int sh = 16 * (j % 2);
-    const uint32_t a0 = (r[0][j / 2] >> sh) & 0xffffu, a1 = (r[1][j / 2] >> sh) & 0xffffu;
-    const uint32_t a2 = (r[2][j / 2] >> sh) & 0xffffu, a3 = (r[3][j / 2] >> sh) & 0xffffu;
-    *reinterpret_cast<u32x2*>(lds + (8 * c + j) * kRowT + slot) = u32x2{a0 | (a1 << 16), a2 | (a3 << 16)};
+    for (int e = 0; e < 8; ++e)
+      r[e] = (u32x2)__builtin_amdgcn_raw_buffer_load_b64(rsrc, off, (8 * (e / 4) + e % 4) * stride, 0);
+  }
+};
+
+__device__ __forceinline__ void store_cols(uint16_t* lds, const u32x2 (&r)[8]) {
+  const int kb = threadIdx.x % 8, ob = cols_ob();
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = r[2 * e][c / 2], hi = r[2 * e + 1][c / 2];
+      w[e] = (c % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+    }
+    *reinterpret_cast<u32x4*>(lds + (4 * ob + c) * kRowT + 8 * kb) = w;
   }
 }
 
@@ -143,16 +191,27 @@ __device__ __forceinline__ void row_operand(const uint16_t* base, bf16x8 (&f)[8]
 }
 
 // ---- forward -------------------------------------------------------------------
+// Per workgroup 128 queries (32 per wave), keys in steps of 64.  The loop is
+// pipelined by one step: while the vector ALUs turn the scores of step j into
+// weights, the matrix cores already compute the scores of step j + 1, so K
+// runs one step ahead of V through LDS.  Iteration j reads K[(j + 1) & 1] and
+// V'[j & 1], and refills K[j & 1] with step j + 2 and V'[(j + 1) & 1] with
+// step j + 1 (indices past the last step are clamped; their scores are never
+// used).  The running maximum is rebased lazily: the accumulators keep their
+// shift until a query's maximum exceeds it by more than kLazy (log2 units),
+// so no weight exceeds 2^kLazy and most steps skip the rescale.
 
 constexpr int kFwdQ = 128;  // queries per workgroup (32 per wave)
 constexpr int kFwdK = 64;   // keys per step
-constexpr size_t kFwdLds = 2 * (64 * kRowN + kD * kRowT) * sizeof(uint16_t);  // K and V', two stages
+constexpr int kKTile = 64 * kRowN;  // bf16 of a K tile in LDS
+constexpr int kVTile = kD * kRowT;  // bf16 of a V' tile in LDS
+constexpr size_t kFwdLds = 2 * (kKTile + kVTile) * sizeof(uint16_t);
+constexpr float kLazy = 8.0f;
 
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int fwd_stage = 64 * kRowN + kD * kRowT;  // bf16 per stage: K, then V'
-  auto Ks = [&](int s) { return lds + s * fwd_stage; };
-  auto Vt = [&](int s) { return lds + s * fwd_stage + 64 * kRowN; };
+  uint16_t* const Kl[2] = {lds, lds + kKTile};
+  uint16_t* const Vl[2] = {lds + 2 * kKTile, lds + 2 * kKTile + kVTile};
   const int nqb = p.seq / kFwdQ;
   const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -165,6 +224,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
   const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
   const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
+  const TileRows rows(p.k_ss);
+  const TileCols cols(p.k_ss);
 
   bf16x8 qf[8];
   row_operand(qbase + (int64_t)query * p.q_ss, qf);
@@ -174,59 +236,73 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   for (int i = 0; i < 4; ++i) o[i] = f32x16{};
   float m = -INFINITY, l = 0.0f;
   const float c = p.scale * kLog2e;
-
+  // An even number of steps (the sequence is a multiple of 128), at least 2.
   const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
-  u32x4 rk[4], rv[4];
-  load_tile(kbase, p.k_ss, rk);
-  load_tile(vbase, p.k_ss, rv);
-  store_rows(Ks(0), rk);
-  store_transposed(Vt(0), rv);
+
+  u32x4 rk[4];
+  u32x2 rv[8];
+  rows.load(kbase, rk);
+  cols.load(vbase, rv);
+  store_rows(Kl[0], rk);
+  store_cols(Vl[0], rv);
+  rows.load(kbase + step_elems, rk);
+  store_rows(Kl[1], rk);
+  __syncthreads();
+  f32x16 sa[2] = {f32x16{}, f32x16{}}, sb[2];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sa[j] = mfma(frag_rows(Kl[0], 32 * j, ks), qf[ks], sa[j]);
   __syncthreads();
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int st = kb & 1;
-    const bool more = kb + 1 < nkb;
-    if (more) {
-      load_tile(kbase + (int64_t)(kb + 1) * kFwdK * p.k_ss, p.k_ss, rk);
-      load_tile(vbase + (int64_t)(kb + 1) * kFwdK * p.k_ss, p.k_ss, rv);
+  // Step j: weights from s (its scores), scores of step j + 1 into sn.
+  auto step = [&](const int j, f32x16 (&s)[2], f32x16 (&sn)[2]) {
+    const int st = j & 1;
+    rows.load(kbase + (int64_t)min(j + 2, nkb - 1) * step_elems, rk);
+    cols.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
+    const int key0 = j * kFwdK;
+    if (p.causal && key0 + kFwdK > q0) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = key0 + 32 * jj + 8 * (i / 4) + 4 * lh + i % 4;
+          if (key > query) s[jj][i] = -INFINITY;
+        }
     }
-    // S' (64 keys x 32 queries) = K Q'.
-    f32x16 s[2] = {f32x16{}, f32x16{}};
+    sn[0] = f32x16{};
+    sn[1] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) s[j] = mfma(frag_rows(Ks(st), 32 * j, ks), qf[ks], s[j]);
-    // Mask (diagonal blocks only), and the running maximum of this lane's
-    // query in scaled units (the scale is positive, so max commutes with it).
-    const int key0 = kb * kFwdK;
-    if (p.causal && key0 + kFwdK > q0) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = key0 + 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-          if (key > query) s[j][i] = -INFINITY;
-        }
-    }
+      for (int jj = 0; jj < 2; ++jj) sn[jj] = mfma(frag_rows(Kl[st ^ 1], 32 * jj, ks), qf[ks], sn[jj]);
+    // This lane's query maximum in scaled units (the scale is positive).
     float mb = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[j][i]);
+      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[jj][i]);
     mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * c;
-    const float mn = fmaxf(m, mb);
+    const bool grow = mb > m + kLazy;
+    const float mn = grow ? mb : m;
     const float shift = isfinite(mn) ? mn : 0.0f;
     float ls = 0.0f;
+    bf16x8 pf[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float w = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -shift));
-        s[j][i] = w;
-        ls += w;
+      for (int part = 0; part < 2; ++part) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float w0 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e], c, -shift));
+          const float w1 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e + 1], c, -shift));
+          ls += w0 + w1;
+          w[e] = pack2(w0, w1);
+        }
+        pf[2 * jj + part] = (bf16x8)w;
       }
-    // Rescale only when some query's maximum grew.
-    if (__ballot(mn > m)) {
+    if (__ballot(grow)) {
       const float alpha = __builtin_amdgcn_exp2f(m - shift);
       l *= alpha;
 #pragma unroll
@@ -235,19 +311,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
     l += ls;
     m = mn;
     // O' (128 d x 32 queries) += V' P', the weights rounded to bf16.
-    bf16x8 pf[4] = {rows_operand(s[0], 0), rows_operand(s[0], 1), rows_operand(s[1], 0), rows_operand(s[1], 1)};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] = mfma(frag_cols(Vt(st), 32 * db, ks), pf[ks], o[db]);
-    if (more) {
-      store_rows(Ks(st ^ 1), rk);
-      store_transposed(Vt(st ^ 1), rv);
-    }
+      for (int db = 0; db < 4; ++db) o[db] = mfma(frag_cols(Vl[st], 32 * db, ks), pf[ks], o[db]);
+    store_rows(Kl[st], rk);
+    store_cols(Vl[st ^ 1], rv);
     __syncthreads();
+  };
+  for (int j = 0; j < nkb; j += 2) {
+    step(j, sa, sb);
+    step(j + 1, sb, sa);
   }
 
-  // Both halves of the wave summed their keys' weights against the same maximum.
+  // Both halves of the wave summed their keys' weights against the same shift.
   l += __shfl_xor(l, 32, 64);
   const float inv = 1.0f / l;
   uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
@@ -332,11 +409,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   };
   const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
   const int nq = p.seq / kBwdQ;
+  const TileRows rows(p.q_ss);
+  const TileCols cols(p.q_ss);
   u32x4 rq[4], rg[4];
+  u32x2 cq[8], cg[8];
   float rl = 0.0f, rd = 0.0f;
   auto fetch = [&](int qb) {
-    load_tile(qbase + (int64_t)qb * kBwdQ * p.q_ss, p.q_ss, rq);
-    load_tile(gbase + (int64_t)qb * kBwdQ * p.q_ss, p.q_ss, rg);
+    const int64_t at = (int64_t)qb * kBwdQ * p.q_ss;
+    rows.load(qbase + at, rq);
+    rows.load(gbase + at, rg);
+    cols.load(qbase + at, cq);
+    cols.load(gbase + at, cg);
     if (threadIdx.x < 64) {
       rl = lbase[(int64_t)(qb * kBwdQ + threadIdx.x) * p.heads];
       rd = dbase[(int64_t)(qb * kBwdQ + threadIdx.x) * p.heads];
@@ -347,9 +430,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
     float *L, *Dl;
     stage(s, &Qs, &Qt, &Gs, &Gt, &L, &Dl);
     store_rows(Qs, rq);
-    store_transposed(Qt, rq);
+    store_cols(Qt, cq);
     store_rows(Gs, rg);
-    store_transposed(Gt, rg);
+    store_cols(Gt, cg);
     if (threadIdx.x < 64) L[threadIdx.x] = rl * kLog2e, Dl[threadIdx.x] = rd;
   };
   fetch(qstart);
@@ -447,22 +530,28 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
 
   const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
+  const TileRows rows(p.k_ss);
+  const TileCols cols(p.k_ss);
   u32x4 rk[4], rv[4];
+  u32x2 ck[8];
   auto Ks = [&](int s) { return lds + s * stage_elems; };
   auto Vs = [&](int s) { return lds + s * stage_elems + 64 * kRowN; };
   auto Kt = [&](int s) { return lds + s * stage_elems + 2 * 64 * kRowN; };
-  load_tile(kbase, p.k_ss, rk);
-  load_tile(vbase, p.k_ss, rv);
+  rows.load(kbase, rk);
+  rows.load(vbase, rv);
+  cols.load(kbase, ck);
   store_rows(Ks(0), rk);
-  store_transposed(Kt(0), rk);
+  store_cols(Kt(0), ck);
   store_rows(Vs(0), rv);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int st = kb & 1;
     const bool more = kb + 1 < nkb;
     if (more) {
-      load_tile(kbase + (int64_t)(kb + 1) * kFwdK * p.k_ss, p.k_ss, rk);
-      load_tile(vbase + (int64_t)(kb + 1) * kFwdK * p.k_ss, p.k_ss, rv);
+      const int64_t at = (int64_t)(kb + 1) * kFwdK * p.k_ss;
+      rows.load(kbase + at, rk);
+      rows.load(vbase + at, rv);
+      cols.load(kbase + at, ck);
     }
     f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
@@ -490,7 +579,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
       for (int db = 0; db < 4; ++db) dq[db] = mfma(frag_cols(Kt(st), 32 * db, ks), sf[ks], dq[db]);
     if (more) {
       store_rows(Ks(st ^ 1), rk);
-      store_transposed(Kt(st ^ 1), rk);
+      store_cols(Kt(st ^ 1), ck);
       store_rows(Vs(st ^ 1), rv);
     }
     __syncthreads();
@@ -522,6 +611,8 @@ int check_desc(const th_attention_desc* d, bool backward) {
              "attention: q, k, v, o must be 16-byte aligned");
   for (int64_t s : {d->q_strides[0], d->q_strides[1], d->q_strides[2], d->k_strides[0], d->k_strides[1], d->k_strides[2]})
     TH_REQUIRE(s % 8 == 0 && s > 0, "attention: strides must be positive multiples of 8 (16-byte rows)");
+  TH_REQUIRE(d->k_strides[1] < (int64_t(1) << 24) && d->q_strides[1] < (int64_t(1) << 24),
+             "attention: position strides must be below 2^24 elements (a 64-position tile spans under 2 GiB)");
   if (backward) {
     TH_REQUIRE(d->lse && d->dout && d->dq && d->dk && d->dv, "attention backward: null lse, dout, dq, dk or dv");
     TH_REQUIRE(aligned(d->dout, 16) && aligned(d->dq, 16) && aligned(d->dk, 16) && aligned(d->dv, 16),
