@@ -42,10 +42,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kD = 128;        // head dimension
-constexpr int kRowN = kD + 8;  // LDS row of a [row][d] tile: 128 bf16 + 8 padding (272 bytes)
-constexpr int kRowT = 64 + 8;  // LDS row of a [d][row] tile of 64 rows: 64 bf16 + 8 padding
+constexpr int kD = 128;                // head dimension
+constexpr int kTileElems = 64 * kD;    // one 64-row tile in LDS (256-byte rows, no padding)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -79,9 +80,11 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// The eight bf16 of registers [8 part, 8 part + 8) of a 32 x 32 accumulator,
-// as the B (or A) operand of a 16-deep product over the accumulator's rows
-// 16 part .. 16 part + 15 (in the row order the permuted tiles use).
+// The eight bf16 of registers [8 part, 8 part + 8) of a 32 x 32 accumulator
+// as the B operand of a 16-deep product over the accumulator's rows
+// 16 part .. 16 part + 15.  Lane l holds rows 8 (i / 4) + 4 (l / 32) + i % 4
+// in register i, so its k-slot 8 (l / 32) + e is row 8 (e / 4) + 4 (l / 32)
+// + e % 4 of the sixteen: the A operand must use the same row order.
 __device__ __forceinline__ bf16x8 rows_operand(const f32x16& acc, int part) {
   u32x4 w;
 #pragma unroll
@@ -89,18 +92,27 @@ __device__ __forceinline__ bf16x8 rows_operand(const f32x16& acc, int part) {
   return (bf16x8)w;
 }
 
-// ---- 64-row tiles: global -> registers -> LDS ------------------------------
-// Every load goes through a buffer resource at a uniform (scalar) base, with
-// per-thread 32-bit byte offsets fixed for the whole kernel; a 64-row tile
-// spans under 2 GiB (the builder checks the position stride).
+// ---- 64-row tiles in LDS ---------------------------------------------------------
+// A tile holds 64 rows of 128 bf16 (256 bytes, one pass over the 64 banks).
+// The sixteen 16-byte chunks of row r are stored XOR-permuted, chunk c at
+// position c ^ swz(r) with swz(r) = 4 (r % 4) + (r / 4) % 4, which keeps the
+// three access patterns below free of bank conflicts:
+//  - 16 lanes storing one row (the positions are a permutation of 0..15);
+//  - 16 lanes reading chunk c of 16 consecutive rows (swz is a bijection on r % 16);
+//  - 32 lanes reading 8 bytes each from four consecutive rows (aligned to 4)
+//    by four consecutive chunks (aligned to 4): the positions
+//    4 ((c / 4) ^ (r % 4)) + ((c % 4) ^ ((r / 4) % 4)) are 16 distinct chunks.
+__device__ __forceinline__ int tile_at(int row, int chunk) {
+  return row * kD + 8 * (chunk ^ (4 * (row % 4) + (row / 4) % 4));
+}
 
+// Every global load goes through a buffer resource at a uniform (scalar)
+// base; a 64-row tile spans under 2 GiB (the builder checks the strides).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const uint16_t* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
-// Row-major staging: thread t holds rows 4 (t / 16) + i (i = 0..3), columns
-// 8 (t % 16) + (0..7), and writes them to [row][d] rows of kRowN: sixteen
-// lanes fill one row's 256 bytes, so the stores never share a bank.
+// Thread t holds rows 4 (t / 16) + i (i = 0..3), chunk t % 16 of a tile.
 struct TileRows {
   int32_t off;     // this thread's byte offset of its first row
   int32_t stride;  // bytes between rows (uniform)
@@ -118,69 +130,33 @@ struct TileRows {
 __device__ __forceinline__ void store_rows(uint16_t* lds, const u32x4 (&r)[4]) {
   const int c = threadIdx.x % 16, g = threadIdx.x / 16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + (4 * g + i) * kRowN + 8 * c) = r[i];
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + tile_at(4 * g + i, c)) = r[i];
 }
 
-// Transposed staging into [d][slot] rows of kRowT.  Slots permute the rows
-// so that a 32 x 32 accumulator's registers feed the next product directly:
-// within each 16 rows, rows 4h..4h+3 and 8+4h..8+4h+3 take slots 8h..8h+7.
-// Thread t owns slot chunk kb = t % 8 (slots 8 kb .. 8 kb + 7, i.e. rows
-// row_of_slot(8 kb + e)) and the four d columns 4 ob .. 4 ob + 3, loaded as
-// eight 8-byte pieces; it transposes them in registers and writes four
-// 16-byte pieces, one per d row.  Lanes 0..7 fill one d row's 128 bytes and
-// lanes 8..15 the row 8 further on (ob order 0, 2, 1, 3, 4, 6, 5, 7, ...),
-// which starts 32 banks away with rows of 36 words, so no two lanes of a
-// store share a bank.
-__device__ __forceinline__ int row_of_slot(int slot) {
-  const int chunk = slot / 8, e = slot % 8;
-  return 16 * (chunk / 2) + 4 * (chunk % 2) + 8 * (e / 4) + e % 4;
-}
-
-__device__ __forceinline__ int cols_ob() {
-  const int j = threadIdx.x / 8;
-  return 2 * (j & 1) + ((j >> 1) & 1) + 4 * (j >> 2);
-}
-
-struct TileCols {
-  int32_t off;     // byte offset of row_of_slot(8 kb), column 4 ob
-  int32_t stride;  // bytes between rows (uniform)
-  __device__ explicit TileCols(int64_t rs) : stride((int32_t)(rs * 2)) {
-    const int kb = threadIdx.x % 8, ob = cols_ob();
-    off = (int32_t)(((int64_t)row_of_slot(8 * kb) * rs + 4 * ob) * 2);
-  }
-  // Slot 8 kb + e is row row_of_slot(8 kb) + 8 (e / 4) + e % 4.
-  __device__ void load(const uint16_t* base, u32x2 (&r)[8]) const {
-    const __amdgpu_buffer_rsrc_t rsrc = rsrc_of(base);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      r[e] = (u32x2)__builtin_amdgcn_raw_buffer_load_b64(rsrc, off, (8 * (e / 4) + e % 4) * stride, 0);
-  }
-};
-
-__device__ __forceinline__ void store_cols(uint16_t* lds, const u32x2 (&r)[8]) {
-  const int kb = threadIdx.x % 8, ob = cols_ob();
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    u32x4 w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = r[2 * e][c / 2], hi = r[2 * e + 1][c / 2];
-      w[e] = (c % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
-    }
-    *reinterpret_cast<u32x4*>(lds + (4 * ob + c) * kRowT + 8 * kb) = w;
-  }
-}
-
-// A operand from a [row][d] tile: rows r0 + lane % 32, d 16 ks + 8 (lane / 32).
+// A operand from a tile, M along its rows: rows r0 + lane % 32, k = columns
+// 16 ks + 8 (lane / 32) + (0..7).
 __device__ __forceinline__ bf16x8 frag_rows(const uint16_t* lds, int r0, int ks) {
   const int lane = threadIdx.x % 64;
-  return *reinterpret_cast<const bf16x8*>(lds + (r0 + lane % 32) * kRowN + 16 * ks + 8 * (lane / 32));
+  return *reinterpret_cast<const bf16x8*>(lds + tile_at(r0 + lane % 32, 2 * ks + lane / 32));
 }
 
-// A operand from a [d][slot] tile: d d0 + lane % 32, the 16 rows of step ks.
-__device__ __forceinline__ bf16x8 frag_cols(const uint16_t* lds, int d0, int ks) {
-  const int lane = threadIdx.x % 64;
-  return *reinterpret_cast<const bf16x8*>(lds + (d0 + lane % 32) * kRowT + 16 * ks + 8 * (lane / 32));
+// A operand from a tile, M along its columns: m = column d0 + lane % 32, k =
+// the rows of 16-row step ks in the order rows_operand gives the B operand
+// (k-slot 8 h + e <-> row 16 ks + 8 (e / 4) + 4 h + e % 4, h = lane / 32).
+// ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the 8-byte
+// pieces addressed by lanes 4 k + i / 4 (k = 0..3).  Lane j here addresses
+// row base + j / 4, columns dgrp + 4 (j % 4) + (0..3), so lane i receives
+// rows base + (0..3) of column dgrp + i; two reads cover the eight rows.
+__device__ __forceinline__ bf16x8 frag_tr(const uint16_t* lds, int d0, int ks) {
+  const int lane = threadIdx.x % 64, j = lane % 16;
+  const int col = d0 + 16 * ((lane / 16) % 2) + 4 * (j % 4);
+  const int row = 16 * ks + 4 * (lane / 32) + j / 4;
+  const int at0 = tile_at(row, col / 8) + col % 8, at1 = tile_at(row + 8, col / 8) + col % 8;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at0));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at1));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, w);
 }
 
 // B operand straight from global: row `row`, d 16 ks + 8 (lane / 32), for ks = 0..7.
@@ -195,23 +171,22 @@ __device__ __forceinline__ void row_operand(const uint16_t* base, bf16x8 (&f)[8]
 // pipelined by one step: while the vector ALUs turn the scores of step j into
 // weights, the matrix cores already compute the scores of step j + 1, so K
 // runs one step ahead of V through LDS.  Iteration j reads K[(j + 1) & 1] and
-// V'[j & 1], and refills K[j & 1] with step j + 2 and V'[(j + 1) & 1] with
+// V[j & 1], and refills K[j & 1] with step j + 2 and V[(j + 1) & 1] with
 // step j + 1 (indices past the last step are clamped; their scores are never
-// used).  The running maximum is rebased lazily: the accumulators keep their
-// shift until a query's maximum exceeds it by more than kLazy (log2 units),
-// so no weight exceeds 2^kLazy and most steps skip the rescale.
+// used).  V is read transposed straight from its row-major tile.  The running
+// maximum is rebased lazily: the accumulators keep their shift until a
+// query's maximum exceeds it by more than kLazy (log2 units), so no weight
+// exceeds 2^kLazy and most steps skip the rescale.
 
 constexpr int kFwdQ = 128;  // queries per workgroup (32 per wave)
 constexpr int kFwdK = 64;   // keys per step
-constexpr int kKTile = 64 * kRowN;  // bf16 of a K tile in LDS
-constexpr int kVTile = kD * kRowT;  // bf16 of a V' tile in LDS
-constexpr size_t kFwdLds = 2 * (kKTile + kVTile) * sizeof(uint16_t);
+constexpr size_t kFwdLds = 4 * kTileElems * sizeof(uint16_t);  // K[2], V[2]
 constexpr float kLazy = 8.0f;
 
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t* const Kl[2] = {lds, lds + kKTile};
-  uint16_t* const Vl[2] = {lds + 2 * kKTile, lds + 2 * kKTile + kVTile};
+  uint16_t* const Kl[2] = {lds, lds + kTileElems};
+  uint16_t* const Vl[2] = {lds + 2 * kTileElems, lds + 3 * kTileElems};
   const int nqb = p.seq / kFwdQ;
   const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -226,7 +201,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
   const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
   const TileRows rows(p.k_ss);
-  const TileCols cols(p.k_ss);
 
   bf16x8 qf[8];
   row_operand(qbase + (int64_t)query * p.q_ss, qf);
@@ -239,12 +213,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   // An even number of steps (the sequence is a multiple of 128), at least 2.
   const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
 
-  u32x4 rk[4];
-  u32x2 rv[8];
+  u32x4 rk[4], rv[4];
   rows.load(kbase, rk);
-  cols.load(vbase, rv);
+  rows.load(vbase, rv);
   store_rows(Kl[0], rk);
-  store_cols(Vl[0], rv);
+  store_rows(Vl[0], rv);
   rows.load(kbase + step_elems, rk);
   store_rows(Kl[1], rk);
   __syncthreads();
@@ -259,7 +232,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   auto step = [&](const int j, f32x16 (&s)[2], f32x16 (&sn)[2]) {
     const int st = j & 1;
     rows.load(kbase + (int64_t)min(j + 2, nkb - 1) * step_elems, rk);
-    cols.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
+    rows.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
     const int key0 = j * kFwdK;
     if (p.causal && key0 + kFwdK > q0) {
 #pragma unroll
@@ -314,9 +287,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] = mfma(frag_cols(Vl[st], 32 * db, ks), pf[ks], o[db]);
+      for (int db = 0; db < 4; ++db) o[db] = mfma(frag_tr(Vl[st], 32 * db, ks), pf[ks], o[db]);
     store_rows(Kl[st], rk);
-    store_cols(Vl[st ^ 1], rv);
+    store_rows(Vl[st ^ 1], rv);
     __syncthreads();
   };
   for (int j = 0; j < nkb; j += 2) {
@@ -358,24 +331,57 @@ __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
   if (lane == 0) p.delta[(b * p.seq + s) * p.heads + h] = v;
 }
 
+// ---- backward: shared pieces -----------------------------------------------------
+// Both kernels run one wave per SIMD (each needs most of the register file),
+// so each wave keeps its matrix core fed by itself: every product phase
+// reads the LDS fragments of the next 16-deep slice while the products of
+// this one issue (the sched_barrier fences keep the compiler from sinking
+// the reads back next to their products).  The next block's global loads
+// are issued once the weights are formed and land after the products.
+
+// Phase A: two 32 x 32 score tiles and two dot-product tiles over d = 128,
+// A operands from row-major tiles x and y (rows r0 = 0 and 32), B operands
+// the wave's own rows xf and yf.
+__device__ __forceinline__ void scores(const uint16_t* x, const uint16_t* y, const bf16x8 (&xf)[8],
+                                       const bf16x8 (&yf)[8], f32x16 (&s)[2], f32x16 (&t)[2]) {
+  s[0] = s[1] = t[0] = t[1] = f32x16{};
+  bf16x8 fa[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) fa[0][j] = frag_rows(x, 32 * j, 0), fa[0][2 + j] = frag_rows(y, 32 * j, 0);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const int cu = ks & 1;
+    if (ks < 7) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        fa[cu ^ 1][j] = frag_rows(x, 32 * j, ks + 1), fa[cu ^ 1][2 + j] = frag_rows(y, 32 * j, ks + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      s[j] = mfma(fa[cu][j], xf[ks], s[j]);
+      t[j] = mfma(fa[cu][2 + j], yf[ks], t[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---- backward: dK, dV for a block of 128 keys -------------------------------------
 // Each wave owns 32 keys.  Per query block of 64: S (64 queries x 32 keys)
 // = Q K' with queries along the registers and keys along the lanes, so the
 // products over queries (dV = P' dO, dK = dS' Q) take P and dS straight from
-// the accumulators as their B operands, against dO' and Q' tiles transposed
-// into [d][slot(query)].
+// the accumulators as their B operands, against dO' and Q' read transposed
+// from the row-major tiles.
 
 constexpr int kBwdK = 128;  // keys per workgroup
 constexpr int kBwdQ = 64;   // queries per step
-constexpr size_t kStageBwd = (size_t)(2 * 64 * kRowN + 2 * kD * kRowT) * sizeof(uint16_t) + 2 * 64 * sizeof(float);
+constexpr size_t kStageBwd = 2 * kTileElems * sizeof(uint16_t) + 2 * 64 * sizeof(float);
 constexpr size_t kDkdvLds = 2 * kStageBwd;
 
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const size_t stage_elems = kStageBwd / sizeof(uint16_t);
-  const int nkb = p.seq / kBwdK;
   const int kbk = (int)blockIdx.x;  // the first key blocks see the most queries: heaviest first
-  (void)nkb;
   const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -398,85 +404,102 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   for (int i = 0; i < 4; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
   const float c = p.scale * kLog2e;
 
-  auto stage = [&](int s, uint16_t** Qs, uint16_t** Qt, uint16_t** Gs, uint16_t** Gt, float** L, float** Dl) {
-    uint16_t* base = lds + s * stage_elems;
-    *Qs = base;
-    *Gs = base + 64 * kRowN;
-    *Qt = base + 2 * 64 * kRowN;
-    *Gt = base + 2 * 64 * kRowN + kD * kRowT;
-    *L = reinterpret_cast<float*>(base + 2 * 64 * kRowN + 2 * kD * kRowT);
-    *Dl = *L + 64;
-  };
+  // Stage layout: Q tile, dO tile, then [lse log2 e | delta] of its 64 queries.
+  auto Qs = [&](int s) { return lds + s * stage_elems; };
+  auto Gs = [&](int s) { return lds + s * stage_elems + kTileElems; };
+  auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
+
   const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
   const int nq = p.seq / kBwdQ;
   const TileRows rows(p.q_ss);
-  const TileCols cols(p.q_ss);
   u32x4 rq[4], rg[4];
-  u32x2 cq[8], cg[8];
-  float rl = 0.0f, rd = 0.0f;
+  // Threads t and t + 128 both carry entry t % 128 of [lse log2 e | delta].
+  const int lt = threadIdx.x % 128;
+  const float* lsrc = lt < 64 ? lbase : dbase;
+  const float lmul = lt < 64 ? kLog2e : 1.0f;
+  float rl = 0.0f;
   auto fetch = [&](int qb) {
     const int64_t at = (int64_t)qb * kBwdQ * p.q_ss;
     rows.load(qbase + at, rq);
     rows.load(gbase + at, rg);
-    cols.load(qbase + at, cq);
-    cols.load(gbase + at, cg);
-    if (threadIdx.x < 64) {
-      rl = lbase[(int64_t)(qb * kBwdQ + threadIdx.x) * p.heads];
-      rd = dbase[(int64_t)(qb * kBwdQ + threadIdx.x) * p.heads];
-    }
+    rl = lsrc[(int64_t)(qb * kBwdQ + lt % 64) * p.heads];
   };
   auto land = [&](int s) {
-    uint16_t *Qs, *Qt, *Gs, *Gt;
-    float *L, *Dl;
-    stage(s, &Qs, &Qt, &Gs, &Gt, &L, &Dl);
-    store_rows(Qs, rq);
-    store_cols(Qt, cq);
-    store_rows(Gs, rg);
-    store_cols(Gt, cg);
-    if (threadIdx.x < 64) L[threadIdx.x] = rl * kLog2e, Dl[threadIdx.x] = rd;
+    store_rows(Qs(s), rq);
+    store_rows(Gs(s), rg);
+    Ls(s)[lt] = rl * lmul;
   };
   fetch(qstart);
   land(0);
   __syncthreads();
   for (int qb = qstart; qb < nq; ++qb) {
     const int st = (qb - qstart) & 1;
-    const bool more = qb + 1 < nq;
-    if (more) fetch(qb + 1);
-    uint16_t *Qs, *Qt, *Gs, *Gt;
-    float *L, *Dl;
-    stage(st, &Qs, &Qt, &Gs, &Gt, &L, &Dl);
     // S = Q K', dP = dO V' (64 queries x 32 keys; queries on registers).
-    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        s[j] = mfma(frag_rows(Qs, 32 * j, ks), kf[ks], s[j]);
-        dp[j] = mfma(frag_rows(Gs, 32 * j, ks), vf[ks], dp[j]);
-      }
+    f32x16 s[2], dp[2];
+    scores(Qs(st), Gs(st), kf, vf, s, dp);
+    // P = exp2(S c - lse log2 e), dS = P (dP - delta); on the diagonal the
+    // masked scores become -inf, so their P and dS are exactly 0.
+    const float* L = Ls(st);
     const int qq0 = qb * kBwdQ;
-    const bool diagonal = p.causal && qq0 < k0 + 32;
+    if (p.causal && qq0 < k0 + 32) {
+      const int lim = key - qq0 - 4 * lh;  // masked: query offset 32 j + 8 (i / 4) + i % 4 < lim
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int qi = 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-        float pv = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -L[qi]));
-        if (diagonal && key > qq0 + qi) pv = 0.0f;
-        s[j][i] = pv;                          // P
-        dp[j][i] = pv * (dp[j][i] - Dl[qi]);   // dS
+        for (int i = 0; i < 16; ++i)
+          if (32 * j + 8 * (i / 4) + i % 4 < lim) s[j][i] = -INFINITY;
+    }
+    bf16x8 pf[4], sf[4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        u32x4 wp, ws;
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          // Registers 8 part + 4 g2 + (0..3): queries 32 j + 8 (2 part + g2) + 4 lh + (0..3).
+          const int q4 = 32 * j + 8 * (2 * part + g2) + 4 * lh;
+          const f32x4 lq = *reinterpret_cast<const f32x4*>(L + q4);
+          const f32x4 dq = *reinterpret_cast<const f32x4*>(L + 64 + q4);
+          float pv[4], sv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 8 * part + 4 * g2 + e;
+            const float w = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq[e]));
+            pv[e] = w;
+            sv[e] = w * (dp[j][i] - dq[e]);
+          }
+          wp[2 * g2] = pack2(pv[0], pv[1]);
+          wp[2 * g2 + 1] = pack2(pv[2], pv[3]);
+          ws[2 * g2] = pack2(sv[0], sv[1]);
+          ws[2 * g2 + 1] = pack2(sv[2], sv[3]);
+        }
+        pf[2 * j + part] = (bf16x8)wp;
+        sf[2 * j + part] = (bf16x8)ws;
       }
+    }
+    fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
     // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
-    bf16x8 pf[4] = {rows_operand(s[0], 0), rows_operand(s[0], 1), rows_operand(s[1], 0), rows_operand(s[1], 1)};
-    bf16x8 sf[4] = {rows_operand(dp[0], 0), rows_operand(dp[0], 1), rows_operand(dp[1], 0), rows_operand(dp[1], 1)};
+    bf16x8 fc[2][8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int db = 0; db < 4; ++db) fc[0][db] = frag_tr(Gs(st), 32 * db, 0), fc[0][4 + db] = frag_tr(Qs(st), 32 * db, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cu = ks & 1;
+      if (ks < 3) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          fc[cu ^ 1][db] = frag_tr(Gs(st), 32 * db, ks + 1), fc[cu ^ 1][4 + db] = frag_tr(Qs(st), 32 * db, ks + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        dv[db] = mfma(frag_cols(Gt, 32 * db, ks), pf[ks], dv[db]);
-        dk[db] = mfma(frag_cols(Qt, 32 * db, ks), sf[ks], dk[db]);
+        dv[db] = mfma(fc[cu][db], pf[ks], dv[db]);
+        dk[db] = mfma(fc[cu][4 + db], sf[ks], dk[db]);
       }
-    if (more) land(st ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    land(st ^ 1);
     __syncthreads();
   }
   // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
@@ -497,14 +520,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 // ---- backward: dQ for a block of 128 queries -----------------------------------------
 // Each wave owns 32 queries.  Per key block of 64: S' = K Q', dP' = V dO'
 // (keys on registers, queries on lanes), dS' = P' .* (dP' - delta), and
-// dQ' (128 d x 32 queries) += K' dS' with K' transposed into [d][slot(key)].
+// dQ' (128 d x 32 queries) += K' dS' with K' read transposed from K's tile.
 
-constexpr size_t kStageDq = (size_t)(2 * 64 * kRowN + kD * kRowT) * sizeof(uint16_t);
-constexpr size_t kDqLds = 2 * kStageDq;
+constexpr size_t kDqLds = 4 * kTileElems * sizeof(uint16_t);  // (K, V) x 2 stages
 
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const size_t stage_elems = kStageDq / sizeof(uint16_t);
   const int nqb = p.seq / kFwdQ;
   const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest first
   const int h = blockIdx.y, b = blockIdx.z;
@@ -530,58 +551,65 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
 
   const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
+  const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
   const TileRows rows(p.k_ss);
-  const TileCols cols(p.k_ss);
   u32x4 rk[4], rv[4];
-  u32x2 ck[8];
-  auto Ks = [&](int s) { return lds + s * stage_elems; };
-  auto Vs = [&](int s) { return lds + s * stage_elems + 64 * kRowN; };
-  auto Kt = [&](int s) { return lds + s * stage_elems + 2 * 64 * kRowN; };
+  auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
+  auto Vs = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
   rows.load(kbase, rk);
   rows.load(vbase, rv);
-  cols.load(kbase, ck);
   store_rows(Ks(0), rk);
-  store_cols(Kt(0), ck);
   store_rows(Vs(0), rv);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int st = kb & 1;
-    const bool more = kb + 1 < nkb;
-    if (more) {
-      const int64_t at = (int64_t)(kb + 1) * kFwdK * p.k_ss;
-      rows.load(kbase + at, rk);
-      rows.load(vbase + at, rv);
-      cols.load(kbase + at, ck);
-    }
-    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        s[j] = mfma(frag_rows(Ks(st), 32 * j, ks), qf[ks], s[j]);
-        dp[j] = mfma(frag_rows(Vs(st), 32 * j, ks), gf[ks], dp[j]);
-      }
+    f32x16 s[2], dp[2];
+    scores(Ks(st), Vs(st), qf, gf, s, dp);
     const int key0 = kb * kFwdK;
-    const bool diagonal = p.causal && key0 + kFwdK > q0;
+    if (p.causal && key0 + kFwdK > q0) {
+      const int lim = query - key0 - 4 * lh;  // masked: key offset 32 j + 8 (i / 4) + i % 4 > lim
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * j + 8 * (i / 4) + i % 4 > lim) s[j][i] = -INFINITY;
+    }
+    bf16x8 sf[4];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = key0 + 32 * j + 8 * (i / 4) + 4 * lh + i % 4;
-        float pv = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq));
-        if (diagonal && key > query) pv = 0.0f;
-        dp[j][i] = pv * (dp[j][i] - dq_delta);  // dS'
+      for (int part = 0; part < 2; ++part) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 8 * part + 2 * e;
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[j][i + 1], c, -lq));
+          w[e] = pack2(p0 * (dp[j][i] - dq_delta), p1 * (dp[j][i + 1] - dq_delta));  // dS'
+        }
+        sf[2 * j + part] = (bf16x8)w;
       }
-    bf16x8 sf[4] = {rows_operand(dp[0], 0), rows_operand(dp[0], 1), rows_operand(dp[1], 0), rows_operand(dp[1], 1)};
+    const int64_t at = (int64_t)min(kb + 1, nkb - 1) * step_elems;  // past the end: a harmless reload
+    rows.load(kbase + at, rk);
+    rows.load(vbase + at, rv);
+    // dQ' (128 d x 32 queries) += K' dS'.
+    bf16x8 fc[2][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int db = 0; db < 4; ++db) fc[0][db] = frag_tr(Ks(st), 32 * db, 0);
 #pragma unroll
-      for (int db = 0; db < 4; ++db) dq[db] = mfma(frag_cols(Kt(st), 32 * db, ks), sf[ks], dq[db]);
-    if (more) {
-      store_rows(Ks(st ^ 1), rk);
-      store_cols(Kt(st ^ 1), ck);
-      store_rows(Vs(st ^ 1), rv);
+    for (int ks = 0; ks < 4; ++ks) {
+      const int cu = ks & 1;
+      if (ks < 3) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) fc[cu ^ 1][db] = frag_tr(Ks(st), 32 * db, ks + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) dq[db] = mfma(fc[cu][db], sf[ks], dq[db]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    store_rows(Ks(st ^ 1), rk);
+    store_rows(Vs(st ^ 1), rv);
     __syncthreads();
   }
   uint16_t* out = p.dq + qoff;
