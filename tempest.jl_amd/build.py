@@ -39,13 +39,21 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags.  The attention kernels keep their matrix-core
+# accumulators in ordinary VGPRs (the VALU works on the scores directly, with
+# no copies out of the accumulation registers).
+EXTRA = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources() -> list[pathlib.Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: pathlib.Path) -> tuple[pathlib.Path, str]:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature; its warning is noise.
     noise = "'-packed-fp32-ops' is not a recognized feature"

@@ -434,6 +434,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   __syncthreads();
   for (int qb = qstart; qb < nq; ++qb) {
     const int st = (qb - qstart) & 1;
+    fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
     // S = Q K', dP = dO V' (64 queries x 32 keys; queries on registers).
     f32x16 s[2], dp[2];
     scores(Qs(st), Gs(st), kf, vf, s, dp);
@@ -478,7 +479,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
         sf[2 * j + part] = (bf16x8)ws;
       }
     }
-    fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
     // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
     bf16x8 fc[2][8];
 #pragma unroll
@@ -563,6 +563,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int st = kb & 1;
+    const int64_t at = (int64_t)min(kb + 1, nkb - 1) * step_elems;  // past the end: a harmless reload
+    rows.load(kbase + at, rk);
+    rows.load(vbase + at, rv);
     f32x16 s[2], dp[2];
     scores(Ks(st), Vs(st), qf, gf, s, dp);
     const int key0 = kb * kFwdK;
@@ -589,9 +592,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
         }
         sf[2 * j + part] = (bf16x8)w;
       }
-    const int64_t at = (int64_t)min(kb + 1, nkb - 1) * step_elems;  // past the end: a harmless reload
-    rows.load(kbase + at, rk);
-    rows.load(vbase + at, rv);
     // dQ' (128 d x 32 queries) += K' dS'.
     bf16x8 fc[2][4];
 #pragma unroll
