@@ -188,128 +188,133 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   uint16_t* const Kl[2] = {lds, lds + kTileElems};
   uint16_t* const Vl[2] = {lds + 2 * kTileElems, lds + 3 * kTileElems};
   const int nqb = p.seq / kFwdQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int hk = h / (p.heads / p.kv_heads);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int lr = lane % 32, lh = lane / 32;
-  const int q0 = qb * kFwdQ + wave * 32;
-  const int query = q0 + lr;
+  // Causal: workgroup x takes query blocks x and nqb - 1 - x, so every
+  // workgroup sweeps the same number of key blocks.
+  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int hk = h / (p.heads / p.kv_heads);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int lr = lane % 32, lh = lane / 32;
+    const int q0 = qb * kFwdQ + wave * 32;
+    const int query = q0 + lr;
 
-  const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
-  const TileRows rows(p.k_ss);
+    const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
+    const TileRows rows(p.k_ss);
 
-  bf16x8 qf[8];
-  row_operand(qbase + (int64_t)query * p.q_ss, qf);
+    bf16x8 qf[8];
+    row_operand(qbase + (int64_t)query * p.q_ss, qf);
 
-  f32x16 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  float m = -INFINITY, l = 0.0f;
-  const float c = p.scale * kLog2e;
-  // An even number of steps (the sequence is a multiple of 128), at least 2.
-  const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
+    f32x16 o[4];
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+    float m = -INFINITY, l = 0.0f;
+    const float c = p.scale * kLog2e;
+    // An even number of steps (the sequence is a multiple of 128), at least 2.
+    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
 
-  u32x4 rk[4], rv[4];
-  rows.load(kbase, rk);
-  rows.load(vbase, rv);
-  store_rows(Kl[0], rk);
-  store_rows(Vl[0], rv);
-  rows.load(kbase + step_elems, rk);
-  store_rows(Kl[1], rk);
-  __syncthreads();
-  f32x16 sa[2] = {f32x16{}, f32x16{}}, sb[2];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) sa[j] = mfma(frag_rows(Kl[0], 32 * j, ks), qf[ks], sa[j]);
-  __syncthreads();
-
-  // Step j: weights from s (its scores), scores of step j + 1 into sn.
-  auto step = [&](const int j, f32x16 (&s)[2], f32x16 (&sn)[2]) {
-    const int st = j & 1;
-    rows.load(kbase + (int64_t)min(j + 2, nkb - 1) * step_elems, rk);
-    rows.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
-    const int key0 = j * kFwdK;
-    if (p.causal && key0 + kFwdK > q0) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = key0 + 32 * jj + 8 * (i / 4) + 4 * lh + i % 4;
-          if (key > query) s[jj][i] = -INFINITY;
-        }
-    }
-    sn[0] = f32x16{};
-    sn[1] = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) sn[jj] = mfma(frag_rows(Kl[st ^ 1], 32 * jj, ks), qf[ks], sn[jj]);
-    // This lane's query maximum in scaled units (the scale is positive).
-    float mb = -INFINITY;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[jj][i]);
-    mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * c;
-    const bool grow = mb > m + kLazy;
-    const float mn = grow ? mb : m;
-    const float shift = isfinite(mn) ? mn : 0.0f;
-    float ls = 0.0f;
-    bf16x8 pf[4];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float w0 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e], c, -shift));
-          const float w1 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e + 1], c, -shift));
-          ls += w0 + w1;
-          w[e] = pack2(w0, w1);
-        }
-        pf[2 * jj + part] = (bf16x8)w;
-      }
-    if (__ballot(grow)) {
-      const float alpha = __builtin_amdgcn_exp2f(m - shift);
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] *= alpha;
-    }
-    l += ls;
-    m = mn;
-    // O' (128 d x 32 queries) += V' P', the weights rounded to bf16.
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o[db] = mfma(frag_tr(Vl[st], 32 * db, ks), pf[ks], o[db]);
-    store_rows(Kl[st], rk);
-    store_rows(Vl[st ^ 1], rv);
+    u32x4 rk[4], rv[4];
+    rows.load(kbase, rk);
+    rows.load(vbase, rv);
+    store_rows(Kl[0], rk);
+    store_rows(Vl[0], rv);
+    rows.load(kbase + step_elems, rk);
+    store_rows(Kl[1], rk);
     __syncthreads();
-  };
-  for (int j = 0; j < nkb; j += 2) {
-    step(j, sa, sb);
-    step(j + 1, sb, sa);
-  }
+    f32x16 sa[2] = {f32x16{}, f32x16{}}, sb[2];
+  #pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+  #pragma unroll
+      for (int j = 0; j < 2; ++j) sa[j] = mfma(frag_rows(Kl[0], 32 * j, ks), qf[ks], sa[j]);
+    __syncthreads();
 
-  // Both halves of the wave summed their keys' weights against the same shift.
-  l += __shfl_xor(l, 32, 64);
-  const float inv = 1.0f / l;
-  uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * db + 8 * g + 4 * lh;
-      *reinterpret_cast<u32x2*>(obase + d) =
-          u32x2{pack2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv), pack2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv)};
+    // Step j: weights from s (its scores), scores of step j + 1 into sn.
+    auto step = [&](const int j, f32x16 (&s)[2], f32x16 (&sn)[2]) {
+      const int st = j & 1;
+      rows.load(kbase + (int64_t)min(j + 2, nkb - 1) * step_elems, rk);
+      rows.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
+      const int key0 = j * kFwdK;
+      if (p.causal && key0 + kFwdK > q0) {
+  #pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = key0 + 32 * jj + 8 * (i / 4) + 4 * lh + i % 4;
+            if (key > query) s[jj][i] = -INFINITY;
+          }
+      }
+      sn[0] = f32x16{};
+      sn[1] = f32x16{};
+  #pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+  #pragma unroll
+        for (int jj = 0; jj < 2; ++jj) sn[jj] = mfma(frag_rows(Kl[st ^ 1], 32 * jj, ks), qf[ks], sn[jj]);
+      // This lane's query maximum in scaled units (the scale is positive).
+      float mb = -INFINITY;
+  #pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[jj][i]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * c;
+      const bool grow = mb > m + kLazy;
+      const float mn = grow ? mb : m;
+      const float shift = isfinite(mn) ? mn : 0.0f;
+      float ls = 0.0f;
+      bf16x8 pf[4];
+  #pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+  #pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          u32x4 w;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w0 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e], c, -shift));
+            const float w1 = __builtin_amdgcn_exp2f(fmaf(s[jj][8 * part + 2 * e + 1], c, -shift));
+            ls += w0 + w1;
+            w[e] = pack2(w0, w1);
+          }
+          pf[2 * jj + part] = (bf16x8)w;
+        }
+      if (__ballot(grow)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - shift);
+        l *= alpha;
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      }
+      l += ls;
+      m = mn;
+      // O' (128 d x 32 queries) += V' P', the weights rounded to bf16.
+  #pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+  #pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] = mfma(frag_tr(Vl[st], 32 * db, ks), pf[ks], o[db]);
+      store_rows(Kl[st], rk);
+      store_rows(Vl[st ^ 1], rv);
+      __syncthreads();
+    };
+    for (int j = 0; j < nkb; j += 2) {
+      step(j, sa, sb);
+      step(j + 1, sb, sa);
     }
-  if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
+
+    // Both halves of the wave summed their keys' weights against the same shift.
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.0f / l;
+    uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
+  #pragma unroll
+    for (int db = 0; db < 4; ++db)
+  #pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * lh;
+        *reinterpret_cast<u32x2*>(obase + d) =
+            u32x2{pack2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv), pack2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv)};
+      }
+    if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
+  }
 }
 
 // ---- backward: delta = rowsum(dO .* O) -------------------------------------------
@@ -333,36 +338,36 @@ __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
 
 // ---- backward: shared pieces -----------------------------------------------------
 // Both kernels run one wave per SIMD (each needs most of the register file),
-// so each wave keeps its matrix core fed by itself: every product phase
-// reads the LDS fragments of the next 16-deep slice while the products of
-// this one issue (the sched_barrier fences keep the compiler from sinking
-// the reads back next to their products).  The next block's global loads
-// are issued once the weights are formed and land after the products.
+// so each wave keeps its matrix core busy by itself.  A step's 64-row score
+// tile is handled in two halves so that the vector work of one half runs
+// while the matrix cores do the other half's products:
+//   A0: scores of rows 0..31;   A1: scores of rows 32..63 || weights of rows 0..31;
+//   C0: gradient products over rows 0..31 || weights of rows 32..63;
+//   C1: gradient products over rows 32..63.
+// LDS fragments are read a few slices ahead of the products that use them;
+// sched_barrier fences that only vector, scalar and transcendental work may
+// cross keep the compiler from sinking those reads back next to their
+// products while letting the other half's arithmetic slide in between.
+// The score accumulators start from the per-row constants they are later
+// offset by (-lse / scale for S, -delta for dP), so the weights need no
+// separate subtraction: P = exp2(c S~), dS = P dP~.
 
-// Phase A: two 32 x 32 score tiles and two dot-product tiles over d = 128,
-// A operands from row-major tiles x and y (rows r0 = 0 and 32), B operands
-// the wave's own rows xf and yf.
-__device__ __forceinline__ void scores(const uint16_t* x, const uint16_t* y, const bf16x8 (&xf)[8],
-                                       const bf16x8 (&yf)[8], f32x16 (&s)[2], f32x16 (&t)[2]) {
-  s[0] = s[1] = t[0] = t[1] = f32x16{};
-  bf16x8 fa[2][4];
+constexpr int kFence = 0x0406;  // VALU, SALU and transcendental instructions may cross
+
+// 16 products over d = 128: s += x[rows 32 j ..] xf, t += y[rows 32 j ..] yf,
+// the A fragments read three slices ahead.
+__device__ __forceinline__ void scores_half(const uint16_t* x, const uint16_t* y, int j, const bf16x8 (&xf)[8],
+                                            const bf16x8 (&yf)[8], f32x16& s, f32x16& t) {
+  bf16x8 fx[4], fy[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) fa[0][j] = frag_rows(x, 32 * j, 0), fa[0][2 + j] = frag_rows(y, 32 * j, 0);
+  for (int ks = 0; ks < 3; ++ks) fx[ks] = frag_rows(x, 32 * j, ks), fy[ks] = frag_rows(y, 32 * j, ks);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    const int cu = ks & 1;
-    if (ks < 7) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        fa[cu ^ 1][j] = frag_rows(x, 32 * j, ks + 1), fa[cu ^ 1][2 + j] = frag_rows(y, 32 * j, ks + 1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      s[j] = mfma(fa[cu][j], xf[ks], s[j]);
-      t[j] = mfma(fa[cu][2 + j], yf[ks], t[j]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    if (ks + 3 < 8) fx[(ks + 3) % 4] = frag_rows(x, 32 * j, ks + 3), fy[(ks + 3) % 4] = frag_rows(y, 32 * j, ks + 3);
+    __builtin_amdgcn_sched_barrier(kFence);
+    s = mfma(fx[ks % 4], xf[ks], s);
+    t = mfma(fy[ks % 4], yf[ks], t);
+    __builtin_amdgcn_sched_barrier(kFence);
   }
 }
 
@@ -378,143 +383,168 @@ constexpr int kBwdQ = 64;   // queries per step
 constexpr size_t kStageBwd = 2 * kTileElems * sizeof(uint16_t) + 2 * 64 * sizeof(float);
 constexpr size_t kDkdvLds = 2 * kStageBwd;
 
+// The gradient products of slices ks0, ks0 + 1 (rows 16 ks0 .. 16 ks0 + 31):
+// dv += dO' P, dk += Q' dS, fragments read half a slice ahead.
+__device__ __forceinline__ void grads_half(const uint16_t* g, const uint16_t* q, int ks0, const bf16x8 (&pf)[4],
+                                           const bf16x8 (&sf)[4], f32x16 (&dv)[4], f32x16 (&dk)[4]) {
+  // Unit u = (slice ks0 + u / 2, d blocks 2 (u % 2), 2 (u % 2) + 1).
+  bf16x8 fg[3][2], fq[3][2];
+  auto read = [&](int u, int r) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int db = 2 * (u % 2) + e;
+      fg[r][e] = frag_tr(g, 32 * db, ks0 + u / 2);
+      fq[r][e] = frag_tr(q, 32 * db, ks0 + u / 2);
+    }
+  };
+  read(0, 0);
+  read(1, 1);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (u + 2 < 4) read(u + 2, (u + 2) % 3);
+    __builtin_amdgcn_sched_barrier(kFence);
+    const int ks = ks0 + u / 2;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int db = 2 * (u % 2) + e;
+      dv[db] = mfma(fg[u % 3][e], pf[ks], dv[db]);
+      dk[db] = mfma(fq[u % 3][e], sf[ks], dk[db]);
+    }
+    __builtin_amdgcn_sched_barrier(kFence);
+  }
+}
+
+// P and dS of score rows 32 j .. 32 j + 31 into pf[2 j], pf[2 j + 1], sf[...].
+__device__ __forceinline__ void weights_rows(const f32x16& s, const f32x16& dp, float c, bf16x8& p0, bf16x8& p1,
+                                             bf16x8& s0, bf16x8& s1) {
+  u32x4 wp[2], ws[2];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float w0 = __builtin_amdgcn_exp2f(s[i] * c), w1 = __builtin_amdgcn_exp2f(s[i + 1] * c);
+    wp[i / 8][(i % 8) / 2] = pack2(w0, w1);
+    ws[i / 8][(i % 8) / 2] = pack2(w0 * dp[i], w1 * dp[i + 1]);
+  }
+  p0 = (bf16x8)wp[0], p1 = (bf16x8)wp[1], s0 = (bf16x8)ws[0], s1 = (bf16x8)ws[1];
+}
+
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const size_t stage_elems = kStageBwd / sizeof(uint16_t);
-  const int kbk = (int)blockIdx.x;  // the first key blocks see the most queries: heaviest first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int hk = h / (p.heads / p.kv_heads);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int lr = lane % 32, lh = lane / 32;
-  const int k0 = kbk * kBwdK + wave * 32;
-  const int key = k0 + lr;
+  const int nkb = p.seq / kBwdK;
+  // Causal: workgroup x takes key blocks x and nkb - 1 - x, so every
+  // workgroup sweeps the same number of query blocks.
+  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nkb) ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int kbk = pass == 0 ? (int)blockIdx.x : nkb - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int hk = h / (p.heads / p.kv_heads);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int lr = lane % 32, lh = lane / 32;
+    const int k0 = kbk * kBwdK + wave * 32;
+    const int key = k0 + lr;
 
-  const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-  const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-  const float* lbase = p.lse + (int64_t)b * p.seq * p.heads + h;
-  const float* dbase = p.delta + (int64_t)b * p.seq * p.heads + h;
-  const int64_t koff = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
+    const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const float* lbase = p.lse + (int64_t)b * p.seq * p.heads + h;
+    const float* dbase = p.delta + (int64_t)b * p.seq * p.heads + h;
+    const int64_t koff = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
 
-  bf16x8 kf[8], vf[8];
-  row_operand(p.k + koff, kf);
-  row_operand(p.v + koff, vf);
+    bf16x8 kf[8], vf[8];
+    row_operand(p.k + koff, kf);
+    row_operand(p.v + koff, vf);
 
-  f32x16 dk[4], dv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
-  const float c = p.scale * kLog2e;
+    f32x16 dk[4], dv[4];
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
+    const float c = p.scale * kLog2e;
 
-  // Stage layout: Q tile, dO tile, then [lse log2 e | delta] of its 64 queries.
-  auto Qs = [&](int s) { return lds + s * stage_elems; };
-  auto Gs = [&](int s) { return lds + s * stage_elems + kTileElems; };
-  auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
+    // Stage layout: Q tile, dO tile, then [-lse / scale | -delta] of its 64 queries.
+    auto Qs = [&](int s) { return lds + s * stage_elems; };
+    auto Gs = [&](int s) { return lds + s * stage_elems + kTileElems; };
+    auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
 
-  const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
-  const int nq = p.seq / kBwdQ;
-  const TileRows rows(p.q_ss);
-  u32x4 rq[4], rg[4];
-  // Threads t and t + 128 both carry entry t % 128 of [lse log2 e | delta].
-  const int lt = threadIdx.x % 128;
-  const float* lsrc = lt < 64 ? lbase : dbase;
-  const float lmul = lt < 64 ? kLog2e : 1.0f;
-  float rl = 0.0f;
-  auto fetch = [&](int qb) {
-    const int64_t at = (int64_t)qb * kBwdQ * p.q_ss;
-    rows.load(qbase + at, rq);
-    rows.load(gbase + at, rg);
-    rl = lsrc[(int64_t)(qb * kBwdQ + lt % 64) * p.heads];
-  };
-  auto land = [&](int s) {
-    store_rows(Qs(s), rq);
-    store_rows(Gs(s), rg);
-    Ls(s)[lt] = rl * lmul;
-  };
-  fetch(qstart);
-  land(0);
-  __syncthreads();
-  for (int qb = qstart; qb < nq; ++qb) {
-    const int st = (qb - qstart) & 1;
-    fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
-    // S = Q K', dP = dO V' (64 queries x 32 keys; queries on registers).
-    f32x16 s[2], dp[2];
-    scores(Qs(st), Gs(st), kf, vf, s, dp);
-    // P = exp2(S c - lse log2 e), dS = P (dP - delta); on the diagonal the
-    // masked scores become -inf, so their P and dS are exactly 0.
-    const float* L = Ls(st);
-    const int qq0 = qb * kBwdQ;
-    if (p.causal && qq0 < k0 + 32) {
-      const int lim = key - qq0 - 4 * lh;  // masked: query offset 32 j + 8 (i / 4) + i % 4 < lim
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (32 * j + 8 * (i / 4) + i % 4 < lim) s[j][i] = -INFINITY;
-    }
-    bf16x8 pf[4], sf[4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        u32x4 wp, ws;
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          // Registers 8 part + 4 g2 + (0..3): queries 32 j + 8 (2 part + g2) + 4 lh + (0..3).
-          const int q4 = 32 * j + 8 * (2 * part + g2) + 4 * lh;
-          const f32x4 lq = *reinterpret_cast<const f32x4*>(L + q4);
-          const f32x4 dq = *reinterpret_cast<const f32x4*>(L + 64 + q4);
-          float pv[4], sv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 8 * part + 4 * g2 + e;
-            const float w = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq[e]));
-            pv[e] = w;
-            sv[e] = w * (dp[j][i] - dq[e]);
-          }
-          wp[2 * g2] = pack2(pv[0], pv[1]);
-          wp[2 * g2 + 1] = pack2(pv[2], pv[3]);
-          ws[2 * g2] = pack2(sv[0], sv[1]);
-          ws[2 * g2 + 1] = pack2(sv[2], sv[3]);
-        }
-        pf[2 * j + part] = (bf16x8)wp;
-        sf[2 * j + part] = (bf16x8)ws;
+    const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
+    const int nq = p.seq / kBwdQ;
+    const TileRows rows(p.q_ss);
+    u32x4 rq[4], rg[4];
+    // Threads t and t + 128 both carry entry t % 128 of [-lse / scale | -delta].
+    const int lt = threadIdx.x % 128;
+    const float* lsrc = lt < 64 ? lbase : dbase;
+    const float lmul = lt < 64 ? -1.0f / p.scale : -1.0f;
+    float rl = 0.0f;
+    auto fetch = [&](int qb) {
+      const int64_t at = (int64_t)qb * kBwdQ * p.q_ss;
+      rows.load(qbase + at, rq);
+      rows.load(gbase + at, rg);
+      rl = lsrc[(int64_t)(qb * kBwdQ + lt % 64) * p.heads];
+    };
+    auto land = [&](int s) {
+      store_rows(Qs(s), rq);
+      store_rows(Gs(s), rg);
+      Ls(s)[lt] = rl * lmul;
+    };
+    // Accumulator start: register i of row block j holds query 32 j + 8 (i / 4) + 4 lh + i % 4.
+    auto start = [&](const float* v, int j) {
+      f32x16 a;
+  #pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(v + 32 * j + 8 * m + 4 * lh);
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * m + e] = x[e];
       }
-    }
-    // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
-    bf16x8 fc[2][8];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) fc[0][db] = frag_tr(Gs(st), 32 * db, 0), fc[0][4 + db] = frag_tr(Qs(st), 32 * db, 0);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int cu = ks & 1;
-      if (ks < 3) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-          fc[cu ^ 1][db] = frag_tr(Gs(st), 32 * db, ks + 1), fc[cu ^ 1][4 + db] = frag_tr(Qs(st), 32 * db, ks + 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        dv[db] = mfma(fc[cu][db], pf[ks], dv[db]);
-        dk[db] = mfma(fc[cu][4 + db], sf[ks], dk[db]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    land(st ^ 1);
+      return a;
+    };
+    fetch(qstart);
+    land(0);
     __syncthreads();
-  }
-  // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
-  const int64_t out = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * db + 8 * g + 4 * lh;
-      const float sc = p.scale;
-      *reinterpret_cast<u32x2*>(p.dk + out + d) =
-          u32x2{pack2(dk[db][4 * g] * sc, dk[db][4 * g + 1] * sc), pack2(dk[db][4 * g + 2] * sc, dk[db][4 * g + 3] * sc)};
-      *reinterpret_cast<u32x2*>(p.dv + out + d) =
-          u32x2{pack2(dv[db][4 * g], dv[db][4 * g + 1]), pack2(dv[db][4 * g + 2], dv[db][4 * g + 3])};
+    for (int qb = qstart; qb < nq; ++qb) {
+      const int st = (qb - qstart) & 1;
+      fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
+      const uint16_t *Q = Qs(st), *G = Gs(st);
+      const float* L = Ls(st);
+      // S~ = Q K' - lse / scale, dP~ = dO V' - delta (64 queries x 32 keys).
+      f32x16 s[2], dp[2];
+      s[0] = start(L, 0), dp[0] = start(L + 64, 0);
+      s[1] = start(L, 1), dp[1] = start(L + 64, 1);
+      scores_half(Q, G, 0, kf, vf, s[0], dp[0]);
+      // On the diagonal the masked scores become -inf: their P and dS are exactly 0.
+      const int qq0 = qb * kBwdQ;
+      const bool diagonal = p.causal && qq0 < k0 + 32;
+      const int lim = key - qq0 - 4 * lh;  // masked: query offset 32 j + 8 (i / 4) + i % 4 < lim
+      if (diagonal) {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (8 * (i / 4) + i % 4 < lim) s[0][i] = -INFINITY;
+      }
+      bf16x8 pf[4], sf[4];
+      scores_half(Q, G, 1, kf, vf, s[1], dp[1]);
+      weights_rows(s[0], dp[0], c, pf[0], pf[1], sf[0], sf[1]);
+      if (diagonal) {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 + 8 * (i / 4) + i % 4 < lim) s[1][i] = -INFINITY;
+      }
+      // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
+      grads_half(G, Q, 0, pf, sf, dv, dk);
+      weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
+      grads_half(G, Q, 2, pf, sf, dv, dk);
+      land(st ^ 1);
+      __syncthreads();
     }
+    // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
+    const int64_t out = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
+  #pragma unroll
+    for (int db = 0; db < 4; ++db)
+  #pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * lh;
+        const float sc = p.scale;
+        *reinterpret_cast<u32x2*>(p.dk + out + d) =
+            u32x2{pack2(dk[db][4 * g] * sc, dk[db][4 * g + 1] * sc), pack2(dk[db][4 * g + 2] * sc, dk[db][4 * g + 3] * sc)};
+        *reinterpret_cast<u32x2*>(p.dv + out + d) =
+            u32x2{pack2(dv[db][4 * g], dv[db][4 * g + 1]), pack2(dv[db][4 * g + 2], dv[db][4 * g + 3])};
+      }
+  }
 }
 
 // ---- backward: dQ for a block of 128 queries -----------------------------------------
@@ -524,105 +554,127 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 
 constexpr size_t kDqLds = 4 * kTileElems * sizeof(uint16_t);  // (K, V) x 2 stages
 
+// dq += K' dS' over slices ks0, ks0 + 1, fragments one slice ahead.
+__device__ __forceinline__ void dq_half(const uint16_t* k, int ks0, const bf16x8 (&sf)[4], f32x16 (&dq)[4]) {
+  bf16x8 f[2][4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) f[0][db] = frag_tr(k, 32 * db, ks0);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    if (u == 0) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) f[1][db] = frag_tr(k, 32 * db, ks0 + 1);
+    }
+    __builtin_amdgcn_sched_barrier(kFence);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) dq[db] = mfma(f[u][db], sf[ks0 + u], dq[db]);
+    __builtin_amdgcn_sched_barrier(kFence);
+  }
+}
+
+// dS' of key rows 32 j .. 32 j + 31 (one query per lane) into sf[2 j], sf[2 j + 1].
+__device__ __forceinline__ void dq_weights(const f32x16& s, const f32x16& dp, float c, bf16x8& s0, bf16x8& s1) {
+  u32x4 w[2];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float p0 = __builtin_amdgcn_exp2f(s[i] * c), p1 = __builtin_amdgcn_exp2f(s[i + 1] * c);
+    w[i / 8][(i % 8) / 2] = pack2(p0 * dp[i], p1 * dp[i + 1]);
+  }
+  s0 = (bf16x8)w[0], s1 = (bf16x8)w[1];
+}
+
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int nqb = p.seq / kFwdQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int hk = h / (p.heads / p.kv_heads);
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int lr = lane % 32, lh = lane / 32;
-  const int q0 = qb * kFwdQ + wave * 32;
-  const int query = q0 + lr;
+  // Causal: workgroup x takes query blocks x and nqb - 1 - x (equal work).
+  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int hk = h / (p.heads / p.kv_heads);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int lr = lane % 32, lh = lane / 32;
+    const int q0 = qb * kFwdQ + wave * 32;
+    const int query = q0 + lr;
 
-  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
-  bf16x8 qf[8], gf[8];
-  row_operand(p.q + qoff, qf);
-  row_operand(p.dout + qoff, gf);
-  const int64_t srow = ((int64_t)b * p.seq + query) * p.heads + h;
-  const float lq = p.lse[srow] * kLog2e;
-  const float dq_delta = p.delta[srow];
-  const float c = p.scale * kLog2e;
+    const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
+    bf16x8 qf[8], gf[8];
+    row_operand(p.q + qoff, qf);
+    row_operand(p.dout + qoff, gf);
+    const int64_t srow = ((int64_t)b * p.seq + query) * p.heads + h;
+    // S~' = K Q' - lse / scale and dP~' = V dO' - delta start from these.
+    const float ls0 = -p.lse[srow] / p.scale;
+    const float dl0 = -p.delta[srow];
+    const float c = p.scale * kLog2e;
 
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  f32x16 dq[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    f32x16 dq[4];
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
 
-  const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
-  const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
-  const TileRows rows(p.k_ss);
-  u32x4 rk[4], rv[4];
-  auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
-  auto Vs = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
-  rows.load(kbase, rk);
-  rows.load(vbase, rv);
-  store_rows(Ks(0), rk);
-  store_rows(Vs(0), rv);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int st = kb & 1;
-    const int64_t at = (int64_t)min(kb + 1, nkb - 1) * step_elems;  // past the end: a harmless reload
-    rows.load(kbase + at, rk);
-    rows.load(vbase + at, rv);
-    f32x16 s[2], dp[2];
-    scores(Ks(st), Vs(st), qf, gf, s, dp);
-    const int key0 = kb * kFwdK;
-    if (p.causal && key0 + kFwdK > q0) {
-      const int lim = query - key0 - 4 * lh;  // masked: key offset 32 j + 8 (i / 4) + i % 4 > lim
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (32 * j + 8 * (i / 4) + i % 4 > lim) s[j][i] = -INFINITY;
-    }
-    bf16x8 sf[4];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 8 * part + 2 * e;
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[j][i], c, -lq));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[j][i + 1], c, -lq));
-          w[e] = pack2(p0 * (dp[j][i] - dq_delta), p1 * (dp[j][i + 1] - dq_delta));  // dS'
-        }
-        sf[2 * j + part] = (bf16x8)w;
-      }
-    // dQ' (128 d x 32 queries) += K' dS'.
-    bf16x8 fc[2][4];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) fc[0][db] = frag_tr(Ks(st), 32 * db, 0);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int cu = ks & 1;
-      if (ks < 3) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) fc[cu ^ 1][db] = frag_tr(Ks(st), 32 * db, ks + 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int db = 0; db < 4; ++db) dq[db] = mfma(fc[cu][db], sf[ks], dq[db]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    store_rows(Ks(st ^ 1), rk);
-    store_rows(Vs(st ^ 1), rv);
+    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
+    const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
+    const TileRows rows(p.k_ss);
+    u32x4 rk[4], rv[4];
+    auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
+    auto Vs = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
+    rows.load(kbase, rk);
+    rows.load(vbase, rv);
+    store_rows(Ks(0), rk);
+    store_rows(Vs(0), rv);
     __syncthreads();
-  }
-  uint16_t* out = p.dq + qoff;
-#pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * db + 8 * g + 4 * lh;
-      const float sc = p.scale;
-      *reinterpret_cast<u32x2*>(out + d) =
-          u32x2{pack2(dq[db][4 * g] * sc, dq[db][4 * g + 1] * sc), pack2(dq[db][4 * g + 2] * sc, dq[db][4 * g + 3] * sc)};
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int st = kb & 1;
+      const int64_t at = (int64_t)min(kb + 1, nkb - 1) * step_elems;  // past the end: a harmless reload
+      rows.load(kbase + at, rk);
+      rows.load(vbase + at, rv);
+      const uint16_t *K = Ks(st), *V = Vs(st);
+      f32x16 s[2], dp[2];
+  #pragma unroll
+      for (int j = 0; j < 2; ++j)
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) s[j][i] = ls0, dp[j][i] = dl0;
+      scores_half(K, V, 0, qf, gf, s[0], dp[0]);
+      const int key0 = kb * kFwdK;
+      const bool diagonal = p.causal && key0 + kFwdK > q0;
+      const int lim = query - key0 - 4 * lh;  // masked: key offset 32 j + 8 (i / 4) + i % 4 > lim
+      if (diagonal) {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (8 * (i / 4) + i % 4 > lim) s[0][i] = -INFINITY;
+      }
+      bf16x8 sf[4];
+      scores_half(K, V, 1, qf, gf, s[1], dp[1]);
+      dq_weights(s[0], dp[0], c, sf[0], sf[1]);
+      if (diagonal) {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 + 8 * (i / 4) + i % 4 > lim) s[1][i] = -INFINITY;
+      }
+      // dQ' (128 d x 32 queries) += K' dS'.
+      dq_half(K, 0, sf, dq);
+      dq_weights(s[1], dp[1], c, sf[2], sf[3]);
+      dq_half(K, 2, sf, dq);
+      store_rows(Ks(st ^ 1), rk);
+      store_rows(Vs(st ^ 1), rv);
+      __syncthreads();
     }
+    uint16_t* out = p.dq + qoff;
+  #pragma unroll
+    for (int db = 0; db < 4; ++db)
+  #pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * lh;
+        const float sc = p.scale;
+        *reinterpret_cast<u32x2*>(out + d) =
+            u32x2{pack2(dq[db][4 * g] * sc, dq[db][4 * g + 1] * sc), pack2(dq[db][4 * g + 2] * sc, dq[db][4 * g + 3] * sc)};
+      }
+  }
 }
+
+// Workgroups along the sequence: causal ones take a block and its mirror.
+unsigned blocks_x(int nblocks, int causal) { return causal ? (unsigned)(nblocks + 1) / 2 : (unsigned)nblocks; }
 
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
@@ -685,8 +737,8 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
   TH_HIP(hipFuncSetAttribute((const void*)attn_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFwdLds));
   AttnArgs a = args_of(d);
   th::Builder b("attention_fwd", 5);
-  int k = b.kernel((const void*)attn_fwd, "attn_fwd", dim3(d->seq / kFwdQ, d->heads, d->batch), dim3(256),
-                   (uint32_t)kFwdLds, a);
+  int k = b.kernel((const void*)attn_fwd, "attn_fwd", dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch),
+                   dim3(256), (uint32_t)kFwdLds, a);
   b.ref(0, k, TH_OFFSET(AttnArgs, q));
   b.ref(1, k, TH_OFFSET(AttnArgs, k));
   b.ref(2, k, TH_OFFSET(AttnArgs, v));
@@ -695,7 +747,7 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
   for (int v = 0; v < 4; ++v) b.align(v, 16);
   const double S = d->seq, BH = (double)d->batch * d->heads;
   const double flops = 4.0 * BH * S * S * kD * (d->causal ? 0.5 : 1.0);
-  b.work(2.0 * BH * S * kD * 4 + 4.0 * BH * S, flops, (int64_t)(d->seq / kFwdQ) * d->heads * d->batch);
+  b.work(2.0 * BH * S * kD * 4 + 4.0 * BH * S, flops, (int64_t)blocks_x(d->seq / kFwdQ, d->causal) * d->heads * d->batch);
   *out = b.release();
   return TH_OK;
 }
@@ -714,9 +766,9 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   b.own(delta);
   a.delta = static_cast<float*>(delta);
   int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, a);
-  int k1 = b.kernel((const void*)attn_bwd_dkdv, "attn_bwd_dkdv", dim3(d->seq / kBwdK, d->heads, d->batch), dim3(256),
+  int k1 = b.kernel((const void*)attn_bwd_dkdv, "attn_bwd_dkdv", dim3(blocks_x(d->seq / kBwdK, d->causal), d->heads, d->batch), dim3(256),
                     (uint32_t)kDkdvLds, a);
-  int k2 = b.kernel((const void*)attn_bwd_dq, "attn_bwd_dq", dim3(d->seq / kFwdQ, d->heads, d->batch), dim3(256),
+  int k2 = b.kernel((const void*)attn_bwd_dq, "attn_bwd_dq", dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch), dim3(256),
                     (uint32_t)kDqLds, a);
   const size_t offs[9] = {TH_OFFSET(AttnArgs, q),   TH_OFFSET(AttnArgs, k),  TH_OFFSET(AttnArgs, v),
                           TH_OFFSET(AttnArgs, o),   TH_OFFSET(AttnArgs, lse), TH_OFFSET(AttnArgs, dout),
@@ -726,7 +778,7 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   for (int v : {0, 1, 2, 3, 5, 6, 7, 8}) b.align(v, 16);
   const double S = d->seq, BH = (double)d->batch * d->heads;
   const double flops = 2.5 * 4.0 * BH * S * S * kD * (d->causal ? 0.5 : 1.0);
-  b.work(2.0 * BH * S * kD * 8 + 8.0 * BH * S, flops, (int64_t)(d->seq / kBwdK) * d->heads * d->batch);
+  b.work(2.0 * BH * S * kD * 8 + 8.0 * BH * S, flops, (int64_t)blocks_x(d->seq / kBwdK, d->causal) * d->heads * d->batch);
   *out = b.release();
   return TH_OK;
 }
