@@ -280,7 +280,7 @@ typedef struct th_attention_desc {
   int32_t batch, heads, kv_heads, seq, head_dim;
   int32_t causal;
   float scale;
-  int32_t reserved;
+  int32_t flags; /* backward: TH_ATTN_RECOMPUTE_DQ; 0 otherwise */
   const void* q;
   const void* k;
   const void* v;
@@ -300,8 +300,14 @@ typedef struct th_attention_desc {
  * forward (ext/cuDNNExt.jl:38-55,116-210). */
 int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
 
+/* Backward flag: never store dS; the dQ sweep recomputes S and dP instead. */
+#define TH_ATTN_RECOMPUTE_DQ 1
+
 /* dq, dk, dv from q, k, v, o, lse (as the forward wrote them) and dout;
- * deterministic (no atomics), kv_heads == heads.
+ * deterministic (no atomics), kv_heads == heads.  The dK/dV sweep stores dS
+ * (bf16, 2*batch*heads*seq^2 bytes of workspace the launch owns) for the dQ
+ * sweep; when that exceeds 16 GiB, or with TH_ATTN_RECOMPUTE_DQ, the dQ sweep
+ * recomputes S and dP instead and the workspace is not allocated.
  * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 dout, 6 dq, 7 dk, 8 dv.  Replaces the
  * cuTile transposed folds of the backward (ext/cuTileExt/transpose.jl:1-213). */
 int th_build_attention_bwd(const th_attention_desc* desc, th_launch** host_out);

@@ -61,6 +61,7 @@ struct AttnArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
+  uint16_t* ds;          // backward workspace: dS' as bf16 [b][h][key][query], or null
   int64_t q_sh, q_ss, q_sb;  // strides (elements) of q, o, dout, dq along head, position, batch
   int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
   int32_t seq, heads, kv_heads, batch;
@@ -371,6 +372,28 @@ __device__ __forceinline__ void scores_half(const uint16_t* x, const uint16_t* y
   }
 }
 
+// The same with the B operands from LDS too: rows 32 w .. 32 w + 31 of the
+// row-major tiles bx, by (w the wave), read with the A fragments two slices
+// ahead.
+__device__ __forceinline__ void scores_lds(const uint16_t* x, const uint16_t* y, int j, const uint16_t* bx,
+                                           const uint16_t* by, int w, f32x16& s, f32x16& t) {
+  bf16x8 f[3][4];
+  auto read = [&](int ks, int r) {
+    f[r][0] = frag_rows(x, 32 * j, ks), f[r][1] = frag_rows(y, 32 * j, ks);
+    f[r][2] = frag_rows(bx, 32 * w, ks), f[r][3] = frag_rows(by, 32 * w, ks);
+  };
+  read(0, 0);
+  read(1, 1);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    if (ks + 2 < 8) read(ks + 2, (ks + 2) % 3);
+    __builtin_amdgcn_sched_barrier(kFence);
+    s = mfma(f[ks % 3][0], f[ks % 3][2], s);
+    t = mfma(f[ks % 3][1], f[ks % 3][3], t);
+    __builtin_amdgcn_sched_barrier(kFence);
+  }
+}
+
 // ---- backward: dK, dV for a block of 128 keys -------------------------------------
 // Each wave owns 32 keys.  Per query block of 64: S (64 queries x 32 keys)
 // = Q K' with queries along the registers and keys along the lanes, so the
@@ -381,7 +404,10 @@ __device__ __forceinline__ void scores_half(const uint16_t* x, const uint16_t* y
 constexpr int kBwdK = 128;  // keys per workgroup
 constexpr int kBwdQ = 64;   // queries per step
 constexpr size_t kStageBwd = 2 * kTileElems * sizeof(uint16_t) + 2 * 64 * sizeof(float);
-constexpr size_t kDkdvLds = 2 * kStageBwd;
+constexpr int kDsRow = 72;  // LDS row (bf16) of a wave's dS' transpose scratch: 64 queries + 8
+constexpr size_t kDsScratch = 2 * kStageBwd;                          // 4 waves x 32 rows of kDsRow
+constexpr size_t kKvBlock = kDsScratch + 4 * 32 * kDsRow * sizeof(uint16_t);  // K, V of the 128 keys
+constexpr size_t kDkdvLds = kKvBlock + 2 * 2 * kTileElems * sizeof(uint16_t);
 
 // The gradient products of slices ks0, ks0 + 1 (rows 16 ks0 .. 16 ks0 + 31):
 // dv += dO' P, dk += Q' dS, fragments read half a slice ahead.
@@ -427,6 +453,9 @@ __device__ __forceinline__ void weights_rows(const f32x16& s, const f32x16& dp, 
   p0 = (bf16x8)wp[0], p1 = (bf16x8)wp[1], s0 = (bf16x8)ws[0], s1 = (bf16x8)ws[1];
 }
 
+// kStore: also write dS' (bf16, exactly the values the dK product uses) to
+// the workspace, for the dQ kernel that reads it instead of recomputing.
+template <bool kStore>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const size_t stage_elems = kStageBwd / sizeof(uint16_t);
@@ -447,11 +476,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
     const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const float* lbase = p.lse + (int64_t)b * p.seq * p.heads + h;
     const float* dbase = p.delta + (int64_t)b * p.seq * p.heads + h;
-    const int64_t koff = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
-
-    bf16x8 kf[8], vf[8];
-    row_operand(p.k + koff, kf);
-    row_operand(p.v + koff, vf);
+    // The workgroup's 128 keys of K and V, row-major in LDS for the whole sweep.
+    uint16_t* const KT = lds + kKvBlock / sizeof(uint16_t);
+    uint16_t* const VT = KT + 2 * kTileElems;
+    {
+      const TileRows krows(p.k_ss);
+      const uint16_t* kb0 = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)kbk * kBwdK * p.k_ss;
+      const uint16_t* vb0 = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)kbk * kBwdK * p.k_ss;
+      u32x4 r[4];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        krows.load(kb0 + (int64_t)half * 64 * p.k_ss, r);
+        store_rows(KT + half * kTileElems, r);
+        krows.load(vb0 + (int64_t)half * 64 * p.k_ss, r);
+        store_rows(VT + half * kTileElems, r);
+      }
+    }
 
     f32x16 dk[4], dv[4];
   #pragma unroll
@@ -506,7 +546,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       f32x16 s[2], dp[2];
       s[0] = start(L, 0), dp[0] = start(L + 64, 0);
       s[1] = start(L, 1), dp[1] = start(L + 64, 1);
-      scores_half(Q, G, 0, kf, vf, s[0], dp[0]);
+      scores_lds(Q, G, 0, KT, VT, wave, s[0], dp[0]);
       // On the diagonal the masked scores become -inf: their P and dS are exactly 0.
       const int qq0 = qb * kBwdQ;
       const bool diagonal = p.causal && qq0 < k0 + 32;
@@ -517,8 +557,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
           if (8 * (i / 4) + i % 4 < lim) s[0][i] = -INFINITY;
       }
       bf16x8 pf[4], sf[4];
-      scores_half(Q, G, 1, kf, vf, s[1], dp[1]);
+      scores_lds(Q, G, 1, KT, VT, wave, s[1], dp[1]);
       weights_rows(s[0], dp[0], c, pf[0], pf[1], sf[0], sf[1]);
+      // Keep these weights here, beside the products above, rather than sunk
+      // past the branch below into the next phase.
+      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(sf[0]), "v"(sf[1]));
       if (diagonal) {
   #pragma unroll
         for (int i = 0; i < 16; ++i)
@@ -528,6 +571,25 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       grads_half(G, Q, 0, pf, sf, dv, dk);
       weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
       grads_half(G, Q, 2, pf, sf, dv, dk);
+      if constexpr (kStore) {
+        // dS' rows [key][qq0 .. qq0 + 63], transposed through this wave's LDS
+        // scratch (32 key rows) so they leave as whole 128-byte lines.
+        // sf[ks] element e is query 16 ks + 8 (e / 4) + 4 lh + e % 4 of this lane's key.
+        uint16_t* w = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const u32x4 x = __builtin_bit_cast(u32x4, sf[ks]);
+          *reinterpret_cast<u32x2*>(w + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
+          *reinterpret_cast<u32x2*>(w + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
+        }
+        uint16_t* rows0 = p.ds + (((int64_t)b * p.heads + h) * p.seq + k0) * p.seq + qq0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = lane / 8 + 8 * i, cc = lane % 8;
+          *reinterpret_cast<u32x4*>(rows0 + (int64_t)r * p.seq + 8 * cc) =
+              *reinterpret_cast<const u32x4*>(w + r * kDsRow + 8 * cc);
+        }
+      }
       land(st ^ 1);
       __syncthreads();
     }
@@ -553,6 +615,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 // dQ' (128 d x 32 queries) += K' dS' with K' read transposed from K's tile.
 
 constexpr size_t kDqLds = 4 * kTileElems * sizeof(uint16_t);  // (K, V) x 2 stages
+constexpr double kDsBudget = 16.0 * (1 << 30);  // bytes of dS' workspace the backward may hold
 
 // dq += K' dS' over slices ks0, ks0 + 1, fragments one slice ahead.
 __device__ __forceinline__ void dq_half(const uint16_t* k, int ks0, const bf16x8 (&sf)[4], f32x16 (&dq)[4]) {
@@ -673,6 +736,68 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   }
 }
 
+// ---- backward: dQ from the stored dS' -------------------------------------------------
+// dQ' (128 d x 128 queries per workgroup) += K' dS' over key blocks of 64,
+// both operands read transposed from row-major LDS tiles: K [key][d] and
+// dS' [key][query] (the dK/dV kernel wrote every entry this sweep reads;
+// masked ones are 0).  One product per step instead of three, no exp.
+
+constexpr size_t kDqDsLds = 4 * kTileElems * sizeof(uint16_t);  // (K, dS') x 2 stages
+
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int nqb = p.seq / kFwdQ;
+  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int hk = h / (p.heads / p.kv_heads);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int lr = lane % 32, lh = lane / 32;
+    const int qw = qb * kFwdQ;  // the workgroup's first query
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const uint16_t* dbase = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + qw;
+    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
+    const TileRows krows(p.k_ss), drows(p.seq);
+    auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
+    auto Ds = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
+    f32x16 dq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
+    u32x4 rk[4], rd[4];
+    krows.load(kbase, rk);
+    drows.load(dbase, rd);
+    store_rows(Ks(0), rk);
+    store_rows(Ds(0), rd);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int st = kb & 1;
+      const int nx = min(kb + 1, nkb - 1);  // past the end: a harmless reload
+      krows.load(kbase + (int64_t)nx * kFwdK * p.k_ss, rk);
+      drows.load(dbase + (int64_t)nx * kFwdK * p.seq, rd);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 bs = frag_tr(Ds(st), 32 * wave, ks);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dq[db] = mfma(frag_tr(Ks(st), 32 * db, ks), bs, dq[db]);
+      }
+      store_rows(Ks(st ^ 1), rk);
+      store_rows(Ds(st ^ 1), rd);
+      __syncthreads();
+    }
+    uint16_t* out = p.dq + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(qw + 32 * wave + lr) * p.q_ss;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * lh;
+        const float sc = p.scale;
+        *reinterpret_cast<u32x2*>(out + d) =
+            u32x2{pack2(dq[db][4 * g] * sc, dq[db][4 * g + 1] * sc), pack2(dq[db][4 * g + 2] * sc, dq[db][4 * g + 3] * sc)};
+      }
+  }
+}
+
 // Workgroups along the sequence: causal ones take a block and its mirror.
 unsigned blocks_x(int nblocks, int causal) { return causal ? (unsigned)(nblocks + 1) / 2 : (unsigned)nblocks; }
 
@@ -756,8 +881,6 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   if (int r = th::require_ready()) return r;
   *out = nullptr;
   if (int r = check_desc(d, true)) return r;
-  TH_HIP(hipFuncSetAttribute((const void*)attn_bwd_dkdv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDkdvLds));
-  TH_HIP(hipFuncSetAttribute((const void*)attn_bwd_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDqLds));
   AttnArgs a = args_of(d);
   th::Builder b("attention_bwd", 9);
   void* delta = nullptr;
@@ -765,11 +888,26 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   if (int r = th::device_alloc((size_t)rows * sizeof(float), &delta)) return r;
   b.own(delta);
   a.delta = static_cast<float*>(delta);
+  // dS' is stored for the dQ sweep when it fits the workspace budget
+  // (4 GiB at B8 H16 S4096); beyond it dQ recomputes S and dP instead.
+  const double ds_bytes = 2.0 * d->batch * d->heads * (double)d->seq * d->seq;
+  const bool store = ds_bytes <= kDsBudget && !(d->flags & TH_ATTN_RECOMPUTE_DQ);
+  if (store) {
+    void* ds = nullptr;
+    if (int r = th::device_alloc((size_t)ds_bytes, &ds)) return r;
+    b.own(ds);
+    a.ds = static_cast<uint16_t*>(ds);
+  }
+  const void* dkdv = store ? (const void*)attn_bwd_dkdv<true> : (const void*)attn_bwd_dkdv<false>;
+  const void* dqk = store ? (const void*)attn_bwd_dq_ds : (const void*)attn_bwd_dq;
+  const size_t dq_lds = store ? kDqDsLds : kDqLds;
+  TH_HIP(hipFuncSetAttribute(dkdv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDkdvLds));
+  TH_HIP(hipFuncSetAttribute(dqk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds));
   int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, a);
-  int k1 = b.kernel((const void*)attn_bwd_dkdv, "attn_bwd_dkdv", dim3(blocks_x(d->seq / kBwdK, d->causal), d->heads, d->batch), dim3(256),
-                    (uint32_t)kDkdvLds, a);
-  int k2 = b.kernel((const void*)attn_bwd_dq, "attn_bwd_dq", dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch), dim3(256),
-                    (uint32_t)kDqLds, a);
+  int k1 = b.kernel(dkdv, store ? "attn_bwd_dkdv_store" : "attn_bwd_dkdv",
+                    dim3(blocks_x(d->seq / kBwdK, d->causal), d->heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
+  int k2 = b.kernel(dqk, store ? "attn_bwd_dq_ds" : "attn_bwd_dq",
+                    dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch), dim3(256), (uint32_t)dq_lds, a);
   const size_t offs[9] = {TH_OFFSET(AttnArgs, q),   TH_OFFSET(AttnArgs, k),  TH_OFFSET(AttnArgs, v),
                           TH_OFFSET(AttnArgs, o),   TH_OFFSET(AttnArgs, lse), TH_OFFSET(AttnArgs, dout),
                           TH_OFFSET(AttnArgs, dq),  TH_OFFSET(AttnArgs, dk), TH_OFFSET(AttnArgs, dv)};
@@ -778,7 +916,8 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   for (int v : {0, 1, 2, 3, 5, 6, 7, 8}) b.align(v, 16);
   const double S = d->seq, BH = (double)d->batch * d->heads;
   const double flops = 2.5 * 4.0 * BH * S * S * kD * (d->causal ? 0.5 : 1.0);
-  b.work(2.0 * BH * S * kD * 8 + 8.0 * BH * S, flops, (int64_t)blocks_x(d->seq / kBwdK, d->causal) * d->heads * d->batch);
+  const double ds_traffic = store ? 2.0 * ds_bytes * (d->causal ? 0.5 : 1.0) : 0.0;
+  b.work(2.0 * BH * S * kD * 8 + 8.0 * BH * S + ds_traffic, flops, (int64_t)blocks_x(d->seq / kBwdK, d->causal) * d->heads * d->batch);
   *out = b.release();
   return TH_OK;
 }

@@ -48,7 +48,7 @@ class GemmDesc(ctypes.Structure):
 class AttentionDesc(ctypes.Structure):
     """th_attention_desc (include/tempest_hip.h)."""
     _fields_ = [("batch", c_i32), ("heads", c_i32), ("kv_heads", c_i32), ("seq", c_i32), ("head_dim", c_i32),
-                ("causal", c_i32), ("scale", c_f32), ("reserved", c_i32), ("q", c_void_p), ("k", c_void_p),
+                ("causal", c_i32), ("scale", c_f32), ("flags", c_i32), ("q", c_void_p), ("k", c_void_p),
                 ("v", c_void_p), ("o", c_void_p), ("lse", c_void_p), ("dout", c_void_p), ("dq", c_void_p),
                 ("dk", c_void_p), ("dv", c_void_p), ("q_strides", c_i64 * 3), ("k_strides", c_i64 * 3)]
 

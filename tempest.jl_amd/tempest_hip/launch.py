@@ -117,11 +117,11 @@ def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b
 # ---- op class (c) -----------------------------------------------------------
 
 def _attention_desc(batch, heads, kv_heads, seq, q, k, v, o, lse=0, dout=0, dq=0, dk=0, dv=0, causal=True,
-                    scale=0.0, q_strides=None, k_strides=None, head_dim=128):
+                    scale=0.0, q_strides=None, k_strides=None, head_dim=128, flags=0):
     qs = q_strides or (head_dim, heads * head_dim, seq * heads * head_dim)
     ks = k_strides or (head_dim, kv_heads * head_dim, seq * kv_heads * head_dim)
     d = _lib.AttentionDesc(batch=batch, heads=heads, kv_heads=kv_heads, seq=seq, head_dim=head_dim,
-                           causal=int(causal), scale=scale, q=q, k=k, v=v, o=o, lse=lse or None,
+                           causal=int(causal), scale=scale, flags=flags, q=q, k=k, v=v, o=o, lse=lse or None,
                            dout=dout or None, dq=dq or None, dk=dk or None, dv=dv or None)
     d.q_strides[:] = list(qs)
     d.k_strides[:] = list(ks)
@@ -135,11 +135,17 @@ def attention_fwd(batch: int, heads: int, kv_heads: int, seq: int, q: int, k: in
     return _built("th_build_attention_fwd", ("q", "k", "v", "o", "lse"), ctypes.byref(d))
 
 
+RECOMPUTE_DQ = 1  # TH_ATTN_RECOMPUTE_DQ
+
+
 def attention_bwd(batch: int, heads: int, seq: int, q: int, k: int, v: int, o: int, lse: int, dout: int, dq: int,
-                  dk: int, dv: int, causal: bool = True, scale: float = 0.0, **strides) -> Launch:
-    """dq, dk, dv of sum(attention(q, k, v) .* dout), from the forward's o and lse."""
+                  dk: int, dv: int, causal: bool = True, scale: float = 0.0, recompute_dq: bool = False,
+                  **strides) -> Launch:
+    """dq, dk, dv of sum(attention(q, k, v) .* dout), from the forward's o and lse.
+    recompute_dq: the dQ sweep recomputes S and dP instead of reading the dS
+    the dK/dV sweep stores (the path taken anyway past 16 GiB of dS)."""
     d = _attention_desc(batch, heads, heads, seq, q, k, v, o, lse, dout, dq, dk, dv, causal=causal, scale=scale,
-                        **strides)
+                        flags=RECOMPUTE_DQ if recompute_dq else 0, **strides)
     return _built("th_build_attention_bwd", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"), ctypes.byref(d))
 
 

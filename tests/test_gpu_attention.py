@@ -56,6 +56,31 @@ def test_backward_matches_oracle(target, B, H, S, causal):
         assert relative(_np(got.view(B, S, H, 128)), ref) < TOL, name
 
 
+@pytest.mark.parametrize("S,causal", [(384, True), (256, False)])
+@pytest.mark.parametrize("recompute", [False, True])
+def test_backward_both_dq_paths(target, S, causal, recompute):
+    """Launch level: the dQ sweep reading the stored dS, and the one that
+    recomputes S and dP, each against the oracle."""
+    import tempest_hip.launch as L
+    announce("attn bwd path", S, causal, "recompute" if recompute else "stored dS")
+    B, H = 2, 2
+    gen = torch.Generator(device="cuda").manual_seed(11 * S + int(recompute))
+    q, k, v, g = (_rand((B, S, H, 128), gen) for _ in range(4))
+    o, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    lse = torch.empty(B, S, H, device="cuda")
+    ptr = lambda t: t.data_ptr()  # noqa: E731
+    fwd = L.attention_fwd(B, H, H, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), causal=causal)
+    bwd = L.attention_bwd(B, H, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), ptr(g), ptr(dq), ptr(dk), ptr(dv),
+                          causal=causal, recompute_dq=recompute)
+    assert ("attn_bwd_dq<" if recompute else "attn_bwd_dq_ds<") in bwd.describe()
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    rq, rk, rv = interpret.attention_bwd(_np(q), _np(k), _np(v), _np(g), causal)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert relative(_np(got), ref) < TOL, name
+
+
 def test_refuses_other_head_dims(target):
     import tempest_hip.launch as L
     from tempest_hip import HIPError
