@@ -321,20 +321,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
 // ---- backward: delta = rowsum(dO .* O) -------------------------------------------
 
 __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
-  // One wave per (query, head, batch) row of 128: 64 lanes x 2 elements.
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  // Sixteen lanes per (query, head, batch) row of 128, 16 bytes each; 16 rows per workgroup.
+  const int64_t row = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
   const int64_t total = (int64_t)p.batch * p.seq * p.heads;
-  if (row >= total) return;
-  const int lane = threadIdx.x % 64;
-  const int h = (int)(row % p.heads);
-  const int64_t s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
-  const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss + 2 * lane;
-  const uint32_t ow = *reinterpret_cast<const uint32_t*>(p.o + at);
-  const uint32_t gw = *reinterpret_cast<const uint32_t*>(p.dout + at);
-  float v = bf16_float((uint16_t)ow) * bf16_float((uint16_t)gw) +
-            bf16_float((uint16_t)(ow >> 16)) * bf16_float((uint16_t)(gw >> 16));
-  v = thd::wave_sum(v);
-  if (lane == 0) p.delta[(b * p.seq + s) * p.heads + h] = v;
+  const int part = threadIdx.x % 16;
+  float v = 0.0f;
+  int64_t b = 0, s = 0;
+  int h = 0;
+  if (row < total) {
+    h = (int)(row % p.heads);
+    s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
+    const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss + 8 * part;
+    const u32x4 ow = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.o + at));
+    const u32x4 gw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.dout + at));
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v += bf16_float((uint16_t)ow[e]) * bf16_float((uint16_t)gw[e]) +
+           bf16_float((uint16_t)(ow[e] >> 16)) * bf16_float((uint16_t)(gw[e] >> 16));
+  }
+#pragma unroll
+  for (int m = 8; m >= 1; m /= 2) v += __shfl_xor(v, m, 16);
+  if (row < total && part == 0) p.delta[(b * p.seq + s) * p.heads + h] = v;
 }
 
 // ---- backward: shared pieces -----------------------------------------------------
@@ -903,7 +910,7 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   const size_t dq_lds = store ? kDqDsLds : kDqLds;
   TH_HIP(hipFuncSetAttribute(dkdv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDkdvLds));
   TH_HIP(hipFuncSetAttribute(dqk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds));
-  int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, a);
+  int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, a);
   int k1 = b.kernel(dkdv, store ? "attn_bwd_dkdv_store" : "attn_bwd_dkdv",
                     dim3(blocks_x(d->seq / kBwdK, d->causal), d->heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
   int k2 = b.kernel(dqk, store ? "attn_bwd_dq_ds" : "attn_bwd_dq",

@@ -95,7 +95,8 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
     case TH_EPI_SQUARE_LOSS: fn = gemm_square_loss(la, lb, check), name = "gemm_bf16_square_loss"; break;
     default: fn = gemm_gelu_backward(la, lb, check), name = "gemm_bf16_gelu_backward"; break;
   }
-  TH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds));
+  const size_t lds_bytes = check ? kLds : kLdsDirect;
+  TH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
 
   th::Builder b("gemm_bf16", 8);
   GemmArgs g{};
@@ -125,7 +126,7 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
     b.own(ws);
     g.partial = static_cast<float*>(ws);
   }
-  int k = b.kernel(fn, name, dim3(blocks), dim3(kThreads), (uint32_t)kLds, g);
+  int k = b.kernel(fn, name, dim3(blocks), dim3(kThreads), (uint32_t)lds_bytes, g);
   b.ref(0, k, TH_OFFSET(GemmArgs, a));
   b.ref(1, k, TH_OFFSET(GemmArgs, b));
   b.ref(2, k, TH_OFFSET(GemmArgs, c));

@@ -255,6 +255,118 @@ __device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t
   }
 }
 
+// ---- the direct path (interior tiles): global -> LDS with no registers -------
+// buffer_load ... lds writes each lane's 16 bytes at M0 + 16 lane, so one
+// wave instruction fills 1 KB of LDS.  The tiles have no padding; instead the
+// 16-byte chunks of each row are XOR-permuted, which keeps both the direct
+// writes and the fragment reads free of bank conflicts:
+//   k-contiguous operand: [256 rows][64 k], 128-byte rows, chunk c of row r
+//     at c ^ ((r / 2) % 8) (16 consecutive rows of one chunk: 16 distinct
+//     bank quads, the rows alternating halves of the banks);
+//   mn-contiguous operand: [64 k][256 mn], 512-byte rows, chunk c of row r at
+//     c ^ 4 (r % 4), read transposed (ds_read_b64_tr_b16): four consecutive
+//     rows x four consecutive chunks land on 16 distinct bank quads.
+// No register transpose, and no staging registers.
+
+constexpr int kTileD = kTile * kDepth;                         // bf16 per operand stage
+constexpr size_t kLdsDirect = 4 * kTileD * sizeof(uint16_t);   // A and B, two stages: 131072 bytes
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ int at_k(int row, int chunk) { return row * kDepth + 8 * (chunk ^ ((row / 2) % 8)); }
+__device__ __forceinline__ int at_mn(int krow, int o) { return krow * kTile + 8 * ((o / 8) ^ (4 * (krow % 4))) + o % 8; }
+
+// Instruction i of wave w fills LDS bf16 [512 (8 w + i), + 512): rows
+// 64 w + 8 i .. + 7 of a k-contiguous tile, k rows 16 w + 2 i, + 1 of an
+// mn-contiguous one.  Each lane's byte offset for K tile 0 is fixed for the
+// sweep; the K advance is the scalar offset.
+template <int L>
+struct Direct {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int32_t off[8];
+  int32_t step;
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int64_t s_k, int o0) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+    if constexpr (L == kK) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 64 * w + 8 * i + l / 8, lc = (l % 8) ^ ((r / 2) % 8);
+        off[i] = (int32_t)(((int64_t)(o0 + r) * s_o + 8 * lc) * 2);
+      }
+      step = kDepth * 2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int kr = 16 * w + 2 * i + l / 32, lc = (l % 32) ^ (4 * (kr % 4));
+        off[i] = (int32_t)(((int64_t)kr * s_k + o0 + 8 * lc) * 2);
+      }
+      step = (int32_t)(kDepth * s_k * 2);
+    }
+  }
+
+  __device__ __forceinline__ void load(int kt, uint16_t* lds) const {
+    const int w = threadIdx.x / 64;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds + 512 * (8 * w + i)), 16, off[i], kt * step, 0, 0);
+  }
+};
+
+// A (or B) operand for rows o0 + lane % 32 and k = 16 kk + 8 (lane / 32) + (0..7).
+template <int L>
+__device__ __forceinline__ bf16x8 frag_direct(const uint16_t* lds, int o0, int kk) {
+  const int lane = threadIdx.x % 64;
+  if constexpr (L == kK) {
+    return *reinterpret_cast<const bf16x8*>(lds + at_k(o0 + lane % 32, 2 * kk + lane / 32));
+  } else {
+    // ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the 8-byte
+    // pieces addressed by lanes 4 q + i / 4 (q = 0..3).  Lane j addresses k
+    // row base + j / 4, columns ogrp + 4 (j % 4) + (0..3), so lane i receives
+    // k rows base + (0..3) of column ogrp + i: k in natural order.
+    const int j = lane % 16;
+    const int o = o0 + 16 * ((lane / 16) % 2) + 4 * (j % 4);
+    const int row = 16 * kk + 8 * (lane / 32) + j / 4;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at_mn(row, o)));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at_mn(row + 4, o)));
+    const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, w);
+  }
+}
+
+// The products of one K tile; the fragments of the next 16-deep step are
+// read while this step's 16 products issue (the fences keep the reads ahead).
+template <int LA, int LB>
+__device__ __forceinline__ void multiply_direct(const uint16_t* As, const uint16_t* Bs, f32x16 (&acc)[4][4], int wm,
+                                                int wn) {
+  bf16x8 af[2][4], bf[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) af[0][i] = frag_direct<LA>(As, wm * 128 + 32 * i, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bf[0][j] = frag_direct<LB>(Bs, wn * 128 + 32 * j, 0);
+#pragma unroll
+  for (int kk = 0; kk < kDepth / 16; ++kk) {
+    const int s = kk & 1;
+    if (kk + 1 < kDepth / 16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[s ^ 1][i] = frag_direct<LA>(As, wm * 128 + 32 * i, kk + 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[s ^ 1][j] = frag_direct<LB>(Bs, wn * 128 + 32 * j, kk + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---- the tile order ----------------------------------------------------------
 
 __device__ __forceinline__ void tile_of(int block, int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -296,6 +408,30 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   // tile kt out of one LDS stage, tile kt+1 (loaded during the step before)
   // lands in the other stage and tile kt+2's loads are issued.
   const int KT = (p.k + kDepth - 1) / kDepth;
+  if constexpr (!CHECK) {
+    // Interior tiles: K tile kt + 1 streams straight into the other LDS stage
+    // while the waves multiply tile kt.
+    auto Ad = [&](int st) { return lds + st * kTileD; };
+    auto Bd = [&](int st) { return lds + (2 + st) * kTileD; };
+    Direct<LA> da;
+    Direct<LB> db;
+    da.init(p.a, p.a_o, p.a_k, m0);
+    db.init(p.b, p.b_o, p.b_k, n0);
+    da.load(0, Ad(0));
+    db.load(0, Bd(0));
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const int st = kt & 1;
+      if (kt + 1 < KT) {
+        da.load(kt + 1, Ad(st ^ 1));
+        db.load(kt + 1, Bd(st ^ 1));
+      }
+      multiply_direct<LA, LB>(Ad(st), Bd(st), acc, wm, wn);
+      __builtin_amdgcn_s_waitcnt(0);  // this tile's reads and the next tile's loads are done
+      __syncthreads();
+    }
+  } else {
   Sweep<LA> sa;
   Sweep<LB> sb;
   if (!CHECK) {
@@ -332,6 +468,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   }
   if (kt < KT) multiply_tile<LA, LB>(As, Bs, As + kStage, Bs + kStage, false, ra1, rb1, acc, wm, wn, lr, lh);
 #undef TH_FETCH
+  }
 
   // ---- epilogue: lane holds C(m, n) for n = n_j + lane % 32 and
   // m = m_i + 8 g + 4 (lane / 32) + (0..3), register 4 g + (0..3).
