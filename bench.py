@@ -258,6 +258,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
+    ap.add_argument("--only", choices=["config1", "config3", "config4", "config5"], default=None,
+                    help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -280,6 +282,10 @@ def main() -> int:
 
     target = th.HIPTarget()
     log("device:", target.device_name())
+    if a.only:
+        fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5}[a.only]
+        print(json.dumps({a.only: fn(target)}), flush=True)
+        return 0
     c2 = config2(target, a.steps, a.warmup)
     log(c2["describe"])
     step_s = c2["step_s"]

@@ -31,6 +31,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <utility>
 
 namespace thg {
 
@@ -267,29 +268,70 @@ __device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t
 //     c ^ 4 (r % 4), read transposed (ds_read_b64_tr_b16): four consecutive
 //     rows x four consecutive chunks land on 16 distinct bank quads.
 // No register transpose, and no staging registers.
+//
+// The sweep's schedule is written out product by product.  Each 16-deep
+// step issues its 16 products one after another; between them go the
+// fragment reads of the next step (one after every other product) and,
+// during the first three steps, the next K tile's 16 direct loads (one
+// after every third product, so the four waves ask the CU's address unit
+// for at most ~43 bytes a clock, under its rate, and no wave stalls on a
+// full queue while it has products to issue).  At the end of the tile each
+// wave waits for its own loads, the waves meet, and the next tile's first
+// fragments are read.
+//
+// The direct loads are issued from inline assembly: the compiler, seeing an
+// LDS write by DMA, would otherwise make every later transposed LDS read
+// wait for all outstanding global loads (a vmcnt(0) before each
+// ds_read_b64_tr_b16), serializing the sweep.  Their completion is waited
+// for explicitly at the barrier, where the stage they fill is next read.
 
 constexpr int kTileD = kTile * kDepth;                         // bf16 per operand stage
 constexpr size_t kLdsDirect = 4 * kTileD * sizeof(uint16_t);   // A and B, two stages: 131072 bytes
+constexpr int kOpBytes = kTileD * 2;                           // one operand's stage: 32 KiB
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 
-__device__ __forceinline__ int at_k(int row, int chunk) { return row * kDepth + 8 * (chunk ^ ((row / 2) % 8)); }
-__device__ __forceinline__ int at_mn(int krow, int o) { return krow * kTile + 8 * ((o / 8) ^ (4 * (krow % 4))) + o % 8; }
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), unrolled.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
-// Instruction i of wave w fills LDS bf16 [512 (8 w + i), + 512): rows
-// 64 w + 8 i .. + 7 of a k-contiguous tile, k rows 16 w + 2 i, + 1 of an
-// mn-contiguous one.  Each lane's byte offset for K tile 0 is fixed for the
-// sweep; the K advance is the scalar offset.
+// One 16-byte lane load from global memory straight into LDS at M0 + 16 lane.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int32_t voff, int32_t soff, uint32_t m0) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0));
+}
+
+// Wait until this wave has at most N vector memory operations in flight and
+// no LDS reads, then meet the other waves.
+template <int N>
+__device__ __forceinline__ void wait_and_meet() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
+}
+
+// One operand of the direct path: its buffer resource, the byte offsets of
+// the wave's eight loads for K tile 0 (the K advance is the scalar offset),
+// and the LDS byte addresses of this lane's fragment reads in stage 0.
 template <int L>
-struct Direct {
+struct Operand {
   __amdgpu_buffer_rsrc_t rsrc;
   int32_t off[8];
   int32_t step;
+  uint32_t rd[4];  // k-contiguous: per 16-deep step; mn-contiguous: per 32-row block
 
-  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int64_t s_k, int o0) {
+  // Instruction i of wave w fills LDS bytes [1024 (8 w + i), + 1024) of the
+  // operand's stage: rows 64 w + 8 i .. + 7 of a k-contiguous tile, k rows
+  // 16 w + 2 i, + 1 of an mn-contiguous one.  `wo` is the wave's first row
+  // (m or n) of the tile, `lds` the operand's stage-0 byte address.
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int64_t s_k, int o0, int wo, uint32_t lds) {
     rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
     if constexpr (L == kK) {
@@ -299,6 +341,10 @@ struct Direct {
         off[i] = (int32_t)(((int64_t)(o0 + r) * s_o + 8 * lc) * 2);
       }
       step = kDepth * 2;
+      // Fragment rows wo + l % 32 (+ 32 i: the same permutation), chunk 2 kk + l / 32.
+      const int r = wo + l % 32;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) rd[kk] = lds + (uint32_t)((r * kDepth + 8 * ((2 * kk + l / 32) ^ ((r / 2) % 8))) * 2);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -306,64 +352,100 @@ struct Direct {
         off[i] = (int32_t)(((int64_t)kr * s_k + o0 + 8 * lc) * 2);
       }
       step = (int32_t)(kDepth * s_k * 2);
+      // ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the
+      // 8-byte pieces addressed by lanes 4 q + i / 4 (q = 0..3).  Lane j
+      // addresses k row j / 4 (+ 8 (l / 32), + 16 kk, + 4 for the upper
+      // half), columns ogrp + 4 (j % 4) + (0..3), so lane i receives k rows
+      // base + (0..3) of column ogrp + i: k in natural order.
+      const int j = l % 16, row = 8 * (l / 32) + j / 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int o = wo + 32 * i + 16 * ((l / 16) % 2) + 4 * (j % 4);
+        rd[i] = lds + (uint32_t)((row * kTile + 8 * ((o / 8) ^ (4 * (row % 4))) + o % 8) * 2);
+      }
     }
   }
 
-  __device__ __forceinline__ void load(int kt, uint16_t* lds) const {
-    const int w = threadIdx.x / 64;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds + 512 * (8 * w + i)), 16, off[i], kt * step, 0, 0);
+  // Load instruction i of K tile kt into the stage at LDS byte address `stage`.
+  __device__ __forceinline__ void load(int kt, uint32_t stage, int i) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    dma16(rsrc, off[i], kt * step, stage + 1024 * (8 * w + i));
+  }
+
+  // Fragment I (rows wo + 32 I + lane % 32, k = 16 KK + 8 (lane / 32) + 0..7)
+  // of the stage `so` bytes past stage 0.
+  template <int I, int KK>
+  __device__ __forceinline__ bf16x8 frag(uint32_t so) const {
+    if constexpr (L == kK) {
+      return *reinterpret_cast<const lds_bf16x8*>((uintptr_t)(rd[KK] + so + I * 32 * kDepth * 2));
+    } else {
+      const uint32_t a = rd[I] + so + KK * 16 * kTile * 2;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(a + 4 * kTile * 2));
+      const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      return __builtin_bit_cast(bf16x8, w);
+    }
   }
 };
 
-// A (or B) operand for rows o0 + lane % 32 and k = 16 kk + 8 (lane / 32) + (0..7).
-template <int L>
-__device__ __forceinline__ bf16x8 frag_direct(const uint16_t* lds, int o0, int kk) {
-  const int lane = threadIdx.x % 64;
-  if constexpr (L == kK) {
-    return *reinterpret_cast<const bf16x8*>(lds + at_k(o0 + lane % 32, 2 * kk + lane / 32));
-  } else {
-    // ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the 8-byte
-    // pieces addressed by lanes 4 q + i / 4 (q = 0..3).  Lane j addresses k
-    // row base + j / 4, columns ogrp + 4 (j % 4) + (0..3), so lane i receives
-    // k rows base + (0..3) of column ogrp + i: k in natural order.
-    const int j = lane % 16;
-    const int o = o0 + 16 * ((lane / 16) % 2) + 4 * (j % 4);
-    const int row = 16 * kk + 8 * (lane / 32) + j / 4;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at_mn(row, o)));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds + at_mn(row + 4, o)));
-    const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8, w);
-  }
-}
-
-// The products of one K tile; the fragments of the next 16-deep step are
-// read while this step's 16 products issue (the fences keep the reads ahead).
+// The K sweep of an interior tile: acc += A(m0.., :) B(:, n0..), two stages.
 template <int LA, int LB>
-__device__ __forceinline__ void multiply_direct(const uint16_t* As, const uint16_t* Bs, f32x16 (&acc)[4][4], int wm,
-                                                int wn) {
+__device__ __forceinline__ void sweep_direct(const GemmArgs& p, int m0, int n0, int wm, int wn,
+                                             f32x16 (&acc)[4][4]) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const uint32_t base = (uint32_t)(uintptr_t)lds;
+  constexpr uint32_t kStageBytes = 2 * kOpBytes;
+  Operand<LA> oa;
+  Operand<LB> ob;
+  oa.init(p.a, p.a_o, p.a_k, m0, wm * 128, base);
+  ob.init(p.b, p.b_o, p.b_k, n0, wn * 128, base + kOpBytes);
+  const int KT = p.k / kDepth;
+  // Load i (0..15) of K tile t into stage st; past the last tile the last
+  // tile is loaded again (in bounds; nothing reads it).
+  auto issue = [&](int t, int st, int i) {
+    const int tt = t < KT ? t : KT - 1;
+    const uint32_t sb = base + st * kStageBytes;
+    if (i < 8)
+      oa.load(tt, sb, i);
+    else
+      ob.load(tt, sb + kOpBytes, i - 8);
+  };
+#pragma unroll
+  for (int i = 0; i < 16; ++i) issue(0, 0, i);
+  wait_and_meet<0>();
   bf16x8 af[2][4], bf[2][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) af[0][i] = frag_direct<LA>(As, wm * 128 + 32 * i, 0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) bf[0][j] = frag_direct<LB>(Bs, wn * 128 + 32 * j, 0);
-#pragma unroll
-  for (int kk = 0; kk < kDepth / 16; ++kk) {
-    const int s = kk & 1;
-    if (kk + 1 < kDepth / 16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) af[s ^ 1][i] = frag_direct<LA>(As, wm * 128 + 32 * i, kk + 1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[s ^ 1][j] = frag_direct<LB>(Bs, wn * 128 + 32 * j, kk + 1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
+  static_for<4>([&](auto I) {
+    af[0][I] = oa.template frag<I, 0>(0);
+    bf[0][I] = ob.template frag<I, 0>(0);
+  });
+  for (int kt = 0; kt < KT; ++kt) {
+    const int st = kt & 1;
+    const uint32_t so = st * kStageBytes;
+    static_for<4>([&](auto KKI) {
+      constexpr int kk = KKI, s = kk & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<16>([&](auto Q) {
+        constexpr int q = Q;
+        acc[q / 4][q % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][q / 4], bf[s][q % 4], acc[q / 4][q % 4], 0, 0, 0);
+        constexpr int slot = 16 * kk + q;
+        if constexpr (slot % 3 == 0 && slot / 3 < 16) issue(kt + 1, st ^ 1, slot / 3);
+        if constexpr (kk < 3 && q % 2 == 0) {
+          constexpr int r = q / 2;  // fragments of step kk + 1: a0 b0 a1 b1 ...
+          if constexpr (r % 2 == 0)
+            af[s ^ 1][r / 2] = oa.template frag<r / 2, kk + 1>(so);
+          else
+            bf[s ^ 1][r / 2] = ob.template frag<r / 2, kk + 1>(so);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+    // The next tile's loads (this wave's) are done; after the barrier every
+    // wave's are, and every wave has finished reading this stage.
+    wait_and_meet<0>();
+    static_for<4>([&](auto I) {
+      af[0][I] = oa.template frag<I, 0>(so ^ kStageBytes);
+      bf[0][I] = ob.template frag<I, 0>(so ^ kStageBytes);
+    });
   }
 }
 
@@ -409,28 +491,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   // lands in the other stage and tile kt+2's loads are issued.
   const int KT = (p.k + kDepth - 1) / kDepth;
   if constexpr (!CHECK) {
-    // Interior tiles: K tile kt + 1 streams straight into the other LDS stage
-    // while the waves multiply tile kt.
-    auto Ad = [&](int st) { return lds + st * kTileD; };
-    auto Bd = [&](int st) { return lds + (2 + st) * kTileD; };
-    Direct<LA> da;
-    Direct<LB> db;
-    da.init(p.a, p.a_o, p.a_k, m0);
-    db.init(p.b, p.b_o, p.b_k, n0);
-    da.load(0, Ad(0));
-    db.load(0, Bd(0));
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      const int st = kt & 1;
-      if (kt + 1 < KT) {
-        da.load(kt + 1, Ad(st ^ 1));
-        db.load(kt + 1, Bd(st ^ 1));
-      }
-      multiply_direct<LA, LB>(Ad(st), Bd(st), acc, wm, wn);
-      __builtin_amdgcn_s_waitcnt(0);  // this tile's reads and the next tile's loads are done
-      __syncthreads();
-    }
+    sweep_direct<LA, LB>(p, m0, n0, wm, wn, acc);
   } else {
   Sweep<LA> sa;
   Sweep<LB> sb;
