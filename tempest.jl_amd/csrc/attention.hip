@@ -31,6 +31,7 @@
 
 #include <cmath>
 
+#include "lds_dma.h"
 #include "th_core.h"
 
 namespace {
@@ -77,6 +78,12 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+// The value lane l ^ 32 holds (v_permlane32_swap: no LDS round trip).
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(threadIdx.x % 64 < 32 ? r[1] : r[0]);
+}
+
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -92,6 +99,11 @@ __device__ __forceinline__ bf16x8 rows_operand(const f32x16& acc, int part) {
   for (int e = 0; e < 4; ++e) w[e] = pack2(acc[8 * part + 2 * e], acc[8 * part + 2 * e + 1]);
   return (bf16x8)w;
 }
+
+// sched_barrier mask: vector, scalar and transcendental instructions may
+// cross the fence; LDS accesses, global loads and products may not.
+constexpr int kFence = 0x0406;
+constexpr int kFenceFwd = kFence;
 
 // ---- 64-row tiles in LDS ---------------------------------------------------------
 // A tile holds 64 rows of 128 bf16 (256 bytes, one pass over the 64 banks).
@@ -174,15 +186,46 @@ __device__ __forceinline__ void row_operand(const uint16_t* base, bf16x8 (&f)[8]
 // runs one step ahead of V through LDS.  Iteration j reads K[(j + 1) & 1] and
 // V[j & 1], and refills K[j & 1] with step j + 2 and V[(j + 1) & 1] with
 // step j + 1 (indices past the last step are clamped; their scores are never
-// used).  V is read transposed straight from its row-major tile.  The running
-// maximum is rebased lazily: the accumulators keep their shift until a
-// query's maximum exceeds it by more than kLazy (log2 units), so no weight
-// exceeds 2^kLazy and most steps skip the rescale.
+// used).  The refills are direct global->LDS loads issued at the top of the
+// iteration, into buffers the previous iteration finished with, and waited
+// for at its end.  V is read transposed straight from its row-major tile.
+// K and V fragments are read a few products ahead of their use (the two
+// products of each 16-deep slice take 8 of the 256 registers; four slices
+// are in flight).  The running maximum is rebased lazily: the accumulators
+// keep their shift until a query's maximum exceeds it by more than kLazy
+// (log2 units), so no weight exceeds 2^kLazy and most steps skip the rescale.
 
 constexpr int kFwdQ = 128;  // queries per workgroup (32 per wave)
 constexpr int kFwdK = 64;   // keys per step
 constexpr size_t kFwdLds = 4 * kTileElems * sizeof(uint16_t);  // K[2], V[2]
 constexpr float kLazy = 8.0f;
+
+// The 64-row tile of rows [row0, row0 + 64) of a (position-major) operand,
+// loaded straight into LDS in the permuted layout of tile_at: instruction i
+// of wave w fills rows 16 w + 4 i .. + 3 (1 KB), lane l the 16 bytes of row
+// 16 w + 4 i + l / 16 at position l % 16, i.e. chunk (l % 16) ^ swz(row).
+struct TileDma {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int32_t off[4];  // byte offsets of this lane's rows for row0 = 0
+  int32_t row_bytes;
+  __device__ TileDma(const uint16_t* base, int64_t rs) {
+    rsrc = th_dev::buffer_of(base);
+    row_bytes = (int32_t)(rs * 2);
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * w + 4 * i + l / 16;
+      const int c = (l % 16) ^ (4 * (r % 4) + (r / 4) % 4);
+      off[i] = (int32_t)(((int64_t)r * rs + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ void load(int row0, const uint16_t* lds) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t dst = (uint32_t)(uintptr_t)lds + 1024 * 4 * w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) th_dev::dma16(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
+  }
+};
 
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -202,10 +245,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
     const int query = q0 + lr;
 
     const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-    const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-    const int64_t step_elems = (int64_t)kFwdK * p.k_ss;
-    const TileRows rows(p.k_ss);
+    const TileDma kt(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
+    const TileDma vt(p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
 
     bf16x8 qf[8];
     row_operand(qbase + (int64_t)query * p.q_ss, qf);
@@ -218,26 +259,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
     // An even number of steps (the sequence is a multiple of 128), at least 2.
     const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
 
-    u32x4 rk[4], rv[4];
-    rows.load(kbase, rk);
-    rows.load(vbase, rv);
-    store_rows(Kl[0], rk);
-    store_rows(Vl[0], rv);
-    rows.load(kbase + step_elems, rk);
-    store_rows(Kl[1], rk);
-    __syncthreads();
-    f32x16 sa[2] = {f32x16{}, f32x16{}}, sb[2];
+    // S' (64 keys x 32 queries) of the tile in K: two 32-key blocks, the
+    // fragments of slice ks + 3 read while slice ks multiplies.
+    auto scores = [&](const uint16_t* K, f32x16 (&s)[2]) {
+      bf16x8 kf[4][2];
   #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+      for (int ks = 0; ks < 3; ++ks) kf[ks][0] = frag_rows(K, 0, ks), kf[ks][1] = frag_rows(K, 32, ks);
+      s[0] = f32x16{};
+      s[1] = f32x16{};
   #pragma unroll
-      for (int j = 0; j < 2; ++j) sa[j] = mfma(frag_rows(Kl[0], 32 * j, ks), qf[ks], sa[j]);
+      for (int ks = 0; ks < 8; ++ks) {
+        if (ks + 3 < 8) kf[(ks + 3) % 4][0] = frag_rows(K, 0, ks + 3), kf[(ks + 3) % 4][1] = frag_rows(K, 32, ks + 3);
+        s[0] = mfma(kf[ks % 4][0], qf[ks], s[0]);
+        s[1] = mfma(kf[ks % 4][1], qf[ks], s[1]);
+      }
+    };
+
+    kt.load(0, Kl[0]);
+    vt.load(0, Vl[0]);
+    kt.load(kFwdK, Kl[1]);
+    th_dev::wait_and_meet<0>();
+    f32x16 sa[2], sb[2];
+    scores(Kl[0], sa);
     __syncthreads();
 
     // Step j: weights from s (its scores), scores of step j + 1 into sn.
     auto step = [&](const int j, f32x16 (&s)[2], f32x16 (&sn)[2]) {
       const int st = j & 1;
-      rows.load(kbase + (int64_t)min(j + 2, nkb - 1) * step_elems, rk);
-      rows.load(vbase + (int64_t)min(j + 1, nkb - 1) * step_elems, rv);
+      kt.load(min(j + 2, nkb - 1) * kFwdK, Kl[st]);
+      vt.load(min(j + 1, nkb - 1) * kFwdK, Vl[st ^ 1]);
       const int key0 = j * kFwdK;
       if (p.causal && key0 + kFwdK > q0) {
   #pragma unroll
@@ -248,19 +298,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
             if (key > query) s[jj][i] = -INFINITY;
           }
       }
-      sn[0] = f32x16{};
-      sn[1] = f32x16{};
-  #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-  #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) sn[jj] = mfma(frag_rows(Kl[st ^ 1], 32 * jj, ks), qf[ks], sn[jj]);
-      // This lane's query maximum in scaled units (the scale is positive).
+      // The scores of step j + 1 on the matrix cores while the vector ALUs
+      // turn step j's into weights (independent work, interleaved below).
+      __builtin_amdgcn_sched_barrier(0);
+      scores(Kl[st ^ 1], sn);
+      // This lane's query maximum in scaled units (the scale is positive);
+      // the other half of the wave holds the same query's other keys.
       float mb = -INFINITY;
   #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
   #pragma unroll
         for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[jj][i]);
-      mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * c;
+      mb = fmaxf(mb, other_half(mb)) * c;
       const bool grow = mb > m + kLazy;
       const float mn = grow ? mb : m;
       const float shift = isfinite(mn) ? mn : 0.0f;
@@ -280,6 +329,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
           }
           pf[2 * jj + part] = (bf16x8)w;
         }
+      // The weights are complete here, before the rescale's branch (which
+      // the compiler would otherwise hoist above them, splitting them from
+      // the products they are interleaved with).
+      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(ls));
+      // Order: the first three slices' K fragments, then each product
+      // followed by its share of the weights' vector work (about six vector
+      // and two transcendental instructions per product) and, for the first
+      // ten products, the fragment read three slices ahead.
+      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+  #pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (q < 10) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       if (__ballot(grow)) {
         const float alpha = __builtin_amdgcn_exp2f(m - shift);
         l *= alpha;
@@ -288,14 +354,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
       }
       l += ls;
       m = mn;
-      // O' (128 d x 32 queries) += V' P', the weights rounded to bf16.
+      // O' (128 d x 32 queries) += V' P', the weights rounded to bf16; the
+      // V fragments of slice ks + 1 read while slice ks multiplies.
+      const uint16_t* V = Vl[st];
+      bf16x8 vf[2][4];
   #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int db = 0; db < 4; ++db) vf[0][db] = frag_tr(V, 32 * db, 0);
   #pragma unroll
-        for (int db = 0; db < 4; ++db) o[db] = mfma(frag_tr(Vl[st], 32 * db, ks), pf[ks], o[db]);
-      store_rows(Kl[st], rk);
-      store_rows(Vl[st ^ 1], rv);
-      __syncthreads();
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4)
+  #pragma unroll
+          for (int db = 0; db < 4; ++db) vf[(ks + 1) % 2][db] = frag_tr(V, 32 * db, ks + 1);
+        __builtin_amdgcn_sched_barrier(kFenceFwd);
+  #pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] = mfma(vf[ks % 2][db], pf[ks], o[db]);
+        __builtin_amdgcn_sched_barrier(kFenceFwd);
+      }
+      th_dev::wait_and_meet<0>();
     };
     for (int j = 0; j < nkb; j += 2) {
       step(j, sa, sb);
@@ -303,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
     }
 
     // Both halves of the wave summed their keys' weights against the same shift.
-    l += __shfl_xor(l, 32, 64);
+    l = l + other_half(l);
     const float inv = 1.0f / l;
     uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
   #pragma unroll
@@ -360,7 +435,6 @@ __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
 // offset by (-lse / scale for S, -delta for dP), so the weights need no
 // separate subtraction: P = exp2(c S~), dS = P dP~.
 
-constexpr int kFence = 0x0406;  // VALU, SALU and transcendental instructions may cross
 
 // 16 products over d = 128: s += x[rows 32 j ..] xf, t += y[rows 32 j ..] yf,
 // the A fragments read three slices ahead.
@@ -866,6 +940,10 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
   if (int r = th::require_ready()) return r;
   *out = nullptr;
   if (int r = check_desc(d, false)) return r;
+  // The forward's direct loads address a (batch, head) sequence of K and V
+  // from one base with 32-bit byte offsets.
+  TH_REQUIRE((double)d->seq * d->k_strides[1] * 2 < 2147483648.0,
+             "attention: a sequence of K or V must span under 2 GiB (seq x position stride x 2 bytes)");
   TH_HIP(hipFuncSetAttribute((const void*)attn_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFwdLds));
   AttnArgs a = args_of(d);
   th::Builder b("attention_fwd", 5);

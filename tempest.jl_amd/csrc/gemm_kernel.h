@@ -33,6 +33,8 @@
 #include <cstdint>
 #include <utility>
 
+#include "lds_dma.h"
+
 namespace thg {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -279,11 +281,8 @@ __device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t
 // wave waits for its own loads, the waves meet, and the next tile's first
 // fragments are read.
 //
-// The direct loads are issued from inline assembly: the compiler, seeing an
-// LDS write by DMA, would otherwise make every later transposed LDS read
-// wait for all outstanding global loads (a vmcnt(0) before each
-// ds_read_b64_tr_b16), serializing the sweep.  Their completion is waited
-// for explicitly at the barrier, where the stage they fill is next read.
+// The direct loads are issued from inline assembly (lds_dma.h says why) and
+// waited for explicitly at the barrier, where the stage they fill is next read.
 
 constexpr int kTileD = kTile * kDepth;                         // bf16 per operand stage
 constexpr size_t kLdsDirect = 4 * kTileD * sizeof(uint16_t);   // A and B, two stages: 131072 bytes
@@ -305,17 +304,8 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
-// One 16-byte lane load from global memory straight into LDS at M0 + 16 lane.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int32_t voff, int32_t soff, uint32_t m0) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0));
-}
-
-// Wait until this wave has at most N vector memory operations in flight and
-// no LDS reads, then meet the other waves.
-template <int N>
-__device__ __forceinline__ void wait_and_meet() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
-}
+using th_dev::dma16;
+using th_dev::wait_and_meet;
 
 // One operand of the direct path: its buffer resource, the byte offsets of
 // the wave's eight loads for K tile 0 (the K advance is the scalar offset),
