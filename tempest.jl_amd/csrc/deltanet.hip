@@ -144,6 +144,121 @@ __device__ __forceinline__ void zero(float (&acc)[TM][TN]) {
     for (int c = 0; c < TN; ++c) acc[r][c] = 0.0f;
 }
 
+
+// ---- fp32 products on the matrix cores ----------------------------------------------
+// v_mfma_f32_16x16x4_f32 multiplies fp32 exactly and accumulates in fp32, as
+// the per-thread FMA tiles do (only the order of the additions differs).
+// Operands sit in LDS as fp32 rows of kLd floats: a row's 16-byte quads land
+// on distinct bank quads for 16 consecutive rows (kLd / 4 odd), and a column
+// read by 16 consecutive rows x 4 row groups hits 64 distinct banks
+// (kLd = 4 mod 16).
+//
+// Lane l = 16 g + r of a 16 x 16 block over 16 consecutive k takes the four
+// k = 16 kb + 4 g + (0..3): one ds_read_b128 per operand when k runs along
+// its rows, four products, each pairing A(i0 + r, k) with B(k, j0 + r); the
+// products' k slot g then holds the same k in both operands.  The block
+// C(i0 + 4 g + v, j0 + r) sits in register v of lane l.
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+constexpr int kLd = 132;
+
+__device__ __forceinline__ f32x4v quad(const float* row) { return *reinterpret_cast<const f32x4v*>(row); }
+
+// The four k of lane g's quad along a column: X(k, c) at x[k * ld + c].
+__device__ __forceinline__ f32x4v column_quad(const float* x, int ld, int k0, int c) {
+  return f32x4v{x[k0 * ld + c], x[(k0 + 1) * ld + c], x[(k0 + 2) * ld + c], x[(k0 + 3) * ld + c]};
+}
+
+__device__ __forceinline__ f32x4v mma4(f32x4v a, f32x4v b, f32x4v c) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+// acc[bi][bj] += X(i0 + 16 bi .., k) Y(j0 + 16 bj .., k) over k in [0, K):
+// both operands with k along their rows (row-major in LDS, stride kLd).
+template <int BI, int BJ>
+__device__ __forceinline__ void mm_nt(f32x4v (&acc)[BI][BJ], const float* X, int i0, const float* Y, int j0, int K) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+  for (int kb = 0; kb < K; kb += 16) {
+    f32x4v a[BI], b[BJ];
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi) a[bi] = quad(X + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) b[bj] = quad(Y + (j0 + 16 * bj + r) * kLd + kb + 4 * g);
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+  }
+}
+
+// acc[bi][bj] += X(i0 + 16 bi .., k) Y(k, j0 + 16 bj ..) over k in [0, K), each
+// operand read along its rows (X(i, k) = X[i * ldx + k], Y(k, j) = Y[j * ldy + k])
+// or, when XT / YT, along its columns (X(i, k) = X[k * ldx + i], Y(k, j) =
+// Y[k * ldy + j]).  Strides satisfy ld / 4 odd and ld = 4 mod 16.
+template <bool XT, bool YT, int BI, int BJ>
+__device__ __forceinline__ void mm_gen(f32x4v (&acc)[BI][BJ], const float* X, int ldx, int i0, const float* Y, int ldy,
+                                       int j0, int K) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+  for (int kb = 0; kb < K; kb += 16) {
+    const int k0 = kb + 4 * g;
+    f32x4v a[BI], b[BJ];
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+      a[bi] = XT ? column_quad(X, ldx, k0, i0 + 16 * bi + r) : quad(X + (i0 + 16 * bi + r) * ldx + k0);
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj)
+      b[bj] = YT ? column_quad(Y, ldy, k0, j0 + 16 * bj + r) : quad(Y + (j0 + 16 * bj + r) * ldy + k0);
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+  }
+}
+
+template <int BI, int BJ>
+__device__ __forceinline__ void clear(f32x4v (&acc)[BI][BJ]) {
+#pragma unroll
+  for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// rows x 128 fp32 from global (row stride 128) into LDS rows of kLd, 16-byte pieces.
+__device__ __forceinline__ void stage_f32(float* dst, const float* src, int rows) {
+  for (int e = threadIdx.x; e < rows * 32; e += 256) {
+    const int r = e / 32, c = 4 * (e % 32);
+    *reinterpret_cast<float4*>(dst + r * kLd + c) = *reinterpret_cast<const float4*>(src + r * kD + c);
+  }
+}
+
+// 64 x 128 bf16 of a (d, heads, positions, batch) array into LDS as fp32 rows of kLd.
+__device__ __forceinline__ void stage_bf16(float* dst, const uint16_t* src, int64_t s_t) {
+  for (int e = threadIdx.x; e < kC * 16; e += 256) {
+    const int r = e / 16, c8 = 8 * (e % 16);
+    const uint4 w = *reinterpret_cast<const uint4*>(src + r * s_t + c8);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[2 * j] = bf((uint16_t)u[j]), f[2 * j + 1] = bf((uint16_t)(u[j] >> 16));
+    *reinterpret_cast<float4*>(dst + r * kLd + c8) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<float4*>(dst + r * kLd + c8 + 4) = make_float4(f[4], f[5], f[6], f[7]);
+  }
+}
+
+// Block (bi, bj) of acc to out (row stride ld), rows i0 + 16 bi + 4 g + v, columns j0 + 16 bj + r, times s.
+template <int BI, int BJ>
+__device__ __forceinline__ void store_blocks(float* out, int ld, const f32x4v (&acc)[BI][BJ], int i0, int j0, float s) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+#pragma unroll
+  for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) out[(int64_t)(i0 + 16 * bi + 4 * g + v) * ld + j0 + 16 * bj + r] = s * acc[bi][bj][v];
+}
+
 // ---- forward: the chunk's WY form -------------------------------------------------
 
 constexpr size_t kPrepLds = (2 * kC * kPadD + kC * kPadC + 2 * kC) * sizeof(float);
@@ -358,154 +473,246 @@ __global__ __launch_bounds__(256) void dn_output(DnArgs p) {
 }
 
 // ---- backward: the state gradient swept back over chunks -------------------------------
+// One workgroup per (sequence, 32 columns of dS), chunks in reverse:
+//   dSn_n = dS;  dU = P' dO + diag(e^(last - ca)) K dS;  dS <- Qg' dO + g dS - W' dU,
+// the products on the matrix cores in fp32.  While a chunk's products run,
+// the previous chunk's inputs (P, the dO columns, Q, K, W, ca) are loaded
+// into registers; they go to LDS once the chunk is done with its own.
 
-constexpr size_t kSgLds = (kD * kPadS + kC * kPadC + kC * kPadS + 3 * kC * kPadD + kC * kPadS + kC) * sizeof(float);
+constexpr int kLdC = 68;   // LDS row of 64 fp32
+constexpr int kLdS = 36;   // LDS row of 32 fp32
+constexpr size_t kSgLds =
+    (kC * kLdC + kC * kLdS + 3 * kC * kLd + kD * kLdS + kC * kLdS + kC) * sizeof(float);
 
-__global__ __launch_bounds__(256) void dn_state_grad(DnArgs p) {
-  extern __shared__ float lds[];
-  float* dS = lds;                  // [128][kPadS]
-  float* P = dS + kD * kPadS;       // [64][kPadC]
-  float* dO = P + kC * kPadC;       // [64][kPadS]
-  float* Q = dO + kC * kPadS;       // [64][kPadD]
-  float* K = Q + kC * kPadD;        // [64][kPadD]
-  float* W = K + kC * kPadD;        // [64][kPadD]
-  float* dU = W + kC * kPadD;       // [64][kPadS]
-  float* ca = dU + kC * kPadS;      // [64]
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+// One chunk's inputs as this thread loads them (plain vector types, so the
+// whole set stays in registers).
+struct SgInputs {
+  f32x4v p[4];     // P: 4 x 16 bytes
+  u32x2v d[2];     // dO columns col0 .. col0 + 31: 2 x 8 bytes (bf16)
+  u32x4v q[4], k[4];  // Q, K: 4 x 16 bytes each (bf16)
+  f32x4v w[8];
+  float ca;
+};
+
+__device__ __forceinline__ void sg_load(SgInputs& in, const DnArgs& p, const Chunk& ck, int col0) {
   const int t = threadIdx.x;
+  const float* Pc = p.P + ck.c * kC * kC;
+  const float* Wc = p.W + ck.c * kC * kD;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) in.p[e] = reinterpret_cast<const f32x4v*>(Pc)[t + 256 * e];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
+    in.d[e] = *reinterpret_cast<const u32x2v*>(p.dout + ck.row0 + (int64_t)r * p.s_t + col0 + c);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    in.q[e] = *reinterpret_cast<const u32x4v*>(p.q + ck.row0 + (int64_t)r * p.s_t + c);
+    in.k[e] = *reinterpret_cast<const u32x4v*>(p.k + ck.row0 + (int64_t)r * p.s_t + c);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + 256 * e];
+  in.ca = t < kC ? p.ca[ck.c * kC + t] : 0.0f;
+}
+
+// The inputs to LDS; Q as Qg = diag(e^ca) Q (ca of the same chunk, already in LDS).
+__device__ __forceinline__ void sg_store(const SgInputs& in, float* P, float* dO, float* Qg, float* K, float* W,
+                                         const float* ca) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + 256 * e, r = x / 16, c = 4 * (x % 16);
+    *reinterpret_cast<f32x4v*>(P + r * kLdC + c) = in.p[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
+    *reinterpret_cast<f32x4v*>(dO + r * kLdS + c) =
+        f32x4v{bf((uint16_t)in.d[e][0]), bf((uint16_t)(in.d[e][0] >> 16)), bf((uint16_t)in.d[e][1]),
+               bf((uint16_t)(in.d[e][1] >> 16))};
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    const float eq = expf(ca[r]);
+    const u32x4v uq = in.q[e], uk = in.k[e];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Qg[r * kLd + c + 2 * j] = eq * bf((uint16_t)uq[j]);
+      Qg[r * kLd + c + 2 * j + 1] = eq * bf((uint16_t)(uq[j] >> 16));
+      K[r * kLd + c + 2 * j] = bf((uint16_t)uk[j]);
+      K[r * kLd + c + 2 * j + 1] = bf((uint16_t)(uk[j] >> 16));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = t + 256 * e, r = x / 32, c = 4 * (x % 32);
+    *reinterpret_cast<f32x4v*>(W + r * kLd + c) = in.w[e];
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
+  extern __shared__ float lds[];
+  float* P = lds;                  // [64][kLdC]
+  float* dO = P + kC * kLdC;       // [64][kLdS]: columns col0 .. col0 + 31 of dO
+  float* Qg = dO + kC * kLdS;      // [64][kLd]: diag(e^ca) Q
+  float* K = Qg + kC * kLd;        // [64][kLd]
+  float* W = K + kC * kLd;         // [64][kLd]
+  float* dS = W + kC * kLd;        // [128][kLdS]: the state gradient's 32 columns
+  float* dU = dS + kD * kLdS;      // [64][kLdS]
+  float* ca = dU + kC * kLdS;      // [64]
+  const int t = threadIdx.x, w = t / 64;
+  const int r = t % 16, g = (t % 64) / 16;
   const int64_t seq = blockIdx.x / (kD / kCols);
   const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
-  for (int e = t; e < kD * kPadS; e += 256) dS[e] = 0.0f;
+  for (int e = t; e < kD * kLdS; e += 256) dS[e] = 0.0f;
+  SgInputs in;
+  {
+    const Chunk ck = chunk_of(p, seq * p.chunks + p.chunks - 1);
+    sg_load(in, p, ck, col0);
+    if (t < kC) ca[t] = in.ca;
+    __syncthreads();
+    sg_store(in, P, dO, Qg, K, W, ca);
+  }
   for (int n = p.chunks - 1; n >= 0; --n) {
     const Chunk ck = chunk_of(p, seq * p.chunks + n);
     __syncthreads();
-    float* dSc = p.dSn + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols; e += 256) dSc[(e / kCols) * kD + col0 + e % kCols] = dS[(e / kCols) * kPadS + e % kCols];
-    const float* Pc = p.P + ck.c * kC * kC;
-    for (int e = t; e < kC * kC; e += 256) P[(e / kC) * kPadC + e % kC] = Pc[e];
-    for (int e = t; e < kC * kCols; e += 256) {
-      const int r = e / kCols, c = e % kCols;
-      dO[r * kPadS + c] = bf(p.dout[ck.row0 + (int64_t)r * p.s_t + col0 + c]);
-    }
-    load_chunk(Q, p.q + ck.row0, p.s_t);
-    load_chunk(K, p.k + ck.row0, p.s_t);
-    const float* Wc = p.W + ck.c * kC * kD;
-    for (int e = t; e < kC * kD; e += 256) W[(e / kD) * kPadD + e % kD] = Wc[e];
-    if (t < 64) ca[t] = p.ca[ck.c * kC + t];
-    __syncthreads();
+    if (n > 0) sg_load(in, p, chunk_of(p, seq * p.chunks + n - 1), col0);
     const float last = ca[kC - 1];
-    // dU = P' dO + Kd dS: thread (2 rows x 4 columns) of 64 x 32.
+    // The gradient at the chunk's end state.
+    float* dSc = p.dSn + ck.c * kD * kD;
+    for (int e = t; e < kD * kCols / 4; e += 256) {
+      const int row = e / 8, c = 4 * (e % 8);
+      *reinterpret_cast<float4*>(dSc + row * kD + col0 + c) = *reinterpret_cast<const float4*>(dS + row * kLdS + c);
+    }
+    // dU (64 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
-      const int i0 = 2 * (t / 8), j0 = 4 * (t % 8);
-      float acc[2][4];
-      zero(acc);
-      mm(acc, i0, j0, kC, [&](int l, int i) { return P[i * kPadC + l]; }, [&](int i, int j) { return dO[i * kPadS + j]; });
-      float kd[2][4];
-      zero(kd);
-      mm(kd, i0, j0, kD, [&](int l, int k) { return K[l * kPadD + k]; }, [&](int k, int j) { return dS[k * kPadS + j]; });
+      f32x4v pd[1][2], kd[1][2];
+      clear(pd);
+      clear(kd);
+      mm_gen<true, true>(pd, P, kLdC, 16 * w, dO, kLdS, 0, kC);
+      mm_gen<false, true>(kd, K, kLd, 16 * w, dS, kLdS, 0, kD);
       float* dUo = p.dU + ck.c * kC * kD;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float e = expf(last - ca[i0 + r]);
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * w + 4 * g + v;
+        const float e = expf(last - ca[i]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float u = acc[r][c] + e * kd[r][c];
-          dU[(i0 + r) * kPadS + j0 + c] = u;
-          dUo[(i0 + r) * kD + col0 + j0 + c] = u;
+        for (int bj = 0; bj < 2; ++bj) {
+          const float u = pd[0][bj][v] + e * kd[0][bj][v];
+          dU[i * kLdS + 16 * bj + r] = u;
+          dUo[i * kD + col0 + 16 * bj + r] = u;
         }
       }
     }
     __syncthreads();
-    // dS <- Qg' dO + g dS - W' dU: thread (4 rows x 4 columns) of 128 x 32.
+    // dS <- Qg' dO + g dS - W' dU (128 x 32): wave w takes rows 32 w .. 32 w + 31.
     {
-      const int i0 = 4 * (t / 8), j0 = 4 * (t % 8);
-      float acc[4][4];
-      zero(acc);
-      mm(acc, i0, j0, kC, [&](int k, int i) { return expf(ca[i]) * Q[i * kPadD + k]; },
-         [&](int i, int j) { return dO[i * kPadS + j]; });
-      float wu[4][4];
-      zero(wu);
-      mm(wu, i0, j0, kC, [&](int k, int i) { return W[i * kPadD + k]; }, [&](int i, int j) { return dU[i * kPadS + j]; });
-      const float g = expf(last);
+      f32x4v qd[2][2], wu[2][2];
+      clear(qd);
+      clear(wu);
+      mm_gen<true, true>(qd, Qg, kLd, 32 * w, dO, kLdS, 0, kC);
+      mm_gen<true, true>(wu, W, kLd, 32 * w, dU, kLdS, 0, kC);
+      const float gl = expf(last);
+      float nw[2][2][4];
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int i = 32 * w + 16 * bi + 4 * g + v, j = 16 * bj + r;
+            nw[bi][bj][v] = qd[bi][bj][v] + gl * dS[i * kLdS + j] - wu[bi][bj][v];
+          }
+      __syncthreads();  // every wave has read dS, dU and this chunk's inputs
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) dS[(32 * w + 16 * bi + 4 * g + v) * kLdS + 16 * bj + r] = nw[bi][bj][v];
+    }
+    if (n > 0) {
+      if (t < kC) ca[t] = in.ca;
       __syncthreads();
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          dS[(i0 + r) * kPadS + j0 + c] = acc[r][c] + g * dS[(i0 + r) * kPadS + j0 + c] - wu[r][c];
+      sg_store(in, P, dO, Qg, K, W, ca);
     }
   }
 }
 
 // ---- backward: the chunk's products (part a) ---------------------------------------
-// dQg = dO S', dW = -dU S', dKd = U dSn', dP = lower(dO U'), dg = <S, dSn>.
+// dQg = dO S', dW = -dU S', dKd = U dSn', dP = lower(dO U'), dg = <S, dSn>,
+// every product on the matrix cores in fp32.  Two phases through LDS: dO, dU
+// and S, then U and dSn (dO stays).  Wave w computes columns 32 w .. 32 w + 31
+// of the 64 x 128 results and row block w of dP.
 
-constexpr size_t kGaLds = (3 * kC * kPadD + 4) * sizeof(float);
+constexpr size_t kGaLds = (2 * kC + kD) * kLd * sizeof(float) + 4 * sizeof(float);
 
-__global__ __launch_bounds__(256) void dn_grad_a(DnArgs p) {
+__global__ __launch_bounds__(256, 1) void dn_grad_a(DnArgs p) {
   extern __shared__ float lds[];
-  float* dO = lds;               // [64][kPadD]
-  float* U = dO + kC * kPadD;    // [64][kPadD]
-  float* dU = U + kC * kPadD;    // [64][kPadD]
-  float* red = dU + kC * kPadD;  // [4]
+  float* dO = lds;              // [64][kLd]
+  float* X = dO + kC * kLd;     // [64][kLd]: dU, then U
+  float* Y = X + kC * kLd;      // [128][kLd]: S, then dSn
+  float* red = Y + kD * kLd;    // [4]
   const Chunk ck = chunk_of(p, blockIdx.x);
-  const int t = threadIdx.x;
-  load_chunk(dO, p.dout + ck.row0, p.s_t);
-  const float* Uc = p.U + ck.c * kC * kD;
-  const float* dUc = p.dU + ck.c * kC * kD;
-  for (int e = t; e < kC * kD; e += 256) U[(e / kD) * kPadD + e % kD] = Uc[e], dU[(e / kD) * kPadD + e % kD] = dUc[e];
-  __syncthreads();
+  const int t = threadIdx.x, w = t / 64;
   const float* Sc = p.S + ck.c * kD * kD;
   const float* dSc = p.dSn + ck.c * kD * kD;
+  stage_bf16(dO, p.dout + ck.row0, p.s_t);
+  stage_f32(X, p.dU + ck.c * kC * kD, kC);
+  stage_f32(Y, Sc, kD);
+  __syncthreads();
   {
-    const int i0 = 4 * (t / 16), j0 = 8 * (t % 16);
-    float q[4][8], w[4][8], kd[4][8];
-    zero(q);
-    zero(w);
-    zero(kd);
-    // (64 x 128) x (128 x 128)': row i of the left against row j of S or dSn.
-    for (int v = 0; v < kD; ++v) {
-      float a0[4], a1[4], a2[4], s0[8], s1[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) a0[r] = dO[(i0 + r) * kPadD + v], a1[r] = dU[(i0 + r) * kPadD + v], a2[r] = U[(i0 + r) * kPadD + v];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) s0[c] = Sc[(j0 + c) * kD + v], s1[c] = dSc[(j0 + c) * kD + v];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          q[r][c] = fmaf(a0[r], s0[c], q[r][c]);
-          w[r][c] = fmaf(a1[r], s0[c], w[r][c]);
-          kd[r][c] = fmaf(a2[r], s1[c], kd[r][c]);
-        }
-    }
-    float* o1 = p.dQg + ck.c * kC * kD;
-    float* o2 = p.dW + ck.c * kC * kD;
-    float* o3 = p.dKd + ck.c * kC * kD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int at = (i0 + r) * kD + j0 + c;
-        o1[at] = q[r][c], o2[at] = -w[r][c], o3[at] = kd[r][c];
-      }
+    f32x4v q[4][2], wq[4][2];
+    clear(q);
+    clear(wq);
+    mm_nt(q, dO, 0, Y, 32 * w, kD);
+    mm_nt(wq, X, 0, Y, 32 * w, kD);
+    store_blocks(p.dQg + ck.c * kC * kD, kD, q, 0, 32 * w, 1.0f);
+    store_blocks(p.dW + ck.c * kC * kD, kD, wq, 0, 32 * w, -1.0f);
+  }
+  __syncthreads();
+  stage_f32(X, p.U + ck.c * kC * kD, kC);
+  stage_f32(Y, dSc, kD);
+  __syncthreads();
+  {
+    f32x4v kd[4][2];
+    clear(kd);
+    mm_nt(kd, X, 0, Y, 32 * w, kD);
+    store_blocks(p.dKd + ck.c * kC * kD, kD, kd, 0, 32 * w, 1.0f);
   }
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4];
-    zero(acc);
-    if (j0 < i0 + 4)
-      mm(acc, i0, j0, kD, [&](int i, int k) { return dO[i * kPadD + k]; }, [&](int k, int j) { return U[j * kPadD + k]; });
+    // Row block w of dP: blocks (w, jb) for jb <= w, the diagonal masked, zeros above.
+    const int r = t % 16, g = (t % 64) / 16;
     float* dPc = p.dP + ck.c * kC * kC;
+    for (int jb = 0; jb < 4; ++jb) {
+      f32x4v acc[1][1];
+      clear(acc);
+      if (jb <= w) mm_nt(acc, dO, 16 * w, X, 16 * jb, kD);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) dPc[(i0 + r) * kC + j0 + c] = (i0 + r >= j0 + c) ? acc[r][c] : 0.0f;
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * w + 4 * g + v, j = 16 * jb + r;
+        dPc[i * kC + j] = i >= j ? acc[0][0][v] : 0.0f;
+      }
+    }
   }
-  // dg = <S, dSn>, a fixed tree.
-  float s = 0.0f;
-  for (int e = t; e < kD * kD; e += 256) s = fmaf(Sc[e], dSc[e], s);
-  s = thd::wave_sum(s);
-  if (t % 64 == 0) red[t / 64] = s;
+  // dg = <S, dSn>: S from global, dSn from LDS, a fixed tree.
+  float sum = 0.0f;
+  for (int e = t; e < kD * kD / 4; e += 256) {
+    const int r = e / 32, c = 4 * (e % 32);
+    const float4 sv = *reinterpret_cast<const float4*>(Sc + r * kD + c);
+    const f32x4v dv = quad(Y + r * kLd + c);
+    sum = fmaf(sv.x, dv[0], sum);
+    sum = fmaf(sv.y, dv[1], sum);
+    sum = fmaf(sv.z, dv[2], sum);
+    sum = fmaf(sv.w, dv[3], sum);
+  }
+  sum = thd::wave_sum(sum);
+  if (t % 64 == 0) red[t / 64] = sum;
   __syncthreads();
   if (t == 0) p.dg[ck.c] = red[0] + red[1] + red[2] + red[3];
 }
