@@ -160,7 +160,11 @@ __device__ __forceinline__ void zero(float (&acc)[TM][TN]) {
 // C(i0 + 4 g + v, j0 + r) sits in register v of lane l.
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
-constexpr int kLd = 132;
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+constexpr int kLd = 132;   // LDS row of 128 fp32
+constexpr int kLdC = 68;   // LDS row of 64 fp32
+constexpr int kLdS = 36;   // LDS row of 32 fp32
 
 __device__ __forceinline__ f32x4v quad(const float* row) { return *reinterpret_cast<const f32x4v*>(row); }
 
@@ -345,70 +349,138 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(DnArgs p) {
 }
 
 // ---- forward: the recurrence across chunks, 32 columns of S per workgroup ---------
+// Per chunk: the starting state is stored, U = U~ - W S, S <- g S + Kd' U,
+// the products on the matrix cores in fp32.  While a chunk's products run,
+// the next chunk's W, U~ columns, K and ca are loaded into registers.
 
-constexpr int kPadS = kCols + 1;
-constexpr size_t kScanLds = (kD * kPadS + kC * kPadD + kC * kPadD + kC * kPadS + kC * kPadS + kC) * sizeof(float);
+struct ScanInputs {  // one chunk's inputs as this thread loads them
+  f32x4v w[8];       // W: 8 x 16 bytes
+  f32x4v u[2];       // U~ columns col0 .. col0 + 31: 2 x 16 bytes
+  u32x4v k[4];       // K: 4 x 16 bytes (bf16)
+  float ca;
+};
 
-__global__ __launch_bounds__(256) void dn_state_scan(DnArgs p) {
-  extern __shared__ float lds[];
-  float* S = lds;                   // [128][kPadS]
-  float* W = S + kD * kPadS;        // [64][kPadD]
-  float* K = W + kC * kPadD;        // [64][kPadD]
-  float* Ut = K + kC * kPadD;       // [64][kPadS]
-  float* U = Ut + kC * kPadS;       // [64][kPadS]
-  float* ca = U + kC * kPadS;       // [64]
+__device__ __forceinline__ void scan_load(ScanInputs& in, const DnArgs& p, const Chunk& ck, int col0) {
   const int t = threadIdx.x;
+  const float* Wc = p.W + ck.c * kC * kD;
+  const float* Uc = p.Ut + ck.c * kC * kD;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + 256 * e];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
+    in.u[e] = *reinterpret_cast<const f32x4v*>(Uc + r * kD + col0 + c);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    in.k[e] = *reinterpret_cast<const u32x4v*>(p.k + ck.row0 + (int64_t)r * p.s_t + c);
+  }
+  in.ca = t < kC ? p.ca[ck.c * kC + t] : 0.0f;
+}
+
+// The inputs to LDS; K as Kd = diag(e^(ca_63 - ca)) K (ca of the same chunk, already in LDS).
+__device__ __forceinline__ void scan_store(const ScanInputs& in, float* W, float* Ut, float* Kd, const float* ca) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = t + 256 * e, r = x / 32, c = 4 * (x % 32);
+    *reinterpret_cast<f32x4v*>(W + r * kLd + c) = in.w[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
+    *reinterpret_cast<f32x4v*>(Ut + r * kLdS + c) = in.u[e];
+  }
+  const float last = ca[kC - 1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    const float ed = expf(last - ca[r]);
+    const u32x4v uk = in.k[e];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      Kd[r * kLd + c + 2 * j] = ed * bf((uint16_t)uk[j]);
+      Kd[r * kLd + c + 2 * j + 1] = ed * bf((uint16_t)(uk[j] >> 16));
+    }
+  }
+}
+
+constexpr size_t kScanLds = (2 * kC * kLd + kC * kLdS + kD * kLdS + kC * kLdS + kC) * sizeof(float);
+
+__global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
+  extern __shared__ float lds[];
+  float* W = lds;                 // [64][kLd]
+  float* Kd = W + kC * kLd;       // [64][kLd]: diag(e^(ca_63 - ca)) K
+  float* Ut = Kd + kC * kLd;      // [64][kLdS]: U~ columns col0 .. col0 + 31
+  float* S = Ut + kC * kLdS;      // [128][kLdS]: the state's 32 columns
+  float* U = S + kD * kLdS;       // [64][kLdS]
+  float* ca = U + kC * kLdS;      // [64]
+  const int t = threadIdx.x, w = t / 64;
+  const int r = t % 16, g = (t % 64) / 16;
   const int64_t seq = blockIdx.x / (kD / kCols);
   const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
-  for (int e = t; e < kD * kPadS; e += 256) S[e] = 0.0f;
+  for (int e = t; e < kD * kLdS; e += 256) S[e] = 0.0f;
+  ScanInputs in;
+  scan_load(in, p, chunk_of(p, seq * p.chunks), col0);
+  if (t < kC) ca[t] = in.ca;
+  __syncthreads();
+  scan_store(in, W, Ut, Kd, ca);
   for (int n = 0; n < p.chunks; ++n) {
     const Chunk ck = chunk_of(p, seq * p.chunks + n);
     __syncthreads();
+    if (n + 1 < p.chunks) scan_load(in, p, chunk_of(p, seq * p.chunks + n + 1), col0);
+    const float gl = expf(ca[kC - 1]);
     // The chunk's starting state, stored for the output and the backward.
     float* Sc = p.S + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols; e += 256) Sc[(e / kCols) * kD + col0 + e % kCols] = S[(e / kCols) * kPadS + e % kCols];
-    const float* Wc = p.W + ck.c * kC * kD;
-    for (int e = t; e < kC * kD / 4; e += 256) {
-      const float4 w = reinterpret_cast<const float4*>(Wc)[e];
-      const int r = (4 * e) / kD, c = (4 * e) % kD;
-      W[r * kPadD + c] = w.x, W[r * kPadD + c + 1] = w.y, W[r * kPadD + c + 2] = w.z, W[r * kPadD + c + 3] = w.w;
+    for (int e = t; e < kD * kCols / 4; e += 256) {
+      const int row = e / 8, c = 4 * (e % 8);
+      *reinterpret_cast<f32x4v*>(Sc + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(S + row * kLdS + c);
     }
-    const float* Uc = p.Ut + ck.c * kC * kD;
-    for (int e = t; e < kC * kCols; e += 256) Ut[(e / kCols) * kPadS + e % kCols] = Uc[(e / kCols) * kD + col0 + e % kCols];
-    load_chunk(K, p.k + ck.row0, p.s_t);
-    if (t < 64) ca[t] = p.ca[ck.c * kC + t];
-    __syncthreads();
-    // U = U~ - W S: thread (2 rows x 4 columns) of 64 x 32.
+    // U = U~ - W S (64 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
-      const int i0 = 2 * (t / 8), j0 = 4 * (t % 8);
-      float acc[2][4];
-      zero(acc);
-      mm(acc, i0, j0, kD, [&](int i, int k) { return W[i * kPadD + k]; }, [&](int k, int j) { return S[k * kPadS + j]; });
+      f32x4v ws[1][2];
+      clear(ws);
+      mm_gen<false, true>(ws, W, kLd, 16 * w, S, kLdS, 0, kD);
       float* Uo = p.U + ck.c * kC * kD;
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float u = Ut[(i0 + r) * kPadS + j0 + c] - acc[r][c];
-          U[(i0 + r) * kPadS + j0 + c] = u;
-          Uo[(i0 + r) * kD + col0 + j0 + c] = u;
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
+          const float u = Ut[i * kLdS + j] - ws[0][bj][v];
+          U[i * kLdS + j] = u;
+          Uo[i * kD + col0 + j] = u;
         }
     }
     __syncthreads();
-    // S <- g S + Kd' U, Kd_l = e^(ca_63 - ca_l) k_l: thread (4 rows x 4 columns) of 128 x 32.
+    // S <- g S + Kd' U (128 x 32): wave w takes rows 32 w .. 32 w + 31.
     {
-      const int i0 = 4 * (t / 8), j0 = 4 * (t % 8);
-      const float last = ca[kC - 1];
-      float acc[4][4];
-      zero(acc);
-      mm(acc, i0, j0, kC, [&](int i, int l) { return expf(last - ca[l]) * K[l * kPadD + i]; },
-         [&](int l, int j) { return U[l * kPadS + j]; });
-      const float g = expf(last);
+      f32x4v ku[2][2];
+      clear(ku);
+      mm_gen<true, true>(ku, Kd, kLd, 32 * w, U, kLdS, 0, kC);
+      float nw[2][2][4];
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int i = 32 * w + 16 * bi + 4 * g + v, j = 16 * bj + r;
+            nw[bi][bj][v] = gl * S[i * kLdS + j] + ku[bi][bj][v];
+          }
+      __syncthreads();  // every wave has read S, U and this chunk's inputs
+#pragma unroll
+      for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) S[(32 * w + 16 * bi + 4 * g + v) * kLdS + 16 * bj + r] = nw[bi][bj][v];
+    }
+    if (n + 1 < p.chunks) {
+      if (t < kC) ca[t] = in.ca;
       __syncthreads();
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) S[(i0 + r) * kPadS + j0 + c] = g * S[(i0 + r) * kPadS + j0 + c] + acc[r][c];
+      scan_store(in, W, Ut, Kd, ca);
     }
   }
 }
@@ -479,13 +551,8 @@ __global__ __launch_bounds__(256) void dn_output(DnArgs p) {
 // the previous chunk's inputs (P, the dO columns, Q, K, W, ca) are loaded
 // into registers; they go to LDS once the chunk is done with its own.
 
-constexpr int kLdC = 68;   // LDS row of 64 fp32
-constexpr int kLdS = 36;   // LDS row of 32 fp32
 constexpr size_t kSgLds =
     (kC * kLdC + kC * kLdS + 3 * kC * kLd + kD * kLdS + kC * kLdS + kC) * sizeof(float);
-
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
 // One chunk's inputs as this thread loads them (plain vector types, so the
 // whole set stays in registers).
@@ -718,202 +785,283 @@ __global__ __launch_bounds__(256, 1) void dn_grad_a(DnArgs p) {
 }
 
 // ---- backward: the chunk's WY form, decays and gates (part b) -----------------------
+// Every product on the matrix cores in fp32 (mm_by below); Q and K sit in LDS
+// as bf16 (their exact values) and are widened as they are read, V is read
+// from global where it is needed, and dW, dU~ take turns in one fp32 buffer.
+// The row sums of the gate gradients are complete within a wave (each wave
+// owns 16 rows of the 64 x 64 work, and 32 of the 128 columns of the
+// 64 x 128 work, whose partials go to LDS by wave) and are folded in a fixed
+// order, so the result does not depend on timing.
 
-// Q and K sit in LDS as bf16 (their exact values), V is read from global
-// where it is needed; per-row partial sums of the gate gradients go to LDS
-// by column group and are folded in a fixed order, so the result does not
-// depend on timing.
-constexpr int kPadH = kD + 8;   // bf16 row of Q, K
-constexpr int kGroups = 16;     // column groups of the 4 x 4 and 4 x 8 micro-tiles
-constexpr size_t kGbLds = 2 * kC * kPadH * sizeof(uint16_t) + (4 * kC * kPadC + 7 * kC * kGroups + 2 * kC) * sizeof(float);
+// Operand readers for mm_by: quad(x, k) is this lane's (x, k .. k + 3).
+struct RowF32 {  // (x, k) at p[x * ld + k]
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
+};
+struct ColF32 {  // (x, k) at p[k * ld + x]
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
+};
+struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
+  const uint16_t* p;
+  int64_t ld;
+  __device__ f32x4v quad(int x, int k) const {
+    const uint2 w = *reinterpret_cast<const uint2*>(p + x * ld + k);
+    return f32x4v{bf((uint16_t)w.x), bf((uint16_t)(w.x >> 16)), bf((uint16_t)w.y), bf((uint16_t)(w.y >> 16))};
+  }
+};
+struct ColBf16 {  // (x, k) at bf16 p[k * ld + x]
+  const uint16_t* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const {
+    return f32x4v{bf(p[k * ld + x]), bf(p[(k + 1) * ld + x]), bf(p[(k + 2) * ld + x]), bf(p[(k + 3) * ld + x])};
+  }
+};
 
-__global__ __launch_bounds__(256) void dn_grad_b(DnArgs p) {
+// acc[bi][bj] += X(i0 + 16 bi .., k) Y(k, j0 + 16 bj ..) over k in [0, K).
+template <int BI, int BJ, class XR, class YR>
+__device__ __forceinline__ void mm_by(f32x4v (&acc)[BI][BJ], const XR& X, int i0, const YR& Y, int j0, int K) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+  for (int kb = 0; kb < K; kb += 16) {
+    f32x4v a[BI], b[BJ];
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi) a[bi] = X.quad(i0 + 16 * bi + r, kb + 4 * g);
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) b[bj] = Y.quad(j0 + 16 * bj + r, kb + 4 * g);
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+  }
+}
+
+// Sum over the 16 lanes of a row group (lanes 16 g .. 16 g + 15), a fixed tree.
+__device__ __forceinline__ float row_group_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+constexpr int kLdH = kD + 8;  // bf16 LDS row of Q, K
+constexpr size_t kGbLds = 2 * kC * kLdH * sizeof(uint16_t) + (kC * kLd + 4 * kC * kLdC) * sizeof(float) +
+                          (2 * kC + 5 * 4 * kC + 2 * kC) * sizeof(float);
+
+__global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
   extern __shared__ float lds[];
-  uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);   // [64][kPadH]
-  uint16_t* Kh = Qh + kC * kPadH;                   // [64][kPadH]
-  float* T = reinterpret_cast<float*>(Kh + kC * kPadH);  // [64][kPadC]
-  float* M = T + kC * kPadC;      // [64][kPadC]: dT, then dA
-  float* N = M + kC * kPadC;      // [64][kPadC]: T' dT, then dG
-  float* R = N + kC * kPadC;      // [64][kPadC]: dQK = dP o Gamma
-  float* wrow = R + kC * kPadC;   // [64][16]: partial sums of w over j, by column group
-  float* wcol = wrow + kC * kGroups;  // [64][16]: partial sums of w over i, by row group
-  float* brow = wcol + kC * kGroups;  // [64][16]: dA Gamma G over j
-  float* kx = brow + kC * kGroups;    // [64][16]: k . dX by column group
-  float* vy = kx + kC * kGroups;      // [64][16]: v . dY
-  float* qq = vy + kC * kGroups;      // [64][16]: q . dQg
-  float* kk = qq + kC * kGroups;      // [64][16]: k . dKd
-  float* ca = kk + kC * kGroups;      // [64]
-  float* be = ca + kC;                // [64]
+  uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
+  uint16_t* Kh = Qh + kC * kLdH;                          // [64][kLdH]
+  float* A0 = reinterpret_cast<float*>(Kh + kC * kLdH);   // [64][kLd]: dW, then dU~
+  float* T = A0 + kC * kLd;        // [64][kLdC]
+  float* M = T + kC * kLdC;        // [64][kLdC]: dT, then dA, then dG + dG'
+  float* N = M + kC * kLdC;        // [64][kLdC]: T' dT, then dG
+  float* R = N + kC * kLdC;        // [64][kLdC]: dQK = dP o Gamma, lower
+  float* wrow = R + kC * kLdC;     // [64]: sum_j w_ij
+  float* brow = wrow + kC;         // [64]: sum_j dA Gamma G
+  float* wcol = brow + kC;         // [4][64]: sum_i w_ij by wave
+  float* kx = wcol + 4 * kC;       // [4][64]: k . dX by wave (columns)
+  float* vy = kx + 4 * kC;         // [4][64]
+  float* qq = vy + 4 * kC;         // [4][64]
+  float* kk = qq + 4 * kC;         // [4][64]
+  float* ca = kk + 4 * kC;         // [64]
+  float* be = ca + kC;             // [64]
   const Chunk ck = chunk_of(p, blockIdx.x);
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, w = t / 64;
+  const int r = t % 16, g = (t % 64) / 16;
   const uint16_t* qg = p.q + ck.row0;
   const uint16_t* kg = p.k + ck.row0;
   const uint16_t* vg = p.v + ck.row0;
   for (int e = t; e < kC * (kD / 8); e += 256) {
-    const int r = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
-    *reinterpret_cast<uint4*>(Qh + r * kPadH + c8) = *reinterpret_cast<const uint4*>(qg + r * p.s_t + c8);
-    *reinterpret_cast<uint4*>(Kh + r * kPadH + c8) = *reinterpret_cast<const uint4*>(kg + r * p.s_t + c8);
+    const int row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
+    *reinterpret_cast<uint4*>(Qh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(qg + row * p.s_t + c8);
+    *reinterpret_cast<uint4*>(Kh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(kg + row * p.s_t + c8);
   }
   const float* Tc = p.T + ck.c * kC * kC;
-  for (int e = t; e < kC * kC; e += 256) T[(e / kC) * kPadC + e % kC] = Tc[e];
-  if (t < 64) {
-    ca[t] = p.ca[ck.c * kC + t];
-    be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
+  for (int e = t; e < kC * kC / 4; e += 256) {
+    const int row = e / 16, c = 4 * (e % 16);
+    *reinterpret_cast<f32x4v*>(T + row * kLdC + c) = *reinterpret_cast<const f32x4v*>(Tc + row * kC + c);
   }
-  __syncthreads();
-  auto Q = [&](int i, int d) { return bf(Qh[i * kPadH + d]); };
-  auto K = [&](int i, int d) { return bf(Kh[i * kPadH + d]); };
-  auto V = [&](int i, int d) { return bf(vg[(int64_t)i * p.s_t + d]); };
   const float* dW = p.dW + ck.c * kC * kD;
   const float* dUt = p.dU + ck.c * kC * kD;
   const float* dQg = p.dQg + ck.c * kC * kD;
   const float* dKd = p.dKd + ck.c * kC * kD;
   const float* dP = p.dP + ck.c * kC * kC;
+  stage_f32(A0, dW, kC);
+  if (t < 64) {
+    ca[t] = p.ca[ck.c * kC + t];
+    be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
+  }
+  __syncthreads();
+  const RowBf16 Kr{Kh, kLdH}, Qr{Qh, kLdH};
+  const ColBf16 Kc{Kh, kLdH}, Qc{Qh, kLdH};
   const float last = ca[kC - 1];
+  const int i0 = 16 * w;  // this wave's rows of the 64 x 64 work
   // dT = dW X' + dU~ Y',  X = diag(beta e^ca) K, Y = diag(beta) V.
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4], acc2[4][4];
-    zero(acc);
-    zero(acc2);
-    mm(acc, i0, j0, kD, [&](int i, int k) { return dW[i * kD + k]; }, [&](int k, int l) { return K(l, k); });
-    mm(acc2, i0, j0, kD, [&](int i, int k) { return dUt[i * kD + k]; }, [&](int k, int l) { return V(l, k); });
+    f32x4v xk[1][4], yv[1][4];
+    clear(xk);
+    clear(yv);
+    mm_by(xk, RowF32{A0, kLd}, i0, Kr, 0, kD);
+    __syncthreads();  // every wave is done with dW
+    stage_f32(A0, dUt, kC);
+    __syncthreads();
+    mm_by(yv, RowF32{A0, kLd}, i0, RowBf16{vg, p.s_t}, 0, kD);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int l = j0 + c;
-        M[(i0 + r) * kPadC + l] = be[l] * (expf(ca[l]) * acc[r][c] + acc2[r][c]);
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 4 * g + v, l = 16 * bj + r;
+        M[i * kLdC + l] = be[l] * (expf(ca[l]) * xk[0][bj][v] + yv[0][bj][v]);
       }
   }
   __syncthreads();
   // N = T' dT.
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4];
-    zero(acc);
-    mm(acc, i0, j0, kC, [&](int i, int l) { return T[l * kPadC + i]; }, [&](int l, int j) { return M[l * kPadC + j]; });
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) N[(i0 + r) * kPadC + j0 + c] = acc[r][c];
+    f32x4v acc[1][4];
+    clear(acc);
+    mm_by(acc, ColF32{T, kLdC}, i0, ColF32{M, kLdC}, 0, kC);
+    store_blocks(N, kLdC, acc, i0, 0, 1.0f);
   }
   __syncthreads();
   // dA = -(N T') o strict lower (into M);  dQK = dP o Gamma, lower (into R).
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4];
-    zero(acc);
-    mm(acc, i0, j0, kC, [&](int i, int l) { return N[i * kPadC + l]; }, [&](int l, int j) { return T[j * kPadC + l]; });
-    __syncthreads();  // N is read above and rewritten below
+    f32x4v acc[1][4];
+    clear(acc);
+    mm_by(acc, RowF32{N, kLdC}, i0, RowF32{T, kLdC}, 0, kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int i = i0 + r, j = j0 + c;
-        M[i * kPadC + j] = i > j ? -acc[r][c] : 0.0f;
-        R[i * kPadC + j] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 4 * g + v, j = 16 * bj + r;
+        M[i * kLdC + j] = i > j ? -acc[0][bj][v] : 0.0f;
+        R[i * kLdC + j] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
       }
   }
-  __syncthreads();
+  // Every row of this wave's M and R was written by this wave; the other
+  // waves' rows are not read before the next barrier.
   // With G = K K', QK = Q K', Gamma: dG = dA o beta_i o Gamma (into N);
   // dbeta_i gets sum_j dA Gamma G; w = (dA beta_i G + dP QK) o Gamma gives
   // dca_i += sum_j w_ij - sum_j w_ji.
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float g[4][4], qk[4][4];
-    zero(g);
-    zero(qk);
-    if (j0 < i0 + 4) {
-      mm(g, i0, j0, kD, [&](int i, int k) { return K(i, k); }, [&](int k, int j) { return K(j, k); });
-      mm(qk, i0, j0, kD, [&](int i, int k) { return Q(i, k); }, [&](int k, int j) { return K(j, k); });
-    }
-    float colw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4v gk[1][4], qk[1][4];
+    clear(gk);
+    clear(qk);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + r;
-      float rowb = 0.0f, roww = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int j = j0 + c;
-        const float gam = expf(ca[i] - ca[j]);
-        const float dA = M[i * kPadC + j];
-        N[i * kPadC + j] = dA * be[i] * gam;
-        rowb += dA * gam * g[r][c];
-        const float w = i >= j ? (dA * be[i] * g[r][c] + dP[i * kC + j] * qk[r][c]) * gam : 0.0f;
-        roww += w;
-        colw[c] += w;
+    for (int bj = 0; bj < 4; ++bj) {
+      if (bj <= w) {
+        f32x4v a1[1][1], a2[1][1];
+        clear(a1);
+        clear(a2);
+        mm_by(a1, Kr, i0, Kr, 16 * bj, kD);
+        mm_by(a2, Qr, i0, Kr, 16 * bj, kD);
+        gk[0][bj] = a1[0][0];
+        qk[0][bj] = a2[0][0];
       }
-      wrow[i * kGroups + t % 16] = roww;
-      brow[i * kGroups + t % 16] = rowb;
     }
+    float roww[4] = {0, 0, 0, 0}, rowb[4] = {0, 0, 0, 0};
+    float colw[4] = {0, 0, 0, 0};  // column 16 bj + r, this wave's rows
 #pragma unroll
-    for (int c = 0; c < 4; ++c) wcol[(j0 + c) * kGroups + t / 16] = colw[c];
+    for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 4 * g + v, j = 16 * bj + r;
+        const float gam = expf(ca[i] - ca[j]);
+        const float dA = M[i * kLdC + j];
+        const float gg = bj <= w ? gk[0][bj][v] : 0.0f, q = bj <= w ? qk[0][bj][v] : 0.0f;
+        N[i * kLdC + j] = dA * be[i] * gam;
+        rowb[v] += dA * gam * gg;
+        const float wv = i >= j ? (dA * be[i] * gg + dP[i * kC + j] * q) * gam : 0.0f;
+        roww[v] += wv;
+        colw[bj] += wv;
+      }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      roww[v] = row_group_sum(roww[v]);
+      rowb[v] = row_group_sum(rowb[v]);
+    }
+    if (r == 0)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) wrow[i0 + 4 * g + v] = roww[v], brow[i0 + 4 * g + v] = rowb[v];
+    // Column sums over this wave's 16 rows: the four row groups g, in order.
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      float x = colw[bj];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      if (g == 0) wcol[w * kC + 16 * bj + r] = x;
+    }
+  }
+  __syncthreads();
+  // M <- dG + dG'.
+  for (int e = t; e < kC * kC; e += 256) {
+    const int i = e / kC, j = e % kC;
+    M[i * kLdC + j] = N[i * kLdC + j] + N[j * kLdC + i];
   }
   __syncthreads();
   // dQ = e^ca dQg + dQK K;  dK = dQK' Q + (dG + dG') K + beta e^ca dX + e^(last - ca) dKd;
-  // dX = T' dW;  dV = beta T' dU~.
+  // dX = T' dW;  dV = beta T' dU~.  Wave w: columns 32 w .. 32 w + 31.
   {
-    const int i0 = 4 * (t / 16), j0 = 8 * (t % 16);
-    float dq[4][8], dk[4][8], dx[4][8], dy[4][8];
-    zero(dq);
-    zero(dk);
-    zero(dx);
-    zero(dy);
-    mm(dq, i0, j0, kC, [&](int i, int l) { return R[i * kPadC + l]; }, [&](int l, int d) { return K(l, d); });
-    mm(dk, i0, j0, kC, [&](int i, int l) { return R[l * kPadC + i]; }, [&](int l, int d) { return Q(l, d); });
-    mm(dk, i0, j0, kC, [&](int i, int l) { return N[i * kPadC + l] + N[l * kPadC + i]; }, [&](int l, int d) { return K(l, d); });
-    mm(dx, i0, j0, kC, [&](int i, int l) { return T[l * kPadC + i]; }, [&](int l, int d) { return dW[l * kD + d]; });
-    mm(dy, i0, j0, kC, [&](int i, int l) { return T[l * kPadC + i]; }, [&](int l, int d) { return dUt[l * kD + d]; });
+    const int d0 = 32 * w;
+    f32x4v dq[4][2], dk[4][2], dx[4][2], dy[4][2];
+    clear(dq);
+    clear(dk);
+    clear(dx);
+    clear(dy);
+    mm_by(dy, ColF32{T, kLdC}, 0, ColF32{A0, kLd}, d0, kC);  // A0 holds dU~
+    mm_by(dq, RowF32{R, kLdC}, 0, Kc, d0, kC);
+    mm_by(dk, ColF32{R, kLdC}, 0, Qc, d0, kC);
+    mm_by(dk, RowF32{M, kLdC}, 0, Kc, d0, kC);
+    __syncthreads();  // every wave is done with dU~
+    stage_f32(A0, dW, kC);
+    __syncthreads();
+    mm_by(dx, ColF32{T, kLdC}, 0, ColF32{A0, kLd}, d0, kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + r;
-      const float e = expf(ca[i]), ed = expf(last - ca[i]);
-      float skx = 0.0f, svy = 0.0f, sqq = 0.0f, skk = 0.0f;
-      uint32_t wq[4], wk[4], wv[4];
+    for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int d = j0 + c;
-        const float gq = dQg[i * kD + d], gk = dKd[i * kD + d];
-        const float vq = e * gq + dq[r][c];
-        const float vk = dk[r][c] + be[i] * e * dx[r][c] + ed * gk;
-        const float vv = be[i] * dy[r][c];
-        skx = fmaf(K(i, d), dx[r][c], skx);
-        svy = fmaf(V(i, d), dy[r][c], svy);
-        sqq = fmaf(Q(i, d), gq, sqq);
-        skk = fmaf(K(i, d), gk, skk);
-        const uint32_t hq = to_bf(vq), hk = to_bf(vk), hv = to_bf(vv);
-        if (c % 2 == 0) {
-          wq[c / 2] = hq, wk[c / 2] = hk, wv[c / 2] = hv;
-        } else {
-          wq[c / 2] |= hq << 16, wk[c / 2] |= hk << 16, wv[c / 2] |= hv << 16;
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * bi + 4 * g + v;
+        const float e = expf(ca[i]), ed = expf(last - ca[i]);
+        float skx = 0.0f, svy = 0.0f, sqq = 0.0f, skk = 0.0f;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          const int d = d0 + 16 * bj + r;
+          const float gq = dQg[i * kD + d], gk = dKd[i * kD + d];
+          const float kv = bf(Kh[i * kLdH + d]), qv = bf(Qh[i * kLdH + d]), vv = bf(vg[(int64_t)i * p.s_t + d]);
+          const float xv = dx[bi][bj][v], yv = dy[bi][bj][v];
+          const float oq = e * gq + dq[bi][bj][v];
+          const float ok = dk[bi][bj][v] + be[i] * e * xv + ed * gk;
+          const float ov = be[i] * yv;
+          skx = fmaf(kv, xv, skx);
+          svy = fmaf(vv, yv, svy);
+          sqq = fmaf(qv, gq, sqq);
+          skk = fmaf(kv, gk, skk);
+          const int64_t at = ck.row0 + (int64_t)i * p.s_t + d;
+          p.dq[at] = to_bf(oq);
+          p.dk[at] = to_bf(ok);
+          p.dv[at] = to_bf(ov);
         }
+        skx = row_group_sum(skx);
+        svy = row_group_sum(svy);
+        sqq = row_group_sum(sqq);
+        skk = row_group_sum(skk);
+        if (r == 0) kx[w * kC + i] = skx, vy[w * kC + i] = svy, qq[w * kC + i] = sqq, kk[w * kC + i] = skk;
       }
-      const int64_t at = ck.row0 + (int64_t)i * p.s_t + j0;
-      *reinterpret_cast<uint4*>(p.dq + at) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-      *reinterpret_cast<uint4*>(p.dk + at) = make_uint4(wk[0], wk[1], wk[2], wk[3]);
-      *reinterpret_cast<uint4*>(p.dv + at) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-      kx[i * kGroups + t % 16] = skx;
-      vy[i * kGroups + t % 16] = svy;
-      qq[i * kGroups + t % 16] = sqq;
-      kk[i * kGroups + t % 16] = skk;
-    }
   }
   __syncthreads();
   // Fold the partials in a fixed order (lane i: row i), then da = the
   // reverse cumulative sum of dca, dca_63 also taking sum kd + dg g.
   if (t < 64) {
     const int i = t;
-    float sw = 0.0f, sc = 0.0f, sb = 0.0f, skx = 0.0f, svy = 0.0f, sqq = 0.0f, skk = 0.0f;
-    for (int gi = 0; gi < kGroups; ++gi) {
-      sw += wrow[i * kGroups + gi];
-      sc += wcol[i * kGroups + gi];
-      sb += brow[i * kGroups + gi];
-      skx += kx[i * kGroups + gi];
-      svy += vy[i * kGroups + gi];
-      sqq += qq[i * kGroups + gi];
-      skk += kk[i * kGroups + gi];
+    float sc = 0.0f, skx = 0.0f, svy = 0.0f, sqq = 0.0f, skk = 0.0f;
+    for (int wv = 0; wv < 4; ++wv) {
+      sc += wcol[wv * kC + i];
+      skx += kx[wv * kC + i];
+      svy += vy[wv * kC + i];
+      sqq += qq[wv * kC + i];
+      skk += kk[wv * kC + i];
     }
+    const float sw = wrow[i], sb = brow[i];
     const float e = expf(ca[i]), ed = expf(last - ca[i]);
     const float kd = ed * skk;
     float dca = sw - sc + be[i] * e * skx + e * sqq - kd;
