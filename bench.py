@@ -214,7 +214,7 @@ def config4(target, steps: int = 3, warmup: int = 1):
             "frac_of_bf16_peak": total / (t_f + t_b) / BF16_PEAK, "flops_per_step": total,
             "fwd": {"ms": t_f * 1e3, "TFLOP/s": f_fwd / t_f / 1e12},
             "bwd": {"ms": t_b * 1e3, "TFLOP/s": f_bwd / t_b / 1e12,
-                    "note": "FA2 convention, 2.5x forward flops; the deterministic dQ sweep recomputes S and dP"}}
+                    "note": "FA2 convention, 2.5x forward flops; deterministic: the dK/dV sweep stores dS, a dQ sweep reads it"}}
 
 
 def config5(target, steps: int = 3, warmup: int = 1):
@@ -246,8 +246,9 @@ def config5(target, steps: int = 3, warmup: int = 1):
     s = e0.elapsed_time(e1) * 1e-3 / steps
     return {"ms_per_step": s * 1e3, "TFLOP/s": w.flops / s / 1e12, "GB/s": w.bytes / s / 1e9,
             "flops_per_step": w.flops, "bytes_per_step": w.bytes,
-            "note": "fp32 FMA kernels (chunk prep, column-split state scan, outputs, reverse state-gradient "
-                    "scan, chunk-local backward); flops/bytes are the algorithmic estimates of th_launch_work"}
+            "note": "fp32 products on the matrix cores (chunk prep, column-split state scan, outputs, reverse "
+                    "state-gradient scan, chunk-local backward); flops/bytes are the algorithmic estimates of "
+                    "th_launch_work"}
 
 
 def main() -> int:

@@ -12,8 +12,8 @@
 //   P = lower (Gamma_ij q_i.k_j),  Qg = diag(e^ca) Q,  Kd = diag(e^(ca_63 - ca)) K,  g = e^ca_63;
 // across chunks:  U = U~ - W S,  O = Qg S + P U,  S <- g S + Kd' U.
 //
-// Kernels (fp32 arithmetic on fp32 FMA units; inputs bf16 q, k, v and fp32
-// a, beta):
+// Kernels (fp32 arithmetic, every product on the matrix cores as
+// v_mfma_f32_16x16x4_f32; inputs bf16 q, k, v and fp32 a, beta):
 //   dn_chunk_prep   one workgroup per chunk: ca, A, T (forward substitution,
 //                   one lane per column), W, U~.
 //   dn_state_scan   one workgroup per (sequence, 32 columns of S): the
@@ -35,8 +35,6 @@ namespace {
 constexpr int kC = 64;    // chunk
 constexpr int kD = 128;   // dk = dv
 constexpr int kCols = 32; // columns of S per scan workgroup
-constexpr int kPadD = kD + 4;
-constexpr int kPadC = kC + 1;
 
 struct DnArgs {
   const uint16_t* q;
@@ -93,20 +91,6 @@ __device__ __forceinline__ Chunk chunk_of(const DnArgs& p, int64_t c) {
   return k;
 }
 
-// A 64 x 128 bf16 chunk of a (d, heads, positions, batch) array into LDS as fp32 [64][kPadD].
-__device__ __forceinline__ void load_chunk(float* dst, const uint16_t* src, int64_t s_t) {
-  for (int e = threadIdx.x; e < kC * (kD / 8); e += 256) {
-    const int r = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
-    const uint4 w = *reinterpret_cast<const uint4*>(src + r * s_t + c8);
-    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dst[r * kPadD + c8 + 2 * j] = bf((uint16_t)u[j]);
-      dst[r * kPadD + c8 + 2 * j + 1] = bf((uint16_t)(u[j] >> 16));
-    }
-  }
-}
-
 // ca = inclusive cumulative sum of a over the chunk (wave 0), into LDS.
 __device__ __forceinline__ void cumulative_gates(float* ca, const DnArgs& p, const Chunk& ck) {
   if (threadIdx.x < 64) {
@@ -119,31 +103,6 @@ __device__ __forceinline__ void cumulative_gates(float* ca, const DnArgs& p, con
     ca[threadIdx.x] = x;
   }
 }
-
-// acc[TM][TN] += sum_k A(i0 + r, k) B(k, j0 + c).
-template <int TM, int TN, class FA, class FB>
-__device__ __forceinline__ void mm(float (&acc)[TM][TN], int i0, int j0, int K, FA A, FB B) {
-  for (int k = 0; k < K; ++k) {
-    float av[TM], bv[TN];
-#pragma unroll
-    for (int r = 0; r < TM; ++r) av[r] = A(i0 + r, k);
-#pragma unroll
-    for (int c = 0; c < TN; ++c) bv[c] = B(k, j0 + c);
-#pragma unroll
-    for (int r = 0; r < TM; ++r)
-#pragma unroll
-      for (int c = 0; c < TN; ++c) acc[r][c] = fmaf(av[r], bv[c], acc[r][c]);
-  }
-}
-
-template <int TM, int TN>
-__device__ __forceinline__ void zero(float (&acc)[TM][TN]) {
-#pragma unroll
-  for (int r = 0; r < TM; ++r)
-#pragma unroll
-    for (int c = 0; c < TN; ++c) acc[r][c] = 0.0f;
-}
-
 
 // ---- fp32 products on the matrix cores ----------------------------------------------
 // v_mfma_f32_16x16x4_f32 multiplies fp32 exactly and accumulates in fp32, as
@@ -263,40 +222,105 @@ __device__ __forceinline__ void store_blocks(float* out, int ld, const f32x4v (&
       for (int v = 0; v < 4; ++v) out[(int64_t)(i0 + 16 * bi + 4 * g + v) * ld + j0 + 16 * bj + r] = s * acc[bi][bj][v];
 }
 
-// ---- forward: the chunk's WY form -------------------------------------------------
+// Operand readers for mm_by: quad(x, k) is this lane's (x, k .. k + 3).
+struct RowF32 {  // (x, k) at p[x * ld + k]
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
+};
+struct ColF32 {  // (x, k) at p[k * ld + x]
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
+};
+struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
+  const uint16_t* p;
+  int64_t ld;
+  __device__ f32x4v quad(int x, int k) const {
+    const uint2 w = *reinterpret_cast<const uint2*>(p + x * ld + k);
+    return f32x4v{bf((uint16_t)w.x), bf((uint16_t)(w.x >> 16)), bf((uint16_t)w.y), bf((uint16_t)(w.y >> 16))};
+  }
+};
+struct ColBf16 {  // (x, k) at bf16 p[k * ld + x]
+  const uint16_t* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const {
+    return f32x4v{bf(p[k * ld + x]), bf(p[(k + 1) * ld + x]), bf(p[(k + 2) * ld + x]), bf(p[(k + 3) * ld + x])};
+  }
+};
 
-constexpr size_t kPrepLds = (2 * kC * kPadD + kC * kPadC + 2 * kC) * sizeof(float);
+// acc[bi][bj] += X(i0 + 16 bi .., k) Y(k, j0 + 16 bj ..) over k in [0, K).
+template <int BI, int BJ, class XR, class YR>
+__device__ __forceinline__ void mm_by(f32x4v (&acc)[BI][BJ], const XR& X, int i0, const YR& Y, int j0, int K) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+  for (int kb = 0; kb < K; kb += 16) {
+    f32x4v a[BI], b[BJ];
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi) a[bi] = X.quad(i0 + 16 * bi + r, kb + 4 * g);
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) b[bj] = Y.quad(j0 + 16 * bj + r, kb + 4 * g);
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+  }
+}
+
+// Sum over the 16 lanes of a row group (lanes 16 g .. 16 g + 15), a fixed tree.
+__device__ __forceinline__ float row_group_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+constexpr int kLdH = kD + 8;  // bf16 LDS row of Q, K
+
+// ---- forward: the chunk's WY form -------------------------------------------------
+// ca, A = strict lower (beta_i Gamma_ij k_i.k_j), T = (I + A)^-1 (forward
+// substitution, one lane per column), W = T diag(beta e^ca) K and
+// U~ = T diag(beta) V; the products on the matrix cores in fp32, K and V in
+// LDS as bf16.
+
+__device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* src, int64_t s_t) {
+  for (int e = threadIdx.x; e < kC * (kD / 8); e += 256) {
+    const int row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
+    *reinterpret_cast<uint4*>(dst + row * kLdH + c8) = *reinterpret_cast<const uint4*>(src + row * s_t + c8);
+  }
+}
+
+constexpr size_t kPrepLds = 2 * kC * kLdH * sizeof(uint16_t) + (3 * kC * kLdC + 2 * kC) * sizeof(float);
 
 __global__ __launch_bounds__(256) void dn_chunk_prep(DnArgs p) {
   extern __shared__ float lds[];
-  float* K = lds;                  // [64][kPadD]
-  float* V = K + kC * kPadD;       // [64][kPadD]
-  float* AT = V + kC * kPadD;      // [64][kPadC]: A, then T
-  float* ca = AT + kC * kPadC;     // [64]
-  float* be = ca + kC;             // [64]
+  uint16_t* Kh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
+  uint16_t* Vh = Kh + kC * kLdH;                          // [64][kLdH]
+  float* AT = reinterpret_cast<float*>(Vh + kC * kLdH);   // [64][kLdC]: A, then T
+  float* TX = AT + kC * kLdC;     // [64][kLdC]: T diag(beta e^ca)
+  float* TY = TX + kC * kLdC;     // [64][kLdC]: T diag(beta)
+  float* ca = TY + kC * kLdC;     // [64]
+  float* be = ca + kC;            // [64]
   const Chunk ck = chunk_of(p, blockIdx.x);
-  const int t = threadIdx.x;
-  load_chunk(K, p.k + ck.row0, p.s_t);
-  load_chunk(V, p.v + ck.row0, p.s_t);
+  const int t = threadIdx.x, w = t / 64;
+  const int r = t % 16, g = (t % 64) / 16;
+  stage_rows_bf16(Kh, p.k + ck.row0, p.s_t);
+  stage_rows_bf16(Vh, p.v + ck.row0, p.s_t);
   cumulative_gates(ca, p, ck);
   if (t < 64) be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
   __syncthreads();
   if (t < 64) p.ca[ck.c * kC + t] = ca[t];
-  // A = strict lower (beta_i Gamma_ij k_i.k_j): thread (4 x 4) micro-tile.
+  // A (64 x 64): wave w takes row block w, blocks at or left of the diagonal.
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4];
-    zero(acc);
-    if (j0 < i0 + 4)
-      mm(acc, i0, j0, kD, [&](int i, int k) { return K[i * kPadD + k]; },
-         [&](int k, int j) { return K[j * kPadD + k]; });
+    const RowBf16 Kr{Kh, kLdH};
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4v acc[1][1];
+      clear(acc);
+      if (bj <= w) mm_by(acc, Kr, 16 * w, Kr, 16 * bj, kD);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int i = i0 + r, j = j0 + c;
-        AT[i * kPadC + j] = i > j ? be[i] * expf(ca[i] - ca[j]) * acc[r][c] : 0.0f;
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
+        AT[i * kLdC + j] = i > j ? be[i] * expf(ca[i] - ca[j]) * acc[0][0][v] : 0.0f;
       }
+    }
   }
   __syncthreads();
   // T = (I + A)^-1 by forward substitution, lane j owning column j:
@@ -306,46 +330,37 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(DnArgs p) {
     float col[kC];
 #pragma unroll
     for (int i = 0; i < kC; ++i) {
-      float s = 0.0f;
+      float sum = 0.0f;
 #pragma unroll
-      for (int l = 0; l < i; ++l) s = fmaf(AT[i * kPadC + l], col[l], s);
-      col[i] = i == j ? 1.0f : (i < j ? 0.0f : -s);
+      for (int l = 0; l < i; ++l) sum = fmaf(AT[i * kLdC + l], col[l], sum);
+      col[i] = i == j ? 1.0f : (i < j ? 0.0f : -sum);
     }
     // One wave: its LDS reads of A above complete before its writes of T below.
 #pragma unroll
-    for (int i = 0; i < kC; ++i) AT[i * kPadC + j] = col[i];
+    for (int i = 0; i < kC; ++i) AT[i * kLdC + j] = col[i];
   }
   __syncthreads();
-  // W = T diag(beta e^ca) K, U~ = T diag(beta) V: thread (4 rows x 8 columns).
   {
-    const int i0 = 4 * (t / 16), j0 = 8 * (t % 16);
-    float w[4][8], u[4][8];
-    zero(w);
-    zero(u);
-    for (int l = 0; l < kC; ++l) {
-      float tv[4], xk[8], yv[8];
-      const float sx = be[l] * expf(ca[l]), sy = be[l];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tv[r] = AT[(i0 + r) * kPadC + l];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) xk[c] = sx * K[l * kPadD + j0 + c], yv[c] = sy * V[l * kPadD + j0 + c];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) w[r][c] = fmaf(tv[r], xk[c], w[r][c]), u[r][c] = fmaf(tv[r], yv[c], u[r][c]);
+    float* Tc = p.T + ck.c * kC * kC;
+    for (int e = t; e < kC * kC; e += 256) {
+      const int i = e / kC, l = e % kC;
+      const float tv = AT[i * kLdC + l];
+      Tc[e] = tv;
+      TX[i * kLdC + l] = tv * be[l] * expf(ca[l]);
+      TY[i * kLdC + l] = tv * be[l];
     }
-    float* Wc = p.W + ck.c * kC * kD;
-    float* Uc = p.Ut + ck.c * kC * kD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 8; c += 4) {
-        *reinterpret_cast<float4*>(Wc + (i0 + r) * kD + j0 + c) = make_float4(w[r][c], w[r][c + 1], w[r][c + 2], w[r][c + 3]);
-        *reinterpret_cast<float4*>(Uc + (i0 + r) * kD + j0 + c) = make_float4(u[r][c], u[r][c + 1], u[r][c + 2], u[r][c + 3]);
-      }
   }
-  float* Tc = p.T + ck.c * kC * kC;
-  for (int e = t; e < kC * kC; e += 256) Tc[e] = AT[(e / kC) * kPadC + e % kC];
+  __syncthreads();
+  // W = TX K, U~ = TY V (64 x 128): wave w takes columns 32 w .. 32 w + 31.
+  {
+    f32x4v wk[4][2], uv[4][2];
+    clear(wk);
+    clear(uv);
+    mm_by(wk, RowF32{TX, kLdC}, 0, ColBf16{Kh, kLdH}, 32 * w, kC);
+    mm_by(uv, RowF32{TY, kLdC}, 0, ColBf16{Vh, kLdH}, 32 * w, kC);
+    store_blocks(p.W + ck.c * kC * kD, kD, wk, 0, 32 * w, 1.0f);
+    store_blocks(p.Ut + ck.c * kC * kD, kD, uv, 0, 32 * w, 1.0f);
+  }
 }
 
 // ---- forward: the recurrence across chunks, 32 columns of S per workgroup ---------
@@ -486,61 +501,62 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
 }
 
 // ---- forward: outputs ----------------------------------------------------------------
+// P = lower(Gamma o Q K'), O = diag(e^ca) Q S + P U; the products on the
+// matrix cores in fp32, Q and K in LDS as bf16.
 
-constexpr size_t kOutLds = (3 * kC * kPadD + kC * kPadC + kC) * sizeof(float);
+constexpr size_t kOutLds = 2 * kC * kLdH * sizeof(uint16_t) + (kD * kLd + kC * kLd + kC * kLdC + kC) * sizeof(float);
 
-__global__ __launch_bounds__(256) void dn_output(DnArgs p) {
+__global__ __launch_bounds__(256, 1) void dn_output(DnArgs p) {
   extern __shared__ float lds[];
-  float* Q = lds;                // [64][kPadD]
-  float* K = Q + kC * kPadD;     // [64][kPadD]
-  float* U = K + kC * kPadD;     // [64][kPadD]
-  float* P = U + kC * kPadD;     // [64][kPadC]
-  float* ca = P + kC * kPadC;    // [64]
+  uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
+  uint16_t* Kh = Qh + kC * kLdH;                          // [64][kLdH]
+  float* S = reinterpret_cast<float*>(Kh + kC * kLdH);    // [128][kLd]
+  float* U = S + kD * kLd;        // [64][kLd]
+  float* P = U + kC * kLd;        // [64][kLdC]
+  float* ca = P + kC * kLdC;      // [64]
   const Chunk ck = chunk_of(p, blockIdx.x);
-  const int t = threadIdx.x;
-  load_chunk(Q, p.q + ck.row0, p.s_t);
-  load_chunk(K, p.k + ck.row0, p.s_t);
-  const float* Uc = p.U + ck.c * kC * kD;
-  for (int e = t; e < kC * kD; e += 256) U[(e / kD) * kPadD + e % kD] = Uc[e];
+  const int t = threadIdx.x, w = t / 64;
+  const int r = t % 16, g = (t % 64) / 16;
+  stage_rows_bf16(Qh, p.q + ck.row0, p.s_t);
+  stage_rows_bf16(Kh, p.k + ck.row0, p.s_t);
+  stage_f32(S, p.S + ck.c * kD * kD, kD);
+  stage_f32(U, p.U + ck.c * kC * kD, kC);
   if (t < 64) ca[t] = p.ca[ck.c * kC + t];
   __syncthreads();
+  const RowBf16 Qr{Qh, kLdH};
   {
-    const int i0 = 4 * (t / 16), j0 = 4 * (t % 16);
-    float acc[4][4];
-    zero(acc);
-    if (j0 < i0 + 4)
-      mm(acc, i0, j0, kD, [&](int i, int k) { return Q[i * kPadD + k]; }, [&](int k, int j) { return K[j * kPadD + k]; });
     float* Pc = p.P + ck.c * kC * kC;
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4v acc[1][1];
+      clear(acc);
+      if (bj <= w) mm_by(acc, Qr, 16 * w, RowBf16{Kh, kLdH}, 16 * bj, kD);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int i = i0 + r, j = j0 + c;
-        const float v = i >= j ? expf(ca[i] - ca[j]) * acc[r][c] : 0.0f;
-        P[i * kPadC + j] = v;
-        Pc[i * kC + j] = v;
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
+        const float x = i >= j ? expf(ca[i] - ca[j]) * acc[0][0][v] : 0.0f;
+        P[i * kLdC + j] = x;
+        Pc[i * kC + j] = x;
       }
+    }
   }
   __syncthreads();
-  // O = diag(e^ca) Q S + P U: thread (4 rows x 8 columns) of 64 x 128.
+  // O (64 x 128): wave w takes columns 32 w .. 32 w + 31.
   {
-    const int i0 = 4 * (t / 16), j0 = 8 * (t % 16);
-    const float* Sc = p.S + ck.c * kD * kD;
-    float qs[4][8], pu[4][8];
-    zero(qs);
-    zero(pu);
-    mm(qs, i0, j0, kD, [&](int i, int k) { return Q[i * kPadD + k]; }, [&](int k, int j) { return Sc[k * kD + j]; });
-    mm(pu, i0, j0, kC, [&](int i, int l) { return P[i * kPadC + l]; }, [&](int l, int j) { return U[l * kPadD + j]; });
+    f32x4v qs[4][2], pu[4][2];
+    clear(qs);
+    clear(pu);
+    mm_by(qs, Qr, 0, ColF32{S, kLd}, 32 * w, kD);
+    mm_by(pu, RowF32{P, kLdC}, 0, ColF32{U, kLd}, 32 * w, kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float e = expf(ca[i0 + r]);
-      uint16_t* orow = p.o + ck.row0 + (int64_t)(i0 + r) * p.s_t + j0;
-      uint32_t w[4];
+    for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
-      for (int c = 0; c < 8; c += 2)
-        w[c / 2] = (uint32_t)to_bf(e * qs[r][c] + pu[r][c]) | ((uint32_t)to_bf(e * qs[r][c + 1] + pu[r][c + 1]) << 16);
-      *reinterpret_cast<uint4*>(orow) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+      for (int v = 0; v < 4; ++v) {
+        const int i = 16 * bi + 4 * g + v;
+        const float e = expf(ca[i]);
+        uint16_t* orow = p.o + ck.row0 + (int64_t)i * p.s_t + 32 * w + r;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) orow[16 * bj] = to_bf(e * qs[bi][bj][v] + pu[bi][bj][v]);
+      }
   }
 }
 
@@ -793,58 +809,6 @@ __global__ __launch_bounds__(256, 1) void dn_grad_a(DnArgs p) {
 // 64 x 128 work, whose partials go to LDS by wave) and are folded in a fixed
 // order, so the result does not depend on timing.
 
-// Operand readers for mm_by: quad(x, k) is this lane's (x, k .. k + 3).
-struct RowF32 {  // (x, k) at p[x * ld + k]
-  const float* p;
-  int ld;
-  __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
-};
-struct ColF32 {  // (x, k) at p[k * ld + x]
-  const float* p;
-  int ld;
-  __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
-};
-struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
-  const uint16_t* p;
-  int64_t ld;
-  __device__ f32x4v quad(int x, int k) const {
-    const uint2 w = *reinterpret_cast<const uint2*>(p + x * ld + k);
-    return f32x4v{bf((uint16_t)w.x), bf((uint16_t)(w.x >> 16)), bf((uint16_t)w.y), bf((uint16_t)(w.y >> 16))};
-  }
-};
-struct ColBf16 {  // (x, k) at bf16 p[k * ld + x]
-  const uint16_t* p;
-  int ld;
-  __device__ f32x4v quad(int x, int k) const {
-    return f32x4v{bf(p[k * ld + x]), bf(p[(k + 1) * ld + x]), bf(p[(k + 2) * ld + x]), bf(p[(k + 3) * ld + x])};
-  }
-};
-
-// acc[bi][bj] += X(i0 + 16 bi .., k) Y(k, j0 + 16 bj ..) over k in [0, K).
-template <int BI, int BJ, class XR, class YR>
-__device__ __forceinline__ void mm_by(f32x4v (&acc)[BI][BJ], const XR& X, int i0, const YR& Y, int j0, int K) {
-  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
-  for (int kb = 0; kb < K; kb += 16) {
-    f32x4v a[BI], b[BJ];
-#pragma unroll
-    for (int bi = 0; bi < BI; ++bi) a[bi] = X.quad(i0 + 16 * bi + r, kb + 4 * g);
-#pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) b[bj] = Y.quad(j0 + 16 * bj + r, kb + 4 * g);
-#pragma unroll
-    for (int bi = 0; bi < BI; ++bi)
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
-  }
-}
-
-// Sum over the 16 lanes of a row group (lanes 16 g .. 16 g + 15), a fixed tree.
-__device__ __forceinline__ float row_group_sum(float x) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
-
-constexpr int kLdH = kD + 8;  // bf16 LDS row of Q, K
 constexpr size_t kGbLds = 2 * kC * kLdH * sizeof(uint16_t) + (kC * kLd + 4 * kC * kLdC) * sizeof(float) +
                           (2 * kC + 5 * 4 * kC + 2 * kC) * sizeof(float);
 
