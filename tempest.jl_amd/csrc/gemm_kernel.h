@@ -285,7 +285,11 @@ __device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t
 // waited for explicitly at the barrier, where the stage they fill is next read.
 
 constexpr int kTileD = kTile * kDepth;                         // bf16 per operand stage
-constexpr size_t kLdsDirect = 4 * kTileD * sizeof(uint16_t);   // A and B, two stages: 131072 bytes
+constexpr int kEpiRow = 136;                                  // LDS row (bf16) of the epilogue's transpose: 128 m + 8
+constexpr size_t kEpiWave = 128 * kEpiRow * sizeof(uint16_t);  // one wave's 128 x 128 tile
+// A and B in two stages (131072 bytes), or after the sweep the four waves'
+// transposed tiles (139264 bytes).
+constexpr size_t kLdsDirect = 4 * kEpiWave > 4 * kTileD * sizeof(uint16_t) ? 4 * kEpiWave : 4 * kTileD * sizeof(uint16_t);
 constexpr int kOpBytes = kTileD * 2;                           // one operand's stage: 32 KiB
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -432,10 +436,141 @@ __device__ __forceinline__ void sweep_direct(const GemmArgs& p, int m0, int n0, 
     // The next tile's loads (this wave's) are done; after the barrier every
     // wave's are, and every wave has finished reading this stage.
     wait_and_meet<0>();
-    static_for<4>([&](auto I) {
-      af[0][I] = oa.template frag<I, 0>(so ^ kStageBytes);
-      bf[0][I] = ob.template frag<I, 0>(so ^ kStageBytes);
-    });
+    if (kt + 1 < KT)
+      static_for<4>([&](auto I) {
+        af[0][I] = oa.template frag<I, 0>(so ^ kStageBytes);
+        bf[0][I] = ob.template frag<I, 0>(so ^ kStageBytes);
+      });
+  }
+  // Every wave has passed the last barrier with no LDS access outstanding:
+  // the stages are free for the epilogue.
+}
+
+// ---- the interior tiles' epilogue: through LDS, whole lines out ------------------
+// The accumulators give each lane four consecutive m of one column n, so
+// storing straight from them writes 8 bytes into each of 32 columns per
+// instruction and lines leave the L2 partly written (about twice the
+// algorithmic bytes reach HBM for the fused epilogues).  Instead each wave
+// rounds its 128 x 128 tile (plus the bias) to bf16 into its own LDS region,
+// column-major with rows of kEpiRow, and reads it back eight m at a time:
+// per instruction 16 lanes cover one column's 128 m (256 contiguous bytes),
+// so every store writes whole lines.  The element-wise work of the fused
+// epilogue (GELU, the square loss, the GELU backward) runs on the values read
+// back, rounding where the values are stored, and the row sums fold this
+// lane's eight m over its columns, then over the four column groups of lanes,
+// in a fixed order.
+__device__ __forceinline__ void tile_of(int block, int tiles_m, int tiles_n, int* tm, int* tn);
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_lds(const GemmArgs& p, const f32x16 (&acc)[4][4]) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  // The tile and wave coordinates are derived again here rather than kept
+  // live across the sweep, where every register is taken.
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int wm = wave / 2, wn = wave % 2;
+  uint16_t* tile = lds + wave * (kEpiWave / sizeof(uint16_t));
+  int lane = threadIdx.x % 64;
+  asm volatile("" : "+v"(lane));  // keep the epilogue's address arithmetic below the sweep
+  const int lr = lane % 32, lh = lane / 32;
+  const int mw = tm * kTile + wm * 128, nw = tn * kTile + wn * 128;
+  // Phase 1: lane (lr, lh) holds m = 32 i + 8 g + 4 lh + (0..3), n = 32 j + lr.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float bias[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bias[g][r] = 0.0f;
+    if (EPI == kGelu || EPI == kSquareLoss || (EPI == kStore && p.bias)) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const u32x2 bb = *reinterpret_cast<const u32x2*>(p.bias + mw + 32 * i + 8 * g + 4 * lh);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bias[g][r] = half_of(bb[r / 2], r % 2);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = bf16_bits(acc[i][j][4 * g + r] + bias[g][r]);
+        *reinterpret_cast<u32x2*>(tile + (32 * j + lr) * kEpiRow + 32 * i + 8 * g + 4 * lh) = pack4(h);
+      }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Phase 2: lane takes m = 8 (lane % 16) + (0..7) of columns 4 t + lane / 16.
+  constexpr bool kSums = EPI == kSquareLoss || EPI == kGeluBackward;
+  const int mc = 8 * (lane % 16), cg = lane / 16;
+  float rs[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) rs[e] = 0.0f;
+  float loss = 0.0f;
+  uint16_t* c = static_cast<uint16_t*>(p.c);
+  for (int t = 0; t < 32; ++t) {
+    const int nl = 4 * t + cg;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(tile + nl * kEpiRow + mc);
+    const int64_t at = (int64_t)(mw + mc) + (int64_t)(nw + nl) * p.ldc;
+    if constexpr (EPI == kStore) {
+      *reinterpret_cast<u32x4*>(c + at) = v;
+    } else if constexpr (EPI == kGelu) {
+      u32x4 hv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = bf16_bits(gelu(half_of(v[e], 0))), hi = bf16_bits(gelu(half_of(v[e], 1)));
+        hv[e] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4*>(c + at) = v;
+      *reinterpret_cast<u32x4*>(p.aux_out + at) = hv;
+    } else if constexpr (EPI == kSquareLoss) {
+      u32x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y0 = half_of(v[e], 0), y1 = half_of(v[e], 1);
+        const uint16_t o0 = bf16_bits(2.0f * y0), o1 = bf16_bits(2.0f * y1);
+        loss = fmaf(y0, y0, loss);
+        loss = fmaf(y1, y1, loss);
+        rs[2 * e] += bf16_float(o0);
+        rs[2 * e + 1] += bf16_float(o1);
+        ov[e] = (uint32_t)o0 | ((uint32_t)o1 << 16);
+      }
+      *reinterpret_cast<u32x4*>(c + at) = ov;
+    } else if constexpr (EPI == kGeluBackward) {
+      const u32x4 z = *reinterpret_cast<const u32x4*>(p.aux + (int64_t)(mw + mc) + (int64_t)(nw + nl) * p.aux_ld);
+      u32x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t o0 = bf16_bits(half_of(v[e], 0) * gelu_grad(half_of(z[e], 0)));
+        const uint16_t o1 = bf16_bits(half_of(v[e], 1) * gelu_grad(half_of(z[e], 1)));
+        rs[2 * e] += bf16_float(o0);
+        rs[2 * e + 1] += bf16_float(o1);
+        ov[e] = (uint32_t)o0 | ((uint32_t)o1 << 16);
+      }
+      *reinterpret_cast<u32x4*>(c + at) = ov;
+    }
+  }
+  if constexpr (kSums) {
+    // The four column groups of lanes (lane / 16) in order: 0 + 1, then + (2 + 3).
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      rs[e] += __shfl_xor(rs[e], 16, 64);
+      rs[e] += __shfl_xor(rs[e], 32, 64);
+    }
+    if (cg == 0) {
+      float* part = p.partial + (int64_t)(tn * 2 + wn) * p.m + mw + mc;
+      *reinterpret_cast<f32x4*>(part) = f32x4{rs[0], rs[1], rs[2], rs[3]};
+      *reinterpret_cast<f32x4*>(part + 4) = f32x4{rs[4], rs[5], rs[6], rs[7]};
+    }
+  }
+  if constexpr (EPI == kSquareLoss) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) loss += __shfl_xor(loss, o, 64);
+    if (lane == 0) p.partial[(int64_t)(2 * p.tiles_n) * p.m + blockIdx.x * 4 + wave] = loss;
   }
 }
 
@@ -521,6 +656,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #undef TH_FETCH
   }
 
+  if constexpr (!CHECK && EPI != kStoreF32) {
+    epilogue_lds<EPI>(p, acc);
+    return;
+  }
   // ---- epilogue: lane holds C(m, n) for n = n_j + lane % 32 and
   // m = m_i + 8 g + 4 (lane / 32) + (0..3), register 4 g + (0..3).
   // The epilogue's indices are derived from opaque copies made here, so that
