@@ -179,6 +179,22 @@ __device__ __forceinline__ void row_operand(const uint16_t* base, bf16x8 (&f)[8]
   for (int ks = 0; ks < 8; ++ks) f[ks] = *reinterpret_cast<const bf16x8*>(base + 16 * ks + 8 * (lane / 32));
 }
 
+// ---- workgroup order ---------------------------------------------------------------
+// Workgroups are dealt to the eight XCDs round-robin by linear index.  The
+// logical block is remapped so that each XCD takes a contiguous range of
+// (x fastest, then y, then z): the blocks of one (head, batch) run together
+// on one XCD and stream the same tiles of the other operands through its L2.
+struct Block {
+  int x, y, z;
+};
+__device__ __forceinline__ Block xcd_block() {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int total = gx * gy * gridDim.z;
+  int t = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+  return Block{t % gx, (t / gx) % gy, t / (gx * gy)};
+}
+
 // ---- forward -------------------------------------------------------------------
 // Per workgroup 128 queries (32 per wave), keys in steps of 64.  The loop is
 // pipelined by one step: while the vector ALUs turn the scores of step j into
@@ -234,10 +250,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
   const int nqb = p.seq / kFwdQ;
   // Causal: workgroup x takes query blocks x and nqb - 1 - x, so every
   // workgroup sweeps the same number of key blocks.
-  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  const Block blk = xcd_block();
+  const int npass = (p.causal && 2 * blk.x + 1 != nqb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
-    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int qb = pass == 0 ? blk.x : nqb - 1 - blk.x;
+    const int h = blk.y, b = blk.z;
     const int hk = h / (p.heads / p.kv_heads);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
@@ -543,10 +560,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   const int nkb = p.seq / kBwdK;
   // Causal: workgroup x takes key blocks x and nkb - 1 - x, so every
   // workgroup sweeps the same number of query blocks.
-  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nkb) ? 2 : 1;
+  const Block blk = xcd_block();
+  const int npass = (p.causal && 2 * blk.x + 1 != nkb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
-    const int kbk = pass == 0 ? (int)blockIdx.x : nkb - 1 - (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int kbk = pass == 0 ? blk.x : nkb - 1 - blk.x;
+    const int h = blk.y, b = blk.z;
     const int hk = h / (p.heads / p.kv_heads);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
@@ -731,10 +749,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int nqb = p.seq / kFwdQ;
   // Causal: workgroup x takes query blocks x and nqb - 1 - x (equal work).
-  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  const Block blk = xcd_block();
+  const int npass = (p.causal && 2 * blk.x + 1 != nqb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
-    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int qb = pass == 0 ? blk.x : nqb - 1 - blk.x;
+    const int h = blk.y, b = blk.z;
     const int hk = h / (p.heads / p.kv_heads);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
@@ -828,10 +847,11 @@ constexpr size_t kDqDsLds = 4 * kTileElems * sizeof(uint16_t);  // (K, dS') x 2 
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int nqb = p.seq / kFwdQ;
-  const int npass = (p.causal && 2 * (int)blockIdx.x + 1 != nqb) ? 2 : 1;
+  const Block blk = xcd_block();
+  const int npass = (p.causal && 2 * blk.x + 1 != nqb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
-    const int qb = pass == 0 ? (int)blockIdx.x : nqb - 1 - (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int qb = pass == 0 ? blk.x : nqb - 1 - blk.x;
+    const int h = blk.y, b = blk.z;
     const int hk = h / (p.heads / p.kv_heads);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;

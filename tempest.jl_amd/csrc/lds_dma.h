@@ -1,5 +1,5 @@
-// Direct global -> LDS loads on gfx950, shared by the product and attention
-// kernels.
+// Device helpers shared by the product and attention kernels: direct global
+// -> LDS loads on gfx950 and a compile-time loop.
 //
 // buffer_load_dwordx4 ... lds writes each lane's 16 bytes at M0 + 16 lane, so
 // one wave instruction fills 1 KB of LDS with no staging registers.  It is
@@ -13,8 +13,19 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 namespace th_dev {
+
+template <int... I, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), unrolled.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
 // One 16-byte lane load from global memory (buffer `rsrc`, byte offset
 // voff + soff) straight into LDS at byte m0 + 16 lane.
