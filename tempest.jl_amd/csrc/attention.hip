@@ -63,6 +63,9 @@ struct AttnArgs {
   uint16_t* dk;
   uint16_t* dv;
   uint16_t* ds;          // backward workspace: dS' as bf16 [b][h][key][query], or null
+  // backward workspace: per (b, h) and 64-query block qb, 128 floats: the 64
+  // queries' -lse / scale, then their -delta ([b][h][qb][2][64]).
+  float* stat;
   int64_t q_sh, q_ss, q_sb;  // strides (elements) of q, o, dout, dq along head, position, batch
   int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
   int32_t seq, heads, kv_heads, batch;
@@ -433,7 +436,12 @@ __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
   }
 #pragma unroll
   for (int m = 8; m >= 1; m /= 2) v += __shfl_xor(v, m, 16);
-  if (row < total && part == 0) p.delta[(b * p.seq + s) * p.heads + h] = v;
+  if (row < total && part == 0) {
+    p.delta[(b * p.seq + s) * p.heads + h] = v;
+    const int64_t at = (((int64_t)b * p.heads + h) * (p.seq / 64) + s / 64) * 128 + s % 64;
+    p.stat[at] = p.lse[(b * p.seq + s) * p.heads + h] * (-1.0f / p.scale);
+    p.stat[at + 64] = -v;
+  }
 }
 
 // ---- backward: shared pieces -----------------------------------------------------
@@ -573,8 +581,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 
     const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-    const float* lbase = p.lse + (int64_t)b * p.seq * p.heads + h;
-    const float* dbase = p.delta + (int64_t)b * p.seq * p.heads + h;
+    const int nq = p.seq / kBwdQ;
     // The workgroup's 128 keys of K and V, row-major in LDS for the whole sweep.
     uint16_t* const KT = lds + kKvBlock / sizeof(uint16_t);
     uint16_t* const VT = KT + 2 * kTileElems;
@@ -603,24 +610,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
     auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
 
     const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
-    const int nq = p.seq / kBwdQ;
-    const TileRows rows(p.q_ss);
-    u32x4 rq[4], rg[4];
-    // Threads t and t + 128 both carry entry t % 128 of [-lse / scale | -delta].
-    const int lt = threadIdx.x % 128;
-    const float* lsrc = lt < 64 ? lbase : dbase;
-    const float lmul = lt < 64 ? -1.0f / p.scale : -1.0f;
-    float rl = 0.0f;
-    auto fetch = [&](int qb) {
-      const int64_t at = (int64_t)qb * kBwdQ * p.q_ss;
-      rows.load(qbase + at, rq);
-      rows.load(gbase + at, rg);
-      rl = lsrc[(int64_t)(qb * kBwdQ + lt % 64) * p.heads];
-    };
-    auto land = [&](int s) {
-      store_rows(Qs(s), rq);
-      store_rows(Gs(s), rg);
-      Ls(s)[lt] = rl * lmul;
+    // A query block's Q and dO tiles and statistics go straight from global
+    // memory into a stage: four 1 KB loads per wave for each tile, and one
+    // 256-byte load of statistics by each of waves 0 and 1.
+    const TileDma qt(qbase, p.q_ss), gt(gbase, p.q_ss);
+    const __amdgpu_buffer_rsrc_t srsrc = th_dev::buffer_of(p.stat + ((int64_t)b * p.heads + h) * nq * 128);
+    auto fetch = [&](int qb, int s) {
+      qt.load(qb * kBwdQ, Qs(s));
+      gt.load(qb * kBwdQ, Gs(s));
+      const int w = __builtin_amdgcn_readfirstlane(wave);
+      if (w < 2) th_dev::dma4(srsrc, 4 * lane, qb * 512 + 256 * w, (uint32_t)(uintptr_t)Ls(s) + 256 * w);
     };
     // Accumulator start: register i of row block j holds query 32 j + 8 (i / 4) + 4 lh + i % 4.
     auto start = [&](const float* v, int j) {
@@ -633,12 +632,34 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       }
       return a;
     };
-    fetch(qstart);
-    land(0);
-    __syncthreads();
+    // dS' of a query block, transposed through this wave's LDS scratch (32
+    // key rows) so that it leaves as whole 128-byte lines.  It is written
+    // there at the end of its step and stored during the next one (or after
+    // the sweep), beside that step's products.
+    uint16_t* const scratch = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
+    u32x4 pend[4];
+    auto scratch_read = [&]() {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = lane / 8 + 8 * i, cc = lane % 8;
+        pend[i] = *reinterpret_cast<const u32x4*>(scratch + r * kDsRow + 8 * cc);
+      }
+    };
+    auto store_pending = [&](int qq0) {
+      uint16_t* rows0 = p.ds + (((int64_t)b * p.heads + h) * p.seq + k0) * p.seq + qq0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = lane / 8 + 8 * i, cc = lane % 8;
+        __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + (int64_t)r * p.seq + 8 * cc));
+      }
+    };
+    fetch(qstart, 0);
+    th_dev::wait_and_meet<0>();
     for (int qb = qstart; qb < nq; ++qb) {
       const int st = (qb - qstart) & 1;
-      fetch(min(qb + 1, nq - 1));  // past the end: a harmless reload into the idle stage
+      fetch(min(qb + 1, nq - 1), st ^ 1);  // past the end: a harmless reload into the idle stage
+      if constexpr (kStore)
+        if (qb > qstart) scratch_read();
       const uint16_t *Q = Qs(st), *G = Gs(st);
       const float* L = Ls(st);
       // S~ = Q K' - lse / scale, dP~ = dO V' - delta (64 queries x 32 keys).
@@ -646,6 +667,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       s[0] = start(L, 0), dp[0] = start(L + 64, 0);
       s[1] = start(L, 1), dp[1] = start(L + 64, 1);
       scores_lds(Q, G, 0, KT, VT, wave, s[0], dp[0]);
+      // The previous block's dS' leaves after this step's loads were issued,
+      // so the wait for those loads at the end of the step can leave these
+      // four stores in flight.
+      if constexpr (kStore)
+        if (qb > qstart) store_pending((qb - 1) * kBwdQ);
       // On the diagonal the masked scores become -inf: their P and dS are exactly 0.
       const int qq0 = qb * kBwdQ;
       const bool diagonal = p.causal && qq0 < k0 + 32;
@@ -671,26 +697,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
       grads_half(G, Q, 2, pf, sf, dv, dk);
       if constexpr (kStore) {
-        // dS' rows [key][qq0 .. qq0 + 63], transposed through this wave's LDS
-        // scratch (32 key rows) so they leave as whole 128-byte lines.
         // sf[ks] element e is query 16 ks + 8 (e / 4) + 4 lh + e % 4 of this lane's key.
-        uint16_t* w = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const u32x4 x = __builtin_bit_cast(u32x4, sf[ks]);
-          *reinterpret_cast<u32x2*>(w + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
-          *reinterpret_cast<u32x2*>(w + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
-        }
-        uint16_t* rows0 = p.ds + (((int64_t)b * p.heads + h) * p.seq + k0) * p.seq + qq0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = lane / 8 + 8 * i, cc = lane % 8;
-          *reinterpret_cast<u32x4*>(rows0 + (int64_t)r * p.seq + 8 * cc) =
-              *reinterpret_cast<const u32x4*>(w + r * kDsRow + 8 * cc);
+          *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
+          *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
         }
       }
-      land(st ^ 1);
-      __syncthreads();
+      // The next stage has landed.  Past the first step the four stores
+      // issued after its loads may still be in flight.
+      if (kStore && qb > qstart) th_dev::wait_and_meet<4>();
+      else th_dev::wait_and_meet<0>();
+    }
+    if constexpr (kStore) {
+      scratch_read();
+      store_pending((nq - 1) * kBwdQ);
     }
     // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
     const int64_t out = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
@@ -988,11 +1010,17 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   if (int r = check_desc(d, true)) return r;
   AttnArgs a = args_of(d);
   th::Builder b("attention_bwd", 9);
+  // The dK/dV sweep loads Q and dO tiles directly into LDS with 32-bit byte
+  // offsets from a (batch, head) base.
+  TH_REQUIRE((double)d->seq * d->q_strides[1] * 2 < 2147483648.0,
+             "attention: a sequence of Q or dO must span under 2 GiB (seq x position stride x 2 bytes)");
   void* delta = nullptr;
   const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
-  if (int r = th::device_alloc((size_t)rows * sizeof(float), &delta)) return r;
+  // delta ([b][s][h]), then the per-block statistics (2 floats per row).
+  if (int r = th::device_alloc((size_t)rows * 3 * sizeof(float), &delta)) return r;
   b.own(delta);
   a.delta = static_cast<float*>(delta);
+  a.stat = a.delta + rows;
   // dS' is stored for the dQ sweep when it fits the workspace budget
   // (4 GiB at B8 H16 S4096); beyond it dQ recomputes S and dP instead.
   const double ds_bytes = 2.0 * d->batch * d->heads * (double)d->seq * d->seq;
