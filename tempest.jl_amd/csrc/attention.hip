@@ -478,24 +478,20 @@ __device__ __forceinline__ void scores_half(const uint16_t* x, const uint16_t* y
   }
 }
 
-// The same with the B operands from LDS too: rows 32 w .. 32 w + 31 of the
-// row-major tiles bx, by (w the wave), read with the A fragments two slices
-// ahead.
-__device__ __forceinline__ void scores_lds(const uint16_t* x, const uint16_t* y, int j, const uint16_t* bx,
-                                           const uint16_t* by, int w, f32x16& s, f32x16& t) {
-  bf16x8 f[3][4];
-  auto read = [&](int ks, int r) {
-    f[r][0] = frag_rows(x, 32 * j, ks), f[r][1] = frag_rows(y, 32 * j, ks);
-    f[r][2] = frag_rows(bx, 32 * w, ks), f[r][3] = frag_rows(by, 32 * w, ks);
-  };
+// The same with the A fragments read two slices ahead and the B operands
+// (the wave's own keys of K and V) held in registers for the whole sweep.
+__device__ __forceinline__ void scores_kv(const uint16_t* x, const uint16_t* y, int j, const bf16x8 (&kf)[8],
+                                          const bf16x8 (&vf)[8], f32x16& s, f32x16& t) {
+  bf16x8 f[3][2];
+  auto read = [&](int ks, int r) { f[r][0] = frag_rows(x, 32 * j, ks), f[r][1] = frag_rows(y, 32 * j, ks); };
   read(0, 0);
   read(1, 1);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     if (ks + 2 < 8) read(ks + 2, (ks + 2) % 3);
     __builtin_amdgcn_sched_barrier(kFence);
-    s = mfma(f[ks % 3][0], f[ks % 3][2], s);
-    t = mfma(f[ks % 3][1], f[ks % 3][3], t);
+    s = mfma(f[ks % 3][0], kf[ks], s);
+    t = mfma(f[ks % 3][1], vf[ks], t);
     __builtin_amdgcn_sched_barrier(kFence);
   }
 }
@@ -510,10 +506,10 @@ __device__ __forceinline__ void scores_lds(const uint16_t* x, const uint16_t* y,
 constexpr int kBwdK = 128;  // keys per workgroup
 constexpr int kBwdQ = 64;   // queries per step
 constexpr size_t kStageBwd = 2 * kTileElems * sizeof(uint16_t) + 2 * 64 * sizeof(float);
-constexpr int kDsRow = 72;  // LDS row (bf16) of a wave's dS' transpose scratch: 64 queries + 8
-constexpr size_t kDsScratch = 2 * kStageBwd;                          // 4 waves x 32 rows of kDsRow
-constexpr size_t kKvBlock = kDsScratch + 4 * 32 * kDsRow * sizeof(uint16_t);  // K, V of the 128 keys
-constexpr size_t kDkdvLds = kKvBlock + 2 * 2 * kTileElems * sizeof(uint16_t);
+constexpr int kBwdStages = 3;  // query blocks in LDS: one read, two loading
+constexpr int kDsRow = 72;     // LDS row (bf16) of a wave's dS' transpose scratch: 64 queries + 8
+constexpr size_t kDsScratch = kBwdStages * kStageBwd;  // 4 waves x 32 rows of kDsRow
+constexpr size_t kDkdvLds = kDsScratch + 4 * 32 * kDsRow * sizeof(uint16_t);
 
 // The gradient products of slices ks0, ks0 + 1 (rows 16 ks0 .. 16 ks0 + 31):
 // dv += dO' P, dk += Q' dS, fragments read half a slice ahead.
@@ -582,21 +578,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
     const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const int nq = p.seq / kBwdQ;
-    // The workgroup's 128 keys of K and V, row-major in LDS for the whole sweep.
-    uint16_t* const KT = lds + kKvBlock / sizeof(uint16_t);
-    uint16_t* const VT = KT + 2 * kTileElems;
+    // This wave's 32 keys of K and V as the B operands of the score products,
+    // in registers for the whole sweep.
+    bf16x8 kf[8], vf[8];
     {
-      const TileRows krows(p.k_ss);
-      const uint16_t* kb0 = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)kbk * kBwdK * p.k_ss;
-      const uint16_t* vb0 = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)kbk * kBwdK * p.k_ss;
-      u32x4 r[4];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        krows.load(kb0 + (int64_t)half * 64 * p.k_ss, r);
-        store_rows(KT + half * kTileElems, r);
-        krows.load(vb0 + (int64_t)half * 64 * p.k_ss, r);
-        store_rows(VT + half * kTileElems, r);
-      }
+      const int64_t at = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
+      row_operand(p.k + at, kf);
+      row_operand(p.v + at, vf);
     }
 
     f32x16 dk[4], dv[4];
@@ -611,15 +599,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
 
     const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
     // A query block's Q and dO tiles and statistics go straight from global
-    // memory into a stage: four 1 KB loads per wave for each tile, and one
-    // 256-byte load of statistics by each of waves 0 and 1.
+    // memory into a stage, two blocks ahead: four 1 KB loads per wave for
+    // each tile, and one 256-byte load of statistics per wave (waves w and
+    // w + 2 fetch the same half, so every wave issues the same nine loads).
     const TileDma qt(qbase, p.q_ss), gt(gbase, p.q_ss);
     const __amdgpu_buffer_rsrc_t srsrc = th_dev::buffer_of(p.stat + ((int64_t)b * p.heads + h) * nq * 128);
     auto fetch = [&](int qb, int s) {
       qt.load(qb * kBwdQ, Qs(s));
       gt.load(qb * kBwdQ, Gs(s));
-      const int w = __builtin_amdgcn_readfirstlane(wave);
-      if (w < 2) th_dev::dma4(srsrc, 4 * lane, qb * 512 + 256 * w, (uint32_t)(uintptr_t)Ls(s) + 256 * w);
+      const int half = __builtin_amdgcn_readfirstlane(wave) % 2;
+      th_dev::dma4(srsrc, 4 * lane, qb * 512 + 256 * half, (uint32_t)(uintptr_t)Ls(s) + 256 * half);
     };
     // Accumulator start: register i of row block j holds query 32 j + 8 (i / 4) + 4 lh + i % 4.
     auto start = [&](const float* v, int j) {
@@ -653,11 +642,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
         __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + (int64_t)r * p.seq + 8 * cc));
       }
     };
+    // Blocks past the end are a harmless reload of the last one into an idle stage.
     fetch(qstart, 0);
-    th_dev::wait_and_meet<0>();
+    fetch(min(qstart + 1, nq - 1), 1);
+    th_dev::wait_and_meet<9>();
+    int st = 0;  // the stage of block qb
     for (int qb = qstart; qb < nq; ++qb) {
-      const int st = (qb - qstart) & 1;
-      fetch(min(qb + 1, nq - 1), st ^ 1);  // past the end: a harmless reload into the idle stage
+      const int s2 = st >= kBwdStages - 2 ? st + 2 - kBwdStages : st + 2;
+      fetch(min(qb + 2, nq - 1), s2);
       if constexpr (kStore)
         if (qb > qstart) scratch_read();
       const uint16_t *Q = Qs(st), *G = Gs(st);
@@ -666,7 +658,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       f32x16 s[2], dp[2];
       s[0] = start(L, 0), dp[0] = start(L + 64, 0);
       s[1] = start(L, 1), dp[1] = start(L + 64, 1);
-      scores_lds(Q, G, 0, KT, VT, wave, s[0], dp[0]);
+      scores_kv(Q, G, 0, kf, vf, s[0], dp[0]);
       // The previous block's dS' leaves after this step's loads were issued,
       // so the wait for those loads at the end of the step can leave these
       // four stores in flight.
@@ -682,7 +674,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
           if (8 * (i / 4) + i % 4 < lim) s[0][i] = -INFINITY;
       }
       bf16x8 pf[4], sf[4];
-      scores_lds(Q, G, 1, KT, VT, wave, s[1], dp[1]);
+      scores_kv(Q, G, 1, kf, vf, s[1], dp[1]);
       weights_rows(s[0], dp[0], c, pf[0], pf[1], sf[0], sf[1]);
       // Keep these weights here, beside the products above, rather than sunk
       // past the branch below into the next phase.
@@ -705,11 +697,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
           *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
         }
       }
-      // The next stage has landed.  Past the first step the four stores
-      // issued after its loads may still be in flight.
-      if (kStore && qb > qstart) th_dev::wait_and_meet<4>();
-      else th_dev::wait_and_meet<0>();
+      // Wait for block qb + 1's stage.  After its nine loads this wave has
+      // issued the previous step's four stores (past its first step), this
+      // step's nine loads, and this step's four stores (past the first).
+      if (!kStore || qb == qstart) th_dev::wait_and_meet<9>();
+      else if (qb == qstart + 1) th_dev::wait_and_meet<13>();
+      else th_dev::wait_and_meet<17>();
+      st = st == kBwdStages - 1 ? 0 : st + 1;
     }
+    // No load may land in this workgroup's LDS after the sweep.
+    th_dev::wait_and_meet<0>();
     if constexpr (kStore) {
       scratch_read();
       store_pending((nq - 1) * kBwdQ);
