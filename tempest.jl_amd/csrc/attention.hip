@@ -62,7 +62,9 @@ struct AttnArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  uint16_t* ds;          // backward workspace: dS' as bf16 [b][h][key][query], or null
+  // backward workspace: dS' as bf16 in contiguous 16 KB tiles, [b][h][query
+  // block of 128][key block of 64][key][query] (64 x 128 per tile), or null.
+  uint16_t* ds;
   // backward workspace: per (b, h) and 64-query block qb, 128 floats: the 64
   // queries' -lse / scale, then their -delta ([b][h][qb][2][64]).
   float* stat;
@@ -634,12 +636,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
         pend[i] = *reinterpret_cast<const u32x4*>(scratch + r * kDsRow + 8 * cc);
       }
     };
+    // This wave's 32 keys are rows 32 (wave % 2) .. + 31 of key block k0 / 64;
+    // queries qq0 .. qq0 + 63 are one half of the rows of query block qq0 / 128.
     auto store_pending = [&](int qq0) {
-      uint16_t* rows0 = p.ds + (((int64_t)b * p.heads + h) * p.seq + k0) * p.seq + qq0;
+      uint16_t* rows0 = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq +
+                        ((int64_t)(qq0 / 128) * (p.seq / 64) + k0 / 64) * (64 * 128) + (k0 % 64) * 128 + qq0 % 128;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = lane / 8 + 8 * i, cc = lane % 8;
-        __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + (int64_t)r * p.seq + 8 * cc));
+        __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + r * 128 + 8 * cc));
       }
     };
     // Blocks past the end are a harmless reload of the last one into an idle stage.
@@ -859,9 +864,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
 // dQ' (128 d x 128 queries per workgroup) += K' dS' over key blocks of 64,
 // both operands read transposed from row-major LDS tiles: K [key][d] and
 // dS' [key][query] (the dK/dV kernel wrote every entry this sweep reads;
-// masked ones are 0).  One product per step instead of three, no exp.
+// masked ones are 0).  One product per step instead of three, no exp.  Its
+// operands all come through transposed LDS reads, whose throughput grows
+// with the reads in flight per CU (a wave keeps at most ~15): so two
+// workgroups per CU, each wave reading a block's twenty fragments at once,
+// and loads (direct global->LDS) one block ahead in a ring of two stages.
 
-constexpr size_t kDqDsLds = 4 * kTileElems * sizeof(uint16_t);  // (K, dS') x 2 stages
+constexpr int kDqStages = 2;
+constexpr size_t kDqDsLds = 2 * kDqStages * kTileElems * sizeof(uint16_t);  // (K, dS') per stage
 
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -875,36 +885,46 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
     const int qw = qb * kFwdQ;  // the workgroup's first query
-    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-    const uint16_t* dbase = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + qw;
-    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;
-    const TileRows krows(p.k_ss), drows(p.seq);
+    const TileDma kt(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
+    // The query block's dS' tiles, one 16 KB tile (64 keys x 128 queries) per key block.
+    const TileDma dt(p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + (int64_t)qb * (p.seq / 64) * (64 * 128), 128);
+    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;  // even, >= 2
     auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
     auto Ds = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
+    // Key block kb into stage kb % kDqStages (blocks past the end: a harmless
+    // reload of the last one into an idle stage).  Eight loads per wave.
+    auto fetch = [&](int kb) {
+      const int s = kb % kDqStages, at = min(kb, nkb - 1) * kFwdK;
+      kt.load(at, Ks(s));
+      dt.load(at, Ds(s));
+    };
     f32x16 dq[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
-    u32x4 rk[4], rd[4];
-    krows.load(kbase, rk);
-    drows.load(dbase, rd);
-    store_rows(Ks(0), rk);
-    store_rows(Ds(0), rd);
-    __syncthreads();
+    fetch(0);
+    th_dev::wait_and_meet<0>();
     for (int kb = 0; kb < nkb; ++kb) {
-      const int st = kb & 1;
-      const int nx = min(kb + 1, nkb - 1);  // past the end: a harmless reload
-      krows.load(kbase + (int64_t)nx * kFwdK * p.k_ss, rk);
-      drows.load(dbase + (int64_t)nx * kFwdK * p.seq, rd);
+      fetch(kb + 1);  // into the stage block kb - 1 used
+      const int st = kb % kDqStages;
+      // All twenty fragments of the block first (one wave per SIMD: nothing
+      // else would hide an LDS round trip per product), then the products.
+      bf16x8 bs[4], kf[4][4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 bs = frag_tr(Ds(st), 32 * wave, ks);
+        bs[ks] = frag_tr(Ds(st), 32 * wave, ks);
 #pragma unroll
-        for (int db = 0; db < 4; ++db) dq[db] = mfma(frag_tr(Ks(st), 32 * db, ks), bs, dq[db]);
+        for (int db = 0; db < 4; ++db) kf[ks][db] = frag_tr(Ks(st), 32 * db, ks);
       }
-      store_rows(Ks(st ^ 1), rk);
-      store_rows(Ds(st ^ 1), rd);
-      __syncthreads();
+      __builtin_amdgcn_sched_barrier(kFence);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dq[db] = mfma(kf[ks][db], bs[ks], dq[db]);
+      // Block kb + 1 has landed.
+      th_dev::wait_and_meet<0>();
     }
+    // No load may land in this workgroup's LDS after the sweep.
+    th_dev::wait_and_meet<0>();
     uint16_t* out = p.dq + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(qw + 32 * wave + lr) * p.q_ss;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
