@@ -288,16 +288,18 @@ __device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* s
   }
 }
 
-constexpr size_t kPrepLds = 2 * kC * kLdH * sizeof(uint16_t) + (3 * kC * kLdC + 2 * kC) * sizeof(float);
+// Under 80 KB, so two workgroups share a CU (one's substitution beside the
+// other's loads and products).
+constexpr size_t kPrepLds = 2 * kC * kLdH * sizeof(uint16_t) + (2 * kC * kLdC + 2 * kC) * sizeof(float);
 
-__global__ __launch_bounds__(256) void dn_chunk_prep(DnArgs p) {
+__global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
   extern __shared__ float lds[];
   uint16_t* Kh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
   uint16_t* Vh = Kh + kC * kLdH;                          // [64][kLdH]
-  float* AT = reinterpret_cast<float*>(Vh + kC * kLdH);   // [64][kLdC]: A, then T
+  float* AT = reinterpret_cast<float*>(Vh + kC * kLdH);   // [64][kLdC]: A, then T, then T diag(beta)
   float* TX = AT + kC * kLdC;     // [64][kLdC]: T diag(beta e^ca)
-  float* TY = TX + kC * kLdC;     // [64][kLdC]: T diag(beta)
-  float* ca = TY + kC * kLdC;     // [64]
+  float* TY = AT;                 // each entry rewritten by the thread that read it
+  float* ca = TX + kC * kLdC;     // [64]
   float* be = ca + kC;            // [64]
   const Chunk ck = chunk_of(p, blockIdx.x);
   const int t = threadIdx.x, w = t / 64;
