@@ -506,23 +506,23 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
 // P = lower(Gamma o Q K'), O = diag(e^ca) Q S + P U; the products on the
 // matrix cores in fp32, Q and K in LDS as bf16.
 
-constexpr size_t kOutLds = 2 * kC * kLdH * sizeof(uint16_t) + (kD * kLd + kC * kLd + kC * kLdC + kC) * sizeof(float);
+// S and U are read by columns straight from memory (each wave's 32 columns
+// once), so only Q, K and P live in LDS and several workgroups share a CU.
+constexpr size_t kOutLds = 2 * kC * kLdH * sizeof(uint16_t) + (kC * kLdC + kC) * sizeof(float);
 
-__global__ __launch_bounds__(256, 1) void dn_output(DnArgs p) {
+__global__ __launch_bounds__(256, 2) void dn_output(DnArgs p) {
   extern __shared__ float lds[];
   uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
   uint16_t* Kh = Qh + kC * kLdH;                          // [64][kLdH]
-  float* S = reinterpret_cast<float*>(Kh + kC * kLdH);    // [128][kLd]
-  float* U = S + kD * kLd;        // [64][kLd]
-  float* P = U + kC * kLd;        // [64][kLdC]
+  float* P = reinterpret_cast<float*>(Kh + kC * kLdH);    // [64][kLdC]
   float* ca = P + kC * kLdC;      // [64]
   const Chunk ck = chunk_of(p, blockIdx.x);
   const int t = threadIdx.x, w = t / 64;
   const int r = t % 16, g = (t % 64) / 16;
+  const float* S = p.S + ck.c * kD * kD;  // [128][128]
+  const float* U = p.U + ck.c * kC * kD;  // [64][128]
   stage_rows_bf16(Qh, p.q + ck.row0, p.s_t);
   stage_rows_bf16(Kh, p.k + ck.row0, p.s_t);
-  stage_f32(S, p.S + ck.c * kD * kD, kD);
-  stage_f32(U, p.U + ck.c * kC * kD, kC);
   if (t < 64) ca[t] = p.ca[ck.c * kC + t];
   __syncthreads();
   const RowBf16 Qr{Qh, kLdH};
@@ -547,8 +547,8 @@ __global__ __launch_bounds__(256, 1) void dn_output(DnArgs p) {
     f32x4v qs[4][2], pu[4][2];
     clear(qs);
     clear(pu);
-    mm_by(qs, Qr, 0, ColF32{S, kLd}, 32 * w, kD);
-    mm_by(pu, RowF32{P, kLdC}, 0, ColF32{U, kLd}, 32 * w, kC);
+    mm_by(qs, Qr, 0, ColF32{S, kD}, 32 * w, kD);
+    mm_by(pu, RowF32{P, kLdC}, 0, ColF32{U, kD}, 32 * w, kC);
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
