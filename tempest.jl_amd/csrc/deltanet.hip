@@ -735,39 +735,63 @@ __global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
 // and S, then U and dSn (dO stays).  Wave w computes columns 32 w .. 32 w + 31
 // of the 64 x 128 results and row block w of dP.
 
-constexpr size_t kGaLds = (2 * kC + kD) * kLd * sizeof(float) + 4 * sizeof(float);
+// S and dSn are read by rows straight from memory (each wave's 32 rows, for
+// both products that use them at once), so only dO and one 64-row operand
+// live in LDS and two workgroups share a CU.
+constexpr size_t kGaLds = 2 * kC * kLd * sizeof(float) + 4 * sizeof(float);
 
-__global__ __launch_bounds__(256, 1) void dn_grad_a(DnArgs p) {
+// acc1 += X1 Y', acc2 += X2 Y' over k in [0, K): X1, X2 rows i0 .. of LDS
+// (stride kLd), Y rows j0 + 16 bj .. of memory (stride kD), each Y quad read once.
+template <int BI, int BJ>
+__device__ __forceinline__ void mm_nt2(f32x4v (&acc1)[BI][BJ], const float* X1, f32x4v (&acc2)[BI][BJ], const float* X2,
+                                       int i0, const float* Y, int j0, int K) {
+  const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
+  for (int kb = 0; kb < K; kb += 16) {
+    f32x4v a1[BI], a2[BI], b[BJ];
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) b[bj] = quad(Y + (j0 + 16 * bj + r) * kD + kb + 4 * g);
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi) {
+      a1[bi] = quad(X1 + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
+      a2[bi] = quad(X2 + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
+    }
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < BJ; ++bj) {
+        acc1[bi][bj] = mma4(a1[bi], b[bj], acc1[bi][bj]);
+        acc2[bi][bj] = mma4(a2[bi], b[bj], acc2[bi][bj]);
+      }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
   extern __shared__ float lds[];
   float* dO = lds;              // [64][kLd]
   float* X = dO + kC * kLd;     // [64][kLd]: dU, then U
-  float* Y = X + kC * kLd;      // [128][kLd]: S, then dSn
-  float* red = Y + kD * kLd;    // [4]
+  float* red = X + kC * kLd;    // [4]
   const Chunk ck = chunk_of(p, blockIdx.x);
   const int t = threadIdx.x, w = t / 64;
   const float* Sc = p.S + ck.c * kD * kD;
   const float* dSc = p.dSn + ck.c * kD * kD;
   stage_bf16(dO, p.dout + ck.row0, p.s_t);
   stage_f32(X, p.dU + ck.c * kC * kD, kC);
-  stage_f32(Y, Sc, kD);
   __syncthreads();
   {
     f32x4v q[4][2], wq[4][2];
     clear(q);
     clear(wq);
-    mm_nt(q, dO, 0, Y, 32 * w, kD);
-    mm_nt(wq, X, 0, Y, 32 * w, kD);
+    mm_nt2(q, dO, wq, X, 0, Sc, 32 * w, kD);
     store_blocks(p.dQg + ck.c * kC * kD, kD, q, 0, 32 * w, 1.0f);
     store_blocks(p.dW + ck.c * kC * kD, kD, wq, 0, 32 * w, -1.0f);
   }
   __syncthreads();
   stage_f32(X, p.U + ck.c * kC * kD, kC);
-  stage_f32(Y, dSc, kD);
   __syncthreads();
   {
     f32x4v kd[4][2];
     clear(kd);
-    mm_nt(kd, X, 0, Y, 32 * w, kD);
+    mm_by(kd, RowF32{X, kLd}, 0, RowF32{dSc, kD}, 32 * w, kD);
     store_blocks(p.dKd + ck.c * kC * kD, kD, kd, 0, 32 * w, 1.0f);
   }
   {
@@ -785,16 +809,16 @@ __global__ __launch_bounds__(256, 1) void dn_grad_a(DnArgs p) {
       }
     }
   }
-  // dg = <S, dSn>: S from global, dSn from LDS, a fixed tree.
+  // dg = <S, dSn>, both from memory, a fixed tree.
   float sum = 0.0f;
   for (int e = t; e < kD * kD / 4; e += 256) {
     const int r = e / 32, c = 4 * (e % 32);
     const float4 sv = *reinterpret_cast<const float4*>(Sc + r * kD + c);
-    const f32x4v dv = quad(Y + r * kLd + c);
-    sum = fmaf(sv.x, dv[0], sum);
-    sum = fmaf(sv.y, dv[1], sum);
-    sum = fmaf(sv.z, dv[2], sum);
-    sum = fmaf(sv.w, dv[3], sum);
+    const float4 dv = *reinterpret_cast<const float4*>(dSc + r * kD + c);
+    sum = fmaf(sv.x, dv.x, sum);
+    sum = fmaf(sv.y, dv.y, sum);
+    sum = fmaf(sv.z, dv.z, sum);
+    sum = fmaf(sv.w, dv.w, sum);
   }
   sum = thd::wave_sum(sum);
   if (t % 64 == 0) red[t / 64] = sum;
