@@ -835,19 +835,36 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
 // 64 x 128 work, whose partials go to LDS by wave) and are folded in a fixed
 // order, so the result does not depend on timing.
 
-constexpr size_t kGbLds = 2 * kC * kLdH * sizeof(uint16_t) + (kC * kLd + 4 * kC * kLdC) * sizeof(float) +
+// dW, dU~ and T are read straight from memory by the products that use them,
+// and dQK = dP o Gamma (lower) is formed as its operands are read, so LDS
+// holds Q, K, M and N only and two workgroups share a CU.
+constexpr size_t kGbLds = 2 * kC * kLdH * sizeof(uint16_t) + 2 * kC * kLdC * sizeof(float) +
                           (2 * kC + 5 * 4 * kC + 2 * kC) * sizeof(float);
 
-__global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
+// dQK(i, j) = dP(i, j) e^(ca_i - ca_j) for i >= j, 0 above: along its rows
+// (quad(i, j) = dQK(i, j .. j + 3)) or, when kT, along its columns.
+template <bool kT>
+struct DqkReader {
+  const float* dP;  // [64][64] in memory
+  const float* ca;  // [64] in LDS
+  __device__ f32x4v quad(int x, int k) const {
+    f32x4v v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = kT ? k + e : x, j = kT ? x : k + e;
+      v[e] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
+    }
+    return v;
+  }
+};
+
+__global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   extern __shared__ float lds[];
   uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
   uint16_t* Kh = Qh + kC * kLdH;                          // [64][kLdH]
-  float* A0 = reinterpret_cast<float*>(Kh + kC * kLdH);   // [64][kLd]: dW, then dU~
-  float* T = A0 + kC * kLd;        // [64][kLdC]
-  float* M = T + kC * kLdC;        // [64][kLdC]: dT, then dA, then dG + dG'
+  float* M = reinterpret_cast<float*>(Kh + kC * kLdH);   // [64][kLdC]: dT, then dA, then dG + dG'
   float* N = M + kC * kLdC;        // [64][kLdC]: T' dT, then dG
-  float* R = N + kC * kLdC;        // [64][kLdC]: dQK = dP o Gamma, lower
-  float* wrow = R + kC * kLdC;     // [64]: sum_j w_ij
+  float* wrow = N + kC * kLdC;     // [64]: sum_j w_ij
   float* brow = wrow + kC;         // [64]: sum_j dA Gamma G
   float* wcol = brow + kC;         // [4][64]: sum_i w_ij by wave
   float* kx = wcol + 4 * kC;       // [4][64]: k . dX by wave (columns)
@@ -867,17 +884,12 @@ __global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
     *reinterpret_cast<uint4*>(Qh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(qg + row * p.s_t + c8);
     *reinterpret_cast<uint4*>(Kh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(kg + row * p.s_t + c8);
   }
-  const float* Tc = p.T + ck.c * kC * kC;
-  for (int e = t; e < kC * kC / 4; e += 256) {
-    const int row = e / 16, c = 4 * (e % 16);
-    *reinterpret_cast<f32x4v*>(T + row * kLdC + c) = *reinterpret_cast<const f32x4v*>(Tc + row * kC + c);
-  }
+  const float* Tc = p.T + ck.c * kC * kC;  // [64][64]
   const float* dW = p.dW + ck.c * kC * kD;
   const float* dUt = p.dU + ck.c * kC * kD;
   const float* dQg = p.dQg + ck.c * kC * kD;
   const float* dKd = p.dKd + ck.c * kC * kD;
   const float* dP = p.dP + ck.c * kC * kC;
-  stage_f32(A0, dW, kC);
   if (t < 64) {
     ca[t] = p.ca[ck.c * kC + t];
     be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
@@ -892,11 +904,8 @@ __global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
     f32x4v xk[1][4], yv[1][4];
     clear(xk);
     clear(yv);
-    mm_by(xk, RowF32{A0, kLd}, i0, Kr, 0, kD);
-    __syncthreads();  // every wave is done with dW
-    stage_f32(A0, dUt, kC);
-    __syncthreads();
-    mm_by(yv, RowF32{A0, kLd}, i0, RowBf16{vg, p.s_t}, 0, kD);
+    mm_by(xk, RowF32{dW, kD}, i0, Kr, 0, kD);
+    mm_by(yv, RowF32{dUt, kD}, i0, RowBf16{vg, p.s_t}, 0, kD);
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
@@ -910,26 +919,25 @@ __global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
   {
     f32x4v acc[1][4];
     clear(acc);
-    mm_by(acc, ColF32{T, kLdC}, i0, ColF32{M, kLdC}, 0, kC);
+    mm_by(acc, ColF32{Tc, kC}, i0, ColF32{M, kLdC}, 0, kC);
     store_blocks(N, kLdC, acc, i0, 0, 1.0f);
   }
   __syncthreads();
-  // dA = -(N T') o strict lower (into M);  dQK = dP o Gamma, lower (into R).
+  // dA = -(N T') o strict lower (into M).
   {
     f32x4v acc[1][4];
     clear(acc);
-    mm_by(acc, RowF32{N, kLdC}, i0, RowF32{T, kLdC}, 0, kC);
+    mm_by(acc, RowF32{N, kLdC}, i0, RowF32{Tc, kC}, 0, kC);
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = i0 + 4 * g + v, j = 16 * bj + r;
         M[i * kLdC + j] = i > j ? -acc[0][bj][v] : 0.0f;
-        R[i * kLdC + j] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
       }
   }
-  // Every row of this wave's M and R was written by this wave; the other
-  // waves' rows are not read before the next barrier.
+  // Every row of this wave's M was written by this wave; the other waves'
+  // rows are not read before the next barrier.
   // With G = K K', QK = Q K', Gamma: dG = dA o beta_i o Gamma (into N);
   // dbeta_i gets sum_j dA Gamma G; w = (dA beta_i G + dP QK) o Gamma gives
   // dca_i += sum_j w_ij - sum_j w_ji.
@@ -989,54 +997,84 @@ __global__ __launch_bounds__(256, 1) void dn_grad_b(DnArgs p) {
     M[i * kLdC + j] = N[i * kLdC + j] + N[j * kLdC + i];
   }
   __syncthreads();
-  // dQ = e^ca dQg + dQK K;  dK = dQK' Q + (dG + dG') K + beta e^ca dX + e^(last - ca) dKd;
-  // dX = T' dW;  dV = beta T' dU~.  Wave w: columns 32 w .. 32 w + 31.
+  // dQ = e^ca dQg + dQK K;  dV = beta T' dU~;  dK = dQK' Q + (dG + dG') K +
+  // beta e^ca dX + e^(last - ca) dKd with dX = T' dW.  Wave w: columns
+  // 32 w .. 32 w + 31, one output at a time (two accumulator sets live).
   {
     const int d0 = 32 * w;
-    f32x4v dq[4][2], dk[4][2], dx[4][2], dy[4][2];
-    clear(dq);
-    clear(dk);
-    clear(dx);
-    clear(dy);
-    mm_by(dy, ColF32{T, kLdC}, 0, ColF32{A0, kLd}, d0, kC);  // A0 holds dU~
-    mm_by(dq, RowF32{R, kLdC}, 0, Kc, d0, kC);
-    mm_by(dk, ColF32{R, kLdC}, 0, Qc, d0, kC);
-    mm_by(dk, RowF32{M, kLdC}, 0, Kc, d0, kC);
-    __syncthreads();  // every wave is done with dU~
-    stage_f32(A0, dW, kC);
-    __syncthreads();
-    mm_by(dx, ColF32{T, kLdC}, 0, ColF32{A0, kLd}, d0, kC);
+    const DqkReader<false> Rr{dP, ca};
+    const DqkReader<true> Rc{dP, ca};
+    {
+      f32x4v dq[4][2];
+      clear(dq);
+      mm_by(dq, Rr, 0, Kc, d0, kC);
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+      for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int i = 16 * bi + 4 * g + v;
-        const float e = expf(ca[i]), ed = expf(last - ca[i]);
-        float skx = 0.0f, svy = 0.0f, sqq = 0.0f, skk = 0.0f;
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * bi + 4 * g + v;
+          const float e = expf(ca[i]);
+          float sq = 0.0f;
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-          const int d = d0 + 16 * bj + r;
-          const float gq = dQg[i * kD + d], gk = dKd[i * kD + d];
-          const float kv = bf(Kh[i * kLdH + d]), qv = bf(Qh[i * kLdH + d]), vv = bf(vg[(int64_t)i * p.s_t + d]);
-          const float xv = dx[bi][bj][v], yv = dy[bi][bj][v];
-          const float oq = e * gq + dq[bi][bj][v];
-          const float ok = dk[bi][bj][v] + be[i] * e * xv + ed * gk;
-          const float ov = be[i] * yv;
-          skx = fmaf(kv, xv, skx);
-          svy = fmaf(vv, yv, svy);
-          sqq = fmaf(qv, gq, sqq);
-          skk = fmaf(kv, gk, skk);
-          const int64_t at = ck.row0 + (int64_t)i * p.s_t + d;
-          p.dq[at] = to_bf(oq);
-          p.dk[at] = to_bf(ok);
-          p.dv[at] = to_bf(ov);
+          for (int bj = 0; bj < 2; ++bj) {
+            const int d = d0 + 16 * bj + r;
+            const float gq = dQg[i * kD + d], qv = bf(Qh[i * kLdH + d]);
+            sq = fmaf(qv, gq, sq);
+            p.dq[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(e * gq + dq[bi][bj][v]);
+          }
+          sq = row_group_sum(sq);
+          if (r == 0) qq[w * kC + i] = sq;
         }
-        skx = row_group_sum(skx);
-        svy = row_group_sum(svy);
-        sqq = row_group_sum(sqq);
-        skk = row_group_sum(skk);
-        if (r == 0) kx[w * kC + i] = skx, vy[w * kC + i] = svy, qq[w * kC + i] = sqq, kk[w * kC + i] = skk;
-      }
+    }
+    {
+      f32x4v dy[4][2];
+      clear(dy);
+      mm_by(dy, ColF32{Tc, kC}, 0, ColF32{dUt, kD}, d0, kC);
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * bi + 4 * g + v;
+          float sv = 0.0f;
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj) {
+            const int d = d0 + 16 * bj + r;
+            const float vv = bf(vg[(int64_t)i * p.s_t + d]), yv = dy[bi][bj][v];
+            sv = fmaf(vv, yv, sv);
+            p.dv[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(be[i] * yv);
+          }
+          sv = row_group_sum(sv);
+          if (r == 0) vy[w * kC + i] = sv;
+        }
+    }
+    {
+      f32x4v dk[4][2], dx[4][2];
+      clear(dk);
+      clear(dx);
+      mm_by(dk, Rc, 0, Qc, d0, kC);
+      mm_by(dk, RowF32{M, kLdC}, 0, Kc, d0, kC);
+      mm_by(dx, ColF32{Tc, kC}, 0, ColF32{dW, kD}, d0, kC);
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * bi + 4 * g + v;
+          const float e = expf(ca[i]), ed = expf(last - ca[i]);
+          float sx = 0.0f, sk = 0.0f;
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj) {
+            const int d = d0 + 16 * bj + r;
+            const float gk = dKd[i * kD + d], kv = bf(Kh[i * kLdH + d]);
+            const float xv = dx[bi][bj][v];
+            sx = fmaf(kv, xv, sx);
+            sk = fmaf(kv, gk, sk);
+            p.dk[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(dk[bi][bj][v] + be[i] * e * xv + ed * gk);
+          }
+          sx = row_group_sum(sx);
+          sk = row_group_sum(sk);
+          if (r == 0) kx[w * kC + i] = sx, kk[w * kC + i] = sk;
+        }
+    }
   }
   __syncthreads();
   // Fold the partials in a fixed order (lane i: row i), then da = the
