@@ -503,6 +503,18 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs& p, const f32x16 (&a
   for (int e = 0; e < 8; ++e) rs[e] = 0.0f;
   float loss = 0.0f;
   uint16_t* c = static_cast<uint16_t*>(p.c);
+  // GELU backward: all of this lane's Z (32 x 16 bytes) is requested before
+  // the first store.  Loaded inside the loop, each read would wait for the
+  // previous iteration's store (the compiler cannot rule out that they
+  // alias), one memory round trip per iteration.  The accumulators are dead
+  // here, so the registers are free.
+  u32x4 zv[EPI == kGeluBackward ? 32 : 1];
+  if constexpr (EPI == kGeluBackward) {
+#pragma unroll
+    for (int t = 0; t < 32; ++t)
+      zv[t] = *reinterpret_cast<const u32x4*>(p.aux + (int64_t)(mw + mc) + (int64_t)(nw + 4 * t + cg) * p.aux_ld);
+  }
+#pragma unroll
   for (int t = 0; t < 32; ++t) {
     const int nl = 4 * t + cg;
     const u32x4 v = *reinterpret_cast<const u32x4*>(tile + nl * kEpiRow + mc);
@@ -532,7 +544,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs& p, const f32x16 (&a
       }
       *reinterpret_cast<u32x4*>(c + at) = ov;
     } else if constexpr (EPI == kGeluBackward) {
-      const u32x4 z = *reinterpret_cast<const u32x4*>(p.aux + (int64_t)(mw + mc) + (int64_t)(nw + nl) * p.aux_ld);
+      const u32x4 z = zv[t];
       u32x4 ov;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
