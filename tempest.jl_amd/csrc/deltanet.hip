@@ -1027,25 +1027,42 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
         }
     }
     {
+      // This lane's V values, all read before the first dV store (same
+      // element type: loaded in the loop, each read would wait for the
+      // previous store).
       f32x4v dy[4][2];
       clear(dy);
       mm_by(dy, ColF32{Tc, kC}, 0, ColF32{dUt, kD}, d0, kC);
+      // In two halves of row blocks: the V values of a half are all read
+      // before its first dV store (same element type: loaded in the loop,
+      // each read would wait for the previous store).
 #pragma unroll
-      for (int bi = 0; bi < 4; ++bi)
+      for (int hb = 0; hb < 2; ++hb) {
+        uint32_t vh[2][4];  // the two bf16 of columns d0 + r, d0 + 16 + r
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = 16 * bi + 4 * g + v;
-          float sv = 0.0f;
+        for (int b2 = 0; b2 < 2; ++b2)
 #pragma unroll
-          for (int bj = 0; bj < 2; ++bj) {
-            const int d = d0 + 16 * bj + r;
-            const float vv = bf(vg[(int64_t)i * p.s_t + d]), yv = dy[bi][bj][v];
-            sv = fmaf(vv, yv, sv);
-            p.dv[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(be[i] * yv);
+          for (int v = 0; v < 4; ++v) {
+            const uint16_t* vr = vg + (int64_t)(16 * (2 * hb + b2) + 4 * g + v) * p.s_t + d0 + r;
+            vh[b2][v] = (uint32_t)vr[0] | ((uint32_t)vr[16] << 16);
           }
-          sv = row_group_sum(sv);
-          if (r == 0) vy[w * kC + i] = sv;
-        }
+#pragma unroll
+        for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int bi = 2 * hb + b2, i = 16 * bi + 4 * g + v;
+            float sv = 0.0f;
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+              const int d = d0 + 16 * bj + r;
+              const float vv = bf((uint16_t)(vh[b2][v] >> (16 * bj))), yv = dy[bi][bj][v];
+              sv = fmaf(vv, yv, sv);
+              p.dv[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(be[i] * yv);
+            }
+            sv = row_group_sum(sv);
+            if (r == 0) vy[w * kC + i] = sv;
+          }
+      }
     }
     {
       f32x4v dk[4][2], dx[4][2];
