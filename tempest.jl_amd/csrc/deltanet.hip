@@ -416,10 +416,10 @@ __device__ __forceinline__ void scan_store(const ScanInputs& in, float* W, float
     const float ed = expf(last - ca[r]);
     const u32x4v uk = in.k[e];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Kd[r * kLd + c + 2 * j] = ed * bf((uint16_t)uk[j]);
-      Kd[r * kLd + c + 2 * j + 1] = ed * bf((uint16_t)(uk[j] >> 16));
-    }
+    for (int h = 0; h < 2; ++h)
+      *reinterpret_cast<f32x4v*>(Kd + r * kLd + c + 4 * h) =
+          f32x4v{ed * bf((uint16_t)uk[2 * h]), ed * bf((uint16_t)(uk[2 * h] >> 16)), ed * bf((uint16_t)uk[2 * h + 1]),
+                 ed * bf((uint16_t)(uk[2 * h + 1] >> 16))};
   }
 }
 
@@ -459,18 +459,24 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
       f32x4v ws[1][2];
       clear(ws);
       mm_gen<false, true>(ws, W, kLd, 16 * w, S, kLdS, 0, kD);
-      float* Uo = p.U + ck.c * kC * kD;
 #pragma unroll
       for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
-          const float u = Ut[i * kLdS + j] - ws[0][bj][v];
-          U[i * kLdS + j] = u;
-          Uo[i * kD + col0 + j] = u;
+          U[i * kLdS + j] = Ut[i * kLdS + j] - ws[0][bj][v];
         }
     }
     __syncthreads();
+    // U to memory from LDS in 16-byte pieces, beside the products below.
+    {
+      float* Uo = p.U + ck.c * kC * kD;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int x = t + 256 * e, row = x / 8, c = 4 * (x % 8);
+        *reinterpret_cast<f32x4v*>(Uo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(U + row * kLdS + c);
+      }
+    }
     // S <- g S + Kd' U (128 x 32): wave w takes rows 32 w .. 32 w + 31.
     {
       f32x4v ku[2][2];
@@ -626,11 +632,13 @@ __device__ __forceinline__ void sg_store(const SgInputs& in, float* P, float* dO
     const float eq = expf(ca[r]);
     const u32x4v uq = in.q[e], uk = in.k[e];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Qg[r * kLd + c + 2 * j] = eq * bf((uint16_t)uq[j]);
-      Qg[r * kLd + c + 2 * j + 1] = eq * bf((uint16_t)(uq[j] >> 16));
-      K[r * kLd + c + 2 * j] = bf((uint16_t)uk[j]);
-      K[r * kLd + c + 2 * j + 1] = bf((uint16_t)(uk[j] >> 16));
+    for (int h = 0; h < 2; ++h) {
+      *reinterpret_cast<f32x4v*>(Qg + r * kLd + c + 4 * h) =
+          f32x4v{eq * bf((uint16_t)uq[2 * h]), eq * bf((uint16_t)(uq[2 * h] >> 16)), eq * bf((uint16_t)uq[2 * h + 1]),
+                 eq * bf((uint16_t)(uq[2 * h + 1] >> 16))};
+      *reinterpret_cast<f32x4v*>(K + r * kLd + c + 4 * h) =
+          f32x4v{bf((uint16_t)uk[2 * h]), bf((uint16_t)(uk[2 * h] >> 16)), bf((uint16_t)uk[2 * h + 1]),
+                 bf((uint16_t)(uk[2 * h + 1] >> 16))};
     }
   }
 #pragma unroll
@@ -681,20 +689,24 @@ __global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
       clear(kd);
       mm_gen<true, true>(pd, P, kLdC, 16 * w, dO, kLdS, 0, kC);
       mm_gen<false, true>(kd, K, kLd, 16 * w, dS, kLdS, 0, kD);
-      float* dUo = p.dU + ck.c * kC * kD;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = 16 * w + 4 * g + v;
         const float e = expf(last - ca[i]);
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-          const float u = pd[0][bj][v] + e * kd[0][bj][v];
-          dU[i * kLdS + 16 * bj + r] = u;
-          dUo[i * kD + col0 + 16 * bj + r] = u;
-        }
+        for (int bj = 0; bj < 2; ++bj) dU[i * kLdS + 16 * bj + r] = pd[0][bj][v] + e * kd[0][bj][v];
       }
     }
     __syncthreads();
+    // dU to memory from LDS in 16-byte pieces, beside the products below.
+    {
+      float* dUo = p.dU + ck.c * kC * kD;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int x = t + 256 * e, row = x / 8, c = 4 * (x % 8);
+        *reinterpret_cast<f32x4v*>(dUo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(dU + row * kLdS + c);
+      }
+    }
     // dS <- Qg' dO + g dS - W' dU (128 x 32): wave w takes rows 32 w .. 32 w + 31.
     {
       f32x4v qd[2][2], wu[2][2];
