@@ -304,7 +304,9 @@ int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
 #define TH_ATTN_RECOMPUTE_DQ 1
 
 /* dq, dk, dv from q, k, v, o, lse (as the forward wrote them) and dout;
- * deterministic (no atomics), kv_heads == heads.  The dK/dV sweep stores dS
+ * deterministic (no atomics).  With grouped heads (kv_heads < heads) dk and
+ * dv sum over the heads / kv_heads query heads that read each key/value
+ * head, swept in turn (test/cuda/attention.jl:132-140).  The dK/dV sweep stores dS
  * (bf16, 2*batch*heads*seq^2 bytes of workspace the launch owns) for the dQ
  * sweep; when that exceeds 16 GiB, or with TH_ATTN_RECOMPUTE_DQ, the dQ sweep
  * recomputes S and dP instead and the workspace is not allocated.

@@ -143,11 +143,15 @@ def attention_fwd(q, k, v, causal=True, scale=None):
 
 
 def attention_bwd(q, k, v, dout, causal=True, scale=None):
-    """Gradients of sum(attention(q, k, v) .* dout) w.r.t. q, k, v in float64
-    (kv_heads == heads), same layout as attention_fwd."""
+    """Gradients of sum(attention(q, k, v) .* dout) w.r.t. q, k, v in float64,
+    same layout as attention_fwd.  With grouped heads the key and value
+    gradients sum over the query heads of a group (test/cuda/attention.jl:132-140)."""
     q, k, v, dout = (np.asarray(a, dtype=np.float64) for a in (q, k, v, dout))
     B, S, H, D = q.shape
+    Hk = k.shape[2]
     scale = 1.0 / np.sqrt(D) if scale is None else scale
+    k = np.repeat(k, H // Hk, axis=2)
+    v = np.repeat(v, H // Hk, axis=2)
     s = np.einsum("bmhd,bnhd->bhmn", q, k) * scale
     if causal:
         mask = np.arange(S)[None, :] > np.arange(S)[:, None]
@@ -160,6 +164,9 @@ def attention_bwd(q, k, v, dout, causal=True, scale=None):
     ds = p * (dp - (dp * p).sum(axis=-1, keepdims=True))
     dq = np.einsum("bhmn,bnhd->bmhd", ds, k) * scale
     dk = np.einsum("bhmn,bmhd->bnhd", ds, q) * scale
+    # Query head h = hk * (H // Hk) + g reads kv head hk: sum over g.
+    dk = dk.reshape(B, S, Hk, H // Hk, D).sum(axis=3)
+    dv = dv.reshape(B, S, Hk, H // Hk, D).sum(axis=3)
     return dq, dk, dv
 
 

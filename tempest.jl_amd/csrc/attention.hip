@@ -570,15 +570,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   const int npass = (p.causal && 2 * blk.x + 1 != nkb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
     const int kbk = pass == 0 ? blk.x : nkb - 1 - blk.x;
-    const int h = blk.y, b = blk.z;
-    const int hk = h / (p.heads / p.kv_heads);
+    // One workgroup per kv head: dK and dV sum over the query heads
+    // hk * group .. hk * group + group - 1 that read it, swept in turn.
+    const int hk = blk.y, b = blk.z;
+    const int group = p.heads / p.kv_heads;
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
     const int k0 = kbk * kBwdK + wave * 32;
     const int key = k0 + lr;
-
-    const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-    const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const int nq = p.seq / kBwdQ;
     // This wave's 32 keys of K and V as the B operands of the score products,
     // in registers for the whole sweep.
@@ -594,128 +593,132 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
     for (int i = 0; i < 4; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
     const float c = p.scale * kLog2e;
 
-    // Stage layout: Q tile, dO tile, then [-lse / scale | -delta] of its 64 queries.
-    auto Qs = [&](int s) { return lds + s * stage_elems; };
-    auto Gs = [&](int s) { return lds + s * stage_elems + kTileElems; };
-    auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
+    for (int h = hk * group; h < (hk + 1) * group; ++h) {
+      const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+      const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+      // Stage layout: Q tile, dO tile, then [-lse / scale | -delta] of its 64 queries.
+      auto Qs = [&](int s) { return lds + s * stage_elems; };
+      auto Gs = [&](int s) { return lds + s * stage_elems + kTileElems; };
+      auto Ls = [&](int s) { return reinterpret_cast<float*>(lds + s * stage_elems + 2 * kTileElems); };
 
-    const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
-    // A query block's Q and dO tiles and statistics go straight from global
-    // memory into a stage, two blocks ahead: four 1 KB loads per wave for
-    // each tile, and one 256-byte load of statistics per wave (waves w and
-    // w + 2 fetch the same half, so every wave issues the same nine loads).
-    const TileDma qt(qbase, p.q_ss), gt(gbase, p.q_ss);
-    const __amdgpu_buffer_rsrc_t srsrc = th_dev::buffer_of(p.stat + ((int64_t)b * p.heads + h) * nq * 128);
-    auto fetch = [&](int qb, int s) {
-      qt.load(qb * kBwdQ, Qs(s));
-      gt.load(qb * kBwdQ, Gs(s));
-      const int half = __builtin_amdgcn_readfirstlane(wave) % 2;
-      th_dev::dma4(srsrc, 4 * lane, qb * 512 + 256 * half, (uint32_t)(uintptr_t)Ls(s) + 256 * half);
-    };
-    // Accumulator start: register i of row block j holds query 32 j + 8 (i / 4) + 4 lh + i % 4.
-    auto start = [&](const float* v, int j) {
-      f32x16 a;
-  #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(v + 32 * j + 8 * m + 4 * lh);
-  #pragma unroll
-        for (int e = 0; e < 4; ++e) a[4 * m + e] = x[e];
-      }
-      return a;
-    };
-    // dS' of a query block, transposed through this wave's LDS scratch (32
-    // key rows) so that it leaves as whole 128-byte lines.  It is written
-    // there at the end of its step and stored during the next one (or after
-    // the sweep), beside that step's products.
-    uint16_t* const scratch = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
-    u32x4 pend[4];
-    auto scratch_read = [&]() {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = lane / 8 + 8 * i, cc = lane % 8;
-        pend[i] = *reinterpret_cast<const u32x4*>(scratch + r * kDsRow + 8 * cc);
-      }
-    };
-    // This wave's 32 keys are rows 32 (wave % 2) .. + 31 of key block k0 / 64;
-    // queries qq0 .. qq0 + 63 are one half of the rows of query block qq0 / 128.
-    auto store_pending = [&](int qq0) {
-      uint16_t* rows0 = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq +
-                        ((int64_t)(qq0 / 128) * (p.seq / 64) + k0 / 64) * (64 * 128) + (k0 % 64) * 128 + qq0 % 128;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = lane / 8 + 8 * i, cc = lane % 8;
-        __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + r * 128 + 8 * cc));
-      }
-    };
-    // Blocks past the end are a harmless reload of the last one into an idle stage.
-    fetch(qstart, 0);
-    fetch(min(qstart + 1, nq - 1), 1);
-    th_dev::wait_and_meet<9>();
-    int st = 0;  // the stage of block qb
-    for (int qb = qstart; qb < nq; ++qb) {
-      const int s2 = st >= kBwdStages - 2 ? st + 2 - kBwdStages : st + 2;
-      fetch(min(qb + 2, nq - 1), s2);
-      if constexpr (kStore)
-        if (qb > qstart) scratch_read();
-      const uint16_t *Q = Qs(st), *G = Gs(st);
-      const float* L = Ls(st);
-      // S~ = Q K' - lse / scale, dP~ = dO V' - delta (64 queries x 32 keys).
-      f32x16 s[2], dp[2];
-      s[0] = start(L, 0), dp[0] = start(L + 64, 0);
-      s[1] = start(L, 1), dp[1] = start(L + 64, 1);
-      scores_kv(Q, G, 0, kf, vf, s[0], dp[0]);
-      // The previous block's dS' leaves after this step's loads were issued,
-      // so the wait for those loads at the end of the step can leave these
-      // four stores in flight.
-      if constexpr (kStore)
-        if (qb > qstart) store_pending((qb - 1) * kBwdQ);
-      // On the diagonal the masked scores become -inf: their P and dS are exactly 0.
-      const int qq0 = qb * kBwdQ;
-      const bool diagonal = p.causal && qq0 < k0 + 32;
-      const int lim = key - qq0 - 4 * lh;  // masked: query offset 32 j + 8 (i / 4) + i % 4 < lim
-      if (diagonal) {
-  #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (8 * (i / 4) + i % 4 < lim) s[0][i] = -INFINITY;
-      }
-      bf16x8 pf[4], sf[4];
-      scores_kv(Q, G, 1, kf, vf, s[1], dp[1]);
-      weights_rows(s[0], dp[0], c, pf[0], pf[1], sf[0], sf[1]);
-      // Keep these weights here, beside the products above, rather than sunk
-      // past the branch below into the next phase.
-      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(sf[0]), "v"(sf[1]));
-      if (diagonal) {
-  #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (32 + 8 * (i / 4) + i % 4 < lim) s[1][i] = -INFINITY;
-      }
-      // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
-      grads_half(G, Q, 0, pf, sf, dv, dk);
-      weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
-      grads_half(G, Q, 2, pf, sf, dv, dk);
-      if constexpr (kStore) {
-        // sf[ks] element e is query 16 ks + 8 (e / 4) + 4 lh + e % 4 of this lane's key.
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const u32x4 x = __builtin_bit_cast(u32x4, sf[ks]);
-          *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
-          *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
+      const int qstart = p.causal ? (kbk * kBwdK) / kBwdQ : 0;
+      // A query block's Q and dO tiles and statistics go straight from global
+      // memory into a stage, two blocks ahead: four 1 KB loads per wave for
+      // each tile, and one 256-byte load of statistics per wave (waves w and
+      // w + 2 fetch the same half, so every wave issues the same nine loads).
+      const TileDma qt(qbase, p.q_ss), gt(gbase, p.q_ss);
+      const __amdgpu_buffer_rsrc_t srsrc = th_dev::buffer_of(p.stat + ((int64_t)b * p.heads + h) * nq * 128);
+      auto fetch = [&](int qb, int s) {
+        qt.load(qb * kBwdQ, Qs(s));
+        gt.load(qb * kBwdQ, Gs(s));
+        const int half = __builtin_amdgcn_readfirstlane(wave) % 2;
+        th_dev::dma4(srsrc, 4 * lane, qb * 512 + 256 * half, (uint32_t)(uintptr_t)Ls(s) + 256 * half);
+      };
+      // Accumulator start: register i of row block j holds query 32 j + 8 (i / 4) + 4 lh + i % 4.
+      auto start = [&](const float* v, int j) {
+        f32x16 a;
+    #pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(v + 32 * j + 8 * m + 4 * lh);
+    #pragma unroll
+          for (int e = 0; e < 4; ++e) a[4 * m + e] = x[e];
         }
+        return a;
+      };
+      // dS' of a query block, transposed through this wave's LDS scratch (32
+      // key rows) so that it leaves as whole 128-byte lines.  It is written
+      // there at the end of its step and stored during the next one (or after
+      // the sweep), beside that step's products.
+      uint16_t* const scratch = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
+      u32x4 pend[4];
+      auto scratch_read = [&]() {
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = lane / 8 + 8 * i, cc = lane % 8;
+          pend[i] = *reinterpret_cast<const u32x4*>(scratch + r * kDsRow + 8 * cc);
+        }
+      };
+      // This wave's 32 keys are rows 32 (wave % 2) .. + 31 of key block k0 / 64;
+      // queries qq0 .. qq0 + 63 are one half of the rows of query block qq0 / 128.
+      auto store_pending = [&](int qq0) {
+        uint16_t* rows0 = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq +
+                          ((int64_t)(qq0 / 128) * (p.seq / 64) + k0 / 64) * (64 * 128) + (k0 % 64) * 128 + qq0 % 128;
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = lane / 8 + 8 * i, cc = lane % 8;
+          __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + r * 128 + 8 * cc));
+        }
+      };
+      // Blocks past the end are a harmless reload of the last one into an idle stage.
+      fetch(qstart, 0);
+      fetch(min(qstart + 1, nq - 1), 1);
+      th_dev::wait_and_meet<9>();
+      int st = 0;  // the stage of block qb
+      for (int qb = qstart; qb < nq; ++qb) {
+        const int s2 = st >= kBwdStages - 2 ? st + 2 - kBwdStages : st + 2;
+        fetch(min(qb + 2, nq - 1), s2);
+        if constexpr (kStore)
+          if (qb > qstart) scratch_read();
+        const uint16_t *Q = Qs(st), *G = Gs(st);
+        const float* L = Ls(st);
+        // S~ = Q K' - lse / scale, dP~ = dO V' - delta (64 queries x 32 keys).
+        f32x16 s[2], dp[2];
+        s[0] = start(L, 0), dp[0] = start(L + 64, 0);
+        s[1] = start(L, 1), dp[1] = start(L + 64, 1);
+        scores_kv(Q, G, 0, kf, vf, s[0], dp[0]);
+        // The previous block's dS' leaves after this step's loads were issued,
+        // so the wait for those loads at the end of the step can leave these
+        // four stores in flight.
+        if constexpr (kStore)
+          if (qb > qstart) store_pending((qb - 1) * kBwdQ);
+        // On the diagonal the masked scores become -inf: their P and dS are exactly 0.
+        const int qq0 = qb * kBwdQ;
+        const bool diagonal = p.causal && qq0 < k0 + 32;
+        const int lim = key - qq0 - 4 * lh;  // masked: query offset 32 j + 8 (i / 4) + i % 4 < lim
+        if (diagonal) {
+    #pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (8 * (i / 4) + i % 4 < lim) s[0][i] = -INFINITY;
+        }
+        bf16x8 pf[4], sf[4];
+        scores_kv(Q, G, 1, kf, vf, s[1], dp[1]);
+        weights_rows(s[0], dp[0], c, pf[0], pf[1], sf[0], sf[1]);
+        // Keep these weights here, beside the products above, rather than sunk
+        // past the branch below into the next phase.
+        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(sf[0]), "v"(sf[1]));
+        if (diagonal) {
+    #pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (32 + 8 * (i / 4) + i % 4 < lim) s[1][i] = -INFINITY;
+        }
+        // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
+        grads_half(G, Q, 0, pf, sf, dv, dk);
+        weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
+        grads_half(G, Q, 2, pf, sf, dv, dk);
+        if constexpr (kStore) {
+          // sf[ks] element e is query 16 ks + 8 (e / 4) + 4 lh + e % 4 of this lane's key.
+  #pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const u32x4 x = __builtin_bit_cast(u32x4, sf[ks]);
+            *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
+            *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
+          }
+        }
+        // Wait for block qb + 1's stage.  After its nine loads this wave has
+        // issued the previous step's four stores (past its first step), this
+        // step's nine loads, and this step's four stores (past the first).
+        if (!kStore || qb == qstart) th_dev::wait_and_meet<9>();
+        else if (qb == qstart + 1) th_dev::wait_and_meet<13>();
+        else th_dev::wait_and_meet<17>();
+        st = st == kBwdStages - 1 ? 0 : st + 1;
       }
-      // Wait for block qb + 1's stage.  After its nine loads this wave has
-      // issued the previous step's four stores (past its first step), this
-      // step's nine loads, and this step's four stores (past the first).
-      if (!kStore || qb == qstart) th_dev::wait_and_meet<9>();
-      else if (qb == qstart + 1) th_dev::wait_and_meet<13>();
-      else th_dev::wait_and_meet<17>();
-      st = st == kBwdStages - 1 ? 0 : st + 1;
-    }
-    // No load may land in this workgroup's LDS after the sweep.
-    th_dev::wait_and_meet<0>();
-    if constexpr (kStore) {
-      scratch_read();
-      store_pending((nq - 1) * kBwdQ);
-    }
+      // No load may land in this workgroup's LDS after the sweep.
+      th_dev::wait_and_meet<0>();
+      if constexpr (kStore) {
+        scratch_read();
+        store_pending((nq - 1) * kBwdQ);
+      }
+    }  // query heads of the group
     // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
     const int64_t out = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
   #pragma unroll
@@ -962,7 +965,6 @@ int check_desc(const th_attention_desc* d, bool backward) {
     TH_REQUIRE(d->lse && d->dout && d->dq && d->dk && d->dv, "attention backward: null lse, dout, dq, dk or dv");
     TH_REQUIRE(aligned(d->dout, 16) && aligned(d->dq, 16) && aligned(d->dk, 16) && aligned(d->dv, 16),
                "attention backward: dout, dq, dk, dv must be 16-byte aligned");
-    TH_REQUIRE(d->kv_heads == d->heads, "attention backward: grouped heads are not built (kv_heads must equal heads)");
   }
   return TH_OK;
 }
@@ -1055,7 +1057,7 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   TH_HIP(hipFuncSetAttribute(dqk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds));
   int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, a);
   int k1 = b.kernel(dkdv, store ? "attn_bwd_dkdv_store" : "attn_bwd_dkdv",
-                    dim3(blocks_x(d->seq / kBwdK, d->causal), d->heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
+                    dim3(blocks_x(d->seq / kBwdK, d->causal), d->kv_heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
   int k2 = b.kernel(dqk, store ? "attn_bwd_dq_ds" : "attn_bwd_dq",
                     dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch), dim3(256), (uint32_t)dq_lds, a);
   const size_t offs[9] = {TH_OFFSET(AttnArgs, q),   TH_OFFSET(AttnArgs, k),  TH_OFFSET(AttnArgs, v),

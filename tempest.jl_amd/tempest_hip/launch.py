@@ -140,12 +140,14 @@ RECOMPUTE_DQ = 1  # TH_ATTN_RECOMPUTE_DQ
 
 def attention_bwd(batch: int, heads: int, seq: int, q: int, k: int, v: int, o: int, lse: int, dout: int, dq: int,
                   dk: int, dv: int, causal: bool = True, scale: float = 0.0, recompute_dq: bool = False,
-                  **strides) -> Launch:
+                  kv_heads: int = 0, **strides) -> Launch:
     """dq, dk, dv of sum(attention(q, k, v) .* dout), from the forward's o and lse.
+    kv_heads (default heads): k, v, dk, dv have kv_heads heads, each read by
+    heads / kv_heads query heads; dk and dv sum over them.
     recompute_dq: the dQ sweep recomputes S and dP instead of reading the dS
     the dK/dV sweep stores (the path taken anyway past 16 GiB of dS)."""
-    d = _attention_desc(batch, heads, heads, seq, q, k, v, o, lse, dout, dq, dk, dv, causal=causal, scale=scale,
-                        flags=RECOMPUTE_DQ if recompute_dq else 0, **strides)
+    d = _attention_desc(batch, heads, kv_heads or heads, seq, q, k, v, o, lse, dout, dq, dk, dv, causal=causal,
+                        scale=scale, flags=RECOMPUTE_DQ if recompute_dq else 0, **strides)
     return _built("th_build_attention_bwd", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"), ctypes.byref(d))
 
 

@@ -110,30 +110,34 @@ def mlp(batch: int = 4096, d_in: int = 4096, hidden: int = 16384, d_out: int = 4
     return Program("mlp", values, groups, ["W1", "b1", "W2", "b2", "x"], ["loss", "dW1", "db1", "dW2", "db2", "dx"])
 
 
-def attention(batch: int = 8, heads: int = 16, seq: int = 4096, head_dim: int = 128, causal: bool = True) -> Program:
+def attention(batch: int = 8, heads: int = 16, seq: int = 4096, head_dim: int = 128, causal: bool = True,
+              kv_heads: int = 0) -> Program:
     """Config 4: (q, k, v, dout) -> attention(q, k, v; causal) and the gradients
     of sum(attention(q, k, v) .* dout) w.r.t. q, k, v; bf16 (d, heads, positions,
-    batch) arrays, fp32 statistics (test/fixtures/operations.jl:21-70).
+    batch) arrays, fp32 statistics (test/fixtures/operations.jl:21-70).  With
+    kv_heads < heads, k, v, dk and dv have kv_heads heads, query head h reading
+    kv head h / (heads / kv_heads) (test/cuda/attention.jl:132-140).
 
     Plan: the forward's product, softmax and product fold into one online
     sweep over keys (the online-softmax rewrite, plan/rewrites.jl:29-41),
     storing o and lse; the backward recomputes the weights from lse."""
     bf, f32 = torch.bfloat16, torch.float32
-    dims = (head_dim, heads, seq, batch)
+    kv_heads = kv_heads or heads
+    dims, kdims = (head_dim, heads, seq, batch), (head_dim, kv_heads, seq, batch)
     values = {
-        "q": Value("q", bf, dims, "input"), "k": Value("k", bf, dims, "input"), "v": Value("v", bf, dims, "input"),
+        "q": Value("q", bf, dims, "input"), "k": Value("k", bf, kdims, "input"), "v": Value("v", bf, kdims, "input"),
         "dout": Value("dout", bf, dims, "input"),
         "o": Value("o", bf, dims, "result"), "lse": Value("lse", f32, (1, heads, seq, batch), "stored"),
-        "dq": Value("dq", bf, dims, "result"), "dk": Value("dk", bf, dims, "result"),
-        "dv": Value("dv", bf, dims, "result"),
+        "dq": Value("dq", bf, dims, "result"), "dk": Value("dk", bf, kdims, "result"),
+        "dv": Value("dv", bf, kdims, "result"),
     }
     fwd = Group("o = attention(q, k, v); lse", ("q", "k", "v", "o", "lse"), ("q", "k", "v"), ("o", "lse"),
-                lambda a: L.attention_fwd(batch, heads, heads, seq, a["q"], a["k"], a["v"], a["o"], a["lse"],
+                lambda a: L.attention_fwd(batch, heads, kv_heads, seq, a["q"], a["k"], a["v"], a["o"], a["lse"],
                                           causal=causal))
     bwd = Group("dq, dk, dv", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"),
                 ("q", "k", "v", "o", "lse", "dout"), ("dq", "dk", "dv"),
                 lambda a: L.attention_bwd(batch, heads, seq, a["q"], a["k"], a["v"], a["o"], a["lse"], a["dout"],
-                                          a["dq"], a["dk"], a["dv"], causal=causal))
+                                          a["dq"], a["dk"], a["dv"], causal=causal, kv_heads=kv_heads))
     return Program("attention", values, [fwd, bwd], ["q", "k", "v", "dout"], ["o", "dq", "dk", "dv"])
 
 

@@ -56,6 +56,48 @@ def test_backward_matches_oracle(target, B, H, S, causal):
         assert relative(_np(got.view(B, S, H, 128)), ref) < TOL, name
 
 
+@pytest.mark.parametrize("B,H,Hk,S,causal,recompute", [(1, 4, 2, 256, True, False), (2, 4, 1, 384, True, False),
+                                                        (1, 6, 2, 256, False, False), (1, 4, 2, 384, True, True)])
+def test_grouped_backward_matches_oracle(target, B, H, Hk, S, causal, recompute):
+    """Grouped heads (test/cuda/attention.jl:132-140): dk and dv of each
+    key/value head sum over the query heads that read it."""
+    import tempest_hip.launch as L
+    announce("attn bwd grouped", B, H, Hk, S, causal, recompute)
+    gen = torch.Generator(device="cuda").manual_seed(13 * S + H + Hk)
+    q, g = _rand((B, S, H, 128), gen), _rand((B, S, H, 128), gen)
+    k, v = _rand((B, S, Hk, 128), gen), _rand((B, S, Hk, 128), gen)
+    o, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    lse = torch.empty(B, S, H, device="cuda")
+    ptr = lambda t: t.data_ptr()  # noqa: E731
+    fwd = L.attention_fwd(B, H, Hk, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), causal=causal)
+    bwd = L.attention_bwd(B, H, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), ptr(g), ptr(dq), ptr(dk), ptr(dv),
+                          causal=causal, recompute_dq=recompute, kv_heads=Hk)
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    rq, rk, rv = interpret.attention_bwd(_np(q), _np(k), _np(v), _np(g), causal)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert relative(_np(got), ref) < TOL, name
+
+
+def test_grouped_program(target):
+    """The compiled program with grouped heads, against the oracle."""
+    import tempest_hip as th
+    announce("attn program grouped")
+    B, H, Hk, S = 1, 4, 2, 256
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    q, g = _rand((B, S, H, 128), gen), _rand((B, S, H, 128), gen)
+    k, v = _rand((B, S, Hk, 128), gen), _rand((B, S, Hk, 128), gen)
+    comp = th.compile(th.programs.attention(B, H, S, kv_heads=Hk), target, q, k, v, g)
+    o, dq, dk, dv = comp(q, k, v, g)
+    ro, _ = interpret.attention_fwd(_np(q), _np(k), _np(v), True)
+    rq, rk, rv = interpret.attention_bwd(_np(q), _np(k), _np(v), _np(g), True)
+    assert relative(_np(o.view(B, S, H, 128)), ro) < TOL
+    for name, got, ref, heads in (("dq", dq, rq, H), ("dk", dk, rk, Hk), ("dv", dv, rv, Hk)):
+        assert relative(_np(got.view(B, S, heads, 128)), ref) < TOL, name
+
+
 @pytest.mark.parametrize("S,causal", [(384, True), (256, False)])
 @pytest.mark.parametrize("recompute", [False, True])
 def test_backward_both_dq_paths(target, S, causal, recompute):

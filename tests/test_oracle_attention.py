@@ -53,3 +53,21 @@ def test_causal_first_query_reads_only_the_first_key():
     o, lse = interpret.attention_fwd(q, k, v, True)
     assert np.allclose(o[0, 0, 0], v[0, 0, 0])
     assert np.isclose(lse[0, 0, 0], (q[0, 0, 0] @ k[0, 0, 0]) / np.sqrt(8))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_grouped_backward_matches_torch(causal):
+    # Four query heads over two kv heads: torch's autograd through the
+    # repeated keys and values sums each group's gradients.
+    rng = np.random.default_rng(3)
+    B, S, H, Hk, D = 2, 7, 4, 2, 8
+    q, g = rng.normal(size=(B, S, H, D)), rng.normal(size=(B, S, H, D))
+    k, v = rng.normal(size=(B, S, Hk, D)), rng.normal(size=(B, S, Hk, D))
+    t = [torch.tensor(a, requires_grad=True) for a in (q, k, v)]
+    kr, vr = (torch.repeat_interleave(x, H // Hk, dim=2) for x in t[1:])
+    ot, _ = _torch_attention(t[0], kr, vr, causal, 1 / np.sqrt(D))
+    (ot * torch.tensor(g)).sum().backward()
+    dq, dk, dv = interpret.attention_bwd(q, k, v, g, causal)
+    for ours, tt in zip((dq, dk, dv), t):
+        assert ours.shape == tt.grad.shape
+        assert relative(ours, tt.grad.numpy()) < 1e-12
