@@ -6,15 +6,19 @@
 // two strides, one of which is 1: "k-contiguous" or "mn-contiguous".  One
 // workgroup of four waves computes a 256 x 256 tile of C; each wave a
 // 128 x 128 quarter as 4 x 4 v_mfma_f32_32x32x16_bf16 blocks (256 fp32
-// accumulators per lane, in AGPRs).  K advances 64 at a time through two LDS
-// stages: while the waves multiply out of one stage, the next tile's global
-// loads are in flight into registers, and land in the other stage after.
-// LDS rows are k-contiguous, 64 bf16 plus 8 of padding (144 bytes), so the
-// 16-byte fragment reads of 16 lanes fall on 16 distinct bank quads.  An
-// mn-contiguous operand is transposed on its way into LDS: each thread loads
-// an 8 x 8 block (eight 16-byte rows along m or n, eight lanes along k side
-// by side so their LDS writes spread over the banks) and writes it back as
-// eight 16-byte rows along k.
+// accumulators per lane, in AGPRs).
+//
+// Interior tiles (sizes multiples of the tile, k of 64) take the direct path:
+// loads straight from global memory into LDS rings several K tiles deep, one
+// barrier per 32 of K (sweep_direct below).  Edge tiles take the checked
+// path: K advances 64 at a time through two LDS stages, the next tile's
+// global loads in flight into registers while the waves multiply out of one
+// stage.  Its LDS rows are k-contiguous, 64 bf16 plus 8 of padding (144
+// bytes), so the 16-byte fragment reads of 16 lanes fall on 16 distinct bank
+// quads.  An mn-contiguous operand is transposed on its way into LDS: each
+// thread loads an 8 x 8 block (eight 16-byte rows along m or n, eight lanes
+// along k side by side so their LDS writes spread over the banks) and writes
+// it back as eight 16-byte rows along k.
 //
 // Workgroups are dealt to the eight XCDs round-robin; the tile order is
 // remapped so each XCD takes a contiguous range of tiles, grouped 8 tile-rows
@@ -31,6 +35,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 #include <utility>
 
 #include "lds_dma.h"
@@ -262,35 +267,50 @@ __device__ __forceinline__ void multiply_tile(const uint16_t* As, const uint16_t
 // buffer_load ... lds writes each lane's 16 bytes at M0 + 16 lane, so one
 // wave instruction fills 1 KB of LDS.  The tiles have no padding; instead the
 // 16-byte chunks of each row are XOR-permuted, which keeps both the direct
-// writes and the fragment reads free of bank conflicts:
-//   k-contiguous operand: [256 rows][64 k], 128-byte rows, chunk c of row r
-//     at c ^ ((r / 2) % 8) (16 consecutive rows of one chunk: 16 distinct
-//     bank quads, the rows alternating halves of the banks);
-//   mn-contiguous operand: [64 k][256 mn], 512-byte rows, chunk c of row r at
-//     c ^ 4 (r % 4), read transposed (ds_read_b64_tr_b16): four consecutive
-//     rows x four consecutive chunks land on 16 distinct bank quads.
-// No register transpose, and no staging registers.
+// writes and the fragment reads free of bank conflicts.
 //
-// The sweep's schedule is written out product by product.  Each 16-deep
-// step issues its 16 products one after another; between them go the
-// fragment reads of the next step (one after every other product) and,
-// during the first three steps, the next K tile's 16 direct loads (one
-// after every third product, so the four waves ask the CU's address unit
-// for at most ~43 bytes a clock, under its rate, and no wave stalls on a
-// full queue while it has products to issue).  At the end of the tile each
-// wave waits for its own loads, the waves meet, and the next tile's first
-// fragments are read.
+// K advances 32 at a time (a "tile" below is 32 deep), and each operand has
+// its own 64 KiB ring in LDS, laid out for its layout:
+//   mn-contiguous: four stages of one tile, [32 k][256 mn] with 512-byte
+//     rows, chunk c of row r at c ^ 4 (r % 4), read transposed
+//     (ds_read_b64_tr_b16): four consecutive rows x four consecutive chunks
+//     land on 16 distinct bank quads.  Each load instruction covers two
+//     whole rows.
+//   k-contiguous: two slots of two tiles each, [256 rows][64 k] with
+//     128-byte rows, chunk c of row r at c ^ ((r / 2) % 8) (16 consecutive
+//     rows of one chunk: 16 distinct bank quads).  A slot rather than a
+//     stage per tile keeps each load on whole 128-byte lines: a 64-byte row
+//     per tile would fetch every line twice, a tile apart, and the CU's fill
+//     rate from L2 would bound the sweep.
 //
-// The direct loads are issued from inline assembly (lds_dma.h says why) and
-// waited for explicitly at the barrier, where the stage they fill is next read.
+// Each tile's 32 products per wave run as two 16-deep steps with one barrier
+// between them.  Step 0 reads the fragments of step 1; the barrier makes the
+// next tile's data visible and frees the stage (or slot) read last; step 1
+// reads the next tile's first fragments.  No wave ever waits on a fragment
+// read at a tile boundary.  The loads of later tiles issue between the
+// products (at most four per step and operand, one after every other or
+// every fourth product):
+//   mn-contiguous: step 0 of tile t, the second half of tile t + 3; step 1,
+//     the first half of tile t + 4 (so a tile's loads lead its use by more
+//     than two tiles);
+//   k-contiguous: step 0 of an even tile 2u, the second half of pair u + 1;
+//     step 1 of an odd tile 2u + 1, the first half of pair u + 2 (pair p
+//     holds tiles 2p, 2p + 1; its loads lead by one to two tiles).
+// Past the last tile the last one is loaded again, into a stage nothing reads
+// any more (or the same bytes into its own), so the issue sequence and every
+// wait count are the same for every tile; mid_wait counts, from this
+// schedule, the loads a wave may leave in flight at each barrier.
+// The direct loads are issued from inline assembly (lds_dma.h says why).
 
-constexpr int kTileD = kTile * kDepth;                         // bf16 per operand stage
+constexpr int kDepthD = 32;                                    // K per tile of the direct path
+constexpr int kStageBytesMN = kTile * kDepthD * 2;             // one mn-contiguous stage: 16 KiB
+constexpr int kSlotBytesK = 2 * kStageBytesMN;                 // one k-contiguous slot: 32 KiB
+constexpr uint32_t kRingBytes = 4 * kStageBytesMN;             // one operand's ring: 64 KiB
 constexpr int kEpiRow = 136;                                  // LDS row (bf16) of the epilogue's transpose: 128 m + 8
 constexpr size_t kEpiWave = 128 * kEpiRow * sizeof(uint16_t);  // one wave's 128 x 128 tile
-// A and B in two stages (131072 bytes), or after the sweep the four waves'
-// transposed tiles (139264 bytes).
-constexpr size_t kLdsDirect = 4 * kEpiWave > 4 * kTileD * sizeof(uint16_t) ? 4 * kEpiWave : 4 * kTileD * sizeof(uint16_t);
-constexpr int kOpBytes = kTileD * 2;                           // one operand's stage: 32 KiB
+// Both rings (131072 bytes), or after the sweep the four waves' transposed
+// tiles (139264 bytes).
+constexpr size_t kLdsDirect = 4 * kEpiWave > 2 * kRingBytes ? 4 * kEpiWave : 2 * kRingBytes;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -302,139 +322,257 @@ using th_dev::static_for;
 using th_dev::dma16;
 using th_dev::wait_and_meet;
 
-// One operand of the direct path: its buffer resource, the byte offsets of
-// the wave's eight loads for K tile 0 (the K advance is the scalar offset),
-// and the LDS byte addresses of this lane's fragment reads in stage 0.
+// The schedule.  Loads of one operand in step s of tile t:
 template <int L>
-struct Operand {
-  __amdgpu_buffer_rsrc_t rsrc;
-  int32_t off[8];
-  int32_t step;
-  uint32_t rd[4];  // k-contiguous: per 16-deep step; mn-contiguous: per 32-row block
+constexpr int ring_loads(int t, int s) {
+  if (L == kMN) return 2;
+  return ((s == 0 && t % 2 == 0) || (s == 1 && t % 2 == 1)) ? 4 : 0;
+}
+// The product after which load j of a step issues: A after products 1 mod 4,
+// B after 3 mod 4 (operand op: 0 = A, 1 = B).
+template <int L>
+constexpr int ring_slot(int op, int j) { return L == kMN ? 2 * op + 1 + 8 * j : 2 * op + 1 + 4 * j; }
+// The tile (mn-contiguous) or pair (k-contiguous) the loads of step s of tile t fill.
+template <int L>
+constexpr int ring_target(int t, int s) {
+  if (L == kMN) return s == 0 ? t + 3 : t + 4;
+  return s == 0 ? t / 2 + 1 : (t + 1) / 2 + 1;
+}
+struct IssuePos { int t, s, q; };
+constexpr bool issued_after(IssuePos a, IssuePos b) {
+  return a.t != b.t ? a.t > b.t : a.s != b.s ? a.s > b.s : a.q > b.q;
+}
+// The last load of one operand that tile t + 1 needs.
+template <int L>
+constexpr IssuePos last_needed(int op, int t) {
+  if (L == kMN) return IssuePos{t - 2, 0, ring_slot<L>(op, 1)};
+  return IssuePos{t % 2 == 0 ? t - 2 : t - 1, 0, ring_slot<L>(op, 3)};
+}
+// Loads issued after the last one tile t + 1 needs, up to the barrier in the
+// middle of tile t: what a wave may leave in flight there.  It depends on
+// t's parity only (t >= 2; the prologue makes it hold for t = -1, 0, 1).
+template <int LA, int LB>
+constexpr int mid_wait(int t) {
+  const IssuePos pa = last_needed<LA>(0, t), pb = last_needed<LB>(1, t);
+  const IssuePos p = issued_after(pa, pb) ? pa : pb;
+  int n = 0;
+  for (int tau = t - 4; tau <= t; ++tau)
+    for (int s = 0; s < 2 && !(tau == t && s == 1); ++s) {
+      for (int j = 0; j < ring_loads<LA>(tau, s); ++j) n += issued_after(IssuePos{tau, s, ring_slot<LA>(0, j)}, p);
+      for (int j = 0; j < ring_loads<LB>(tau, s); ++j) n += issued_after(IssuePos{tau, s, ring_slot<LB>(1, j)}, p);
+    }
+  return n;
+}
+static_assert(mid_wait<kK, kK>(10) == 16 && mid_wait<kK, kK>(11) == 0, "direct path schedule");
+static_assert(mid_wait<kMN, kK>(10) == 16 && mid_wait<kMN, kK>(11) == 4, "direct path schedule");
+static_assert(mid_wait<kK, kMN>(10) == 16 && mid_wait<kK, kMN>(11) == 4, "direct path schedule");
+static_assert(mid_wait<kMN, kMN>(10) == 16 && mid_wait<kMN, kMN>(11) == 16, "direct path schedule");
 
-  // Instruction i of wave w fills LDS bytes [1024 (8 w + i), + 1024) of the
-  // operand's stage: rows 64 w + 8 i .. + 7 of a k-contiguous tile, k rows
-  // 16 w + 2 i, + 1 of an mn-contiguous one.  `wo` is the wave's first row
-  // (m or n) of the tile, `lds` the operand's stage-0 byte address.
-  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int64_t s_k, int o0, int wo, uint32_t lds) {
+// One operand's ring: its buffer resource, the byte offsets of the wave's
+// load instructions for K tile (or pair) 0 (the K advance is the scalar
+// offset), and the LDS byte addresses of this lane's fragment reads in stage
+// (slot) 0.  `wo` is the wave's first row (m or n) of the tile, `ring` the
+// ring's LDS byte address, `nk` the number of 32-deep tiles.
+template <int L>
+struct Ring;
+
+template <>
+struct Ring<kMN> {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int32_t off[4];
+  int32_t step;
+  uint32_t rd[4];  // per 32-row block
+  uint32_t ring;
+  int last;
+
+  // Instruction i of wave w fills bytes [1024 (4 w + i), + 1024) of a stage:
+  // k rows 8 w + 2 i, + 1.
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_k, int o0, int wo, uint32_t ring_, int nk) {
     rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
     const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-    if constexpr (L == kK) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = 64 * w + 8 * i + l / 8, lc = (l % 8) ^ ((r / 2) % 8);
-        off[i] = (int32_t)(((int64_t)(o0 + r) * s_o + 8 * lc) * 2);
-      }
-      step = kDepth * 2;
-      // Fragment rows wo + l % 32 (+ 32 i: the same permutation), chunk 2 kk + l / 32.
-      const int r = wo + l % 32;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) rd[kk] = lds + (uint32_t)((r * kDepth + 8 * ((2 * kk + l / 32) ^ ((r / 2) % 8))) * 2);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int kr = 16 * w + 2 * i + l / 32, lc = (l % 32) ^ (4 * (kr % 4));
-        off[i] = (int32_t)(((int64_t)kr * s_k + o0 + 8 * lc) * 2);
-      }
-      step = (int32_t)(kDepth * s_k * 2);
-      // ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the
-      // 8-byte pieces addressed by lanes 4 q + i / 4 (q = 0..3).  Lane j
-      // addresses k row j / 4 (+ 8 (l / 32), + 16 kk, + 4 for the upper
-      // half), columns ogrp + 4 (j % 4) + (0..3), so lane i receives k rows
-      // base + (0..3) of column ogrp + i: k in natural order.
-      const int j = l % 16, row = 8 * (l / 32) + j / 4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int o = wo + 32 * i + 16 * ((l / 16) % 2) + 4 * (j % 4);
-        rd[i] = lds + (uint32_t)((row * kTile + 8 * ((o / 8) ^ (4 * (row % 4))) + o % 8) * 2);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int kr = 8 * w + 2 * i + l / 32, lc = (l % 32) ^ (4 * (kr % 4));
+      off[i] = (int32_t)(((int64_t)kr * s_k + o0 + 8 * lc) * 2);
     }
+    step = (int32_t)(kDepthD * s_k * 2);
+    // ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of the
+    // 8-byte pieces addressed by lanes 4 q + i / 4 (q = 0..3).  Lane j
+    // addresses k row j / 4 (+ 8 (l / 32), + 16 kk, + 4 for the upper
+    // half), columns ogrp + 4 (j % 4) + (0..3), so lane i receives k rows
+    // base + (0..3) of column ogrp + i: k in natural order.
+    const int j = l % 16, row = 8 * (l / 32) + j / 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int o = wo + 32 * i + 16 * ((l / 16) % 2) + 4 * (j % 4);
+      rd[i] = ring_ + (uint32_t)((row * kTile + 8 * ((o / 8) ^ (4 * (row % 4))) + o % 8) * 2);
+    }
+    ring = ring_;
+    last = nk - 1;
   }
-
-  // Load instruction i of K tile kt into the stage at LDS byte address `stage`.
-  __device__ __forceinline__ void load(int kt, uint32_t stage, int i) const {
+  // Instruction i (0..3) of tile t, into stage t mod 4.
+  __device__ __forceinline__ void load(int t, int i) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    dma16(rsrc, off[i], kt * step, stage + 1024 * (8 * w + i));
+    dma16(rsrc, off[i], min(t, last) * step, ring + (t & 3) * kStageBytesMN + 1024 * (4 * w + i));
   }
-
-  // Fragment I (rows wo + 32 I + lane % 32, k = 16 KK + 8 (lane / 32) + 0..7)
-  // of the stage `so` bytes past stage 0.
-  template <int I, int KK>
-  __device__ __forceinline__ bf16x8 frag(uint32_t so) const {
-    if constexpr (L == kK) {
-      return *reinterpret_cast<const lds_bf16x8*>((uintptr_t)(rd[KK] + so + I * 32 * kDepth * 2));
-    } else {
-      const uint32_t a = rd[I] + so + KK * 16 * kTile * 2;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a);
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(a + 4 * kTile * 2));
-      const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      return __builtin_bit_cast(bf16x8, w);
-    }
+  // Load j of step S of tile t (PAR = t mod 2).
+  template <int S, int PAR, int J>
+  __device__ __forceinline__ void step_load(int t) const {
+    if constexpr (S == 0)
+      load(t + 3, 2 + J);
+    else
+      load(t + 4, J);
+  }
+  // Fragment I (rows wo + 32 I + lane % 32, k = 16 KK + 8 (lane / 32) + 0..7) of tile t.
+  template <int I, int KK, int PAR>
+  __device__ __forceinline__ bf16x8 frag(int t) const {
+    const uint32_t a = rd[I] + (t & 3) * kStageBytesMN + KK * 16 * kTile * 2;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(a + 4 * kTile * 2));
+    const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, w);
   }
 };
 
-// The K sweep of an interior tile: acc += A(m0.., :) B(:, n0..), two stages.
+template <>
+struct Ring<kK> {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int32_t off[8];
+  uint32_t rd[4];  // per 16-deep step of a pair
+  uint32_t ring;
+  int last;
+
+  // Instruction i of wave w fills bytes [1024 (8 w + i), + 1024) of a slot:
+  // rows 64 w + 8 i .. + 7.
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t s_o, int o0, int wo, uint32_t ring_, int nk) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 64 * w + 8 * i + l / 8, lc = (l % 8) ^ ((r / 2) % 8);
+      off[i] = (int32_t)(((int64_t)(o0 + r) * s_o + 8 * lc) * 2);
+    }
+    // Fragment rows wo + l % 32 (+ 32 i: the same permutation), chunk 2 kk + l / 32.
+    const int r = wo + l % 32;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      rd[kk] = ring_ + (uint32_t)((r * 2 * kDepthD + 8 * ((2 * kk + l / 32) ^ ((r / 2) % 8))) * 2);
+    ring = ring_;
+    last = nk / 2 - 1;
+  }
+  // Instruction i (0..7) of pair p, into slot p mod 2.
+  __device__ __forceinline__ void load(int p, int i) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    dma16(rsrc, off[i], min(p, last) * (4 * kDepthD), ring + (p & 1) * kSlotBytesK + 1024 * (8 * w + i));
+  }
+  template <int S, int PAR, int J>
+  __device__ __forceinline__ void step_load(int t) const {
+    if constexpr (S == 0 && PAR == 0)
+      load(t / 2 + 1, 4 + J);
+    else if constexpr (S == 1 && PAR == 1)
+      load((t + 1) / 2 + 1, J);
+  }
+  template <int I, int KK, int PAR>
+  __device__ __forceinline__ bf16x8 frag(int t) const {
+    return *reinterpret_cast<const lds_bf16x8*>(
+        (uintptr_t)(rd[2 * PAR + KK] + ((t >> 1) & 1) * kSlotBytesK + I * 32 * 2 * kDepthD * 2));
+  }
+};
+
+// The K sweep of an interior tile: acc += A(m0.., :) B(:, n0..); k a multiple of 64.
 template <int LA, int LB>
 __device__ __forceinline__ void sweep_direct(const GemmArgs& p, int m0, int n0, int wm, int wn,
                                              f32x16 (&acc)[4][4]) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const uint32_t base = (uint32_t)(uintptr_t)lds;
-  constexpr uint32_t kStageBytes = 2 * kOpBytes;
-  Operand<LA> oa;
-  Operand<LB> ob;
-  oa.init(p.a, p.a_o, p.a_k, m0, wm * 128, base);
-  ob.init(p.b, p.b_o, p.b_k, n0, wn * 128, base + kOpBytes);
-  const int KT = p.k / kDepth;
-  // Load i (0..15) of K tile t into stage st; past the last tile the last
-  // tile is loaded again (in bounds; nothing reads it).
-  auto issue = [&](int t, int st, int i) {
-    const int tt = t < KT ? t : KT - 1;
-    const uint32_t sb = base + st * kStageBytes;
-    if (i < 8)
-      oa.load(tt, sb, i);
-    else
-      ob.load(tt, sb + kOpBytes, i - 8);
+  const uint32_t ra = (uint32_t)(uintptr_t)lds, rb = ra + kRingBytes;
+  const int nk = p.k / kDepthD;  // even
+  Ring<LA> A;
+  Ring<LB> B;
+  if constexpr (LA == kK)
+    A.init(p.a, p.a_o, m0, wm * 128, ra, nk);
+  else
+    A.init(p.a, p.a_k, m0, wm * 128, ra, nk);
+  if constexpr (LB == kK)
+    B.init(p.b, p.b_o, n0, wn * 128, rb, nk);
+  else
+    B.init(p.b, p.b_k, n0, wn * 128, rb, nk);
+  // The loads of step S of tile tau that issue after product Q.
+  auto loads_at = [&](int tau, auto S, auto PARI, auto Q) {
+    constexpr int st = S, par = PARI, q = Q;
+    static_for<4>([&](auto J) {
+      if constexpr (J < ring_loads<LA>(par, st) && ring_slot<LA>(0, J) == q) A.template step_load<st, par, J>(tau);
+      if constexpr (J < ring_loads<LB>(par, st) && ring_slot<LB>(1, J) == q) B.template step_load<st, par, J>(tau);
+    });
   };
-#pragma unroll
-  for (int i = 0; i < 16; ++i) issue(0, 0, i);
-  wait_and_meet<0>();
+  // The prologue issues what the steps of tiles -4 .. -1 would have (loads
+  // of tiles before 0 left out), in the same order, so that every wait count
+  // of the sweep holds from its first barrier.
+  auto virtual_step = [&](auto TAU, auto S) {
+    constexpr int tau = TAU, st = S;
+    using Par = std::integral_constant<int, ((tau % 2) + 2) % 2>;
+    static_for<16>([&](auto Q) {
+      static_for<4>([&](auto J) {
+        if constexpr (J < ring_loads<LA>(Par::value, st) && ring_slot<LA>(0, J) == Q && ring_target<LA>(tau, st) >= 0)
+          A.template step_load<st, Par::value, J>(tau);
+        if constexpr (J < ring_loads<LB>(Par::value, st) && ring_slot<LB>(1, J) == Q && ring_target<LB>(tau, st) >= 0)
+          B.template step_load<st, Par::value, J>(tau);
+      });
+    });
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  static_for<4>([&](auto T) {
+    using Tau = std::integral_constant<int, T - 4>;
+    virtual_step(Tau{}, S0{});
+    if constexpr (T == 3) wait_and_meet<mid_wait<LA, LB>(11)>();  // the middle of tile -1: tile 0 has landed
+    virtual_step(Tau{}, S1{});
+  });
   bf16x8 af[2][4], bf[2][4];
   static_for<4>([&](auto I) {
-    af[0][I] = oa.template frag<I, 0>(0);
-    bf[0][I] = ob.template frag<I, 0>(0);
+    af[0][I] = A.template frag<I, 0, 0>(0);
+    bf[0][I] = B.template frag<I, 0, 0>(0);
   });
-  for (int kt = 0; kt < KT; ++kt) {
-    const int st = kt & 1;
-    const uint32_t so = st * kStageBytes;
-    static_for<4>([&](auto KKI) {
-      constexpr int kk = KKI, s = kk & 1;
+  for (int t0 = 0; t0 < nk; t0 += 2) {
+    static_for<2>([&](auto PARI) {
+      constexpr int par = PARI;
+      const int t = t0 + par;
+      // Step 0: products of (t, 0); fragments of (t, 1).
       __builtin_amdgcn_sched_barrier(0);
       static_for<16>([&](auto Q) {
         constexpr int q = Q;
-        acc[q / 4][q % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][q / 4], bf[s][q % 4], acc[q / 4][q % 4], 0, 0, 0);
-        constexpr int slot = 16 * kk + q;
-        if constexpr (slot % 3 == 0 && slot / 3 < 16) issue(kt + 1, st ^ 1, slot / 3);
-        if constexpr (kk < 3 && q % 2 == 0) {
-          constexpr int r = q / 2;  // fragments of step kk + 1: a0 b0 a1 b1 ...
+        acc[q / 4][q % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][q / 4], bf[0][q % 4], acc[q / 4][q % 4], 0, 0, 0);
+        loads_at(t, S0{}, PARI, Q);
+        if constexpr (q % 2 == 0) {
+          constexpr int r = q / 2;  // a0 b0 a1 b1 ...
           if constexpr (r % 2 == 0)
-            af[s ^ 1][r / 2] = oa.template frag<r / 2, kk + 1>(so);
+            af[1][r / 2] = A.template frag<r / 2, 1, par>(t);
           else
-            bf[s ^ 1][r / 2] = ob.template frag<r / 2, kk + 1>(so);
+            bf[1][r / 2] = B.template frag<r / 2, 1, par>(t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // Tile t + 1 has landed (every wave's share), and every wave is done
+      // reading the stage (slot) the next loads fill.
+      wait_and_meet<mid_wait<LA, LB>(10 + par)>();
+      // Step 1: products of (t, 1); fragments of (t + 1, 0) (past the last
+      // tile, bytes nothing uses).
+      static_for<16>([&](auto Q) {
+        constexpr int q = Q;
+        acc[q / 4][q % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][q / 4], bf[1][q % 4], acc[q / 4][q % 4], 0, 0, 0);
+        loads_at(t, S1{}, PARI, Q);
+        if constexpr (q % 2 == 0) {
+          constexpr int r = q / 2;
+          if constexpr (r % 2 == 0)
+            af[0][r / 2] = A.template frag<r / 2, 0, 1 - par>(t + 1);
+          else
+            bf[0][r / 2] = B.template frag<r / 2, 0, 1 - par>(t + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
       });
     });
-    // The next tile's loads (this wave's) are done; after the barrier every
-    // wave's are, and every wave has finished reading this stage.
-    wait_and_meet<0>();
-    if (kt + 1 < KT)
-      static_for<4>([&](auto I) {
-        af[0][I] = oa.template frag<I, 0>(so ^ kStageBytes);
-        bf[0][I] = ob.template frag<I, 0>(so ^ kStageBytes);
-      });
   }
-  // Every wave has passed the last barrier with no LDS access outstanding:
-  // the stages are free for the epilogue.
+  // No load may land in LDS once the epilogue uses it.
+  wait_and_meet<0>();
 }
 
 // ---- the interior tiles' epilogue: through LDS, whole lines out ------------------
