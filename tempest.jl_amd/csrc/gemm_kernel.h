@@ -84,21 +84,35 @@ __device__ __forceinline__ u32x2 pack4(const uint16_t (&h)[4]) {
   return u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
 }
 
-// tanh(u) = 1 - 2 / (exp(2u) + 1): one exponential and one reciprocal, exact
-// at both ends (exp overflows to inf: 1; underflows to 0: -1); its few-ulp
-// error is far below the bf16 rounding every caller applies after.
-__device__ __forceinline__ float fast_tanh(float u) {
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * u) + 1.0f);
+// GELU, tanh form (test/fixtures/programs.jl:19), and its derivative.  With
+// u = c (x + a x^3) and s = 1 / (1 + e^(2u)):
+//   1 + tanh u = 2 (1 - s),  1 - tanh^2 u = 4 s (1 - s),  so
+//   gelu(x) = x (1 - s),  gelu'(x) = (1 - s) (1 + 2 c x s (1 + 3 a x^2)),
+// and 1 - s = e^(2u) s, which has no cancellation for negative x.  e^(2u) is
+// exp2(x (k1 + k2 x^2)) with log2(e) folded into the constants, the exponent
+// capped at 126 so that e stays finite: there e s rounds to 1 and s is about
+// 2^-126, so gelu(x) = x and gelu'(x) = 1 for large x; for large negative x
+// e underflows to 0 and both are 0.  One exponential, one reciprocal and
+// eight or nine other operations per element (the epilogues that apply them
+// are bound by vector instructions).
+struct GeluParts {
+  float om;  // 1 - s
+  float s;
+};
+__device__ __forceinline__ GeluParts gelu_parts(float x, float x2) {
+  constexpr float k1 = 2.30220831f;   // 2 c log2(e), c = 0.7978846
+  constexpr float k2 = 0.102943245f;  // 2 c a log2(e), a = 0.044715
+  const float e = __builtin_amdgcn_exp2f(fminf(x * fmaf(k2, x2, k1), 126.0f));
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  return GeluParts{e * s, s};
 }
-
-// GELU, tanh form (test/fixtures/programs.jl:19), and its derivative.
-__device__ __forceinline__ float gelu(float x) {
-  const float t = fast_tanh(0.7978846f * (x + 0.044715f * x * x * x));
-  return 0.5f * x * (1.0f + t);
-}
+__device__ __forceinline__ float gelu(float x) { return x * gelu_parts(x, x * x).om; }
 __device__ __forceinline__ float gelu_grad(float x) {
-  const float t = fast_tanh(0.7978846f * (x + 0.044715f * x * x * x));
-  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * 0.7978846f * (1.0f + 3.0f * 0.044715f * x * x);
+  constexpr float k3 = 1.5957692f;    // 2 c
+  constexpr float k4 = 0.214064459f;  // 6 c a
+  const float x2 = x * x;
+  const GeluParts g = gelu_parts(x, x2);
+  return g.om * fmaf(g.s, x * fmaf(k4, x2, k3), 1.0f);
 }
 
 // ---- global -> registers -> LDS ----------------------------------------------
