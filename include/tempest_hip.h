@@ -28,7 +28,8 @@ enum {
   TH_E_ARGUMENT = -1,     /* shapes, strides or alignment a kernel cannot take */
   TH_E_STATE = -2,        /* no th_init, or a handle used after release        */
   TH_E_UNSUPPORTED = -3,  /* a case this build does not implement              */
-  TH_E_MEMORY = -4        /* an allocation failed                              */
+  TH_E_MEMORY = -4,       /* an allocation failed                              */
+  TH_E_COMPILE = -5       /* a generated kernel failed to compile              */
 };
 
 typedef struct th_launch th_launch; /* one claim's built launch: kernels + arguments */
@@ -207,6 +208,124 @@ int th_build_layernorm_fwd(int64_t rows, int32_t n, int64_t ld, float eps, const
 /* The sum of `count` floats into one (a full reduction, the cuTile `:full`
  * sketch, ext/cuTileExt/cuTileExt.jl:638-641): values 0 x, 1 out. */
 int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out);
+
+/* ---- op class (a), generated: the floor for any pointwise or reduction group
+ *
+ * A group is a domain of up to four axes (axis 0 fastest), its values (dense
+ * one-dimensional buffers), its terms and, for a reduction group, its folds
+ * over the axes marked in `reduced`, run in phases.  The library writes a
+ * gfx950 kernel for the group (one per phase when the folds' positions split
+ * among workgroups), compiles it at run time and keeps the code object in a
+ * content-keyed cache on disk ($TEMPEST_HIP_CACHE, else $XDG_CACHE_HOME/
+ * tempest_hip, else ~/.cache/tempest_hip).  Replaces the floor's generated
+ * kernels: scalar_kernel (codegen/scalar.jl:186-250), split_kernels
+ * (scalar.jl:284-348), floor_launch / floor_split / merge_lanes
+ * (ext/CUDAExt.jl:926-1017) and the kernel cache (runtime/cache.jl). */
+
+#define TH_FLOOR_RANK 4
+
+enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1 };
+
+/* Terms (Load, Lit, Ix, Stat, Apply of src/Compiler/IR):
+ *   TH_TERM_LOAD   element index(i) of value `ref`, widened to fp32
+ *   TH_TERM_LIT    the number `lit`
+ *   TH_TERM_INDEX  the fp32 value of the affine expression `index` of the
+ *                  domain's zero-based positions
+ *   TH_TERM_STAT   fold `ref`'s result, as `observe` reads it
+ *   TH_TERM_APPLY  function `fn` of terms args[0..arity) (earlier terms) */
+enum { TH_TERM_LOAD = 0, TH_TERM_LIT = 1, TH_TERM_INDEX = 2, TH_TERM_STAT = 3, TH_TERM_APPLY = 4 };
+
+/* Functions, on fp32 (comparisons give 1 or 0; ifelse(c, a, b) takes a where
+ * c != 0; round is to nearest, ties to even; max/min ignore a NaN operand). */
+enum {
+  TH_FN_ADD = 0, TH_FN_SUB, TH_FN_MUL, TH_FN_DIV, TH_FN_NEG, TH_FN_ABS, TH_FN_ABS2, TH_FN_SQRT,
+  TH_FN_EXP, TH_FN_LOG, TH_FN_TANH, TH_FN_SIN, TH_FN_COS, TH_FN_LOG1P, TH_FN_EXPM1, TH_FN_POW,
+  TH_FN_MAX, TH_FN_MIN, TH_FN_LT, TH_FN_LE, TH_FN_GT, TH_FN_GE, TH_FN_EQ, TH_FN_NE,
+  TH_FN_IFELSE, TH_FN_ROUND, TH_FN_FLOOR, TH_FN_CEIL, TH_FN_SIGN, TH_FN_CLAMP, TH_FN_FMA,
+  TH_FN_INV, TH_FN_COUNT
+};
+
+/* Folds (src/Compiler/IR/folds.jl:66-309), accumulating in fp32:
+ *   TH_FOLD_SUM, _PROD, _MAX, _MIN  of the body
+ *   TH_FOLD_EXP     Relative{Exponential}: the maximum m of the body y and
+ *                   the sum of weight * exp(y - lse_shift(m)) (weight 1 when
+ *                   the fold's weight is -1)
+ *   TH_FOLD_SQUARE  Relative{Square}: the mean of the body and the sum of
+ *                   squared deviations from it (Chan's combination) */
+enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_FOLD_SQUARE };
+
+/* What a Stat term reads of a fold: the value (SUM, PROD, MAX, MIN); the
+ * statistic (EXP: m, SQUARE: the mean); the sum (EXP: the weighted sum of
+ * exponentials, SQUARE: the squared deviations); or, for EXP, the log-sum-exp
+ * lse_shift(m) + log(sum) (LOGSUMEXP, folds.jl:263). */
+enum { TH_OBSERVE_VALUE = 0, TH_OBSERVE_STATISTIC = 1, TH_OBSERVE_SUM = 2, TH_OBSERVE_LOGSUMEXP = 3 };
+
+/* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions. */
+typedef struct th_affine {
+  int64_t constant;
+  int64_t coeff[TH_FLOOR_RANK];
+} th_affine;
+
+typedef struct th_floor_value {
+  int32_t dtype;    /* TH_F32 or TH_BF16 */
+  int32_t reserved;
+  int64_t length;   /* elements */
+  void* ptr;
+} th_floor_value;
+
+typedef struct th_term {
+  int32_t op;       /* TH_TERM_* */
+  int32_t fn;       /* TH_FN_*, for TH_TERM_APPLY */
+  int32_t args[3];
+  int32_t ref;      /* the value of a load, the fold of a statistic */
+  int32_t observe;  /* TH_OBSERVE_*, for TH_TERM_STAT */
+  float lit;
+  th_affine index;  /* a load's element, an index term's expression */
+} th_term;
+
+typedef struct th_fold {
+  int32_t kind;     /* TH_FOLD_* */
+  int32_t phase;    /* >= 1; a fold's terms read statistics of earlier phases only */
+  int32_t body;     /* term */
+  int32_t weight;   /* term, or -1; TH_FOLD_EXP only */
+} th_fold;
+
+/* Output: value[index(i)] = term, rounded to the value's type.  `full` outputs
+ * are written at every position of the domain; the others once per item of a
+ * reduction group, with the folded positions at zero (a fold's result stored
+ * at its placement, or a statistic of it). */
+typedef struct th_output {
+  int32_t value;
+  int32_t term;
+  int32_t full;
+  int32_t reserved;
+  th_affine index;
+} th_output;
+
+typedef struct th_floor_desc {
+  int32_t kind;                       /* TH_GROUP_* */
+  int32_t rank;                       /* 1..TH_FLOOR_RANK */
+  int64_t extents[TH_FLOOR_RANK];
+  uint32_t reduced;                   /* bit k: axis k is folded */
+  int32_t n_values, n_terms, n_folds, n_outputs;
+  int32_t reserved;
+  const th_floor_value* values;
+  const th_term* terms;               /* in order: args refer to earlier terms */
+  const th_fold* folds;
+  const th_output* outputs;
+} th_floor_desc;
+
+/* The group's launch.  Values: the group's values, in order.  Every address
+ * the terms and outputs reach over the domain must lie inside its value. */
+int th_build_floor(const th_floor_desc* desc, th_launch** host_out);
+
+/* The generated source and how the group maps onto the device (a comment at
+ * its head); needs no device.  *host_needed gets the size with the final NUL. */
+int th_floor_source(const th_floor_desc* desc, char* host_out, size_t capacity, size_t* host_needed);
+
+/* Generate and compile the group's kernels into the code-object cache,
+ * without a device (the "does it build" check of a group). */
+int th_floor_compile(const th_floor_desc* desc);
 
 /* ---- the small program of config 1 -------------------------------------- */
 

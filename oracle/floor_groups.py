@@ -1,0 +1,144 @@
+"""TEST INFRASTRUCTURE ONLY: the Float64 meaning of a floor group.
+
+A group (tempest_hip.floor.FloorGroup.spec()) is evaluated as the reference's
+plan-free interpreter evaluates the program it came from
+(src/Compiler/program/interpret.jl): every term over the whole domain at
+once, in Float64, each fold over the group's folded axes by the fold algebra
+of src/Compiler/IR/folds.jl (a sum, product, maximum or minimum; the
+exponential fold's maximum m and sum of weight * exp(y - lse_shift(m)),
+folds.jl:126-133,160-176,193-194; the square fold's mean and sum of squared
+deviations, folds.jl:135-192), phase after phase, then the outputs: a full
+output at every position of the domain, the others once per item with the
+folded positions at zero (scalar.jl:232-248).  Written values are rounded
+once to their type (Float32, or bfloat16 to nearest, ties to even).
+
+Parity pinned by (tests/test_oracle_floor.py): each fold kind against the
+sequential restatement in ``oracle.folds`` on the same elements (lift, then
+combine earlier-first); each of the reference's fixture programs expressed as
+groups against a closed form written independently with numpy
+(test/fixtures/programs.jl:60-90 and the row programs); the reference's
+doctest sum(abs2, [1, 2, 3, 4]) == 30 (runtime/compile.jl:35-40); a planted
+mistake (the exponential fold without its rebase) is caught.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .data import bf16_round
+
+_UNARY = {
+    "neg": np.negative, "abs": np.abs, "abs2": np.square, "sqrt": np.sqrt, "exp": np.exp, "log": np.log,
+    "tanh": np.tanh, "sin": np.sin, "cos": np.cos, "log1p": np.log1p, "expm1": np.expm1,
+    "round": np.rint, "floor": np.floor, "ceil": np.ceil, "sign": np.sign, "inv": lambda x: 1.0 / x,
+}
+_BINARY = {
+    "+": np.add, "-": np.subtract, "*": np.multiply, "/": np.divide, "^": np.power,
+    "max": np.fmax, "min": np.fmin,
+    "<": lambda a, b: (a < b) * 1.0, "<=": lambda a, b: (a <= b) * 1.0, ">": lambda a, b: (a > b) * 1.0,
+    ">=": lambda a, b: (a >= b) * 1.0, "==": lambda a, b: (a == b) * 1.0, "!=": lambda a, b: (a != b) * 1.0,
+}
+
+
+def _ternary(fn, a, b, c):
+    if fn == "ifelse":
+        return np.where(a != 0, b, c)
+    if fn == "clamp":
+        return np.where(a > c, c, np.where(a < b, b, a))
+    if fn == "fma":
+        return a * b + c
+    raise ValueError(fn)
+
+
+def fold_reduce(kind: str, y: np.ndarray, g, axes: tuple):
+    """A fold's state over ``axes`` of ``y`` (keepdims), as a dict of observations."""
+    if kind == "sum":
+        return {"value": y.sum(axis=axes, keepdims=True)}
+    if kind == "prod":
+        return {"value": y.prod(axis=axes, keepdims=True)}
+    if kind == "max":
+        return {"value": y.max(axis=axes, keepdims=True, initial=-np.inf)}
+    if kind == "min":
+        return {"value": y.min(axis=axes, keepdims=True, initial=np.inf)}
+    if kind == "exp":
+        m = y.max(axis=axes, keepdims=True, initial=-np.inf)
+        sh = np.where(np.isfinite(m), m, 0.0)
+        w = 1.0 if g is None else g
+        s = (w * np.exp(y - sh)).sum(axis=axes, keepdims=True)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            return {"statistic": m, "sum": s, "logsumexp": sh + np.log(s)}
+    if kind == "square":
+        n = np.prod([y.shape[a] for a in axes]) if y.size else 0
+        with np.errstate(invalid="ignore"):
+            mean = y.sum(axis=axes, keepdims=True) / n
+        return {"statistic": mean, "sum": ((y - mean) ** 2).sum(axis=axes, keepdims=True)}
+    raise ValueError(kind)
+
+
+def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) -> dict[str, np.ndarray]:
+    """The group's written values, given every value's contents (1-D);
+    rounded to the values' types, or Float64 with ``rounded=False``."""
+    ext = tuple(spec["extents"])
+    rank = len(ext)
+    idx = np.indices(ext, dtype=np.int64)  # idx[k]: position along axis k
+    reduced = tuple(spec["reduced"])
+    vals = list(spec["values"])
+    out = {o["value"]: np.array(arrays[o["value"]], dtype=np.float64, copy=True) for o in spec["outputs"]}
+
+    def addr(t, at):
+        a = np.full(at[0].shape, t["constant"], dtype=np.int64)
+        for k in range(rank):
+            if t["coeffs"][k]:
+                a = a + t["coeffs"][k] * at[k]
+        return a
+
+    stats: dict[int, dict] = {}
+
+    def term(i, at, memo):
+        if i in memo:
+            return memo[i]
+        t = spec["terms"][i]
+        op = t["op"]
+        if op == "load":
+            r = np.asarray(arrays[vals[t["ref"]]], dtype=np.float64)[addr(t, at)]
+        elif op == "lit":
+            r = np.float64(t["lit"])
+        elif op == "index":
+            r = addr(t, at).astype(np.float64)
+        elif op == "stat":
+            r = stats[t["ref"]][t["observe"]]
+        else:
+            a = [term(j, at, memo) for j in t["args"]]
+            fn = t["fn"]
+            with np.errstate(all="ignore"):
+                r = _UNARY[fn](a[0]) if len(a) == 1 else _BINARY[fn](*a) if len(a) == 2 else _ternary(fn, *a)
+        memo[i] = r
+        return r
+
+    full_at = [idx[k] for k in range(rank)]
+    if spec["kind"] == "reduction":
+        for phase in sorted({f["phase"] for f in spec["folds"]}):
+            memo: dict = {}
+            for k, f in enumerate(spec["folds"]):
+                if f["phase"] != phase:
+                    continue
+                y = np.broadcast_to(term(f["body"], full_at, memo), ext).astype(np.float64)
+                g = None if f["weight"] < 0 else np.broadcast_to(term(f["weight"], full_at, memo), ext)
+                stats[k] = fold_reduce(f["kind"], y, g, reduced)
+    # Once outputs: the folded positions at zero, the kept ones everywhere.
+    once_at = [idx[k][tuple(slice(0, 1) if j in reduced else slice(None) for j in range(rank))]
+               for k in range(rank)]
+    memo_full: dict = {}
+    memo_once: dict = {}
+    for o in spec["outputs"]:
+        at = full_at if o["full"] else once_at
+        memo = memo_full if o["full"] else memo_once
+        v = np.broadcast_to(term(o["term"], at, memo), at[0].shape)
+        out[o["value"]][addr(o, at).ravel()] = v.ravel()
+    if not rounded:
+        return out
+    result = {}
+    for n, a in out.items():
+        dt = spec["values"][n][0]
+        result[n] = bf16_round(a.astype(np.float32)) if dt == "bf16" else a.astype(np.float32)
+    return result
+

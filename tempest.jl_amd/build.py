@@ -73,8 +73,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
         if out.strip() and verbose:
             print(out, file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
+    # hiprtc compiles the generated floor kernels at run time.
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *[str(o) for o, _ in results]]
+           *[str(o) for o, _ in results], "-lhiprtc"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"link failed:\n{p.stdout}{p.stderr}")

@@ -55,7 +55,10 @@ int device_alloc(size_t bytes, void** out) {
 
 int launch_kernel(const Kernel& k, hipStream_t s) {
   void* params[1] = {const_cast<unsigned char*>(k.args)};
-  hipError_t e = hipLaunchKernel(k.fn, k.grid, k.block, params, k.shmem, s);
+  hipError_t e = k.module
+                     ? hipModuleLaunchKernel(k.module, k.grid.x, k.grid.y, k.grid.z, k.block.x, k.block.y,
+                                             k.block.z, k.shmem, s, params, nullptr)
+                     : hipLaunchKernel(k.fn, k.grid, k.block, params, k.shmem, s);
   if (e != hipSuccess) return hip_fail(e, k.name);
   return TH_OK;
 }
@@ -326,7 +329,9 @@ namespace th {
 
 static hipKernelNodeParams node_params(const Kernel& k, void** params) {
   hipKernelNodeParams p{};
-  p.func = const_cast<void*>(k.fn);
+  // A module function stands where a kernel's host stub would: the graph
+  // resolves it as the function itself.
+  p.func = k.module ? static_cast<void*>(k.module) : const_cast<void*>(k.fn);
   p.gridDim = k.grid;
   p.blockDim = k.block;
   p.sharedMemBytes = k.shmem;

@@ -55,6 +55,9 @@ int require_ready();
 // argument struct, kept as bytes so that values can be repointed in place.
 struct Kernel {
   const void* fn = nullptr;
+  // A kernel compiled at run time (the generated floor): its module function,
+  // launched through the module API; `fn` is then null.
+  hipFunction_t module = nullptr;
   const char* name = "";
   dim3 grid{1, 1, 1};
   dim3 block{1, 1, 1};
@@ -115,6 +118,22 @@ class Builder {
   // Value `v` must stay aligned to `bytes` when it is repointed.
   void align(int v, uint32_t bytes) { l_->align[v] = std::max(l_->align[v], bytes); }
   void own(void* p) { l_->owned.push_back(p); }
+  // A kernel compiled at run time: `fn` is a module function.
+  template <class Args>
+  int module_kernel(hipFunction_t fn, const char* name, dim3 grid, dim3 block, uint32_t shmem,
+                    const Args& a, size_t bytes) {
+    static_assert(sizeof(Args) <= sizeof(Kernel::args), "kernel argument struct too large");
+    Kernel k;
+    k.module = fn;
+    k.name = name;
+    k.grid = grid;
+    k.block = block;
+    k.shmem = shmem;
+    std::memcpy(k.args, &a, bytes);
+    k.args_size = (uint32_t)bytes;
+    l_->kernels.push_back(k);
+    return static_cast<int>(l_->kernels.size()) - 1;
+  }
   void work(double bytes, double flops, int64_t blocks) {
     l_->work.bytes = bytes;
     l_->work.flops = flops;

@@ -1,0 +1,317 @@
+"""Op class (a), generated: the floor for any pointwise or reduction group.
+
+The reference's floor realizes any group one item at a time from the group's
+terms (src/Compiler/codegen/scalar.jl:1-250): ``Load`` (an element of a value
+at an affine position), ``Lit``, ``Ix`` (a position as a number), ``Stat``
+(a fold's result) and ``Apply`` (a function of terms); a reduction group
+folds some of its axes, in phases, and writes outputs at every position
+(``full``) or once per item.  ``FloorGroup`` states such a group and hands it
+to ``th_build_floor`` (include/tempest_hip.h), which writes a gfx950 kernel
+for it, compiles it at run time and caches the code object on disk.
+
+Axes are the reference's column-major ones (axis 0 fastest); positions are
+zero-based, so an affine index of a dense n x m value at (i0, i1) is
+``i0 + n * i1``.
+
+    g = FloorGroup("reduction", (n, m), reduced=(0,))
+    x = g.value("x", "f32", n * m)
+    ...
+    e = g.fold("exp", g.load("x", (1, n)))          # Relative{Exponential}
+    g.output("lse", e.logsumexp, (0, 1), full=False)
+    launch = g.build({"x": ptr_x, "lse": ptr_lse})
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Sequence
+
+from . import _lib
+from ._lib import call
+from .launch import Launch
+from .runtime import Group
+
+RANK = 4
+
+GROUP = {"pointwise": 0, "reduction": 1}
+TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4}
+FN = {name: k for k, name in enumerate([
+    "+", "-", "*", "/", "neg", "abs", "abs2", "sqrt", "exp", "log", "tanh", "sin", "cos", "log1p", "expm1", "^",
+    "max", "min", "<", "<=", ">", ">=", "==", "!=", "ifelse", "round", "floor", "ceil", "sign", "clamp", "fma",
+    "inv"])}
+ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", ">", ">=", "==", "!=") else
+                3 if name in ("ifelse", "clamp", "fma") else 1) for name in FN}
+FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5}
+OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}
+DTYPE = {"f32": 0, "bf16": 1}
+
+
+class Affine(ctypes.Structure):
+    _fields_ = [("constant", _lib.c_i64), ("coeff", _lib.c_i64 * RANK)]
+
+
+class FloorValue(ctypes.Structure):
+    _fields_ = [("dtype", _lib.c_i32), ("reserved", _lib.c_i32), ("length", _lib.c_i64), ("ptr", _lib.c_void_p)]
+
+
+class TermStruct(ctypes.Structure):
+    _fields_ = [("op", _lib.c_i32), ("fn", _lib.c_i32), ("args", _lib.c_i32 * 3), ("ref", _lib.c_i32),
+                ("observe", _lib.c_i32), ("lit", _lib.c_f32), ("index", Affine)]
+
+
+class FoldStruct(ctypes.Structure):
+    _fields_ = [("kind", _lib.c_i32), ("phase", _lib.c_i32), ("body", _lib.c_i32), ("weight", _lib.c_i32)]
+
+
+class OutputStruct(ctypes.Structure):
+    _fields_ = [("value", _lib.c_i32), ("term", _lib.c_i32), ("full", _lib.c_i32), ("reserved", _lib.c_i32),
+                ("index", Affine)]
+
+
+class FloorDesc(ctypes.Structure):
+    _fields_ = [("kind", _lib.c_i32), ("rank", _lib.c_i32), ("extents", _lib.c_i64 * RANK),
+                ("reduced", ctypes.c_uint32), ("n_values", _lib.c_i32), ("n_terms", _lib.c_i32),
+                ("n_folds", _lib.c_i32), ("n_outputs", _lib.c_i32), ("reserved", _lib.c_i32),
+                ("values", ctypes.POINTER(FloorValue)), ("terms", ctypes.POINTER(TermStruct)),
+                ("folds", ctypes.POINTER(FoldStruct)), ("outputs", ctypes.POINTER(OutputStruct))]
+
+
+_SIGNATURES = {
+    "th_build_floor": [ctypes.POINTER(FloorDesc), _lib.P(_lib.c_void_p)],
+    "th_floor_source": [ctypes.POINTER(FloorDesc), _lib.c_char_p, _lib.c_size, _lib.P(_lib.c_size)],
+    "th_floor_compile": [ctypes.POINTER(FloorDesc)],
+}
+_lib.SIGNATURES.update(_SIGNATURES)
+
+
+def _call(name: str, *args) -> None:
+    # The library may have been loaded before this module added its entries.
+    f = getattr(_lib.load(), name)
+    if f.argtypes != _SIGNATURES[name]:
+        f.argtypes, f.restype = _SIGNATURES[name], _lib.c_int
+    call(name, *args)
+
+
+class Term:
+    """A term of a FloorGroup; arithmetic on terms (and numbers) applies."""
+
+    __slots__ = ("group", "index")
+
+    def __init__(self, group: "FloorGroup", index: int):
+        self.group = group
+        self.index = index
+
+    def _f(self, fn, *others):
+        return self.group.apply(fn, self, *others)
+
+    def __add__(self, o): return self._f("+", o)
+    def __radd__(self, o): return self.group.apply("+", o, self)
+    def __sub__(self, o): return self._f("-", o)
+    def __rsub__(self, o): return self.group.apply("-", o, self)
+    def __mul__(self, o): return self._f("*", o)
+    def __rmul__(self, o): return self.group.apply("*", o, self)
+    def __truediv__(self, o): return self._f("/", o)
+    def __rtruediv__(self, o): return self.group.apply("/", o, self)
+    def __neg__(self): return self._f("neg")
+    def __pow__(self, o): return self._f("^", o)
+
+
+@dataclass
+class Fold:
+    group: "FloorGroup"
+    number: int
+    kind: str
+
+    def _stat(self, observe: str) -> Term:
+        return self.group._term("stat", ref=self.number, observe=OBSERVE[observe])
+
+    @property
+    def value(self) -> Term:
+        """A plain fold's result (sum, prod, max, min)."""
+        return self._stat("value")
+
+    @property
+    def statistic(self) -> Term:
+        """The exponential fold's maximum; the square fold's mean."""
+        return self._stat("statistic")
+
+    @property
+    def sum(self) -> Term:
+        """The exponential fold's weighted sum of exp(y - lse_shift(m)); the
+        square fold's sum of squared deviations."""
+        return self._stat("sum")
+
+    @property
+    def logsumexp(self) -> Term:
+        return self._stat("logsumexp")
+
+
+def _affine(coeffs: Sequence[int] | None, constant: int, rank: int) -> tuple:
+    c = list(coeffs or ())
+    if len(c) > rank:
+        raise ValueError(f"{len(c)} coefficients for a rank-{rank} domain")
+    return (int(constant), tuple(int(x) for x in c) + (0,) * (RANK - len(c)))
+
+
+@dataclass
+class FloorGroup:
+    """A pointwise or reduction group of the floor (scalar.jl:186-250)."""
+
+    kind: str
+    extents: tuple
+    reduced: tuple = ()
+    name: str = "floor group"
+    values: dict = field(default_factory=dict)      # name -> (dtype, length), in value order
+    terms: list = field(default_factory=list)       # (op, fn, args, ref, observe, lit, affine)
+    folds: list = field(default_factory=list)       # (kind, phase, body, weight)
+    outputs: list = field(default_factory=list)     # (value, term, full, affine)
+
+    def __post_init__(self):
+        if self.kind not in GROUP:
+            raise ValueError(f"unknown group kind {self.kind!r}")
+        self.extents = tuple(int(e) for e in self.extents)
+        if not 1 <= len(self.extents) <= RANK:
+            raise ValueError("a group's domain has 1 to 4 axes")
+        self.reduced = tuple(int(k) for k in self.reduced)
+
+    # -- building the group -------------------------------------------------------
+
+    def value(self, name: str, dtype: str, length: int) -> str:
+        if dtype not in DTYPE:
+            raise ValueError(f"values are f32 or bf16, not {dtype!r}")
+        self.values[name] = (dtype, int(length))
+        return name
+
+    def _term(self, op: str, fn: int = 0, args=(), ref: int = 0, observe: int = 0, lit: float = 0.0,
+              affine=(0, (0,) * RANK)) -> Term:
+        self.terms.append((TERM[op], fn, tuple(args) + (0,) * (3 - len(args)), ref, observe, float(lit), affine))
+        return Term(self, len(self.terms) - 1)
+
+    def _as_term(self, x) -> Term:
+        if isinstance(x, Term):
+            if x.group is not self:
+                raise ValueError("a term of another group")
+            return x
+        return self.lit(float(x))
+
+    def load(self, name: str, coeffs: Sequence[int] | None = None, constant: int = 0) -> Term:
+        """Element ``constant + sum(coeffs[k] * i_k)`` of value ``name``."""
+        ref = list(self.values).index(name)
+        return self._term("load", ref=ref, affine=_affine(coeffs, constant, len(self.extents)))
+
+    def lit(self, x: float) -> Term:
+        return self._term("lit", lit=x)
+
+    def index(self, coeffs: Sequence[int], constant: int = 0) -> Term:
+        """The number ``constant + sum(coeffs[k] * i_k)`` (Ix)."""
+        return self._term("index", affine=_affine(coeffs, constant, len(self.extents)))
+
+    def apply(self, fn: str, *args) -> Term:
+        if fn not in FN:
+            raise ValueError(f"unknown function {fn!r}")
+        if len(args) != ARITY[fn]:
+            raise ValueError(f"{fn} takes {ARITY[fn]} arguments")
+        ts = [self._as_term(a) for a in args]
+        return self._term("apply", fn=FN[fn], args=[t.index for t in ts])
+
+    def fold(self, kind: str, body, weight=None, phase: int = 1) -> Fold:
+        if self.kind != "reduction":
+            raise ValueError("only a reduction group folds")
+        if kind not in FOLD:
+            raise ValueError(f"unknown fold {kind!r}")
+        b = self._as_term(body).index
+        w = -1 if weight is None else self._as_term(weight).index
+        self.folds.append((FOLD[kind], int(phase), b, w))
+        return Fold(self, len(self.folds) - 1, kind)
+
+    def output(self, name: str, term, coeffs: Sequence[int] | None = None, constant: int = 0,
+               full: bool = True) -> None:
+        v = list(self.values).index(name)
+        self.outputs.append((v, self._as_term(term).index, int(bool(full)),
+                             _affine(coeffs, constant, len(self.extents))))
+
+    # -- the ABI ---------------------------------------------------------------------
+
+    def _desc(self, ptrs: Sequence[int]):
+        nv, nt, nf, no = len(self.values), len(self.terms), len(self.folds), len(self.outputs)
+        values = (FloorValue * nv)()
+        for k, ((dt, n), p) in enumerate(zip(self.values.values(), ptrs)):
+            values[k].dtype, values[k].length, values[k].ptr = DTYPE[dt], n, p
+        terms = (TermStruct * max(nt, 1))()
+        for k, (op, fn, args, ref, obs, lit, (c0, cs)) in enumerate(self.terms):
+            t = terms[k]
+            t.op, t.fn, t.ref, t.observe, t.lit = op, fn, ref, obs, lit
+            t.args[:] = list(args)
+            t.index.constant = c0
+            t.index.coeff[:] = list(cs)
+        folds = (FoldStruct * max(nf, 1))()
+        for k, (kind, phase, body, weight) in enumerate(self.folds):
+            folds[k].kind, folds[k].phase, folds[k].body, folds[k].weight = kind, phase, body, weight
+        outs = (OutputStruct * max(no, 1))()
+        for k, (v, term, full, (c0, cs)) in enumerate(self.outputs):
+            outs[k].value, outs[k].term, outs[k].full = v, term, full
+            outs[k].index.constant = c0
+            outs[k].index.coeff[:] = list(cs)
+        d = FloorDesc()
+        d.kind, d.rank = GROUP[self.kind], len(self.extents)
+        d.extents[:] = list(self.extents) + [1] * (RANK - len(self.extents))
+        d.reduced = sum(1 << k for k in self.reduced)
+        d.n_values, d.n_terms, d.n_folds, d.n_outputs = nv, nt, nf, no
+        d.values, d.terms, d.folds, d.outputs = values, terms, folds, outs
+        return d, (values, terms, folds, outs)
+
+    def _stand_in(self) -> list[int]:
+        # Addresses for a build without a device: 256-byte aligned, as device
+        # allocations are, so the source is the one a device build writes.
+        return [(k + 1) << 20 for k in range(len(self.values))]
+
+    def source(self, ptrs: Sequence[int] | None = None) -> str:
+        """The generated HIP source (needs no device)."""
+        d, keep = self._desc(ptrs or self._stand_in())
+        need = _lib.c_size()
+        _call("th_floor_source", ctypes.byref(d), None, 0, ctypes.byref(need))
+        buf = ctypes.create_string_buffer(need.value)
+        _call("th_floor_source", ctypes.byref(d), buf, need.value, ctypes.byref(need))
+        return buf.value.decode()
+
+    def compile(self, ptrs: Sequence[int] | None = None) -> None:
+        """Compile into the code-object cache (needs no device)."""
+        d, keep = self._desc(ptrs or self._stand_in())
+        _call("th_floor_compile", ctypes.byref(d))
+
+    def build(self, ptrs: dict[str, int]) -> Launch:
+        """The group's launch over the values at ``ptrs`` (name -> device address)."""
+        order = list(self.values)
+        missing = [n for n in order if n not in ptrs]
+        if missing:
+            raise ValueError(f"{self.name}: no address for {missing}")
+        d, keep = self._desc([int(ptrs[n]) for n in order])
+        out = ctypes.c_void_p()
+        _call("th_build_floor", ctypes.byref(d), ctypes.byref(out))
+        return Launch(out, tuple(order))
+
+    def as_group(self) -> Group:
+        """The group as a kernel of a Program (runtime.Group)."""
+        order = tuple(self.values)
+        writes = tuple(dict.fromkeys(order[v] for v, *_ in self.outputs))
+        reads = tuple(dict.fromkeys(order[self.terms[t][3]] for t in range(len(self.terms))
+                                    if self.terms[t][0] == TERM["load"]))
+        return Group(self.name, order, reads, writes, self.build)
+
+    def spec(self) -> dict:
+        """A plain description of the group (for checkers)."""
+        inv_fn = {v: k for k, v in FN.items()}
+        inv_fold = {v: k for k, v in FOLD.items()}
+        inv_obs = {v: k for k, v in OBSERVE.items()}
+        inv_term = {v: k for k, v in TERM.items()}
+        return {
+            "kind": self.kind, "extents": self.extents, "reduced": self.reduced,
+            "values": dict(self.values),
+            "terms": [{"op": inv_term[op], "fn": inv_fn.get(fn) if op == TERM["apply"] else None,
+                       "args": list(args[:ARITY[inv_fn[fn]]]) if op == TERM["apply"] else [],
+                       "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1])}
+                      for op, fn, args, ref, obs, lit, aff in self.terms],
+            "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w} for k, p, b, w in self.folds],
+            "outputs": [{"value": list(self.values)[v], "term": t, "full": bool(f), "constant": aff[0],
+                         "coeffs": list(aff[1])} for v, t, f, aff in self.outputs],
+        }

@@ -163,3 +163,61 @@ def deltanet(batch: int = 4, heads: int = 16, seq: int = 8192, d: int = 128) -> 
                   lambda x: L.deltanet(batch, heads, seq, *(x[n] for n in names), d=d))
     return Program("deltanet", values, [group], ["q", "k", "v", "a", "beta", "dout"],
                    ["o", "dq", "dk", "dv", "da", "dbeta"])
+
+
+# ---- config 2 through the generated floor ------------------------------------
+
+def _floor_row_program(name: str, rows: int, n: int, row_group) -> Program:
+    """sum(f(x) .* g) and its gradient as the floor forms it: a reduction
+    group over each column (its folds in phases, dx at every position and the
+    column's share of the loss once), then the loss's full fold."""
+    from .floor import FloorGroup
+
+    f32 = torch.float32
+    values = {
+        "x": Value("x", f32, (n, rows), "input"),
+        "g": Value("g", f32, (n, rows), "input"),
+        "loss": Value("loss", f32, (), "result"),
+        "dx": Value("dx", f32, (n, rows), "result"),
+        "r": Value("r", f32, (rows,), "stored"),
+    }
+    g1 = FloorGroup("reduction", (n, rows), reduced=(0,), name=f"{name}: its folds and gradient")
+    for v in ("x", "g", "dx"):
+        g1.value(v, "f32", n * rows)
+    g1.value("r", "f32", rows)
+    row_group(g1, g1.load("x", (1, n)), g1.load("g", (1, n)))
+    g2 = FloorGroup("reduction", (rows,), reduced=(0,), name=f"{name}: the loss")
+    g2.value("r", "f32", rows)
+    g2.value("loss", "f32", 1)
+    g2.output("loss", g2.fold("sum", g2.load("r", (1,))).value, full=False)
+    return Program(name, values, [g1.as_group(), g2.as_group()], ["x", "g"], ["loss", "dx"])
+
+
+def floor_softmax_columns(rows: int, n: int) -> Program:
+    """Config 2a through the generated floor: y = exp.(x .- logsumexp(x; dims = 1))
+    (test/fixtures/programs.jl:8), r = sum(y .* g; dims = 1),
+    dx = y .* (g .- r)."""
+    def row(g, x, t):
+        e = g.fold("exp", x)                        # phase 1: the column's log-sum-exp
+        y = g.apply("exp", x - e.logsumexp)
+        s = g.fold("sum", y * t, phase=2)           # phase 2: sum(y .* g)
+        g.output("dx", y * (t - s.value), (1, n))
+        g.output("r", s.value, (0, 1), full=False)
+    return _floor_row_program("floor_softmax_columns", rows, n, row)
+
+
+def floor_layernorm(rows: int, n: int, eps: float = 1e-5) -> Program:
+    """Config 2b through the generated floor, in the program's two passes
+    (test/fixtures/programs.jl:13-17, weight 1): m = sum(x)/n,
+    v = sum(abs2, x .- m)/n, y = (x .- m) ./ sqrt(v + eps), r = sum(y .* g),
+    dx = (g .- sum(g)/n .- y .* r/n) ./ sqrt(v + eps)."""
+    def row(g, x, t):
+        m = g.fold("sum", x).value / n                               # phase 1
+        v = g.fold("sum", g.apply("abs2", x - m), phase=2).value / n  # phase 2
+        rs = g.apply("inv", g.apply("sqrt", v + eps))
+        y = (x - m) * rs
+        sg = g.fold("sum", t, phase=3).value                         # phase 3
+        r = g.fold("sum", y * t, phase=3).value
+        g.output("dx", (t - sg / n - y * (r / n)) * rs, (1, n))
+        g.output("r", r, (0, 1), full=False)
+    return _floor_row_program("floor_layernorm", rows, n, row)

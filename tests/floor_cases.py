@@ -1,0 +1,431 @@
+"""The reference's fixture programs, planned as generated-floor groups.
+
+Each case is a program of test/fixtures/programs.jl:60-90 (and the row
+programs of config 2) written as the groups the floor would run: a list of
+FloorGroups run in order over named values, the inputs (the reference tests'
+closed-form ``data()``), and a closed form of the result written directly
+with numpy, independent of the groups, that pins the oracle's evaluation.
+
+Arrays are column-major as in the reference: an n x m array is stored with
+element (i0, i1) at i0 + n * i1 (numpy: ``a.ravel(order="F")``).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.data import data
+from tempest_hip.floor import FloorGroup
+
+
+def F(a):
+    return np.asarray(a, dtype=np.float64).ravel(order="F")
+
+
+class Case:
+    def __init__(self, name, groups, inputs, stored, results, closed, dtypes=None):
+        self.name = name
+        self.groups = groups        # FloorGroups, in order
+        self.inputs = inputs        # name -> 1-D float64
+        self.stored = stored        # name -> length (intermediates, zero-filled)
+        self.results = results      # names checked
+        self.closed = closed        # inputs -> {name: expected}
+        self.dtypes = dtypes or {}  # name -> "bf16" (default "f32")
+
+    def lengths(self):
+        out = {k: len(v) for k, v in self.inputs.items()}
+        out.update(self.stored)
+        return out
+
+
+def _full_sum(src: str, n: int, dst: str = "loss", extra: str | None = None) -> FloorGroup:
+    """loss = sum(src) (+ extra[0]): the full fold after a row group."""
+    g = FloorGroup("reduction", (n,), reduced=(0,), name=f"sum({src})")
+    g.value(src, "f32", n)
+    if extra:
+        g.value(extra, "f32", 1)
+    g.value(dst, "f32", 1)
+    s = g.fold("sum", g.load(src, (1,))).value
+    g.output(dst, s + g.load(extra, (0,)) if extra else s, full=False)
+    return g
+
+
+def _whole(name, shape, build, inputs, closed, dst="loss"):
+    """One group folding every axis into a number."""
+    g = FloorGroup("reduction", shape, reduced=tuple(range(len(shape))), name=name)
+    for k, v in inputs.items():
+        g.value(k, "f32", len(v))
+    g.value(dst, "f32", 1)
+    g.output(dst, build(g), full=False)
+    return Case(name, [g], inputs, {dst: 1}, [dst], closed)
+
+
+def _lin(shape):
+    """Column-major coefficients of a dense array of `shape`."""
+    c, s = [], 1
+    for e in shape:
+        c.append(s)
+        s *= e
+    return c
+
+
+def dot_product():
+    a, b = data(32), data(32, scale=0.3)
+    return _whole("dot product", (32,), lambda g: g.fold("sum", g.load("a", (1,)) * g.load("b", (1,))).value,
+                  {"a": F(a), "b": F(b)}, lambda v: {"loss": [np.sum(v["a"] * v["b"])]})
+
+
+def sum_abs2_tanh():
+    x = data(8, 6)
+    return _whole("sum abs2 tanh", (8, 6),
+                  lambda g: g.fold("sum", g.apply("abs2", g.apply("tanh", g.load("x", (1, 8))))).value,
+                  {"x": F(x)}, lambda v: {"loss": [np.sum(np.tanh(v["x"]) ** 2)]})
+
+
+def full_logsumexp():
+    x = data(8, 6)
+
+    def closed(v):
+        m = v["x"].max()
+        return {"loss": [m + np.log(np.sum(np.exp(v["x"] - m)))]}
+    return _whole("full logsumexp", (8, 6), lambda g: g.fold("exp", g.load("x", (1, 8))).logsumexp,
+                  {"x": F(x)}, closed)
+
+
+def maximum_and_shifted_sum():
+    x = data(8, 6)
+
+    def build(g):
+        xx = g.load("x", (1, 8))
+        m = g.fold("max", xx).value
+        return g.fold("sum", g.apply("exp", xx - m), phase=2).value
+    return _whole("maximum and shifted sum", (8, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum(np.exp(v["x"] - v["x"].max()))]})
+
+
+def minus_mean():
+    x = data(8, 6)
+
+    def build(g):
+        xx = g.load("x", (1, 8))
+        s = g.fold("sum", xx).value
+        return g.fold("sum", g.apply("abs2", xx - s / 48.0), phase=2).value
+    return _whole("x .- mean", (8, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum((v["x"] - v["x"].mean()) ** 2)]})
+
+
+def swish():
+    x = data(8, 6)
+    return _whole("swish", (8, 6), lambda g: g.fold("sum", (lambda t: t / (1.0 + g.apply("exp", -t)))(
+        g.load("x", (1, 8)))).value, {"x": F(x)}, lambda v: {"loss": [np.sum(v["x"] / (1 + np.exp(-v["x"])))]})
+
+
+def powers():
+    x = data(8, 6)
+
+    def build(g):
+        t = g.load("x", (1, 8))
+        return g.fold("sum", t ** 2.0 + t ** 3.0 + g.apply("sqrt", g.apply("abs", t) + 1.0)).value
+    return _whole("powers", (8, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum(v["x"] ** 2 + v["x"] ** 3 + np.sqrt(np.abs(v["x"]) + 1))]})
+
+
+def clamp_and_max():
+    x = data(8, 6)
+
+    def build(g):
+        t = g.load("x", (1, 8))
+        return g.fold("sum", g.apply("clamp", t, -0.5, 0.5) + g.apply("max", t, 0.1)).value
+    return _whole("clamp and max", (8, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum(np.clip(v["x"], -0.5, 0.5) + np.maximum(v["x"], 0.1))]})
+
+
+def strided_view_and_index():
+    """sum(abs2, view(x, 2:2:8, :) .+ x[3, 2]): rows 1, 3, 5, 7 (zero-based) and element (2, 1)."""
+    x = data(8, 6)
+
+    def build(g):
+        v = g.load("x", (2, 8), constant=1)
+        s = g.load("x", (0, 0), constant=2 + 8 * 1)
+        return g.fold("sum", g.apply("abs2", v + s)).value
+    return _whole("strided view and index", (4, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum((v["x"].reshape(8, 6, order="F")[1::2, :] +
+                                              v["x"].reshape(8, 6, order="F")[2, 1]) ** 2)]})
+
+
+def rounded_counted_tested():
+    """sum(abs2, x .* round.(3x)) + count(>(0), x) * sum(x) + all(x .< 3) * sum(abs2, x)
+    + sum(any(x .> 1; dims = 1) .* x) (programs.jl:63-64; round to Int32 is to
+    nearest, ties to even, as Julia's round)."""
+    x = data(8, 6)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="whole-array folds")
+    g1.value("x", "f32", 48)
+    g1.value("part", "f32", 1)
+    t = g1.load("x", (1, 8))
+    a = g1.fold("sum", g1.apply("abs2", t * g1.apply("round", 3.0 * t))).value
+    c = g1.fold("sum", g1.apply(">", t, 0.0)).value
+    s = g1.fold("sum", t).value
+    al = g1.fold("min", g1.apply("<", t, 3.0)).value
+    q = g1.fold("sum", g1.apply("abs2", t)).value
+    g1.output("part", a + c * s + al * q, full=False)
+    g2 = FloorGroup("reduction", (8, 6), reduced=(0,), name="any per column")
+    g2.value("x", "f32", 48)
+    g2.value("r", "f32", 6)
+    t2 = g2.load("x", (1, 8))
+    anyc = g2.fold("max", g2.apply(">", t2, 1.0)).value
+    g2.output("r", g2.fold("sum", anyc * t2, phase=2).value, (0, 1), full=False)
+    g3 = _full_sum("r", 6, extra="part")
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        r = np.sum(X * np.rint(3 * X) * X * np.rint(3 * X)) + np.sum(X > 0) * X.sum() + \
+            float(np.all(X < 3)) * np.sum(X ** 2) + np.sum(np.any(X > 1, axis=0)[None, :] * X)
+        return {"loss": [r]}
+    return Case("rounded, counted and tested", [g1, g2, g3], {"x": F(x)}, {"part": 1, "r": 6, "loss": 1},
+                ["loss"], closed)
+
+
+def _column_then_sum(name, shape, reduced, build_row, inputs, closed, items):
+    g1 = FloorGroup("reduction", shape, reduced=reduced, name=name)
+    for k, v in inputs.items():
+        g1.value(k, "f32", len(v))
+    g1.value("r", "f32", items)
+    build_row(g1)
+    g2 = _full_sum("r", items)
+    return Case(name, [g1, g2], inputs, {"r": items, "loss": 1}, ["r", "loss"], closed)
+
+
+def column_maxima():
+    x, w = data(8, 6), data(1, 6)
+
+    def row(g):
+        m = g.fold("max", g.load("x", (1, 8))).value
+        g.output("r", m * g.load("w", (0, 1)), (0, 1), full=False)
+
+    def closed(v):
+        r = v["x"].reshape(8, 6, order="F").max(axis=0) * v["w"]
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("column maxima", (8, 6), (0,), row, {"x": F(x), "w": F(w)}, closed, 6)
+
+
+def row_minima():
+    x = data(8, 6)
+
+    def row(g):
+        g.output("r", g.fold("min", g.load("x", (1, 8))).value, (1, 0), full=False)
+
+    def closed(v):
+        r = v["x"].reshape(8, 6, order="F").min(axis=1)
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("row minima", (8, 6), (1,), row, {"x": F(x)}, closed, 8)
+
+
+def products():
+    x = data(5, 3, scale=0.4)
+
+    def row(g):
+        g.output("r", g.fold("prod", g.load("x", (1, 5))).value, (0, 1), full=False)
+
+    def closed(v):
+        r = v["x"].reshape(5, 3, order="F").prod(axis=0)
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("products", (5, 3), (0,), row, {"x": F(x)}, closed, 3)
+
+
+def _softmax_closed(x, t, shape, axis):
+    X, T = x.reshape(shape, order="F"), t.reshape(shape, order="F")
+    e = np.exp(X - X.max(axis=axis, keepdims=True))
+    y = e / e.sum(axis=axis, keepdims=True)
+    return (y * T).sum(axis=axis)
+
+
+def softmax_columns(n=8, m=6):
+    x, t = data(n, m), data(n, m, scale=0.7)
+
+    def row(g):
+        xx, tt = g.load("x", (1, n)), g.load("t", (1, n))
+        e = g.fold("exp", xx)
+        g.output("r", g.fold("sum", g.apply("exp", xx - e.logsumexp) * tt, phase=2).value, (0, 1), full=False)
+
+    def closed(v):
+        r = _softmax_closed(v["x"], v["t"], (n, m), 0)
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum(f"softmax columns {n}x{m}", (n, m), (0,), row, {"x": F(x), "t": F(t)}, closed, m)
+
+
+def softmax_rows(n=8, m=6):
+    """Softmax over dims = 2: the folded axis is the strided one (items adjacent)."""
+    x, t = data(n, m), data(n, m, scale=0.7)
+
+    def row(g):
+        xx, tt = g.load("x", (1, n)), g.load("t", (1, n))
+        e = g.fold("exp", xx)
+        g.output("r", g.fold("sum", g.apply("exp", xx - e.logsumexp) * tt, phase=2).value, (1, 0), full=False)
+
+    def closed(v):
+        r = _softmax_closed(v["x"], v["t"], (n, m), 1)
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum(f"softmax rows {n}x{m}", (n, m), (1,), row, {"x": F(x), "t": F(t)}, closed, n)
+
+
+def rank3_softmax():
+    """sum(exp.(x .- logsumexp(x; dims = 3)) .* t), x 4 x 3 x 5: the last axis folds."""
+    x, t = data(4, 3, 5), data(4, 3, 5, scale=0.2)
+
+    def row(g):
+        xx, tt = g.load("x", (1, 4, 12)), g.load("t", (1, 4, 12))
+        e = g.fold("exp", xx)
+        g.output("r", g.fold("sum", g.apply("exp", xx - e.logsumexp) * tt, phase=2).value, (1, 4, 0), full=False)
+
+    def closed(v):
+        r = _softmax_closed(v["x"], v["t"], (4, 3, 5), 2).ravel(order="F")
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("rank 3 softmax", (4, 3, 5), (2,), row, {"x": F(x), "t": F(t)}, closed, 12)
+
+
+def rmsnorm():
+    x, w = data(8, 6), data(8, scale=0.1)
+
+    def row(g):
+        xx = g.load("x", (1, 8))
+        s = g.fold("sum", g.apply("abs2", xx)).value
+        y = xx / g.apply("sqrt", s / 8.0 + 1e-5) * g.load("w", (1, 0))
+        g.output("r", g.fold("sum", g.apply("abs2", y), phase=2).value, (0, 1), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        y = X / np.sqrt((X ** 2).sum(axis=0, keepdims=True) / 8 + 1e-5) * v["w"][:, None]
+        r = (y ** 2).sum(axis=0)
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("RMSNorm", (8, 6), (0,), row, {"x": F(x), "w": F(w)}, closed, 6)
+
+
+def _layernorm_closed(v, n, m):
+    X = v["x"].reshape(n, m, order="F")
+    mu = X.mean(axis=0, keepdims=True)
+    var = ((X - mu) ** 2).mean(axis=0, keepdims=True)
+    y = (X - mu) / np.sqrt(var + 1e-5) * v["w"][:, None]
+    r = (y ** 2).sum(axis=0)
+    return {"r": r, "loss": [r.sum()]}
+
+
+def layer_norm(n=8, m=6):
+    x, w = data(n, m), data(n, scale=0.1)
+
+    def row(g):
+        xx = g.load("x", (1, n))
+        mu = g.fold("sum", xx).value / float(n)
+        var = g.fold("sum", g.apply("abs2", xx - mu), phase=2).value / float(n)
+        y = (xx - mu) / g.apply("sqrt", var + 1e-5) * g.load("w", (1, 0))
+        g.output("r", g.fold("sum", g.apply("abs2", y), phase=3).value, (0, 1), full=False)
+    return _column_then_sum(f"layer norm {n}x{m}", (n, m), (0,), row, {"x": F(x), "w": F(w)},
+                            lambda v: _layernorm_closed(v, n, m), m)
+
+
+def layer_norm_welford(n=8, m=6):
+    """The same LayerNorm with mean and variance from one square fold (Chan/Welford)."""
+    x, w = data(n, m), data(n, scale=0.1)
+
+    def row(g):
+        xx = g.load("x", (1, n))
+        f = g.fold("square", xx)
+        y = (xx - f.statistic) / g.apply("sqrt", f.sum / float(n) + 1e-5) * g.load("w", (1, 0))
+        g.output("r", g.fold("sum", g.apply("abs2", y), phase=2).value, (0, 1), full=False)
+    return _column_then_sum(f"layer norm by Welford {n}x{m}", (n, m), (0,), row, {"x": F(x), "w": F(w)},
+                            lambda v: _layernorm_closed(v, n, m), m)
+
+
+def welford_variance():
+    """sum(var(x; dims = 1) .* data(1, 6)), var = M2 / n as VARIANCE observes it."""
+    x, w = data(8, 6), data(1, 6)
+
+    def row(g):
+        f = g.fold("square", g.load("x", (1, 8)))
+        g.output("r", f.sum / 8.0 * g.load("w", (0, 1)), (0, 1), full=False)
+
+    def closed(v):
+        r = v["x"].reshape(8, 6, order="F").var(axis=0) * v["w"]
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("Welford's variance", (8, 6), (0,), row, {"x": F(x), "w": F(w)}, closed, 6)
+
+
+def map_over_two_arrays():
+    """sum(abs2, map((a, b) -> a * b + a, x, y)): a pointwise group, then the fold."""
+    x, y = data(8, 6), data(8, 6, scale=0.4)
+    g1 = FloorGroup("pointwise", (8, 6), name="a * b + a")
+    for k in ("x", "y", "z"):
+        g1.value(k, "f32", 48)
+    a, b = g1.load("x", (1, 8)), g1.load("y", (1, 8))
+    g1.output("z", a * b + a, (1, 8))
+    g2 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="sum abs2")
+    g2.value("z", "f32", 48)
+    g2.value("loss", "f32", 1)
+    g2.output("loss", g2.fold("sum", g2.apply("abs2", g2.load("z", (1, 8)))).value, full=False)
+
+    def closed(v):
+        z = v["x"] * v["y"] + v["x"]
+        return {"z": z, "loss": [np.sum(z ** 2)]}
+    return Case("map over two arrays", [g1, g2], {"x": F(x), "y": F(y)}, {"z": 48, "loss": 1}, ["z", "loss"], closed)
+
+
+def permutation():
+    """permutedims(x, (2, 1, 3)) of a 4 x 3 x 5 array: y (3 x 4 x 5)[j0, j1, j2] = x[j1, j0, j2]."""
+    x = data(4, 3, 5)
+    g = FloorGroup("pointwise", (3, 4, 5), name="permutedims")
+    g.value("x", "f32", 60)
+    g.value("y", "f32", 60)
+    g.output("y", g.load("x", (4, 1, 12)), (1, 3, 12))
+    return Case("permutation", [g], {"x": F(x)}, {"y": 60}, ["y"],
+                lambda v: {"y": v["x"].reshape(4, 3, 5, order="F").transpose(1, 0, 2).ravel(order="F")})
+
+
+def bias_tanh_bf16(n=64, m=40):
+    """y = tanh.(x .+ b) with b a column broadcast along the rows, y stored as bfloat16."""
+    x, b = data(n, m), data(n, scale=0.3)
+    g = FloorGroup("pointwise", (n, m), name="tanh.(x .+ b) to bf16")
+    g.value("x", "f32", n * m)
+    g.value("b", "f32", n)
+    g.value("y", "bf16", n * m)
+    g.output("y", g.apply("tanh", g.load("x", (1, n)) + g.load("b", (1, 0))), (1, n))
+    return Case("bias and tanh to bf16", [g], {"x": F(x), "b": F(b)}, {"y": n * m}, ["y"],
+                lambda v: {"y": np.tanh(v["x"].reshape(n, m, order="F") + v["b"][:, None]).ravel(order="F")},
+                dtypes={"y": "bf16"})
+
+
+def index_scaled(n=12, m=5):
+    """y = x .* (i .+ 1), the row's position as a number (Ix)."""
+    x = data(n, m)
+    g = FloorGroup("pointwise", (n, m), name="x .* position")
+    g.value("x", "f32", n * m)
+    g.value("y", "f32", n * m)
+    g.output("y", g.load("x", (1, n)) * (g.index((1, 0)) + 1.0), (1, n))
+    return Case("index scaled", [g], {"x": F(x)}, {"y": n * m}, ["y"],
+                lambda v: {"y": (v["x"].reshape(n, m, order="F") * (np.arange(n)[:, None] + 1)).ravel(order="F")})
+
+
+def kat_sum_abs2():
+    """compile(x -> sum(abs2, x), ...)([1, 2, 3, 4]) == 30 (runtime/compile.jl:35-40)."""
+    return _whole("sum(abs2, [1, 2, 3, 4])", (4,), lambda g: g.fold("sum", g.apply("abs2", g.load("x", (1,)))).value,
+                  {"x": np.array([1.0, 2.0, 3.0, 4.0])}, lambda v: {"loss": [30.0]})
+
+
+CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
+         clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
+         softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
+         map_over_two_arrays, permutation, bias_tanh_bf16, index_scaled, kat_sum_abs2]
+
+
+def run_oracle(case: Case) -> dict:
+    """Every value after the case's groups, by the oracle, in order."""
+    from oracle.floor_groups import evaluate
+    from oracle.data import bf16_round
+    vals = {k: np.array(v, dtype=np.float64) for k, v in case.inputs.items()}
+    for k, n in case.stored.items():
+        vals[k] = np.zeros(n)
+    for k in vals:
+        # What the device holds: Float32 inputs, bfloat16 where the case says so.
+        vals[k] = (bf16_round(vals[k].astype(np.float32)) if case.dtypes.get(k) == "bf16"
+                   else vals[k].astype(np.float32)).astype(np.float64)
+    for g in case.groups:
+        out = evaluate(g.spec(), vals)
+        vals.update({k: v.astype(np.float64) for k, v in out.items()})
+    return vals

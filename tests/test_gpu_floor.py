@@ -1,0 +1,191 @@
+"""The generated floor on the GPU: every fixture program's groups against the
+oracle; config 2's programs through the floor at ragged, streamed, split and
+full sizes against the row oracle; column folds with lanes and parts; a
+whole-array fold split into parts; graphs, repointing and a compiled call."""
+import numpy as np
+import pytest
+import torch
+
+import floor_cases as FC
+from conftest import announce
+from oracle import interpret
+from oracle.data import bf16_round, data, relative
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5       # fp32 pointwise/reduction, norm-wise relative (as agree())
+TOL_BF16 = 1e-2  # values stored as bfloat16 (one rounding: 2^-9 relative)
+
+
+def _tensors(case):
+    out = {}
+    for k, n in case.lengths().items():
+        if k in case.inputs:
+            v = np.asarray(case.inputs[k], dtype=np.float32)
+        else:
+            v = np.zeros(n, dtype=np.float32)
+        t = torch.from_numpy(v).cuda()
+        out[k] = t.to(torch.bfloat16) if case.dtypes.get(k) == "bf16" else t
+    return out
+
+
+@pytest.mark.parametrize("make", FC.CASES, ids=[c.__name__ for c in FC.CASES])
+def test_fixture_programs(target, make):
+    case = make()
+    announce("floor fixture", case.name)
+    ts = _tensors(case)
+    launches = [g.build({k: ts[k].data_ptr() for k in g.values}) for g in case.groups]
+    for l in launches:
+        l()
+    torch.cuda.synchronize()
+    want = FC.run_oracle(case)
+    for k in case.results:
+        got = ts[k].float().cpu().numpy().astype(np.float64)
+        tol = TOL_BF16 if case.dtypes.get(k) == "bf16" else TOL
+        assert relative(got, want[k]) < tol, (case.name, k, relative(got, want[k]))
+        if case.dtypes.get(k) == "bf16":
+            # One rounding of the fp32 result: within half an ulp of bf16.
+            assert np.all(np.abs(got - want[k]) <= np.abs(want[k]) * 2.0 ** -8 + 1e-30)
+
+
+def _row_inputs(rows, n, seed):
+    if seed is None:
+        return (np.ascontiguousarray(data(n, rows).T).astype(np.float32),
+                np.ascontiguousarray(data(n, rows, scale=0.7).T).astype(np.float32))
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((rows, n), dtype=np.float32), rng.standard_normal((rows, n), dtype=np.float32)
+
+
+@pytest.mark.parametrize("which", ["softmax", "layernorm"])
+@pytest.mark.parametrize("rows,n,seed", [(6, 8, None), (700, 256, None), (40, 9000, None), (9, 1027, 1),
+                                         (3, 16384, 2), (2, 40000, 3), (1, 6, 4), (5, 1, 5), (4096, 1000, 6)])
+def test_config2_programs_through_the_floor(target, which, rows, n, seed):
+    import tempest_hip as th
+    announce("floor config2", which, rows, n)
+    x, g = _row_inputs(rows, n, seed)
+    prog = th.programs.floor_softmax_columns(rows, n) if which == "softmax" else th.programs.floor_layernorm(rows, n)
+    c = th.compile(prog, target, torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda())
+    loss, dx = c(torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda())
+    f = interpret.softmax_grad if which == "softmax" else interpret.layernorm_grad
+    ref_loss, ref_dx = f(x, g)
+    assert relative(dx.cpu().numpy(), ref_dx) < TOL
+    scale = max(1.0, np.abs(ref_dx).sum() / rows)
+    assert abs(loss - ref_loss) <= TOL * scale
+
+
+@pytest.mark.parametrize("n,m", [(300, 5000), (70000, 8), (64, 64), (3, 100000)])
+def test_column_folds_with_lanes_and_parts(target, n, m):
+    """Softmax over dims = 2 of an n x m array: items adjacent in memory, the
+    folded positions a stride of n apart."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor columns", n, m)
+    rng = np.random.default_rng(n + m)
+    x = rng.standard_normal(n * m).astype(np.float32)
+    t = rng.standard_normal(n * m).astype(np.float32)
+    g = FloorGroup("reduction", (n, m), reduced=(1,))
+    g.value("x", "f32", n * m)
+    g.value("t", "f32", n * m)
+    g.value("y", "f32", n * m)
+    g.value("r", "f32", n)
+    xx, tt = g.load("x", (1, n)), g.load("t", (1, n))
+    e = g.fold("exp", xx)
+    y = g.apply("exp", xx - e.logsumexp)
+    g.output("y", y, (1, n))
+    g.output("r", g.fold("sum", y * tt, phase=2).value, (1, 0), full=False)
+    ts = {k: torch.from_numpy(v).cuda() for k, v in (("x", x), ("t", t))}
+    ts["y"] = torch.zeros(n * m, device="cuda")
+    ts["r"] = torch.zeros(n, device="cuda")
+    g.build({k: v.data_ptr() for k, v in ts.items()})()
+    torch.cuda.synchronize()
+    X, T = x.astype(np.float64).reshape(m, n).T, t.astype(np.float64).reshape(m, n).T
+    ey = np.exp(X - X.max(axis=1, keepdims=True))
+    Y = ey / ey.sum(axis=1, keepdims=True)
+    assert relative(ts["y"].cpu().numpy().reshape(m, n).T, Y) < TOL
+    assert relative(ts["r"].cpu().numpy(), (Y * T).sum(axis=1)) < TOL
+
+
+@pytest.mark.parametrize("count", [1 << 22, 1 << 20, 3 * 7 * 9973])
+def test_whole_array_fold_in_parts(target, count):
+    """sum(abs2, x) and maximum(x) over one item of millions of positions:
+    parts fold into a workspace, the last launch merges them."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor whole fold", count)
+    x = np.random.default_rng(count).standard_normal(count).astype(np.float32)
+    g = FloorGroup("reduction", (count,), reduced=(0,))
+    g.value("x", "f32", count)
+    g.value("out", "f32", 2)
+    xx = g.load("x", (1,))
+    g.output("out", g.fold("sum", g.apply("abs2", xx)).value, full=False)
+    g.output("out", g.fold("max", xx).value, constant=1, full=False)
+    ts = {"x": torch.from_numpy(x).cuda(), "out": torch.zeros(2, device="cuda")}
+    launch = g.build({k: v.data_ptr() for k, v in ts.items()})
+    for _ in range(2):  # the workspace is rewritten each run
+        launch()
+    torch.cuda.synchronize()
+    out = ts["out"].cpu().numpy()
+    x64 = x.astype(np.float64)
+    assert abs(out[0] - np.sum(x64 * x64)) <= TOL * np.sum(x64 * x64)
+    assert out[1] == x.max()
+
+
+def test_graph_replay_and_repoint(target):
+    """A compiled floor program called on moved arrays: the graph's module
+    kernel nodes are retargeted, the results follow the new inputs."""
+    import tempest_hip as th
+    announce("floor graph repoint")
+    rows, n = 300, 2048
+    prog = th.programs.floor_softmax_columns(rows, n)
+    x0, g0 = _row_inputs(rows, n, 11)
+    c = th.compile(prog, target, torch.from_numpy(x0).cuda(), torch.from_numpy(g0).cuda())
+    for seed in (12, 13, 12):
+        x, g = _row_inputs(rows, n, seed)
+        xt, gt = torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda()
+        loss, dx = c(xt, gt)
+        ref_loss, ref_dx = interpret.softmax_grad(x, g)
+        assert relative(dx.cpu().numpy(), ref_dx) < TOL
+        assert abs(loss - ref_loss) <= TOL * max(1.0, np.abs(ref_dx).sum() / rows)
+    ex = c.executable
+    for _ in range(3):  # replays with eager work between them
+        ex.replay()
+        torch.cuda.synchronize()
+        assert relative(ex.outputs()[1].cpu().numpy(), ref_dx) < TOL
+
+
+def test_bf16_inputs_widen(target):
+    """A bf16 value read by a reduction: widened exactly, folded in fp32."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor bf16 inputs")
+    n, m = 1000, 37
+    x = bf16_round(np.random.default_rng(7).standard_normal(n * m).astype(np.float32))
+    g = FloorGroup("reduction", (n, m), reduced=(0,))
+    g.value("x", "bf16", n * m)
+    g.value("s", "f32", m)
+    g.output("s", g.fold("sum", g.load("x", (1, n))).value, (0, 1), full=False)
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    s = torch.zeros(m, device="cuda")
+    g.build({"x": xt.data_ptr(), "s": s.data_ptr()})()
+    torch.cuda.synchronize()
+    assert relative(s.cpu().numpy(), x.astype(np.float64).reshape(m, n).sum(axis=1)) < TOL
+
+
+def test_config2_full_size_through_the_floor(target):
+    """32768 x 8192: sampled rows of dx against the oracle, the loss against
+    the oracle's per-row losses summed."""
+    import tempest_hip as th
+    rows, n = 32768, 8192
+    gen = torch.Generator(device="cuda").manual_seed(20261201)
+    x = torch.randn(rows, n, device="cuda", generator=gen)
+    g = torch.randn(rows, n, device="cuda", generator=gen)
+    idx = torch.tensor([0, 1, 777, 16384, rows - 1], device="cuda")
+    xs, gs = x.index_select(0, idx).cpu().numpy(), g.index_select(0, idx).cpu().numpy()
+    for which in ("softmax", "layernorm"):
+        announce("floor config2 full", which)
+        prog = th.programs.floor_softmax_columns(rows, n) if which == "softmax" else th.programs.floor_layernorm(rows, n)
+        c = th.compile(prog, target, x, g)
+        loss, dx = c(x, g)
+        f = interpret.softmax_grad if which == "softmax" else interpret.layernorm_grad
+        _, ref = f(xs, gs)
+        assert relative(dx.index_select(0, idx).cpu().numpy(), ref) < TOL
+        assert np.isfinite(loss)
+        del c, dx
+        torch.cuda.empty_cache()

@@ -1,0 +1,145 @@
+"""The generated floor on the CPU: the oracle's group evaluation pinned by
+closed forms and the sequential fold algebra; every fixture group's kernel
+written and compiled for gfx950 without a device; the ABI's rejections."""
+import numpy as np
+import pytest
+
+import floor_cases as FC
+from oracle import floor_groups as FG
+from oracle import folds as F
+from oracle.data import relative
+
+CASES = {c.__name__: c for c in FC.CASES}
+
+
+def _cast_inputs(case):
+    return {k: np.asarray(v, dtype=np.float32).astype(np.float64) for k, v in case.inputs.items()}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_oracle_matches_closed_form(name):
+    case = CASES[name]()
+    vals = FC.run_oracle(case)
+    want = case.closed(_cast_inputs(case))
+    for k in case.results:
+        tol = 1e-2 if case.dtypes.get(k) == "bf16" else 1e-6
+        assert relative(vals[k], np.asarray(want[k], dtype=np.float64)) < tol, (name, k)
+
+
+def test_kat_sum_of_squares_exact():
+    # src/Compiler/runtime/compile.jl:35-40: exactly 30.
+    assert FC.run_oracle(FC.kat_sum_abs2())["loss"][0] == 30.0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_vectorized_folds_match_sequential_algebra(seed):
+    rng = np.random.default_rng(seed)
+    y = rng.normal(size=(23, 5)) * 3
+    g = rng.normal(size=(23, 5))
+    for j in range(5):
+        col, w = list(y[:, j]), list(zip(y[:, j], g[:, j]))
+        got = {k: FG.fold_reduce(k, y[:, j:j + 1], g[:, j:j + 1] if k == "exp" else None, (0,))
+               for k in ("sum", "prod", "max", "min", "exp", "square")}
+        assert np.isclose(got["sum"]["value"][0, 0], F.fold(F.SumFold(), col), rtol=1e-13)
+        assert np.isclose(got["max"]["value"][0, 0], F.fold(F.MaxFold(), col), rtol=0)
+        assert np.isclose(got["min"]["value"][0, 0], -F.fold(F.MaxFold(), [-v for v in col]), rtol=0)
+        prod = F.fold(F.GenericFold(init_fn=lambda: (1.0,), combine_fn=lambda a, b: (a[0] * b[0],)), col)
+        assert np.isclose(got["prod"]["value"][0, 0], prod, rtol=1e-12)
+        weighted = F.Relative(F.Exponential(), F.nth_sum(0))
+        assert np.isclose(got["exp"]["sum"][0, 0], F.fold(weighted, w), rtol=1e-12)
+        assert np.isclose(got["exp"]["statistic"][0, 0], F.fold(F.Relative(F.Exponential(), F.statistic), w))
+        plain = FG.fold_reduce("exp", y[:, j:j + 1], None, (0,))
+        assert np.isclose(plain["logsumexp"][0, 0], F.fold(F.LOGSUMEXP, col), rtol=1e-13)
+        sq_mean = F.fold(F.Relative(F.Square(), F.statistic), col)
+        sq_m2 = F.fold(F.Relative(F.Square(), F.nth_sum(0)), col)
+        assert np.isclose(got["square"]["statistic"][0, 0], sq_mean, rtol=1e-12)
+        assert np.isclose(got["square"]["sum"][0, 0], sq_m2, rtol=1e-12)
+
+
+def test_planted_missing_rebase_is_caught(monkeypatch):
+    """An exponential fold that forgets to shift by its maximum must fail the
+    closed form of a softmax with large entries."""
+    real = FG.fold_reduce
+
+    def planted(kind, y, g, axes):
+        if kind != "exp":
+            return real(kind, y, g, axes)
+        w = 1.0 if g is None else g
+        s = (w * np.exp(y)).sum(axis=axes, keepdims=True)      # no rebase
+        m = y.max(axis=axes, keepdims=True)
+        return {"statistic": m, "sum": s, "logsumexp": m + np.log(s)}
+    monkeypatch.setattr(FG, "fold_reduce", planted)
+    case = FC.softmax_columns()
+    case.inputs["x"] = case.inputs["x"] * 30.0
+    vals = FC.run_oracle(case)
+    want = case.closed(_cast_inputs(case))
+    assert relative(vals["loss"], np.asarray(want["loss"])) > 1e-3
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_kernels_compile_without_a_device(name):
+    case = CASES[name]()
+    for g in case.groups:
+        src = g.source()
+        assert src.startswith("// tempest-hip floor:") and "extern \"C\" __global__" in src
+        g.compile()  # hiprtc for gfx950, into the code-object cache
+
+
+@pytest.mark.parametrize("rows,n", [(32768, 8192), (700, 256), (2, 40000), (9, 1027)])
+def test_config2_floor_programs_compile(rows, n):
+    import tempest_hip as th
+    for prog in (th.programs.floor_softmax_columns(rows, n), th.programs.floor_layernorm(rows, n)):
+        for grp in prog.groups:
+            grp.build.__self__.compile()
+
+
+def test_plans_take_each_mapping():
+    """Rows (resident, streamed, split), columns (lanes and parts), pointwise."""
+    from tempest_hip.floor import FloorGroup
+
+    def head(extents, reduced, unit_axis):
+        g = FloorGroup("reduction", extents, reduced=reduced)
+        n = int(np.prod(extents))
+        g.value("x", "f32", n)
+        g.value("r", "f32", n)
+        coeffs = [1, extents[0]] if unit_axis == 0 else [1, extents[0]]
+        x = g.load("x", coeffs)
+        g.output("r", g.fold("sum", x).value, [0 if k in reduced else c for k, c in enumerate(coeffs)], full=False)
+        return g.source().splitlines()[0]
+    assert "rows" in head((8192, 64), (0,), 0) and "resident" in head((8192, 64), (0,), 0)
+    assert "streamed" in head((100000, 64), (0,), 0)
+    assert "parts" in head((1 << 22, 1), (0,), 0) and ", parts 1," not in head((1 << 22, 1), (0,), 0)
+    col = head((300, 5000), (1,), 0)
+    assert col.startswith("// tempest-hip floor: columns") and ", lanes 4," in col and ", parts 1," not in col
+    assert ", lanes 1, parts 1," in head((300000, 8), (1,), 0)
+
+
+@pytest.mark.parametrize("break_it,message", [
+    ("load_outside", "outside its value"),
+    ("later_stat", "own or a later phase"),
+    ("pointwise_fold", "only a reduction group folds"),
+    ("write_outside", "writes outside"),
+])
+def test_abi_rejects(break_it, message):
+    from tempest_hip import HIPError
+    from tempest_hip.floor import FloorGroup
+    g = FloorGroup("reduction", (8, 6), reduced=(0,))
+    g.value("x", "f32", 48)
+    g.value("r", "f32", 6)
+    x = g.load("x", (1, 8))
+    try:
+        if break_it == "load_outside":
+            bad = g.load("x", (1, 9))
+            g.output("r", g.fold("sum", bad).value, (0, 1), full=False)
+        elif break_it == "later_stat":
+            f2 = g.fold("sum", x, phase=2)
+            g.output("r", g.fold("sum", x * f2.value, phase=2).value, (0, 1), full=False)
+        elif break_it == "pointwise_fold":
+            FloorGroup("pointwise", (8,)).fold("sum", 1.0)
+        else:
+            g.output("r", g.fold("sum", x).value, (0, 2), full=False)
+        g.source()
+    except (HIPError, ValueError) as e:
+        assert message in str(e)
+    else:
+        raise AssertionError("accepted")
