@@ -86,6 +86,46 @@ def config2(target, steps: int, warmup: int):
                 bytes_ln=bytes_ln, parity=parity, describe=es.explain() + "\n" + el.explain())
 
 
+def config2_floor(target, x, g, steps: int = 10, warmup: int = 3):
+    """Config 2's programs through the generated floor (kernels written from
+    the groups' terms and compiled at run time), on the same X, G: per-program
+    device time and GB/s of the same algorithmic bytes, and sampled-row parity."""
+    import torch
+    import tempest_hip as th
+
+    out = {}
+    alg = 3.0 * 4 * ROWS * N
+    for name, make in (("softmax", th.programs.floor_softmax_columns), ("layernorm", th.programs.floor_layernorm)):
+        c = th.compile(make(ROWS, N), target, x, g)
+        ex = c.executable
+        for _ in range(warmup):
+            ex.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            ex.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        s = e0.elapsed_time(e1) * 1e-3 / steps
+        entry = {"us": s * 1e6, "GB/s": alg / s / 1e9, "frac_of_hbm_peak": alg / s / HBM_PEAK,
+                 "plan": ex.explain().splitlines()[1].strip()[:400]}
+        try:
+            from oracle import interpret
+            from oracle.data import relative
+            idx = torch.tensor([0, 777, 16384, ROWS - 1], device="cuda")
+            xs, gs = x.index_select(0, idx).cpu().numpy(), g.index_select(0, idx).cpu().numpy()
+            f = interpret.softmax_grad if name == "softmax" else interpret.layernorm_grad
+            entry["parity_rel"] = relative(ex.outputs()[1].index_select(0, idx).cpu().numpy(), f(xs, gs)[1])
+        except Exception as err:
+            entry["parity_rel"] = repr(err)
+        out[name] = entry
+        del c, ex
+    out["note"] = ("generated floor: one reduction group per program (the column's folds in phases, loads kept in "
+                   "registers, dx written once) and the loss's full fold; events bracket both launches")
+    return out
+
+
 def cpu_baseline(x, g, budget_s: float = 10.0):
     """The oracle's Float32 floor (oracle/floor.c, one thread) on the first
     rows of the same X, G, 1024 rows at a time, both programs, until the
@@ -259,7 +299,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
-    ap.add_argument("--only", choices=["config1", "config3", "config4", "config5"], default=None,
+    ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config5"], default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
@@ -283,6 +323,12 @@ def main() -> int:
 
     target = th.HIPTarget()
     log("device:", target.device_name())
+    if a.only == "config2_floor":
+        gen = torch.Generator(device="cuda").manual_seed(20261201)
+        x = torch.randn(ROWS, N, device="cuda", generator=gen)
+        g = torch.randn(ROWS, N, device="cuda", generator=gen)
+        print(json.dumps({a.only: config2_floor(target, x, g, a.steps, a.warmup)}), flush=True)
+        return 0
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
@@ -306,6 +352,11 @@ def main() -> int:
                 "note": "per-program events bracket the fused row kernel and the loss's one-block sum"}
     configs = {"config2_parity_rel": c2["parity"]}
     if not a.only_config2:
+        try:
+            configs["config2_floor"] = config2_floor(target, c2["x"], c2["g"])
+        except Exception as err:
+            configs["config2_floor"] = {"error": repr(err)}
+        log("config2_floor:", json.dumps(configs["config2_floor"]))
         try:
             configs["config1_tanh_layer"] = config1(target)
         except Exception as err:

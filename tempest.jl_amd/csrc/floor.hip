@@ -289,7 +289,10 @@ int plan(const th_floor_desc* d, Plan& pl) {
       pl.vax = pl.W > 1 ? s0 : -1;
       pl.qn = pl.count / pl.W;
       pl.L = (int)std::min<int64_t>(256, std::max<int64_t>(64, nextpow2(pl.qn)));
-      if (pl.items < 8 * kCUs && pl.qn >= (int64_t)pl.L * 16) {
+      // Split an item's positions among workgroups only when few items leave
+      // the device idle and each lane would otherwise sweep 256+ steps: a
+      // shorter fold costs less than the extra launch and merge.
+      if (pl.items < 8 * kCUs && pl.qn >= (int64_t)pl.L * 256) {
         int64_t want = (8 * kCUs + pl.items - 1) / std::max<int64_t>(pl.items, 1);
         want = std::min<int64_t>(want, pl.qn / ((int64_t)pl.L * 8));
         pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(want, 1024));
@@ -369,12 +372,27 @@ __device__ __forceinline__ float th_ld(const float* p, long i) { return p[i]; }
 __device__ __forceinline__ float th_ld(const th_bf16* p, long i) { return th_bf(p[i]); }
 __device__ __forceinline__ float th_ld(float* p, long i) { return p[i]; }
 __device__ __forceinline__ float th_ld(th_bf16* p, long i) { return th_bf(p[i]); }
+__device__ __forceinline__ float th_ldn(const float* p, long i) { return __builtin_nontemporal_load(p + i); }
+__device__ __forceinline__ float th_ldn(const th_bf16* p, long i) { return th_bf(__builtin_nontemporal_load(p + i)); }
+__device__ __forceinline__ float th_ldn(float* p, long i) { return th_ldn((const float*)p, i); }
+__device__ __forceinline__ float th_ldn(th_bf16* p, long i) { return th_ldn((const th_bf16*)p, i); }
 __device__ __forceinline__ void th_st(float* p, long i, float v) { p[i] = v; }
 __device__ __forceinline__ void th_st(th_bf16* p, long i, float v) { p[i] = th_tobf(v); }
+__device__ __forceinline__ void th_stn(float* p, long i, float v) { __builtin_nontemporal_store(v, p + i); }
+__device__ __forceinline__ void th_stn(th_bf16* p, long i, float v) { __builtin_nontemporal_store(th_tobf(v), p + i); }
 __device__ __forceinline__ float th_abs(float x) { return fabsf(x); }
 __device__ __forceinline__ float th_abs2(float x) { return x * x; }
 __device__ __forceinline__ float th_sqrt(float x) { return sqrtf(x); }
-__device__ __forceinline__ float th_exp(float x) { return expf(x); }
+// exp(x) = 2^h 2^l, h = x log2(e) rounded, l its rounding error (an fma)
+// plus the tail of log2(e); 2^l = 1 + l ln 2 to second order.  About 2 ulp
+// against 13 instructions of the library's expf; x = -inf, +inf and NaN give
+// 0, inf and NaN (l is then NaN, and fminf takes the 1).
+__device__ __forceinline__ float th_exp(float x) {
+  const float h = x * 0x1.715476p+0f;
+  const float l = fmaf(x, 0x1.4ae0bep-26f, fmaf(x, 0x1.715476p+0f, -h));
+  const float e = __builtin_amdgcn_exp2f(h);
+  return fmaf(e, fminf(l * 0x1.62e430p-1f, 1.0f), e);
+}
 __device__ __forceinline__ float th_log(float x) { return logf(x); }
 __device__ __forceinline__ float th_tanh(float x) { return tanhf(x); }
 __device__ __forceinline__ float th_sin(float x) { return sinf(x); }
@@ -404,14 +422,14 @@ __device__ __forceinline__ float th_shift(float m) { return __builtin_isfinite(m
 // One exponential a step: the smaller of m and y is rebased to the larger.
 __device__ __forceinline__ void th_exp_step(float& m, float& s, float y, float g) {
   const float n = fmaxf(m, y);
-  const float e = expf(fminf(m, y) - th_shift(n));
+  const float e = th_exp(fminf(m, y) - th_shift(n));
   s = (y > m) ? s * e + g : s + g * e;
   m = n;
 }
 __device__ __forceinline__ void th_exp_comb(float& m, float& s, float m2, float s2) {
   const float n = fmaxf(m, m2);
   const float h = th_shift(n);
-  s = s * expf(m - h) + s2 * expf(m2 - h);
+  s = s * th_exp(m - h) + s2 * th_exp(m2 - h);
   m = n;
 }
 // Relative{Square}: state (n, mean, squared deviations), Welford's step and
@@ -442,6 +460,13 @@ __device__ __forceinline__ th_v th_ld4(const th_bf16* p, long i) {
   const th_h4 h = *(const th_h4*)(p + i);
   return (th_v){th_bf(h[0]), th_bf(h[1]), th_bf(h[2]), th_bf(h[3])};
 }
+__device__ __forceinline__ th_v th_ld4n(const float* p, long i) { return __builtin_nontemporal_load((const th_v*)(p + i)); }
+__device__ __forceinline__ th_v th_ld4n(const th_bf16* p, long i) {
+  const th_h4 h = __builtin_nontemporal_load((const th_h4*)(p + i));
+  return (th_v){th_bf(h[0]), th_bf(h[1]), th_bf(h[2]), th_bf(h[3])};
+}
+__device__ __forceinline__ th_v th_ld4n(float* p, long i) { return th_ld4n((const float*)p, i); }
+__device__ __forceinline__ th_v th_ld4n(th_bf16* p, long i) { return th_ld4n((const th_bf16*)p, i); }
 __device__ __forceinline__ th_v th_ld4(float* p, long i) { return th_ld4((const float*)p, i); }
 __device__ __forceinline__ th_v th_ld4(th_bf16* p, long i) { return th_ld4((const th_bf16*)p, i); }
 template <class T> __device__ __forceinline__ th_v th_lds4(T p, long i, long s) {
@@ -450,6 +475,10 @@ template <class T> __device__ __forceinline__ th_v th_lds4(T p, long i, long s) 
 __device__ __forceinline__ void th_st4(float* p, long i, th_v v) { *(th_v*)(p + i) = v; }
 __device__ __forceinline__ void th_st4(th_bf16* p, long i, th_v v) {
   *(th_h4*)(p + i) = (th_h4){th_tobf(v[0]), th_tobf(v[1]), th_tobf(v[2]), th_tobf(v[3])};
+}
+__device__ __forceinline__ void th_st4n(float* p, long i, th_v v) { __builtin_nontemporal_store(v, (th_v*)(p + i)); }
+__device__ __forceinline__ void th_st4n(th_bf16* p, long i, th_v v) {
+  __builtin_nontemporal_store((th_h4){th_tobf(v[0]), th_tobf(v[1]), th_tobf(v[2]), th_tobf(v[3])}, (th_h4*)(p + i));
 }
 template <class T> __device__ __forceinline__ void th_sts4(T p, long i, long s, th_v v) {
   th_st(p, i, v[0]); th_st(p, i + s, v[1]); th_st(p, i + 2 * s, v[2]); th_st(p, i + 3 * s, v[3]);
@@ -547,18 +576,19 @@ class Writer {
 
   // The value of term t in a scope: `vec` gives th_v values, `cached` reads
   // the swept loads from their registers (index `it`).
-  std::string term_expr(int t, bool vec, bool cached, const std::map<int, std::string>& names) {
+  std::string term_expr(int t, bool vec, bool cached, const std::map<int, std::string>& names,
+                        bool nt = false) {
     const th_term& m = d_->terms[t];
+    const std::string n = nt ? "n" : "";
     auto arg = [&](int j) { return names.at(m.args[j]); };
     switch (m.op) {
       case TH_TERM_LOAD: {
         if (cached && pl_.dep[t]) return "c" + std::to_string(t) + "[it]";
         std::string p = vname(m.ref), at = affine(pl_, m.index);
-        if (!vec) return "th_ld(" + p + ", " + at + ")";
-        if (pl_.W == 1) return "th_ld(" + p + ", " + at + ")";
+        if (!vec || pl_.W == 1) return "th_ld" + n + "(" + p + ", " + at + ")";
         const int64_t cv = m.index.coeff[pl_.vax];
         if (cv == 0) return "th_splat(th_ld(" + p + ", " + at + "))";
-        if (vector_access(pl_, m.ref, m.index)) return "th_ld4(" + p + ", " + at + ")";
+        if (vector_access(pl_, m.ref, m.index)) return "th_ld4" + n + "(" + p + ", " + at + ")";
         return "th_lds4(" + p + ", " + at + ", " + std::to_string(cv) + "L)";
       }
       case TH_TERM_LIT:
@@ -632,7 +662,8 @@ class Writer {
     if (pl_.resident) {
       o << ind << "#pragma unroll\n" << ind << "for (int it = 0; it < " << pl_.iters << "; ++it) {\n";
       o << ind << "  const long q = (long)it * " << pl_.L << " + lane;\n";
-      o << ind << "  if (q < " << qn << (guard_live ? " && live" : "") << ") {\n";
+      const bool guard_q = pl_.qn % pl_.L != 0;
+      o << ind << "  if (" << (guard_q ? "q < " + qn : std::string("true")) << (guard_live ? " && live" : "") << ") {\n";
     } else {
       std::string start = split_parts ? "(long)part * " + std::to_string(pl_.L) + " + lane" : "(long)lane";
       std::string step = std::to_string((long)pl_.L * (split_parts ? pl_.P : 1)) + "L";
@@ -868,15 +899,17 @@ class Writer {
 
   void store(const std::string& ind, const th_output& x, const std::string& val, bool vec) {
     std::string p = vname(x.value), at = affine(pl_, x.index);
+    // Full outputs are written once and not read again here: non-temporal.
+    const std::string n = x.full ? "n" : "";
     if (!vec || pl_.W == 1) {
-      o_ << ind << "th_st(" << p << ", " << at << ", " << val << ");\n";
+      o_ << ind << "th_st" << n << "(" << p << ", " << at << ", " << val << ");\n";
       return;
     }
     const int64_t cv = x.index.coeff[pl_.vax];
     if (cv == 0) {
       o_ << ind << "th_st(" << p << ", " << at << ", (" << val << ")[" << pl_.W - 1 << "]);\n";
     } else if (vector_access(pl_, x.value, x.index)) {
-      o_ << ind << "th_st4(" << p << ", " << at << ", " << val << ");\n";
+      o_ << ind << "th_st4" << n << "(" << p << ", " << at << ", " << val << ");\n";
     } else {
       o_ << ind << "th_sts4(" << p << ", " << at << ", " << cv << "L, " << val << ");\n";
     }
@@ -922,7 +955,7 @@ class Writer {
       std::map<int, std::string> none;
       for (int t = 0; t < d_->n_terms; ++t)
         if (d_->terms[t].op == TH_TERM_LOAD && pl_.dep[t])
-          o << "      c" << t << "[it] = " << term_expr(t, pl_.W > 1, false, none) << ";\n";
+          o << "      c" << t << "[it] = " << term_expr(t, pl_.W > 1, false, none, true) << ";\n";
       o << "    } else {\n";
       for (int t = 0; t < d_->n_terms; ++t)
         if (d_->terms[t].op == TH_TERM_LOAD && pl_.dep[t]) o << "      c" << t << "[it] = th_splat(0.0f);\n";

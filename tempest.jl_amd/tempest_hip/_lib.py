@@ -61,6 +61,39 @@ class DeltaNetDesc(ctypes.Structure):
                 ("da", c_void_p), ("dbeta", c_void_p), ("strides", c_i64 * 3), ("gate_strides", c_i64 * 3)]
 
 
+FLOOR_RANK = 4
+
+
+class Affine(ctypes.Structure):
+    _fields_ = [("constant", c_i64), ("coeff", c_i64 * FLOOR_RANK)]
+
+
+class FloorValue(ctypes.Structure):
+    _fields_ = [("dtype", c_i32), ("reserved", c_i32), ("length", c_i64), ("ptr", c_void_p)]
+
+
+class TermStruct(ctypes.Structure):
+    _fields_ = [("op", c_i32), ("fn", c_i32), ("args", c_i32 * 3), ("ref", c_i32),
+                ("observe", c_i32), ("lit", c_f32), ("index", Affine)]
+
+
+class FoldStruct(ctypes.Structure):
+    _fields_ = [("kind", c_i32), ("phase", c_i32), ("body", c_i32), ("weight", c_i32)]
+
+
+class OutputStruct(ctypes.Structure):
+    _fields_ = [("value", c_i32), ("term", c_i32), ("full", c_i32), ("reserved", c_i32),
+                ("index", Affine)]
+
+
+class FloorDesc(ctypes.Structure):
+    _fields_ = [("kind", c_i32), ("rank", c_i32), ("extents", c_i64 * FLOOR_RANK),
+                ("reduced", ctypes.c_uint32), ("n_values", c_i32), ("n_terms", c_i32),
+                ("n_folds", c_i32), ("n_outputs", c_i32), ("reserved", c_i32),
+                ("values", ctypes.POINTER(FloorValue)), ("terms", ctypes.POINTER(TermStruct)),
+                ("folds", ctypes.POINTER(FoldStruct)), ("outputs", ctypes.POINTER(OutputStruct))]
+
+
 class HIPError(RuntimeError):
     """A libtempest_hip entry point returned a non-zero status."""
 
@@ -110,6 +143,9 @@ SIGNATURES: dict[str, list] = {
     "th_build_attention_bwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_deltanet_fwd": [P(DeltaNetDesc), P(c_void_p)],
     "th_build_deltanet": [P(DeltaNetDesc), P(c_void_p)],
+    "th_build_floor": [P(FloorDesc), P(c_void_p)],
+    "th_floor_source": [P(FloorDesc), c_char_p, c_size, P(c_size)],
+    "th_floor_compile": [P(FloorDesc)],
     "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, P(c_void_p)],
 }

@@ -27,11 +27,11 @@ from dataclasses import dataclass, field
 from typing import Sequence
 
 from . import _lib
-from ._lib import call
+from ._lib import Affine, FloorDesc, FloorValue, FoldStruct, OutputStruct, TermStruct, call  # noqa: F401
 from .launch import Launch
 from .runtime import Group
 
-RANK = 4
+RANK = _lib.FLOOR_RANK
 
 GROUP = {"pointwise": 0, "reduction": 1}
 TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4}
@@ -44,52 +44,6 @@ ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", 
 FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5}
 OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}
 DTYPE = {"f32": 0, "bf16": 1}
-
-
-class Affine(ctypes.Structure):
-    _fields_ = [("constant", _lib.c_i64), ("coeff", _lib.c_i64 * RANK)]
-
-
-class FloorValue(ctypes.Structure):
-    _fields_ = [("dtype", _lib.c_i32), ("reserved", _lib.c_i32), ("length", _lib.c_i64), ("ptr", _lib.c_void_p)]
-
-
-class TermStruct(ctypes.Structure):
-    _fields_ = [("op", _lib.c_i32), ("fn", _lib.c_i32), ("args", _lib.c_i32 * 3), ("ref", _lib.c_i32),
-                ("observe", _lib.c_i32), ("lit", _lib.c_f32), ("index", Affine)]
-
-
-class FoldStruct(ctypes.Structure):
-    _fields_ = [("kind", _lib.c_i32), ("phase", _lib.c_i32), ("body", _lib.c_i32), ("weight", _lib.c_i32)]
-
-
-class OutputStruct(ctypes.Structure):
-    _fields_ = [("value", _lib.c_i32), ("term", _lib.c_i32), ("full", _lib.c_i32), ("reserved", _lib.c_i32),
-                ("index", Affine)]
-
-
-class FloorDesc(ctypes.Structure):
-    _fields_ = [("kind", _lib.c_i32), ("rank", _lib.c_i32), ("extents", _lib.c_i64 * RANK),
-                ("reduced", ctypes.c_uint32), ("n_values", _lib.c_i32), ("n_terms", _lib.c_i32),
-                ("n_folds", _lib.c_i32), ("n_outputs", _lib.c_i32), ("reserved", _lib.c_i32),
-                ("values", ctypes.POINTER(FloorValue)), ("terms", ctypes.POINTER(TermStruct)),
-                ("folds", ctypes.POINTER(FoldStruct)), ("outputs", ctypes.POINTER(OutputStruct))]
-
-
-_SIGNATURES = {
-    "th_build_floor": [ctypes.POINTER(FloorDesc), _lib.P(_lib.c_void_p)],
-    "th_floor_source": [ctypes.POINTER(FloorDesc), _lib.c_char_p, _lib.c_size, _lib.P(_lib.c_size)],
-    "th_floor_compile": [ctypes.POINTER(FloorDesc)],
-}
-_lib.SIGNATURES.update(_SIGNATURES)
-
-
-def _call(name: str, *args) -> None:
-    # The library may have been loaded before this module added its entries.
-    f = getattr(_lib.load(), name)
-    if f.argtypes != _SIGNATURES[name]:
-        f.argtypes, f.restype = _SIGNATURES[name], _lib.c_int
-    call(name, *args)
 
 
 class Term:
@@ -269,15 +223,15 @@ class FloorGroup:
         """The generated HIP source (needs no device)."""
         d, keep = self._desc(ptrs or self._stand_in())
         need = _lib.c_size()
-        _call("th_floor_source", ctypes.byref(d), None, 0, ctypes.byref(need))
+        call("th_floor_source", ctypes.byref(d), None, 0, ctypes.byref(need))
         buf = ctypes.create_string_buffer(need.value)
-        _call("th_floor_source", ctypes.byref(d), buf, need.value, ctypes.byref(need))
+        call("th_floor_source", ctypes.byref(d), buf, need.value, ctypes.byref(need))
         return buf.value.decode()
 
     def compile(self, ptrs: Sequence[int] | None = None) -> None:
         """Compile into the code-object cache (needs no device)."""
         d, keep = self._desc(ptrs or self._stand_in())
-        _call("th_floor_compile", ctypes.byref(d))
+        call("th_floor_compile", ctypes.byref(d))
 
     def build(self, ptrs: dict[str, int]) -> Launch:
         """The group's launch over the values at ``ptrs`` (name -> device address)."""
@@ -287,7 +241,7 @@ class FloorGroup:
             raise ValueError(f"{self.name}: no address for {missing}")
         d, keep = self._desc([int(ptrs[n]) for n in order])
         out = ctypes.c_void_p()
-        _call("th_build_floor", ctypes.byref(d), ctypes.byref(out))
+        call("th_build_floor", ctypes.byref(d), ctypes.byref(out))
         return Launch(out, tuple(order))
 
     def as_group(self) -> Group:

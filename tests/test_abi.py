@@ -75,3 +75,32 @@ def test_slot_planner_reuses_free_slots():
         spans.sort()
         for (a0, a1), (b0, b1) in zip(spans, spans[1:]):
             assert a1 < b0
+
+
+def test_floor_structures_match_the_header(tmp_path):
+    """sizeof and member offsets of the generated floor's structures, as gcc
+    lays out include/tempest_hip.h, against the ctypes mirror."""
+    import subprocess
+    import tempest_hip._lib as L
+    members = {"th_affine": (L.Affine, ["constant", "coeff"]),
+               "th_floor_value": (L.FloorValue, ["dtype", "length", "ptr"]),
+               "th_term": (L.TermStruct, ["op", "fn", "args", "ref", "observe", "lit", "index"]),
+               "th_fold": (L.FoldStruct, ["kind", "phase", "body", "weight"]),
+               "th_output": (L.OutputStruct, ["value", "term", "full", "index"]),
+               "th_floor_desc": (L.FloorDesc, ["kind", "rank", "extents", "reduced", "n_values", "n_terms",
+                                               "n_folds", "n_outputs", "values", "terms", "folds", "outputs"])}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT}/include/tempest_hip.h"', 'int main(void) {']
+    for s, (_, ms) in members.items():
+        lines.append(f'  printf("{s} %zu\\n", sizeof({s}));')
+        for m in ms:
+            lines.append(f'  printf("{s}.{m} %zu\\n", offsetof({s}, {m}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n") if l)
+    for s, (cls, ms) in members.items():
+        assert int(got[s]) == ctypes.sizeof(cls), s
+        for m in ms:
+            assert int(got[f"{s}.{m}"]) == getattr(cls, m).offset, (s, m)
