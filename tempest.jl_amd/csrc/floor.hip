@@ -49,7 +49,7 @@ constexpr int kRank = TH_FLOOR_RANK;
 constexpr int kMaxArgs = 64;        // pointers in a kernel's argument struct (512 bytes)
 constexpr int kCUs = 256;           // MI355X
 constexpr int kResidentFloats = 128;  // registers a thread may spend keeping loads
-constexpr int kMaxIters = 16;
+constexpr int kMaxIters = 32;
 
 int arity(int fn) {
   switch (fn) {
@@ -667,6 +667,8 @@ class Writer {
     } else {
       std::string start = split_parts ? "(long)part * " + std::to_string(pl_.L) + " + lane" : "(long)lane";
       std::string step = std::to_string((long)pl_.L * (split_parts ? pl_.P : 1)) + "L";
+      // Four steps unrolled: four loads of each value in flight per lane.
+      o << ind << "#pragma unroll 4\n";
       o << ind << "for (long q = " << start << "; q < " << (guard_live ? "(live ? " + qn + " : 0L)" : qn)
         << "; q += " << step << ") {\n";
       o << ind << "  {\n";
