@@ -218,4 +218,105 @@ function build(::HIPRows, ::HIPTarget, b::Binding, resources)
     (HIPLaunch(out[], Any[x.buffer, g.buffer, dx.buffer, loss]), "fused softmax gradient, rows resident")
 end
 
+# ---- the floor: any pointwise or reduction group, generated ---------------------------
+#
+# The reference's floor turns a group into Julia code (scalar_kernel,
+# src/Compiler/codegen/scalar.jl:186-250) and CUDA compiles it (floor_launch,
+# ext/CUDAExt.jl:926-937).  Here the group's terms cross the C ABI as arrays
+# (th_floor_desc) and libtempest_hip writes and compiles the gfx950 kernel.
+# Supported: Var atoms in addresses (Div, Mod and Indirect atoms throw, and the
+# build falls back), the functions of FLOOR_FN, and the folds of FLOOR_FOLD.
+
+struct FloorValue; dtype::Int32; reserved::Int32; length::Int64; ptr::Ptr{Cvoid}; end
+struct CAffine; constant::Int64; coeff::NTuple{4, Int64}; end
+struct CTerm; op::Int32; fn::Int32; args::NTuple{3, Int32}; ref::Int32; observe::Int32; lit::Float32; index::CAffine; end
+struct CFold; kind::Int32; phase::Int32; body::Int32; weight::Int32; end
+struct COutput; value::Int32; term::Int32; full::Int32; reserved::Int32; index::CAffine; end
+struct FloorDesc
+    kind::Int32; rank::Int32; extents::NTuple{4, Int64}; reduced::UInt32
+    n_values::Int32; n_terms::Int32; n_folds::Int32; n_outputs::Int32; reserved::Int32
+    values::Ptr{FloorValue}; terms::Ptr{CTerm}; folds::Ptr{CFold}; outputs::Ptr{COutput}
+end
+
+const FLOOR_FN = IdDict{Any, Int32}(+ => 0, - => 1, * => 2, / => 3, abs => 5, abs2 => 6, sqrt => 7, exp => 8,
+    log => 9, tanh => 10, sin => 11, cos => 12, log1p => 13, expm1 => 14, (^) => 15, max => 16, min => 17,
+    (<) => 18, (<=) => 19, (>) => 20, (>=) => 21, (==) => 22, (!=) => 23, ifelse => 24, round => 25,
+    floor => 26, ceil => 27, sign => 28, clamp => 29, fma => 30, inv => 31)
+
+# A fold value's (kind, observe): SumFold, MaxFold, MinFold, ProdFold; the
+# exponential and square laws with their Statistic / Sum(1) / LOGSUMEXP observes.
+function floor_fold(fold)
+    F = Tempest.Compiler.IR
+    fold isa F.SumFold && return (0, 0)
+    fold isa F.ProdFold && return (1, 0)
+    fold isa F.MaxFold && return (2, 0)
+    fold isa F.MinFold && return (3, 0)
+    if fold isa F.Relative
+        kind = fold.law isa F.Exponential ? 4 : fold.law isa F.Square ? 5 : throw(ArgumentError("fold law"))
+        obs = fold.observe isa F.Statistic ? 1 : fold.observe isa F.Sum ? 2 : kind == 4 ? 3 : throw(ArgumentError("observe"))
+        return (kind, obs)
+    end
+    throw(ArgumentError("the generated floor has no fold $(typeof(fold))"))
+end
+
+function caffine(e, vars)
+    c = zeros(Int64, 4)
+    for (atom, k) in e.terms
+        atom isa Tempest.Compiler.IR.Var || throw(ArgumentError("only positions in floor addresses"))
+        c[atom.n] += k
+    end
+    CAffine(e.constant, Tuple(c))
+end
+
+# The group as th_floor_desc arrays; `slots` numbers its values, `buffers` their storage.
+function floor_descriptor(graph, g, slots, buffers)
+    C = Tempest.Compiler
+    terms, index = CTerm[], IdDict{Any, Int32}()
+    folds = [r for r in g.reductions]
+    fold_no = Dict(r => Int32(i - 1) for (i, r) in enumerate(folds))
+    z = CAffine(0, (0, 0, 0, 0))
+    function add!(t)
+        haskey(index, t) && return index[t]
+        ct = if t isa C.IR.Load
+            CTerm(0, 0, (0, 0, 0), findfirst(==(t.value), slots) - 1, 0, 0f0,
+                  caffine(C.address(graph.values[t.value], t.index, C.Domain(g.domain)), nothing))
+        elseif t isa C.IR.Lit
+            CTerm(1, 0, (0, 0, 0), 0, 0, Float32(t.value), z)
+        elseif t isa C.IR.Ix
+            CTerm(2, 0, (0, 0, 0), 0, 0, 0f0, caffine(t.expr, nothing))
+        elseif t isa C.IR.Stat
+            CTerm(3, 0, (0, 0, 0), fold_no[t.value], floor_fold(graph.values[t.value].definition.fold)[2], 0f0, z)
+        elseif t isa C.IR.Apply
+            a = Int32[add!(x) for x in t.args]
+            CTerm(4, FLOOR_FN[t.f], (get(a, 1, 0), get(a, 2, 0), get(a, 3, 0)), 0, 0, 0f0, z)
+        else
+            throw(ArgumentError("the generated floor has no term $(typeof(t))"))
+        end
+        push!(terms, ct)
+        index[t] = Int32(length(terms) - 1)
+    end
+    cfolds = [CFold(floor_fold(graph.values[r].definition.fold)[1], g.phase[r], add!(g.terms[r]), -1) for r in folds]
+    outs = [COutput(findfirst(==(m), slots) - 1, add!(g.terms[m]), graph.values[m].dims == g.domain, 0,
+                    caffine(C.address(graph.values[m], C.identity_index(g.domain), C.Domain(g.domain)), nothing))
+            for m in g.outputs]
+    vals = [FloorValue(graph.values[v].eltype === Float32 ? 0 : 1, 0, C.storage_length(graph.values[v]),
+                       address(buffers[i])) for (i, v) in enumerate(slots)]
+    ext = ntuple(k -> k <= length(g.domain) ? Int64(g.domain[k]) : 1, 4)
+    reduced = UInt32(sum((1 << (k - 1) for k in C.primary_axes(graph, g)); init = 0))
+    (vals, terms, cfolds, outs, ext, reduced, isempty(folds) ? 0 : 1)
+end
+
+function build_floor(target::HIPTarget, p, g, buffers)
+    slots = Tempest.Compiler.kernel_slots(p, g, Tempest.Compiler.floor_stored(p, g))
+    vals, terms, folds, outs, ext, reduced, kind = floor_descriptor(p.graph, g, slots, [buffers[v] for v in slots])
+    GC.@preserve vals terms folds outs begin
+        d = Ref(FloorDesc(kind, length(g.domain), ext, reduced,
+                          length(vals), length(terms), length(folds), length(outs), 0,
+                          pointer(vals), pointer(terms), pointer(folds), pointer(outs)))
+        out = Ref{Ptr{Cvoid}}()
+        check(ccall((:th_build_floor, LIB), Cint, (Ptr{FloorDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_floor")
+    end
+    HIPLaunch(out[], Any[buffers[v] for v in slots])
+end
+
 end # module
