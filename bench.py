@@ -127,28 +127,133 @@ def config2_floor(target, x, g, steps: int = 10, warmup: int = 3):
 
 
 def cpu_baseline(x, g, budget_s: float = 10.0):
-    """The oracle's Float32 floor (oracle/floor.c, one thread) on the first
-    rows of the same X, G, 1024 rows at a time, both programs, until the
-    budget is spent or 16384 rows are done."""
-    import numpy as np
+    """The oracle's Float32 floor (oracle/floor.c, one thread) over the whole
+    X, G (both programs, all 32768 rows, 1024 at a time), repeated until the
+    budget is spent."""
     from oracle import floor
 
-    done = 0
-    spent = 0.0
+    xs, gs = x.cpu().numpy(), g.cpu().numpy()
+    passes, spent = 0, 0.0
     chunk = 1024
-    while spent < budget_s and done < 16384:
-        xs = x[done:done + chunk].cpu().numpy()
-        gs = g[done:done + chunk].cpu().numpy()
+    while spent < budget_s or passes == 0:
         t = time.perf_counter()
-        floor.softmax_grad(xs, gs)
-        floor.layernorm_grad(xs, gs)
+        for r in range(0, ROWS, chunk):
+            floor.softmax_grad(xs[r:r + chunk], gs[r:r + chunk])
+            floor.layernorm_grad(xs[r:r + chunk], gs[r:r + chunk])
         spent += time.perf_counter() - t
-        done += chunk
-    rate = 2 * 3.0 * 4 * done * N / spent / 1e9
+        passes += 1
+        if passes >= 8:
+            break
+    step_s = spent / passes
+    rate = 2 * 3.0 * 4 * ROWS * N / step_s / 1e9
     return {"value": rate, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"oracle/floor.c (the reference's CPU floor restated in C, -O2, 1 thread): both programs "
-                      f"on the first {done} of {ROWS} rows ({spent:.1f} s)",
-            "seconds_full_step_extrapolated": spent * ROWS / done}
+                      f"over all {ROWS} rows, {passes} passes ({spent:.1f} s)",
+            "seconds_full_step": step_s}
+
+
+def _one_thread():
+    from threadpoolctl import threadpool_limits
+    return threadpool_limits(1)
+
+
+def cpu_config1(reps: int = 2000):
+    """Config 1 on one core: the floor's order (oracle/floor.c), microseconds a step."""
+    import numpy as np
+    from oracle import floor
+    rng = np.random.default_rng(1)
+    w, b, x = rng.standard_normal((32, 64)), rng.standard_normal(64), rng.standard_normal((32, 16))
+    floor.tanh_layer_grad(w, b, x)
+    t = time.perf_counter()
+    for _ in range(reps):
+        floor.tanh_layer_grad(w, b, x)
+    s = (time.perf_counter() - t) / reps
+    return {"value": s * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"oracle/floor.c tanh_layer_grad, {reps} steps (host wrappers included)"}
+
+
+def cpu_config3(cols: int = 4):
+    """Config 3's six products on one core, each on `cols` of its output
+    columns (every element a sequential fp32 fold over bf16 factors, the
+    floor's order), extrapolated by the columns: the products are 2mnk flops
+    each and their elements independent, so the slice's share of the work is
+    exactly cols / n.  The fused element-wise work is left out (< 0.1 %)."""
+    import numpy as np
+    from oracle import floor
+    rng = np.random.default_rng(3)
+    batch, d_in, hidden, d_out = 4096, 4096, 16384, 4096
+    # Operand bits for timing: normal values truncated to bf16, one buffer
+    # large enough for every product's A (its contents do not change the work).
+    pool = (rng.standard_normal(hidden * d_in, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+    def bits(n):
+        return pool[:n]
+    # (m, n, k, A layout (a_m, a_k) with A m x k stored as the product reads it, B k-contiguous)
+    shapes = [("Z1 = W1 x", hidden, batch, d_in, (1, hidden)), ("y = W2 H", d_out, batch, hidden, (1, d_out)),
+              ("dW2 = dy H'", d_out, hidden, batch, (1, d_out)), ("dZ1 = W2' dy", hidden, batch, d_out, (d_out, 1)),
+              ("dW1 = dZ1 x'", hidden, d_in, batch, (1, hidden)), ("dx = W1' dZ1", d_in, batch, hidden, (hidden, 1))]
+    total, spent, flops_done = 0.0, 0.0, 0.0
+    for name, m, n, k, (a_m, a_k) in shapes:
+        a = bits(m * k)
+        b = bits(k * cols)
+        t = time.perf_counter()
+        floor.matmul_bf16(a, a_m, a_k, b, 1, k, m, k, 0, cols)
+        dt = time.perf_counter() - t
+        spent += dt
+        flops_done += 2.0 * m * k * cols
+        total += dt * n / cols
+    return {"value": 6 * 2.0 * batch * hidden * d_in / total / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/floor.c matmul_bf16: {cols} output columns of each of the six products "
+                      f"({flops_done / 1e9:.2f} GFLOP in {spent:.1f} s), extrapolated by n / {cols}",
+            "seconds_full_step_extrapolated": total}
+
+
+def cpu_config4(step: int = 4):
+    """Config 4 on one core: forward and backward of one (batch, head) for
+    every `step`-th query (oracle/floor.c attention_sample, the program's
+    folds in sequence), extrapolated by (query, key) pairs: the work of a
+    query is proportional to the keys it sees, so the full step is the
+    sample's time x (all pairs / sampled pairs) x batch x heads."""
+    import numpy as np
+    from oracle import floor
+    B, H, S, D = 8, 16, 4096, 128
+    rng = np.random.default_rng(4)
+    q, k, v, g = ((rng.standard_normal((S, D), dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+                  for _ in range(4))
+    t = time.perf_counter()
+    floor.attention_sample(q, k, v, g, 1 / np.sqrt(D), 0, step)
+    dt = time.perf_counter() - t
+    sampled = sum(i + 1 for i in range(0, S, step))
+    pairs = S * (S + 1) // 2
+    total = dt * pairs / sampled * B * H
+    flops = 4 * B * H * S * S * D / 2 * 3.5
+    return {"value": flops / total / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/floor.c attention_sample: one (batch, head), every {step}th query "
+                      f"({sampled} of {pairs} pairs, {dt:.1f} s), extrapolated by pairs x {B * H}",
+            "seconds_full_step_extrapolated": total}
+
+
+def cpu_config5():
+    """Config 5 on one core: the oracle's chunked DeltaNet forward and
+    gradient (oracle/interpret.py, float64, BLAS held to one thread) for one
+    (batch, head) sequence, times batch x heads (the sequences are independent)."""
+    import numpy as np
+    from oracle import interpret
+    B, H, T = 4, 16, 8192
+    rng = np.random.default_rng(5)
+    unit = lambda x: x / np.linalg.norm(x, axis=-1, keepdims=True)  # noqa: E731
+    q, k = unit(rng.standard_normal((1, T, 1, 128))), unit(rng.standard_normal((1, T, 1, 128)))
+    v, do = rng.standard_normal((1, T, 1, 128)), rng.standard_normal((1, T, 1, 128))
+    a = -np.logaddexp(0, rng.standard_normal((1, T, 1)))
+    beta = 1 / (1 + np.exp(-rng.standard_normal((1, T, 1))))
+    with _one_thread():
+        t = time.perf_counter()
+        interpret.deltanet_grad(q, k, v, a, beta, do)
+        dt = time.perf_counter() - t
+    return {"value": dt * B * H * 1e3, "unit": "ms/step", "cores": 1, "kind": "port",
+            "sample": f"oracle/interpret.py deltanet_grad (chunked, float64, one BLAS thread): one (batch, head) "
+                      f"sequence of {T} in {dt:.2f} s, times {B * H}",
+            "seconds_full_step_extrapolated": dt * B * H}
 
 
 def config1(target):
@@ -382,6 +487,17 @@ def main() -> int:
             cpu = cpu_baseline(c2["x"], c2["g"])
         except Exception as err:
             cpu = {"error": repr(err)}
+        log("cpu_baseline:", json.dumps(cpu))
+        # The other configs' CPU paths, each beside its own figures.
+        for key, fn in (("config1_tanh_layer", cpu_config1), ("config3_mlp", cpu_config3),
+                        ("config4_attention", cpu_config4), ("config5_deltanet", cpu_config5)):
+            try:
+                r = fn()
+            except Exception as err:
+                r = {"error": repr(err)}
+            if isinstance(configs.get(key), dict):
+                configs[key]["cpu_baseline"] = r
+            log(key, "cpu:", json.dumps(r))
     line = {
         "metric": "GB/s fused reduce (config 2: softmax and LayerNorm fwd+grad over X 32768x8192 fp32)",
         "value": value, "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,

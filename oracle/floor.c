@@ -155,3 +155,81 @@ void floor_tanh_layer_grad(int32_t d, int32_t h, int32_t c, const float* w, cons
     db[j] = s;
   }
 }
+
+/* bfloat16 bits widened to float. */
+static float bf(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+/*
+ * Config 3's products as the floor runs them on one core: C(i, j) = the fold
+ * over l of A(i, l) B(l, j), an item per element of C in column-major order,
+ * each fold sequential in fp32 over bf16 factors widened (codegen/scalar.jl:
+ * 200-256; half factors accumulate in fp32, IR/folds.jl:306-309).  A(i, l) is
+ * a[i a_m + l a_k], B(l, j) is b[l b_k + j b_n]; only the columns j0 .. j1 - 1
+ * of C are computed (a slice whose work is (j1 - j0) / n of the product's).
+ */
+void floor_matmul_bf16(int32_t m, int32_t k, const uint16_t* a, int64_t a_m, int64_t a_k, const uint16_t* b,
+                       int64_t b_k, int64_t b_n, float* c, int64_t c_ld, int32_t j0, int32_t j1) {
+  for (int32_t j = j0; j < j1; ++j)
+    for (int32_t i = 0; i < m; ++i) {
+      float s = 0.0f;
+      for (int32_t l = 0; l < k; ++l) s += bf(a[i * a_m + l * a_k]) * bf(b[l * b_k + j * b_n]);
+      c[i + (int64_t)(j - j0) * c_ld] = s;
+    }
+}
+
+/*
+ * Config 4 on one core for one (batch, head) and a sample of its queries
+ * (q0, q0 + step, ...): the program's forward (scores over the keys a query
+ * sees, causal; its maximum, exponentials and sum; o = P V) and backward
+ * (delta = dO . o, dP = dO V', dS = P (dP - delta), dq = scale dS K,
+ * dk += scale dS' q, dv += P' dO) for each sampled query, every fold
+ * sequential in fp32 (test/fixtures/operations.jl:21-70).  q, k, v, dout:
+ * bf16 rows of d at `stride` elements per position.  dq: one row per sampled
+ * query; dk, dv: seq x d fp32, accumulated.  `p` is seq floats of scratch.
+ * Work: 12 d flops per (query, key) pair it sweeps.
+ */
+void floor_attention_sample(int32_t seq, int32_t d, float scale, const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, const uint16_t* dout, int64_t stride, int32_t q0, int32_t step,
+                            float* dq, float* dk, float* dv, float* p) {
+  int32_t row = 0;
+  for (int32_t i = q0; i < seq; i += step, ++row) {
+    const uint16_t* qi = q + (int64_t)i * stride;
+    const uint16_t* gi = dout + (int64_t)i * stride;
+    float mx = -INFINITY;
+    for (int32_t j = 0; j <= i; ++j) {
+      float s = 0.0f;
+      for (int32_t e = 0; e < d; ++e) s += bf(qi[e]) * bf(k[(int64_t)j * stride + e]);
+      p[j] = s * scale;
+      mx = p[j] > mx ? p[j] : mx;
+    }
+    float l = 0.0f;
+    for (int32_t j = 0; j <= i; ++j) {
+      p[j] = expf(p[j] - lse_shift(mx));
+      l += p[j];
+    }
+    float delta = 0.0f;
+    float* dqi = dq + (int64_t)row * d;
+    for (int32_t e = 0; e < d; ++e) {
+      float o = 0.0f;
+      for (int32_t j = 0; j <= i; ++j) o += p[j] * bf(v[(int64_t)j * stride + e]);
+      delta += bf(gi[e]) * (o / l);
+      dqi[e] = 0.0f;
+    }
+    for (int32_t j = 0; j <= i; ++j) {
+      const float pj = p[j] / l;
+      float dp = 0.0f;
+      for (int32_t e = 0; e < d; ++e) dp += bf(gi[e]) * bf(v[(int64_t)j * stride + e]);
+      const float ds = pj * (dp - delta);
+      for (int32_t e = 0; e < d; ++e) {
+        dqi[e] += scale * ds * bf(k[(int64_t)j * stride + e]);
+        dk[(int64_t)j * d + e] += scale * ds * bf(qi[e]);
+        dv[(int64_t)j * d + e] += pj * bf(gi[e]);
+      }
+    }
+  }
+}

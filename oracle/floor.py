@@ -2,8 +2,10 @@
 
 The library is built by ``make -C oracle`` (also by __graft_entry__.build()).
 Each function takes numpy float32 arrays in the layout the kernels use and
-runs on one thread.  Pinning: tests/test_oracle_floor.py checks every
-function against the Float64 interpreter within Float32 rounding.
+runs on one thread.  Pinning: tests/test_oracle_rows.py and
+tests/test_oracle_tiny.py check the row and config-1 functions against the
+Float64 interpreter within Float32 rounding; tests/test_oracle_cpu_floor.py
+checks the product and attention slices against numpy and the interpreter.
 """
 from __future__ import annotations
 
@@ -31,8 +33,13 @@ def lib() -> ctypes.CDLL:
         L.floor_softmax_fwd.argtypes = [i64, i32, i64, _f32p, _f32p]
         L.floor_layernorm_fwd.argtypes = [i64, i32, i64, f32, _f32p, _f32p]
         L.floor_tanh_layer_grad.argtypes = [i32, i32, i32, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        u16p = ctypes.POINTER(ctypes.c_uint16)
+        L.floor_matmul_bf16.argtypes = [i32, i32, u16p, i64, i64, u16p, i64, i64, _f32p, i64, i32, i32]
+        L.floor_attention_sample.argtypes = [i32, i32, f32, u16p, u16p, u16p, u16p, i64, i32, i32,
+                                             _f32p, _f32p, _f32p, _f32p]
         for f in (L.floor_softmax_grad, L.floor_layernorm_grad, L.floor_softmax_fwd,
-                  L.floor_layernorm_fwd, L.floor_tanh_layer_grad):
+                  L.floor_layernorm_fwd, L.floor_tanh_layer_grad, L.floor_matmul_bf16,
+                  L.floor_attention_sample):
             f.restype = None
         _LIB = L
     return _LIB
@@ -93,3 +100,34 @@ def tanh_layer_grad(w: np.ndarray, b: np.ndarray, x: np.ndarray):
     dz = np.zeros((h, c), np.float32, order="F")
     lib().floor_tanh_layer_grad(d, h, c, _p(wf), _p(bf), _p(xf), _p(loss), _p(dw), _p(db), _p(dx), _p(dz))
     return float(loss[0]), dw, db, dx
+
+
+def _u16(a: np.ndarray):
+    assert a.dtype == np.uint16
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def matmul_bf16(a_bits: np.ndarray, a_m: int, a_k: int, b_bits: np.ndarray, b_k: int, b_n: int,
+                m: int, k: int, j0: int, j1: int) -> np.ndarray:
+    """Columns j0 .. j1-1 of C = A B (m x k times k x n, bf16 bits with the
+    given element strides), each element a sequential fp32 fold over k;
+    returned as an m x (j1 - j0) float32 array, column-major."""
+    c = np.zeros((m, j1 - j0), np.float32, order="F")
+    lib().floor_matmul_bf16(m, k, _u16(a_bits), a_m, a_k, _u16(b_bits), b_k, b_n, _p(c), m, j0, j1)
+    return c
+
+
+def attention_sample(q, k, v, dout, scale: float, q0: int, step: int):
+    """One (batch, head): q, k, v, dout are seq x d bf16 bits (row per
+    position).  Returns dq of the sampled queries (q0, q0 + step, ...) and the
+    dk, dv those queries contribute (seq x d)."""
+    seq, d = q.shape
+    rows = len(range(q0, seq, step))
+    dq = np.zeros((rows, d), np.float32)
+    dk = np.zeros((seq, d), np.float32)
+    dv = np.zeros((seq, d), np.float32)
+    p = np.zeros(seq, np.float32)
+    qs, ks, vs, gs = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, dout))
+    lib().floor_attention_sample(seq, d, scale, _u16(qs), _u16(ks), _u16(vs), _u16(gs), d, q0, step,
+                                 _p(dq), _p(dk), _p(dv), _p(p))
+    return dq, dk, dv
