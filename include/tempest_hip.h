@@ -224,7 +224,13 @@ int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out
 
 #define TH_FLOOR_RANK 4
 
-enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1 };
+/* A scan group sweeps its scanned axes (`reduced`) one item at a time, in
+ * order (reversed with TH_FLOOR_REVERSE): at each position every fold takes
+ * its element in (phase, index) order, a scan's result there is what later
+ * folds and the full outputs read, and the plain folds' results are read by
+ * the once outputs after the sweep (scan_kernel, codegen/scalar.jl:350-398). */
+enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1, TH_GROUP_SCAN = 2 };
+#define TH_FLOOR_REVERSE 1
 
 /* Terms (Load, Lit, Ix, Stat, Apply of src/Compiler/IR):
  *   TH_TERM_LOAD   element index(i) of value `ref`, widened to fp32
@@ -251,13 +257,18 @@ enum {
  *                   the sum of weight * exp(y - lse_shift(m)) (weight 1 when
  *                   the fold's weight is -1)
  *   TH_FOLD_SQUARE  Relative{Square}: the mean of the body and the sum of
- *                   squared deviations from it (Chan's combination) */
-enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_FOLD_SQUARE };
+ *                   squared deviations from it (Chan's combination)
+ *   TH_FOLD_LINEAR  the linear recurrence h = a h' + b from h = 0, a the
+ *                   body and b the weight: state (product of the a's, h),
+ *                   combined earlier-first as (a2 a1, a2 b1 + b2) (the
+ *                   `chain` of test/fixtures/programs.jl:54-55) */
+enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_FOLD_SQUARE, TH_FOLD_LINEAR };
 
-/* What a Stat term reads of a fold: the value (SUM, PROD, MAX, MIN); the
- * statistic (EXP: m, SQUARE: the mean); the sum (EXP: the weighted sum of
- * exponentials, SQUARE: the squared deviations); or, for EXP, the log-sum-exp
- * lse_shift(m) + log(sum) (LOGSUMEXP, folds.jl:263). */
+/* What a Stat term reads of a fold: the value (SUM, PROD, MAX, MIN; LINEAR:
+ * h); the statistic (EXP: m, SQUARE: the mean, LINEAR: the product of the
+ * a's); the sum (EXP: the weighted sum of exponentials, SQUARE: the squared
+ * deviations); or, for EXP, the log-sum-exp lse_shift(m) + log(sum)
+ * (LOGSUMEXP, folds.jl:263). */
 enum { TH_OBSERVE_VALUE = 0, TH_OBSERVE_STATISTIC = 1, TH_OBSERVE_SUM = 2, TH_OBSERVE_LOGSUMEXP = 3 };
 
 /* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions. */
@@ -285,10 +296,17 @@ typedef struct th_term {
 
 typedef struct th_fold {
   int32_t kind;     /* TH_FOLD_* */
-  int32_t phase;    /* >= 1; a fold's terms read statistics of earlier phases only */
+  int32_t phase;    /* >= 1; a fold's terms read statistics of earlier phases only
+                       (in a scan group: of folds earlier in (phase, index) order) */
   int32_t body;     /* term */
-  int32_t weight;   /* term, or -1; TH_FOLD_EXP only */
+  int32_t weight;   /* term, or -1; TH_FOLD_EXP and TH_FOLD_LINEAR (required) only */
+  int32_t scan;     /* scan groups: TH_SCAN_*; 0 elsewhere */
+  int32_t reserved;
 } th_fold;
+
+/* A scan group's fold: its result after the sweep (a plain fold), or at each
+ * position including (inclusive) or before (exclusive) the position's element. */
+enum { TH_SCAN_NONE = 0, TH_SCAN_INCLUSIVE = 1, TH_SCAN_EXCLUSIVE = 2 };
 
 /* Output: value[index(i)] = term, rounded to the value's type.  `full` outputs
  * are written at every position of the domain; the others once per item of a
@@ -306,9 +324,9 @@ typedef struct th_floor_desc {
   int32_t kind;                       /* TH_GROUP_* */
   int32_t rank;                       /* 1..TH_FLOOR_RANK */
   int64_t extents[TH_FLOOR_RANK];
-  uint32_t reduced;                   /* bit k: axis k is folded */
+  uint32_t reduced;                   /* bit k: axis k is folded (scan groups: scanned) */
   int32_t n_values, n_terms, n_folds, n_outputs;
-  int32_t reserved;
+  int32_t flags;                      /* TH_FLOOR_REVERSE for a scan from the last position */
   const th_floor_value* values;
   const th_term* terms;               /* in order: args refer to earlier terms */
   const th_fold* folds;

@@ -7,10 +7,16 @@ once, in Float64, each fold over the group's folded axes by the fold algebra
 of src/Compiler/IR/folds.jl (a sum, product, maximum or minimum; the
 exponential fold's maximum m and sum of weight * exp(y - lse_shift(m)),
 folds.jl:126-133,160-176,193-194; the square fold's mean and sum of squared
-deviations, folds.jl:135-192), phase after phase, then the outputs: a full
+deviations, folds.jl:135-192; the linear recurrence h = a h' + b, the
+`chain` of test/fixtures/programs.jl:54-55), phase after phase, then the outputs: a full
 output at every position of the domain, the others once per item with the
-folded positions at zero (scalar.jl:232-248).  Written values are rounded
-once to their type (Float32, or bfloat16 to nearest, ties to even).
+folded positions at zero (scalar.jl:232-248).  A scan group steps its
+scanned positions in order (reversed if asked), every item at once: at each
+position the folds take their elements in (phase, definition) order, a
+scan's result read before (exclusive) or after (inclusive) its element, then
+the full outputs (scan_kernel, scalar.jl:350-398; in_sequence, folds.jl:
+372-386).  Written values are rounded once to their type (Float32, or
+bfloat16 to nearest, ties to even).
 
 Parity pinned by (tests/test_oracle_floor.py): each fold kind against the
 sequential restatement in ``oracle.folds`` on the same elements (lift, then
@@ -66,6 +72,18 @@ def fold_reduce(kind: str, y: np.ndarray, g, axes: tuple):
         s = (w * np.exp(y - sh)).sum(axis=axes, keepdims=True)
         with np.errstate(divide="ignore", invalid="ignore"):
             return {"statistic": m, "sum": s, "logsumexp": sh + np.log(s)}
+    if kind == "linear":
+        # In order over the folded positions, first axis fastest: h = a h + b.
+        yy = np.moveaxis(y, axes, tuple(range(len(axes))))
+        gg = np.moveaxis(np.broadcast_to(g, y.shape), axes, tuple(range(len(axes))))
+        cnt = int(np.prod(yy.shape[:len(axes)]))
+        ya = yy.reshape((cnt,) + yy.shape[len(axes):], order="F")
+        ga = gg.reshape((cnt,) + gg.shape[len(axes):], order="F")
+        p, h = np.ones(ya.shape[1:]), np.zeros(ya.shape[1:])
+        for i in range(cnt):
+            p, h = p * ya[i], ya[i] * h + ga[i]
+        shape = tuple(1 if k in axes else y.shape[k] for k in range(y.ndim))
+        return {"value": h.reshape(shape), "statistic": p.reshape(shape)}
     if kind == "square":
         n = np.prod([y.shape[a] for a in axes]) if y.size else 0
         with np.errstate(invalid="ignore"):
@@ -115,6 +133,8 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
         return r
 
     full_at = [idx[k] for k in range(rank)]
+    if spec["kind"] == "scan":
+        return _scan(spec, arrays, out, idx, addr, term, stats, rounded)
     if spec["kind"] == "reduction":
         for phase in sorted({f["phase"] for f in spec["folds"]}):
             memo: dict = {}
@@ -142,3 +162,93 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
         result[n] = bf16_round(a.astype(np.float32)) if dt == "bf16" else a.astype(np.float32)
     return result
 
+
+
+def _observe(kind, st):
+    if kind in ("sum", "prod", "max", "min"):
+        return {"value": st[0]}
+    if kind == "exp":
+        m, s = st
+        sh = np.where(np.isfinite(m), m, 0.0)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            return {"statistic": m, "sum": s, "logsumexp": sh + np.log(s)}
+    if kind == "square":
+        n, mean, q = st
+        return {"statistic": np.where(n > 0, mean, np.nan), "sum": q}
+    return {"value": st[1], "statistic": st[0]}  # linear: (product, h)
+
+
+def _step(kind, st, y, g):
+    if kind == "sum":
+        return (st[0] + y,)
+    if kind == "prod":
+        return (st[0] * y,)
+    if kind == "max":
+        return (np.maximum(st[0], y),)
+    if kind == "min":
+        return (np.minimum(st[0], y),)
+    if kind == "exp":  # combine with lift(y, g), the oracle.folds rebase
+        m, s = st
+        n = np.maximum(m, y)
+        sh = np.where(np.isfinite(n), n, 0.0)
+        with np.errstate(invalid="ignore"):
+            return (n, s * np.exp(m - sh) + g * np.exp(y - sh))
+    if kind == "square":  # Welford
+        n, mean, q = st
+        n1 = n + 1
+        e = y - mean
+        mean1 = mean + e / n1
+        return (n1, mean1, q + e * (y - mean1))
+    p, h = st  # linear
+    return (p * y, y * h + g)
+
+
+_INIT = {"sum": (0.0,), "prod": (1.0,), "max": (-np.inf,), "min": (np.inf,), "exp": (-np.inf, 0.0),
+         "square": (0.0, 0.0, 0.0), "linear": (1.0, 0.0)}
+
+
+def _scan(spec, arrays, out, idx, addr, term, stats, rounded):
+    ext = tuple(spec["extents"])
+    rank = len(ext)
+    swept = tuple(spec["reduced"])
+    kept_shape = tuple(1 if k in swept else ext[k] for k in range(rank))
+    order = sorted(range(len(spec["folds"])), key=lambda f: spec["folds"][f]["phase"])
+    states = {f: tuple(np.full(kept_shape, v) for v in _INIT[spec["folds"][f]["kind"]]) for f in order}
+    positions = list(np.ndindex(*[ext[k] for k in swept][::-1]))  # last axis slowest
+    positions = [tuple(reversed(p)) for p in positions]            # first swept axis fastest
+    if spec.get("reverse"):
+        positions = positions[::-1]
+    for pos in positions:
+        sl = [slice(None)] * rank
+        for k, c in zip(swept, pos):
+            sl[k] = slice(c, c + 1)
+        at = [idx[k][tuple(sl)] for k in range(rank)]
+        memo: dict = {}
+        for f in order:
+            fd = spec["folds"][f]
+            if fd["scan"] == "exclusive":
+                stats[f] = _observe(fd["kind"], states[f])
+                memo.clear()
+            y = np.broadcast_to(term(fd["body"], at, memo), kept_shape)
+            g = None if fd["weight"] < 0 else np.broadcast_to(term(fd["weight"], at, memo), kept_shape)
+            states[f] = _step(fd["kind"], states[f], y, 1.0 if g is None else g)
+            if fd["scan"] == "inclusive":
+                stats[f] = _observe(fd["kind"], states[f])
+                memo.clear()
+        for o in spec["outputs"]:
+            if o["full"]:
+                v = np.broadcast_to(term(o["term"], at, memo), kept_shape)
+                out[o["value"]][addr(o, at).ravel()] = v.ravel()
+    for f in order:
+        if spec["folds"][f]["scan"] is None:
+            stats[f] = _observe(spec["folds"][f]["kind"], states[f])
+    once_at = [idx[k][tuple(slice(0, 1) if j in swept else slice(None) for j in range(rank))] for k in range(rank)]
+    memo = {}
+    for o in spec["outputs"]:
+        if not o["full"]:
+            v = np.broadcast_to(term(o["term"], once_at, memo), once_at[0].shape)
+            out[o["value"]][addr(o, once_at).ravel()] = v.ravel()
+    if not rounded:
+        return out
+    return {n: (bf16_round(a.astype(np.float32)) if spec["values"][n][0] == "bf16" else a.astype(np.float32))
+            for n, a in out.items()}

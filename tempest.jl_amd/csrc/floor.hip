@@ -74,12 +74,15 @@ const char* fn_name(int fn) {
 }
 
 // Components of a fold's state.
-int state_size(int kind) { return kind == TH_FOLD_EXP ? 2 : kind == TH_FOLD_SQUARE ? 3 : 1; }
+int state_size(int kind) {
+  return kind == TH_FOLD_EXP || kind == TH_FOLD_LINEAR ? 2 : kind == TH_FOLD_SQUARE ? 3 : 1;
+}
 
 bool observe_ok(int kind, int obs) {
   switch (kind) {
     case TH_FOLD_EXP: return obs == TH_OBSERVE_STATISTIC || obs == TH_OBSERVE_SUM || obs == TH_OBSERVE_LOGSUMEXP;
     case TH_FOLD_SQUARE: return obs == TH_OBSERVE_STATISTIC || obs == TH_OBSERVE_SUM;
+    case TH_FOLD_LINEAR: return obs == TH_OBSERVE_VALUE || obs == TH_OBSERVE_STATISTIC;
     default: return obs == TH_OBSERVE_VALUE;
   }
 }
@@ -95,7 +98,10 @@ std::string flt(float x) {
 // How a group maps onto the device.
 struct Plan {
   const th_floor_desc* d = nullptr;
-  bool reduction = false;
+  bool reduction = false;        // a reduction or a scan group: items sweep their folded axes
+  bool scan = false;             // a scan group: one thread per item, in order
+  bool reverse = false;
+  std::vector<int> order;        // a scan group's folds in (phase, index) order
   int rank = 1;
   int64_t E[kRank] = {1, 1, 1, 1};
   std::vector<int> kept, swept;  // axes, fastest first
@@ -124,11 +130,14 @@ bool in_box(const th_affine& a, const int64_t* ext, int rank, int64_t length) {
 
 int validate(const th_floor_desc* d) {
   TH_REQUIRE(d != nullptr, "th_build_floor: null description");
-  TH_REQUIRE(d->kind == TH_GROUP_POINTWISE || d->kind == TH_GROUP_REDUCTION, "th_build_floor: unknown group kind");
+  TH_REQUIRE(d->kind == TH_GROUP_POINTWISE || d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN,
+             "th_build_floor: unknown group kind");
+  TH_REQUIRE(d->flags == 0 || (d->kind == TH_GROUP_SCAN && d->flags == TH_FLOOR_REVERSE),
+             "th_build_floor: only a scan group runs in reverse");
   TH_REQUIRE(d->rank >= 1 && d->rank <= kRank, "th_build_floor: rank must be 1..4");
   for (int k = 0; k < d->rank; ++k) TH_REQUIRE(d->extents[k] >= 0, "th_build_floor: negative extent");
   const uint32_t all = (1u << d->rank) - 1;
-  if (d->kind == TH_GROUP_REDUCTION) {
+  if (d->kind != TH_GROUP_POINTWISE) {
     TH_REQUIRE(d->reduced != 0 && (d->reduced & ~all) == 0, "th_build_floor: a reduction folds some of its axes");
     TH_REQUIRE(d->n_folds >= 1 && d->folds, "th_build_floor: a reduction group has folds");
   } else {
@@ -158,7 +167,7 @@ int validate(const th_floor_desc* d) {
       case TH_TERM_INDEX:
         break;
       case TH_TERM_STAT:
-        TH_REQUIRE(d->kind == TH_GROUP_REDUCTION, at + "statistic in a pointwise group");
+        TH_REQUIRE(d->kind != TH_GROUP_POINTWISE, at + "statistic in a pointwise group");
         TH_REQUIRE(m.ref >= 0 && m.ref < d->n_folds, at + "statistic of no fold");
         TH_REQUIRE(observe_ok(d->folds[m.ref].kind, m.observe), at + "the fold has no such observation");
         break;
@@ -176,11 +185,15 @@ int validate(const th_floor_desc* d) {
   for (int f = 0; f < d->n_folds; ++f) {
     const th_fold& x = d->folds[f];
     std::string at = "th_build_floor: fold " + std::to_string(f) + ": ";
-    TH_REQUIRE(x.kind >= TH_FOLD_SUM && x.kind <= TH_FOLD_SQUARE, at + "unknown fold");
+    TH_REQUIRE(x.kind >= TH_FOLD_SUM && x.kind <= TH_FOLD_LINEAR, at + "unknown fold");
     TH_REQUIRE(x.phase >= 1, at + "phases start at 1");
     TH_REQUIRE(x.body >= 0 && x.body < d->n_terms, at + "no body");
-    TH_REQUIRE(x.weight == -1 || (x.kind == TH_FOLD_EXP && x.weight >= 0 && x.weight < d->n_terms),
-               at + "only the exponential fold takes a weight");
+    TH_REQUIRE(x.weight == -1 || ((x.kind == TH_FOLD_EXP || x.kind == TH_FOLD_LINEAR) && x.weight >= 0 &&
+                                  x.weight < d->n_terms),
+               at + "only the exponential and linear folds take a weight");
+    TH_REQUIRE(x.kind != TH_FOLD_LINEAR || x.weight >= 0, at + "the linear fold's weight is its offset b");
+    TH_REQUIRE(x.scan == TH_SCAN_NONE || (d->kind == TH_GROUP_SCAN && x.scan <= TH_SCAN_EXCLUSIVE),
+               at + "only a scan group's folds scan");
   }
   for (int o = 0; o < d->n_outputs; ++o) {
     const th_output& x = d->outputs[o];
@@ -188,7 +201,7 @@ int validate(const th_floor_desc* d) {
     TH_REQUIRE(x.value >= 0 && x.value < d->n_values, at + "no value");
     TH_REQUIRE(x.term >= 0 && x.term < d->n_terms, at + "no term");
     TH_REQUIRE(x.full == 0 || x.full == 1, at + "full is 0 or 1");
-    TH_REQUIRE(x.full == 1 || d->kind == TH_GROUP_REDUCTION, at + "a pointwise group writes every position");
+    TH_REQUIRE(x.full == 1 || d->kind != TH_GROUP_POINTWISE, at + "a pointwise group writes every position");
     int64_t ext[kRank];
     for (int k = 0; k < d->rank; ++k)
       ext[k] = (!x.full && (d->reduced >> k & 1)) ? std::min<int64_t>(d->extents[k], 1) : d->extents[k];
@@ -231,7 +244,9 @@ int64_t nextpow2(int64_t x) {
 int plan(const th_floor_desc* d, Plan& pl) {
   if (int r = validate(d)) return r;
   pl.d = d;
-  pl.reduction = d->kind == TH_GROUP_REDUCTION;
+  pl.reduction = d->kind != TH_GROUP_POINTWISE;
+  pl.scan = d->kind == TH_GROUP_SCAN;
+  pl.reverse = (d->flags & TH_FLOOR_REVERSE) != 0;
   pl.rank = d->rank;
   for (int k = 0; k < d->rank; ++k) pl.E[k] = d->extents[k];
   for (int k = 0; k < d->rank; ++k) ((pl.reduction && (d->reduced >> k & 1)) ? pl.swept : pl.kept).push_back(k);
@@ -253,6 +268,8 @@ int plan(const th_floor_desc* d, Plan& pl) {
       }
     } else if (m.op == TH_TERM_APPLY) {
       for (int j = 0; j < arity(m.fn); ++j) pl.dep[t] |= pl.dep[m.args[j]];
+    } else if (m.op == TH_TERM_STAT && d->kind == TH_GROUP_SCAN) {
+      pl.dep[t] = d->folds[m.ref].scan != TH_SCAN_NONE;  // a scan's result moves along the sweep
     }
   }
   pl.read.assign(d->n_values, 0);
@@ -261,7 +278,39 @@ int plan(const th_floor_desc* d, Plan& pl) {
     if (d->terms[t].op == TH_TERM_LOAD) pl.read[d->terms[t].ref] = 1;
   for (int o = 0; o < d->n_outputs; ++o) pl.written[d->outputs[o].value] = 1;
 
-  if (pl.reduction) {
+  if (pl.scan) {
+    // Folds in (phase, index) order; a fold reads only the folds before it.
+    for (int f = 0; f < d->n_folds; ++f) pl.order.push_back(f);
+    std::stable_sort(pl.order.begin(), pl.order.end(),
+                     [&](int a, int b) { return d->folds[a].phase < d->folds[b].phase; });
+    std::vector<int> rank_of(d->n_folds);
+    for (size_t j = 0; j < pl.order.size(); ++j) rank_of[pl.order[j]] = (int)j;
+    for (int f = 0; f < d->n_folds; ++f) {
+      std::vector<int> roots{d->folds[f].body};
+      if (d->folds[f].weight >= 0) roots.push_back(d->folds[f].weight);
+      std::vector<char> r = reach(d, roots);
+      for (int t = 0; t < nt; ++t)
+        if (r[t] && d->terms[t].op == TH_TERM_STAT) {
+          const int g = d->terms[t].ref;
+          TH_REQUIRE(rank_of[g] < rank_of[f], "th_build_floor: fold " + std::to_string(f) +
+                                                  " reads a fold that takes its element after it");
+          TH_REQUIRE(d->folds[g].scan != TH_SCAN_NONE, "th_build_floor: fold " + std::to_string(f) +
+                                                           " reads a plain fold's result inside the sweep");
+        }
+    }
+    for (int o = 0; o < d->n_outputs; ++o) {
+      std::vector<char> r = reach(d, {d->outputs[o].term});
+      for (int t = 0; t < nt; ++t)
+        if (r[t] && d->terms[t].op == TH_TERM_STAT)
+          TH_REQUIRE(d->outputs[o].full == 0 || d->folds[d->terms[t].ref].scan != TH_SCAN_NONE,
+                     "th_build_floor: output " + std::to_string(o) + " reads a plain fold's result at a position");
+    }
+    // One thread per item, items side by side, each sweeping in order.
+    pl.rows = false;
+    pl.S = 256;
+    pl.L = pl.P = pl.W = 1;
+    pl.qn = pl.count;
+  } else if (pl.reduction) {
     for (int f = 0; f < d->n_folds; ++f) pl.phases.push_back(d->folds[f].phase);
     std::sort(pl.phases.begin(), pl.phases.end());
     pl.phases.erase(std::unique(pl.phases.begin(), pl.phases.end()), pl.phases.end());
@@ -432,6 +481,9 @@ __device__ __forceinline__ void th_exp_comb(float& m, float& s, float m2, float 
   s = s * th_exp(m - h) + s2 * th_exp(m2 - h);
   m = n;
 }
+// The linear recurrence h = a h' + b: state (product of the a's, h).
+__device__ __forceinline__ void th_lin_step(float& p, float& h, float a, float b) { p *= a; h = fmaf(a, h, b); }
+__device__ __forceinline__ void th_lin_comb(float& p, float& h, float p2, float h2) { h = fmaf(p2, h, h2); p *= p2; }
 // Relative{Square}: state (n, mean, squared deviations), Welford's step and
 // Chan's combination.
 __device__ __forceinline__ void th_sq_step(float& n, float& a, float& q, float y) {
@@ -498,6 +550,7 @@ __device__ __forceinline__ void th_exp_step(th_v& m, th_v& s, th_v y, th_v g) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) { float a = m[j], b = s[j]; th_exp_step(a, b, y[j], g[j]); m[j] = a; s[j] = b; }
 }
+__device__ __forceinline__ void th_lin_step(th_v& p, th_v& h, th_v a, th_v b) { p *= a; h = a * h + b; }
 __device__ __forceinline__ void th_sq_step(th_v& n, th_v& a, th_v& q, th_v y) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) { float x = n[j], b = a[j], c = q[j]; th_sq_step(x, b, c, y[j]); n[j] = x; a[j] = b; q[j] = c; }
@@ -525,6 +578,9 @@ class Writer {
     if (!pl_.reduction) {
       stages.push_back({base + "_0", -1});
       pointwise(stages.back().name);
+    } else if (pl_.scan) {
+      stages.push_back({base + "_0", -1});
+      scan(stages.back().name);
     } else if (pl_.P == 1) {
       stages.push_back({base + "_0", -1});
       reduction(stages.back().name, -1);
@@ -543,6 +599,9 @@ class Writer {
     std::ostringstream s;
     if (!pl_.reduction) {
       s << "pointwise, " << pl_.items << " positions, width " << pl_.W;
+    } else if (pl_.scan) {
+      s << "scan, " << pl_.items << " items of " << pl_.count << " positions, a thread per item"
+        << (pl_.reverse ? ", reversed" : "");
     } else {
       s << (pl_.rows ? "rows" : "columns") << ", " << pl_.items << " items of " << pl_.count
         << " positions, side " << pl_.S << ", lanes " << pl_.L << ", parts " << pl_.P << ", width " << pl_.W
@@ -702,6 +761,7 @@ class Writer {
       case TH_FOLD_MAX: return "(-__builtin_inff())";
       case TH_FOLD_MIN: return "__builtin_inff()";
       case TH_FOLD_EXP: return j == 0 ? "(-__builtin_inff())" : "0.0f";
+      case TH_FOLD_LINEAR: return j == 0 ? "1.0f" : "0.0f";
       default: return "0.0f";
     }
   }
@@ -714,6 +774,7 @@ class Writer {
       case TH_FOLD_MAX: return a[0] + " = fmaxf(" + a[0] + ", " + b[0] + ");";
       case TH_FOLD_MIN: return a[0] + " = fminf(" + a[0] + ", " + b[0] + ");";
       case TH_FOLD_EXP: return "th_exp_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
+      case TH_FOLD_LINEAR: return "th_lin_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
       default: return "th_sq_comb(" + a[0] + ", " + a[1] + ", " + a[2] + ", " + b[0] + ", " + b[1] + ", " + b[2] + ");";
     }
   }
@@ -798,6 +859,8 @@ class Writer {
         e = obs == TH_OBSERVE_STATISTIC ? c[0] : obs == TH_OBSERVE_SUM ? c[1] : "th_shift(" + c[0] + ") + logf(" + c[1] + ")";
       } else if (kind == TH_FOLD_SQUARE) {
         e = obs == TH_OBSERVE_STATISTIC ? "(" + c[0] + " > 0.0f ? " + c[1] + " : __builtin_nanf(\"\"))" : c[2];
+      } else if (kind == TH_FOLD_LINEAR) {
+        e = obs == TH_OBSERVE_STATISTIC ? c[0] : c[1];
       } else {
         e = c[0];
       }
@@ -850,6 +913,10 @@ class Writer {
             o << b << "th_exp_step(" << s << "_0, " << s << "_1, " << y << ", " << g << ");\n";
             break;
           }
+          case TH_FOLD_LINEAR:
+            o << b << "th_lin_step(" << s << "_0, " << s << "_1, " << y << ", "
+              << name_of(x.weight, names, hoisted, pl_.W > 1) << ");\n";
+            break;
           default:
             o << b << "th_sq_step(" << s << "_0, " << s << "_1, " << s << "_2, " << y << ");\n";
         }
@@ -1009,6 +1076,71 @@ class Writer {
         }
       });
       o << "  }\n";
+    }
+    o << "}\n";
+  }
+
+  // One thread per item sweeps the scanned positions in order; at each, the
+  // folds take their elements in (phase, index) order (an exclusive scan's
+  // result read before its element, an inclusive one's after), then the
+  // full outputs; the plain folds' results and the once outputs after.
+  void scan(const std::string& name) {
+    std::ostringstream& o = o_;
+    header(name);
+    o << "  const long item = (long)blockIdx.x * " << pl_.S << " + threadIdx.x;\n";
+    o << "  if (item >= " << pl_.items << "L) return;\n";
+    delinearize("  ", "item", pl_.kept);
+    for (int f = 0; f < d_->n_folds; ++f) {
+      for (int obs = 0; obs <= TH_OBSERVE_LOGSUMEXP; ++obs)
+        if (observe_ok(d_->folds[f].kind, obs)) o << "  float " << stat_name(f, obs) << " = 0.0f; (void)" << stat_name(f, obs) << ";\n";
+      for (int c = 0; c < state_size(d_->folds[f].kind); ++c)
+        o << "  float s" << f << "_" << c << " = " << identity(d_->folds[f].kind, c) << ";\n";
+    }
+    auto comps_of = [&](int f) { return comps("s" + std::to_string(f), state_size(d_->folds[f].kind)); };
+    o << "  for (long q = 0; q < " << pl_.count << "L; ++q) {\n";
+    o << "    const long pos = " << (pl_.reverse ? std::to_string(pl_.count - 1) + "L - q" : std::string("q")) << ";\n";
+    delinearize("    ", "pos", pl_.swept);
+    std::map<int, std::string> names;
+    for (int f : pl_.order) {
+      const th_fold& x = d_->folds[f];
+      if (x.scan == TH_SCAN_EXCLUSIVE) observe("    ", f, comps_of(f));
+      std::vector<int> roots{x.body};
+      if (x.weight >= 0) roots.push_back(x.weight);
+      emit("    ", reach(d_, roots), false, false, names, nullptr);
+      const std::string y = names.at(x.body), sf = "s" + std::to_string(f);
+      switch (x.kind) {
+        case TH_FOLD_SUM: o << "    " << sf << "_0 += " << y << ";\n"; break;
+        case TH_FOLD_PROD: o << "    " << sf << "_0 *= " << y << ";\n"; break;
+        case TH_FOLD_MAX: o << "    " << sf << "_0 = th_max(" << sf << "_0, " << y << ");\n"; break;
+        case TH_FOLD_MIN: o << "    " << sf << "_0 = th_min(" << sf << "_0, " << y << ");\n"; break;
+        case TH_FOLD_EXP:
+          o << "    th_exp_step(" << sf << "_0, " << sf << "_1, " << y << ", "
+            << (x.weight >= 0 ? names.at(x.weight) : std::string("1.0f")) << ");\n";
+          break;
+        case TH_FOLD_LINEAR:
+          o << "    th_lin_step(" << sf << "_0, " << sf << "_1, " << y << ", " << names.at(x.weight) << ");\n";
+          break;
+        default:
+          o << "    th_sq_step(" << sf << "_0, " << sf << "_1, " << sf << "_2, " << y << ");\n";
+      }
+      if (x.scan == TH_SCAN_INCLUSIVE) observe("    ", f, comps_of(f));
+    }
+    std::vector<int> full, once;
+    for (int x = 0; x < d_->n_outputs; ++x) (d_->outputs[x].full ? full : once).push_back(x);
+    std::vector<int> roots;
+    for (int x : full) roots.push_back(d_->outputs[x].term);
+    emit("    ", reach(d_, roots), false, false, names, nullptr);
+    for (int x : full) store("    ", d_->outputs[x], names.at(d_->outputs[x].term), false);
+    o << "  }\n";
+    for (int f = 0; f < d_->n_folds; ++f)
+      if (d_->folds[f].scan == TH_SCAN_NONE) observe("  ", f, comps_of(f));
+    if (!once.empty()) {
+      for (int k : pl_.swept) o << "  i" << k << " = 0;\n";
+      std::vector<int> r2;
+      for (int x : once) r2.push_back(d_->outputs[x].term);
+      std::map<int, std::string> names2;
+      emit("  ", reach(d_, r2), false, false, names2, nullptr);
+      for (int x : once) store("  ", d_->outputs[x], names2.at(d_->outputs[x].term), false);
     }
     o << "}\n";
   }
@@ -1196,7 +1328,7 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
     mod = it->second.get();
   }
   const th_floor_desc* d = desc;
-  const int nws = pl.reduction && pl.P > 1 ? d->n_folds : 0;
+  const int nws = pl.reduction && !pl.scan && pl.P > 1 ? d->n_folds : 0;
   struct Args {
     void* p[kMaxArgs];
   } args{};

@@ -230,11 +230,11 @@ end
 struct FloorValue; dtype::Int32; reserved::Int32; length::Int64; ptr::Ptr{Cvoid}; end
 struct CAffine; constant::Int64; coeff::NTuple{4, Int64}; end
 struct CTerm; op::Int32; fn::Int32; args::NTuple{3, Int32}; ref::Int32; observe::Int32; lit::Float32; index::CAffine; end
-struct CFold; kind::Int32; phase::Int32; body::Int32; weight::Int32; end
+struct CFold; kind::Int32; phase::Int32; body::Int32; weight::Int32; scan::Int32; reserved::Int32; end
 struct COutput; value::Int32; term::Int32; full::Int32; reserved::Int32; index::CAffine; end
 struct FloorDesc
     kind::Int32; rank::Int32; extents::NTuple{4, Int64}; reduced::UInt32
-    n_values::Int32; n_terms::Int32; n_folds::Int32; n_outputs::Int32; reserved::Int32
+    n_values::Int32; n_terms::Int32; n_folds::Int32; n_outputs::Int32; flags::Int32
     values::Ptr{FloorValue}; terms::Ptr{CTerm}; folds::Ptr{CFold}; outputs::Ptr{COutput}
 end
 
@@ -295,7 +295,10 @@ function floor_descriptor(graph, g, slots, buffers)
         push!(terms, ct)
         index[t] = Int32(length(terms) - 1)
     end
-    cfolds = [CFold(floor_fold(graph.values[r].definition.fold)[1], g.phase[r], add!(g.terms[r]), -1) for r in folds]
+    # A scan group's scans (Scan definitions, inclusive or exclusive) and its plain folds.
+    scan_of(d) = d isa C.IR.Scan ? (d.exclusive ? 2 : 1) : 0
+    cfolds = [CFold(floor_fold(graph.values[r].definition.fold)[1], g.phase[r], add!(g.terms[r]), -1,
+                    scan_of(graph.values[r].definition), 0) for r in folds]
     outs = [COutput(findfirst(==(m), slots) - 1, add!(g.terms[m]), graph.values[m].dims == g.domain, 0,
                     caffine(C.address(graph.values[m], C.identity_index(g.domain), C.Domain(g.domain)), nothing))
             for m in g.outputs]
@@ -303,15 +306,17 @@ function floor_descriptor(graph, g, slots, buffers)
                        address(buffers[i])) for (i, v) in enumerate(slots)]
     ext = ntuple(k -> k <= length(g.domain) ? Int64(g.domain[k]) : 1, 4)
     reduced = UInt32(sum((1 << (k - 1) for k in C.primary_axes(graph, g)); init = 0))
-    (vals, terms, cfolds, outs, ext, reduced, isempty(folds) ? 0 : 1)
+    kind = isempty(folds) ? 0 : g.kind isa C.ScanKind ? 2 : 1
+    (vals, terms, cfolds, outs, ext, reduced, kind)
 end
 
 function build_floor(target::HIPTarget, p, g, buffers)
     slots = Tempest.Compiler.kernel_slots(p, g, Tempest.Compiler.floor_stored(p, g))
     vals, terms, folds, outs, ext, reduced, kind = floor_descriptor(p.graph, g, slots, [buffers[v] for v in slots])
     GC.@preserve vals terms folds outs begin
+        reverse = kind == 2 && p.graph.values[first(g.reductions)].definition.reverse ? 1 : 0
         d = Ref(FloorDesc(kind, length(g.domain), ext, reduced,
-                          length(vals), length(terms), length(folds), length(outs), 0,
+                          length(vals), length(terms), length(folds), length(outs), reverse,
                           pointer(vals), pointer(terms), pointer(folds), pointer(outs)))
         out = Ref{Ptr{Cvoid}}()
         check(ccall((:th_build_floor, LIB), Cint, (Ptr{FloorDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_floor")

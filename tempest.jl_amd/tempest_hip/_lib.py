@@ -78,7 +78,8 @@ class TermStruct(ctypes.Structure):
 
 
 class FoldStruct(ctypes.Structure):
-    _fields_ = [("kind", c_i32), ("phase", c_i32), ("body", c_i32), ("weight", c_i32)]
+    _fields_ = [("kind", c_i32), ("phase", c_i32), ("body", c_i32), ("weight", c_i32), ("scan", c_i32),
+                ("reserved", c_i32)]
 
 
 class OutputStruct(ctypes.Structure):
@@ -89,7 +90,7 @@ class OutputStruct(ctypes.Structure):
 class FloorDesc(ctypes.Structure):
     _fields_ = [("kind", c_i32), ("rank", c_i32), ("extents", c_i64 * FLOOR_RANK),
                 ("reduced", ctypes.c_uint32), ("n_values", c_i32), ("n_terms", c_i32),
-                ("n_folds", c_i32), ("n_outputs", c_i32), ("reserved", c_i32),
+                ("n_folds", c_i32), ("n_outputs", c_i32), ("flags", c_i32),
                 ("values", ctypes.POINTER(FloorValue)), ("terms", ctypes.POINTER(TermStruct)),
                 ("folds", ctypes.POINTER(FoldStruct)), ("outputs", ctypes.POINTER(OutputStruct))]
 

@@ -33,7 +33,7 @@ from .runtime import Group
 
 RANK = _lib.FLOOR_RANK
 
-GROUP = {"pointwise": 0, "reduction": 1}
+GROUP = {"pointwise": 0, "reduction": 1, "scan": 2}
 TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4}
 FN = {name: k for k, name in enumerate([
     "+", "-", "*", "/", "neg", "abs", "abs2", "sqrt", "exp", "log", "tanh", "sin", "cos", "log1p", "expm1", "^",
@@ -41,7 +41,8 @@ FN = {name: k for k, name in enumerate([
     "inv"])}
 ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", ">", ">=", "==", "!=") else
                 3 if name in ("ifelse", "clamp", "fma") else 1) for name in FN}
-FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5}
+FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6}
+SCAN = {None: 0, "inclusive": 1, "exclusive": 2}
 OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}
 DTYPE = {"f32": 0, "bf16": 1}
 
@@ -99,6 +100,11 @@ class Fold:
     def logsumexp(self) -> Term:
         return self._stat("logsumexp")
 
+    @property
+    def product(self) -> Term:
+        """The linear fold's product of its factors a."""
+        return self._stat("statistic")
+
 
 def _affine(coeffs: Sequence[int] | None, constant: int, rank: int) -> tuple:
     c = list(coeffs or ())
@@ -113,8 +119,9 @@ class FloorGroup:
 
     kind: str
     extents: tuple
-    reduced: tuple = ()
+    reduced: tuple = ()                             # folded axes (a scan group: scanned)
     name: str = "floor group"
+    reverse: bool = False                           # a scan group from its last position
     values: dict = field(default_factory=dict)      # name -> (dtype, length), in value order
     terms: list = field(default_factory=list)       # (op, fn, args, ref, observe, lit, affine)
     folds: list = field(default_factory=list)       # (kind, phase, body, weight)
@@ -168,14 +175,21 @@ class FloorGroup:
         ts = [self._as_term(a) for a in args]
         return self._term("apply", fn=FN[fn], args=[t.index for t in ts])
 
-    def fold(self, kind: str, body, weight=None, phase: int = 1) -> Fold:
-        if self.kind != "reduction":
+    def fold(self, kind: str, body, weight=None, phase: int = 1, scan: str | None = None) -> Fold:
+        """A fold of ``body`` over the group's folded axes.  ``weight``: the
+        exponential fold's weight, the linear fold's offset b (h = body h' + b).
+        In a scan group, ``scan`` = "inclusive" or "exclusive" makes its result
+        the running one at each position; folds take their elements in
+        (phase, order of definition) order."""
+        if self.kind == "pointwise":
             raise ValueError("only a reduction group folds")
         if kind not in FOLD:
             raise ValueError(f"unknown fold {kind!r}")
+        if scan not in SCAN or (scan and self.kind != "scan"):
+            raise ValueError("only a scan group's folds scan (inclusive or exclusive)")
         b = self._as_term(body).index
         w = -1 if weight is None else self._as_term(weight).index
-        self.folds.append((FOLD[kind], int(phase), b, w))
+        self.folds.append((FOLD[kind], int(phase), b, w, SCAN[scan]))
         return Fold(self, len(self.folds) - 1, kind)
 
     def output(self, name: str, term, coeffs: Sequence[int] | None = None, constant: int = 0,
@@ -199,8 +213,9 @@ class FloorGroup:
             t.index.constant = c0
             t.index.coeff[:] = list(cs)
         folds = (FoldStruct * max(nf, 1))()
-        for k, (kind, phase, body, weight) in enumerate(self.folds):
+        for k, (kind, phase, body, weight, scan) in enumerate(self.folds):
             folds[k].kind, folds[k].phase, folds[k].body, folds[k].weight = kind, phase, body, weight
+            folds[k].scan = scan
         outs = (OutputStruct * max(no, 1))()
         for k, (v, term, full, (c0, cs)) in enumerate(self.outputs):
             outs[k].value, outs[k].term, outs[k].full = v, term, full
@@ -211,6 +226,7 @@ class FloorGroup:
         d.extents[:] = list(self.extents) + [1] * (RANK - len(self.extents))
         d.reduced = sum(1 << k for k in self.reduced)
         d.n_values, d.n_terms, d.n_folds, d.n_outputs = nv, nt, nf, no
+        d.flags = 1 if self.reverse else 0
         d.values, d.terms, d.folds, d.outputs = values, terms, folds, outs
         return d, (values, terms, folds, outs)
 
@@ -258,14 +274,16 @@ class FloorGroup:
         inv_fold = {v: k for k, v in FOLD.items()}
         inv_obs = {v: k for k, v in OBSERVE.items()}
         inv_term = {v: k for k, v in TERM.items()}
+        inv_scan = {v: k for k, v in SCAN.items()}
         return {
-            "kind": self.kind, "extents": self.extents, "reduced": self.reduced,
+            "kind": self.kind, "extents": self.extents, "reduced": self.reduced, "reverse": self.reverse,
             "values": dict(self.values),
             "terms": [{"op": inv_term[op], "fn": inv_fn.get(fn) if op == TERM["apply"] else None,
                        "args": list(args[:ARITY[inv_fn[fn]]]) if op == TERM["apply"] else [],
                        "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1])}
                       for op, fn, args, ref, obs, lit, aff in self.terms],
-            "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w} for k, p, b, w in self.folds],
+            "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w, "scan": inv_scan[sc]}
+                      for k, p, b, w, sc in self.folds],
             "outputs": [{"value": list(self.values)[v], "term": t, "full": bool(f), "constant": aff[0],
                          "coeffs": list(aff[1])} for v, t, f, aff in self.outputs],
         }

@@ -408,10 +408,158 @@ def kat_sum_abs2():
                   {"x": np.array([1.0, 2.0, 3.0, 4.0])}, lambda v: {"loss": [30.0]})
 
 
+# ---- scan groups (scan_kernel, codegen/scalar.jl:350-398) ----------------------------
+
+def cumulative_sums():
+    """sum(cumsum(x; dims = 1) .* data(8, 6; scale = 0.3)) + sum(abs2, cumsum(x[:, 2]))."""
+    x, w = data(8, 6), data(8, 6, scale=0.3)
+    ga = FloorGroup("scan", (8, 6), reduced=(0,), name="cumsum(x; dims = 1) .* w, summed per column")
+    ga.value("x", "f32", 48)
+    ga.value("w", "f32", 48)
+    ga.value("r", "f32", 6)
+    c = ga.fold("sum", ga.load("x", (1, 8)), scan="inclusive")
+    ga.output("r", ga.fold("sum", c.value * ga.load("w", (1, 8)), phase=2).value, (0, 1), full=False)
+    gb = FloorGroup("scan", (8,), reduced=(0,), name="sum(abs2, cumsum(x[:, 2]))")
+    gb.value("x", "f32", 48)
+    gb.value("part", "f32", 1)
+    c2 = gb.fold("sum", gb.load("x", (1,), constant=8), scan="inclusive")
+    gb.output("part", gb.fold("sum", gb.apply("abs2", c2.value), phase=2).value, full=False)
+    gc = _full_sum("r", 6, extra="part")
+
+    def closed(v):
+        X, W = v["x"].reshape(8, 6, order="F"), v["w"].reshape(8, 6, order="F")
+        return {"loss": [np.sum(np.cumsum(X, axis=0) * W) + np.sum(np.cumsum(X[:, 1]) ** 2)]}
+    return Case("cumulative sums", [ga, gb, gc], {"x": F(x), "w": F(w)}, {"r": 6, "part": 1, "loss": 1},
+                ["loss"], closed)
+
+
+def cumulative_products_through_a_zero():
+    """sum(cumprod(x; dims = 2) .* data(5, 4)), x with a zero at (2, 3)."""
+    x = data(5, 4, scale=0.4)
+    x[1, 2] = 0.0
+    w = data(5, 4)
+    g = FloorGroup("scan", (5, 4), reduced=(1,), name="cumprod along rows")
+    g.value("x", "f32", 20)
+    g.value("w", "f32", 20)
+    g.value("r", "f32", 5)
+    c = g.fold("prod", g.load("x", (1, 5)), scan="inclusive")
+    g.output("r", g.fold("sum", c.value * g.load("w", (1, 5)), phase=2).value, (1, 0), full=False)
+
+    def closed(v):
+        X, W = v["x"].reshape(5, 4, order="F"), v["w"].reshape(5, 4, order="F")
+        r = np.sum(np.cumprod(X, axis=1) * W, axis=1)
+        return {"r": r, "loss": [r.sum()]}
+    return Case("cumulative products through a zero", [g, _full_sum("r", 5)], {"x": F(x), "w": F(w)},
+                {"r": 5, "loss": 1}, ["r", "loss"], closed)
+
+
+def running_maxima_and_minima():
+    """sum(accumulate(max, x; dims = 1) .* w) + sum of the running minimum in linear order."""
+    x, w = data(8, 6, scale=0.7), data(8, 6, scale=0.3)
+    ga = FloorGroup("scan", (8, 6), reduced=(0,), name="running maximum down columns")
+    ga.value("x", "f32", 48)
+    ga.value("w", "f32", 48)
+    ga.value("r", "f32", 6)
+    m = ga.fold("max", ga.load("x", (1, 8)), scan="inclusive")
+    ga.output("r", ga.fold("sum", m.value * ga.load("w", (1, 8)), phase=2).value, (0, 1), full=False)
+    gb = FloorGroup("scan", (8, 6), reduced=(0, 1), name="running minimum in linear order")
+    gb.value("x", "f32", 48)
+    gb.value("part", "f32", 1)
+    mn = gb.fold("min", gb.load("x", (1, 8)), scan="inclusive")
+    gb.output("part", gb.fold("sum", mn.value, phase=2).value, full=False)
+
+    def closed(v):
+        X, W = v["x"].reshape(8, 6, order="F"), v["w"].reshape(8, 6, order="F")
+        return {"loss": [np.sum(np.maximum.accumulate(X, axis=0) * W) + np.sum(np.minimum.accumulate(v["x"]))]}
+    return Case("running maxima and minima", [ga, gb, _full_sum("r", 6, extra="part")], {"x": F(x), "w": F(w)},
+                {"r": 6, "part": 1, "loss": 1}, ["loss"], closed)
+
+
+def linear_recurrence():
+    """sum(abs2, recurrence(a, b)): h = a h' + b from 0 (programs.jl:54-55, 86-88)."""
+    a, b = 0.9 + 0.1 * data(30, scale=0.3), data(30, scale=0.7)
+    g = FloorGroup("scan", (30,), reduced=(0,), name="h = a h' + b")
+    g.value("a", "f32", 30)
+    g.value("b", "f32", 30)
+    g.value("h", "f32", 30)
+    g.value("loss", "f32", 1)
+    h = g.fold("linear", g.load("a", (1,)), weight=g.load("b", (1,)), scan="inclusive")
+    g.output("h", h.value, (1,))
+    g.output("loss", g.fold("sum", g.apply("abs2", h.value), phase=2).value, full=False)
+
+    def closed(v):
+        hs, hh = [], 0.0
+        for ai, bi in zip(v["a"], v["b"]):
+            hh = ai * hh + bi
+            hs.append(hh)
+        hs = np.array(hs)
+        return {"h": hs, "loss": [np.sum(hs ** 2)]}
+    return Case("a linear recurrence", [g], {"a": F(a), "b": F(b)}, {"h": 30, "loss": 1}, ["h", "loss"], closed)
+
+
+def running_average():
+    """sum(abs2, accumulate((s, e) -> s / 2 + e, x; dims = 2, init = 1)): h = h'/2 + e
+    from 1, i.e. the linear fold's value plus its product (h from 0, plus 1 times
+    the product of the halves)."""
+    x = data(8, 6)
+    g = FloorGroup("scan", (8, 6), reduced=(1,), name="running average along rows")
+    g.value("x", "f32", 48)
+    g.value("r", "f32", 8)
+    h = g.fold("linear", g.lit(0.5), weight=g.load("x", (1, 8)), scan="inclusive")
+    g.output("r", g.fold("sum", g.apply("abs2", h.value + h.product), phase=2).value, (1, 0), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        hh = np.ones(8)
+        tot = np.zeros(8)
+        for j in range(6):
+            hh = hh / 2 + X[:, j]
+            tot += hh ** 2
+        return {"r": tot, "loss": [tot.sum()]}
+    return Case("a running average", [g, _full_sum("r", 8)], {"x": F(x)}, {"r": 8, "loss": 1}, ["r", "loss"], closed)
+
+
+def reverse_exclusive_sums(n=9, m=5):
+    """y[i, j] = sum of x[i', j] over i' > i: an exclusive scan from the last position."""
+    x = data(n, m)
+    g = FloorGroup("scan", (n, m), reduced=(0,), reverse=True, name="suffix sums, exclusive")
+    g.value("x", "f32", n * m)
+    g.value("y", "f32", n * m)
+    c = g.fold("sum", g.load("x", (1, n)), scan="exclusive")
+    g.output("y", c.value, (1, n))
+
+    def closed(v):
+        X = v["x"].reshape(n, m, order="F")
+        return {"y": (np.cumsum(X[::-1], axis=0)[::-1] - X).ravel(order="F")}
+    return Case("reverse exclusive sums", [g], {"x": F(x)}, {"y": n * m}, ["y"], closed)
+
+
+def running_logsumexp_and_mean(n=12, m=4):
+    """Running log-sum-exp (the exponential fold as a scan) and running mean
+    (the square fold as a scan) down each column."""
+    x = data(n, m) * 3
+    g = FloorGroup("scan", (n, m), reduced=(0,), name="running logsumexp and mean")
+    g.value("x", "f32", n * m)
+    g.value("lse", "f32", n * m)
+    g.value("mean", "f32", n * m)
+    xx = g.load("x", (1, n))
+    g.output("lse", g.fold("exp", xx, scan="inclusive").logsumexp, (1, n))
+    g.output("mean", g.fold("square", xx, scan="inclusive").statistic, (1, n))
+
+    def closed(v):
+        X = v["x"].reshape(n, m, order="F")
+        lse = np.logaddexp.accumulate(X, axis=0)
+        mean = np.cumsum(X, axis=0) / np.arange(1, n + 1)[:, None]
+        return {"lse": lse.ravel(order="F"), "mean": mean.ravel(order="F")}
+    return Case("running logsumexp and mean", [g], {"x": F(x)}, {"lse": n * m, "mean": n * m}, ["lse", "mean"], closed)
+
+
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
-         map_over_two_arrays, permutation, bias_tanh_bf16, index_scaled, kat_sum_abs2]
+         map_over_two_arrays, permutation, bias_tanh_bf16, index_scaled, kat_sum_abs2,
+         cumulative_sums, cumulative_products_through_a_zero, running_maxima_and_minima, linear_recurrence,
+         running_average, reverse_exclusive_sums, running_logsumexp_and_mean]
 
 
 def run_oracle(case: Case) -> dict:

@@ -85,10 +85,11 @@ def test_floor_structures_match_the_header(tmp_path):
     members = {"th_affine": (L.Affine, ["constant", "coeff"]),
                "th_floor_value": (L.FloorValue, ["dtype", "length", "ptr"]),
                "th_term": (L.TermStruct, ["op", "fn", "args", "ref", "observe", "lit", "index"]),
-               "th_fold": (L.FoldStruct, ["kind", "phase", "body", "weight"]),
+               "th_fold": (L.FoldStruct, ["kind", "phase", "body", "weight", "scan"]),
                "th_output": (L.OutputStruct, ["value", "term", "full", "index"]),
                "th_floor_desc": (L.FloorDesc, ["kind", "rank", "extents", "reduced", "n_values", "n_terms",
-                                               "n_folds", "n_outputs", "values", "terms", "folds", "outputs"])}
+                                               "n_folds", "n_outputs", "flags", "values", "terms", "folds",
+                                               "outputs"])}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT}/include/tempest_hip.h"', 'int main(void) {']
     for s, (_, ms) in members.items():
         lines.append(f'  printf("{s} %zu\\n", sizeof({s}));')

@@ -189,3 +189,43 @@ def test_config2_full_size_through_the_floor(target):
         assert np.isfinite(loss)
         del c, dx
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("n,m,axis,reverse", [(300, 2000, 1, False), (1000, 64, 0, True), (1, 100000, 1, False)])
+def test_scans_at_size(target, n, m, axis, reverse):
+    """Inclusive sums and a linear recurrence along one axis of an n x m
+    array, a thread per item (items side by side when the scanned axis is the
+    strided one)."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor scan", n, m, axis, reverse)
+    rng = np.random.default_rng(n * 7 + m)
+    x = rng.standard_normal(n * m).astype(np.float32)
+    a = (0.9 + 0.1 * rng.random(n * m)).astype(np.float32)
+    g = FloorGroup("scan", (n, m), reduced=(axis,), reverse=reverse)
+    for k in ("x", "a", "c", "h"):
+        g.value(k, "f32", n * m)
+    xx, aa = g.load("x", (1, n)), g.load("a", (1, n))
+    g.output("c", g.fold("sum", xx, scan="inclusive").value, (1, n))
+    g.output("h", g.fold("linear", aa, weight=xx, scan="inclusive").value, (1, n))
+    ts = {"x": torch.from_numpy(x).cuda(), "a": torch.from_numpy(a).cuda(),
+          "c": torch.zeros(n * m, device="cuda"), "h": torch.zeros(n * m, device="cuda")}
+    g.build({k: v.data_ptr() for k, v in ts.items()})()
+    torch.cuda.synchronize()
+    X = x.astype(np.float64).reshape(m, n).T
+    A = a.astype(np.float64).reshape(m, n).T
+    if reverse:
+        X, A = np.flip(X, axis), np.flip(A, axis)
+    C = np.cumsum(X, axis=axis)
+    H = np.zeros_like(X)
+    hh = np.zeros(X.shape[1 - axis])
+    for i in range(X.shape[axis]):
+        sl = (i, slice(None)) if axis == 0 else (slice(None), i)
+        hh = A[sl] * hh + X[sl]
+        H[sl] = hh
+    if reverse:
+        C, H = np.flip(C, axis), np.flip(H, axis)
+    got_c = ts["c"].cpu().numpy().reshape(m, n).T
+    got_h = ts["h"].cpu().numpy().reshape(m, n).T
+    # Sequential fp32 sums of up to 1e5 terms: error grows like the running magnitude.
+    assert relative(got_c, C) < (1e-5 if X.shape[axis] <= 2000 else 1e-4)
+    assert relative(got_h, H) < TOL
