@@ -271,14 +271,21 @@ enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_
  * (LOGSUMEXP, folds.jl:263). */
 enum { TH_OBSERVE_VALUE = 0, TH_OBSERVE_STATISTIC = 1, TH_OBSERVE_SUM = 2, TH_OBSERVE_LOGSUMEXP = 3 };
 
-/* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions. */
+/* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions,
+ * + gather_coeff * (the value of term `gather`, a load of an integer value)
+ * when gather >= 0 (an Indirect atom, IR/expressions.jl).  A gathered
+ * address is clamped into its value on the device: an index out of range
+ * reads or writes the nearest element instead of faulting. */
 typedef struct th_affine {
   int64_t constant;
   int64_t coeff[TH_FLOOR_RANK];
+  int32_t gather;
+  int32_t reserved;
+  int64_t gather_coeff;
 } th_affine;
 
 typedef struct th_floor_value {
-  int32_t dtype;    /* TH_F32 or TH_BF16 */
+  int32_t dtype;    /* TH_F32 or TH_BF16; TH_I32 or TH_I64 for values only read (indices) */
   int32_t reserved;
   int64_t length;   /* elements */
   void* ptr;
@@ -311,12 +318,15 @@ enum { TH_SCAN_NONE = 0, TH_SCAN_INCLUSIVE = 1, TH_SCAN_EXCLUSIVE = 2 };
 /* Output: value[index(i)] = term, rounded to the value's type.  `full` outputs
  * are written at every position of the domain; the others once per item of a
  * reduction group, with the folded positions at zero (a fold's result stored
- * at its placement, or a statistic of it). */
+ * at its placement, or a statistic of it).  With `accumulate`, value[index(i)]
+ * += term instead, atomically (fp32 values only): a fold by key whose
+ * positions may repeat (accumulate!(::SumFold), ext/CUDAExt.jl:923-924); the
+ * order of the additions, and so the last bits of a sum, may change run to run. */
 typedef struct th_output {
   int32_t value;
   int32_t term;
   int32_t full;
-  int32_t reserved;
+  int32_t accumulate;
   th_affine index;
 } th_output;
 
@@ -359,7 +369,7 @@ int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c,
 
 /* ---- op class (b): bf16 products on the matrix cores --------------------- */
 
-enum { TH_F32 = 0, TH_BF16 = 1 };
+enum { TH_F32 = 0, TH_BF16 = 1, TH_I32 = 2, TH_I64 = 3 };
 
 /* What the product's group fuses after it.  Every epilogue works on the fp32
  * accumulator and rounds once to bf16 where it stores, except where noted.

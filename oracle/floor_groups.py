@@ -102,11 +102,15 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
     vals = list(spec["values"])
     out = {o["value"]: np.array(arrays[o["value"]], dtype=np.float64, copy=True) for o in spec["outputs"]}
 
-    def addr(t, at):
+    def addr(t, at, memo=None, length=None):
         a = np.full(at[0].shape, t["constant"], dtype=np.int64)
         for k in range(rank):
             if t["coeffs"][k]:
                 a = a + t["coeffs"][k] * at[k]
+        if t.get("gather", -1) >= 0:
+            # An Indirect atom: the integer a load reads, held inside the value.
+            a = a + t["gather_coeff"] * np.asarray(term(t["gather"], at, memo), dtype=np.int64)
+            a = np.clip(a, 0, length - 1)
         return a
 
     stats: dict[int, dict] = {}
@@ -117,11 +121,12 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
         t = spec["terms"][i]
         op = t["op"]
         if op == "load":
-            r = np.asarray(arrays[vals[t["ref"]]], dtype=np.float64)[addr(t, at)]
+            src = np.asarray(arrays[vals[t["ref"]]])
+            r = (src if src.dtype.kind == "i" else src.astype(np.float64))[addr(t, at, memo, len(src))]
         elif op == "lit":
             r = np.float64(t["lit"])
         elif op == "index":
-            r = addr(t, at).astype(np.float64)
+            r = addr(t, at, memo).astype(np.float64)
         elif op == "stat":
             r = stats[t["ref"]][t["observe"]]
         else:
@@ -152,8 +157,13 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
     for o in spec["outputs"]:
         at = full_at if o["full"] else once_at
         memo = memo_full if o["full"] else memo_once
-        v = np.broadcast_to(term(o["term"], at, memo), at[0].shape)
-        out[o["value"]][addr(o, at).ravel()] = v.ravel()
+        v = np.broadcast_to(term(o["term"], at, memo), at[0].shape).astype(np.float64)
+        dst = out[o["value"]]
+        where = addr(o, at, memo, len(dst)).ravel()
+        if o.get("accumulate"):
+            np.add.at(dst, where, v.ravel())  # a fold by key: repeated positions add
+        else:
+            dst[where] = v.ravel()
     if not rounded:
         return out
     result = {}
@@ -238,7 +248,7 @@ def _scan(spec, arrays, out, idx, addr, term, stats, rounded):
         for o in spec["outputs"]:
             if o["full"]:
                 v = np.broadcast_to(term(o["term"], at, memo), kept_shape)
-                out[o["value"]][addr(o, at).ravel()] = v.ravel()
+                out[o["value"]][addr(o, at, memo, len(out[o["value"]])).ravel()] = v.ravel()
     for f in order:
         if spec["folds"][f]["scan"] is None:
             stats[f] = _observe(spec["folds"][f]["kind"], states[f])
@@ -247,7 +257,7 @@ def _scan(spec, arrays, out, idx, addr, term, stats, rounded):
     for o in spec["outputs"]:
         if not o["full"]:
             v = np.broadcast_to(term(o["term"], once_at, memo), once_at[0].shape)
-            out[o["value"]][addr(o, once_at).ravel()] = v.ravel()
+            out[o["value"]][addr(o, once_at, memo, len(out[o["value"]])).ravel()] = v.ravel()
     if not rounded:
         return out
     return {n: (bf16_round(a.astype(np.float32)) if spec["values"][n][0] == "bf16" else a.astype(np.float32))

@@ -116,9 +116,14 @@ struct Plan {
   std::vector<char> dep;         // term reads the swept positions
   std::vector<char> vec_ok;      // per value: 16-byte (f32) / 8-byte (bf16) accesses allowed
   std::vector<char> written, read;
+  bool gathers = false;          // some address is data-dependent: width 1, nothing kept in registers
 };
 
+bool is_int(int dtype) { return dtype == TH_I32 || dtype == TH_I64; }
+int esize(int dtype) { return dtype == TH_BF16 ? 2 : dtype == TH_I64 ? 8 : 4; }
+
 bool in_box(const th_affine& a, const int64_t* ext, int rank, int64_t length) {
+  if (a.gather >= 0) return true;  // data-dependent: clamped on the device
   int64_t lo = a.constant, hi = a.constant;
   for (int k = 0; k < rank; ++k) {
     if (ext[k] <= 0) return true;  // an empty domain reads nothing
@@ -150,13 +155,23 @@ int validate(const th_floor_desc* d) {
   TH_REQUIRE(d->n_values + nws <= kMaxArgs, "th_build_floor: more than 64 values and folds");
   for (int v = 0; v < d->n_values; ++v) {
     const th_floor_value& x = d->values[v];
-    TH_REQUIRE(x.dtype == TH_F32 || x.dtype == TH_BF16, "th_build_floor: values are fp32 or bf16");
+    TH_REQUIRE(x.dtype == TH_F32 || x.dtype == TH_BF16 || is_int(x.dtype),
+               "th_build_floor: values are fp32, bf16, or int32 / int64 indices");
     TH_REQUIRE(x.length >= 0, "th_build_floor: negative value length");
     TH_REQUIRE(x.ptr != nullptr, "th_build_floor: null value pointer");
   }
+  // A gathered address adds an earlier term's value: a load of integers.
+  auto gather_ok = [&](const th_affine& a, int before) {
+    if (a.gather < 0) return true;
+    if (a.gather >= before || a.gather >= d->n_terms) return false;
+    const th_term& g = d->terms[a.gather];
+    return g.op == TH_TERM_LOAD && is_int(d->values[g.ref].dtype) && g.ref >= 0 && g.ref < d->n_values;
+  };
   for (int t = 0; t < d->n_terms; ++t) {
     const th_term& m = d->terms[t];
     std::string at = "th_build_floor: term " + std::to_string(t) + ": ";
+    TH_REQUIRE(m.op == TH_TERM_LOAD ? gather_ok(m.index, t) : m.index.gather < 0,
+               at + "a gathered address adds an earlier load of integers");
     switch (m.op) {
       case TH_TERM_LOAD:
         TH_REQUIRE(m.ref >= 0 && m.ref < d->n_values, at + "load of no value");
@@ -206,6 +221,10 @@ int validate(const th_floor_desc* d) {
     for (int k = 0; k < d->rank; ++k)
       ext[k] = (!x.full && (d->reduced >> k & 1)) ? std::min<int64_t>(d->extents[k], 1) : d->extents[k];
     TH_REQUIRE(in_box(x.index, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
+    TH_REQUIRE(gather_ok(x.index, d->n_terms), at + "a gathered address adds a load of integers");
+    TH_REQUIRE(!is_int(d->values[x.value].dtype), at + "integer values are only read");
+    TH_REQUIRE(x.accumulate == 0 || (x.accumulate == 1 && d->values[x.value].dtype == TH_F32),
+               at + "accumulating outputs are fp32");
   }
   return TH_OK;
 }
@@ -215,7 +234,9 @@ std::vector<char> reach(const th_floor_desc* d, const std::vector<int>& roots) {
   std::vector<char> r(d->n_terms, 0);
   for (int t : roots) r[t] = 1;
   for (int t = d->n_terms - 1; t >= 0; --t) {
-    if (!r[t] || d->terms[t].op != TH_TERM_APPLY) continue;
+    if (!r[t]) continue;
+    if (d->terms[t].op == TH_TERM_LOAD && d->terms[t].index.gather >= 0) r[d->terms[t].index.gather] = 1;
+    if (d->terms[t].op != TH_TERM_APPLY) continue;
     for (int j = 0; j < arity(d->terms[t].fn); ++j) r[d->terms[t].args[j]] = 1;
   }
   return r;
@@ -256,6 +277,8 @@ int plan(const th_floor_desc* d, Plan& pl) {
   for (int k : pl.swept) pl.count *= pl.E[k];
   const int nt = d->n_terms;
 
+  for (int t = 0; t < nt; ++t) pl.gathers |= d->terms[t].op == TH_TERM_LOAD && d->terms[t].index.gather >= 0;
+  for (int o = 0; o < d->n_outputs; ++o) pl.gathers |= d->outputs[o].index.gather >= 0;
   // Which terms move along the swept positions.
   pl.dep.assign(nt, 0);
   for (int t = 0; t < nt; ++t) {
@@ -265,6 +288,7 @@ int plan(const th_floor_desc* d, Plan& pl) {
         pl.dep[t] = 1;
       } else {
         for (int k : pl.swept) pl.dep[t] |= m.index.coeff[k] != 0;
+        if (m.op == TH_TERM_LOAD && m.index.gather >= 0) pl.dep[t] |= pl.dep[m.index.gather];
       }
     } else if (m.op == TH_TERM_APPLY) {
       for (int j = 0; j < arity(m.fn); ++j) pl.dep[t] |= pl.dep[m.args[j]];
@@ -334,7 +358,7 @@ int plan(const th_floor_desc* d, Plan& pl) {
     pl.rows = pl.kept.empty() || pos_unit >= item_unit;
     if (pl.rows) {
       pl.S = 1;
-      pl.W = (pl.E[s0] % 4 == 0 && pl.count >= 256) ? 4 : 1;
+      pl.W = (pl.E[s0] % 4 == 0 && pl.count >= 256 && !pl.gathers) ? 4 : 1;
       pl.vax = pl.W > 1 ? s0 : -1;
       pl.qn = pl.count / pl.W;
       pl.L = (int)std::min<int64_t>(256, std::max<int64_t>(64, nextpow2(pl.qn)));
@@ -356,7 +380,7 @@ int plan(const th_floor_desc* d, Plan& pl) {
       pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(want / pl.L, 1024));
     }
     // Loads kept in registers across the phases when an item's share fits.
-    if (pl.P == 1) {
+    if (pl.P == 1 && !pl.gathers) {
       int64_t iters = (pl.qn + pl.L - 1) / pl.L;
       int cached = 0;
       for (int t = 0; t < nt; ++t) cached += d->terms[t].op == TH_TERM_LOAD && pl.dep[t];
@@ -370,7 +394,7 @@ int plan(const th_floor_desc* d, Plan& pl) {
     for (int k = 0; k < pl.rank; ++k) pl.kept.push_back(k);
     pl.items = 1;
     for (int k = 0; k < pl.rank; ++k) pl.items *= pl.E[k];
-    pl.W = (pl.E[0] % 4 == 0 && pl.E[0] >= 4) ? 4 : 1;
+    pl.W = (pl.E[0] % 4 == 0 && pl.E[0] >= 4 && !pl.gathers) ? 4 : 1;
     pl.vax = pl.W > 1 ? 0 : -1;
     pl.qn = pl.items / pl.W;
     pl.S = 256;
@@ -429,6 +453,11 @@ __device__ __forceinline__ void th_st(float* p, long i, float v) { p[i] = v; }
 __device__ __forceinline__ void th_st(th_bf16* p, long i, float v) { p[i] = th_tobf(v); }
 __device__ __forceinline__ void th_stn(float* p, long i, float v) { __builtin_nontemporal_store(v, p + i); }
 __device__ __forceinline__ void th_stn(th_bf16* p, long i, float v) { __builtin_nontemporal_store(th_tobf(v), p + i); }
+__device__ __forceinline__ long th_ldi(const int* p, long i) { return (long)p[i]; }
+__device__ __forceinline__ long th_ldi(const long* p, long i) { return p[i]; }
+// A gathered position, held inside its value (0 .. n - 1).
+__device__ __forceinline__ long th_clampi(long i, long n) { return i < 0 ? 0 : (i >= n ? n - 1 : i); }
+__device__ __forceinline__ void th_add(float* p, long i, float v) { atomicAdd(p + i, v); }
 __device__ __forceinline__ float th_abs(float x) { return fabsf(x); }
 __device__ __forceinline__ float th_abs2(float x) { return x * x; }
 __device__ __forceinline__ float th_sqrt(float x) { return sqrtf(x); }
@@ -617,8 +646,29 @@ class Writer {
   std::ostringstream o_;
   int uid_ = 0;
 
-  std::string vtype(int v) const { return d_->values[v].dtype == TH_F32 ? "float" : "th_bf16"; }
+  std::string vtype(int v) const {
+    switch (d_->values[v].dtype) {
+      case TH_F32: return "float";
+      case TH_BF16: return "th_bf16";
+      case TH_I32: return "int";
+      default: return "long";
+    }
+  }
+  // The long variable each emitted integer load lives in (the latest scope's).
+  std::map<int, std::string> gvar_;
+  // An address: the affine part, plus the gathered term's value, clamped.
+  std::string addr(const th_affine& a, int value) {
+    std::string e = affine(pl_, a);
+    if (a.gather < 0) return e;
+    return "th_clampi(" + e + " + " + std::to_string(a.gather_coeff) + "L * " + gvar_.at(a.gather) + ", " +
+           std::to_string(d_->values[value].length) + "L)";
+  }
   std::string vname(int v) const { return "v" + std::to_string(v); }
+  // An output's term, and the term its address gathers by.
+  void out_roots(std::vector<int>& roots, int x) const {
+    roots.push_back(d_->outputs[x].term);
+    if (d_->outputs[x].index.gather >= 0) roots.push_back(d_->outputs[x].index.gather);
+  }
 
   void header(const std::string& name) {
     std::ostringstream& o = o_;
@@ -643,7 +693,8 @@ class Writer {
     switch (m.op) {
       case TH_TERM_LOAD: {
         if (cached && pl_.dep[t]) return "c" + std::to_string(t) + "[it]";
-        std::string p = vname(m.ref), at = affine(pl_, m.index);
+        std::string p = vname(m.ref), at = addr(m.index, m.ref);
+        if (is_int(d_->values[m.ref].dtype)) return "th_ldi(" + p + ", " + at + ")";
         if (!vec || pl_.W == 1) return "th_ld" + n + "(" + p + ", " + at + ")";
         const int64_t cv = m.index.coeff[pl_.vax];
         if (cv == 0) return "th_splat(th_ld(" + p + ", " + at + "))";
@@ -694,6 +745,14 @@ class Writer {
         }
       }
       std::string n = "t" + std::to_string(uid_++);
+      const th_term& m = d_->terms[t];
+      if (m.op == TH_TERM_LOAD && is_int(d_->values[m.ref].dtype)) {
+        // An integer: kept as such for the addresses that gather by it.
+        o_ << ind << "const long " << n << " = " << term_expr(t, false, false, names) << ";\n";
+        gvar_[t] = n;
+        names[t] = vec ? "th_splat((float)" + n + ")" : "(float)" + n;
+        continue;
+      }
       o_ << ind << "const " << ty << " " << n << " = " << term_expr(t, vec, cached, names) << ";\n";
       names[t] = n;
     }
@@ -967,7 +1026,11 @@ class Writer {
   }
 
   void store(const std::string& ind, const th_output& x, const std::string& val, bool vec) {
-    std::string p = vname(x.value), at = affine(pl_, x.index);
+    std::string p = vname(x.value), at = addr(x.index, x.value);
+    if (x.accumulate) {  // a fold by key: positions may repeat
+      o_ << ind << "th_add(" << p << ", " << at << ", " << val << ");\n";
+      return;
+    }
     // Full outputs are written once and not read again here: non-temporal.
     const std::string n = x.full ? "n" : "";
     if (!vec || pl_.W == 1) {
@@ -1052,7 +1115,7 @@ class Writer {
       o << "  if (lane == 0 && part == 0 && live) {\n";
       for (int k : pl_.swept) o << "    i" << k << " = 0;\n";
       std::vector<int> roots;
-      for (int x : once) roots.push_back(d_->outputs[x].term);
+      for (int x : once) out_roots(roots, x);
       std::map<int, std::string> names;
       emit("    ", reach(d_, roots), false, false, names, nullptr);
       for (int x : once) store("    ", d_->outputs[x], names.at(d_->outputs[x].term), false);
@@ -1060,7 +1123,7 @@ class Writer {
     }
     if (!full.empty()) {
       std::vector<int> roots;
-      for (int x : full) roots.push_back(d_->outputs[x].term);
+      for (int x : full) out_roots(roots, x);
       std::vector<char> r = reach(d_, roots);
       o << "  {\n";
       std::map<int, std::string> hoisted;
@@ -1128,7 +1191,7 @@ class Writer {
     std::vector<int> full, once;
     for (int x = 0; x < d_->n_outputs; ++x) (d_->outputs[x].full ? full : once).push_back(x);
     std::vector<int> roots;
-    for (int x : full) roots.push_back(d_->outputs[x].term);
+    for (int x : full) out_roots(roots, x);
     emit("    ", reach(d_, roots), false, false, names, nullptr);
     for (int x : full) store("    ", d_->outputs[x], names.at(d_->outputs[x].term), false);
     o << "  }\n";
@@ -1137,7 +1200,7 @@ class Writer {
     if (!once.empty()) {
       for (int k : pl_.swept) o << "  i" << k << " = 0;\n";
       std::vector<int> r2;
-      for (int x : once) r2.push_back(d_->outputs[x].term);
+      for (int x : once) out_roots(r2, x);
       std::map<int, std::string> names2;
       emit("  ", reach(d_, r2), false, false, names2, nullptr);
       for (int x : once) store("  ", d_->outputs[x], names2.at(d_->outputs[x].term), false);
@@ -1159,7 +1222,7 @@ class Writer {
     }
     o << "  }\n";
     std::vector<int> roots;
-    for (int x = 0; x < d_->n_outputs; ++x) roots.push_back(d_->outputs[x].term);
+    for (int x = 0; x < d_->n_outputs; ++x) out_roots(roots, x);
     std::map<int, std::string> names;
     emit("  ", reach(d_, roots), pl_.W > 1, false, names, nullptr);
     for (int x = 0; x < d_->n_outputs; ++x) store("  ", d_->outputs[x], names.at(d_->outputs[x].term), true);
@@ -1356,11 +1419,11 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
   // Algorithmic bytes: every value read once, every output written once.
   double bytes = 0;
   for (int v = 0; v < d->n_values; ++v)
-    if (pl.read[v]) bytes += (double)d->values[v].length * (d->values[v].dtype == TH_F32 ? 4 : 2);
+    if (pl.read[v]) bytes += (double)d->values[v].length * esize(d->values[v].dtype);
   for (int x = 0; x < d->n_outputs; ++x) {
     const th_floor_value& v = d->values[d->outputs[x].value];
     double n = d->outputs[x].full ? (double)pl.items * (pl.reduction ? pl.count : 1) : (double)pl.items;
-    bytes += n * (v.dtype == TH_F32 ? 4 : 2);
+    bytes += n * esize(v.dtype);
   }
   b.work(bytes, 0.0, pl.reduction ? (pl.items + pl.S - 1) / pl.S * pl.P : (pl.qn + pl.S - 1) / pl.S);
   *out = b.release();

@@ -224,14 +224,15 @@ end
 # src/Compiler/codegen/scalar.jl:186-250) and CUDA compiles it (floor_launch,
 # ext/CUDAExt.jl:926-937).  Here the group's terms cross the C ABI as arrays
 # (th_floor_desc) and libtempest_hip writes and compiles the gfx950 kernel.
-# Supported: Var atoms in addresses (Div, Mod and Indirect atoms throw, and the
-# build falls back), the functions of FLOOR_FN, and the folds of FLOOR_FOLD.
+# Supported: Var atoms in addresses and one Indirect atom (a gathered index;
+# Div and Mod atoms throw, and the build falls back), the functions of FLOOR_FN,
+# and the folds of FLOOR_FOLD.
 
 struct FloorValue; dtype::Int32; reserved::Int32; length::Int64; ptr::Ptr{Cvoid}; end
-struct CAffine; constant::Int64; coeff::NTuple{4, Int64}; end
+struct CAffine; constant::Int64; coeff::NTuple{4, Int64}; gather::Int32; reserved::Int32; gather_coeff::Int64; end
 struct CTerm; op::Int32; fn::Int32; args::NTuple{3, Int32}; ref::Int32; observe::Int32; lit::Float32; index::CAffine; end
 struct CFold; kind::Int32; phase::Int32; body::Int32; weight::Int32; scan::Int32; reserved::Int32; end
-struct COutput; value::Int32; term::Int32; full::Int32; reserved::Int32; index::CAffine; end
+struct COutput; value::Int32; term::Int32; full::Int32; accumulate::Int32; index::CAffine; end
 struct FloorDesc
     kind::Int32; rank::Int32; extents::NTuple{4, Int64}; reduced::UInt32
     n_values::Int32; n_terms::Int32; n_folds::Int32; n_outputs::Int32; flags::Int32
@@ -259,13 +260,20 @@ function floor_fold(fold)
     throw(ArgumentError("the generated floor has no fold $(typeof(fold))"))
 end
 
-function caffine(e, vars)
+# `gathered(atom)` adds the load an Indirect atom reads and returns its term number.
+function caffine(e, gathered)
     c = zeros(Int64, 4)
+    gather, gc = Int32(-1), 0
     for (atom, k) in e.terms
-        atom isa Tempest.Compiler.IR.Var || throw(ArgumentError("only positions in floor addresses"))
-        c[atom.n] += k
+        if atom isa Tempest.Compiler.IR.Var
+            c[atom.n] += k
+        elseif atom isa Tempest.Compiler.IR.Indirect && gather < 0
+            gather, gc = gathered(atom), k
+        else
+            throw(ArgumentError("floor addresses take positions and one gathered index"))
+        end
     end
-    CAffine(e.constant, Tuple(c))
+    CAffine(e.constant, Tuple(c), gather, 0, gc)
 end
 
 # The group as th_floor_desc arrays; `slots` numbers its values, `buffers` their storage.
@@ -274,16 +282,18 @@ function floor_descriptor(graph, g, slots, buffers)
     terms, index = CTerm[], IdDict{Any, Int32}()
     folds = [r for r in g.reductions]
     fold_no = Dict(r => Int32(i - 1) for (i, r) in enumerate(folds))
-    z = CAffine(0, (0, 0, 0, 0))
+    z = CAffine(0, (0, 0, 0, 0), -1, 0, 0)
+    # An Indirect atom reads value `a.value` at `a.index`: a load term of its own.
+    gathered(a) = add!(C.IR.Load(a.value, a.index))
     function add!(t)
         haskey(index, t) && return index[t]
         ct = if t isa C.IR.Load
             CTerm(0, 0, (0, 0, 0), findfirst(==(t.value), slots) - 1, 0, 0f0,
-                  caffine(C.address(graph.values[t.value], t.index, C.Domain(g.domain)), nothing))
+                  caffine(C.address(graph.values[t.value], t.index, C.Domain(g.domain)), gathered))
         elseif t isa C.IR.Lit
             CTerm(1, 0, (0, 0, 0), 0, 0, Float32(t.value), z)
         elseif t isa C.IR.Ix
-            CTerm(2, 0, (0, 0, 0), 0, 0, 0f0, caffine(t.expr, nothing))
+            CTerm(2, 0, (0, 0, 0), 0, 0, 0f0, caffine(t.expr, gathered))
         elseif t isa C.IR.Stat
             CTerm(3, 0, (0, 0, 0), fold_no[t.value], floor_fold(graph.values[t.value].definition.fold)[2], 0f0, z)
         elseif t isa C.IR.Apply
@@ -300,9 +310,11 @@ function floor_descriptor(graph, g, slots, buffers)
     cfolds = [CFold(floor_fold(graph.values[r].definition.fold)[1], g.phase[r], add!(g.terms[r]), -1,
                     scan_of(graph.values[r].definition), 0) for r in folds]
     outs = [COutput(findfirst(==(m), slots) - 1, add!(g.terms[m]), graph.values[m].dims == g.domain, 0,
-                    caffine(C.address(graph.values[m], C.identity_index(g.domain), C.Domain(g.domain)), nothing))
+                    caffine(C.address(graph.values[m], C.identity_index(g.domain), C.Domain(g.domain)), gathered))
             for m in g.outputs]
-    vals = [FloorValue(graph.values[v].eltype === Float32 ? 0 : 1, 0, C.storage_length(graph.values[v]),
+    code(T) = T === Float32 ? 0 : T === Tempest.BFloat16 ? 1 : T === Int32 ? 2 : T === Int64 ? 3 :
+        throw(ArgumentError("the generated floor has no $T values"))
+    vals = [FloorValue(code(graph.values[v].eltype), 0, C.storage_length(graph.values[v]),
                        address(buffers[i])) for (i, v) in enumerate(slots)]
     ext = ntuple(k -> k <= length(g.domain) ? Int64(g.domain[k]) : 1, 4)
     reduced = UInt32(sum((1 << (k - 1) for k in C.primary_axes(graph, g)); init = 0))

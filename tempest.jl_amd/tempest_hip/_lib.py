@@ -65,7 +65,8 @@ FLOOR_RANK = 4
 
 
 class Affine(ctypes.Structure):
-    _fields_ = [("constant", c_i64), ("coeff", c_i64 * FLOOR_RANK)]
+    _fields_ = [("constant", c_i64), ("coeff", c_i64 * FLOOR_RANK), ("gather", c_i32), ("reserved", c_i32),
+                ("gather_coeff", c_i64)]
 
 
 class FloorValue(ctypes.Structure):
@@ -83,7 +84,7 @@ class FoldStruct(ctypes.Structure):
 
 
 class OutputStruct(ctypes.Structure):
-    _fields_ = [("value", c_i32), ("term", c_i32), ("full", c_i32), ("reserved", c_i32),
+    _fields_ = [("value", c_i32), ("term", c_i32), ("full", c_i32), ("accumulate", c_i32),
                 ("index", Affine)]
 
 

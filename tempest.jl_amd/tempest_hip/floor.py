@@ -44,7 +44,7 @@ ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", 
 FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6}
 SCAN = {None: 0, "inclusive": 1, "exclusive": 2}
 OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}
-DTYPE = {"f32": 0, "bf16": 1}
+DTYPE = {"f32": 0, "bf16": 1, "i32": 2, "i64": 3}
 
 
 class Term:
@@ -106,11 +106,12 @@ class Fold:
         return self._stat("statistic")
 
 
-def _affine(coeffs: Sequence[int] | None, constant: int, rank: int) -> tuple:
+def _affine(coeffs: Sequence[int] | None, constant: int, rank: int, gather=None, gather_coeff: int = 1) -> tuple:
     c = list(coeffs or ())
     if len(c) > rank:
         raise ValueError(f"{len(c)} coefficients for a rank-{rank} domain")
-    return (int(constant), tuple(int(x) for x in c) + (0,) * (RANK - len(c)))
+    g = -1 if gather is None else gather.index
+    return (int(constant), tuple(int(x) for x in c) + (0,) * (RANK - len(c)), g, int(gather_coeff))
 
 
 @dataclass
@@ -138,13 +139,14 @@ class FloorGroup:
     # -- building the group -------------------------------------------------------
 
     def value(self, name: str, dtype: str, length: int) -> str:
+        """A value the group reads or writes: f32 or bf16, or i32 / i64 indices (read only)."""
         if dtype not in DTYPE:
-            raise ValueError(f"values are f32 or bf16, not {dtype!r}")
+            raise ValueError(f"values are f32, bf16, i32 or i64, not {dtype!r}")
         self.values[name] = (dtype, int(length))
         return name
 
     def _term(self, op: str, fn: int = 0, args=(), ref: int = 0, observe: int = 0, lit: float = 0.0,
-              affine=(0, (0,) * RANK)) -> Term:
+              affine=(0, (0,) * RANK, -1, 0)) -> Term:
         self.terms.append((TERM[op], fn, tuple(args) + (0,) * (3 - len(args)), ref, observe, float(lit), affine))
         return Term(self, len(self.terms) - 1)
 
@@ -155,10 +157,12 @@ class FloorGroup:
             return x
         return self.lit(float(x))
 
-    def load(self, name: str, coeffs: Sequence[int] | None = None, constant: int = 0) -> Term:
-        """Element ``constant + sum(coeffs[k] * i_k)`` of value ``name``."""
+    def load(self, name: str, coeffs: Sequence[int] | None = None, constant: int = 0, gather: Term | None = None,
+             gather_coeff: int = 1) -> Term:
+        """Element ``constant + sum(coeffs[k] * i_k) (+ gather_coeff * gather)`` of
+        value ``name``; ``gather`` is a load of integers (an Indirect atom)."""
         ref = list(self.values).index(name)
-        return self._term("load", ref=ref, affine=_affine(coeffs, constant, len(self.extents)))
+        return self._term("load", ref=ref, affine=_affine(coeffs, constant, len(self.extents), gather, gather_coeff))
 
     def lit(self, x: float) -> Term:
         return self._term("lit", lit=x)
@@ -193,10 +197,13 @@ class FloorGroup:
         return Fold(self, len(self.folds) - 1, kind)
 
     def output(self, name: str, term, coeffs: Sequence[int] | None = None, constant: int = 0,
-               full: bool = True) -> None:
+               full: bool = True, gather: Term | None = None, gather_coeff: int = 1,
+               accumulate: bool = False) -> None:
+        """Write ``term`` at the address (every position, or once per item);
+        ``accumulate`` adds it instead, atomically (a fold by key)."""
         v = list(self.values).index(name)
         self.outputs.append((v, self._as_term(term).index, int(bool(full)),
-                             _affine(coeffs, constant, len(self.extents))))
+                             _affine(coeffs, constant, len(self.extents), gather, gather_coeff), int(bool(accumulate))))
 
     # -- the ABI ---------------------------------------------------------------------
 
@@ -206,20 +213,20 @@ class FloorGroup:
         for k, ((dt, n), p) in enumerate(zip(self.values.values(), ptrs)):
             values[k].dtype, values[k].length, values[k].ptr = DTYPE[dt], n, p
         terms = (TermStruct * max(nt, 1))()
-        for k, (op, fn, args, ref, obs, lit, (c0, cs)) in enumerate(self.terms):
+        for k, (op, fn, args, ref, obs, lit, (c0, cs, gt, gc)) in enumerate(self.terms):
             t = terms[k]
             t.op, t.fn, t.ref, t.observe, t.lit = op, fn, ref, obs, lit
             t.args[:] = list(args)
-            t.index.constant = c0
+            t.index.constant, t.index.gather, t.index.gather_coeff = c0, gt, gc
             t.index.coeff[:] = list(cs)
         folds = (FoldStruct * max(nf, 1))()
         for k, (kind, phase, body, weight, scan) in enumerate(self.folds):
             folds[k].kind, folds[k].phase, folds[k].body, folds[k].weight = kind, phase, body, weight
             folds[k].scan = scan
         outs = (OutputStruct * max(no, 1))()
-        for k, (v, term, full, (c0, cs)) in enumerate(self.outputs):
-            outs[k].value, outs[k].term, outs[k].full = v, term, full
-            outs[k].index.constant = c0
+        for k, (v, term, full, (c0, cs, gt, gc), acc) in enumerate(self.outputs):
+            outs[k].value, outs[k].term, outs[k].full, outs[k].accumulate = v, term, full, acc
+            outs[k].index.constant, outs[k].index.gather, outs[k].index.gather_coeff = c0, gt, gc
             outs[k].index.coeff[:] = list(cs)
         d = FloorDesc()
         d.kind, d.rank = GROUP[self.kind], len(self.extents)
@@ -263,7 +270,7 @@ class FloorGroup:
     def as_group(self) -> Group:
         """The group as a kernel of a Program (runtime.Group)."""
         order = tuple(self.values)
-        writes = tuple(dict.fromkeys(order[v] for v, *_ in self.outputs))
+        writes = tuple(dict.fromkeys(order[o[0]] for o in self.outputs))
         reads = tuple(dict.fromkeys(order[self.terms[t][3]] for t in range(len(self.terms))
                                     if self.terms[t][0] == TERM["load"]))
         return Group(self.name, order, reads, writes, self.build)
@@ -280,10 +287,12 @@ class FloorGroup:
             "values": dict(self.values),
             "terms": [{"op": inv_term[op], "fn": inv_fn.get(fn) if op == TERM["apply"] else None,
                        "args": list(args[:ARITY[inv_fn[fn]]]) if op == TERM["apply"] else [],
-                       "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1])}
+                       "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1]),
+                       "gather": aff[2], "gather_coeff": aff[3]}
                       for op, fn, args, ref, obs, lit, aff in self.terms],
             "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w, "scan": inv_scan[sc]}
                       for k, p, b, w, sc in self.folds],
             "outputs": [{"value": list(self.values)[v], "term": t, "full": bool(f), "constant": aff[0],
-                         "coeffs": list(aff[1])} for v, t, f, aff in self.outputs],
+                         "coeffs": list(aff[1]), "gather": aff[2], "gather_coeff": aff[3], "accumulate": bool(acc)}
+                        for v, t, f, aff, acc in self.outputs],
         }

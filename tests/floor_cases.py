@@ -554,12 +554,136 @@ def running_logsumexp_and_mean(n=12, m=4):
     return Case("running logsumexp and mean", [g], {"x": F(x)}, {"lse": n * m, "mean": n * m}, ["lse", "mean"], closed)
 
 
+# ---- gathers (Indirect atoms) and folds by key -------------------------------------
+
+def _idx(a):
+    return np.asarray(a, dtype=np.int64).ravel(order="F")
+
+
+def gather_by_a_list():
+    """sum(abs2, x[:, [3, 1, 3, 6]]): the columns by a list of (1-based) indices."""
+    x, i = data(8, 6), _idx([3, 1, 3, 6])
+    g = FloorGroup("reduction", (8, 4), reduced=(0, 1), name="x[:, i]")
+    g.value("x", "f32", 48)
+    g.value("i", "i64", 4)
+    g.value("loss", "f32", 1)
+    col = g.load("i", (0, 1))
+    g.output("loss", g.fold("sum", g.apply("abs2", g.load("x", (1, 0), constant=-8, gather=col, gather_coeff=8))).value,
+             full=False)
+    return Case("gather by a constant list", [g], {"x": F(x), "i": i}, {"loss": 1}, ["loss"],
+                lambda v: {"loss": [np.sum(v["x"].reshape(8, 6, order="F")[:, [2, 0, 2, 5]] ** 2)]},
+                dtypes={"i": "i64"})
+
+
+def gather_by_an_int32_matrix():
+    """sum(abs2, x[:, i]), i = Int32[2 5; 6 1; 1 1]: an 8 x 3 x 2 gather."""
+    x, i = data(8, 6), np.array([[2, 5], [6, 1], [1, 1]])
+    g = FloorGroup("reduction", (8, 3, 2), reduced=(0, 1, 2), name="x[:, i], i a matrix")
+    g.value("x", "f32", 48)
+    g.value("i", "i32", 6)
+    g.value("loss", "f32", 1)
+    col = g.load("i", (0, 1, 3))
+    g.output("loss", g.fold("sum", g.apply("abs2", g.load("x", (1, 0, 0), constant=-8, gather=col,
+                                                          gather_coeff=8))).value, full=False)
+    return Case("gather by a traced Int32 matrix", [g], {"x": F(x), "i": _idx(i)}, {"loss": 1}, ["loss"],
+                lambda v: {"loss": [np.sum(v["x"].reshape(8, 6, order="F")[:, i.ravel(order="F") - 1] ** 2)]},
+                dtypes={"i": "i32"})
+
+
+def gather_rows_by_an_int64_matrix():
+    """sum(abs2, tanh.(x[i, :])), i = [8 1; 2 8]: rows gathered, a 2 x 2 x 6 array."""
+    x, i = data(8, 6), np.array([[8, 1], [2, 8]])
+    g = FloorGroup("reduction", (2, 2, 6), reduced=(0, 1, 2), name="x[i, :]")
+    g.value("x", "f32", 48)
+    g.value("i", "i64", 4)
+    g.value("loss", "f32", 1)
+    row = g.load("i", (1, 2, 0))
+    xx = g.load("x", (0, 0, 8), constant=-1, gather=row, gather_coeff=1)
+    g.output("loss", g.fold("sum", g.apply("abs2", g.apply("tanh", xx))).value, full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        return {"loss": [np.sum(np.tanh(X[i.ravel(order="F") - 1, :]) ** 2)]}
+    return Case("gather rows by a traced Int64 matrix", [g], {"x": F(x), "i": _idx(i)}, {"loss": 1}, ["loss"],
+                closed, dtypes={"i": "i64"})
+
+
+def gather_by_linear_and_scalar_indices():
+    """sum(abs2, x[i]) + x[2, t], i = [40, 3, 17], t = 5."""
+    x = data(8, 6)
+    g = FloorGroup("reduction", (3,), reduced=(0,), name="x[i] and x[2, t]")
+    g.value("x", "f32", 48)
+    g.value("i", "i64", 3)
+    g.value("t", "i64", 1)
+    g.value("loss", "f32", 1)
+    s = g.fold("sum", g.apply("abs2", g.load("x", (0,), constant=-1, gather=g.load("i", (1,)), gather_coeff=1))).value
+    xt = g.load("x", (0,), constant=1 - 8, gather=g.load("t", (0,)), gather_coeff=8)
+    g.output("loss", s + xt, full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        return {"loss": [np.sum(v["x"][[39, 2, 16]] ** 2) + X[1, 4]]}
+    return Case("gather by linear and scalar indices", [g], {"x": F(x), "i": _idx([40, 3, 17]), "t": _idx([5])},
+                {"loss": 1}, ["loss"], closed, dtypes={"i": "i64", "t": "i64"})
+
+
+def embedding_and_layer_norm():
+    """sum(abs2, layernorm(E[:, t] .+ P, w)): E 8 x 10, P 8 x 3, t = Int32[3 1; 10 3; 7 7]."""
+    E, P, w = data(8, 10, scale=0.3), data(8, 3, scale=0.2), data(8, scale=0.1)
+    t = np.array([[3, 1], [10, 3], [7, 7]])
+    g = FloorGroup("reduction", (8, 3, 2), reduced=(0,), name="layernorm(E[:, t] .+ P, w)")
+    g.value("E", "f32", 80)
+    g.value("P", "f32", 24)
+    g.value("w", "f32", 8)
+    g.value("t", "i32", 6)
+    g.value("r", "f32", 6)
+    tok = g.load("t", (0, 1, 3))
+    xx = g.load("E", (1, 0, 0), constant=-8, gather=tok, gather_coeff=8) + g.load("P", (1, 8, 0))
+    mu = g.fold("sum", xx).value / 8.0
+    var = g.fold("sum", g.apply("abs2", xx - mu), phase=2).value / 8.0
+    y = (xx - mu) / g.apply("sqrt", var + 1e-5) * g.load("w", (1, 0, 0))
+    g.output("r", g.fold("sum", g.apply("abs2", y), phase=3).value, (0, 1, 3), full=False)
+
+    def closed(v):
+        Ev, Pv = v["E"].reshape(8, 10, order="F"), v["P"].reshape(8, 3, order="F")
+        X = Ev[:, t - 1] + Pv[:, :, None]  # 8 x 3 x 2
+        mu_ = X.mean(axis=0, keepdims=True)
+        var_ = ((X - mu_) ** 2).mean(axis=0, keepdims=True)
+        Y = (X - mu_) / np.sqrt(var_ + 1e-5) * v["w"][:, None, None]
+        r = (Y ** 2).sum(axis=0).ravel(order="F")
+        return {"r": r, "loss": [r.sum()]}
+    return Case("embedding lookup and layer norm", [g, _full_sum("r", 6)],
+                {"E": F(E), "P": F(P), "w": F(w), "t": _idx(t)}, {"r": 6, "loss": 1}, ["r", "loss"], closed,
+                dtypes={"t": "i32"})
+
+
+def scatter_add_gradient():
+    """The gradient of x[:, i] with i = [3, 1, 3, 6]: dx[:, i] .+= dy, column 3
+    twice (a fold by key, accumulate!(::SumFold))."""
+    dy, i = data(8, 4, scale=0.5), _idx([3, 1, 3, 6])
+    g = FloorGroup("pointwise", (8, 4), name="dx[:, i] .+= dy")
+    g.value("dy", "f32", 32)
+    g.value("i", "i64", 4)
+    g.value("dx", "f32", 48)
+    g.output("dx", g.load("dy", (1, 8)), (1, 0), constant=-8, gather=g.load("i", (0, 1)), gather_coeff=8,
+             accumulate=True)
+
+    def closed(v):
+        dx = np.zeros((8, 6))
+        np.add.at(dx.T, [2, 0, 2, 5], v["dy"].reshape(8, 4, order="F").T)
+        return {"dx": dx.ravel(order="F")}
+    return Case("scatter add (a fold by key)", [g], {"dy": F(dy), "i": i}, {"dx": 48}, ["dx"], closed,
+                dtypes={"i": "i64"})
+
+
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
          map_over_two_arrays, permutation, bias_tanh_bf16, index_scaled, kat_sum_abs2,
          cumulative_sums, cumulative_products_through_a_zero, running_maxima_and_minima, linear_recurrence,
-         running_average, reverse_exclusive_sums, running_logsumexp_and_mean]
+         running_average, reverse_exclusive_sums, running_logsumexp_and_mean,
+         gather_by_a_list, gather_by_an_int32_matrix, gather_rows_by_an_int64_matrix,
+         gather_by_linear_and_scalar_indices, embedding_and_layer_norm, scatter_add_gradient]
 
 
 def run_oracle(case: Case) -> dict:
@@ -570,8 +694,12 @@ def run_oracle(case: Case) -> dict:
     for k, n in case.stored.items():
         vals[k] = np.zeros(n)
     for k in vals:
-        # What the device holds: Float32 inputs, bfloat16 where the case says so.
-        vals[k] = (bf16_round(vals[k].astype(np.float32)) if case.dtypes.get(k) == "bf16"
+        # What the device holds: Float32 inputs, bfloat16 or integers where the case says so.
+        dt = case.dtypes.get(k)
+        if dt in ("i32", "i64"):
+            vals[k] = np.asarray(case.inputs[k], dtype=np.int64)
+            continue
+        vals[k] = (bf16_round(vals[k].astype(np.float32)) if dt == "bf16"
                    else vals[k].astype(np.float32)).astype(np.float64)
     for g in case.groups:
         out = evaluate(g.spec(), vals)

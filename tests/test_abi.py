@@ -82,11 +82,11 @@ def test_floor_structures_match_the_header(tmp_path):
     lays out include/tempest_hip.h, against the ctypes mirror."""
     import subprocess
     import tempest_hip._lib as L
-    members = {"th_affine": (L.Affine, ["constant", "coeff"]),
+    members = {"th_affine": (L.Affine, ["constant", "coeff", "gather", "gather_coeff"]),
                "th_floor_value": (L.FloorValue, ["dtype", "length", "ptr"]),
                "th_term": (L.TermStruct, ["op", "fn", "args", "ref", "observe", "lit", "index"]),
                "th_fold": (L.FoldStruct, ["kind", "phase", "body", "weight", "scan"]),
-               "th_output": (L.OutputStruct, ["value", "term", "full", "index"]),
+               "th_output": (L.OutputStruct, ["value", "term", "full", "accumulate", "index"]),
                "th_floor_desc": (L.FloorDesc, ["kind", "rank", "extents", "reduced", "n_values", "n_terms",
                                                "n_folds", "n_outputs", "flags", "values", "terms", "folds",
                                                "outputs"])}

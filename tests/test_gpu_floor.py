@@ -19,13 +19,18 @@ TOL_BF16 = 1e-2  # values stored as bfloat16 (one rounding: 2^-9 relative)
 
 def _tensors(case):
     out = {}
+    ints = {"i32": np.int32, "i64": np.int64}
     for k, n in case.lengths().items():
+        dt = case.dtypes.get(k)
+        if dt in ints:
+            out[k] = torch.from_numpy(np.asarray(case.inputs[k], dtype=ints[dt])).cuda()
+            continue
         if k in case.inputs:
             v = np.asarray(case.inputs[k], dtype=np.float32)
         else:
             v = np.zeros(n, dtype=np.float32)
         t = torch.from_numpy(v).cuda()
-        out[k] = t.to(torch.bfloat16) if case.dtypes.get(k) == "bf16" else t
+        out[k] = t.to(torch.bfloat16) if dt == "bf16" else t
     return out
 
 
@@ -229,3 +234,36 @@ def test_scans_at_size(target, n, m, axis, reverse):
     # Sequential fp32 sums of up to 1e5 terms: error grows like the running magnitude.
     assert relative(got_c, C) < (1e-5 if X.shape[axis] <= 2000 else 1e-4)
     assert relative(got_h, H) < TOL
+
+
+def test_embedding_gather_and_scatter_add_at_size(target):
+    """y[:, j] = E[:, t[j]] for 20000 tokens of a 1024 x 30000 table, then the
+    gradient dE[:, t[j]] += dy[:, j] (repeated tokens add atomically)."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor embedding gather / scatter")
+    d, vocab, n = 1024, 30000, 20000
+    rng = np.random.default_rng(21)
+    E = rng.standard_normal(d * vocab).astype(np.float32)
+    tok = rng.integers(1, 200, n).astype(np.int32)  # 1-based, heavily repeated
+    dy = rng.standard_normal(d * n).astype(np.float32)
+    fwd = FloorGroup("pointwise", (d, n), name="E[:, t]")
+    fwd.value("E", "f32", d * vocab)
+    fwd.value("t", "i32", n)
+    fwd.value("y", "f32", d * n)
+    fwd.output("y", fwd.load("E", (1, 0), constant=-d, gather=fwd.load("t", (0, 1)), gather_coeff=d), (1, d))
+    bwd = FloorGroup("pointwise", (d, n), name="dE[:, t] .+= dy")
+    bwd.value("dy", "f32", d * n)
+    bwd.value("t", "i32", n)
+    bwd.value("dE", "f32", d * vocab)
+    bwd.output("dE", bwd.load("dy", (1, d)), (1, 0), constant=-d, gather=bwd.load("t", (0, 1)), gather_coeff=d,
+               accumulate=True)
+    ts = {"E": torch.from_numpy(E).cuda(), "t": torch.from_numpy(tok).cuda(), "y": torch.zeros(d * n, device="cuda"),
+          "dy": torch.from_numpy(dy).cuda(), "dE": torch.zeros(d * vocab, device="cuda")}
+    fwd.build({k: ts[k].data_ptr() for k in fwd.values})()
+    bwd.build({k: ts[k].data_ptr() for k in bwd.values})()
+    torch.cuda.synchronize()
+    Em = E.reshape(vocab, d)
+    assert np.array_equal(ts["y"].cpu().numpy().reshape(n, d), Em[tok - 1])
+    want = np.zeros((vocab, d))
+    np.add.at(want, tok - 1, dy.reshape(n, d).astype(np.float64))
+    assert relative(ts["dE"].cpu().numpy().reshape(vocab, d), want) < TOL

@@ -13,7 +13,8 @@ CASES = {c.__name__: c for c in FC.CASES}
 
 
 def _cast_inputs(case):
-    return {k: np.asarray(v, dtype=np.float32).astype(np.float64) for k, v in case.inputs.items()}
+    return {k: (np.asarray(v) if case.dtypes.get(k) in ("i32", "i64") else
+                np.asarray(v, dtype=np.float32).astype(np.float64)) for k, v in case.inputs.items()}
 
 
 @pytest.mark.parametrize("name", list(CASES))
