@@ -72,7 +72,10 @@ __global__ void th_blank_kernel(int) {}
 
 // Read `words` 32-bit words, keeping their xor only where zeros could not give
 // it, so that the reads stay: the cache clearing of a timing
-// (read_through, ext/CUDAExt.jl:837-850).
+// (read_through, ext/CUDAExt.jl:837-850).  Ordinary loads, which allocate in
+// L2 and in the Infinity Cache (MALL), so that reading twice their size
+// evicts both; non-temporal loads left the MALL holding what a timed launch
+// read before (a 16 MB column sum then measured 16 TB/s).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct ClearArgs {
   const u32x4* a;
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void th_clear_kernel(ClearArgs c) {
   uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   uint32_t s = 0;
   for (; i < c.n; i += stride) {
-    u32x4 v = __builtin_nontemporal_load(c.a + i);
+    u32x4 v = c.a[i];
     s ^= v[0] ^ v[1] ^ v[2] ^ v[3];
   }
   if (s == 0xffffffffu) c.sink[0] = s;
@@ -146,8 +149,10 @@ int th_device_rates(th_rates* out) {
   int clock_khz = 0, bus_bits = 0;
   TH_HIP(hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeMemoryClockRate, ctx().device));
   TH_HIP(hipDeviceGetAttribute(&bus_bits, hipDeviceAttributeMemoryBusWidth, ctx().device));
-  // HBM transfers twice a clock; bytes/s = 2 * clock * pins / 8.
-  double bandwidth = 2.0 * 1.0e3 * clock_khz * bus_bits / 8.0;
+  // HBM3E as the runtime reports it on MI355X: a 2 GHz memory clock, four
+  // transfers a clock on each of 8192 pins (8 Gb/s a pin, 8.2 TB/s);
+  // bytes/s = 4 * clock * pins / 8.
+  double bandwidth = 4.0 * 1.0e3 * clock_khz * bus_bits / 8.0;
   // CDNA4 has 256 MiB of MALL (Infinity Cache) behind the XCDs' L2.
   double cache = (double)p.l2CacheSize + 256.0 * 1024 * 1024;
   out->launch = 5.0e-7;
