@@ -246,6 +246,13 @@ struct TileDma {
 #pragma unroll
     for (int i = 0; i < 4; ++i) th_dev::dma16(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
   }
+  // The same for tiles read once (non-temporal).
+  __device__ __forceinline__ void load_stream(int row0, const uint16_t* lds) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t dst = (uint32_t)(uintptr_t)lds + 1024 * 4 * w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) th_dev::dma16_nt(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
+  }
 };
 
 __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
@@ -899,7 +906,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
     auto fetch = [&](int kb) {
       const int s = kb % kDqStages, at = min(kb, nkb - 1) * kFwdK;
       kt.load(at, Ks(s));
-      dt.load(at, Ds(s));
+      // dS' is read once: non-temporal, so the stream does not evict the K
+      // tiles every query block of this head rereads from L2.
+      dt.load_stream(at, Ds(s));
     };
     f32x16 dq[4];
 #pragma unroll

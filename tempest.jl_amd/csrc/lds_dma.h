@@ -33,6 +33,12 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, int32_t voff,
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0));
 }
 
+// The same for a stream read once: non-temporal, so that it does not evict
+// from L2 what other loads reuse.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t rsrc, int32_t voff, int32_t soff, uint32_t m0) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(m0));
+}
+
 // One 4-byte lane load from global memory straight into LDS at byte
 // m0 + 4 lane.
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, int32_t voff, int32_t soff, uint32_t m0) {
