@@ -871,17 +871,51 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
 }
 
 // ---- backward: dQ from the stored dS' -------------------------------------------------
-// dQ' (128 d x 128 queries per workgroup) += K' dS' over key blocks of 64,
+// dQ' (128 d x 128 queries per workgroup) += K' dS' over key blocks of 32,
 // both operands read transposed from row-major LDS tiles: K [key][d] and
 // dS' [key][query] (the dK/dV kernel wrote every entry this sweep reads;
-// masked ones are 0).  One product per step instead of three, no exp.  Its
-// operands all come through transposed LDS reads, whose throughput grows
-// with the reads in flight per CU (a wave keeps at most ~15): so two
-// workgroups per CU, each wave reading a block's twenty fragments at once,
-// and loads (direct global->LDS) one block ahead in a ring of two stages.
+// masked ones are 0).  One product per step instead of three, no exp.  The
+// sweep streams dS' (read once, non-temporal) and is bound by how many bytes
+// are in flight: blocks of 32 keys (8 KB of K and 8 KB of dS' each) in a ring
+// of four stages are issued three blocks ahead, each step waiting only for
+// the next block, in the 64 KB of LDS that leaves two workgroups a CU.  (A
+// ring of 64-key blocks one ahead kept one block in flight and read dS' at
+// ~3.7 TB/s; read in this order with plain loads it streams at 7.1 TB/s.)
 
-constexpr int kDqStages = 2;
-constexpr size_t kDqDsLds = 2 * kDqStages * kTileElems * sizeof(uint16_t);  // (K, dS') per stage
+constexpr int kDqRows = 32;    // keys per step
+constexpr int kDqStages = 4;   // stages in the ring
+constexpr int kDqAhead = 3;    // blocks in flight beyond the one being read
+constexpr int kDqTileElems = kDqRows * kD;
+constexpr size_t kDqDsLds = 2 * kDqStages * kDqTileElems * sizeof(uint16_t);  // (K, dS') per stage
+
+// Direct global -> LDS loads of a 32-row tile: each wave 8 rows, two 1 KB
+// instructions; rows XOR-permuted as tile_at lays them out.
+struct HalfTileDma {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int32_t off[2];
+  int32_t row_bytes;
+  __device__ HalfTileDma(const uint16_t* base, int64_t rs) {
+    rsrc = th_dev::buffer_of(base);
+    row_bytes = (int32_t)(rs * 2);
+    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 8 * w + 4 * i + l / 16;
+      const int c = (l % 16) ^ (4 * (r % 4) + (r / 4) % 4);
+      off[i] = (int32_t)(((int64_t)r * rs + 8 * c) * 2);
+    }
+  }
+  template <bool kStream>
+  __device__ __forceinline__ void load(int row0, const uint16_t* lds) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t dst = (uint32_t)(uintptr_t)lds + 1024 * 2 * w;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (kStream) th_dev::dma16_nt(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
+      else th_dev::dma16(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
+    }
+  }
+};
 
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
@@ -895,58 +929,72 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
     const int qw = qb * kFwdQ;  // the workgroup's first query
-    const TileDma kt(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
-    // The query block's dS' tiles, one 16 KB tile (64 keys x 128 queries) per key block.
-    const TileDma dt(p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + (int64_t)qb * (p.seq / 64) * (64 * 128), 128);
-    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kFwdK : p.seq / kFwdK;  // even, >= 2
-    auto Ks = [&](int s) { return lds + 2 * s * kTileElems; };
-    auto Ds = [&](int s) { return lds + (2 * s + 1) * kTileElems; };
-    // Key block kb into stage kb % kDqStages (blocks past the end: a harmless
-    // reload of the last one into an idle stage).  Eight loads per wave.
+    const HalfTileDma kt(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
+    // The query block's dS' tiles (64 keys x 128 queries, 16 KB each, one per
+    // 64 keys, contiguous): key row r of the sweep is row r of their concatenation.
+    const HalfTileDma dt(p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + (int64_t)qb * (p.seq / 64) * (64 * 128), 128);
+    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kDqRows : p.seq / kDqRows;  // >= 4
+    auto Ks = [&](int s) { return lds + 2 * s * kDqTileElems; };
+    auto Ds = [&](int s) { return lds + (2 * s + 1) * kDqTileElems; };
+    // Block kb into stage kb % kDqStages (blocks past the end: a harmless
+    // reload of the last one into a stage no step reads again).  Four loads a wave.
     auto fetch = [&](int kb) {
-      const int s = kb % kDqStages, at = min(kb, nkb - 1) * kFwdK;
-      kt.load(at, Ks(s));
-      // dS' is read once: non-temporal, so the stream does not evict the K
-      // tiles every query block of this head rereads from L2.
-      dt.load_stream(at, Ds(s));
+      const int s = kb % kDqStages, at = min(kb, nkb - 1) * kDqRows;
+      kt.load<false>(at, Ks(s));
+      dt.load<true>(at, Ds(s));
     };
-    f32x16 dq[4];
+    // Wave (wi, wj) owns d 64 wi .. + 63 and queries 64 wj .. + 63 of the
+    // workgroup's 128 x 128 dQ': 2 + 2 fragments a 16-key slice instead of 4 + 1
+    // for all d of 32 queries, the transposed LDS reads being what the
+    // sweep's LDS traffic is made of.
+    const int wi = wave % 2, wj = wave / 2;
+    f32x16 dq[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
-    fetch(0);
-    th_dev::wait_and_meet<0>();
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) dq[e][f] = f32x16{};
+#pragma unroll
+    for (int kb = 0; kb < kDqAhead; ++kb) fetch(kb);
+    th_dev::wait_and_meet<4 * (kDqAhead - 1)>();  // block 0 has landed
     for (int kb = 0; kb < nkb; ++kb) {
-      fetch(kb + 1);  // into the stage block kb - 1 used
+      // Into the stage block kb - 1 used: every wave finished reading it
+      // before the barrier that ended the previous step.
+      fetch(kb + kDqAhead);
       const int st = kb % kDqStages;
-      // All twenty fragments of the block first (one wave per SIMD: nothing
-      // else would hide an LDS round trip per product), then the products.
-      bf16x8 bs[4], kf[4][4];
+      bf16x8 bs[2][2], kf[2][2];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bs[ks] = frag_tr(Ds(st), 32 * wave, ks);
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int db = 0; db < 4; ++db) kf[ks][db] = frag_tr(Ks(st), 32 * db, ks);
-      }
+        for (int e = 0; e < 2; ++e) {
+          bs[ks][e] = frag_tr(Ds(st), 64 * wj + 32 * e, ks);
+          kf[ks][e] = frag_tr(Ks(st), 64 * wi + 32 * e, ks);
+        }
       __builtin_amdgcn_sched_barrier(kFence);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int db = 0; db < 4; ++db) dq[db] = mfma(kf[ks][db], bs[ks], dq[db]);
-      // Block kb + 1 has landed.
-      th_dev::wait_and_meet<0>();
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int f = 0; f < 2; ++f) dq[e][f] = mfma(kf[ks][e], bs[ks][f], dq[e][f]);
+      // Block kb + 1 has landed; blocks kb + 2 .. kb + kDqAhead stay in flight.
+      th_dev::wait_and_meet<4 * (kDqAhead - 1)>();
     }
     // No load may land in this workgroup's LDS after the sweep.
     th_dev::wait_and_meet<0>();
-    uint16_t* out = p.dq + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(qw + 32 * wave + lr) * p.q_ss;
+    // Lane holds dQ'(d, query) for query 64 wj + 32 f + lr, d = 64 wi + 32 e + 8 g + 4 lh + (0..3).
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int f = 0; f < 2; ++f) {
+      uint16_t* out = p.dq + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(qw + 64 * wj + 32 * f + lr) * p.q_ss;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = 32 * db + 8 * g + 4 * lh;
-        const float sc = p.scale;
-        *reinterpret_cast<u32x2*>(out + d) =
-            u32x2{pack2(dq[db][4 * g] * sc, dq[db][4 * g + 1] * sc), pack2(dq[db][4 * g + 2] * sc, dq[db][4 * g + 3] * sc)};
-      }
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = 64 * wi + 32 * e + 8 * g + 4 * lh;
+          const float sc = p.scale;
+          *reinterpret_cast<u32x2*>(out + d) = u32x2{pack2(dq[e][f][4 * g] * sc, dq[e][f][4 * g + 1] * sc),
+                                                     pack2(dq[e][f][4 * g + 2] * sc, dq[e][f][4 * g + 3] * sc)};
+        }
+    }
   }
 }
 
