@@ -121,8 +121,32 @@ def config2_floor(target, x, g, steps: int = 10, warmup: int = 3):
             entry["parity_rel"] = repr(err)
         out[name] = entry
         del c, ex
+    # A scan through the floor: y = cumsum(x; dims = 1) over the same X, a
+    # workgroup per column (read x, write y: 8 bytes an element).
+    from tempest_hip.floor import FloorGroup
+    sg = FloorGroup("scan", (N, ROWS), reduced=(0,), name="cumsum(x; dims = 1)")
+    sg.value("x", "f32", ROWS * N)
+    sg.value("y", "f32", ROWS * N)
+    sg.output("y", sg.fold("sum", sg.load("x", (1, N)), scan="inclusive").value, (1, N))
+    y = torch.empty_like(x)
+    sl = sg.build({"x": x.data_ptr(), "y": y.data_ptr()})
+    sl()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        sl()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / steps
+    idx = torch.tensor([0, 16384, ROWS - 1], device="cuda")
+    ref = torch.cumsum(x.index_select(0, idx).double(), dim=1)
+    out["cumsum_scan"] = {"us": t * 1e6, "GB/s": 8.0 * ROWS * N / t / 1e9, "plan": sg.source().splitlines()[0][22:],
+                          "parity_rel": float((y.index_select(0, idx).double() - ref).norm() / ref.norm())}
+    del y
     out["note"] = ("generated floor: one reduction group per program (the column's folds in phases, loads kept in "
-                   "registers, dx written once) and the loss's full fold; events bracket both launches")
+                   "registers, dx written once) and the loss's full fold; events bracket both launches; "
+                   "cumsum_scan: a scan group over the same X")
     return out
 
 

@@ -329,11 +329,33 @@ int plan(const th_floor_desc* d, Plan& pl) {
           TH_REQUIRE(d->outputs[o].full == 0 || d->folds[d->terms[t].ref].scan != TH_SCAN_NONE,
                      "th_build_floor: output " + std::to_string(o) + " reads a plain fold's result at a position");
     }
-    // One thread per item, items side by side, each sweeping in order.
-    pl.rows = false;
-    pl.S = 256;
-    pl.L = pl.P = pl.W = 1;
-    pl.qn = pl.count;
+    // Where the memory terms run along the first scanned axis, a workgroup
+    // per item scans its positions in parallel (chunks of 256 lanes, four
+    // positions a lane going forward); else a thread per item, items side by
+    // side, each sweeping in order.
+    int pos_unit = 0, item_unit = 0;
+    const int s0 = pl.swept[0], k0 = pl.kept.empty() ? -1 : pl.kept[0];
+    auto score = [&](const th_affine& a) {
+      if (std::llabs(a.coeff[s0]) == 1 && pl.E[s0] > 1) ++pos_unit;
+      else if (k0 >= 0 && std::llabs(a.coeff[k0]) == 1 && pl.E[k0] > 1) ++item_unit;
+    };
+    for (int t = 0; t < nt; ++t)
+      if (d->terms[t].op == TH_TERM_LOAD && pl.dep[t]) score(d->terms[t].index);
+    for (int o = 0; o < d->n_outputs; ++o)
+      if (d->outputs[o].full) score(d->outputs[o].index);
+    pl.rows = pl.count >= 64 && (pl.kept.empty() || pos_unit > item_unit);
+    if (pl.rows) {
+      pl.S = 1;
+      pl.L = 256;
+      pl.P = 1;
+      pl.W = (!pl.reverse && !pl.gathers && pl.E[s0] % 4 == 0 && pl.count >= 256) ? 4 : 1;
+      pl.vax = pl.W > 1 ? s0 : -1;
+      pl.qn = pl.count / pl.W;
+    } else {
+      pl.S = 256;
+      pl.L = pl.P = pl.W = 1;
+      pl.qn = pl.count;
+    }
   } else if (pl.reduction) {
     for (int f = 0; f < d->n_folds; ++f) pl.phases.push_back(d->folds[f].phase);
     std::sort(pl.phases.begin(), pl.phases.end());
@@ -629,7 +651,8 @@ class Writer {
     if (!pl_.reduction) {
       s << "pointwise, " << pl_.items << " positions, width " << pl_.W;
     } else if (pl_.scan) {
-      s << "scan, " << pl_.items << " items of " << pl_.count << " positions, a thread per item"
+      s << "scan, " << pl_.items << " items of " << pl_.count << " positions, "
+        << (pl_.rows ? "a workgroup per item, width " + std::to_string(pl_.W) : std::string("a thread per item"))
         << (pl_.reverse ? ", reversed" : "");
     } else {
       s << (pl_.rows ? "rows" : "columns") << ", " << pl_.items << " items of " << pl_.count
@@ -645,6 +668,7 @@ class Writer {
   const th_floor_desc* d_;
   std::ostringstream o_;
   int uid_ = 0;
+  bool stat_vec_ = false;  // scan results read per position (the parallel scan)
 
   std::string vtype(int v) const {
     switch (d_->values[v].dtype) {
@@ -711,6 +735,8 @@ class Writer {
         return "(th_splat(" + x + ") + " + flt((float)cv) + " * th_iota())";
       }
       case TH_TERM_STAT: {
+        if (stat_vec_ && d_->folds[m.ref].scan != TH_SCAN_NONE)
+          return "s" + stat_name(m.ref, m.observe);  // this lane's positions
         std::string s = stat_name(m.ref, m.observe);
         return vec ? "th_splat(" + s + ")" : s;
       }
@@ -908,8 +934,10 @@ class Writer {
     o << ind << "}\n";
   }
 
-  // Assign the statistics fold f's merged state gives.
-  void observe(const std::string& ind, int f, const std::vector<std::string>& c) {
+  // Assign the statistics fold f's merged state gives (to `prefix` + name + `suffix`).
+  void observe(const std::string& ind, int f, const std::vector<std::string>& c) { observe_to(ind, f, c, "", ""); }
+  void observe_to(const std::string& ind, int f, const std::vector<std::string>& c, const std::string& prefix,
+                  const std::string& suffix) {
     const int kind = d_->folds[f].kind;
     for (int obs = 0; obs <= TH_OBSERVE_LOGSUMEXP; ++obs) {
       if (!observe_ok(kind, obs)) continue;
@@ -923,7 +951,7 @@ class Writer {
       } else {
         e = c[0];
       }
-      o_ << ind << stat_name(f, obs) << " = " << e << ";\n";
+      o_ << ind << prefix << stat_name(f, obs) << suffix << " = " << e << ";\n";
     }
   }
 
@@ -1148,6 +1176,10 @@ class Writer {
   // result read before its element, an inclusive one's after), then the
   // full outputs; the plain folds' results and the once outputs after.
   void scan(const std::string& name) {
+    if (pl_.rows) {
+      scan_rows(name);
+      return;
+    }
     std::ostringstream& o = o_;
     header(name);
     o << "  const long item = (long)blockIdx.x * " << pl_.S << " + threadIdx.x;\n";
@@ -1204,6 +1236,146 @@ class Writer {
       std::map<int, std::string> names2;
       emit("  ", reach(d_, r2), false, false, names2, nullptr);
       for (int x : once) store("  ", d_->outputs[x], names2.at(d_->outputs[x].term), false);
+    }
+    o << "}\n";
+  }
+
+  // A's state components as lift(y, g): the element's own state.
+  static std::vector<std::string> lift(int kind, const std::string& y, const std::string& g) {
+    switch (kind) {
+      case TH_FOLD_EXP: return {y, g};
+      case TH_FOLD_SQUARE: return {"1.0f", y, "0.0f"};
+      case TH_FOLD_LINEAR: return {y, g};
+      default: return {y};
+    }
+  }
+
+  // The scan of one item by its workgroup: chunks of L x W positions in scan
+  // order; each lane scans its W positions, the lanes' totals are scanned
+  // across the wave by shuffles (the earlier state always first: the linear
+  // fold's combine does not commute) and across waves through LDS, and the
+  // chunk's total is carried into the next.  At each position a fold's result
+  // is what later folds and the full outputs read.
+  void scan_rows(const std::string& name) {
+    std::ostringstream& o = o_;
+    header(name);
+    const int W = pl_.W, L = pl_.L, waves = L / 64;
+    const std::string vt = W > 1 ? "th_v" : "float";
+    o << "  __shared__ float th_lds[" << waves * 3 << "];\n";
+    o << "  const int lane = threadIdx.x, wl = threadIdx.x & 63, wave = threadIdx.x >> 6;\n";
+    o << "  const long item = blockIdx.x;\n";
+    delinearize("  ", "item", pl_.kept);
+    for (int f = 0; f < d_->n_folds; ++f) {
+      const int kind = d_->folds[f].kind;
+      for (int obs = 0; obs <= TH_OBSERVE_LOGSUMEXP; ++obs)
+        if (observe_ok(kind, obs)) {
+          o << "  float " << stat_name(f, obs) << " = 0.0f; (void)" << stat_name(f, obs) << ";\n";
+          o << "  " << vt << " s" << stat_name(f, obs) << "; (void)s" << stat_name(f, obs) << ";\n";
+        }
+      for (int c = 0; c < state_size(kind); ++c)
+        o << "  float c" << f << "_" << c << " = " << identity(kind, c) << ";\n";  // the carry
+    }
+    const int64_t chunk = (int64_t)L * W;
+    o << "  for (long c0 = 0; c0 < " << pl_.count << "L; c0 += " << chunk << "L) {\n";
+    o << "    const long p0 = c0 + (long)lane * " << W << ";\n";
+    o << "    const bool ok = p0 < " << pl_.count << "L;\n";
+    o << "    const long pos = ok ? " << (pl_.reverse ? std::to_string(pl_.count - 1) + "L - p0" : std::string("p0"))
+      << " : 0L;\n";
+    delinearize("    ", "pos", pl_.swept);
+    stat_vec_ = true;
+    std::map<int, std::string> names;
+    const std::string in = "    ";
+    for (int f : pl_.order) {
+      const th_fold& x = d_->folds[f];
+      const int kind = x.kind, K = state_size(kind);
+      std::vector<int> roots{x.body};
+      if (x.weight >= 0) roots.push_back(x.weight);
+      emit(in, reach(d_, roots), W > 1, false, names, nullptr);
+      const std::string y = names.at(x.body);
+      const std::string g = x.weight >= 0 ? names.at(x.weight) : (W > 1 ? "th_splat(1.0f)" : "1.0f");
+      const std::string F = std::to_string(f);
+      // This lane's prefix states over its W positions: l<f>_<j>_<k>.
+      for (int j = 0; j < W; ++j) {
+        const std::string yj = W > 1 ? "(" + y + ")[" + std::to_string(j) + "]" : y;
+        const std::string gj = W > 1 ? "(" + g + ")[" + std::to_string(j) + "]" : g;
+        std::vector<std::string> el = lift(kind, yj, gj), cur;
+        for (int k = 0; k < K; ++k) {
+          const std::string nm = "l" + F + "_" + std::to_string(j) + "_" + std::to_string(k);
+          cur.push_back(nm);
+          if (j == 0) o << in << "float " << nm << " = ok ? " << el[k] << " : " << identity(kind, k) << ";\n";
+          else o << in << "float " << nm << " = l" << F << "_" << j - 1 << "_" << k << ";\n";
+        }
+        if (j > 0) {
+          std::vector<std::string> e2;
+          for (int k = 0; k < K; ++k) {
+            const std::string en = "e" + F + "_" + std::to_string(j) + "_" + std::to_string(k);
+            o << in << "const float " << en << " = " << el[k] << ";\n";
+            e2.push_back(en);
+          }
+          o << in << "if (ok) { " << combine(kind, cur, e2) << " }\n";
+        }
+      }
+      // The lanes' totals scanned: t (inclusive within the wave), then the
+      // exclusive prefix of this lane within the chunk, b.
+      std::vector<std::string> t = comps("t" + F, K), b = comps("b" + F, K), q = comps("q" + F, K), a = comps("a" + F, K);
+      for (int k = 0; k < K; ++k) o << in << "float " << t[k] << " = l" << F << "_" << W - 1 << "_" << k << ";\n";
+      o << in << "#pragma unroll\n" << in << "for (int o = 1; o < 64; o <<= 1) {\n";
+      for (int k = 0; k < K; ++k) o << in << "  float " << q[k] << " = __shfl_up(" << t[k] << ", o, 64);\n";
+      o << in << "  if (wl >= o) { " << combine(kind, q, t) << " ";
+      for (int k = 0; k < K; ++k) o << t[k] << " = " << q[k] << "; ";
+      o << "}\n" << in << "}\n";
+      for (int k = 0; k < K; ++k) o << in << "if (wl == 63) th_lds[wave * " << K << " + " << k << "] = " << t[k] << ";\n";
+      for (int k = 0; k < K; ++k)
+        o << in << "float " << b[k] << " = __shfl_up(" << t[k] << ", 1, 64);\n"
+          << in << "if (wl == 0) " << b[k] << " = " << identity(kind, k) << ";\n";
+      o << in << "__syncthreads();\n";
+      // a: the carry, then every earlier wave's total, then b.
+      for (int k = 0; k < K; ++k) o << in << "float " << a[k] << " = c" << F << "_" << k << ";\n";
+      o << in << "for (int u = 0; u < wave; ++u) {\n";
+      for (int k = 0; k < K; ++k) o << in << "  const float " << q[k] << " = th_lds[u * " << K << " + " << k << "];\n";
+      o << in << "  " << combine(kind, a, q) << "\n" << in << "}\n";
+      o << in << combine(kind, a, b) << "\n";
+      // The chunk's total into the carry (every lane alike).
+      o << in << "for (int u = 0; u < " << waves << "; ++u) {\n";
+      for (int k = 0; k < K; ++k) o << in << "  const float " << q[k] << " = th_lds[u * " << K << " + " << k << "];\n";
+      std::vector<std::string> cc = comps("c" + F, K);
+      o << in << "  " << combine(kind, cc, q) << "\n" << in << "}\n";
+      o << in << "__syncthreads();\n";
+      if (x.scan != TH_SCAN_NONE) {
+        // This lane's results: a then its positions' prefixes (exclusive: the one before).
+        for (int j = 0; j < W; ++j) {
+          std::vector<std::string> r = comps("r" + F + "_" + std::to_string(j), K), lj;
+          for (int k = 0; k < K; ++k) o << in << "float " << r[k] << " = " << a[k] << ";\n";
+          const int upto = x.scan == TH_SCAN_INCLUSIVE ? j : j - 1;
+          if (upto >= 0) {
+            for (int k = 0; k < K; ++k) lj.push_back("l" + F + "_" + std::to_string(upto) + "_" + std::to_string(k));
+            o << in << combine(kind, r, lj) << "\n";
+          }
+          observe_to(in, f, r, "s", W > 1 ? "[" + std::to_string(j) + "]" : "");
+        }
+      }
+    }
+    std::vector<int> full, once, roots;
+    for (int x = 0; x < d_->n_outputs; ++x) (d_->outputs[x].full ? full : once).push_back(x);
+    for (int x : full) out_roots(roots, x);
+    emit(in, reach(d_, roots), W > 1, false, names, nullptr);
+    o << in << "if (ok) {\n";
+    for (int x : full) store(in + "  ", d_->outputs[x], names.at(d_->outputs[x].term), W > 1);
+    o << in << "}\n";
+    stat_vec_ = false;
+    o << "  }\n";
+    // The plain folds' results, and the once outputs (lane 0).
+    for (int f = 0; f < d_->n_folds; ++f)
+      if (d_->folds[f].scan == TH_SCAN_NONE) observe("  ", f, comps("c" + std::to_string(f), state_size(d_->folds[f].kind)));
+    if (!once.empty()) {
+      o << "  if (lane == 0) {\n";
+      for (int k : pl_.swept) o << "    i" << k << " = 0;\n";
+      std::vector<int> r2;
+      for (int x : once) out_roots(r2, x);
+      std::map<int, std::string> names2;
+      emit("    ", reach(d_, r2), false, false, names2, nullptr);
+      for (int x : once) store("    ", d_->outputs[x], names2.at(d_->outputs[x].term), false);
+      o << "  }\n";
     }
     o << "}\n";
   }

@@ -267,3 +267,47 @@ def test_embedding_gather_and_scatter_add_at_size(target):
     want = np.zeros((vocab, d))
     np.add.at(want, tok - 1, dy.reshape(n, d).astype(np.float64))
     assert relative(ts["dE"].cpu().numpy().reshape(vocab, d), want) < TOL
+
+
+@pytest.mark.parametrize("n,m,reverse", [(4096, 37, False), (100000, 1, False), (5003, 6, True), (64, 900, False)])
+def test_parallel_scans(target, n, m, reverse):
+    """Scans along the contiguous axis by a workgroup per item: an inclusive
+    sum, and an exclusive linear recurrence whose offset reads the sum at the
+    same position (h = a h' + x c, from 0)."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor parallel scan", n, m, reverse)
+    rng = np.random.default_rng(n + m)
+    x = rng.standard_normal(n * m).astype(np.float32)
+    a = (0.9 + 0.1 * rng.random(n * m)).astype(np.float32)
+    g = FloorGroup("scan", (n, m), reduced=(0,), reverse=reverse)
+    for k in ("x", "a", "c", "h", "tot"):
+        g.value(k, "f32", n * m if k != "tot" else m)
+    xx, aa = g.load("x", (1, n)), g.load("a", (1, n))
+    c = g.fold("sum", xx, scan="inclusive")
+    h = g.fold("linear", aa, weight=xx * c.value, scan="exclusive", phase=2)
+    tot = g.fold("max", xx, phase=3)  # a plain fold beside the scans
+    g.output("c", c.value, (1, n))
+    g.output("h", h.value, (1, n))
+    g.output("tot", tot.value, (0, 1), full=False)
+    assert "a workgroup per item" in g.source().splitlines()[0]
+    ts = {k: torch.from_numpy(v).cuda() for k, v in (("x", x), ("a", a))}
+    for k in ("c", "h"):
+        ts[k] = torch.zeros(n * m, device="cuda")
+    ts["tot"] = torch.zeros(m, device="cuda")
+    g.build({k: ts[k].data_ptr() for k in g.values})()
+    torch.cuda.synchronize()
+    X, A = x.astype(np.float64).reshape(m, n), a.astype(np.float64).reshape(m, n)
+    if reverse:
+        X, A = X[:, ::-1], A[:, ::-1]
+    C = np.cumsum(X, axis=1)
+    H = np.zeros_like(X)
+    hh = np.zeros(m)
+    for i in range(n):  # exclusive: the state before position i
+        H[:, i] = hh
+        hh = A[:, i] * hh + X[:, i] * C[:, i]
+    if reverse:
+        C, H = C[:, ::-1], H[:, ::-1]
+    tol_c = 1e-5 if n <= 5003 else 1e-4  # fp32 sums of 1e5 terms
+    assert relative(ts["c"].cpu().numpy().reshape(m, n), C) < tol_c
+    assert relative(ts["h"].cpu().numpy().reshape(m, n), H) < tol_c
+    assert np.array_equal(ts["tot"].cpu().numpy(), x.reshape(m, n).max(axis=1))

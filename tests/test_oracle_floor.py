@@ -144,3 +144,27 @@ def test_abi_rejects(break_it, message):
         assert message in str(e)
     else:
         raise AssertionError("accepted")
+
+
+def test_scans_along_the_contiguous_axis_take_a_workgroup_per_item():
+    """A scan whose loads run along its positions plans a parallel scan (four
+    positions a lane going forward, one in reverse); a strided one, a thread
+    per item.  Each plan's kernel compiles."""
+    from tempest_hip.floor import FloorGroup
+
+    def group(n, m, axis, reverse=False):
+        g = FloorGroup("scan", (n, m), reduced=(axis,), reverse=reverse)
+        for k in ("x", "a", "c", "h"):
+            g.value(k, "f32", n * m)
+        x, a = g.load("x", (1, n)), g.load("a", (1, n))
+        c = g.fold("sum", x, scan="inclusive")
+        h = g.fold("linear", a, weight=x * c.value, scan="exclusive", phase=2)
+        g.output("c", c.value, (1, n))
+        g.output("h", h.value, (1, n))
+        return g
+    fwd, rev, col = group(4096, 3, 0), group(1000, 5, 0, reverse=True), group(300, 2000, 1)
+    assert "a workgroup per item, width 4" in fwd.source().splitlines()[0]
+    assert "a workgroup per item, width 1, reversed" in rev.source().splitlines()[0]
+    assert "a thread per item" in col.source().splitlines()[0]
+    for g in (fwd, rev, col):
+        g.compile()
