@@ -271,17 +271,32 @@ enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_
  * (LOGSUMEXP, folds.jl:263). */
 enum { TH_OBSERVE_VALUE = 0, TH_OBSERVE_STATISTIC = 1, TH_OBSERVE_SUM = 2, TH_OBSERVE_LOGSUMEXP = 3 };
 
+/* A Div or Mod atom: coeff * (inner div or mod divisor), inner = constant +
+ * sum over k of inner[k] * i_k, with floor division and a remainder in
+ * 0..divisor-1 (Div and Mod of IR/expressions.jl:24-34). */
+enum { TH_PART_NONE = 0, TH_PART_DIV = 1, TH_PART_MOD = 2 };
+typedef struct th_part {
+  int32_t kind;       /* TH_PART_* */
+  int32_t reserved;
+  int64_t divisor;    /* > 0 */
+  int64_t coeff;
+  int64_t constant;
+  int64_t inner[TH_FLOOR_RANK];
+} th_part;
+
 /* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions,
+ * + the two parts (Div and Mod atoms, unused ones TH_PART_NONE),
  * + gather_coeff * (the value of term `gather`, a load of an integer value)
- * when gather >= 0 (an Indirect atom, IR/expressions.jl).  A gathered
- * address is clamped into its value on the device: an index out of range
- * reads or writes the nearest element instead of faulting. */
+ * when gather >= 0 (an Indirect atom; the atoms of IR/expressions.jl).  A
+ * gathered address is clamped into its value on the device: an index out of
+ * range reads or writes the nearest element instead of faulting. */
 typedef struct th_affine {
   int64_t constant;
   int64_t coeff[TH_FLOOR_RANK];
   int32_t gather;
   int32_t reserved;
   int64_t gather_coeff;
+  th_part part[2];
 } th_affine;
 
 typedef struct th_floor_value {

@@ -107,6 +107,9 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
         for k in range(rank):
             if t["coeffs"][k]:
                 a = a + t["coeffs"][k] * at[k]
+        for kind, inner, dv, cf, c in t.get("parts", ()):  # Div (1) and Mod (2) atoms: floor division
+            e = c + sum(inner[k] * at[k] for k in range(rank) if inner[k])
+            a = a + cf * (np.floor_divide(e, dv) if kind == 1 else np.mod(e, dv))
         if t.get("gather", -1) >= 0:
             # An Indirect atom: the integer a load reads, held inside the value.
             a = a + t["gather_coeff"] * np.asarray(term(t["gather"], at, memo), dtype=np.int64)

@@ -122,16 +122,55 @@ struct Plan {
 bool is_int(int dtype) { return dtype == TH_I32 || dtype == TH_I64; }
 int esize(int dtype) { return dtype == TH_BF16 ? 2 : dtype == TH_I64 ? 8 : 4; }
 
+// A div or mod atom is well formed: a known kind and a positive divisor.
+bool parts_ok(const th_affine& a) {
+  for (const th_part& q : a.part) {
+    if (q.kind == TH_PART_NONE) continue;
+    if ((q.kind != TH_PART_DIV && q.kind != TH_PART_MOD) || q.divisor <= 0) return false;
+  }
+  return true;
+}
+
+int64_t fld(int64_t x, int64_t d) { return x >= 0 ? x / d : -((-x + d - 1) / d); }
+
+// The least and greatest of constant + sum coeff[k] i_k over the domain.
+void span(int64_t constant, const int64_t* coeff, const int64_t* ext, int rank, int64_t& lo, int64_t& hi) {
+  lo = hi = constant;
+  for (int k = 0; k < rank; ++k) {
+    const int64_t c = coeff[k] * (ext[k] - 1);
+    if (c < 0) lo += c; else hi += c;
+  }
+}
+
+// The range of a part's atom (before its coefficient) over the domain.
+void part_span(const th_part& q, const int64_t* ext, int rank, int64_t& lo, int64_t& hi) {
+  span(q.constant, q.inner, ext, rank, lo, hi);
+  if (q.kind == TH_PART_DIV) {
+    lo = fld(lo, q.divisor), hi = fld(hi, q.divisor);
+  } else if (fld(lo, q.divisor) == fld(hi, q.divisor)) {  // no wrap: an interval of remainders
+    lo -= fld(lo, q.divisor) * q.divisor, hi -= fld(hi, q.divisor) * q.divisor;
+  } else {
+    lo = 0, hi = q.divisor - 1;
+  }
+}
+
 bool in_box(const th_affine& a, const int64_t* ext, int rank, int64_t length) {
   if (a.gather >= 0) return true;  // data-dependent: clamped on the device
-  int64_t lo = a.constant, hi = a.constant;
-  for (int k = 0; k < rank; ++k) {
+  for (int k = 0; k < rank; ++k)
     if (ext[k] <= 0) return true;  // an empty domain reads nothing
-    int64_t c = a.coeff[k] * (ext[k] - 1);
-    if (c < 0) lo += c; else hi += c;
+  int64_t lo, hi;
+  span(a.constant, a.coeff, ext, rank, lo, hi);
+  for (const th_part& q : a.part) {
+    if (q.kind == TH_PART_NONE || q.coeff == 0) continue;
+    int64_t plo, phi;
+    part_span(q, ext, rank, plo, phi);
+    if (q.coeff > 0) lo += q.coeff * plo, hi += q.coeff * phi;
+    else lo += q.coeff * phi, hi += q.coeff * plo;
   }
   return lo >= 0 && hi < length;
 }
+
+bool has_parts(const th_affine& a) { return a.part[0].kind != TH_PART_NONE || a.part[1].kind != TH_PART_NONE; }
 
 int validate(const th_floor_desc* d) {
   TH_REQUIRE(d != nullptr, "th_build_floor: null description");
@@ -172,6 +211,7 @@ int validate(const th_floor_desc* d) {
     std::string at = "th_build_floor: term " + std::to_string(t) + ": ";
     TH_REQUIRE(m.op == TH_TERM_LOAD ? gather_ok(m.index, t) : m.index.gather < 0,
                at + "a gathered address adds an earlier load of integers");
+    TH_REQUIRE(parts_ok(m.index), at + "a div or mod atom takes a positive divisor");
     switch (m.op) {
       case TH_TERM_LOAD:
         TH_REQUIRE(m.ref >= 0 && m.ref < d->n_values, at + "load of no value");
@@ -222,6 +262,7 @@ int validate(const th_floor_desc* d) {
       ext[k] = (!x.full && (d->reduced >> k & 1)) ? std::min<int64_t>(d->extents[k], 1) : d->extents[k];
     TH_REQUIRE(in_box(x.index, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
     TH_REQUIRE(gather_ok(x.index, d->n_terms), at + "a gathered address adds a load of integers");
+    TH_REQUIRE(parts_ok(x.index), at + "a div or mod atom takes a positive divisor");
     TH_REQUIRE(!is_int(d->values[x.value].dtype), at + "integer values are only read");
     TH_REQUIRE(x.accumulate == 0 || (x.accumulate == 1 && d->values[x.value].dtype == TH_F32),
                at + "accumulating outputs are fp32");
@@ -279,6 +320,9 @@ int plan(const th_floor_desc* d, Plan& pl) {
 
   for (int t = 0; t < nt; ++t) pl.gathers |= d->terms[t].op == TH_TERM_LOAD && d->terms[t].index.gather >= 0;
   for (int o = 0; o < d->n_outputs; ++o) pl.gathers |= d->outputs[o].index.gather >= 0;
+  // Div and mod atoms break the run of W consecutive positions: width 1, as a gather.
+  for (int t = 0; t < nt; ++t) pl.gathers |= has_parts(d->terms[t].index);
+  for (int o = 0; o < d->n_outputs; ++o) pl.gathers |= has_parts(d->outputs[o].index);
   // Which terms move along the swept positions.
   pl.dep.assign(nt, 0);
   for (int t = 0; t < nt; ++t) {
@@ -288,6 +332,9 @@ int plan(const th_floor_desc* d, Plan& pl) {
         pl.dep[t] = 1;
       } else {
         for (int k : pl.swept) pl.dep[t] |= m.index.coeff[k] != 0;
+        for (const th_part& q : m.index.part)
+          if (q.kind != TH_PART_NONE && q.coeff != 0)
+            for (int k : pl.swept) pl.dep[t] |= q.inner[k] != 0;
         if (m.op == TH_TERM_LOAD && m.index.gather >= 0) pl.dep[t] |= pl.dep[m.index.gather];
       }
     } else if (m.op == TH_TERM_APPLY) {
@@ -448,6 +495,21 @@ std::string affine(const Plan& pl, const th_affine& a) {
   s << "(" << a.constant << "L";
   for (int k = 0; k < pl.rank; ++k)
     if (a.coeff[k] != 0 && pl.E[k] > 1) s << " + " << a.coeff[k] << "L * i" << k;
+  for (const th_part& q : a.part) {
+    if (q.kind == TH_PART_NONE || q.coeff == 0) continue;
+    std::ostringstream in;
+    in << "(" << q.constant << "L";
+    for (int k = 0; k < pl.rank; ++k)
+      if (q.inner[k] != 0 && pl.E[k] > 1) in << " + " << q.inner[k] << "L * i" << k;
+    in << ")";
+    int64_t lo, hi;
+    span(q.constant, q.inner, pl.E, pl.rank, lo, hi);
+    s << " + " << q.coeff << "L * ";
+    if (lo >= 0)  // never negative: C's / and % are the floor division and remainder
+      s << "(" << in.str() << (q.kind == TH_PART_DIV ? " / " : " % ") << q.divisor << "L)";
+    else
+      s << (q.kind == TH_PART_DIV ? "th_fld(" : "th_fmod(") << in.str() << ", " << q.divisor << "L)";
+  }
   s << ")";
   return s.str();
 }
@@ -479,6 +541,9 @@ __device__ __forceinline__ long th_ldi(const int* p, long i) { return (long)p[i]
 __device__ __forceinline__ long th_ldi(const long* p, long i) { return p[i]; }
 // A gathered position, held inside its value (0 .. n - 1).
 __device__ __forceinline__ long th_clampi(long i, long n) { return i < 0 ? 0 : (i >= n ? n - 1 : i); }
+// Floor division by a positive d, and the remainder in 0 .. d - 1 (Div and Mod atoms).
+__device__ __forceinline__ long th_fld(long x, long d) { return x >= 0 ? x / d : -((-x + d - 1) / d); }
+__device__ __forceinline__ long th_fmod(long x, long d) { return x - d * th_fld(x, d); }
 __device__ __forceinline__ void th_add(float* p, long i, float v) { atomicAdd(p + i, v); }
 __device__ __forceinline__ float th_abs(float x) { return fabsf(x); }
 __device__ __forceinline__ float th_abs2(float x) { return x * x; }

@@ -224,12 +224,17 @@ end
 # src/Compiler/codegen/scalar.jl:186-250) and CUDA compiles it (floor_launch,
 # ext/CUDAExt.jl:926-937).  Here the group's terms cross the C ABI as arrays
 # (th_floor_desc) and libtempest_hip writes and compiles the gfx950 kernel.
-# Supported: Var atoms in addresses and one Indirect atom (a gathered index;
-# Div and Mod atoms throw, and the build falls back), the functions of FLOOR_FN,
-# and the folds of FLOOR_FOLD.
+# Supported: Var atoms in addresses, up to two Div or Mod atoms of positions
+# and one Indirect atom (a gathered index; other forms throw and the build
+# falls back), the functions of FLOOR_FN, and the folds of FLOOR_FOLD.
 
 struct FloorValue; dtype::Int32; reserved::Int32; length::Int64; ptr::Ptr{Cvoid}; end
-struct CAffine; constant::Int64; coeff::NTuple{4, Int64}; gather::Int32; reserved::Int32; gather_coeff::Int64; end
+struct CPart; kind::Int32; reserved::Int32; divisor::Int64; coeff::Int64; constant::Int64; inner::NTuple{4, Int64}; end
+struct CAffine
+    constant::Int64; coeff::NTuple{4, Int64}; gather::Int32; reserved::Int32; gather_coeff::Int64
+    part::NTuple{2, CPart}
+end
+const NO_PART = CPart(0, 0, 1, 0, 0, (0, 0, 0, 0))
 struct CTerm; op::Int32; fn::Int32; args::NTuple{3, Int32}; ref::Int32; observe::Int32; lit::Float32; index::CAffine; end
 struct CFold; kind::Int32; phase::Int32; body::Int32; weight::Int32; scan::Int32; reserved::Int32; end
 struct COutput; value::Int32; term::Int32; full::Int32; accumulate::Int32; index::CAffine; end
@@ -262,18 +267,30 @@ end
 
 # `gathered(atom)` adds the load an Indirect atom reads and returns its term number.
 function caffine(e, gathered)
+    IR = Tempest.Compiler.IR
     c = zeros(Int64, 4)
     gather, gc = Int32(-1), 0
+    parts = CPart[]
     for (atom, k) in e.terms
-        if atom isa Tempest.Compiler.IR.Var
+        if atom isa IR.Var
             c[atom.n] += k
-        elseif atom isa Tempest.Compiler.IR.Indirect && gather < 0
+        elseif atom isa IR.Indirect && gather < 0
             gather, gc = gathered(atom), k
+        elseif (atom isa IR.Div || atom isa IR.Mod) && length(parts) < 2
+            inner = zeros(Int64, 4)
+            for (a, j) in atom.e.terms
+                a isa IR.Var || throw(ArgumentError("floor div / mod atoms take positions"))
+                inner[a.n] += j
+            end
+            push!(parts, CPart(atom isa IR.Div ? 1 : 2, 0, atom.d, k, atom.e.constant, Tuple(inner)))
         else
-            throw(ArgumentError("floor addresses take positions and one gathered index"))
+            throw(ArgumentError("floor addresses take positions, two div / mod atoms and one gathered index"))
         end
     end
-    CAffine(e.constant, Tuple(c), gather, 0, gc)
+    while length(parts) < 2
+        push!(parts, NO_PART)
+    end
+    CAffine(e.constant, Tuple(c), gather, 0, gc, (parts[1], parts[2]))
 end
 
 # The group as th_floor_desc arrays; `slots` numbers its values, `buffers` their storage.
@@ -282,7 +299,7 @@ function floor_descriptor(graph, g, slots, buffers)
     terms, index = CTerm[], IdDict{Any, Int32}()
     folds = [r for r in g.reductions]
     fold_no = Dict(r => Int32(i - 1) for (i, r) in enumerate(folds))
-    z = CAffine(0, (0, 0, 0, 0), -1, 0, 0)
+    z = CAffine(0, (0, 0, 0, 0), -1, 0, 0, (NO_PART, NO_PART))
     # An Indirect atom reads value `a.value` at `a.index`: a load term of its own.
     gathered(a) = add!(C.IR.Load(a.value, a.index))
     function add!(t)

@@ -64,9 +64,14 @@ class DeltaNetDesc(ctypes.Structure):
 FLOOR_RANK = 4
 
 
+class Part(ctypes.Structure):
+    _fields_ = [("kind", c_i32), ("reserved", c_i32), ("divisor", c_i64), ("coeff", c_i64), ("constant", c_i64),
+                ("inner", c_i64 * FLOOR_RANK)]
+
+
 class Affine(ctypes.Structure):
     _fields_ = [("constant", c_i64), ("coeff", c_i64 * FLOOR_RANK), ("gather", c_i32), ("reserved", c_i32),
-                ("gather_coeff", c_i64)]
+                ("gather_coeff", c_i64), ("part", Part * 2)]
 
 
 class FloorValue(ctypes.Structure):

@@ -106,12 +106,41 @@ class Fold:
         return self._stat("statistic")
 
 
-def _affine(coeffs: Sequence[int] | None, constant: int, rank: int, gather=None, gather_coeff: int = 1) -> tuple:
+PART = {"div": 1, "mod": 2}
+
+
+def _affine(coeffs: Sequence[int] | None, constant: int, rank: int, gather=None, gather_coeff: int = 1,
+            parts=()) -> tuple:
+    """(constant, coefficients, gather term, gather coefficient, div/mod parts).
+    A part is ("div" | "mod", inner coefficients, divisor, coefficient[, inner
+    constant]): coefficient * fld or mod(inner constant + sum inner[k] i_k,
+    divisor), the Div and Mod atoms; at most two."""
     c = list(coeffs or ())
     if len(c) > rank:
         raise ValueError(f"{len(c)} coefficients for a rank-{rank} domain")
+    if len(parts) > 2:
+        raise ValueError("at most two div / mod atoms an address")
     g = -1 if gather is None else gather.index
-    return (int(constant), tuple(int(x) for x in c) + (0,) * (RANK - len(c)), g, int(gather_coeff))
+    ps = []
+    for part in parts:
+        kind, inner, dv, cf = part[:4]
+        inner = list(inner)
+        if len(inner) > rank:
+            raise ValueError(f"{len(inner)} inner coefficients for a rank-{rank} domain")
+        ps.append((PART[kind], tuple(int(x) for x in inner) + (0,) * (RANK - len(inner)), int(dv), int(cf),
+                   int(part[4]) if len(part) > 4 else 0))
+    ps = tuple(ps)
+    return (int(constant), tuple(int(x) for x in c) + (0,) * (RANK - len(c)), g, int(gather_coeff), ps)
+
+
+def _fill(dst, aff) -> None:
+    c0, cs, gt, gc, ps = aff
+    dst.constant, dst.gather, dst.gather_coeff = c0, gt, gc
+    dst.coeff[:] = list(cs)
+    for j, (kind, inner, dv, cf, c) in enumerate(ps):
+        q = dst.part[j]
+        q.kind, q.divisor, q.coeff, q.constant = kind, dv, cf, c
+        q.inner[:] = list(inner)
 
 
 @dataclass
@@ -146,7 +175,7 @@ class FloorGroup:
         return name
 
     def _term(self, op: str, fn: int = 0, args=(), ref: int = 0, observe: int = 0, lit: float = 0.0,
-              affine=(0, (0,) * RANK, -1, 0)) -> Term:
+              affine=(0, (0,) * RANK, -1, 0, ())) -> Term:
         self.terms.append((TERM[op], fn, tuple(args) + (0,) * (3 - len(args)), ref, observe, float(lit), affine))
         return Term(self, len(self.terms) - 1)
 
@@ -158,18 +187,20 @@ class FloorGroup:
         return self.lit(float(x))
 
     def load(self, name: str, coeffs: Sequence[int] | None = None, constant: int = 0, gather: Term | None = None,
-             gather_coeff: int = 1) -> Term:
-        """Element ``constant + sum(coeffs[k] * i_k) (+ gather_coeff * gather)`` of
-        value ``name``; ``gather`` is a load of integers (an Indirect atom)."""
+             gather_coeff: int = 1, parts=()) -> Term:
+        """Element ``constant + sum(coeffs[k] * i_k) (+ gather_coeff * gather)
+        (+ each part: coefficient * fld|mod(inner affine, divisor))`` of value
+        ``name``; ``gather`` is a load of integers (an Indirect atom)."""
         ref = list(self.values).index(name)
-        return self._term("load", ref=ref, affine=_affine(coeffs, constant, len(self.extents), gather, gather_coeff))
+        return self._term("load", ref=ref,
+                          affine=_affine(coeffs, constant, len(self.extents), gather, gather_coeff, parts))
 
     def lit(self, x: float) -> Term:
         return self._term("lit", lit=x)
 
-    def index(self, coeffs: Sequence[int], constant: int = 0) -> Term:
-        """The number ``constant + sum(coeffs[k] * i_k)`` (Ix)."""
-        return self._term("index", affine=_affine(coeffs, constant, len(self.extents)))
+    def index(self, coeffs: Sequence[int], constant: int = 0, parts=()) -> Term:
+        """The number ``constant + sum(coeffs[k] * i_k)`` (+ div / mod parts) (Ix)."""
+        return self._term("index", affine=_affine(coeffs, constant, len(self.extents), parts=parts))
 
     def apply(self, fn: str, *args) -> Term:
         if fn not in FN:
@@ -198,12 +229,13 @@ class FloorGroup:
 
     def output(self, name: str, term, coeffs: Sequence[int] | None = None, constant: int = 0,
                full: bool = True, gather: Term | None = None, gather_coeff: int = 1,
-               accumulate: bool = False) -> None:
+               accumulate: bool = False, parts=()) -> None:
         """Write ``term`` at the address (every position, or once per item);
         ``accumulate`` adds it instead, atomically (a fold by key)."""
         v = list(self.values).index(name)
         self.outputs.append((v, self._as_term(term).index, int(bool(full)),
-                             _affine(coeffs, constant, len(self.extents), gather, gather_coeff), int(bool(accumulate))))
+                             _affine(coeffs, constant, len(self.extents), gather, gather_coeff, parts),
+                             int(bool(accumulate))))
 
     # -- the ABI ---------------------------------------------------------------------
 
@@ -213,21 +245,19 @@ class FloorGroup:
         for k, ((dt, n), p) in enumerate(zip(self.values.values(), ptrs)):
             values[k].dtype, values[k].length, values[k].ptr = DTYPE[dt], n, p
         terms = (TermStruct * max(nt, 1))()
-        for k, (op, fn, args, ref, obs, lit, (c0, cs, gt, gc)) in enumerate(self.terms):
+        for k, (op, fn, args, ref, obs, lit, aff) in enumerate(self.terms):
             t = terms[k]
             t.op, t.fn, t.ref, t.observe, t.lit = op, fn, ref, obs, lit
             t.args[:] = list(args)
-            t.index.constant, t.index.gather, t.index.gather_coeff = c0, gt, gc
-            t.index.coeff[:] = list(cs)
+            _fill(t.index, aff)
         folds = (FoldStruct * max(nf, 1))()
         for k, (kind, phase, body, weight, scan) in enumerate(self.folds):
             folds[k].kind, folds[k].phase, folds[k].body, folds[k].weight = kind, phase, body, weight
             folds[k].scan = scan
         outs = (OutputStruct * max(no, 1))()
-        for k, (v, term, full, (c0, cs, gt, gc), acc) in enumerate(self.outputs):
+        for k, (v, term, full, aff, acc) in enumerate(self.outputs):
             outs[k].value, outs[k].term, outs[k].full, outs[k].accumulate = v, term, full, acc
-            outs[k].index.constant, outs[k].index.gather, outs[k].index.gather_coeff = c0, gt, gc
-            outs[k].index.coeff[:] = list(cs)
+            _fill(outs[k].index, aff)
         d = FloorDesc()
         d.kind, d.rank = GROUP[self.kind], len(self.extents)
         d.extents[:] = list(self.extents) + [1] * (RANK - len(self.extents))
@@ -288,11 +318,12 @@ class FloorGroup:
             "terms": [{"op": inv_term[op], "fn": inv_fn.get(fn) if op == TERM["apply"] else None,
                        "args": list(args[:ARITY[inv_fn[fn]]]) if op == TERM["apply"] else [],
                        "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1]),
-                       "gather": aff[2], "gather_coeff": aff[3]}
+                       "gather": aff[2], "gather_coeff": aff[3], "parts": list(aff[4])}
                       for op, fn, args, ref, obs, lit, aff in self.terms],
             "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w, "scan": inv_scan[sc]}
                       for k, p, b, w, sc in self.folds],
             "outputs": [{"value": list(self.values)[v], "term": t, "full": bool(f), "constant": aff[0],
-                         "coeffs": list(aff[1]), "gather": aff[2], "gather_coeff": aff[3], "accumulate": bool(acc)}
+                         "coeffs": list(aff[1]), "gather": aff[2], "gather_coeff": aff[3], "parts": list(aff[4]),
+                         "accumulate": bool(acc)}
                         for v, t, f, aff, acc in self.outputs],
         }

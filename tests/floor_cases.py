@@ -378,6 +378,57 @@ def permutation():
                 lambda v: {"y": v["x"].reshape(4, 3, 5, order="F").transpose(1, 0, 2).ravel(order="F")})
 
 
+def permutation_and_reshape():
+    """reshape(permutedims(x, (2, 1, 3)), 3, 20) of a 4 x 3 x 5 array, then
+    sum(abs2, y .* w): y[a, b] = x[b mod 4, a, b div 4], an address with a Div
+    and a Mod atom of the position b; and the way back, z[(b mod 4) + 4a +
+    12 (b div 4)] = y[a, b], the same atoms in a store (z == x)."""
+    x, w = data(4, 3, 5), data(3, 20, scale=0.7)
+    parts = [("mod", (0, 1), 4, 1), ("div", (0, 1), 4, 12)]
+    g1 = FloorGroup("pointwise", (3, 20), name="reshape(permutedims(x, (2, 1, 3)), 3, 20)")
+    g1.value("x", "f32", 60)
+    g1.value("y", "f32", 60)
+    g1.output("y", g1.load("x", (4, 0), parts=parts), (1, 3))
+    g2 = FloorGroup("reduction", (3, 20), reduced=(0, 1), name="sum(abs2, y .* w)")
+    for v in ("x", "w"):
+        g2.value(v, "f32", 60)
+    g2.value("loss", "f32", 1)
+    g2.output("loss", g2.fold("sum", g2.apply("abs2", g2.load("x", (4, 0), parts=parts) * g2.load("w", (1, 3)))).value,
+              full=False)
+    g3 = FloorGroup("pointwise", (3, 20), name="the way back")
+    g3.value("y", "f32", 60)
+    g3.value("z", "f32", 60)
+    g3.output("z", g3.load("y", (1, 3)), (4, 0), parts=parts)
+
+    def closed(v):
+        y = v["x"].reshape(4, 3, 5, order="F").transpose(1, 0, 2).reshape(3, 20, order="F")
+        return {"y": y.ravel(order="F"), "loss": [np.sum((y * v["w"].reshape(3, 20, order="F")) ** 2)],
+                "z": v["x"]}
+    return Case("permutation and reshape (Div and Mod atoms)", [g1, g2, g3], {"x": F(x), "w": F(w)},
+                {"y": 60, "loss": 1, "z": 60}, ["y", "loss", "z"], closed)
+
+
+def permute_reshape_and_roll():
+    """reshape(permutedims(x, (2, 1)), 2, 30) of a 6 x 10 array: y[a, b] =
+    x[L mod 10, L div 10] ... read as x[L div 10 + 6 (L mod 10)] with L = a +
+    2b, atoms of two positions; and a roll, r[a, b] = x[mod(a + 2b - 7, 60)],
+    a Mod atom whose expression goes negative (floor division, remainder in
+    0..59)."""
+    x = data(6, 10)
+    g = FloorGroup("pointwise", (2, 30), name="reshape(permutedims(x, (2, 1)), 2, 30) and a roll")
+    g.value("x", "f32", 60)
+    g.value("y", "f32", 60)
+    g.value("r", "f32", 60)
+    g.output("y", g.load("x", (0, 0), parts=[("div", (1, 2), 10, 1), ("mod", (1, 2), 10, 6)]), (1, 2))
+    g.output("r", g.load("x", (0, 0), parts=[("mod", (1, 2), 60, 1, -7)]), (1, 2))
+
+    def closed(v):
+        y = v["x"].reshape(6, 10, order="F").T.reshape(2, 30, order="F")
+        return {"y": y.ravel(order="F"), "r": np.roll(v["x"], 7)}
+    return Case("permute, reshape and roll (Div and Mod of two positions)", [g], {"x": F(x)},
+                {"y": 60, "r": 60}, ["y", "r"], closed)
+
+
 def bias_tanh_bf16(n=64, m=40):
     """y = tanh.(x .+ b) with b a column broadcast along the rows, y stored as bfloat16."""
     x, b = data(n, m), data(n, scale=0.3)
@@ -679,7 +730,8 @@ def scatter_add_gradient():
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
-         map_over_two_arrays, permutation, bias_tanh_bf16, index_scaled, kat_sum_abs2,
+         map_over_two_arrays, permutation, permutation_and_reshape, permute_reshape_and_roll,
+         bias_tanh_bf16, index_scaled, kat_sum_abs2,
          cumulative_sums, cumulative_products_through_a_zero, running_maxima_and_minima, linear_recurrence,
          running_average, reverse_exclusive_sums, running_logsumexp_and_mean,
          gather_by_a_list, gather_by_an_int32_matrix, gather_rows_by_an_int64_matrix,

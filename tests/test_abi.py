@@ -82,7 +82,8 @@ def test_floor_structures_match_the_header(tmp_path):
     lays out include/tempest_hip.h, against the ctypes mirror."""
     import subprocess
     import tempest_hip._lib as L
-    members = {"th_affine": (L.Affine, ["constant", "coeff", "gather", "gather_coeff"]),
+    members = {"th_part": (L.Part, ["kind", "divisor", "coeff", "constant", "inner"]),
+               "th_affine": (L.Affine, ["constant", "coeff", "gather", "gather_coeff", "part"]),
                "th_floor_value": (L.FloorValue, ["dtype", "length", "ptr"]),
                "th_term": (L.TermStruct, ["op", "fn", "args", "ref", "observe", "lit", "index"]),
                "th_fold": (L.FoldStruct, ["kind", "phase", "body", "weight", "scan"]),

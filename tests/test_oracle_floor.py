@@ -120,6 +120,9 @@ def test_plans_take_each_mapping():
     ("later_stat", "own or a later phase"),
     ("pointwise_fold", "only a reduction group folds"),
     ("write_outside", "writes outside"),
+    ("zero_divisor", "positive divisor"),
+    ("part_outside", "outside its value"),
+    ("part_store_outside", "writes outside"),
 ])
 def test_abi_rejects(break_it, message):
     from tempest_hip import HIPError
@@ -137,6 +140,13 @@ def test_abi_rejects(break_it, message):
             g.output("r", g.fold("sum", x * f2.value, phase=2).value, (0, 1), full=False)
         elif break_it == "pointwise_fold":
             FloorGroup("pointwise", (8,)).fold("sum", 1.0)
+        elif break_it == "zero_divisor":
+            g.output("r", g.fold("sum", g.load("x", (1, 0), parts=[("div", (0, 1), 0, 8)])).value, (0, 1), full=False)
+        elif break_it == "part_outside":  # i1 div 2 reaches 2: 7 + 9 * 2 + 24 = 49 > 47
+            g.output("r", g.fold("sum", g.load("x", (1, 0), 24, parts=[("div", (0, 1), 2, 9)])).value, (0, 1),
+                     full=False)
+        elif break_it == "part_store_outside":  # i1 mod 4 reaches 3: 3 * 2 = 6 > 5
+            g.output("r", g.fold("sum", x).value, (0, 0), full=False, parts=[("mod", (0, 1), 4, 2)])
         else:
             g.output("r", g.fold("sum", x).value, (0, 2), full=False)
         g.source()
