@@ -178,3 +178,62 @@ def test_scans_along_the_contiguous_axis_take_a_workgroup_per_item():
     assert "a thread per item" in col.source().splitlines()[0]
     for g in (fwd, rev, col):
         g.compile()
+
+
+def _part_address_range(extents, coeffs, constant, parts):
+    """The least and greatest address over the domain, by enumeration."""
+    at = np.meshgrid(*[np.arange(e) for e in extents], indexing="ij")
+    a = constant + sum(c * at[k] for k, c in enumerate(coeffs))
+    for kind, inner, dv, cf, *c0 in parts:
+        e = (c0[0] if c0 else 0) + sum(c * at[k] for k, c in enumerate(inner))
+        a = a + cf * (np.floor_divide(e, dv) if kind == "div" else np.mod(e, dv))
+    return int(np.min(a)), int(np.max(a))
+
+
+def _accepts(extents, coeffs, constant, parts, length):
+    from tempest_hip import HIPError
+    from tempest_hip.floor import FloorGroup
+    g = FloorGroup("pointwise", extents)
+    g.value("x", "f32", length)
+    g.value("y", "f32", int(np.prod(extents)))
+    g.output("y", g.load("x", coeffs, constant, parts=parts), [1, extents[0]][:len(extents)])
+    try:
+        g.source()
+    except HIPError as e:
+        assert "outside its value" in str(e)
+        return False
+    return True
+
+
+@pytest.mark.parametrize("parts,constant", [
+    ([("mod", (1,), 20, 1, 10)], 0),        # 10..13, no wrap
+    ([("mod", (1,), 20, 1, -8)], 0),        # -8..-5 mod 20 = 12..15
+    ([("div", (1,), 4, -3, -5)], 0),        # fld(-5..-2, 4) = -2..-1, times -3: 3..6
+    ([("div", (1, 4), 3, 2), ("mod", (1, 4), 3, 1)], 1),
+])
+def test_div_mod_bounds_are_exact_where_the_steps_are_unit(parts, constant):
+    """An address of div/mod atoms is accepted exactly when its enumerated
+    range lies in the value: at the smallest length that holds it, and not one
+    element shorter."""
+    extents = (4, 3)
+    lo, hi = _part_address_range(extents, (0, 0), constant, parts)
+    assert lo >= 0
+    assert _accepts(extents, (0, 0), constant, parts, hi + 1)
+    assert not _accepts(extents, (0, 0), constant, parts, hi)
+
+
+def test_div_mod_bounds_are_sound_on_random_atoms():
+    """Whatever the atoms, an accepted address never leaves its value."""
+    rng = np.random.default_rng(11)
+    for _ in range(300):
+        extents = (int(rng.integers(1, 6)), int(rng.integers(1, 6)))
+        parts = []
+        for _ in range(int(rng.integers(1, 3))):
+            parts.append((["div", "mod"][rng.integers(2)], tuple(int(v) for v in rng.integers(-4, 5, 2)),
+                          int(rng.integers(1, 9)), int(rng.integers(-3, 4)), int(rng.integers(-10, 10))))
+        coeffs = tuple(int(v) for v in rng.integers(0, 3, 2))
+        lo, hi = _part_address_range(extents, coeffs, 0, parts)
+        constant = max(0, -lo)
+        length = int(rng.integers(max(1, hi + constant - 2), hi + constant + 3))
+        if _accepts(extents, coeffs, constant, parts, length):
+            assert lo + constant >= 0 and hi + constant < length, (extents, coeffs, constant, parts, length)
