@@ -248,7 +248,9 @@ enum {
   TH_FN_EXP, TH_FN_LOG, TH_FN_TANH, TH_FN_SIN, TH_FN_COS, TH_FN_LOG1P, TH_FN_EXPM1, TH_FN_POW,
   TH_FN_MAX, TH_FN_MIN, TH_FN_LT, TH_FN_LE, TH_FN_GT, TH_FN_GE, TH_FN_EQ, TH_FN_NE,
   TH_FN_IFELSE, TH_FN_ROUND, TH_FN_FLOOR, TH_FN_CEIL, TH_FN_SIGN, TH_FN_CLAMP, TH_FN_FMA,
-  TH_FN_INV, TH_FN_COUNT
+  TH_FN_INV,
+  TH_FN_BFLOAT16, /* x rounded to bfloat16 (nearest, ties to even) and widened back: Cast{BFloat16} */
+  TH_FN_COUNT
 };
 
 /* Folds (src/Compiler/IR/folds.jl:66-309), accumulating in fp32:

@@ -36,6 +36,7 @@ _UNARY = {
     "neg": np.negative, "abs": np.abs, "abs2": np.square, "sqrt": np.sqrt, "exp": np.exp, "log": np.log,
     "tanh": np.tanh, "sin": np.sin, "cos": np.cos, "log1p": np.log1p, "expm1": np.expm1,
     "round": np.rint, "floor": np.floor, "ceil": np.ceil, "sign": np.sign, "inv": lambda x: 1.0 / x,
+    "bfloat16": lambda x: bf16_round(np.asarray(x, dtype=np.float32)).astype(np.float64),
 }
 _BINARY = {
     "+": np.add, "-": np.subtract, "*": np.multiply, "/": np.divide, "^": np.power,

@@ -69,7 +69,7 @@ const char* fn_name(int fn) {
       "", "", "", "", "", "th_abs", "th_abs2", "th_sqrt", "th_exp", "th_log", "th_tanh", "th_sin",
       "th_cos", "th_log1p", "th_expm1", "th_pow", "th_max", "th_min", "th_lt", "th_le", "th_gt",
       "th_ge", "th_eq", "th_ne", "th_ifelse", "th_round", "th_floor", "th_ceil", "th_sign",
-      "th_clamp", "th_fma", "th_inv"};
+      "th_clamp", "th_fma", "th_inv", "th_rbf"};
   return names[fn];
 }
 
@@ -172,6 +172,8 @@ bool in_box(const th_affine& a, const int64_t* ext, int rank, int64_t length) {
 
 bool has_parts(const th_affine& a) { return a.part[0].kind != TH_PART_NONE || a.part[1].kind != TH_PART_NONE; }
 
+std::vector<char> reach(const th_floor_desc* d, const std::vector<int>& roots);
+
 int validate(const th_floor_desc* d) {
   TH_REQUIRE(d != nullptr, "th_build_floor: null description");
   TH_REQUIRE(d->kind == TH_GROUP_POINTWISE || d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN,
@@ -257,15 +259,42 @@ int validate(const th_floor_desc* d) {
     TH_REQUIRE(x.term >= 0 && x.term < d->n_terms, at + "no term");
     TH_REQUIRE(x.full == 0 || x.full == 1, at + "full is 0 or 1");
     TH_REQUIRE(x.full == 1 || d->kind != TH_GROUP_POINTWISE, at + "a pointwise group writes every position");
+    // Once outputs are written with the folded positions at zero, also when
+    // the folded axes are empty.
     int64_t ext[kRank];
-    for (int k = 0; k < d->rank; ++k)
-      ext[k] = (!x.full && (d->reduced >> k & 1)) ? std::min<int64_t>(d->extents[k], 1) : d->extents[k];
+    for (int k = 0; k < d->rank; ++k) ext[k] = (!x.full && (d->reduced >> k & 1)) ? 1 : d->extents[k];
     TH_REQUIRE(in_box(x.index, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
     TH_REQUIRE(gather_ok(x.index, d->n_terms), at + "a gathered address adds a load of integers");
     TH_REQUIRE(parts_ok(x.index), at + "a div or mod atom takes a positive divisor");
     TH_REQUIRE(!is_int(d->values[x.value].dtype), at + "integer values are only read");
     TH_REQUIRE(x.accumulate == 0 || (x.accumulate == 1 && d->values[x.value].dtype == TH_F32),
                at + "accumulating outputs are fp32");
+  }
+  if (d->kind != TH_GROUP_POINTWISE) {
+    // Loads evaluated outside the sweep: those whose address does not move
+    // along the folded axes (hoisted, read by every item even when the folded
+    // positions are empty) and those the once outputs read (with the folded
+    // positions at zero).
+    int64_t at0[kRank];
+    for (int k = 0; k < d->rank; ++k) at0[k] = (d->reduced >> k & 1) ? 1 : d->extents[k];
+    std::vector<int> roots;
+    for (int o = 0; o < d->n_outputs; ++o)
+      if (!d->outputs[o].full) roots.push_back(d->outputs[o].term);
+    const std::vector<char> once = reach(d, roots);
+    for (int t = 0; t < d->n_terms; ++t) {
+      const th_term& m = d->terms[t];
+      if (m.op != TH_TERM_LOAD) continue;
+      bool moves = false;
+      for (int k = 0; k < d->rank; ++k) {
+        if (!(d->reduced >> k & 1)) continue;
+        moves |= m.index.coeff[k] != 0;
+        for (const th_part& q : m.index.part) moves |= q.kind != TH_PART_NONE && q.coeff != 0 && q.inner[k] != 0;
+      }
+      if (once[t] || !moves)
+        TH_REQUIRE(in_box(m.index, at0, d->rank, d->values[m.ref].length),
+                   "th_build_floor: term " + std::to_string(t) +
+                       ": load outside its value where it is read with the folded positions at zero");
+    }
   }
   return TH_OK;
 }
@@ -581,6 +610,8 @@ __device__ __forceinline__ float th_sign(float x) { return x > 0.0f ? 1.0f : (x 
 __device__ __forceinline__ float th_clamp(float x, float lo, float hi) { return x > hi ? hi : (x < lo ? lo : x); }
 __device__ __forceinline__ float th_fma(float a, float b, float c) { return fmaf(a, b, c); }
 __device__ __forceinline__ float th_inv(float x) { return 1.0f / x; }
+// Cast{BFloat16}: rounded to bfloat16, then widened back to fp32.
+__device__ __forceinline__ float th_rbf(float x) { return th_bf(th_tobf(x)); }
 // lse_shift (src/Compiler/IR/folds.jl:194): the maximum when finite, else 0.
 __device__ __forceinline__ float th_shift(float m) { return __builtin_isfinite(m) ? m : 0.0f; }
 // Relative{Exponential}: state (m, s), s the weighted sum of exp(y - shift(m)).
@@ -658,7 +689,7 @@ template <class T> __device__ __forceinline__ void th_sts4(T p, long i, long s, 
   return (th_v){f(x[0], y[0], z[0]), f(x[1], y[1], z[1]), f(x[2], y[2], z[2]), f(x[3], y[3], z[3])}; }
 TH_V1(th_abs) TH_V1(th_abs2) TH_V1(th_sqrt) TH_V1(th_exp) TH_V1(th_log) TH_V1(th_tanh) TH_V1(th_sin)
 TH_V1(th_cos) TH_V1(th_log1p) TH_V1(th_expm1) TH_V1(th_round) TH_V1(th_floor) TH_V1(th_ceil)
-TH_V1(th_sign) TH_V1(th_inv)
+TH_V1(th_sign) TH_V1(th_inv) TH_V1(th_rbf)
 TH_V2(th_pow) TH_V2(th_max) TH_V2(th_min) TH_V2(th_lt) TH_V2(th_le) TH_V2(th_gt) TH_V2(th_ge)
 TH_V2(th_eq) TH_V2(th_ne)
 TH_V3(th_ifelse) TH_V3(th_clamp) TH_V3(th_fma)
@@ -1163,7 +1194,9 @@ class Writer {
     o << "  (void)part;\n";
     o << "  const long item = blk * " << pl_.S << "L + sidx;\n";
     o << "  const bool live = item < " << pl_.items << "L;\n  (void)live;\n";
-    delinearize("  ", "item", pl_.kept);
+    // A thread past the last item takes item 0's positions: terms hoisted out
+    // of the sweep are evaluated by every thread, and must stay in bounds.
+    delinearize("  ", pl_.items % pl_.S ? "(live ? item : 0L)" : "item", pl_.kept);
     for (int f = 0; f < d_->n_folds; ++f)
       for (int obs = 0; obs <= TH_OBSERVE_LOGSUMEXP; ++obs)
         if (observe_ok(d_->folds[f].kind, obs)) o << "  float " << stat_name(f, obs) << " = 0.0f; (void)" << stat_name(f, obs) << ";\n";

@@ -247,7 +247,8 @@ end
 const FLOOR_FN = IdDict{Any, Int32}(+ => 0, - => 1, * => 2, / => 3, abs => 5, abs2 => 6, sqrt => 7, exp => 8,
     log => 9, tanh => 10, sin => 11, cos => 12, log1p => 13, expm1 => 14, (^) => 15, max => 16, min => 17,
     (<) => 18, (<=) => 19, (>) => 20, (>=) => 21, (==) => 22, (!=) => 23, ifelse => 24, round => 25,
-    floor => 26, ceil => 27, sign => 28, clamp => 29, fma => 30, inv => 31)
+    floor => 26, ceil => 27, sign => 28, clamp => 29, fma => 30, inv => 31,
+    Tempest.Compiler.IR.Cast{Tempest.BFloat16}() => 32)
 
 # A fold value's (kind, observe): SumFold, MaxFold, MinFold, ProdFold; the
 # exponential and square laws with their Statistic / Sum(1) / LOGSUMEXP observes.
@@ -335,8 +336,17 @@ function floor_descriptor(graph, g, slots, buffers)
                        address(buffers[i])) for (i, v) in enumerate(slots)]
     ext = ntuple(k -> k <= length(g.domain) ? Int64(g.domain[k]) : 1, 4)
     reduced = UInt32(sum((1 << (k - 1) for k in C.primary_axes(graph, g)); init = 0))
-    kind = isempty(folds) ? 0 : g.kind isa C.ScanKind ? 2 : 1
-    (vals, terms, cfolds, outs, ext, reduced, kind)
+    (vals, terms, cfolds, outs, ext, reduced, floor_kind(g.kind))
+end
+
+# The group kinds the generated floor takes, by name; any other kind throws,
+# so that the build falls back to its next option instead of dropping state.
+function floor_kind(kind)
+    C = Tempest.Compiler
+    kind isa C.PointwiseKind && return Int32(0)
+    kind isa C.ReductionKind && return Int32(1)
+    kind isa C.ScanKind && return Int32(2)
+    throw(ArgumentError("the generated floor takes pointwise, reduction and scan groups, not $(typeof(kind))"))
 end
 
 function build_floor(target::HIPTarget, p, g, buffers)

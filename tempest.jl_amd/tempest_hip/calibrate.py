@@ -48,12 +48,15 @@ TIMING_BASIS = 2.0  # the reference's definition of a launch's time (record.jl:1
 MEMORY_COLUMNS = (16, 4096, 65536, 262144)
 APPLIED_SHAPE = (4096, 512)
 APPLIED_TIMES = 8
-# (name in the rates file, floor function, arity); identity and the Float32
-# cast apply nothing on fp32 values.
-APPLIED = [("exp", "exp", 1), ("log", "log", 1), ("tanh", "tanh", 1), ("sqrt", "sqrt", 1), ("sin", "sin", 1),
-           ("cos", "cos", 1), ("abs", "abs", 1), ("abs2", "abs2", 1), ("inv", "inv", 1), ("*", "*", 2),
-           ("+", "+", 2), ("-", "-", 2), ("/", "/", 2), ("^", "^", 2), ("max", "max", 2), ("min", "min", 2),
-           ("identity", None, 1), ("Float32", None, 1)]
+# (name in the rates file, how one application is written), as the
+# reference's apply_chain (src/Compiler/cover/calibrate.jl:236-239) applies
+# each: a unary function to y; a binary one to y and the constant 1.5; ^ as
+# y^3 (Julia's literal power, two products); a cast as the cast of y plus 1.5.
+APPLIED = [(name, (lambda g, y, f=name: g.apply(f, y))) for name in
+           ("exp", "log", "tanh", "sqrt", "sin", "cos", "abs", "abs2", "inv")]
+APPLIED += [(name, (lambda g, y, f=name: g.apply(f, y, 1.5))) for name in ("*", "+", "-", "/", "max", "min")]
+APPLIED += [("^", lambda g, y: y * y * y), ("identity", lambda g, y: y), ("Float32", lambda g, y: y + 1.5),
+            ("BFloat16", lambda g, y: g.apply("bfloat16", y) + 1.5)]
 SAMPLES = 10
 
 
@@ -122,13 +125,11 @@ def calibrate(target) -> dict[str, float]:
     x = (torch.rand(rows * n, device="cuda", generator=gen) * 0.5 + 0.25)  # in (0.25, 0.75): every f finite
     r = torch.zeros(n, device="cuda")
     alone, _, _ = _timed(target, _column_sum(rows, n), {"x": x, "r": r})
-    for name, fn, arity in APPLIED:
-        def body(g, t, fn=fn, arity=arity):
+    for name, once in APPLIED:
+        def body(g, t, once=once):
             y = t
             for _ in range(APPLIED_TIMES):
-                if fn is None:
-                    continue
-                y = g.apply(fn, y) if arity == 1 else g.apply(fn, y, t)
+                y = once(g, y)
             return y
         t, _, _ = _timed(target, _column_sum(rows, n, body), {"x": x, "r": r})
         rates[f"applied streamed any {name}"] = max(0.0, (t - alone) / (APPLIED_TIMES * rows * n))

@@ -38,7 +38,7 @@ TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4}
 FN = {name: k for k, name in enumerate([
     "+", "-", "*", "/", "neg", "abs", "abs2", "sqrt", "exp", "log", "tanh", "sin", "cos", "log1p", "expm1", "^",
     "max", "min", "<", "<=", ">", ">=", "==", "!=", "ifelse", "round", "floor", "ceil", "sign", "clamp", "fma",
-    "inv"])}
+    "inv", "bfloat16"])}
 ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", ">", ">=", "==", "!=") else
                 3 if name in ("ifelse", "clamp", "fma") else 1) for name in FN}
 FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6}

@@ -311,3 +311,75 @@ def test_parallel_scans(target, n, m, reverse):
     assert relative(ts["c"].cpu().numpy().reshape(m, n), C) < tol_c
     assert relative(ts["h"].cpu().numpy().reshape(m, n), H) < tol_c
     assert np.array_equal(ts["tot"].cpu().numpy(), x.reshape(m, n).max(axis=1))
+
+
+def test_column_fold_with_a_hoisted_load_and_idle_threads(target):
+    """A (2, 100000, 3) fold over axis 1 with a load of x at (i0, 0, i2)
+    outside the sweep: 6 items in a 64-item workgroup, so 58 threads have no
+    item and must not read past x (they take item 0's positions)."""
+    from tempest_hip.floor import FloorGroup
+    n0, n1, n2 = 2, 100000, 3
+    announce("floor column fold, hoisted load", n0, n1, n2)
+    g = FloorGroup("reduction", (n0, n1, n2), reduced=(1,))
+    g.value("x", "f32", n0 * n1 * n2)
+    g.value("r", "f32", n0 * n2)
+    x = g.load("x", (1, n0, n0 * n1))
+    x0 = g.load("x", (1, 0, n0 * n1))
+    g.output("r", g.fold("sum", x * x0).value, (1, 0, n0), full=False)
+    assert g.source().splitlines()[0].startswith("// tempest-hip floor: columns")
+    rng = np.random.default_rng(3)
+    xs = rng.standard_normal(n0 * n1 * n2).astype(np.float32)
+    ts = {"x": torch.from_numpy(xs).cuda(), "r": torch.zeros(n0 * n2, device="cuda")}
+    g.build({k: ts[k].data_ptr() for k in g.values})()
+    torch.cuda.synchronize()
+    X = xs.astype(np.float64).reshape(n2, n1, n0)
+    want = (X * X[:, :1, :]).sum(axis=1)  # (n2, n0): r[i0 + n0 * i2]
+    assert relative(ts["r"].cpu().numpy().reshape(n2, n0), want) < TOL
+
+
+@pytest.mark.parametrize("n,m,dtype", [(1000, 3, "f32"), (4099, 2, "bf16"), (64, 5, "f32")])
+def test_parallel_scans_of_every_fold(target, n, m, dtype):
+    """The workgroup-parallel scan's other folds: a running log-sum-exp (the
+    exponential fold, -inf identities in idle lanes), the running mean and
+    squared deviations (the square fold), a running product and a running
+    minimum, at lengths that leave idle lanes in the last chunk, from fp32 or
+    bf16 values."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor parallel scan folds", n, m, dtype)
+    rng = np.random.default_rng(n * 31 + m)
+    x = rng.standard_normal(n * m).astype(np.float32)
+    p = (0.95 + 0.1 * rng.random(n * m)).astype(np.float32)
+    if dtype == "bf16":
+        x, p = bf16_round(x), bf16_round(p)
+    g = FloorGroup("scan", (n, m), reduced=(0,))
+    g.value("x", dtype, n * m)
+    g.value("p", dtype, n * m)
+    for k in ("lse", "mean", "dev", "prod", "min"):
+        g.value(k, "f32", n * m)
+    xx, pp = g.load("x", (1, n)), g.load("p", (1, n))
+    e = g.fold("exp", xx, scan="inclusive")
+    s = g.fold("square", xx, scan="inclusive")
+    q = g.fold("prod", pp, scan="inclusive")
+    lo = g.fold("min", xx, scan="inclusive")
+    g.output("lse", e.logsumexp, (1, n))
+    g.output("mean", s.statistic, (1, n))
+    g.output("dev", s.sum, (1, n))
+    g.output("prod", q.value, (1, n))
+    g.output("min", lo.value, (1, n))
+    assert "a workgroup per item" in g.source().splitlines()[0]
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    ts = {"x": torch.from_numpy(x).cuda().to(tdt), "p": torch.from_numpy(p).cuda().to(tdt)}
+    for k in ("lse", "mean", "dev", "prod", "min"):
+        ts[k] = torch.zeros(n * m, device="cuda")
+    g.build({k: ts[k].data_ptr() for k in g.values})()
+    torch.cuda.synchronize()
+    X, Pm = x.astype(np.float64).reshape(m, n), p.astype(np.float64).reshape(m, n)
+    cnt = np.arange(1, n + 1)
+    mean = np.cumsum(X, axis=1) / cnt
+    dev = np.cumsum(X * X, axis=1) - cnt * mean * mean
+    got = {k: ts[k].cpu().numpy().astype(np.float64).reshape(m, n) for k in ("lse", "mean", "dev", "prod", "min")}
+    assert relative(got["lse"], np.logaddexp.accumulate(X, axis=1)) < TOL
+    assert relative(got["mean"], mean) < 1e-4  # a running mean of up to 4099 terms in fp32
+    assert relative(got["dev"], dev) < 1e-4
+    assert relative(got["prod"], np.cumprod(Pm, axis=1)) < 1e-4
+    assert np.array_equal(got["min"], np.minimum.accumulate(X, axis=1))

@@ -237,3 +237,56 @@ def test_div_mod_bounds_are_sound_on_random_atoms():
         length = int(rng.integers(max(1, hi + constant - 2), hi + constant + 3))
         if _accepts(extents, coeffs, constant, parts, length):
             assert lo + constant >= 0 and hi + constant < length, (extents, coeffs, constant, parts, length)
+
+
+def test_column_reduction_hoists_loads_of_live_items_only():
+    """A reduction over axis 1 of a (2, 100000, 3) array, plus a load of x at
+    (i0, 0, i2) hoisted out of the sweep: 6 items in workgroups of 64, so 58
+    threads have no item.  They must take item 0's positions, or the hoisted
+    load reads up to 24 MB past the value."""
+    from tempest_hip.floor import FloorGroup
+    n0, n1, n2 = 2, 100000, 3
+    g = FloorGroup("reduction", (n0, n1, n2), reduced=(1,))
+    g.value("x", "f32", n0 * n1 * n2)
+    g.value("r", "f32", n0 * n2)
+    x = g.load("x", (1, n0, n0 * n1))
+    x0 = g.load("x", (1, 0, n0 * n1))
+    g.output("r", g.fold("sum", x * x0).value, (1, 0, n0), full=False)
+    src = g.source()
+    head = src.splitlines()[0]
+    assert head.startswith("// tempest-hip floor: columns"), head
+    assert "(live ? item : 0L)" in src
+    g.compile()
+
+
+@pytest.mark.parametrize("extents,length", [((1000, 0), 1), ((0, 7), 7)])
+def test_once_outputs_of_an_empty_fold_are_checked(extents, length):
+    """sum over an empty axis still writes every item's result, at the folded
+    position zero: a (1000, 0) reduction over axis 1 writing r[i0] into a
+    one-element value is refused (the kernel would write 1000 elements).  An
+    empty kept axis writes nothing and is accepted."""
+    from tempest_hip import HIPError
+    from tempest_hip.floor import FloorGroup
+    g = FloorGroup("reduction", extents, reduced=(1,))
+    g.value("x", "f32", 0)
+    g.value("r", "f32", length)
+    g.output("r", g.fold("sum", g.load("x", (1, extents[0]))).value, (1, 0), full=False)
+    if extents[0] == 0:
+        g.source()
+        return
+    with pytest.raises(HIPError, match="writes outside"):
+        g.source()
+
+
+def test_once_output_loads_are_checked_at_folded_zero():
+    """A once output that reads x at the folded position zero, over an empty
+    folded axis: the load runs once per item, so x must hold it."""
+    from tempest_hip import HIPError
+    from tempest_hip.floor import FloorGroup
+    g = FloorGroup("reduction", (16, 0), reduced=(1,))
+    g.value("x", "f32", 8)
+    g.value("r", "f32", 16)
+    s = g.fold("sum", g.load("x", (1, 16)))
+    g.output("r", s.value + g.load("x", (1, 16)), (1, 0), full=False)
+    with pytest.raises(HIPError, match="folded positions at zero"):
+        g.source()

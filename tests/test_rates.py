@@ -15,7 +15,7 @@ def test_rates_file_has_the_reference_keys_and_sane_values():
     assert 1e-7 < r["floor memory latency"] < 2e-5
     assert 2e12 < r["floor memory bandwidth"] <= r["device bandwidth"]
     assert 5e14 < r["HIP BFloat16 rate"] < 2.5e15 and r["HIP BFloat16 split"] == r["HIP BFloat16 rate"]
-    for name, _, _ in calibrate.APPLIED:
+    for name, _ in calibrate.APPLIED:
         v = r[f"applied streamed any {name}"]
         assert 0.0 <= v < 1e-10, name
     # Transcendentals cost more than a multiply in a streamed fold.
