@@ -189,6 +189,18 @@ int th_build_softmax_grad(int64_t rows, int32_t n, int64_t ld,
                           const float* x, const float* g, float* dx, float* loss,
                           th_launch** host_out);
 
+/* th_build_softmax_grad's program run at once on the library's stream, with
+ * no device allocation: no counterpart in the reference.  It is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The per-row loss partials
+ * go to a static device scratch of 2^20 floats that each GPU holds until the
+ * process ends, so rows must be at most 1048576 (TH_E_ARGUMENT beyond).  Every
+ * call on a GPU shares that GPU's scratch: calls that overlap on one GPU (on
+ * different streams, or from different threads) race.  The same kernels as
+ * th_build_softmax_grad, so the results are bit-identical to its launch's. */
+int th_softmax_grad_noalloc(int64_t rows, int32_t n, int64_t ld,
+                            const float* x, const float* g, float* dx, float* loss);
+
 /* LayerNorm (weight 1, bias 0) over each contiguous run of n and its
  * gradient: y = (x .- m) ./ sqrt.(v .+ eps) with m, v the run's mean and
  * mean square deviation (two passes, test/fixtures/programs.jl:13-17),

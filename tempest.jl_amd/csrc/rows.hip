@@ -524,7 +524,67 @@ int build_rows(Op op, const char* title, int64_t rows, int32_t n, int64_t ld, fl
 
 }  // namespace
 
+// ---- the softmax gradient that allocates nothing --------------------------
+//
+// th_softmax_grad_noalloc keeps its per-row loss partials in this array, one
+// copy per GPU, held until the process ends.  Host code reaches it only
+// through the address hipGetSymbolAddress gives on each device (the array's
+// name in host code is a stand-in, not a device address).
+constexpr int64_t kScratchRows = int64_t(1) << 20;  // 4 MiB of fp32 partials
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchRows];
+static float* g_scratch[kScratchDevices];
+
+namespace th {
+
+int rows_scratch_setup(int device) {
+  TH_REQUIRE(device >= 0 && device < kScratchDevices, "rows_scratch_setup: device out of range");
+  if (g_scratch[device]) return TH_OK;
+  void* ptr = nullptr;
+  TH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  g_scratch[device] = static_cast<float*>(ptr);
+  return TH_OK;
+}
+
+}  // namespace th
+
 extern "C" {
+
+int th_softmax_grad_noalloc(int64_t rows, int32_t n, int64_t ld, const float* x, const float* g,
+                            float* dx, float* loss) {
+  if (int r = th::require_ready()) return r;
+  const char* title = "th_softmax_grad_noalloc";
+  TH_REQUIRE(rows >= 1 && rows <= kScratchRows,
+             std::string(title) + ": rows must be in 1.." + std::to_string(kScratchRows) +
+                 " (the partials' static scratch holds that many)");
+  TH_REQUIRE(n >= 1, std::string(title) + ": n must be positive");
+  TH_REQUIRE(ld >= n, std::string(title) + ": ld must be at least n");
+  TH_REQUIRE(x && g && dx && loss, std::string(title) + ": null pointer");
+  float* partial = g_scratch[th::ctx().device];
+  if (!partial) return th::fail(TH_E_STATE, std::string(title) + ": scratch address not set up by th_init");
+  const bool aligned = aligned16(x) && aligned16(g) && aligned16(dx);
+  const char* kname = "";
+  const void* fn = pick(kSoftmaxGrad, n, ld, aligned, &kname);
+  // Every row's partial is written before sum_all reads it: nothing to clear.
+  th::Kernel k;
+  k.fn = fn;
+  k.name = kname;
+  k.grid = dim3((unsigned)rows);
+  k.block = dim3(kThreads);
+  RowArgs a{x, g, dx, partial, rows, ld, n, 0.0f};
+  std::memcpy(k.args, &a, sizeof a);
+  k.args_size = sizeof a;
+  if (int r = th::launch_kernel(k, th::ctx().stream)) return r;
+  th::Kernel k2;
+  k2.fn = (const void*)sum_all;
+  k2.name = "sum_all";
+  k2.grid = dim3(1);
+  k2.block = dim3(1024);
+  SumArgs sa{partial, loss, rows};
+  std::memcpy(k2.args, &sa, sizeof sa);
+  k2.args_size = sizeof sa;
+  return th::launch_kernel(k2, th::ctx().stream);
+}
 
 int th_build_softmax_grad(int64_t rows, int32_t n, int64_t ld, const float* x, const float* g,
                           float* dx, float* loss, th_launch** out) {

@@ -112,6 +112,7 @@ int th_init(int device) {
   TH_HIP(hipSetDevice(device));
   TH_HIP(hipGetDeviceProperties(&c.prop, device));
   TH_HIP(hipStreamCreateWithFlags(&c.own, hipStreamNonBlocking));
+  if (int r = rows_scratch_setup(device)) return r;
   c.stream = c.own;
   c.device = device;
   c.ready = true;

@@ -154,6 +154,9 @@ class Builder {
 #define TH_OFFSET(Args, member) offsetof(Args, member)
 
 int launch_kernel(const Kernel& k, hipStream_t s);
+// Find, on `device` (current), the address of the static scratch that
+// th_softmax_grad_noalloc uses; th_init calls it once per device.
+int rows_scratch_setup(int device);
 int device_alloc(size_t bytes, void** out);
 
 }  // namespace th
