@@ -444,19 +444,24 @@ int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
 
 /* ---- op class (c): causal flash attention ------------------------------- */
 
-/* Attention over (features, heads, positions, batch) column-major bf16 arrays
+/* Attention over (features, heads, positions, batch) column-major arrays
  * (test/fixtures/operations.jl:5-70): element (d, h, s, b) of q, o, dout, dq
  * at d + h*q_strides[0] + s*q_strides[1] + b*q_strides[2], of k, v, dk, dv at
- * d + h*k_strides[0] + s*k_strides[1] + b*k_strides[2].  head_dim 128, seq a
- * multiple of 128; query head h reads key/value head h / (heads / kv_heads).
- * lse is fp32, (1, heads, positions, batch): element (h, s, b) at
- * h + heads*(s + seq*b), the natural log-sum-exp of each query's scaled scores.
- * scale <= 0 means 1/sqrt(head_dim). */
+ * d + h*k_strides[0] + s*k_strides[1] + b*k_strides[2]; query head h reads
+ * key/value head h / (heads / kv_heads).  lse is fp32, (1, heads, positions,
+ * batch): element (h, s, b) at h + heads*(s + seq*b), the natural log-sum-exp
+ * of each query's scaled scores.  scale <= 0 means 1/sqrt(head_dim).
+ * Two implementations: bf16 with head_dim 128, seq a multiple of 128, keys
+ * as many as queries and no device-held masks runs the matrix-core kernels;
+ * anything else with head_dim 1..256 (fp32 or bf16 arrays, any lengths,
+ * starts and lengths masks) runs the general kernels, which compute in fp32
+ * on the vector ALUs (the cuDNN claim's d <= 256, ext/cuDNNExt.jl:95-100, and
+ * the reference's attention tests, test/cuda/attention.jl:10-16,218-271). */
 typedef struct th_attention_desc {
   int32_t batch, heads, kv_heads, seq, head_dim;
   int32_t causal;
   float scale;
-  int32_t flags; /* backward: TH_ATTN_RECOMPUTE_DQ; 0 otherwise */
+  int32_t flags; /* TH_ATTN_F32; backward: TH_ATTN_RECOMPUTE_DQ */
   const void* q;
   const void* k;
   const void* v;
@@ -468,10 +473,23 @@ typedef struct th_attention_desc {
   void* dv;
   int64_t q_strides[3]; /* along heads, positions, batch */
   int64_t k_strides[3];
+  int32_t kv_seq;         /* positions of k and v; 0: the same as seq */
+  int32_t reserved;
+  /* Masks the device holds (NULL: none), read when the launch runs:
+   * starts, int32 (positions, batch): the 1-based first key query (s, b)
+   * sees, at s + seq * b (documents packed in sequences);
+   * lengths, int32 (batch): the keys sequence b holds (decode over a cache).
+   * Query j (0-based) of batch b sees key i when i < lengths[b],
+   * i >= starts[j + seq b] - 1 and, causal, i <= j. */
+  const int32_t* starts;
+  const int32_t* lengths;
 } th_attention_desc;
 
-/* o = softmax(scale * k'q, masked causal) * v per head, and lse (if non-NULL).
- * Values: 0 q, 1 k, 2 v, 3 o, 4 lse.  Replaces the cuTile online-softmax
+/* q, k, v, o, dout, dq, dk, dv hold fp32 instead of bf16. */
+#define TH_ATTN_F32 2
+
+/* o = softmax(scale * k'q, masked) * v per head, and lse (if non-NULL).
+ * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 starts, 6 lengths.  Replaces the cuTile online-softmax
  * product sweep (ext/cuTileExt/build.jl:326-532) and cuDNNAttention's SDPA
  * forward (ext/cuDNNExt.jl:38-55,116-210). */
 int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
@@ -480,13 +498,14 @@ int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
 #define TH_ATTN_RECOMPUTE_DQ 1
 
 /* dq, dk, dv from q, k, v, o, lse (as the forward wrote them) and dout;
- * deterministic (no atomics).  With grouped heads (kv_heads < heads) dk and
+ * deterministic (no atomics); the general kernels need lse.  With grouped heads (kv_heads < heads) dk and
  * dv sum over the heads / kv_heads query heads that read each key/value
  * head, swept in turn (test/cuda/attention.jl:132-140).  The dK/dV sweep stores dS
  * (bf16, 2*batch*heads*seq^2 bytes of workspace the launch owns) for the dQ
  * sweep; when that exceeds 16 GiB, or with TH_ATTN_RECOMPUTE_DQ, the dQ sweep
  * recomputes S and dP instead and the workspace is not allocated.
- * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 dout, 6 dq, 7 dk, 8 dv.  Replaces the
+ * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 dout, 6 dq, 7 dk, 8 dv, 9 starts,
+ * 10 lengths.  Replaces the
  * cuTile transposed folds of the backward (ext/cuTileExt/transpose.jl:1-213). */
 int th_build_attention_bwd(const th_attention_desc* desc, th_launch** host_out);
 

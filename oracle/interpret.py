@@ -118,44 +118,63 @@ def mlp_grad(W1, b1, W2, b2, x):
     return loss, dW1, db1, dW2, db2, dx
 
 
-def attention_fwd(q, k, v, causal=True, scale=None):
+def attention_visible(B, S, Sk, causal=True, starts=None, lengths=None):
+    """Which keys each query sees, (batch, 1, queries, keys): key n (0-based) is
+    seen by query m of batch b when n < lengths[b], n >= starts[b, m] - 1
+    (1-based starts: documents packed in sequences) and, causal, n <= m --
+    the masks of test/cuda/attention.jl:218-271 and the causal formula of
+    test/fixtures/operations.jl:21-70."""
+    n = np.arange(Sk)[None, None, None, :]
+    m = np.arange(S)[None, None, :, None]
+    seen = np.ones((B, 1, S, Sk), dtype=bool)
+    if causal:
+        seen &= n <= m
+    if starts is not None:
+        seen &= n >= np.asarray(starts).reshape(B, 1, S, 1) - 1
+    if lengths is not None:
+        seen &= n < np.asarray(lengths).reshape(B, 1, 1, 1)
+    return seen
+
+
+def attention_fwd(q, k, v, causal=True, scale=None, starts=None, lengths=None):
     """attention(q, k, v; causal, scale) of test/fixtures/operations.jl:21-70 in
     float64.  Arrays are numpy (batch, positions, heads, d): the memory of the
-    reference's (d, heads, positions, batch) column-major arrays.  Query head h
-    reads key/value head h // (heads // kv_heads).  Returns (o, lse), lse
+    reference's (d, heads, positions, batch) column-major arrays; k and v may
+    hold another number of positions than q.  Query head h reads key/value
+    head h // (heads // kv_heads).  starts (batch, positions), lengths (batch):
+    the device-held masks of attention_visible.  Returns (o, lse), lse
     (batch, positions, heads)."""
     q, k, v = (np.asarray(a, dtype=np.float64) for a in (q, k, v))
     B, S, H, D = q.shape
-    Hk = k.shape[2]
+    Sk, Hk = k.shape[1], k.shape[2]
     scale = 1.0 / np.sqrt(D) if scale is None else scale
     kk = np.repeat(k, H // Hk, axis=2)
     vv = np.repeat(v, H // Hk, axis=2)
     s = np.einsum("bmhd,bnhd->bhmn", q, kk) * scale
-    if causal:
-        mask = np.arange(S)[None, :] > np.arange(S)[:, None]  # key n after query m
-        s = np.where(mask[None, None], -np.inf, s)
+    s = np.where(attention_visible(B, S, Sk, causal, starts, lengths), s, -np.inf)
     m = s.max(axis=-1, keepdims=True)
-    e = np.exp(s - m)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(s - m)
     l = e.sum(axis=-1, keepdims=True)
-    o = np.einsum("bhmn,bnhd->bmhd", e / l, vv)
-    lse = (m + np.log(l))[..., 0].transpose(0, 2, 1)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        o = np.einsum("bhmn,bnhd->bmhd", e / l, vv)
+        lse = (m + np.log(l))[..., 0].transpose(0, 2, 1)
     return o, lse
 
 
-def attention_bwd(q, k, v, dout, causal=True, scale=None):
+def attention_bwd(q, k, v, dout, causal=True, scale=None, starts=None, lengths=None):
     """Gradients of sum(attention(q, k, v) .* dout) w.r.t. q, k, v in float64,
-    same layout as attention_fwd.  With grouped heads the key and value
-    gradients sum over the query heads of a group (test/cuda/attention.jl:132-140)."""
+    same layout and masks as attention_fwd.  With grouped heads the key and
+    value gradients sum over the query heads of a group
+    (test/cuda/attention.jl:132-140)."""
     q, k, v, dout = (np.asarray(a, dtype=np.float64) for a in (q, k, v, dout))
     B, S, H, D = q.shape
-    Hk = k.shape[2]
+    Sk, Hk = k.shape[1], k.shape[2]
     scale = 1.0 / np.sqrt(D) if scale is None else scale
     k = np.repeat(k, H // Hk, axis=2)
     v = np.repeat(v, H // Hk, axis=2)
     s = np.einsum("bmhd,bnhd->bhmn", q, k) * scale
-    if causal:
-        mask = np.arange(S)[None, :] > np.arange(S)[:, None]
-        s = np.where(mask[None, None], -np.inf, s)
+    s = np.where(attention_visible(B, S, Sk, causal, starts, lengths), s, -np.inf)
     p = np.exp(s - s.max(axis=-1, keepdims=True))
     p /= p.sum(axis=-1, keepdims=True)
     g = np.einsum("bmhd->bhmd", dout)
@@ -165,8 +184,8 @@ def attention_bwd(q, k, v, dout, causal=True, scale=None):
     dq = np.einsum("bhmn,bnhd->bmhd", ds, k) * scale
     dk = np.einsum("bhmn,bmhd->bnhd", ds, q) * scale
     # Query head h = hk * (H // Hk) + g reads kv head hk: sum over g.
-    dk = dk.reshape(B, S, Hk, H // Hk, D).sum(axis=3)
-    dv = dv.reshape(B, S, Hk, H // Hk, D).sum(axis=3)
+    dk = dk.reshape(B, Sk, Hk, H // Hk, D).sum(axis=3)
+    dv = dv.reshape(B, Sk, Hk, H // Hk, D).sum(axis=3)
     return dq, dk, dv
 
 

@@ -1054,9 +1054,27 @@ AttnArgs args_of(const th_attention_desc* d) {
 
 }  // namespace
 
+// Whether the matrix-core kernels take the descriptor: bf16, head_dim 128,
+// seq a multiple of 128, as many keys as queries, no device-held masks,
+// 16-byte rows and operands, tiles and sequences their offsets can span.
+bool matrix_cores_take(const th_attention_desc* d, bool backward) {
+  const bool ok = (d->flags & TH_ATTN_F32) == 0 && (d->kv_seq == 0 || d->kv_seq == d->seq) && !d->starts &&
+                  !d->lengths && d->head_dim == kD && d->seq > 0 && d->seq % 128 == 0;
+  if (!ok) return false;
+  const char* saved = th_last_error();
+  const std::string keep = saved;
+  const bool fits = check_desc(d, backward) == TH_OK &&
+                    (double)d->seq * d->k_strides[1] * 2 < 2147483648.0 &&
+                    (double)d->seq * d->q_strides[1] * 2 < 2147483648.0;
+  th::set_error(keep);
+  return fits;
+}
+
 extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** out) {
   if (int r = th::require_ready()) return r;
   *out = nullptr;
+  TH_REQUIRE(d != nullptr, "attention: null descriptor");
+  if (!matrix_cores_take(d, false)) return th::build_attention_general_fwd(d, out);
   if (int r = check_desc(d, false)) return r;
   // The forward's direct loads address a (batch, head) sequence of K and V
   // from one base with 32-bit byte offsets.
@@ -1064,7 +1082,7 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
              "attention: a sequence of K or V must span under 2 GiB (seq x position stride x 2 bytes)");
   TH_HIP(hipFuncSetAttribute((const void*)attn_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFwdLds));
   AttnArgs a = args_of(d);
-  th::Builder b("attention_fwd", 5);
+  th::Builder b("attention_fwd", 7);  // values 5, 6 (the masks) are read only by the general kernels
   int k = b.kernel((const void*)attn_fwd, "attn_fwd", dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch),
                    dim3(256), (uint32_t)kFwdLds, a);
   b.ref(0, k, TH_OFFSET(AttnArgs, q));
@@ -1083,9 +1101,11 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
 extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** out) {
   if (int r = th::require_ready()) return r;
   *out = nullptr;
+  TH_REQUIRE(d != nullptr, "attention: null descriptor");
+  if (!matrix_cores_take(d, true)) return th::build_attention_general_bwd(d, out);
   if (int r = check_desc(d, true)) return r;
   AttnArgs a = args_of(d);
-  th::Builder b("attention_bwd", 9);
+  th::Builder b("attention_bwd", 11);  // values 9, 10 (the masks) are read only by the general kernels
   // The dK/dV sweep loads Q and dO tiles directly into LDS with 32-bit byte
   // offsets from a (batch, head) base.
   TH_REQUIRE((double)d->seq * d->q_strides[1] * 2 < 2147483648.0,

@@ -159,6 +159,10 @@ int launch_kernel(const Kernel& k, hipStream_t s);
 int rows_scratch_setup(int device);
 int device_alloc(size_t bytes, void** out);
 
+// Attention for what the matrix-core kernels do not take (attention_generic.hip).
+int build_attention_general_fwd(const th_attention_desc* d, th_launch** out);
+int build_attention_general_bwd(const th_attention_desc* d, th_launch** out);
+
 }  // namespace th
 
 // ---- device helpers shared by kernels ---------------------------------------

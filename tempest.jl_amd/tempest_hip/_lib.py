@@ -50,7 +50,8 @@ class AttentionDesc(ctypes.Structure):
     _fields_ = [("batch", c_i32), ("heads", c_i32), ("kv_heads", c_i32), ("seq", c_i32), ("head_dim", c_i32),
                 ("causal", c_i32), ("scale", c_f32), ("flags", c_i32), ("q", c_void_p), ("k", c_void_p),
                 ("v", c_void_p), ("o", c_void_p), ("lse", c_void_p), ("dout", c_void_p), ("dq", c_void_p),
-                ("dk", c_void_p), ("dv", c_void_p), ("q_strides", c_i64 * 3), ("k_strides", c_i64 * 3)]
+                ("dk", c_void_p), ("dv", c_void_p), ("q_strides", c_i64 * 3), ("k_strides", c_i64 * 3),
+                ("kv_seq", c_i32), ("reserved", c_i32), ("starts", c_void_p), ("lengths", c_void_p)]
 
 
 class DeltaNetDesc(ctypes.Structure):

@@ -117,22 +117,31 @@ def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b
 # ---- op class (c) -----------------------------------------------------------
 
 def _attention_desc(batch, heads, kv_heads, seq, q, k, v, o, lse=0, dout=0, dq=0, dk=0, dv=0, causal=True,
-                    scale=0.0, q_strides=None, k_strides=None, head_dim=128, flags=0):
+                    scale=0.0, q_strides=None, k_strides=None, head_dim=128, flags=0, kv_seq=0, starts=0, lengths=0,
+                    f32=False):
+    ks_n = kv_seq or seq
     qs = q_strides or (head_dim, heads * head_dim, seq * heads * head_dim)
-    ks = k_strides or (head_dim, kv_heads * head_dim, seq * kv_heads * head_dim)
+    ks = k_strides or (head_dim, kv_heads * head_dim, ks_n * kv_heads * head_dim)
     d = _lib.AttentionDesc(batch=batch, heads=heads, kv_heads=kv_heads, seq=seq, head_dim=head_dim,
-                           causal=int(causal), scale=scale, flags=flags, q=q, k=k, v=v, o=o, lse=lse or None,
-                           dout=dout or None, dq=dq or None, dk=dk or None, dv=dv or None)
+                           causal=int(causal), scale=scale, flags=flags | (ATTN_F32 if f32 else 0), q=q, k=k, v=v,
+                           o=o, lse=lse or None, dout=dout or None, dq=dq or None, dk=dk or None, dv=dv or None,
+                           kv_seq=kv_seq, starts=starts or None, lengths=lengths or None)
     d.q_strides[:] = list(qs)
     d.k_strides[:] = list(ks)
     return d
 
 
+ATTN_F32 = 2  # TH_ATTN_F32
+
+
 def attention_fwd(batch: int, heads: int, kv_heads: int, seq: int, q: int, k: int, v: int, o: int, lse: int = 0,
-                  causal: bool = True, scale: float = 0.0, **strides) -> Launch:
-    """o = attention(q, k, v; causal) over (d, heads, positions, batch) bf16 arrays; lse fp32."""
-    d = _attention_desc(batch, heads, kv_heads, seq, q, k, v, o, lse, causal=causal, scale=scale, **strides)
-    return _built("th_build_attention_fwd", ("q", "k", "v", "o", "lse"), ctypes.byref(d))
+                  causal: bool = True, scale: float = 0.0, **extra) -> Launch:
+    """o = attention(q, k, v; causal) over (d, heads, positions, batch) arrays
+    (bf16, or fp32 with f32=True); lse fp32.  extra: head_dim, kv_seq (keys'
+    positions), starts (int32 (positions, batch), 1-based first key of each
+    query), lengths (int32 (batch), keys of each sequence), q_strides, k_strides."""
+    d = _attention_desc(batch, heads, kv_heads, seq, q, k, v, o, lse, causal=causal, scale=scale, **extra)
+    return _built("th_build_attention_fwd", ("q", "k", "v", "o", "lse", "starts", "lengths"), ctypes.byref(d))
 
 
 RECOMPUTE_DQ = 1  # TH_ATTN_RECOMPUTE_DQ
@@ -140,15 +149,16 @@ RECOMPUTE_DQ = 1  # TH_ATTN_RECOMPUTE_DQ
 
 def attention_bwd(batch: int, heads: int, seq: int, q: int, k: int, v: int, o: int, lse: int, dout: int, dq: int,
                   dk: int, dv: int, causal: bool = True, scale: float = 0.0, recompute_dq: bool = False,
-                  kv_heads: int = 0, **strides) -> Launch:
+                  kv_heads: int = 0, **extra) -> Launch:
     """dq, dk, dv of sum(attention(q, k, v) .* dout), from the forward's o and lse.
     kv_heads (default heads): k, v, dk, dv have kv_heads heads, each read by
     heads / kv_heads query heads; dk and dv sum over them.
     recompute_dq: the dQ sweep recomputes S and dP instead of reading the dS
     the dK/dV sweep stores (the path taken anyway past 16 GiB of dS)."""
     d = _attention_desc(batch, heads, kv_heads or heads, seq, q, k, v, o, lse, dout, dq, dk, dv, causal=causal,
-                        scale=scale, flags=RECOMPUTE_DQ if recompute_dq else 0, **strides)
-    return _built("th_build_attention_bwd", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"), ctypes.byref(d))
+                        scale=scale, flags=RECOMPUTE_DQ if recompute_dq else 0, **extra)
+    return _built("th_build_attention_bwd",
+                  ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv", "starts", "lengths"), ctypes.byref(d))
 
 
 # ---- config 5 ---------------------------------------------------------------

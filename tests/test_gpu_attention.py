@@ -123,14 +123,18 @@ def test_backward_both_dq_paths(target, S, causal, recompute):
         assert relative(_np(got), ref) < TOL, name
 
 
-def test_refuses_other_head_dims(target):
+def test_head_dims_route_to_the_kernels_that_take_them(target):
+    """d 128 at a multiple of 128 takes the matrix-core kernel; d 64 and a
+    length of 100 take the general kernels; d beyond 256 is refused."""
     import tempest_hip.launch as L
     from tempest_hip import HIPError
-    t = torch.zeros(1, 128, 1, 128, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(HIPError, match="head_dim"):
-        L.attention_fwd(1, 1, 1, 128, t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(), head_dim=64)
-    with pytest.raises(HIPError, match="multiple of 128"):
-        L.attention_fwd(1, 1, 1, 100, t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr())
+    t = torch.zeros(1, 128, 1, 300, dtype=torch.bfloat16, device="cuda")
+    p = t.data_ptr()
+    assert "attn_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p).describe()
+    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=64).describe()
+    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 100, p, p, p, p).describe()
+    with pytest.raises(HIPError, match="head_dim must be 1..256"):
+        L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=300)
 
 
 def test_config4_full_size_sampled_heads(target):
