@@ -398,7 +398,7 @@ int th_build_tanh_layer_grad(int32_t d, int32_t h, int32_t c,
 
 /* ---- op class (b): bf16 products on the matrix cores --------------------- */
 
-enum { TH_F32 = 0, TH_BF16 = 1, TH_I32 = 2, TH_I64 = 3 };
+enum { TH_F32 = 0, TH_BF16 = 1, TH_I32 = 2, TH_I64 = 3, TH_F16 = 4 };
 
 /* What the product's group fuses after it.  Every epilogue works on the fp32
  * accumulator and rounds once to bf16 where it stores, except where noted.
@@ -413,14 +413,23 @@ enum { TH_F32 = 0, TH_BF16 = 1, TH_I32 = 2, TH_I64 = 3 };
  *                         sum over j of dz[i, j], rounded to bf16. */
 enum { TH_EPI_STORE = 0, TH_EPI_GELU = 1, TH_EPI_SQUARE_LOSS = 2, TH_EPI_GELU_BACKWARD = 3 };
 
-/* C (m x n, column-major, leading dimension c_ld) = A (m x k) * B (k x n).
- * A's element (i, l) is a[i*a_m + l*a_k], B's (l, j) is b[l*b_k + j*b_n]; one
- * stride of each operand must be 1 (k-contiguous or m/n-contiguous), m, n, k
- * and the other strides multiples of 8, operands 16-byte aligned.  A and B are
- * bf16, products accumulate in fp32.
- * Values: 0 a, 1 b, 2 c, 3 bias, 4 aux, 5 aux_out, 6 row_sums, 7 loss.
+/* C (m x n, column-major, leading dimension c_ld) = A (m x k) * B (k x n),
+ * for each of `batch` products (C_z = D_z + A_z B_z with TH_GEMM_ACCUMULATE).
+ * A's element (i, l) is a[i*a_m + l*a_k], B's (l, j) is b[l*b_k + j*b_n];
+ * product z's operands start a_batch, b_batch, c_batch (d_batch) elements
+ * further.  Factors are bf16 unless flags say fp32 or fp16; products
+ * accumulate in fp32 and the result is rounded once.
+ * Two implementations: bf16 factors with a unit stride on each operand, m, n,
+ * k and the other strides multiples of 8 and operands 16-byte aligned run the
+ * bf16 tile kernel (256 x 256 tiles, every epilogue, and K split over parts
+ * summed by a second launch when the tiles alone would leave the device idle);
+ * anything else with TH_EPI_STORE and no bias runs the general kernel (64 x 64
+ * tiles on the fp32 matrix cores, any shape and strides, a result of the
+ * factors' type or fp32).
+ * Values: 0 a, 1 b, 2 c, 3 bias, 4 aux, 5 aux_out, 6 row_sums, 7 loss, 8 d.
  * Replaces the cuTile product sketch (ext/cuTileExt/contract.jl:32-206) and
- * cuBLASProducts' gemm (ext/cuBLASExt.jl:247-259). */
+ * cuBLASProducts (ext/cuBLASExt.jl:23-36,247-259): its product, widened and
+ * accumulated templates over a batch. */
 typedef struct th_gemm_desc {
   int32_t m, n, k;
   int32_t c_dtype;   /* TH_BF16 or TH_F32 (TH_F32 only with TH_EPI_STORE) */
@@ -438,7 +447,18 @@ typedef struct th_gemm_desc {
   void* aux_out;     /* bf16, C's layout */
   void* row_sums;    /* bf16, m */
   float* loss;       /* fp32, one */
+  int32_t batch;     /* products (0 or 1: one) */
+  int32_t flags;     /* TH_GEMM_* */
+  int64_t a_batch, b_batch, c_batch;
+  const void* d;     /* TH_GEMM_ACCUMULATE: C = D + A*B, D laid out as C, may be C itself */
+  int64_t d_ld, d_batch;  /* 0, 0: C's */
+  int32_t splits;    /* parts K is split into on the tile kernel: 0 chosen, 1 none */
+  int32_t reserved2;
 } th_gemm_desc;
+
+#define TH_GEMM_F32_FACTORS 1  /* a and b hold fp32 */
+#define TH_GEMM_F16_FACTORS 2  /* a and b hold fp16 */
+#define TH_GEMM_ACCUMULATE 4   /* C = D + A*B (cuBLASExt.jl:25, `accumulated`) */
 
 int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
 

@@ -118,6 +118,37 @@ def mlp_grad(W1, b1, W2, b2, x):
     return loss, dW1, db1, dW2, db2, dx
 
 
+def product(a, b, d=None):
+    """contract(A, B, (1, 3, 4), (3, 2, 4), (1, 2, 4)) (+ D): A (m, k[, batch])
+    times B (k, n[, batch]) per batch, Julia axes, factors widened to float64
+    and nothing rounded (program/interpret.jl:58-63; ext/cuBLASExt.jl:23-25)."""
+    a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+    c = np.einsum("mk...,kn...->mn...", a, b)
+    return c if d is None else c + np.asarray(d, dtype=np.float64)
+
+
+def linear_bias_gelu_grad(w, x, b):
+    """The fixture "linear, bias, GELU" (test/fixtures/programs.jl:83):
+    loss = sum(abs2, gelu.(w * x .+ b)) and its gradient w.r.t. (w, x, b)."""
+    w, x, b = (np.asarray(v, dtype=np.float64) for v in (w, x, b))
+    z = w @ x + b[:, None]
+    y = gelu(z)
+    dz = 2 * y * gelu_grad(z)
+    return float((y * y).sum()), dz @ x.T, w.T @ dz, dz.sum(axis=1)
+
+
+def tanh_mlp_grad(x, w1, b1, w2, b2):
+    """The fixture "MLP" (test/fixtures/programs.jl:17,79): loss =
+    sum(abs2, w2 * tanh.(w1 * x .+ b1) .+ b2) and its gradient w.r.t.
+    (x, w1, b1, w2, b2), with tanh' = 1 - y^2 (program/differentiate.jl:106-155)."""
+    x, w1, b1, w2, b2 = (np.asarray(v, dtype=np.float64) for v in (x, w1, b1, w2, b2))
+    h = np.tanh(w1 @ x + b1[:, None])
+    y = w2 @ h + b2[:, None]
+    dy = 2 * y
+    dz = (w2.T @ dy) * (1 - h * h)
+    return float((y * y).sum()), w1.T @ dz, dz @ x.T, dz.sum(axis=1), dy @ h.T, dy.sum(axis=1)
+
+
 def attention_visible(B, S, Sk, causal=True, starts=None, lengths=None):
     """Which keys each query sees, (batch, 1, queries, keys): key n (0-based) is
     seen by query m of batch b when n < lengths[b], n >= starts[b, m] - 1

@@ -40,6 +40,37 @@ __global__ __launch_bounds__(256) void sum_loss(LossArgs a) {
   if (threadIdx.x == 0) a.loss[0] = (float)(lds[0] + lds[1] + lds[2] + lds[3]);
 }
 
+// The parts of K summed (in part order), plus the bias and what the product
+// is added to, rounded once to the result's type: C_z = D_z + sum_s W_zs + bias.
+struct ReduceArgs {
+  const float* ws;       // [batch][splits][m x n], column-major at ld m
+  void* c;               // result, column-major at c_ld, product z at c_batch
+  const uint16_t* bias;  // bf16, m, or null
+  const void* d;         // or null: laid out as C at d_ld, d_batch
+  int64_t c_ld, c_batch, d_ld, d_batch;
+  int32_t m, n, splits, c_dtype;
+};
+
+__global__ __launch_bounds__(256) void sum_splits(ReduceArgs a) {
+  const int64_t mn = (int64_t)a.m * a.n;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= mn) return;
+  const int64_t z = blockIdx.y;
+  const int64_t i = e % a.m, j = e / a.m;
+  const float* w = a.ws + z * a.splits * mn + e;
+  float v = 0.0f;
+  for (int s = 0; s < a.splits; ++s) v += w[s * mn];
+  if (a.bias) v += bf16_float(a.bias[i]);
+  const int64_t at_d = z * a.d_batch + i + j * a.d_ld, at = z * a.c_batch + i + j * a.c_ld;
+  if (a.c_dtype == TH_F32) {
+    if (a.d) v += static_cast<const float*>(a.d)[at_d];
+    static_cast<float*>(a.c)[at] = v;
+  } else {
+    if (a.d) v += bf16_float(static_cast<const uint16_t*>(a.d)[at_d]);
+    static_cast<uint16_t*>(a.c)[at] = bf16_bits(v);
+  }
+}
+
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 }  // namespace
@@ -47,25 +78,40 @@ bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) 
 
 using namespace thg;
 
+// Whether the bf16 tile kernel takes the descriptor: bf16 factors, a unit
+// stride on each operand, sizes and strides multiples of 8, 16-byte operands.
+bool tile_kernel_takes(const th_gemm_desc* d) {
+  if (d->flags & (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS)) return false;
+  if (d->c_dtype != TH_BF16 && d->c_dtype != TH_F32) return false;
+  if (d->m % 8 || d->n % 8 || d->k % 8) return false;
+  const bool ua = d->a_k == 1 || d->a_m == 1, ub = d->b_k == 1 || d->b_n == 1;
+  if (!ua || !ub) return false;
+  const int64_t sa = d->a_k == 1 ? d->a_m : d->a_k, sb = d->b_k == 1 ? d->b_n : d->b_k;
+  if (sa % 8 || sb % 8 || d->c_ld % 8 || d->c_ld < d->m) return false;
+  if (d->batch > 1 && (d->a_batch % 8 || d->b_batch % 8 || d->c_batch % 8)) return false;
+  return aligned(d->a, 16) && aligned(d->b, 16) && aligned(d->c, 16);
+}
+
 extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   if (int r = th::require_ready()) return r;
   *out = nullptr;
   TH_REQUIRE(d != nullptr, "th_build_gemm: null descriptor");
   const int M = d->m, N = d->n, K = d->k;
+  const int batch = d->batch > 0 ? d->batch : 1;
   TH_REQUIRE(M >= 1 && N >= 1 && K >= 1, "th_build_gemm: m, n, k must be positive");
-  TH_REQUIRE(M % 8 == 0 && N % 8 == 0 && K % 8 == 0,
-             "th_build_gemm: m, n and k must be multiples of 8 (16-byte rows)");
   TH_REQUIRE(d->a && d->b && d->c, "th_build_gemm: null operand");
-  const int la = d->a_k == 1 ? kK : (d->a_m == 1 ? kMN : -1);
-  const int lb = d->b_k == 1 ? kK : (d->b_n == 1 ? kMN : -1);
-  TH_REQUIRE(la >= 0 && lb >= 0, "th_build_gemm: each operand needs a unit stride along k or along m/n");
-  const int64_t sa = la == kK ? d->a_m : d->a_k, sb = lb == kK ? d->b_n : d->b_k;
-  TH_REQUIRE(sa % 8 == 0 && sb % 8 == 0 && d->c_ld % 8 == 0 && d->c_ld >= M,
-             "th_build_gemm: leading dimensions must be multiples of 8 and c_ld >= m");
-  TH_REQUIRE(aligned(d->a, 16) && aligned(d->b, 16) && aligned(d->c, 16),
-             "th_build_gemm: operands must be 16-byte aligned");
+  TH_REQUIRE((d->flags & ~(TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS | TH_GEMM_ACCUMULATE)) == 0 &&
+                 (d->flags & (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS)) != (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS),
+             "th_build_gemm: unknown flags");
+  const bool accumulate = (d->flags & TH_GEMM_ACCUMULATE) != 0;
+  TH_REQUIRE(!accumulate || d->d, "th_build_gemm: accumulating needs d");
   const int epi = d->epilogue;
   TH_REQUIRE(epi >= TH_EPI_STORE && epi <= TH_EPI_GELU_BACKWARD, "th_build_gemm: unknown epilogue");
+  TH_REQUIRE(epi == TH_EPI_STORE || (batch == 1 && !accumulate),
+             "th_build_gemm: fused epilogues take one product and nothing to add");
+  if (!tile_kernel_takes(d)) return th::build_gemm_general(d, out);
+  const int la = d->a_k == 1 ? kK : kMN;
+  const int lb = d->b_k == 1 ? kK : kMN;
   TH_REQUIRE(d->c_dtype == TH_BF16 || (d->c_dtype == TH_F32 && epi == TH_EPI_STORE),
              "th_build_gemm: fused epilogues write bf16");
   TH_REQUIRE(!d->bias || aligned(d->bias, 8), "th_build_gemm: bias must be 8-byte aligned");
@@ -79,17 +125,34 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
                "th_build_gemm: the GELU backward needs aux (8-byte aligned, ld >= m, ld % 4 == 0) and row_sums");
 
   const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
+  // K split over parts where the tiles alone would leave most CUs idle: up to
+  // 256 workgroups, each part at least 1024 deep and a multiple of 64.
+  int splits = d->splits > 0 ? d->splits : 1;
+  if (d->splits == 0 && epi == TH_EPI_STORE) {
+    const int tiles = tiles_m * tiles_n * batch;
+    if (tiles < 128 && K >= 2048) splits = std::max(1, std::min((256 + tiles - 1) / tiles, K / 1024));
+  }
+  TH_REQUIRE(splits == 1 || epi == TH_EPI_STORE, "th_build_gemm: only a plain product splits K");
+  int ksplit = K;
+  if (splits > 1) {
+    ksplit = ((K + splits - 1) / splits + kDepth - 1) / kDepth * kDepth;
+    splits = (K + ksplit - 1) / ksplit;
+  }
+  TH_REQUIRE(splits <= 65535 && batch <= 65535, "th_build_gemm: grid too large");
+  // Parts and what is added go through an fp32 workspace and a second launch.
+  const bool staged = splits > 1 || accumulate;
   // Interior tiles read through 32-bit buffer offsets: operands past 2 GiB
   // take the bounds-checked kernel, which addresses with 64-bit pointers.
   const int64_t a_bytes = 2 * (la == kK ? (int64_t)(M - 1) * d->a_m + K : (int64_t)(K - 1) * d->a_k + M);
   const int64_t b_bytes = 2 * (lb == kK ? (int64_t)(N - 1) * d->b_n + K : (int64_t)(K - 1) * d->b_k + N);
-  const bool check = (M % kTile) || (N % kTile) || (K % kDepth) || a_bytes > 0x7fffffff || b_bytes > 0x7fffffff;
+  const bool check = (M % kTile) || (N % kTile) || (K % kDepth) || (ksplit % kDepth) || a_bytes > 0x7fffffff ||
+                     b_bytes > 0x7fffffff;
   const void* fn = nullptr;
   const char* name = "";
   switch (epi) {
     case TH_EPI_STORE:
-      fn = d->c_dtype == TH_F32 ? gemm_store_f32(la, lb, check) : gemm_store(la, lb, check);
-      name = d->c_dtype == TH_F32 ? "gemm_bf16_store_f32" : "gemm_bf16_store";
+      fn = (staged || d->c_dtype == TH_F32) ? gemm_store_f32(la, lb, check) : gemm_store(la, lb, check);
+      name = staged ? "gemm_bf16_parts_f32" : d->c_dtype == TH_F32 ? "gemm_bf16_store_f32" : "gemm_bf16_store";
       break;
     case TH_EPI_GELU: fn = gemm_gelu(la, lb, check), name = "gemm_bf16_gelu"; break;
     case TH_EPI_SQUARE_LOSS: fn = gemm_square_loss(la, lb, check), name = "gemm_bf16_square_loss"; break;
@@ -98,12 +161,12 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   const size_t lds_bytes = check ? kLds : kLdsDirect;
   TH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes));
 
-  th::Builder b("gemm_bf16", 8);
+  th::Builder b("gemm_bf16", 9);
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(d->a);
   g.b = static_cast<const uint16_t*>(d->b);
   g.c = d->c;
-  g.bias = static_cast<const uint16_t*>(d->bias);
+  g.bias = staged ? nullptr : static_cast<const uint16_t*>(d->bias);
   g.aux = static_cast<const uint16_t*>(d->aux);
   g.aux_out = static_cast<uint16_t*>(d->aux_out);
   g.a_o = la == kK ? d->a_m : 1;
@@ -117,6 +180,21 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   g.k = K;
   g.tiles_m = tiles_m;
   g.tiles_n = tiles_n;
+  g.a_batch = d->a_batch;
+  g.b_batch = d->b_batch;
+  g.c_batch = d->c_batch;
+  g.c_split = 0;
+  g.ksplit = ksplit;
+  const int64_t mn = (int64_t)M * N;
+  if (staged) {
+    void* ws = nullptr;
+    if (int r = th::device_alloc((size_t)batch * splits * mn * sizeof(float), &ws)) return r;
+    b.own(ws);
+    g.c = ws;
+    g.ldc = M;
+    g.c_batch = (int64_t)splits * mn;
+    g.c_split = mn;
+  }
   const bool sums = epi == TH_EPI_SQUARE_LOSS || epi == TH_EPI_GELU_BACKWARD;
   const int blocks = tiles_m * tiles_n;
   if (sums) {
@@ -126,15 +204,25 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
     b.own(ws);
     g.partial = static_cast<float*>(ws);
   }
-  int k = b.kernel(fn, name, dim3(blocks), dim3(kThreads), (uint32_t)lds_bytes, g);
+  int k = b.kernel(fn, name, dim3(blocks, splits, batch), dim3(kThreads), (uint32_t)lds_bytes, g);
   b.ref(0, k, TH_OFFSET(GemmArgs, a));
   b.ref(1, k, TH_OFFSET(GemmArgs, b));
-  b.ref(2, k, TH_OFFSET(GemmArgs, c));
-  b.ref(3, k, TH_OFFSET(GemmArgs, bias));
+  if (!staged) b.ref(2, k, TH_OFFSET(GemmArgs, c));
+  if (!staged) b.ref(3, k, TH_OFFSET(GemmArgs, bias));
   b.ref(4, k, TH_OFFSET(GemmArgs, aux));
   b.ref(5, k, TH_OFFSET(GemmArgs, aux_out));
   for (int v : {0, 1, 2}) b.align(v, 16);
   for (int v : {3, 4, 5}) b.align(v, 8);
+  if (staged) {
+    ReduceArgs ra{static_cast<const float*>(g.c), d->c, static_cast<const uint16_t*>(d->bias),
+                  accumulate ? d->d : nullptr, d->c_ld, d->c_batch, d->d_ld ? d->d_ld : d->c_ld,
+                  d->d_ld ? d->d_batch : d->c_batch, M, N, splits, d->c_dtype};
+    int kr = b.kernel((const void*)sum_splits, "sum_splits", dim3((unsigned)((mn + 255) / 256), batch), dim3(256), 0,
+                      ra);
+    b.ref(2, kr, TH_OFFSET(ReduceArgs, c));
+    b.ref(3, kr, TH_OFFSET(ReduceArgs, bias));
+    b.ref(8, kr, TH_OFFSET(ReduceArgs, d));
+  }
   if (sums) {
     RowSumArgs rs{g.partial, static_cast<uint16_t*>(d->row_sums), M, 2 * tiles_n};
     int k2 = b.kernel((const void*)sum_parts, "sum_parts", dim3((M + 255) / 256), dim3(256), 0, rs);
@@ -145,11 +233,11 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
     int k3 = b.kernel((const void*)sum_loss, "sum_loss", dim3(1), dim3(256), 0, ls);
     b.ref(7, k3, TH_OFFSET(LossArgs, loss));
   }
-  const double mm = M, nn = N, kk = K;
+  const double mm = M, nn = N, kk = K, bb = batch;
   const double cbytes = d->c_dtype == TH_F32 ? 4 : 2;
-  double bytes = 2.0 * (mm * kk + kk * nn) + cbytes * mm * nn;
+  double bytes = bb * (2.0 * (mm * kk + kk * nn) + cbytes * mm * nn * (accumulate ? 2 : 1));
   if (epi == TH_EPI_GELU || epi == TH_EPI_GELU_BACKWARD) bytes += 2.0 * mm * nn;
-  b.work(bytes, 2.0 * mm * nn * kk, blocks);
+  b.work(bytes, 2.0 * bb * mm * nn * kk, (int64_t)blocks * splits * batch);
   *out = b.release();
   return TH_OK;
 }

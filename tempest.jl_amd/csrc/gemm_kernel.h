@@ -71,6 +71,11 @@ struct GemmArgs {
   int64_t ldc, aux_ld;
   int32_t m, n, k;
   int32_t tiles_m, tiles_n;
+  // Batches (blockIdx.z) and parts of K (blockIdx.y): product z's operands
+  // start a_batch, b_batch elements further, its result c_batch further; part
+  // s sums k in [s ksplit, (s + 1) ksplit) into the result c_split further.
+  int64_t a_batch, b_batch, c_batch, c_split;
+  int32_t ksplit;
 };
 
 // Round to bf16, nearest even (one v_cvt_pk_bf16_f32 on gfx950).
@@ -753,6 +758,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   uint16_t* As = lds;
   uint16_t* Bs = lds + 2 * kStage;
+  if (gridDim.y > 1 || gridDim.z > 1) {
+    const int64_t z = blockIdx.z, k0 = (int64_t)blockIdx.y * p.ksplit;
+    p.a += z * p.a_batch + k0 * p.a_k;
+    p.b += z * p.b_batch + k0 * p.b_k;
+    const int64_t at = z * p.c_batch + (int64_t)blockIdx.y * p.c_split;
+    if constexpr (EPI == kStoreF32) p.c = static_cast<float*>(p.c) + at;
+    else p.c = static_cast<uint16_t*>(p.c) + at;
+    p.k = (int32_t)min((int64_t)p.ksplit, (int64_t)p.k - k0);
+  }
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
   int m0 = tm * kTile, n0 = tn * kTile;

@@ -162,6 +162,8 @@ int device_alloc(size_t bytes, void** out);
 // Attention for what the matrix-core kernels do not take (attention_generic.hip).
 int build_attention_general_fwd(const th_attention_desc* d, th_launch** out);
 int build_attention_general_bwd(const th_attention_desc* d, th_launch** out);
+// Products the bf16 tile kernel does not take (gemm_general.hip).
+int build_gemm_general(const th_gemm_desc* d, th_launch** out);
 
 }  // namespace th
 

@@ -42,7 +42,9 @@ class GemmDesc(ctypes.Structure):
                 ("reserved", c_i32), ("a", c_void_p), ("a_m", c_i64), ("a_k", c_i64), ("b", c_void_p),
                 ("b_k", c_i64), ("b_n", c_i64), ("c", c_void_p), ("c_ld", c_i64), ("bias", c_void_p),
                 ("aux", c_void_p), ("aux_ld", c_i64), ("aux_out", c_void_p), ("row_sums", c_void_p),
-                ("loss", c_void_p)]
+                ("loss", c_void_p), ("batch", c_i32), ("flags", c_i32), ("a_batch", c_i64), ("b_batch", c_i64),
+                ("c_batch", c_i64), ("d", c_void_p), ("d_ld", c_i64), ("d_batch", c_i64), ("splits", c_i32),
+                ("reserved2", c_i32)]
 
 
 class AttentionDesc(ctypes.Structure):

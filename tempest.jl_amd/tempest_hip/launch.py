@@ -98,20 +98,28 @@ def tanh_layer_grad(d: int, h: int, c: int, w: int, b: int, x: int, loss: int, d
 
 # ---- op class (b) -----------------------------------------------------------
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 4
 STORE, GELU, SQUARE_LOSS, GELU_BACKWARD = 0, 1, 2, 3
+F32_FACTORS, F16_FACTORS, ACCUMULATE = 1, 2, 4  # TH_GEMM_*
 
 
 def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b_n: int, c: int, c_ld: int,
          c_dtype: int = BF16, epilogue: int = STORE, bias: int = 0, aux: int = 0, aux_ld: int = 0,
-         aux_out: int = 0, row_sums: int = 0, loss: int = 0) -> Launch:
-    """C (m x n, column-major at c_ld) = A (m x k) * B (k x n) on the matrix cores,
-    A(i, l) at a[i*a_m + l*a_k], B(l, j) at b[l*b_k + j*b_n], bf16 operands."""
-    d = _lib.GemmDesc(m=m, n=n, k=k, c_dtype=c_dtype, epilogue=epilogue, a=a, a_m=a_m, a_k=a_k, b=b, b_k=b_k,
-                      b_n=b_n, c=c, c_ld=c_ld, bias=bias or None, aux=aux or None, aux_ld=aux_ld,
-                      aux_out=aux_out or None, row_sums=row_sums or None, loss=loss or None)
-    return _built("th_build_gemm", ("a", "b", "c", "bias", "aux", "aux_out", "row_sums", "loss"),
-                  ctypes.byref(d))
+         aux_out: int = 0, row_sums: int = 0, loss: int = 0, batch: int = 1, a_batch: int = 0, b_batch: int = 0,
+         c_batch: int = 0, factors: int = BF16, d: int = 0, d_ld: int = 0, d_batch: int = 0,
+         splits: int = 0) -> Launch:
+    """C (m x n, column-major at c_ld) = A (m x k) * B (k x n) (+ D with d), for
+    each of `batch` products; A(i, l) at a[i*a_m + l*a_k], B(l, j) at
+    b[l*b_k + j*b_n], product z's operands *_batch elements further; factors
+    BF16, F32 or F16; splits: parts of K on the bf16 tile kernel (0 chosen)."""
+    flags = {BF16: 0, F32: F32_FACTORS, F16: F16_FACTORS}[factors] | (ACCUMULATE if d else 0)
+    desc = _lib.GemmDesc(m=m, n=n, k=k, c_dtype=c_dtype, epilogue=epilogue, a=a, a_m=a_m, a_k=a_k, b=b, b_k=b_k,
+                         b_n=b_n, c=c, c_ld=c_ld, bias=bias or None, aux=aux or None, aux_ld=aux_ld,
+                         aux_out=aux_out or None, row_sums=row_sums or None, loss=loss or None, batch=batch,
+                         flags=flags, a_batch=a_batch, b_batch=b_batch, c_batch=c_batch, d=d or None, d_ld=d_ld,
+                         d_batch=d_batch, splits=splits)
+    return _built("th_build_gemm", ("a", "b", "c", "bias", "aux", "aux_out", "row_sums", "loss", "d"),
+                  ctypes.byref(desc))
 
 
 # ---- op class (c) -----------------------------------------------------------

@@ -73,14 +73,18 @@ def test_product_bf16_result_with_bias_and_ldc(target, la, lb):
     assert torch.all(c[:, m:] == 0)  # nothing written between m and ldc
 
 
-def test_refuses_what_it_cannot_take(target):
+def test_shapes_route_to_the_kernel_that_takes_them(target):
+    """Plain products the tile kernel cannot take (m not a multiple of 8, no
+    unit stride) run on the general kernel; a fused epilogue there is refused."""
     import tempest_hip.launch as L
     from tempest_hip import HIPError
     t = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(HIPError, match="multiples of 8"):
-        L.gemm(60, 64, 64, t.data_ptr(), 64, 1, t.data_ptr(), 1, 64, t.data_ptr(), 64)
-    with pytest.raises(HIPError, match="unit stride"):
-        L.gemm(64, 64, 64, t.data_ptr(), 64, 2, t.data_ptr(), 1, 64, t.data_ptr(), 64)
+    p = t.data_ptr()
+    assert "gemm_bf16_store" in L.gemm(64, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
+    assert "gemm_general" in L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
+    assert "gemm_general" in L.gemm(64, 64, 32, p, 64, 2, p, 1, 64, p, 64).describe()
+    with pytest.raises(HIPError, match="fused epilogues"):
+        L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64, epilogue=L.GELU, bias=p, aux_out=p)
 
 
 def _mlp_inputs(batch, d_in, hidden, d_out, seed):
