@@ -241,8 +241,22 @@ int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out
  * its element in (phase, index) order, a scan's result there is what later
  * folds and the full outputs read, and the plain folds' results are read by
  * the once outputs after the sweep (scan_kernel, codegen/scalar.jl:350-398). */
-enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1, TH_GROUP_SCAN = 2 };
+enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1, TH_GROUP_SCAN = 2, TH_GROUP_RECURRENCE = 3 };
 #define TH_FLOOR_REVERSE 1
+
+/* A recurrence group (recurrence_kernel, codegen/scalar.jl:402-440) steps
+ * along one axis, named by the flags (TH_FLOOR_STEP(axis)), a thread per
+ * position of its parallel axes (those not in `reduced`); at each step it
+ * computes and stores its outputs in order, each over the positions of the
+ * other `reduced` axes its address mentions (the rest at zero), reading what
+ * the steps before and this one stored.  An output's `full` field says when
+ * it runs: TH_STEP_EACH at every step; TH_STEP_FIRST at the first alone (a
+ * state where it starts); TH_STEP_LAST at the last alone; TH_STEP_CARRY at
+ * every step but the last, its address already one step on (a value carried
+ * into its state for the next step).  A recurrence group has no folds but
+ * recomputed ones.  TH_FLOOR_REVERSE steps from the last position. */
+#define TH_FLOOR_STEP(axis) ((axis) << 8)
+enum { TH_STEP_EACH = 0, TH_STEP_FIRST = 1, TH_STEP_LAST = 2, TH_STEP_CARRY = 3 };
 
 /* Terms (Load, Lit, Ix, Stat, Apply of src/Compiler/IR):
  *   TH_TERM_LOAD   element index(i) of value `ref`, widened to fp32
@@ -250,8 +264,13 @@ enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1, TH_GROUP_SCAN = 2 };
  *   TH_TERM_INDEX  the fp32 value of the affine expression `index` of the
  *                  domain's zero-based positions
  *   TH_TERM_STAT   fold `ref`'s result, as `observe` reads it
- *   TH_TERM_APPLY  function `fn` of terms args[0..arity) (earlier terms) */
-enum { TH_TERM_LOAD = 0, TH_TERM_LIT = 1, TH_TERM_INDEX = 2, TH_TERM_STAT = 3, TH_TERM_APPLY = 4 };
+ *   TH_TERM_APPLY  function `fn` of terms args[0..arity) (earlier terms)
+ *   TH_TERM_RECOMPUTE  fold `ref` (phase 0) computed where it is read, as
+ *                  `observe` reads it: its body swept over the fold's own
+ *                  axes (Recomputed, src/Compiler/IR/terms.jl:70-86;
+ *                  codegen/scalar.jl:88-110) */
+enum { TH_TERM_LOAD = 0, TH_TERM_LIT = 1, TH_TERM_INDEX = 2, TH_TERM_STAT = 3, TH_TERM_APPLY = 4,
+       TH_TERM_RECOMPUTE = 5 };
 
 /* Functions, on fp32 (comparisons give 1 or 0; ifelse(c, a, b) takes a where
  * c != 0; round is to nearest, ties to even; max/min ignore a NaN operand). */
@@ -275,12 +294,20 @@ enum {
  *   TH_FOLD_LINEAR  the linear recurrence h = a h' + b from h = 0, a the
  *                   body and b the weight: state (product of the a's, h),
  *                   combined earlier-first as (a2 a1, a2 b1 + b2) (the
- *                   `chain` of test/fixtures/programs.jl:54-55) */
-enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_FOLD_SQUARE, TH_FOLD_LINEAR };
+ *                   `chain` of test/fixtures/programs.jl:54-55)
+ *   TH_FOLD_ARGMAX, _ARGMIN  the extreme of the body and where it is, the
+ *                   weight the element's index (required): state (y, i),
+ *                   combined as Base's findmax (isless: NaN the largest,
+ *                   -0.0 before 0.0) and findmin (isgreater: NaN the
+ *                   smallest), the smaller index among equals (the `Better`
+ *                   fold of src/Compiler/program/tracing.jl:735-790); indices
+ *                   are exact to 2^24 */
+enum { TH_FOLD_SUM = 0, TH_FOLD_PROD, TH_FOLD_MAX, TH_FOLD_MIN, TH_FOLD_EXP, TH_FOLD_SQUARE, TH_FOLD_LINEAR,
+       TH_FOLD_ARGMAX, TH_FOLD_ARGMIN };
 
 /* What a Stat term reads of a fold: the value (SUM, PROD, MAX, MIN; LINEAR:
- * h); the statistic (EXP: m, SQUARE: the mean, LINEAR: the product of the
- * a's); the sum (EXP: the weighted sum of exponentials, SQUARE: the squared
+ * h; ARGMAX, ARGMIN: the extreme); the statistic (EXP: m, SQUARE: the mean,
+ * LINEAR: the product of the a's; ARGMAX, ARGMIN: its index); the sum (EXP: the weighted sum of exponentials, SQUARE: the squared
  * deviations); or, for EXP, the log-sum-exp lse_shift(m) + log(sum)
  * (LOGSUMEXP, folds.jl:263). */
 enum { TH_OBSERVE_VALUE = 0, TH_OBSERVE_STATISTIC = 1, TH_OBSERVE_SUM = 2, TH_OBSERVE_LOGSUMEXP = 3 };
@@ -300,7 +327,8 @@ typedef struct th_part {
 
 /* constant + sum over k of coeff[k] * i_k, the i_k the zero-based positions,
  * + the two parts (Div and Mod atoms, unused ones TH_PART_NONE),
- * + gather_coeff * (the value of term `gather`, a load of an integer value)
+ * + gather_coeff * (the value of term `gather`, a load of an integer value,
+ * or of a float value holding integers, truncated)
  * when gather >= 0 (an Indirect atom; the atoms of IR/expressions.jl).  A
  * gathered address is clamped into its value on the device: an index out of
  * range reads or writes the nearest element instead of faulting. */
@@ -333,11 +361,14 @@ typedef struct th_term {
 typedef struct th_fold {
   int32_t kind;     /* TH_FOLD_* */
   int32_t phase;    /* >= 1; a fold's terms read statistics of earlier phases only
-                       (in a scan group: of folds earlier in (phase, index) order) */
+                       (in a scan group: of folds earlier in (phase, index) order);
+                       0: a fold recomputed where a TH_TERM_RECOMPUTE reads it */
   int32_t body;     /* term */
-  int32_t weight;   /* term, or -1; TH_FOLD_EXP and TH_FOLD_LINEAR (required) only */
+  int32_t weight;   /* term, or -1; TH_FOLD_EXP, _LINEAR, _ARGMAX, _ARGMIN (required) only */
   int32_t scan;     /* scan groups: TH_SCAN_*; 0 elsewhere */
-  int32_t reserved;
+  int32_t n_inner;  /* phase 0: the axes it sweeps, 1..TH_FLOOR_RANK - rank */
+  int64_t inner[TH_FLOOR_RANK]; /* their extents, positions rank, rank + 1, ... of
+                                   the addresses of the terms its body reaches */
 } th_fold;
 
 /* A scan group's fold: its result after the sweep (a plain fold), or at each

@@ -85,6 +85,19 @@ def fold_reduce(kind: str, y: np.ndarray, g, axes: tuple):
             p, h = p * ya[i], ya[i] * h + ga[i]
         shape = tuple(1 if k in axes else y.shape[k] for k in range(y.ndim))
         return {"value": h.reshape(shape), "statistic": p.reshape(shape)}
+    if kind in ("argmax", "argmin"):
+        # In order over the folded positions, first axis fastest, by the
+        # extreme's combine (each pair of elements ordered alike whatever the order).
+        yy = np.moveaxis(y, axes, tuple(range(len(axes))))
+        gg = np.moveaxis(np.broadcast_to(g, y.shape), axes, tuple(range(len(axes))))
+        cnt = int(np.prod(yy.shape[:len(axes)]))
+        ya = yy.reshape((cnt,) + yy.shape[len(axes):], order="F")
+        ga = gg.reshape((cnt,) + gg.shape[len(axes):], order="F")
+        st = tuple(np.full(ya.shape[1:], v) for v in _INIT[kind])
+        for i in range(cnt):
+            st = _step(kind, st, ya[i], ga[i])
+        shape = tuple(1 if k in axes else y.shape[k] for k in range(y.ndim))
+        return {"value": st[0].reshape(shape), "statistic": st[1].reshape(shape)}
     if kind == "square":
         n = np.prod([y.shape[a] for a in axes]) if y.size else 0
         with np.errstate(invalid="ignore"):
@@ -96,6 +109,7 @@ def fold_reduce(kind: str, y: np.ndarray, g, axes: tuple):
 def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) -> dict[str, np.ndarray]:
     """The group's written values, given every value's contents (1-D);
     rounded to the values' types, or Float64 with ``rounded=False``."""
+    arrays = dict(arrays)
     ext = tuple(spec["extents"])
     rank = len(ext)
     idx = np.indices(ext, dtype=np.int64)  # idx[k]: position along axis k
@@ -104,8 +118,8 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
     out = {o["value"]: np.array(arrays[o["value"]], dtype=np.float64, copy=True) for o in spec["outputs"]}
 
     def addr(t, at, memo=None, length=None):
-        a = np.full(at[0].shape, t["constant"], dtype=np.int64)
-        for k in range(rank):
+        a = np.full(np.shape(at[0]), t["constant"], dtype=np.int64)
+        for k in range(len(at)):  # past the domain's rank: a recomputed fold's own axes
             if t["coeffs"][k]:
                 a = a + t["coeffs"][k] * at[k]
         for kind, inner, dv, cf, c in t.get("parts", ()):  # Div (1) and Mod (2) atoms: floor division
@@ -133,6 +147,21 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
             r = addr(t, at, memo).astype(np.float64)
         elif op == "stat":
             r = stats[t["ref"]][t["observe"]]
+        elif op == "recompute":
+            # The fold over its own axes, appended after the positions' shape
+            # (Recomputed, codegen/scalar.jl:88-110).
+            f = spec["folds"][t["ref"]]
+            inner = tuple(f["inner"])
+            shape = np.broadcast_shapes(*[np.shape(a) for a in at])
+            grids = np.indices(inner, dtype=np.int64)
+            ext_at = [np.broadcast_to(np.reshape(a, np.shape(a) + (1,) * len(inner)), shape + inner) for a in at]
+            ext_at += [np.broadcast_to(grids[q].reshape((1,) * len(shape) + inner), shape + inner)
+                       for q in range(len(inner))]
+            inner_memo: dict = {}
+            y = np.broadcast_to(term(f["body"], ext_at, inner_memo), shape + inner).astype(np.float64)
+            g = None if f["weight"] < 0 else np.broadcast_to(term(f["weight"], ext_at, inner_memo), shape + inner)
+            st = fold_reduce(f["kind"], y, g, tuple(range(len(shape), len(shape) + len(inner))))
+            r = st[t["observe"]].reshape(shape)
         else:
             a = [term(j, at, memo) for j in t["args"]]
             fn = t["fn"]
@@ -142,6 +171,8 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
         return r
 
     full_at = [idx[k] for k in range(rank)]
+    if spec["kind"] == "recurrence":
+        return _recurrence(spec, arrays, out, addr, term, rounded)
     if spec["kind"] == "scan":
         return _scan(spec, arrays, out, idx, addr, term, stats, rounded)
     if spec["kind"] == "reduction":
@@ -178,6 +209,43 @@ def evaluate(spec: dict, arrays: dict[str, np.ndarray], rounded: bool = True) ->
 
 
 
+def _recurrence(spec, arrays, out, addr, term, rounded):
+    """A recurrence group (recurrence_kernel, codegen/scalar.jl:402-440): its
+    steps in order, at each its outputs in order over the other reduced axes
+    their addresses mention, the loads reading what was stored so far."""
+    ext = tuple(spec["extents"])
+    rank = len(ext)
+    step, reverse = spec["step"], spec.get("reverse", False)
+    E = ext[step]
+    # Loads read the written values as they are written.
+    for n, a in out.items():
+        arrays[n] = a
+    for s_ in range(E):
+        pos = E - 1 - s_ if reverse else s_
+        for o in spec["outputs"]:
+            rule = o["full"]
+            if (rule == 1 and s_ != 0) or (rule == 2 and s_ != E - 1) or (rule == 3 and s_ == E - 1):
+                continue
+            ranges = []
+            for k in range(rank):
+                mentioned = o["coeffs"][k] != 0 or any(q[1][k] for q in o.get("parts", ()) if q[3])
+                if k == step:
+                    ranges.append([pos])
+                elif k not in spec["reduced"] or mentioned:
+                    ranges.append(range(ext[k]))
+                else:
+                    ranges.append([0])
+            at = list(np.meshgrid(*[np.asarray(r, dtype=np.int64) for r in ranges], indexing="ij"))
+            memo: dict = {}
+            v = np.broadcast_to(term(o["term"], at, memo), at[0].shape).astype(np.float64)
+            dst = out[o["value"]]
+            dst[addr(o, at, memo, len(dst)).ravel()] = v.ravel()
+    if not rounded:
+        return out
+    return {n: (bf16_round(a.astype(np.float32)) if spec["values"][n][0] == "bf16" else a.astype(np.float32))
+            for n, a in out.items()}
+
+
 def _observe(kind, st):
     if kind in ("sum", "prod", "max", "min"):
         return {"value": st[0]}
@@ -189,10 +257,35 @@ def _observe(kind, st):
     if kind == "square":
         n, mean, q = st
         return {"statistic": np.where(n > 0, mean, np.nan), "sum": q}
+    if kind in ("argmax", "argmin"):
+        return {"value": st[0], "statistic": st[1]}
     return {"value": st[1], "statistic": st[0]}  # linear: (product, h)
 
 
+def lesser(x, y):
+    """Base's isless in comparisons alone (program/tracing.jl:788-792): NaN
+    the largest, -0.0 before 0.0."""
+    with np.errstate(divide="ignore"):
+        return np.where(np.isnan(x), False, np.isnan(y) | (x < y) | ((x == y) & (1.0 / x < 1.0 / y)))
+
+
+def greater(x, y):
+    """Base's isgreater, the order findmin keeps: NaN the smallest."""
+    with np.errstate(divide="ignore"):
+        return np.where(np.isnan(x), False, np.isnan(y) | (y < x) | ((x == y) & (1.0 / y < 1.0 / x)))
+
+
+def better(largest, a, b):
+    """Of two (element, index) states the one an extreme keeps, the earlier of
+    equals (`Better`, program/tracing.jl:779-784)."""
+    precedes, follows = (lesser(a[0], b[0]), lesser(b[0], a[0])) if largest else (greater(a[0], b[0]), greater(b[0], a[0]))
+    t = precedes | (~follows & (b[1] < a[1]))
+    return np.where(t, b[0], a[0]), np.where(t, b[1], a[1])
+
+
 def _step(kind, st, y, g):
+    if kind in ("argmax", "argmin"):
+        return better(kind == "argmax", st, (y, g))
     if kind == "sum":
         return (st[0] + y,)
     if kind == "prod":
@@ -218,7 +311,7 @@ def _step(kind, st, y, g):
 
 
 _INIT = {"sum": (0.0,), "prod": (1.0,), "max": (-np.inf,), "min": (np.inf,), "exp": (-np.inf, 0.0),
-         "square": (0.0, 0.0, 0.0), "linear": (1.0, 0.0)}
+         "square": (0.0, 0.0, 0.0), "linear": (1.0, 0.0), "argmax": (-np.inf, np.inf), "argmin": (np.inf, np.inf)}
 
 
 def _scan(spec, arrays, out, idx, addr, term, stats, rounded):

@@ -75,14 +75,17 @@ const char* fn_name(int fn) {
 
 // Components of a fold's state.
 int state_size(int kind) {
-  return kind == TH_FOLD_EXP || kind == TH_FOLD_LINEAR ? 2 : kind == TH_FOLD_SQUARE ? 3 : 1;
+  return kind == TH_FOLD_EXP || kind == TH_FOLD_LINEAR || kind == TH_FOLD_ARGMAX || kind == TH_FOLD_ARGMIN ? 2
+         : kind == TH_FOLD_SQUARE ? 3 : 1;
 }
 
 bool observe_ok(int kind, int obs) {
   switch (kind) {
     case TH_FOLD_EXP: return obs == TH_OBSERVE_STATISTIC || obs == TH_OBSERVE_SUM || obs == TH_OBSERVE_LOGSUMEXP;
     case TH_FOLD_SQUARE: return obs == TH_OBSERVE_STATISTIC || obs == TH_OBSERVE_SUM;
-    case TH_FOLD_LINEAR: return obs == TH_OBSERVE_VALUE || obs == TH_OBSERVE_STATISTIC;
+    case TH_FOLD_LINEAR:
+    case TH_FOLD_ARGMAX:
+    case TH_FOLD_ARGMIN: return obs == TH_OBSERVE_VALUE || obs == TH_OBSERVE_STATISTIC;
     default: return obs == TH_OBSERVE_VALUE;
   }
 }
@@ -99,6 +102,8 @@ std::string flt(float x) {
 struct Plan {
   const th_floor_desc* d = nullptr;
   bool reduction = false;        // a reduction or a scan group: items sweep their folded axes
+  bool recurrence = false;       // a recurrence group: a thread per item steps along `step`
+  int step = -1;                 // the recurrence's step axis
   bool scan = false;             // a scan group: one thread per item, in order
   bool reverse = false;
   std::vector<int> order;        // a scan group's folds in (phase, index) order
@@ -174,20 +179,33 @@ bool has_parts(const th_affine& a) { return a.part[0].kind != TH_PART_NONE || a.
 
 std::vector<char> reach(const th_floor_desc* d, const std::vector<int>& roots);
 
+// The step axis of a recurrence group, from its flags.
+int step_axis(const th_floor_desc* d) { return (d->flags >> 8) & 7; }
+
 int validate(const th_floor_desc* d) {
   TH_REQUIRE(d != nullptr, "th_build_floor: null description");
-  TH_REQUIRE(d->kind == TH_GROUP_POINTWISE || d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN,
+  TH_REQUIRE(d->kind == TH_GROUP_POINTWISE || d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN ||
+                 d->kind == TH_GROUP_RECURRENCE,
              "th_build_floor: unknown group kind");
-  TH_REQUIRE(d->flags == 0 || (d->kind == TH_GROUP_SCAN && d->flags == TH_FLOOR_REVERSE),
-             "th_build_floor: only a scan group runs in reverse");
+  const bool rec = d->kind == TH_GROUP_RECURRENCE;
+  TH_REQUIRE(d->flags == 0 || (d->kind == TH_GROUP_SCAN && d->flags == TH_FLOOR_REVERSE) ||
+                 (rec && (d->flags & ~(TH_FLOOR_REVERSE | TH_FLOOR_STEP(7))) == 0),
+             "th_build_floor: only a scan or a recurrence group runs in reverse");
   TH_REQUIRE(d->rank >= 1 && d->rank <= kRank, "th_build_floor: rank must be 1..4");
   for (int k = 0; k < d->rank; ++k) TH_REQUIRE(d->extents[k] >= 0, "th_build_floor: negative extent");
   const uint32_t all = (1u << d->rank) - 1;
-  if (d->kind != TH_GROUP_POINTWISE) {
+  TH_REQUIRE(d->n_folds == 0 || d->folds, "th_build_floor: null folds");
+  int stepped = 0;  // folds run in phases (not recomputed where read)
+  for (int f = 0; f < d->n_folds; ++f) stepped += d->folds[f].phase >= 1;
+  if (d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN) {
     TH_REQUIRE(d->reduced != 0 && (d->reduced & ~all) == 0, "th_build_floor: a reduction folds some of its axes");
-    TH_REQUIRE(d->n_folds >= 1 && d->folds, "th_build_floor: a reduction group has folds");
+    TH_REQUIRE(stepped >= 1, "th_build_floor: a reduction group has folds");
+  } else if (rec) {
+    TH_REQUIRE(step_axis(d) < d->rank && (d->reduced >> step_axis(d) & 1) && (d->reduced & ~all) == 0,
+               "th_build_floor: a recurrence steps along one of its reduced axes");
+    TH_REQUIRE(stepped == 0, "th_build_floor: a recurrence group's folds are recomputed where read");
   } else {
-    TH_REQUIRE(d->reduced == 0 && d->n_folds == 0, "th_build_floor: a pointwise group folds nothing");
+    TH_REQUIRE(d->reduced == 0 && stepped == 0, "th_build_floor: a pointwise group folds nothing");
   }
   TH_REQUIRE(d->n_values >= 1 && d->values, "th_build_floor: no values");
   TH_REQUIRE(d->n_terms >= 1 && d->terms, "th_build_floor: no terms");
@@ -206,13 +224,14 @@ int validate(const th_floor_desc* d) {
     if (a.gather < 0) return true;
     if (a.gather >= before || a.gather >= d->n_terms) return false;
     const th_term& g = d->terms[a.gather];
-    return g.op == TH_TERM_LOAD && is_int(d->values[g.ref].dtype) && g.ref >= 0 && g.ref < d->n_values;
+    // Integers, or floats holding integers (an extreme's index), truncated.
+    return g.op == TH_TERM_LOAD && g.ref >= 0 && g.ref < d->n_values;
   };
   for (int t = 0; t < d->n_terms; ++t) {
     const th_term& m = d->terms[t];
     std::string at = "th_build_floor: term " + std::to_string(t) + ": ";
     TH_REQUIRE(m.op == TH_TERM_LOAD ? gather_ok(m.index, t) : m.index.gather < 0,
-               at + "a gathered address adds an earlier load of integers");
+               at + "a gathered address adds an earlier load");
     TH_REQUIRE(parts_ok(m.index), at + "a div or mod atom takes a positive divisor");
     switch (m.op) {
       case TH_TERM_LOAD:
@@ -224,8 +243,16 @@ int validate(const th_floor_desc* d) {
       case TH_TERM_INDEX:
         break;
       case TH_TERM_STAT:
-        TH_REQUIRE(d->kind != TH_GROUP_POINTWISE, at + "statistic in a pointwise group");
+        TH_REQUIRE(d->kind != TH_GROUP_POINTWISE && !rec, at + "statistic in a pointwise or recurrence group");
         TH_REQUIRE(m.ref >= 0 && m.ref < d->n_folds, at + "statistic of no fold");
+        TH_REQUIRE(d->folds[m.ref].phase >= 1, at + "a statistic reads a fold run in a phase");
+        TH_REQUIRE(observe_ok(d->folds[m.ref].kind, m.observe), at + "the fold has no such observation");
+        break;
+      case TH_TERM_RECOMPUTE:
+        TH_REQUIRE(m.ref >= 0 && m.ref < d->n_folds, at + "recomputes no fold");
+        TH_REQUIRE(d->folds[m.ref].phase == 0, at + "a recomputed fold has phase 0");
+        TH_REQUIRE(d->folds[m.ref].body < t && d->folds[m.ref].weight < t,
+                   at + "a recomputed fold's body is an earlier term");
         TH_REQUIRE(observe_ok(d->folds[m.ref].kind, m.observe), at + "the fold has no such observation");
         break;
       case TH_TERM_APPLY: {
@@ -242,13 +269,20 @@ int validate(const th_floor_desc* d) {
   for (int f = 0; f < d->n_folds; ++f) {
     const th_fold& x = d->folds[f];
     std::string at = "th_build_floor: fold " + std::to_string(f) + ": ";
-    TH_REQUIRE(x.kind >= TH_FOLD_SUM && x.kind <= TH_FOLD_LINEAR, at + "unknown fold");
-    TH_REQUIRE(x.phase >= 1, at + "phases start at 1");
+    TH_REQUIRE(x.kind >= TH_FOLD_SUM && x.kind <= TH_FOLD_ARGMIN, at + "unknown fold");
+    const bool weighted = x.kind == TH_FOLD_EXP || x.kind == TH_FOLD_LINEAR || x.kind == TH_FOLD_ARGMAX ||
+                          x.kind == TH_FOLD_ARGMIN;
+    TH_REQUIRE(x.phase >= 1 || (x.phase == 0 && x.scan == TH_SCAN_NONE && x.n_inner >= 1 &&
+                                 d->rank + x.n_inner <= kRank),
+               at + "phases start at 1; a recomputed fold (phase 0) sweeps 1..4 - rank axes of its own");
+    if (x.phase == 0)
+      for (int k = 0; k < x.n_inner; ++k) TH_REQUIRE(x.inner[k] >= 0, at + "negative extent");
     TH_REQUIRE(x.body >= 0 && x.body < d->n_terms, at + "no body");
-    TH_REQUIRE(x.weight == -1 || ((x.kind == TH_FOLD_EXP || x.kind == TH_FOLD_LINEAR) && x.weight >= 0 &&
-                                  x.weight < d->n_terms),
-               at + "only the exponential and linear folds take a weight");
+    TH_REQUIRE(x.weight == -1 || (weighted && x.weight >= 0 && x.weight < d->n_terms),
+               at + "only the exponential, linear and extreme folds take a weight");
     TH_REQUIRE(x.kind != TH_FOLD_LINEAR || x.weight >= 0, at + "the linear fold's weight is its offset b");
+    TH_REQUIRE((x.kind != TH_FOLD_ARGMAX && x.kind != TH_FOLD_ARGMIN) || x.weight >= 0,
+               at + "an extreme's weight is its element's index");
     TH_REQUIRE(x.scan == TH_SCAN_NONE || (d->kind == TH_GROUP_SCAN && x.scan <= TH_SCAN_EXCLUSIVE),
                at + "only a scan group's folds scan");
   }
@@ -257,20 +291,81 @@ int validate(const th_floor_desc* d) {
     std::string at = "th_build_floor: output " + std::to_string(o) + ": ";
     TH_REQUIRE(x.value >= 0 && x.value < d->n_values, at + "no value");
     TH_REQUIRE(x.term >= 0 && x.term < d->n_terms, at + "no term");
-    TH_REQUIRE(x.full == 0 || x.full == 1, at + "full is 0 or 1");
-    TH_REQUIRE(x.full == 1 || d->kind != TH_GROUP_POINTWISE, at + "a pointwise group writes every position");
-    // Once outputs are written with the folded positions at zero, also when
-    // the folded axes are empty.
-    int64_t ext[kRank];
-    for (int k = 0; k < d->rank; ++k) ext[k] = (!x.full && (d->reduced >> k & 1)) ? 1 : d->extents[k];
-    TH_REQUIRE(in_box(x.index, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
-    TH_REQUIRE(gather_ok(x.index, d->n_terms), at + "a gathered address adds a load of integers");
+    if (rec) {
+      TH_REQUIRE(x.full >= TH_STEP_EACH && x.full <= TH_STEP_CARRY, at + "a recurrence output's rule is 0..3");
+      TH_REQUIRE(x.accumulate == 0, at + "a recurrence stores, it does not accumulate");
+      // Over the parallel axes, the step axis, and the other reduced axes its
+      // address mentions (the rest at zero).  A value carried into its state
+      // is written at every step but the last, its address one step on.
+      const int sa = step_axis(d);
+      int64_t ext[kRank];
+      th_affine a = x.index;
+      for (int k = 0; k < d->rank; ++k) {
+        bool mentioned = a.coeff[k] != 0;
+        for (const th_part& q : a.part) mentioned |= q.kind != TH_PART_NONE && q.coeff != 0 && q.inner[k] != 0;
+        ext[k] = (d->reduced >> k & 1) && k != sa && !mentioned ? std::min<int64_t>(d->extents[k], 1) : d->extents[k];
+      }
+      if (x.full == TH_STEP_CARRY) {
+        for (const th_part& q : a.part)
+          TH_REQUIRE(q.kind == TH_PART_NONE || q.coeff == 0 || q.inner[sa] == 0,
+                     at + "a carried value's div or mod atoms do not move along the steps");
+        ext[sa] = std::max<int64_t>(d->extents[sa] - 1, 0);
+        if (d->flags & TH_FLOOR_REVERSE) a.constant += a.coeff[sa];  // written at steps E-1 .. 1
+      }
+      TH_REQUIRE(in_box(a, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
+    } else {
+      TH_REQUIRE(x.full == 0 || x.full == 1, at + "full is 0 or 1");
+      TH_REQUIRE(x.full == 1 || d->kind != TH_GROUP_POINTWISE, at + "a pointwise group writes every position");
+      // Once outputs are written with the folded positions at zero, also when
+      // the folded axes are empty.
+      int64_t ext[kRank];
+      for (int k = 0; k < d->rank; ++k) ext[k] = (!x.full && (d->reduced >> k & 1)) ? 1 : d->extents[k];
+      TH_REQUIRE(in_box(x.index, ext, d->rank, d->values[x.value].length), at + "writes outside its value");
+    }
+    TH_REQUIRE(gather_ok(x.index, d->n_terms), at + "a gathered address adds a load");
     TH_REQUIRE(parts_ok(x.index), at + "a div or mod atom takes a positive divisor");
     TH_REQUIRE(!is_int(d->values[x.value].dtype), at + "integer values are only read");
     TH_REQUIRE(x.accumulate == 0 || (x.accumulate == 1 && d->values[x.value].dtype == TH_F32),
                at + "accumulating outputs are fp32");
   }
-  if (d->kind != TH_GROUP_POINTWISE) {
+  // Terms a recomputed fold's body reaches take the fold's own axes, at
+  // positions rank, rank + 1, ...; no other term or output moves along them.
+  std::vector<int> extra(d->n_terms, 0);
+  for (int f = 0; f < d->n_folds; ++f) {
+    const th_fold& x = d->folds[f];
+    if (x.phase != 0) continue;
+    std::vector<int> roots{x.body};
+    if (x.weight >= 0) roots.push_back(x.weight);
+    const std::vector<char> r = reach(d, roots);
+    int64_t ext[kRank];
+    for (int k = 0; k < kRank; ++k) ext[k] = k < d->rank ? d->extents[k] : (k - d->rank < x.n_inner ? x.inner[k - d->rank] : 1);
+    for (int t = 0; t < d->n_terms; ++t) {
+      if (!r[t]) continue;
+      const th_term& m = d->terms[t];
+      TH_REQUIRE(m.op != TH_TERM_RECOMPUTE, "th_build_floor: fold " + std::to_string(f) +
+                                                ": a recomputed fold's body recomputes no other fold");
+      extra[t] = std::max(extra[t], x.n_inner);
+      if (m.op == TH_TERM_LOAD)
+        TH_REQUIRE(in_box(m.index, ext, d->rank + x.n_inner, d->values[m.ref].length),
+                   "th_build_floor: term " + std::to_string(t) + ": load outside its value over fold " +
+                       std::to_string(f) + "'s axes");
+    }
+  }
+  auto beyond = [&](const th_affine& a, int allowed) {
+    for (int k = d->rank + allowed; k < kRank; ++k)
+      if (a.coeff[k] != 0) return true;
+    for (const th_part& q : a.part)
+      for (int k = d->rank; k < kRank; ++k)
+        if (q.kind != TH_PART_NONE && q.inner[k] != 0) return true;
+    return false;
+  };
+  for (int t = 0; t < d->n_terms; ++t)
+    TH_REQUIRE(!beyond(d->terms[t].index, extra[t]),
+               "th_build_floor: term " + std::to_string(t) + ": an address moves along an axis beyond the domain");
+  for (int o = 0; o < d->n_outputs; ++o)
+    TH_REQUIRE(!beyond(d->outputs[o].index, 0),
+               "th_build_floor: output " + std::to_string(o) + ": an address moves along an axis beyond the domain");
+  if (d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN) {
     // Loads evaluated outside the sweep: those whose address does not move
     // along the folded axes (hoisted, read by every item even when the folded
     // positions are empty) and those the once outputs read (with the folded
@@ -335,7 +430,9 @@ int64_t nextpow2(int64_t x) {
 int plan(const th_floor_desc* d, Plan& pl) {
   if (int r = validate(d)) return r;
   pl.d = d;
-  pl.reduction = d->kind != TH_GROUP_POINTWISE;
+  pl.reduction = d->kind == TH_GROUP_REDUCTION || d->kind == TH_GROUP_SCAN;
+  pl.recurrence = d->kind == TH_GROUP_RECURRENCE;
+  pl.step = pl.recurrence ? step_axis(d) : -1;
   pl.scan = d->kind == TH_GROUP_SCAN;
   pl.reverse = (d->flags & TH_FLOOR_REVERSE) != 0;
   pl.rank = d->rank;
@@ -352,6 +449,8 @@ int plan(const th_floor_desc* d, Plan& pl) {
   // Div and mod atoms break the run of W consecutive positions: width 1, as a gather.
   for (int t = 0; t < nt; ++t) pl.gathers |= has_parts(d->terms[t].index);
   for (int o = 0; o < d->n_outputs; ++o) pl.gathers |= has_parts(d->outputs[o].index);
+  // A recomputed fold sweeps its own axes in a loop: width 1, as a gather.
+  for (int t = 0; t < nt; ++t) pl.gathers |= d->terms[t].op == TH_TERM_RECOMPUTE;
   // Which terms move along the swept positions.
   pl.dep.assign(nt, 0);
   for (int t = 0; t < nt; ++t) {
@@ -370,6 +469,13 @@ int plan(const th_floor_desc* d, Plan& pl) {
       for (int j = 0; j < arity(m.fn); ++j) pl.dep[t] |= pl.dep[m.args[j]];
     } else if (m.op == TH_TERM_STAT && d->kind == TH_GROUP_SCAN) {
       pl.dep[t] = d->folds[m.ref].scan != TH_SCAN_NONE;  // a scan's result moves along the sweep
+    } else if (m.op == TH_TERM_RECOMPUTE) {
+      // Its body's own axes are not the swept ones: it moves where its body does.
+      const th_fold& f = d->folds[m.ref];
+      std::vector<int> roots{f.body};
+      if (f.weight >= 0) roots.push_back(f.weight);
+      const std::vector<char> r = reach(d, roots);
+      for (int k = 0; k < t; ++k) pl.dep[t] |= r[k] && pl.dep[k];
     }
   }
   pl.read.assign(d->n_values, 0);
@@ -380,12 +486,13 @@ int plan(const th_floor_desc* d, Plan& pl) {
 
   if (pl.scan) {
     // Folds in (phase, index) order; a fold reads only the folds before it.
-    for (int f = 0; f < d->n_folds; ++f) pl.order.push_back(f);
+    for (int f = 0; f < d->n_folds; ++f)
+      if (d->folds[f].phase >= 1) pl.order.push_back(f);
     std::stable_sort(pl.order.begin(), pl.order.end(),
                      [&](int a, int b) { return d->folds[a].phase < d->folds[b].phase; });
-    std::vector<int> rank_of(d->n_folds);
+    std::vector<int> rank_of(d->n_folds, -1);
     for (size_t j = 0; j < pl.order.size(); ++j) rank_of[pl.order[j]] = (int)j;
-    for (int f = 0; f < d->n_folds; ++f) {
+    for (int f : pl.order) {
       std::vector<int> roots{d->folds[f].body};
       if (d->folds[f].weight >= 0) roots.push_back(d->folds[f].weight);
       std::vector<char> r = reach(d, roots);
@@ -433,10 +540,12 @@ int plan(const th_floor_desc* d, Plan& pl) {
       pl.qn = pl.count;
     }
   } else if (pl.reduction) {
-    for (int f = 0; f < d->n_folds; ++f) pl.phases.push_back(d->folds[f].phase);
+    for (int f = 0; f < d->n_folds; ++f)
+      if (d->folds[f].phase >= 1) pl.phases.push_back(d->folds[f].phase);
     std::sort(pl.phases.begin(), pl.phases.end());
     pl.phases.erase(std::unique(pl.phases.begin(), pl.phases.end()), pl.phases.end());
     for (int f = 0; f < d->n_folds; ++f) {
+      if (d->folds[f].phase == 0) continue;
       std::vector<int> roots{d->folds[f].body};
       if (d->folds[f].weight >= 0) roots.push_back(d->folds[f].weight);
       TH_REQUIRE(max_stat_phase(d, reach(d, roots)) < d->folds[f].phase,
@@ -487,6 +596,17 @@ int plan(const th_floor_desc* d, Plan& pl) {
         pl.iters = (int)iters;
       }
     }
+  } else if (pl.recurrence) {
+    // A thread per position of the parallel axes, stepping in order.
+    pl.kept.clear();
+    pl.swept.clear();
+    for (int k = 0; k < pl.rank; ++k) ((d->reduced >> k & 1) ? pl.swept : pl.kept).push_back(k);
+    pl.items = 1;
+    for (int k : pl.kept) pl.items *= pl.E[k];
+    pl.W = 1;
+    pl.qn = pl.items;
+    pl.S = 256;
+    pl.L = 1;
   } else {
     pl.kept.clear();
     for (int k = 0; k < pl.rank; ++k) pl.kept.push_back(k);
@@ -522,8 +642,8 @@ bool vector_access(const Plan& pl, int value, const th_affine& a) {
 std::string affine(const Plan& pl, const th_affine& a) {
   std::ostringstream s;
   s << "(" << a.constant << "L";
-  for (int k = 0; k < pl.rank; ++k)
-    if (a.coeff[k] != 0 && pl.E[k] > 1) s << " + " << a.coeff[k] << "L * i" << k;
+  for (int k = 0; k < kRank; ++k)
+    if (a.coeff[k] != 0 && (k >= pl.rank || pl.E[k] > 1)) s << " + " << a.coeff[k] << "L * i" << k;
   for (const th_part& q : a.part) {
     if (q.kind == TH_PART_NONE || q.coeff == 0) continue;
     std::ostringstream in;
@@ -631,6 +751,25 @@ __device__ __forceinline__ void th_exp_comb(float& m, float& s, float m2, float 
 // The linear recurrence h = a h' + b: state (product of the a's, h).
 __device__ __forceinline__ void th_lin_step(float& p, float& h, float a, float b) { p *= a; h = fmaf(a, h, b); }
 __device__ __forceinline__ void th_lin_comb(float& p, float& h, float p2, float h2) { h = fmaf(p2, h, h2); p *= p2; }
+// The extreme and where it is: state (y, i).  Base's isless (NaN the
+// largest, -0.0 before 0.0) for findmax, its isgreater (NaN the smallest) for
+// findmin, in comparisons alone; the smaller index among equals.
+__device__ __forceinline__ bool th_lesser(float x, float y) {
+  return x != x ? false : ((y != y) || x < y || (x == y && 1.0f / x < 1.0f / y));
+}
+__device__ __forceinline__ bool th_greater(float x, float y) {
+  return x != x ? false : ((y != y) || y < x || (x == y && 1.0f / y < 1.0f / x));
+}
+__device__ __forceinline__ void th_amax_comb(float& y, float& i, float y2, float i2) {
+  const bool t = th_lesser(y, y2) || (!th_lesser(y2, y) && i2 < i);
+  y = t ? y2 : y;
+  i = t ? i2 : i;
+}
+__device__ __forceinline__ void th_amin_comb(float& y, float& i, float y2, float i2) {
+  const bool t = th_greater(y, y2) || (!th_greater(y2, y) && i2 < i);
+  y = t ? y2 : y;
+  i = t ? i2 : i;
+}
 // Relative{Square}: state (n, mean, squared deviations), Welford's step and
 // Chan's combination.
 __device__ __forceinline__ void th_sq_step(float& n, float& a, float& q, float y) {
@@ -698,6 +837,14 @@ __device__ __forceinline__ void th_exp_step(th_v& m, th_v& s, th_v y, th_v g) {
   for (int j = 0; j < 4; ++j) { float a = m[j], b = s[j]; th_exp_step(a, b, y[j], g[j]); m[j] = a; s[j] = b; }
 }
 __device__ __forceinline__ void th_lin_step(th_v& p, th_v& h, th_v a, th_v b) { p *= a; h = a * h + b; }
+__device__ __forceinline__ void th_amax_comb(th_v& y, th_v& i, th_v y2, th_v i2) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { float a = y[j], b = i[j]; th_amax_comb(a, b, y2[j], i2[j]); y[j] = a; i[j] = b; }
+}
+__device__ __forceinline__ void th_amin_comb(th_v& y, th_v& i, th_v y2, th_v i2) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { float a = y[j], b = i[j]; th_amin_comb(a, b, y2[j], i2[j]); y[j] = a; i[j] = b; }
+}
 __device__ __forceinline__ void th_sq_step(th_v& n, th_v& a, th_v& q, th_v y) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) { float x = n[j], b = a[j], c = q[j]; th_sq_step(x, b, c, y[j]); n[j] = x; a[j] = b; q[j] = c; }
@@ -722,7 +869,10 @@ class Writer {
     o << "// tempest-hip floor: " << describe() << "\n";
     o << kPrelude << (pl_.W > 1 ? kVector : kScalar);
     o << "struct th_args { void* p[" << (d_->n_values + (pl_.reduction ? d_->n_folds : 0)) << "]; };\n";
-    if (!pl_.reduction) {
+    if (pl_.recurrence) {
+      stages.push_back({base + "_0", -1});
+      recurrence(stages.back().name);
+    } else if (!pl_.reduction) {
       stages.push_back({base + "_0", -1});
       pointwise(stages.back().name);
     } else if (pl_.scan) {
@@ -744,7 +894,10 @@ class Writer {
 
   std::string describe() const {
     std::ostringstream s;
-    if (!pl_.reduction) {
+    if (pl_.recurrence) {
+      s << "recurrence, " << pl_.items << " items stepping " << pl_.E[pl_.step] << " positions of axis " << pl_.step
+        << (pl_.reverse ? ", reversed" : "");
+    } else if (!pl_.reduction) {
       s << "pointwise, " << pl_.items << " positions, width " << pl_.W;
     } else if (pl_.scan) {
       s << "scan, " << pl_.items << " items of " << pl_.count << " positions, "
@@ -868,6 +1021,11 @@ class Writer {
       }
       std::string n = "t" + std::to_string(uid_++);
       const th_term& m = d_->terms[t];
+      if (m.op == TH_TERM_RECOMPUTE) {
+        recompute(ind, t, n);
+        names[t] = vec ? "th_splat(" + n + ")" : n;
+        continue;
+      }
       if (m.op == TH_TERM_LOAD && is_int(d_->values[m.ref].dtype)) {
         // An integer: kept as such for the addresses that gather by it.
         o_ << ind << "const long " << n << " = " << term_expr(t, false, false, names) << ";\n";
@@ -877,7 +1035,89 @@ class Writer {
       }
       o_ << ind << "const " << ty << " " << n << " = " << term_expr(t, vec, cached, names) << ";\n";
       names[t] = n;
+      // A float load an address gathers by (groups that gather run at width 1).
+      if (m.op == TH_TERM_LOAD && !vec) gvar_[t] = "((long)" + n + ")";
     }
+  }
+
+  // A fold computed where it is read (Recomputed, codegen/scalar.jl:88-110):
+  // a loop over its own axes (positions rank, rank + 1, ...), its body
+  // computed afresh at each, then the observation read into `n`.
+  void recompute(const std::string& ind, int t, const std::string& n) {
+    const th_term& m = d_->terms[t];
+    const th_fold& f = d_->folds[m.ref];
+    const int K = state_size(f.kind);
+    const std::string base = "r" + std::to_string(uid_++), j = "j" + base;
+    std::vector<std::string> c = comps(base, K);
+    for (int k = 0; k < K; ++k) o_ << ind << "float " << c[k] << " = " << identity(f.kind, k) << ";\n";
+    int64_t count = 1;
+    for (int q = 0; q < f.n_inner; ++q) count *= f.inner[q];
+    o_ << ind << "for (long " << j << " = 0; " << j << " < " << count << "L; ++" << j << ") {\n";
+    const std::string in = ind + "  ";
+    o_ << in << "long r = " << j << ";\n";
+    for (int q = 0; q < f.n_inner; ++q) {
+      const int k = pl_.rank + q;
+      if (q + 1 == f.n_inner) o_ << in << "i" << k << " = r;\n";
+      else o_ << in << "i" << k << " = r % " << f.inner[q] << "L; r /= " << f.inner[q] << "L;\n";
+    }
+    std::vector<int> roots{f.body};
+    if (f.weight >= 0) roots.push_back(f.weight);
+    std::map<int, std::string> inner;
+    const std::map<int, std::string> saved = gvar_;
+    emit(in, reach(d_, roots), false, false, inner, nullptr);
+    o_ << in << step_stmt(f.kind, c, inner.at(f.body), f.weight >= 0 ? inner.at(f.weight) : std::string("1.0f"))
+       << "\n";
+    gvar_ = saved;
+    o_ << ind << "}\n";
+    o_ << ind << "const float " << n << " = " << observe_expr(f.kind, m.observe, c) << ";\n";
+  }
+
+  // A recurrence (recurrence_kernel, codegen/scalar.jl:402-440): a thread per
+  // position of the parallel axes steps along the step axis; at each step the
+  // outputs run in order, each over the other reduced axes its address
+  // mentions, reading what the steps so far stored (plain loads and stores:
+  // a thread reads its own writes).
+  void recurrence(const std::string& name) {
+    std::ostringstream& o = o_;
+    header(name);
+    const int sa = pl_.step;
+    const int64_t E = pl_.E[sa];
+    o << "  const long item = (long)blockIdx.x * " << pl_.S << " + threadIdx.x;\n";
+    o << "  if (item >= " << pl_.items << "L) return;\n";
+    delinearize("  ", "item", pl_.kept);
+    o << "  for (long s = 0; s < " << E << "L; ++s) {\n";
+    o << "    i" << sa << " = " << (pl_.reverse ? std::to_string(E - 1) + "L - s" : std::string("s")) << ";\n";
+    for (int x = 0; x < d_->n_outputs; ++x) {
+      const th_output& out = d_->outputs[x];
+      const char* when = out.full == TH_STEP_FIRST ? "s == 0L" : out.full == TH_STEP_LAST ? "s == LASTL"
+                         : out.full == TH_STEP_CARRY ? "s != LASTL" : "true";
+      std::string cond = when;
+      const size_t at = cond.find("LAST");
+      if (at != std::string::npos) cond.replace(at, 4, std::to_string(E - 1));
+      std::vector<int> inner;
+      for (int k : pl_.swept) {
+        if (k == sa) continue;
+        bool mentioned = out.index.coeff[k] != 0;
+        for (const th_part& q : out.index.part) mentioned |= q.kind != TH_PART_NONE && q.coeff != 0 && q.inner[k] != 0;
+        if (mentioned) inner.push_back(k);
+      }
+      int64_t count = 1;
+      for (int k : inner) count *= pl_.E[k];
+      o << "    if (" << cond << ") {  // output " << x << "\n";
+      for (int k : pl_.swept)
+        if (k != sa) o << "      i" << k << " = 0;\n";
+      o << "      for (long p = 0; p < " << count << "L; ++p) {\n";
+      delinearize("        ", "p", inner);
+      std::vector<int> roots;
+      out_roots(roots, x);
+      std::map<int, std::string> names;
+      emit("        ", reach(d_, roots), false, false, names, nullptr);
+      th_output plain = out;
+      plain.full = 0;
+      store("        ", plain, names.at(out.term), false);
+      o << "      }\n    }\n";
+    }
+    o << "  }\n}\n";
   }
 
   // Hoisted terms (not moving along the sweep) then swept ones.
@@ -943,6 +1183,8 @@ class Writer {
       case TH_FOLD_MIN: return "__builtin_inff()";
       case TH_FOLD_EXP: return j == 0 ? "(-__builtin_inff())" : "0.0f";
       case TH_FOLD_LINEAR: return j == 0 ? "1.0f" : "0.0f";
+      case TH_FOLD_ARGMAX: return j == 0 ? "(-__builtin_inff())" : "__builtin_inff()";
+      case TH_FOLD_ARGMIN: return "__builtin_inff()";
       default: return "0.0f";
     }
   }
@@ -956,6 +1198,8 @@ class Writer {
       case TH_FOLD_MIN: return a[0] + " = fminf(" + a[0] + ", " + b[0] + ");";
       case TH_FOLD_EXP: return "th_exp_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
       case TH_FOLD_LINEAR: return "th_lin_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
+      case TH_FOLD_ARGMAX: return "th_amax_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
+      case TH_FOLD_ARGMIN: return "th_amin_comb(" + a[0] + ", " + a[1] + ", " + b[0] + ", " + b[1] + ");";
       default: return "th_sq_comb(" + a[0] + ", " + a[1] + ", " + a[2] + ", " + b[0] + ", " + b[1] + ", " + b[2] + ");";
     }
   }
@@ -1032,22 +1276,39 @@ class Writer {
 
   // Assign the statistics fold f's merged state gives (to `prefix` + name + `suffix`).
   void observe(const std::string& ind, int f, const std::vector<std::string>& c) { observe_to(ind, f, c, "", ""); }
+  // What observation `obs` of a fold of `kind` reads of its state components c.
+  static std::string observe_expr(int kind, int obs, const std::vector<std::string>& c) {
+    if (kind == TH_FOLD_EXP)
+      return obs == TH_OBSERVE_STATISTIC ? c[0] : obs == TH_OBSERVE_SUM ? c[1] : "th_shift(" + c[0] + ") + logf(" + c[1] + ")";
+    if (kind == TH_FOLD_SQUARE)
+      return obs == TH_OBSERVE_STATISTIC ? "(" + c[0] + " > 0.0f ? " + c[1] + " : __builtin_nanf(\"\"))" : c[2];
+    if (kind == TH_FOLD_LINEAR) return obs == TH_OBSERVE_STATISTIC ? c[0] : c[1];
+    if (kind == TH_FOLD_ARGMAX || kind == TH_FOLD_ARGMIN) return obs == TH_OBSERVE_STATISTIC ? c[1] : c[0];
+    return c[0];
+  }
+
+  // One element (y, weight g) into the state components c of a fold of `kind`.
+  static std::string step_stmt(int kind, const std::vector<std::string>& c, const std::string& y,
+                               const std::string& g) {
+    switch (kind) {
+      case TH_FOLD_SUM: return c[0] + " += " + y + ";";
+      case TH_FOLD_PROD: return c[0] + " *= " + y + ";";
+      case TH_FOLD_MAX: return c[0] + " = th_max(" + c[0] + ", " + y + ");";
+      case TH_FOLD_MIN: return c[0] + " = th_min(" + c[0] + ", " + y + ");";
+      case TH_FOLD_EXP: return "th_exp_step(" + c[0] + ", " + c[1] + ", " + y + ", " + g + ");";
+      case TH_FOLD_LINEAR: return "th_lin_step(" + c[0] + ", " + c[1] + ", " + y + ", " + g + ");";
+      case TH_FOLD_ARGMAX: return "th_amax_comb(" + c[0] + ", " + c[1] + ", " + y + ", " + g + ");";
+      case TH_FOLD_ARGMIN: return "th_amin_comb(" + c[0] + ", " + c[1] + ", " + y + ", " + g + ");";
+      default: return "th_sq_step(" + c[0] + ", " + c[1] + ", " + c[2] + ", " + y + ");";
+    }
+  }
+
   void observe_to(const std::string& ind, int f, const std::vector<std::string>& c, const std::string& prefix,
                   const std::string& suffix) {
     const int kind = d_->folds[f].kind;
     for (int obs = 0; obs <= TH_OBSERVE_LOGSUMEXP; ++obs) {
       if (!observe_ok(kind, obs)) continue;
-      std::string e;
-      if (kind == TH_FOLD_EXP) {
-        e = obs == TH_OBSERVE_STATISTIC ? c[0] : obs == TH_OBSERVE_SUM ? c[1] : "th_shift(" + c[0] + ") + logf(" + c[1] + ")";
-      } else if (kind == TH_FOLD_SQUARE) {
-        e = obs == TH_OBSERVE_STATISTIC ? "(" + c[0] + " > 0.0f ? " + c[1] + " : __builtin_nanf(\"\"))" : c[2];
-      } else if (kind == TH_FOLD_LINEAR) {
-        e = obs == TH_OBSERVE_STATISTIC ? c[0] : c[1];
-      } else {
-        e = c[0];
-      }
-      o_ << ind << prefix << stat_name(f, obs) << suffix << " = " << e << ";\n";
+      o_ << ind << prefix << stat_name(f, obs) << suffix << " = " << observe_expr(kind, obs, c) << ";\n";
     }
   }
 
@@ -1099,6 +1360,11 @@ class Writer {
           case TH_FOLD_LINEAR:
             o << b << "th_lin_step(" << s << "_0, " << s << "_1, " << y << ", "
               << name_of(x.weight, names, hoisted, pl_.W > 1) << ");\n";
+            break;
+          case TH_FOLD_ARGMAX:
+          case TH_FOLD_ARGMIN:
+            o << b << (x.kind == TH_FOLD_ARGMAX ? "th_amax_comb(" : "th_amin_comb(") << s << "_0, " << s << "_1, "
+              << y << ", " << name_of(x.weight, names, hoisted, pl_.W > 1) << ");\n";
             break;
           default:
             o << b << "th_sq_step(" << s << "_0, " << s << "_1, " << s << "_2, " << y << ");\n";
@@ -1313,6 +1579,11 @@ class Writer {
         case TH_FOLD_LINEAR:
           o << "    th_lin_step(" << sf << "_0, " << sf << "_1, " << y << ", " << names.at(x.weight) << ");\n";
           break;
+        case TH_FOLD_ARGMAX:
+        case TH_FOLD_ARGMIN:
+          o << "    " << (x.kind == TH_FOLD_ARGMAX ? "th_amax_comb(" : "th_amin_comb(") << sf << "_0, " << sf
+            << "_1, " << y << ", " << names.at(x.weight) << ");\n";
+          break;
         default:
           o << "    th_sq_step(" << sf << "_0, " << sf << "_1, " << sf << "_2, " << y << ");\n";
       }
@@ -1343,7 +1614,9 @@ class Writer {
     switch (kind) {
       case TH_FOLD_EXP: return {y, g};
       case TH_FOLD_SQUARE: return {"1.0f", y, "0.0f"};
-      case TH_FOLD_LINEAR: return {y, g};
+      case TH_FOLD_LINEAR:
+      case TH_FOLD_ARGMAX:
+      case TH_FOLD_ARGMIN: return {y, g};
       default: return {y};
     }
   }

@@ -88,7 +88,7 @@ class TermStruct(ctypes.Structure):
 
 class FoldStruct(ctypes.Structure):
     _fields_ = [("kind", c_i32), ("phase", c_i32), ("body", c_i32), ("weight", c_i32), ("scan", c_i32),
-                ("reserved", c_i32)]
+                ("n_inner", c_i32), ("inner", c_i64 * FLOOR_RANK)]
 
 
 class OutputStruct(ctypes.Structure):

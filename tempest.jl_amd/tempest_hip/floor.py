@@ -33,15 +33,16 @@ from .runtime import Group
 
 RANK = _lib.FLOOR_RANK
 
-GROUP = {"pointwise": 0, "reduction": 1, "scan": 2}
-TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4}
+GROUP = {"pointwise": 0, "reduction": 1, "scan": 2, "recurrence": 3}
+TERM = {"load": 0, "lit": 1, "index": 2, "stat": 3, "apply": 4, "recompute": 5}
+STEP = {"each": 0, "first": 1, "last": 2, "carry": 3}  # a recurrence output's rule
 FN = {name: k for k, name in enumerate([
     "+", "-", "*", "/", "neg", "abs", "abs2", "sqrt", "exp", "log", "tanh", "sin", "cos", "log1p", "expm1", "^",
     "max", "min", "<", "<=", ">", ">=", "==", "!=", "ifelse", "round", "floor", "ceil", "sign", "clamp", "fma",
     "inv", "bfloat16"])}
 ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", ">", ">=", "==", "!=") else
                 3 if name in ("ifelse", "clamp", "fma") else 1) for name in FN}
-FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6}
+FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6, "argmax": 7, "argmin": 8}
 SCAN = {None: 0, "inclusive": 1, "exclusive": 2}
 OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}
 DTYPE = {"f32": 0, "bf16": 1, "i32": 2, "i64": 3}
@@ -76,9 +77,11 @@ class Fold:
     group: "FloorGroup"
     number: int
     kind: str
+    recomputed: bool = False  # computed where it is read (phase 0), over axes of its own
 
     def _stat(self, observe: str) -> Term:
-        return self.group._term("stat", ref=self.number, observe=OBSERVE[observe])
+        return self.group._term("recompute" if self.recomputed else "stat", ref=self.number,
+                                observe=OBSERVE[observe])
 
     @property
     def value(self) -> Term:
@@ -105,6 +108,11 @@ class Fold:
         """The linear fold's product of its factors a."""
         return self._stat("statistic")
 
+    @property
+    def index(self) -> Term:
+        """An extreme fold's index (its weight where the extreme is)."""
+        return self._stat("statistic")
+
 
 PART = {"div": 1, "mod": 2}
 
@@ -116,8 +124,8 @@ def _affine(coeffs: Sequence[int] | None, constant: int, rank: int, gather=None,
     constant]): coefficient * fld or mod(inner constant + sum inner[k] i_k,
     divisor), the Div and Mod atoms; at most two."""
     c = list(coeffs or ())
-    if len(c) > rank:
-        raise ValueError(f"{len(c)} coefficients for a rank-{rank} domain")
+    if len(c) > RANK:  # beyond the domain's rank: a recomputed fold's own axes
+        raise ValueError(f"{len(c)} coefficients: at most {RANK} positions")
     if len(parts) > 2:
         raise ValueError("at most two div / mod atoms an address")
     g = -1 if gather is None else gather.index
@@ -151,10 +159,11 @@ class FloorGroup:
     extents: tuple
     reduced: tuple = ()                             # folded axes (a scan group: scanned)
     name: str = "floor group"
-    reverse: bool = False                           # a scan group from its last position
+    reverse: bool = False                           # a scan or recurrence group from its last position
+    step: int = -1                                  # a recurrence group's step axis (one of `reduced`)
     values: dict = field(default_factory=dict)      # name -> (dtype, length), in value order
     terms: list = field(default_factory=list)       # (op, fn, args, ref, observe, lit, affine)
-    folds: list = field(default_factory=list)       # (kind, phase, body, weight)
+    folds: list = field(default_factory=list)       # (kind, phase, body, weight, scan, inner extents)
     outputs: list = field(default_factory=list)     # (value, term, full, affine)
 
     def __post_init__(self):
@@ -224,16 +233,32 @@ class FloorGroup:
             raise ValueError("only a scan group's folds scan (inclusive or exclusive)")
         b = self._as_term(body).index
         w = -1 if weight is None else self._as_term(weight).index
-        self.folds.append((FOLD[kind], int(phase), b, w, SCAN[scan]))
+        self.folds.append((FOLD[kind], int(phase), b, w, SCAN[scan], ()))
         return Fold(self, len(self.folds) - 1, kind)
+
+    def recompute(self, kind: str, body, inner: Sequence[int], weight=None) -> Fold:
+        """A fold computed where it is read (the reference's Recomputed term):
+        its body over the group's positions and axes of its own, of extents
+        ``inner``, numbered after the group's (coefficient rank, rank + 1, ...
+        of the addresses its body reaches)."""
+        if kind not in FOLD:
+            raise ValueError(f"unknown fold {kind!r}")
+        b = self._as_term(body).index
+        w = -1 if weight is None else self._as_term(weight).index
+        self.folds.append((FOLD[kind], 0, b, w, 0, tuple(int(e) for e in inner)))
+        return Fold(self, len(self.folds) - 1, kind, recomputed=True)
 
     def output(self, name: str, term, coeffs: Sequence[int] | None = None, constant: int = 0,
                full: bool = True, gather: Term | None = None, gather_coeff: int = 1,
-               accumulate: bool = False, parts=()) -> None:
+               accumulate: bool = False, parts=(), when: str | None = None) -> None:
         """Write ``term`` at the address (every position, or once per item);
-        ``accumulate`` adds it instead, atomically (a fold by key)."""
+        ``accumulate`` adds it instead, atomically (a fold by key).  In a
+        recurrence group, ``when`` is the step rule: "each", "first" (a state
+        where it starts), "last", or "carry" (every step but the last, the
+        address one step on)."""
         v = list(self.values).index(name)
-        self.outputs.append((v, self._as_term(term).index, int(bool(full)),
+        rule = STEP[when or "each"] if self.kind == "recurrence" else int(bool(full))
+        self.outputs.append((v, self._as_term(term).index, rule,
                              _affine(coeffs, constant, len(self.extents), gather, gather_coeff, parts),
                              int(bool(accumulate))))
 
@@ -251,9 +276,10 @@ class FloorGroup:
             t.args[:] = list(args)
             _fill(t.index, aff)
         folds = (FoldStruct * max(nf, 1))()
-        for k, (kind, phase, body, weight, scan) in enumerate(self.folds):
+        for k, (kind, phase, body, weight, scan, inner) in enumerate(self.folds):
             folds[k].kind, folds[k].phase, folds[k].body, folds[k].weight = kind, phase, body, weight
-            folds[k].scan = scan
+            folds[k].scan, folds[k].n_inner = scan, len(inner)
+            folds[k].inner[:] = list(inner) + [0] * (RANK - len(inner))
         outs = (OutputStruct * max(no, 1))()
         for k, (v, term, full, aff, acc) in enumerate(self.outputs):
             outs[k].value, outs[k].term, outs[k].full, outs[k].accumulate = v, term, full, acc
@@ -263,7 +289,7 @@ class FloorGroup:
         d.extents[:] = list(self.extents) + [1] * (RANK - len(self.extents))
         d.reduced = sum(1 << k for k in self.reduced)
         d.n_values, d.n_terms, d.n_folds, d.n_outputs = nv, nt, nf, no
-        d.flags = 1 if self.reverse else 0
+        d.flags = (1 if self.reverse else 0) | ((self.step << 8) if self.kind == "recurrence" else 0)
         d.values, d.terms, d.folds, d.outputs = values, terms, folds, outs
         return d, (values, terms, folds, outs)
 
@@ -320,9 +346,10 @@ class FloorGroup:
                        "ref": ref, "observe": inv_obs[obs], "lit": lit, "constant": aff[0], "coeffs": list(aff[1]),
                        "gather": aff[2], "gather_coeff": aff[3], "parts": list(aff[4])}
                       for op, fn, args, ref, obs, lit, aff in self.terms],
-            "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w, "scan": inv_scan[sc]}
-                      for k, p, b, w, sc in self.folds],
-            "outputs": [{"value": list(self.values)[v], "term": t, "full": bool(f), "constant": aff[0],
+            "folds": [{"kind": inv_fold[k], "phase": p, "body": b, "weight": w, "scan": inv_scan[sc], "inner": inner}
+                      for k, p, b, w, sc, inner in self.folds],
+            "step": self.step,
+            "outputs": [{"value": list(self.values)[v], "term": t, "full": int(f), "constant": aff[0],
                          "coeffs": list(aff[1]), "gather": aff[2], "gather_coeff": aff[3], "parts": list(aff[4]),
                          "accumulate": bool(acc)}
                         for v, t, f, aff, acc in self.outputs],

@@ -727,6 +727,160 @@ def scatter_add_gradient():
                 dtypes={"i": "i64"})
 
 
+# ---- extremes and where they are (the `Better` fold, program/tracing.jl:735-790) ----
+
+def extremes_and_where_they_are():
+    """x -> sum(findmax(x; dims = 1)[1] .* data(1, 6)) + sum(getindex.(argmin(x;
+    dims = 2), 2)) + x[argmax(x)] + argmin(abs, x) + sum(last.(extrema(x; dims
+    = 2)) .* data(8)), x = data(8, 6) (test/fixtures/programs.jl:144-145).
+    The element argmin(abs, x) finds is read by a gather at the index the fold
+    stored."""
+    x, w, d8 = data(8, 6), data(1, 6), data(8)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0,), name="findmax(x; dims = 1)")
+    g1.value("x", "f32", 48)
+    g1.value("w", "f32", 6)
+    g1.value("r1", "f32", 6)
+    fm = g1.fold("argmax", g1.load("x", (1, 8)), weight=g1.index((1, 0), 1))
+    g1.output("r1", fm.value * g1.load("w", (0, 1)), (0, 1), full=False)
+    g2 = FloorGroup("reduction", (8, 6), reduced=(1,), name="argmin(x; dims = 2), extrema(x; dims = 2)")
+    g2.value("x", "f32", 48)
+    g2.value("d8", "f32", 8)
+    g2.value("r2", "f32", 8)
+    xx = g2.load("x", (1, 8))
+    am = g2.fold("argmin", xx, weight=g2.index((0, 1), 1))   # the column, 1-based
+    mx = g2.fold("max", xx)
+    g2.output("r2", am.index + mx.value * g2.load("d8", (1, 0)), (1, 0), full=False)
+    g3 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="x[argmax(x)], argmin(abs, x)")
+    g3.value("x", "f32", 48)
+    g3.value("s", "f32", 3)
+    x3 = g3.load("x", (1, 8))
+    lin = g3.index((1, 8), 1)
+    g3.output("s", g3.fold("argmax", x3, weight=lin).value, (0, 0), full=False)
+    g3.output("s", g3.fold("argmin", g3.apply("abs", x3), weight=lin).index, (0, 0), constant=1, full=False)
+    g5 = FloorGroup("reduction", (6,), reduced=(0,), name="sum(r1)")
+    g5.value("r1", "f32", 6)
+    g5.value("s", "f32", 3)
+    g5.output("s", g5.fold("sum", g5.load("r1", (1,))).value, (0,), constant=2, full=False)
+    g4 = FloorGroup("reduction", (8,), reduced=(0,), name="the sum")
+    for k, n in (("x", 48), ("s", 3), ("r2", 8), ("loss", 1)):
+        g4.value(k, "f32", n)
+    at = g4.load("x", (0,), constant=-1, gather=g4.load("s", (0,), constant=1), gather_coeff=1)
+    total = g4.fold("sum", g4.load("r2", (1,))).value + g4.load("s", (0,), constant=2) + g4.load("s", (0,)) + at
+    g4.output("loss", total, (0,), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        r1_ = X.max(axis=0) * v["w"]
+        r2_ = (np.argmin(X, axis=1) + 1) + X.max(axis=1) * v["d8"]
+        i = int(np.argmin(np.abs(v["x"])))
+        s_ = [X.max(), i + 1, r1_.sum()]
+        return {"r1": r1_, "r2": r2_, "s": s_, "loss": [r1_.sum() + r2_.sum() + s_[0] + v["x"][i]]}
+    return Case("extremes and where they are", [g1, g2, g3, g5, g4], {"x": F(x), "w": F(w), "d8": F(d8)},
+                {"r1": 6, "r2": 8, "s": 3, "loss": 1}, ["r1", "r2", "s", "loss"], closed)
+
+
+def extremes_of_a_vector():
+    """v -> v[argmax(v)] * findmin(v)[2] + sum(extrema(v)) + findmax(abs2, v)[1],
+    v = data(30) (test/fixtures/programs.jl:146)."""
+    v0 = data(30)
+    g = FloorGroup("reduction", (30,), reduced=(0,), name="extremes of a vector")
+    g.value("v", "f32", 30)
+    g.value("loss", "f32", 1)
+    v = g.load("v", (1,))
+    i = g.index((1,), 1)
+    a = g.fold("argmax", v, weight=i).value
+    b = g.fold("argmin", v, weight=i).index
+    ext = g.fold("min", v).value + g.fold("max", v).value
+    c = g.fold("argmax", g.apply("abs2", v), weight=i).value
+    g.output("loss", a * b + ext + c, (0,), full=False)
+
+    def closed(val):
+        u = val["v"]
+        return {"loss": [u[np.argmax(u)] * (np.argmin(u) + 1) + u.min() + u.max() + (u ** 2).max()]}
+    return Case("the extremes of a vector", [g], {"v": F(v0)}, {"loss": 1}, ["loss"], closed)
+
+
+# ---- recomputed folds and recurrences ----------------------------------------------
+
+def mean_recomputed():
+    """x .- mean(x; dims = 1) with the mean recomputed where each element reads
+    it (a Recomputed term, codegen/scalar.jl:88-110), then sum(abs2, .)."""
+    x = data(8, 6)
+    g = FloorGroup("pointwise", (8, 6), name="x .- mean, recomputed")
+    g.value("x", "f32", 48)
+    g.value("y", "f32", 48)
+    mean = g.recompute("sum", g.load("x", (0, 8, 1)), inner=(8,)).value / 8.0
+    g.output("y", g.load("x", (1, 8)) - mean, (1, 8))
+    g2 = FloorGroup("reduction", (48,), reduced=(0,), name="sum(abs2, y)")
+    g2.value("y", "f32", 48)
+    g2.value("loss", "f32", 1)
+    g2.output("loss", g2.fold("sum", g2.apply("abs2", g2.load("y", (1,)))).value, full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        Y = X - X.mean(axis=0)
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(Y ** 2)]}
+    return Case("x .- mean, the mean recomputed", [g, g2], {"x": F(x)}, {"y": 48, "loss": 1}, ["y", "loss"], closed)
+
+
+def recurrence_with_recomputed_sums():
+    """h = tanh.(W' * unit(x[:, t]) .+ h) over the columns of x, unit(x) =
+    x ./ sqrt(sum(abs2, x) + 1e-6) (test/cuda/folds.jl:85-99): a recurrence
+    group stepping along t, its state's start stored at the first step, its
+    new state carried one step on, the product and the norm recomputed in
+    each step."""
+    W, x, h0 = data(256, 64, scale=0.1), data(256, 4, scale=0.3), data(64, scale=0.2)
+    g = FloorGroup("recurrence", (64, 4), reduced=(1,), step=1, name="h = tanh(W' unit(x[:, t]) + h)")
+    for k, n in (("W", 256 * 64), ("x", 1024), ("h0", 64), ("H", 64 * 5), ("Y", 64 * 4)):
+        g.value(k, "f32", n)
+    prod = g.recompute("sum", g.load("W", (256, 0, 1)) * g.load("x", (0, 256, 1)), inner=(256,)).value
+    norm = g.recompute("sum", g.apply("abs2", g.load("x", (0, 256, 1))), inner=(256,)).value
+    h = g.apply("tanh", prod / g.apply("sqrt", norm + 1e-6) + g.load("H", (1, 64)))
+    g.output("H", g.load("h0", (1, 0)), (1, 64), when="first")
+    g.output("H", h, (1, 64), constant=64, when="carry")
+    g.output("Y", h, (1, 64), when="each")
+
+    def closed(v):
+        Wm, X = v["W"].reshape(256, 64, order="F"), v["x"].reshape(256, 4, order="F")
+        hh, H, Y = v["h0"].copy(), np.zeros((64, 5)), np.zeros((64, 4))
+        H[:, 0] = hh
+        for t in range(4):
+            u = X[:, t] / np.sqrt(np.sum(X[:, t] ** 2) + 1e-6)
+            hh = np.tanh(Wm.T @ u + hh)
+            Y[:, t] = hh
+            if t < 3:
+                H[:, t + 1] = hh
+        return {"H": H.ravel(order="F"), "Y": Y.ravel(order="F")}
+    return Case("a recurrence whose steps recompute sums", [g], {"W": F(W), "x": F(x), "h0": F(h0)},
+                {"H": 320, "Y": 256}, ["H", "Y"], closed)
+
+
+def reverse_recurrence():
+    """h = a h' + b stepped from the last position back (a carried state in
+    reverse): h at t reads the state t + 1 left."""
+    a, b, h0 = 0.9 + 0.1 * data(5, 7, scale=0.3), data(5, 7, scale=0.7), data(5, scale=0.5)
+    g = FloorGroup("recurrence", (5, 7), reduced=(1,), step=1, reverse=True, name="h = a h' + b, reversed")
+    for k, n in (("a", 35), ("b", 35), ("h0", 5), ("H", 35), ("Y", 35)):
+        g.value(k, "f32", n)
+    h = g.load("a", (1, 5)) * g.load("H", (1, 5)) + g.load("b", (1, 5))
+    g.output("H", g.load("h0", (1, 0)), (1, 5), when="first")
+    g.output("H", h, (1, 5), constant=-5, when="carry")
+    g.output("Y", h, (1, 5), when="each")
+
+    def closed(v):
+        A, B = v["a"].reshape(5, 7, order="F"), v["b"].reshape(5, 7, order="F")
+        H, Y, hh = np.zeros((5, 7)), np.zeros((5, 7)), v["h0"].copy()
+        H[:, 6] = hh
+        for t in range(6, -1, -1):
+            hh = A[:, t] * hh + B[:, t]
+            Y[:, t] = hh
+            if t > 0:
+                H[:, t - 1] = hh
+        return {"H": H.ravel(order="F"), "Y": Y.ravel(order="F")}
+    return Case("a recurrence in reverse", [g], {"a": F(a), "b": F(b), "h0": F(h0)}, {"H": 35, "Y": 35},
+                ["H", "Y"], closed)
+
+
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
@@ -735,7 +889,9 @@ CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, mi
          cumulative_sums, cumulative_products_through_a_zero, running_maxima_and_minima, linear_recurrence,
          running_average, reverse_exclusive_sums, running_logsumexp_and_mean,
          gather_by_a_list, gather_by_an_int32_matrix, gather_rows_by_an_int64_matrix,
-         gather_by_linear_and_scalar_indices, embedding_and_layer_norm, scatter_add_gradient]
+         gather_by_linear_and_scalar_indices, embedding_and_layer_norm, scatter_add_gradient,
+         extremes_and_where_they_are, extremes_of_a_vector, mean_recomputed, recurrence_with_recomputed_sums,
+         reverse_recurrence]
 
 
 def run_oracle(case: Case) -> dict:

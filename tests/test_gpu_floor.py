@@ -383,3 +383,67 @@ def test_parallel_scans_of_every_fold(target, n, m, dtype):
     assert relative(got["dev"], dev) < 1e-4
     assert relative(got["prod"], np.cumprod(Pm, axis=1)) < 1e-4
     assert np.array_equal(got["min"], np.minimum.accumulate(X, axis=1))
+
+
+@pytest.mark.parametrize("shape,axis", [((5000, 37), 0), ((37, 5000), 1), ((300, 700), 0)])
+def test_extreme_folds_merge_like_base(target, shape, axis):
+    """findmax / findmin folds over rows (lanes merged by shuffles), over
+    columns (lanes merged through LDS), on elements full of ties, signed zeros
+    and NaNs: the extreme and the first index where it is, as Base finds them."""
+    from oracle import floor_groups as FG
+    from tempest_hip.floor import FloorGroup
+    n, m = shape
+    announce("floor extreme folds", shape, axis)
+    rng = np.random.default_rng(n + 3 * m)
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.0, 3.0, -np.inf], dtype=np.float32)
+    x = pool[rng.integers(0, len(pool), n * m)]
+    x[rng.integers(0, n * m, 5)] = np.nan
+    g = FloorGroup("reduction", shape, reduced=(axis,))
+    g.value("x", "f32", n * m)
+    items = m if axis == 0 else n
+    for k in ("vmax", "imax", "vmin", "imin"):
+        g.value(k, "f32", items)
+    xx = g.load("x", (1, n))
+    pos = g.index((1, 0) if axis == 0 else (0, 1), 1)
+    hi = g.fold("argmax", xx, weight=pos)
+    lo = g.fold("argmin", xx, weight=pos)
+    at = (0, 1) if axis == 0 else (1, 0)
+    for k, t in (("vmax", hi.value), ("imax", hi.index), ("vmin", lo.value), ("imin", lo.index)):
+        g.output(k, t, at, full=False)
+    ts = {"x": torch.from_numpy(x).cuda()}
+    for k in ("vmax", "imax", "vmin", "imin"):
+        ts[k] = torch.zeros(items, device="cuda")
+    g.build({k: ts[k].data_ptr() for k in g.values})()
+    torch.cuda.synchronize()
+    X = x.astype(np.float64).reshape(m, n).T  # X[i0, i1]
+    idx = (np.arange(n)[:, None] + 1.0) * np.ones((1, m)) if axis == 0 else np.ones((n, 1)) * (np.arange(m)[None] + 1.0)
+    for kind, v, i in (("argmax", "vmax", "imax"), ("argmin", "vmin", "imin")):
+        st = FG.fold_reduce(kind, X, idx, (axis,))
+        want_v, want_i = st["value"].ravel(), st["statistic"].ravel()
+        got_v, got_i = ts[v].cpu().numpy().astype(np.float64), ts[i].cpu().numpy().astype(np.float64)
+        assert np.array_equal(got_i, want_i), kind
+        assert np.array_equal(np.isnan(got_v), np.isnan(want_v))
+        ok = ~np.isnan(want_v)
+        assert np.array_equal(got_v[ok], want_v[ok]) and np.array_equal(np.signbit(got_v[ok]), np.signbit(want_v[ok]))
+
+
+def test_extreme_fold_split_over_parts(target):
+    """findmax over 2^22 elements in one item: the positions split among
+    workgroups, the parts' states merged by a second launch."""
+    from tempest_hip.floor import FloorGroup
+    n = 1 << 22
+    announce("floor extreme fold in parts", n)
+    rng = np.random.default_rng(12)
+    x = rng.integers(0, 1000, n).astype(np.float32)
+    g = FloorGroup("reduction", (n,), reduced=(0,))
+    g.value("x", "f32", n)
+    g.value("r", "f32", 2)
+    f = g.fold("argmax", g.load("x", (1,)), weight=g.index((1,), 1))
+    g.output("r", f.value, (0,), full=False)
+    g.output("r", f.index, (0,), constant=1, full=False)
+    assert "parts" in g.source().splitlines()[0] and ", parts 1," not in g.source().splitlines()[0]
+    ts = {"x": torch.from_numpy(x).cuda(), "r": torch.zeros(2, device="cuda")}
+    g.build({k: ts[k].data_ptr() for k in g.values})()
+    torch.cuda.synchronize()
+    r = ts["r"].cpu().numpy()
+    assert r[0] == x.max() and r[1] == float(np.argmax(x) + 1)  # the first of the equal maxima

@@ -290,3 +290,61 @@ def test_once_output_loads_are_checked_at_folded_zero():
     g.output("r", s.value + g.load("x", (1, 16)), (1, 0), full=False)
     with pytest.raises(HIPError, match="folded positions at zero"):
         g.source()
+
+
+def _base_extreme(y, idx, largest):
+    """findmax / findmin by brute force over Base's orders: isless (NaN the
+    largest, -0.0 before 0.0) for findmax, isgreater (NaN the smallest) for
+    findmin, the first index among equals."""
+    import math
+
+    def key(j):
+        x = float(y[j])
+        nan = x != x
+        pos = (not nan) and math.copysign(1.0, x) > 0
+        return (nan, 0.0 if nan else x, pos, -idx[j]) if largest else (not nan, 0.0 if nan else x, pos, idx[j])
+    j = (max if largest else min)(range(len(y)), key=key)
+    return y[j], idx[j]
+
+
+@pytest.mark.parametrize("largest", [True, False])
+def test_extreme_folds_follow_base_order(largest):
+    """The oracle's extreme folds (sequential, and combined in any grouping)
+    against brute force over Base's orders, on elements full of ties, signed
+    zeros, infinities and NaNs."""
+    from oracle import floor_groups as FG
+    rng = np.random.default_rng(7 + largest)
+    pool = np.array([0.0, -0.0, 1.0, -1.0, 2.5, np.inf, -np.inf, np.nan])
+    kind = "argmax" if largest else "argmin"
+    for trial in range(200):
+        n = int(rng.integers(1, 12))
+        y = pool[rng.integers(0, len(pool) - (0 if trial % 3 == 0 else 1), n)]
+        idx = rng.permutation(n).astype(np.float64) + 1
+        st = FG.fold_reduce(kind, y[:, None], idx[:, None], (0,))
+        want_y, want_i = _base_extreme(y, idx, largest)
+        assert st["statistic"][0, 0] == want_i, (y, idx)
+        assert (np.isnan(want_y) and np.isnan(st["value"][0, 0])) or (
+            st["value"][0, 0] == want_y and np.signbit(st["value"][0, 0]) == np.signbit(want_y))
+        # Any grouping: a random split into two halves, combined.
+        cut = int(rng.integers(0, n + 1))
+        a = FG.fold_reduce(kind, y[:cut, None], idx[:cut, None], (0,)) if cut else None
+        b = FG.fold_reduce(kind, y[cut:, None], idx[cut:, None], (0,)) if cut < n else None
+        parts = [p for p in (a, b) if p is not None]
+        st2 = (parts[0]["value"], parts[0]["statistic"])
+        for p in parts[1:]:
+            st2 = FG.better(largest, st2, (p["value"], p["statistic"]))
+        assert st2[1][0, 0] == want_i
+
+
+def test_a_planted_tie_break_mistake_is_caught(monkeypatch):
+    """The extreme fold without its index tie-break keeps the later of equal
+    elements: the brute-force order catches it."""
+    from oracle import floor_groups as FG
+    def no_tie_break(largest, a, b):
+        t = FG.lesser(a[0], b[0]) if largest else FG.greater(a[0], b[0])
+        t = t | (a[0] == b[0])
+        return np.where(t, b[0], a[0]), np.where(t, b[1], a[1])
+    monkeypatch.setattr(FG, "better", no_tie_break)
+    y, idx = np.array([1.0, 3.0, 3.0]), np.array([1.0, 2.0, 3.0])
+    st = FG.fold_reduce("argmax", y[:, None], idx[:, None], (0,))
+    assert st["statistic"][0, 0] != _base_extreme(y, idx, True)[1]
