@@ -115,6 +115,23 @@ int th_arena_slot(th_arena* arena, int slot, void** host_out);
 int th_arena_bytes(th_arena* arena, uint64_t* host_out);
 int th_arena_destroy(th_arena* arena);
 
+/* The slot pool: one reserved range of `reserve` bytes of device addresses
+ * (hipMemAddressReserve), mapped to memory (hipMemCreate, hipMemMap) as
+ * blocks are taken; without virtual memory management, one allocation of
+ * that size.  th_pool_alloc takes a block (first fit, else past the highest
+ * block, 256-byte or `align`-aligned); th_pool_free returns it.  Every block
+ * lies in [base, base + reserved): the planner's slots, allocated one by one
+ * as `planned` does (src/Compiler/runtime/runtime.jl:415, allocate(t, T, n)
+ * per slot), land in one range.  Replaces allocate(::CUDATarget, T, n),
+ * ext/CUDAExt.jl:23, for the slots of an executable.  th_pool_destroy waits
+ * for the device and unmaps everything. */
+typedef struct th_pool th_pool;
+int th_pool_create(uint64_t reserve, th_pool** host_out);
+int th_pool_alloc(th_pool* pool, uint64_t bytes, uint64_t align, void** host_out);
+int th_pool_free(th_pool* pool, void* ptr);
+int th_pool_info(th_pool* pool, void** host_base, uint64_t* host_reserved, uint64_t* host_mapped);
+int th_pool_destroy(th_pool* pool);
+
 /* ---- launches ---------------------------------------------------------- */
 
 /* Run a launch's kernels on the stream, in order: a step of `execute!`.
@@ -492,6 +509,13 @@ typedef struct th_gemm_desc {
 #define TH_GEMM_ACCUMULATE 4   /* C = D + A*B (cuBLASExt.jl:25, `accumulated`) */
 
 int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
+
+/* Products alike but for where their operands start, as one launch: each of
+ * descs[0..count) built as th_build_gemm builds it, run in order.  Value v of
+ * product i is value 9 i + v of the launch.  Replaces cuBLASProducts' build
+ * over a vector of bindings (cublasGemmBatchedEx on arrays of addresses,
+ * ext/cuBLASExt.jl:262-326). */
+int th_build_gemm_grouped(const th_gemm_desc* descs, int count, th_launch** host_out);
 
 /* ---- op class (c): causal flash attention ------------------------------- */
 

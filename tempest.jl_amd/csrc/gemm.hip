@@ -241,3 +241,45 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   *out = b.release();
   return TH_OK;
 }
+
+extern "C" int th_build_gemm_grouped(const th_gemm_desc* descs, int count, th_launch** out) {
+  if (int r = th::require_ready()) return r;
+  *out = nullptr;
+  TH_REQUIRE(descs != nullptr && count >= 1, "th_build_gemm_grouped: no products");
+  std::vector<th_launch*> parts;
+  auto drop = [&]() {
+    for (th_launch* l : parts) th_launch_destroy(l);
+  };
+  for (int i = 0; i < count; ++i) {
+    th_launch* l = nullptr;
+    if (int r = th_build_gemm(&descs[i], &l)) {
+      drop();
+      return r;
+    }
+    parts.push_back(l);
+  }
+  // One launch: every product's kernels in order, its values after the
+  // previous products', its workspaces owned by the whole.
+  th_launch* g = new th_launch();
+  g->name = "gemm_grouped";
+  for (th_launch* l : parts) {
+    const int k0 = (int)g->kernels.size();
+    g->kernels.insert(g->kernels.end(), l->kernels.begin(), l->kernels.end());
+    for (size_t v = 0; v < l->values.size(); ++v) {
+      std::vector<th::Ref> refs = l->values[v];
+      for (th::Ref& r : refs) r.kernel += k0;
+      g->values.push_back(refs);
+      g->align.push_back(l->align[v]);
+    }
+    g->owned.insert(g->owned.end(), l->owned.begin(), l->owned.end());
+    l->owned.clear();
+    g->work.bytes += l->work.bytes;
+    g->work.flops += l->work.flops;
+    g->work.blocks += l->work.blocks;
+  }
+  g->work.kernels = (int32_t)g->kernels.size();
+  g->work.values = (int32_t)g->values.size();
+  drop();
+  *out = g;
+  return TH_OK;
+}

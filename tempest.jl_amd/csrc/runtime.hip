@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -227,6 +228,20 @@ struct th_arena {
   std::vector<uint64_t> offsets;
 };
 
+// A reserved range of device addresses, mapped to memory as blocks are taken
+// from it: every block the pool hands out lies in [base, base + reserved).
+struct th_pool {
+  int device = 0;
+  bool vmm = true;           // a reservation mapped on demand; else one allocation
+  void* base = nullptr;
+  uint64_t reserved = 0;     // bytes of address space
+  uint64_t mapped = 0;       // bytes mapped from base
+  uint64_t granularity = 0;
+  uint64_t top = 0;          // the end of the highest block taken
+  std::vector<std::pair<hipMemGenericAllocationHandle_t, uint64_t>> chunks;
+  std::map<uint64_t, uint64_t> free, used;  // offset -> bytes
+};
+
 extern "C" {
 
 int th_arena_create(const uint64_t* sizes, int n, uint64_t align, th_arena** out) {
@@ -268,6 +283,157 @@ int th_arena_destroy(th_arena* a) {
   if (!a) return TH_OK;
   if (a->base) TH_HIP(hipFree(a->base));
   delete a;
+  return TH_OK;
+}
+
+// ---- the slot pool: one reserved range of addresses ---------------------------
+
+int th_pool_create(uint64_t reserve, th_pool** out) {
+  if (int r = require_ready()) return r;
+  *out = nullptr;
+  TH_REQUIRE(reserve > 0, "th_pool_create: reserve some bytes");
+  th_pool* p = new th_pool();
+  p->device = ctx().device;
+  hipMemAllocationProp prop{};
+  prop.type = hipMemAllocationTypePinned;
+  prop.location.type = hipMemLocationTypeDevice;
+  prop.location.id = p->device;
+  size_t gran = 0;
+  hipError_t e = hipMemGetAllocationGranularity(&gran, &prop, hipMemAllocationGranularityRecommended);
+  if (e == hipSuccess && gran > 0) {
+    p->granularity = gran;
+    p->reserved = (reserve + gran - 1) / gran * gran;
+    e = hipMemAddressReserve(&p->base, p->reserved, gran, nullptr, 0);
+  }
+  if (e != hipSuccess) {
+    // No virtual memory management: the whole range as one allocation.
+    (void)hipGetLastError();
+    p->vmm = false;
+    p->reserved = (reserve + 255) / 256 * 256;
+    p->granularity = 256;
+    if (int r = device_alloc(p->reserved, &p->base)) {
+      delete p;
+      return r;
+    }
+    p->mapped = p->reserved;
+  }
+  *out = p;
+  return TH_OK;
+}
+
+// Map physical memory behind the reservation up to `end` bytes.
+static int pool_map(th_pool* p, uint64_t end) {
+  if (end <= p->mapped) return TH_OK;
+  if (!p->vmm || end > p->reserved)
+    return fail(TH_E_MEMORY, "th_pool_alloc: the pool's " + std::to_string(p->reserved) + " reserved bytes are full");
+  uint64_t bytes = std::max<uint64_t>(end - p->mapped, uint64_t(64) << 20);
+  bytes = std::min<uint64_t>((bytes + p->granularity - 1) / p->granularity * p->granularity, p->reserved - p->mapped);
+  hipMemAllocationProp prop{};
+  prop.type = hipMemAllocationTypePinned;
+  prop.location.type = hipMemLocationTypeDevice;
+  prop.location.id = p->device;
+  hipMemGenericAllocationHandle_t h;
+  hipError_t e = hipMemCreate(&h, bytes, &prop, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(TH_E_MEMORY, std::string("th_pool_alloc: hipMemCreate of ") + std::to_string(bytes) +
+                                 " bytes failed: " + hipGetErrorString(e));
+  }
+  char* at = static_cast<char*>(p->base) + p->mapped;
+  e = hipMemMap(at, bytes, 0, h, 0);
+  if (e == hipSuccess) {
+    hipMemAccessDesc access{};
+    access.location.type = hipMemLocationTypeDevice;
+    access.location.id = p->device;
+    access.flags = hipMemAccessFlagsProtReadWrite;
+    e = hipMemSetAccess(at, bytes, &access, 1);
+    if (e != hipSuccess) (void)hipMemUnmap(at, bytes);
+  }
+  if (e != hipSuccess) {
+    (void)hipMemRelease(h);
+    return hip_fail(e, "th_pool_alloc: mapping the pool");
+  }
+  p->chunks.push_back({h, bytes});
+  p->mapped += bytes;
+  return TH_OK;
+}
+
+int th_pool_alloc(th_pool* p, uint64_t bytes, uint64_t align, void** out) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(p != nullptr, "th_pool_alloc: null pool");
+  *out = nullptr;
+  if (align < 256) align = 256;
+  TH_REQUIRE((align & (align - 1)) == 0, "th_pool_alloc: alignment must be a power of two");
+  bytes = std::max<uint64_t>((bytes + 255) / 256 * 256, 256);
+  // The first free block that holds it, else past the highest block.
+  uint64_t at = UINT64_MAX;
+  for (auto it = p->free.begin(); it != p->free.end(); ++it) {
+    const uint64_t start = (it->first + align - 1) & ~(align - 1);
+    if (start + bytes <= it->first + it->second) {
+      at = start;
+      const uint64_t lo = it->first, hi = it->first + it->second;
+      p->free.erase(it);
+      if (start > lo) p->free[lo] = start - lo;
+      if (start + bytes < hi) p->free[start + bytes] = hi - (start + bytes);
+      break;
+    }
+  }
+  if (at == UINT64_MAX) {
+    at = (p->top + align - 1) & ~(align - 1);
+    if (int r = pool_map(p, at + bytes)) return r;
+    if (at > p->top) p->free[p->top] = at - p->top;
+    p->top = at + bytes;
+  }
+  p->used[at] = bytes;
+  *out = static_cast<char*>(p->base) + at;
+  return TH_OK;
+}
+
+int th_pool_free(th_pool* p, void* ptr) {
+  TH_REQUIRE(p != nullptr, "th_pool_free: null pool");
+  if (!ptr) return TH_OK;
+  const uint64_t at = static_cast<uint64_t>(static_cast<char*>(ptr) - static_cast<char*>(p->base));
+  auto it = p->used.find(at);
+  TH_REQUIRE(ptr >= p->base && it != p->used.end(), "th_pool_free: not a block of this pool");
+  uint64_t lo = at, hi = at + it->second;
+  p->used.erase(it);
+  // Coalesce with the free neighbours; a free block at the top lowers it.
+  auto next = p->free.find(hi);
+  if (next != p->free.end()) hi += next->second, p->free.erase(next);
+  auto prev = p->free.lower_bound(lo);
+  if (prev != p->free.begin()) {
+    --prev;
+    if (prev->first + prev->second == lo) lo = prev->first, p->free.erase(prev);
+  }
+  if (hi == p->top) p->top = lo;
+  else p->free[lo] = hi - lo;
+  return TH_OK;
+}
+
+int th_pool_info(th_pool* p, void** base, uint64_t* reserved, uint64_t* mapped) {
+  TH_REQUIRE(p != nullptr, "th_pool_info: null pool");
+  *base = p->base;
+  *reserved = p->reserved;
+  *mapped = p->mapped;
+  return TH_OK;
+}
+
+int th_pool_destroy(th_pool* p) {
+  if (!p) return TH_OK;
+  // Nothing may still read the pool's memory.
+  TH_HIP(hipDeviceSynchronize());
+  if (p->vmm) {
+    uint64_t off = 0;
+    for (const auto& c : p->chunks) {
+      TH_HIP(hipMemUnmap(static_cast<char*>(p->base) + off, c.second));
+      TH_HIP(hipMemRelease(c.first));
+      off += c.second;
+    }
+    if (p->base) TH_HIP(hipMemAddressFree(p->base, p->reserved));
+  } else if (p->base) {
+    TH_HIP(hipFree(p->base));
+  }
+  delete p;
   return TH_OK;
 }
 

@@ -11,9 +11,9 @@ without a GPU, construction raises.
 """
 from ._lib import HIPError, LIBRARY, load  # noqa: F401
 from .launch import Launch  # noqa: F401
-from .runtime import Compiled, Executable, Group, Program, Value, compile, prepare, storage  # noqa: F401
+from .runtime import Compiled, Executable, Group, Pool, Program, Value, compile, prepare, storage  # noqa: F401
 from .target import Graph, HIPTarget, Move  # noqa: F401
 from . import programs  # noqa: F401
 
 __all__ = ["HIPError", "LIBRARY", "load", "Launch", "Compiled", "Executable", "Group", "Program", "Value",
-           "compile", "prepare", "storage", "Graph", "HIPTarget", "Move", "programs"]
+           "compile", "prepare", "storage", "Graph", "HIPTarget", "Move", "Pool", "programs"]

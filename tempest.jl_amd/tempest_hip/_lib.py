@@ -131,6 +131,11 @@ SIGNATURES: dict[str, list] = {
     "th_arena_slot": [c_void_p, c_int, P(c_void_p)],
     "th_arena_bytes": [c_void_p, P(c_u64)],
     "th_arena_destroy": [c_void_p],
+    "th_pool_create": [c_u64, P(c_void_p)],
+    "th_pool_alloc": [c_void_p, c_u64, c_u64, P(c_void_p)],
+    "th_pool_free": [c_void_p, c_void_p],
+    "th_pool_info": [c_void_p, P(c_void_p), P(c_u64), P(c_u64)],
+    "th_pool_destroy": [c_void_p],
     "th_launch_run": [c_void_p],
     "th_launch_repoint": [c_void_p, c_int, c_void_p],
     "th_launch_work": [c_void_p, P(Work)],
@@ -150,6 +155,7 @@ SIGNATURES: dict[str, list] = {
     "th_build_layernorm_fwd": [c_i64, c_i32, c_i64, c_f32, c_void_p, c_void_p, P(c_void_p)],
     "th_build_sum": [c_i64, c_void_p, c_void_p, P(c_void_p)],
     "th_build_gemm": [P(GemmDesc), P(c_void_p)],
+    "th_build_gemm_grouped": [P(GemmDesc), c_int, P(c_void_p)],
     "th_build_attention_fwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_attention_bwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_deltanet_fwd": [P(DeltaNetDesc), P(c_void_p)],

@@ -152,14 +152,72 @@ class Arena:
             pass
 
 
-class Executable:
-    """A prepared program: its storage, launches and (once captured) graph."""
+class Pool:
+    """A reserved range of device addresses that hands out blocks (th_pool_*):
+    the slots of executables allocated one at a time, as ``planned`` allocates
+    each (src/Compiler/runtime/runtime.jl:415), all inside one range."""
 
-    def __init__(self, program: Program, target: HIPTarget, inputs: Sequence[torch.Tensor], point: bool = True):
+    def __init__(self, reserve: int = 64 << 30):
+        self._h = ctypes.c_void_p()
+        call("th_pool_create", ctypes.c_uint64(reserve), ctypes.byref(self._h))
+
+    def alloc(self, nbytes: int, align: int = 256) -> int:
+        p = ctypes.c_void_p()
+        call("th_pool_alloc", self._h, ctypes.c_uint64(nbytes), ctypes.c_uint64(align), ctypes.byref(p))
+        return p.value
+
+    def free(self, ptr: int) -> None:
+        call("th_pool_free", self._h, ctypes.c_void_p(ptr))
+
+    def info(self) -> tuple[int, int, int]:
+        """(base address, reserved bytes, mapped bytes)."""
+        b, r, m = ctypes.c_void_p(), ctypes.c_uint64(), ctypes.c_uint64()
+        call("th_pool_info", self._h, ctypes.byref(b), ctypes.byref(r), ctypes.byref(m))
+        return b.value, r.value, m.value
+
+    def destroy(self) -> None:
+        if self._h is not None:
+            call("th_pool_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class PoolSlots:
+    """The slots of one executable taken from a Pool one by one, freed with it."""
+
+    def __init__(self, pool: Pool, sizes: Sequence[int], align: int = 256):
+        self.pool = pool
+        self.addresses = [pool.alloc(n, align) for n in sizes]
+        self.bytes = sum(sizes)
+
+    def destroy(self) -> None:
+        for a in self.addresses:
+            self.pool.free(a)
+        self.addresses = []
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Executable:
+    """A prepared program: its storage, launches and (once captured) graph.
+    Its slots lie in one arena slab, or, given a Pool, are taken from the
+    pool's reserved range one by one."""
+
+    def __init__(self, program: Program, target: HIPTarget, inputs: Sequence[torch.Tensor], point: bool = True,
+                 pool: Pool | None = None):
         self.program = program
         self.target = target
         self.storage = storage(program)
-        self.arena = Arena(self.storage.sizes)
+        self.arena = Arena(self.storage.sizes) if pool is None else PoolSlots(pool, self.storage.sizes)
         self.own: dict[str, torch.Tensor] = {}
         self.bound: dict[str, torch.Tensor] = {}
         self.addresses: dict[str, int] = {}
@@ -282,8 +340,9 @@ class Executable:
         return "\n".join(lines)
 
 
-def prepare(program: Program, target: HIPTarget, *inputs: torch.Tensor, point: bool = True) -> Executable:
-    return Executable(program, target, inputs, point=point)
+def prepare(program: Program, target: HIPTarget, *inputs: torch.Tensor, point: bool = True,
+            pool: Pool | None = None) -> Executable:
+    return Executable(program, target, inputs, point=point, pool=pool)
 
 
 class Compiled:

@@ -800,6 +800,178 @@ def extremes_of_a_vector():
     return Case("the extremes of a vector", [g], {"v": F(v0)}, {"loss": 1}, ["loss"], closed)
 
 
+# ---- writes (test/fixtures/programs.jl:119-131): stores at addresses of their own ----
+
+def _copy(src, dst, shape):
+    """dst = copy(src): a pointwise group over `shape`."""
+    g = FloorGroup("pointwise", shape, name=f"{dst} = copy({src})")
+    n = int(np.prod(shape))
+    g.value(src, "f32", n)
+    g.value(dst, "f32", n)
+    g.output(dst, g.load(src, _lin(shape)), _lin(shape))
+    return g
+
+
+def _fill(dst, shape, value):
+    g = FloorGroup("pointwise", shape, name=f"{dst} .= {value}")
+    g.value(dst, "f32", int(np.prod(shape)))
+    g.output(dst, value, _lin(shape))
+    return g
+
+
+def _loss(shape, names, build):
+    """loss = sum over `shape` of build(g, loads...), one group."""
+    g = FloorGroup("reduction", shape, reduced=tuple(range(len(shape))), name="loss")
+    n = int(np.prod(shape))
+    for k in names:
+        g.value(k, "f32", n)
+    g.value("loss", "f32", 1)
+    g.output("loss", g.fold("sum", build(g, *[g.load(k, _lin(shape)) for k in names])).value, full=False)
+    return g
+
+
+def write_of_a_slice():
+    """y = copy(x); y[2:4, :] = v; sum(abs2, tanh.(y))."""
+    x, v = data(8, 6), data(3, 6, scale=0.3)
+    w = FloorGroup("pointwise", (3, 6), name="y[2:4, :] = v")
+    w.value("v", "f32", 18)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("v", (1, 3)), (1, 8), constant=1)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        Y[1:4, :] = val["v"].reshape(3, 6, order="F")
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.tanh(Y) ** 2)]}
+    return Case("a write of a slice", [_copy("x", "y", (8, 6)), w,
+                                       _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("tanh", y)))],
+                {"x": F(x), "v": F(v)}, {"y": 48, "loss": 1}, ["y", "loss"], closed)
+
+
+def padding_by_a_write():
+    """y = zeros(10, 8); y[2:9, 2:7] = x; sum(abs2, y .* data(10, 8))."""
+    x, d = data(8, 6), data(10, 8)
+    w = FloorGroup("pointwise", (8, 6), name="y[2:end-1, 2:end-1] = x")
+    w.value("x", "f32", 48)
+    w.value("y", "f32", 80)
+    w.output("y", w.load("x", (1, 8)), (1, 10), constant=11)
+
+    def closed(val):
+        Y = np.zeros((10, 8))
+        Y[1:9, 1:7] = val["x"].reshape(8, 6, order="F")
+        return {"y": Y.ravel(order="F"), "loss": [np.sum((Y * val["d"].reshape(10, 8, order="F")) ** 2)]}
+    return Case("padding by a write", [_fill("y", (10, 8), 0.0), w,
+                                       _loss((10, 8), ["y", "d"], lambda g, y, dd: g.apply("abs2", y * dd))],
+                {"x": F(x), "d": F(d)}, {"y": 80, "loss": 1}, ["y", "loss"], closed)
+
+
+def writes_through_views():
+    """y = zero(x); view(y, :, 2:3) .= x[:, 1:2] .* 2; y[1, :] .= 1; sum(abs2, y .+ x)."""
+    x = data(8, 6)
+    w1 = FloorGroup("pointwise", (8, 2), name="view(y, :, 2:3) .= x[:, 1:2] .* 2")
+    w1.value("x", "f32", 48)
+    w1.value("y", "f32", 48)
+    w1.output("y", w1.load("x", (1, 8)) * 2.0, (1, 8), constant=8)
+    w2 = FloorGroup("pointwise", (6,), name="y[1, :] .= 1")
+    w2.value("y", "f32", 48)
+    w2.output("y", 1.0, (8,))
+
+    def closed(val):
+        X = val["x"].reshape(8, 6, order="F")
+        Y = np.zeros((8, 6))
+        Y[:, 1:3] = X[:, 0:2] * 2
+        Y[0, :] = 1
+        return {"y": Y.ravel(order="F"), "loss": [np.sum((Y + X) ** 2)]}
+    return Case("writes through views", [_fill("y", (8, 6), 0.0), w1, w2,
+                                         _loss((8, 6), ["y", "x"], lambda g, y, xx: g.apply("abs2", y + xx))],
+                {"x": F(x)}, {"y": 48, "loss": 1}, ["y", "loss"], closed)
+
+
+def strided_and_reversed_writes():
+    """y = copy(x); y[1:2:8, end:-2:1] = v; sum(abs2, sin.(y)): rows 1, 3, 5, 7
+    and columns 6, 4, 2, an address with a negative coefficient."""
+    x, v = data(8, 6), data(4, 3, scale=0.3)
+    w = FloorGroup("pointwise", (4, 3), name="y[1:2:8, end:-2:1] = v")
+    w.value("v", "f32", 12)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("v", (1, 4)), (2, -16), constant=40)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        Y[0:8:2, 5::-2] = val["v"].reshape(4, 3, order="F")
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.sin(Y) ** 2)]}
+    return Case("strided and reversed writes", [_copy("x", "y", (8, 6)), w,
+                                                _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("sin", y)))],
+                {"x": F(x), "v": F(v)}, {"y": 48, "loss": 1}, ["y", "loss"], closed)
+
+
+def write_at_traced_positions():
+    """y = copy(x); y[:, i] .= v; y[i[1], 1] = 2 * v[3]; sum(abs2, tanh.(y)),
+    i = Int32[4, 1]: stores at gathered addresses, the last landing."""
+    x, v, i = data(8, 6), data(8, 2, scale=0.3), _idx([4, 1])
+    w1 = FloorGroup("pointwise", (8, 2), name="y[:, i] .= v")
+    w1.value("v", "f32", 16)
+    w1.value("i", "i32", 2)
+    w1.value("y", "f32", 48)
+    w1.output("y", w1.load("v", (1, 8)), (1, 0), constant=-8, gather=w1.load("i", (0, 1)), gather_coeff=8)
+    w2 = FloorGroup("pointwise", (1,), name="y[i[1], 1] = 2 v[3]")
+    w2.value("v", "f32", 16)
+    w2.value("i", "i32", 2)
+    w2.value("y", "f32", 48)
+    w2.output("y", w2.load("v", (0,), constant=2) * 2.0, (0,), constant=-1, gather=w2.load("i", (0,)), gather_coeff=1)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        V = val["v"].reshape(8, 2, order="F")
+        Y[:, [3, 0]] = V
+        Y[3, 0] = 2 * val["v"][2]
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.tanh(Y) ** 2)]}
+    return Case("a write at traced positions", [_copy("x", "y", (8, 6)), w1, w2,
+                                                _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("tanh", y)))],
+                {"x": F(x), "v": F(v), "i": i}, {"y": 48, "loss": 1}, ["y", "loss"], closed, dtypes={"i": "i32"})
+
+
+def mean_divided_in_place():
+    """r = sum(x; dims = 1); r ./= size(x, 1); sum(abs2, x .- r): a value
+    written, then read and written again in place."""
+    x = data(8, 6)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0,), name="r = sum(x; dims = 1)")
+    g1.value("x", "f32", 48)
+    g1.value("r", "f32", 6)
+    g1.output("r", g1.fold("sum", g1.load("x", (1, 8))).value, (0, 1), full=False)
+    g2 = FloorGroup("pointwise", (6,), name="r ./= 8")
+    g2.value("r", "f32", 6)
+    g2.output("r", g2.load("r", (1,)) / 8.0, (1,))
+    g3 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="sum(abs2, x .- r)")
+    g3.value("x", "f32", 48)
+    g3.value("r", "f32", 6)
+    g3.value("loss", "f32", 1)
+    g3.output("loss", g3.fold("sum", g3.apply("abs2", g3.load("x", (1, 8)) - g3.load("r", (0, 1)))).value, full=False)
+
+    def closed(val):
+        X = val["x"].reshape(8, 6, order="F")
+        r = X.sum(axis=0) / 8
+        return {"r": r, "loss": [np.sum((X - r) ** 2)]}
+    return Case("a mean divided in place", [g1, g2, g3], {"x": F(x)}, {"r": 6, "loss": 1}, ["r", "loss"], closed)
+
+
+def permutedims_and_copyto():
+    """y = permutedims(x) into a 6 x 8 array; z = copyto!(similar(x, 48), y);
+    sum(abs2, z .* data(48))."""
+    x, d = data(8, 6), data(48)
+    g1 = FloorGroup("pointwise", (8, 6), name="permutedims!(y, x, (2, 1))")
+    g1.value("x", "f32", 48)
+    g1.value("y", "f32", 48)
+    g1.output("y", g1.load("x", (1, 8)), (6, 1))
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").T
+        z = Y.ravel(order="F")
+        return {"y": z, "z": z, "loss": [np.sum((z * val["d"]) ** 2)]}
+    return Case("permutedims! and copyto!", [g1, _copy("y", "z", (48,)),
+                                             _loss((48,), ["z", "d"], lambda g, z, dd: g.apply("abs2", z * dd))],
+                {"x": F(x), "d": F(d)}, {"y": 48, "z": 48, "loss": 1}, ["y", "z", "loss"], closed)
+
+
 # ---- recomputed folds and recurrences ----------------------------------------------
 
 def mean_recomputed():
@@ -891,7 +1063,8 @@ CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, mi
          gather_by_a_list, gather_by_an_int32_matrix, gather_rows_by_an_int64_matrix,
          gather_by_linear_and_scalar_indices, embedding_and_layer_norm, scatter_add_gradient,
          extremes_and_where_they_are, extremes_of_a_vector, mean_recomputed, recurrence_with_recomputed_sums,
-         reverse_recurrence]
+         reverse_recurrence, write_of_a_slice, padding_by_a_write, writes_through_views, strided_and_reversed_writes,
+         write_at_traced_positions, mean_divided_in_place, permutedims_and_copyto]
 
 
 def run_oracle(case: Case) -> dict:

@@ -141,3 +141,74 @@ def test_timing_and_rates(target):
     assert 0 < t < 0.1
     w = l.work()
     assert w.bytes == 3 * 4 * 1024 * 4096 and w.kernels == 2
+
+
+def test_slots_taken_one_by_one_lie_in_one_reservation(target):
+    """A pool's reserved range (th_pool_*): the config-3 MLP program's slots
+    and a second executable's, allocated one at a time as `planned` does
+    (runtime.jl:415), all inside [base, base + reserved), the results the
+    arena's; freed blocks are reused."""
+    import tempest_hip as th
+    announce("slot pool")
+    pool = th.Pool(reserve=8 << 30)
+    base, reserved, mapped = pool.info()
+    assert reserved >= 8 << 30 and mapped <= reserved
+    rows, n = 300, 1000
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x, g = torch.randn(rows, n, device="cuda", generator=gen), torch.randn(rows, n, device="cuda", generator=gen)
+    prog = th.programs.mlp(512, 256, 1024, 256)
+    inputs = [(torch.randn(*reversed(prog.values[k].dims), device="cuda", generator=gen) * 0.05).to(torch.bfloat16)
+              for k in prog.inputs]
+    ex = th.prepare(prog, target, *inputs, pool=pool)
+    ref = th.prepare(prog, target, *inputs)
+    for e in (ex, ref):
+        e.execute()
+    torch.cuda.synchronize()
+    slots = [ex.addresses[name] for name, v in prog.values.items() if v.role == "stored"]
+    assert slots and all(base <= a < base + reserved for a in slots)
+    for a, b in zip(ex.outputs(), ref.outputs()):
+        if isinstance(a, torch.Tensor):
+            assert torch.equal(a, b)
+        else:
+            assert a == b
+    first = list(ex.arena.addresses)
+    ex.arena.destroy()
+    again = th.runtime.PoolSlots(pool, ex.storage.sizes)
+    assert again.addresses == first  # the freed blocks, first fit
+    softmax = th.prepare(th.programs.softmax_columns(rows, n), target, x, g, pool=pool)
+    softmax.execute()
+    torch.cuda.synchronize()
+    assert all(base <= a < base + reserved for a in softmax.arena.addresses)
+    again.destroy()
+
+
+def test_grouped_products_are_one_launch(target):
+    """Products alike but for where their operands start (cuBLASProducts'
+    build over bindings, ext/cuBLASExt.jl:262-326): one launch of three, each
+    product's values numbered after the previous ones'."""
+    import ctypes
+    import tempest_hip.launch as L
+    from tempest_hip import _lib
+    announce("grouped products")
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    As = [torch.randn(256, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(3)]
+    Bs = [torch.randn(256, 512, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(3)]
+    Cs = [torch.zeros(256, 256, device="cuda") for _ in range(3)]
+    descs = (_lib.GemmDesc * 3)()
+    for i in range(3):
+        descs[i] = _lib.GemmDesc(m=256, n=256, k=512, c_dtype=L.F32, a=As[i].data_ptr(), a_m=512, a_k=1,
+                                 b=Bs[i].data_ptr(), b_k=1, b_n=512, c=Cs[i].data_ptr(), c_ld=256, splits=1)
+    out = ctypes.c_void_p()
+    _lib.call("th_build_gemm_grouped", descs, 3, ctypes.byref(out))
+    l = L.Launch(out, tuple(f"{v}{i}" for i in range(3) for v in ("a", "b", "c", "bias", "aux", "aux_out",
+                                                                     "row_sums", "loss", "d")))
+    assert l.work().kernels == 3 and l.work().values == 27
+    # Product 1 moved to product 2's output: repointed by its own value number.
+    spare = torch.zeros(256, 256, device="cuda")
+    l.repoint("c1", spare.data_ptr())
+    l()
+    torch.cuda.synchronize()
+    for i, c in enumerate((Cs[0], spare, Cs[2])):
+        want = (As[i].double() @ Bs[i].double().T).T
+        assert relative(c.double().cpu().numpy(), want.cpu().numpy()) < 1e-5
+    assert not Cs[1].any()
