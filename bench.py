@@ -38,6 +38,31 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def graph_vs_direct(target, ex, reps: int, warmup: int = 2) -> dict:
+    """One step of an executable replayed as a graph and launched kernel by
+    kernel, each the device time per step from events around `reps` steps
+    back to back, and which of the two its capture chose from the device's
+    measured dispatch costs."""
+    import torch
+    g = target.capture(ex.launches, graph=True)
+    try:
+        t_graph = target.time_graph(g, warmup, reps)
+    finally:
+        g.release()
+    for _ in range(warmup):
+        ex.execute()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ex.execute()
+    e1.record()
+    torch.cuda.synchronize()
+    t_direct = e0.elapsed_time(e1) * 1e-3 / reps
+    return {"us_graph": t_graph * 1e6, "us_direct": t_direct * 1e6,
+            "kernels": sum(l.work().kernels for l in ex.launches),
+            "chosen": "graph" if ex.graphed else "direct"}
+
+
 def config2(target, steps: int, warmup: int):
     import torch
     import tempest_hip as th
@@ -82,8 +107,9 @@ def config2(target, steps: int, warmup: int):
             parity[name] = relative(dx.index_select(0, idx).cpu().numpy(), f(xs, gs)[1])
     except Exception as err:  # the bench's number stands without it
         parity["error"] = repr(err)
+    dispatch = {"softmax": graph_vs_direct(target, es, steps), "layernorm": graph_vs_direct(target, el, steps)}
     return dict(x=x, g=g, step_s=step_s, s_soft=s_soft, s_ln=s_ln, alg=alg, bytes_soft=bytes_soft,
-                bytes_ln=bytes_ln, parity=parity, describe=es.explain() + "\n" + el.explain())
+                bytes_ln=bytes_ln, parity=parity, dispatch=dispatch, describe=es.explain() + "\n" + el.explain())
 
 
 def config2_floor(target, x, g, steps: int = 10, warmup: int = 3):
@@ -290,9 +316,7 @@ def config1(target):
     x = torch.randn(16, 32, device="cuda", generator=gen)   # Julia x 32 x 16
     comp = th.compile(th.programs.tanh_layer(), target, w, b, x)
     ex = comp.executable
-    graph_s = target.time_graph(ex.graph, warmup=20, reps=2000)
-    launch = ex.launches[0]
-    execute_s = target.time_run(launch, warmup=20, reps=2000)
+    dispatch = graph_vs_direct(target, ex, reps=2000, warmup=20)
     for _ in range(50):
         comp(w, b, x)
     torch.cuda.synchronize()
@@ -301,8 +325,8 @@ def config1(target):
     for _ in range(n):
         comp(w, b, x)  # point, replay, copy dw/db/dx, read the loss
     call_s = (time.perf_counter() - t) / n
-    return {"us_per_step_graph": graph_s * 1e6, "us_per_step_execute": execute_s * 1e6,
-            "us_per_compiled_call_host": call_s * 1e6,
+    return {"us_per_step_graph": dispatch["us_graph"], "us_per_step_execute": dispatch["us_direct"],
+            "recording": dispatch["chosen"], "us_per_compiled_call_host": call_s * 1e6,
             "note": "graph/execute: device time per step from events around 2000 back-to-back replays/runs; "
                     "compiled call: host wall time of c(w, b, x) incl. result copies and the loss read"}
 
@@ -346,7 +370,8 @@ def config3(target, steps: int = 5, warmup: int = 2):
         s = evs[0].elapsed_time(evs[1]) * 1e-3 / 3
         per[g.name] = {"us": s * 1e6, "TFLOP/s": l.work().flops / s / 1e12}
     return {"ms_per_step": step_s * 1e3, "TFLOP/s": flops / step_s / 1e12,
-            "frac_of_bf16_peak": flops / step_s / BF16_PEAK, "flops_per_step": flops, "per_launch": per}
+            "frac_of_bf16_peak": flops / step_s / BF16_PEAK, "flops_per_step": flops, "per_launch": per,
+            "dispatch": graph_vs_direct(target, ex, steps)}
 
 
 def config4(target, steps: int = 3, warmup: int = 1):
@@ -479,7 +504,7 @@ def main() -> int:
                 "per_kernel": {"softmax_grad": {"us": c2["s_soft"] * 1e6, "GB/s": c2["alg"] / c2["s_soft"] / 1e9},
                                "layernorm_grad": {"us": c2["s_ln"] * 1e6, "GB/s": c2["alg"] / c2["s_ln"] / 1e9}},
                 "note": "per-program events bracket the fused row kernel and the loss's one-block sum"}
-    configs = {"config2_parity_rel": c2["parity"]}
+    configs = {"config2_parity_rel": c2["parity"], "config2_dispatch": c2["dispatch"]}
     if not a.only_config2:
         try:
             configs["config2_floor"] = config2_floor(target, c2["x"], c2["g"])

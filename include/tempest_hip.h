@@ -190,6 +190,16 @@ int th_time_graph(th_graph* graph, int warmup, int reps, double* host_seconds);
 /* Mean device seconds of one run of `launch` (warm), as th_time_graph. */
 int th_time_run(th_launch* launch, int warmup, int reps, double* host_seconds);
 
+/* What dispatch costs on this device, measured once per process with an
+ * empty kernel, each the mean of a long back-to-back run: `graph_base`, what
+ * replaying a graph costs beyond its launches; `in_graph`, one launch inside a
+ * replayed graph (th_rates.launch); `direct`, one launch made directly.  A
+ * recording of K launches replays faster as a graph when
+ * graph_base + K in_graph < K direct, else as its launches one by one.
+ * Extends replay_overhead and LAUNCH, ext/CUDAExt.jl:874-906, whose target
+ * always records a graph (capture(::CUDATarget, ...), ext/CUDAExt.jl:565). */
+int th_dispatch_costs(double* graph_base, double* in_graph, double* direct);
+
 /* ---- op class (a): fused pointwise + reductions -------------------------- */
 
 /* Softmax over each contiguous run of n (a column of the reference's n x rows

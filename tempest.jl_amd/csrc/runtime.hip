@@ -66,6 +66,12 @@ int launch_kernel(const Kernel& k, hipStream_t s) {
 
 }  // namespace th
 
+namespace th {
+// Timing helpers (below): the cache-clearing buffer, and what a replay adds.
+static int ensure_clearing();
+static int replay_overhead(double* out);
+}  // namespace th
+
 using namespace th;
 
 // A kernel that does nothing: what a replay alone adds is timed with it.
@@ -157,7 +163,14 @@ int th_device_rates(th_rates* out) {
   double bandwidth = 4.0 * 1.0e3 * clock_khz * bus_bits / 8.0;
   // CDNA4 has 256 MiB of MALL (Infinity Cache) behind the XCDs' L2.
   double cache = (double)p.l2CacheSize + 256.0 * 1024 * 1024;
-  out->launch = 5.0e-7;
+  // The launch gap measured on this device, once per process.
+  {
+    std::lock_guard<std::mutex> lock(g_timing);
+    if (int r = ensure_clearing()) return r;
+    double overhead = 0;
+    if (int r = replay_overhead(&overhead)) return r;
+  }
+  out->launch = ctx().launch_gap;
   out->bandwidth = bandwidth;
   out->cached = 2.0 * bandwidth;
   out->cache = cache;
@@ -687,6 +700,33 @@ static int replay_overhead(double* out) {
   th_graph_release(batch);
   if (r) return r;
   c.replay_overhead = std::max(0.0, t_alone - t_batch / many.size());
+  // An empty kernel's share of a long graph: the gap between launches inside
+  // a replayed graph, the cover's per-launch price (ext/CUDAExt.jl:904-906).
+  c.launch_gap = t_batch / many.size();
+  // What a replay costs beyond its launches, back to back (a one-launch
+  // graph replayed 100 times), and what a direct launch costs back to back:
+  // the two sides of graph-or-direct for a recording of K launches.
+  if ((r = th_graph_capture(one, 1, &alone))) return r;
+  double t_one = 0;
+  r = mean_replay(alone, 5, 100, &t_one);
+  th_graph_release(alone);
+  if (r) return r;
+  c.graph_base = std::max(0.0, t_one - c.launch_gap);
+  for (int i = 0; i < 5; ++i)
+    if ((r = launch_kernel(blank.kernels[0], c.stream))) return r;
+  hipEvent_t a, b;
+  TH_HIP(hipEventCreate(&a));
+  TH_HIP(hipEventCreate(&b));
+  TH_HIP(hipEventRecord(a, c.stream));
+  for (int i = 0; i < 200; ++i)
+    if ((r = launch_kernel(blank.kernels[0], c.stream))) return r;
+  TH_HIP(hipEventRecord(b, c.stream));
+  TH_HIP(hipEventSynchronize(b));
+  float ms = 0;
+  TH_HIP(hipEventElapsedTime(&ms, a, b));
+  TH_HIP(hipEventDestroy(a));
+  TH_HIP(hipEventDestroy(b));
+  c.direct_gap = ms * 1e-3 / 200;
   *out = c.replay_overhead;
   return TH_OK;
 }
@@ -722,6 +762,21 @@ int th_time_launch(th_launch* l, int samples, double* seconds) {
   th_graph_release(g);
   if (r) return r;
   *seconds = std::max(0.0, t - overhead);
+  return TH_OK;
+}
+
+int th_dispatch_costs(double* graph_base, double* in_graph, double* direct) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(graph_base && in_graph && direct, "th_dispatch_costs: null output");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  TH_HIP(hipStreamSynchronize(c.stream));
+  if (int r = ensure_clearing()) return r;
+  double overhead = 0;
+  if (int r = replay_overhead(&overhead)) return r;
+  *graph_base = c.graph_base;
+  *in_graph = c.launch_gap;
+  *direct = c.direct_gap;
   return TH_OK;
 }
 

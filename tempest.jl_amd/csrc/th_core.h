@@ -44,6 +44,9 @@ struct Context {
   size_t clear_bytes = 0;
   uint32_t* sink = nullptr;
   double replay_overhead = -1.0;
+  double launch_gap = -1.0;  // seconds a launch takes inside a long replayed graph
+  double graph_base = -1.0;  // seconds a replay costs beyond its launches, back to back
+  double direct_gap = -1.0;  // seconds a direct launch of an empty kernel takes, back to back
 };
 
 Context& ctx();

@@ -135,21 +135,45 @@ end
 launches_of(run::HIPLaunch) = (run,)
 launches_of(run::HIPFloorRun) = run.launches
 
+"""
+Steps that replay faster launched one by one than as one graph: a recording
+of the launches themselves, which carry their own repointed arguments (as the
+reference's target records a run of crossings, ext/CUDAExt.jl:561-566).
+"""
+struct HIPDirect
+    launches::Vector{HIPLaunch}
+    keep::Any
+end
+
+# Whether `kernels` kernels replay faster as one graph than launched directly,
+# from the costs th_dispatch_costs measures on this device once per process.
+function graph_pays(kernels)
+    base, gap, direct = Ref{Cdouble}(), Ref{Cdouble}(), Ref{Cdouble}()
+    check(ccall((:th_dispatch_costs, LIB), Cint, (Ptr{Cdouble}, Ptr{Cdouble}, Ptr{Cdouble}), base, gap, direct),
+        "th_dispatch_costs")
+    base[] + kernels * gap[] < kernels * direct[]
+end
+
 function capture(::HIPTarget, steps, keep)
-    handles = Ptr{Cvoid}[l.handle for s in steps for l in launches_of(s.step.run)]
+    launches = HIPLaunch[l for s in steps for l in launches_of(s.step.run)]
+    graph_pays(sum(l -> launch_work(l).kernels, launches; init = 0)) || return HIPDirect(launches, keep)
+    handles = Ptr{Cvoid}[l.handle for l in launches]
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_graph_capture, LIB), Cint, (Ptr{Ptr{Cvoid}}, Cint, Ptr{Ptr{Cvoid}}), handles, length(handles), out),
         "th_graph_capture")
     HIPGraph(out[], keep)
 end
-recapture(t::HIPTarget, g::HIPGraph, steps, keep) = (release(t, g); capture(t, steps, keep))
+recapture(t::HIPTarget, g::Union{HIPGraph, HIPDirect}, steps, keep) = (release(t, g); capture(t, steps, keep))
 replay(::HIPTarget, g::HIPGraph) = check(ccall((:th_graph_replay, LIB), Cint, (Ptr{Cvoid},), g.handle), "th_graph_replay")
+replay(::HIPTarget, d::HIPDirect) = foreach(l -> l(), d.launches)
 release(::HIPTarget, g::HIPGraph) =
     (g.handle == C_NULL || ccall((:th_graph_release, LIB), Cint, (Ptr{Cvoid},), g.handle); g.handle = C_NULL; nothing)
+release(::HIPTarget, ::HIPDirect) = nothing
 
 # Our kernels' argument layouts are known: the launches are repointed, then
 # their graph nodes take their arguments in place; nothing is learned or
 # re-recorded (ext/CUDAExt.jl:604-668 learns them).
+retarget!(::HIPTarget, ::HIPDirect, steps, moves, repoint) = (repoint(); true)
 function retarget!(::HIPTarget, g::HIPGraph, steps, moves, repoint)
     repoint()
     n = sum(s -> length(launches_of(s.step.run)), steps; init = 0)

@@ -12,8 +12,8 @@ without a GPU, construction raises.
 from ._lib import HIPError, LIBRARY, load  # noqa: F401
 from .launch import Launch  # noqa: F401
 from .runtime import Compiled, Executable, Group, Pool, Program, Value, compile, prepare, storage  # noqa: F401
-from .target import Graph, HIPTarget, Move  # noqa: F401
+from .target import Direct, Graph, HIPTarget, Move  # noqa: F401
 from . import programs  # noqa: F401
 
 __all__ = ["HIPError", "LIBRARY", "load", "Launch", "Compiled", "Executable", "Group", "Program", "Value",
-           "compile", "prepare", "storage", "Graph", "HIPTarget", "Move", "Pool", "programs"]
+           "compile", "prepare", "storage", "Direct", "Graph", "HIPTarget", "Move", "Pool", "programs"]

@@ -28,7 +28,7 @@ import torch
 
 from ._lib import call
 from .launch import Launch
-from .target import Graph, HIPTarget, Move
+from .target import Direct, Graph, HIPTarget, Move
 
 _ELEMENT = {torch.float32: 4, torch.bfloat16: 2, torch.float16: 2, torch.float64: 8, torch.int32: 4,
             torch.int64: 8, torch.uint8: 1}
@@ -221,18 +221,29 @@ class Executable:
         self.own: dict[str, torch.Tensor] = {}
         self.bound: dict[str, torch.Tensor] = {}
         self.addresses: dict[str, int] = {}
+        # The results share one allocation, each at a 256-byte boundary, so a
+        # call returns them with one copy and reads its numbers at once.
+        self.result_at: dict[str, tuple[int, int]] = {}
+        at = 0
+        for name, v in program.values.items():
+            if v.role == "result":
+                nbytes = max(1, v.count) * _ELEMENT[v.dtype]
+                self.result_at[name] = (at, nbytes)
+                at += (nbytes + 255) // 256 * 256
+        self.results = target.allocate(torch.uint8, max(at, 256))
         for name, v in program.values.items():
             if v.role == "stored":
                 self.addresses[name] = self.arena.addresses[self.storage.slots[name]]
             elif v.role == "result":
-                t = target.allocate(v.dtype, max(1, v.count))
+                off, nbytes = self.result_at[name]
+                t = self.results[off:off + nbytes].view(v.dtype)
                 self.own[name] = t
                 self.addresses[name] = t.data_ptr()
         self._check(inputs)
         for name, x in zip(program.inputs, inputs):
             self._take(name, x, point)
         self.launches = [g.build(dict(self.addresses)) for g in program.groups]
-        self.graph: Graph | None = None
+        self.graph: Graph | Direct | None = None
         self._moved: set[int] = set()
 
     # -- binding -------------------------------------------------------------
@@ -292,23 +303,31 @@ class Executable:
         self._moved.clear()  # the launches themselves carry the new addresses
         return self
 
-    def capture(self) -> "Executable":
-        """capture!(ex) (runtime.jl:1185): one graph of every launch."""
+    def capture(self, graph: bool | None = None) -> "Executable":
+        """capture!(ex) (runtime.jl:1185): one graph of every launch, or the
+        launches themselves where the target measures direct launches faster
+        for this many kernels (HIPTarget.graph_pays); ``graph`` forces it."""
         if self.graph is not None:
-            self.graph = self.target.recapture(self.graph, self.launches)
+            self.graph = self.target.recapture(self.graph, self.launches, as_graph=graph)
         else:
-            self.graph = self.target.capture(self.launches)
+            self.graph = self.target.capture(self.launches, graph=graph)
         self._moved.clear()
         return self
+
+    @property
+    def graphed(self) -> bool:
+        """Whether what capture recorded replays as a graph."""
+        return isinstance(self.graph, Graph)
 
     def replay(self) -> "Executable":
         """replay!(ex) (runtime.jl:1208): retarget what moved, then one graph launch."""
         if self.graph is None:
             raise RuntimeError("replay before capture")
-        for k in sorted(self._moved):
-            l = self.launches[k]
-            self.target.retarget(self.graph, k, [Move(n, 0, self.addresses[n], 0) for n in self.program.groups[k].values],
-                                 lambda: None)
+        if isinstance(self.graph, Graph):
+            for k in sorted(self._moved):
+                self.target.retarget(self.graph, k,
+                                     [Move(n, 0, self.addresses[n], 0) for n in self.program.groups[k].values],
+                                     lambda: None)
         self._moved.clear()
         self.target.replay(self.graph)
         return self
@@ -337,6 +356,9 @@ class Executable:
                  f"in {len(self.storage.sizes)} slots"]
         for g, l in zip(self.program.groups, self.launches):
             lines.append(f"  {g.name}: reads {', '.join(g.reads)}; writes {', '.join(g.writes)}; {l.describe()}")
+        if self.graph is not None:
+            lines.append("  replays as " + ("one graph" if self.graphed else "its launches, one by one (cheaper "
+                                            "than a graph for this many kernels on this device)"))
         return "\n".join(lines)
 
 
@@ -349,10 +371,19 @@ class Compiled:
     """compile(f, args...) for a planned program (compile.jl:48-62, 310-349)."""
 
     def __init__(self, program: Program, target: HIPTarget, inputs: Sequence[torch.Tensor], capture: bool = True):
-        self.executable = prepare(program, target, *inputs)
+        self.executable = ex = prepare(program, target, *inputs)
         self.signature = [(x.dtype, tuple(x.shape)) for x in inputs]
         if capture:
-            self.executable.capture()
+            ex.capture()
+        # Where each result lies in the executable's result allocation, and
+        # the span holding the numbers (read to the host in one copy).
+        self._layout = []
+        for name in program.outputs:
+            v = program.values[name]
+            off, nbytes = ex.result_at[name]
+            self._layout.append((off, nbytes, v.dtype, v.scalar, tuple(reversed(v.dims)) if len(v.dims) > 1 else None))
+        spans = [(off, off + nbytes) for off, nbytes, _, scalar, _ in self._layout if scalar]
+        self._numbers = (min(a for a, _ in spans), max(b for _, b in spans)) if spans else None
 
     def __call__(self, *args: torch.Tensor):
         sig = [(getattr(x, "dtype", None), tuple(getattr(x, "shape", ()))) for x in args]
@@ -364,10 +395,21 @@ class Compiled:
         return self.returned()
 
     def returned(self):
-        """Arrays copied, numbers read to the host (compile.jl:334-349)."""
+        """Arrays copied, numbers read to the host (compile.jl:334-349): one
+        copy of the result allocation, whose views are the arrays returned,
+        then one read of the span holding the numbers."""
+        fresh = self.executable.results.clone()
+        host = None
+        if self._numbers is not None:
+            lo, hi = self._numbers
+            host = fresh[lo:hi].cpu()
         out = []
-        for t in self.executable.outputs():
-            out.append(t.item() if t.dim() == 0 else t.clone())
+        for off, nbytes, dtype, scalar, shape in self._layout:
+            if scalar:
+                out.append(host[off - self._numbers[0]:off - self._numbers[0] + nbytes].view(dtype)[0].item())
+            else:
+                t = fresh[off:off + nbytes].view(dtype)
+                out.append(t.view(*shape) if shape is not None else t)
         return tuple(out)
 
 

@@ -60,6 +60,18 @@ class Graph:
             pass
 
 
+class Direct:
+    """What ``capture`` records where launching the steps one by one costs
+    less than replaying them as a graph: the launches themselves, which carry
+    their own (repointed) arguments."""
+
+    def __init__(self, steps: Sequence[Launch]):
+        self.steps = list(steps)
+
+    def release(self) -> None:
+        self.steps = []
+
+
 _initialised: int | None = None
 
 
@@ -83,6 +95,7 @@ class HIPTarget:
         self.online = online
         self.rounded_backward = rounded_backward
         self.deterministic_ = deterministic
+        self._dispatch: tuple[float, float, float] | None = None
         self._init()
 
     # -- device -----------------------------------------------------------------
@@ -165,15 +178,39 @@ class HIPTarget:
 
     # -- graphs ---------------------------------------------------------------------
 
-    def capture(self, steps: Sequence[Launch], keep=None) -> Graph:  # target.jl:541; CUDAExt.jl:565
+    def dispatch_costs(self) -> tuple[float, float, float]:
+        """(graph_base, in_graph, direct): device seconds, back to back, of a
+        graph replay beyond its launches, a launch inside a replayed graph and
+        a direct launch (th_dispatch_costs; measured once per process)."""
+        if self._dispatch is None:
+            a, b, c = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+            call("th_dispatch_costs", ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+            self._dispatch = (a.value, b.value, c.value)
+        return self._dispatch
+
+    def graph_pays(self, steps: Sequence[Launch]) -> bool:
+        """Whether K kernels replay faster as one graph than launched one by
+        one: graph_base + K in_graph < K direct."""
+        k = sum(s.work().kernels for s in steps)
+        base, gap, direct = self.dispatch_costs()
+        return base + k * gap < k * direct
+
+    def capture(self, steps: Sequence[Launch], keep=None, graph: bool | None = None) -> Graph | Direct:
+        """capture(target, steps, keep) (target.jl:541; CUDAExt.jl:565): one
+        graph of the steps, or, where launching them directly measures faster
+        on this device (``graph_pays``), the steps themselves; ``graph``
+        forces the choice."""
+        if not (self.graph_pays(steps) if graph is None else graph):
+            return Direct(steps)
         arr = (ctypes.c_void_p * len(steps))(*[s.handle.value for s in steps])
         out = ctypes.c_void_p()
         call("th_graph_capture", arr, len(steps), ctypes.byref(out))
         return Graph(out, steps)
 
-    def recapture(self, graph: Graph, steps: Sequence[Launch], keep=None) -> Graph:  # target.jl:550
+    def recapture(self, graph: Graph | Direct, steps: Sequence[Launch], keep=None,
+                  as_graph: bool | None = None) -> Graph | Direct:  # target.jl:550
         graph.release()
-        return self.capture(steps, keep)
+        return self.capture(steps, keep, as_graph)
 
     def retarget(self, graph: Graph, step: int, moves: Sequence[Move], repoint) -> bool:
         """retarget!(target, graph, steps, moves, repoint) (target.jl:552-565,
@@ -182,11 +219,16 @@ class HIPTarget:
         argument layouts are known, so nothing is learned and no re-record is
         needed: always true."""
         repoint()
-        call("th_graph_retarget", graph.handle, step)
+        if isinstance(graph, Graph):
+            call("th_graph_retarget", graph.handle, step)
         return True
 
-    def replay(self, graph: Graph) -> None:  # target.jl:568; CUDAExt.jl:739
-        call("th_graph_replay", graph.handle)
+    def replay(self, graph: Graph | Direct) -> None:  # target.jl:568; CUDAExt.jl:739
+        if isinstance(graph, Direct):
+            for s in graph.steps:
+                s()
+        else:
+            call("th_graph_replay", graph.handle)
 
     def release(self, graph: Graph) -> None:  # target.jl:571
         graph.release()
