@@ -39,8 +39,9 @@ typedef struct th_arena th_arena;   /* the slot arena: one device slab          
 /* Device rates as the cover prices them.
  * Replaces device_rates(::CUDATarget), ext/CUDAExt.jl:913-921. */
 typedef struct th_rates {
-  double launch;    /* seconds between launches inside a replayed graph      */
-  double cached;    /* bytes/s for a launch whose data the caches hold       */
+  double launch;    /* seconds between launches inside a replayed graph:
+                       an empty kernel's share of a long one (measured)    */
+  double cached;    /* bytes/s read from what L2 + MALL hold (measured)      */
   double bandwidth; /* bytes/s from HBM (memory clock x bus width)           */
   double cache;     /* bytes of last-level cache (L2 + MALL)                 */
   double blocks;    /* workgroups that fill the device (CUs)                 */
@@ -439,8 +440,22 @@ int th_build_floor(const th_floor_desc* desc, th_launch** host_out);
 int th_floor_source(const th_floor_desc* desc, char* host_out, size_t capacity, size_t* host_needed);
 
 /* Generate and compile the group's kernels into the code-object cache,
- * without a device (the "does it build" check of a group). */
+ * without a device (the "does it build" check of a group).
+ *
+ * The cache is a directory of code objects (TEMPEST_HIP_CACHE, else
+ * $XDG_CACHE_HOME/tempest_hip, else ~/.cache/tempest_hip), each named by a
+ * hash of its generated source and the compiler options; the source names
+ * the hiprtc and HIP runtime versions and the store's schema, so another
+ * toolchain's entries are never read.  The store is bounded by
+ * TEMPEST_HIP_CACHE_CAPACITY (bytes, or with a K/M/G suffix; 512 MiB by
+ * default; 0 turns it off) and removes the entries used least recently.
+ * Replaces the kernel store of src/Compiler/runtime/cache.jl:1-60 with its
+ * bound JULIA_OBJCACHE_CAPACITY (:43-45). */
 int th_floor_compile(const th_floor_desc* desc);
+
+/* Code objects loaded from the store and compiled, in this process: the
+ * counts cache_counts() reports, src/Compiler/runtime/cache.jl:56-58. */
+int th_floor_cache_counts(int64_t* host_loaded, int64_t* host_compiled);
 
 /* ---- the small program of config 1 -------------------------------------- */
 

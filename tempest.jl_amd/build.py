@@ -47,6 +47,14 @@ EXTRA = {
 }
 
 
+# The check build: AddressSanitizer and UndefinedBehaviorSanitizer on the host
+# code alone (the device code compiles as usual, uninstrumented), for the CPU
+# tests of what the library does without a device (the floor's validation,
+# planning, source writing, hiprtc and the code-object store).
+SAN_FLAGS = ("-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined "
+             "-Xarch_host -fno-sanitize-recover=undefined -Xarch_host -fno-omit-frame-pointer").split()
+
+
 def sources() -> list[pathlib.Path]:
     return sorted(CSRC.glob("*.hip"))
 
@@ -83,12 +91,56 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
     return LIB
 
 
+def build_sanitized(dest: pathlib.Path, jobs: int | None = None) -> pathlib.Path:
+    """The sanitized check library, built under `dest` (objects and
+    libtempest_hip.so).  Load it with TEMPEST_HIP_LIBRARY set to its path and
+    the sanitizer runtime preloaded (sanitizer_runtime())."""
+    dest = pathlib.Path(dest)
+    (dest / "obj").mkdir(parents=True, exist_ok=True)
+    lib = dest / "libtempest_hip.so"
+
+    def one(src: pathlib.Path) -> pathlib.Path:
+        obj = dest / "obj" / (src.stem + ".o")
+        cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), *SAN_FLAGS, "-Xarch_host", "-O1", "-Xarch_host", "-g",
+               "-c", str(src), "-o", str(obj)]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError(f"hipcc (sanitized host) failed on {src.name}:\n{p.stdout}{p.stderr}")
+        return obj
+
+    srcs = sources()
+    with cf.ThreadPoolExecutor(max_workers=jobs or min(len(srcs), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(one, srcs))
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", *SAN_FLAGS, "-o", str(lib),
+           *map(str, objs), "-lhiprtc"]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{p.stdout}{p.stderr}")
+    return lib
+
+
+def sanitizer_runtime() -> pathlib.Path:
+    """The AddressSanitizer runtime the sanitized library links against (the
+    ROCm clang's own), to preload: python itself is not instrumented."""
+    clang = pathlib.Path(HIPCC).resolve().parent / "../llvm/bin/clang"
+    if not clang.exists():
+        clang = pathlib.Path("/opt/rocm/llvm/bin/clang")
+    out = subprocess.run([str(clang), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                         text=True, check=True).stdout.strip()
+    path = pathlib.Path(out)
+    if not path.is_absolute() or not path.exists():
+        raise RuntimeError(f"no AddressSanitizer runtime found ({out!r})")
+    return path
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--sanitize", metavar="DIR", default=None,
+                    help="build only the host-sanitized (ASan + UBSan) check library, under DIR")
     a = ap.parse_args()
-    print(build(a.jobs, a.verbose))
+    print(build_sanitized(pathlib.Path(a.sanitize), a.jobs) if a.sanitize else build(a.jobs, a.verbose))
 
 
 if __name__ == "__main__":

@@ -23,9 +23,12 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <dirent.h>
+#include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cinttypes>
 #include <cmath>
 #include <cstdio>
@@ -860,6 +863,23 @@ struct Stage {
   int phase_index;  // the phase a split stage folds; -1 for the stage that stores
 };
 
+// What decides a code object beside its source and options: the hiprtc that
+// compiles it, the HIP runtime that loads it, and the layout of this store.
+// It is written into every generated source, so the store's key (a hash of
+// the source) changes with it and entries of another toolchain are never read.
+const int kStoreSchema = 2;
+
+std::string toolchain() {
+  static const std::string s = [] {
+    int major = 0, minor = 0, runtime = 0;
+    hiprtcVersion(&major, &minor);
+    if (hipRuntimeGetVersion(&runtime) != hipSuccess) runtime = HIP_VERSION;
+    return "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + ", HIP runtime " +
+           std::to_string(runtime) + ", store schema " + std::to_string(kStoreSchema);
+  }();
+  return s;
+}
+
 class Writer {
  public:
   explicit Writer(const Plan& pl) : pl_(pl), d_(pl.d) {}
@@ -867,6 +887,7 @@ class Writer {
   std::string source(std::vector<Stage>& stages, const std::string& base) {
     std::ostringstream& o = o_;
     o << "// tempest-hip floor: " << describe() << "\n";
+    o << "// toolchain: " << toolchain() << "\n";
     o << kPrelude << (pl_.W > 1 ? kVector : kScalar);
     o << "struct th_args { void* p[" << (d_->n_values + (pl_.reduction ? d_->n_folds : 0)) << "]; };\n";
     if (pl_.recurrence) {
@@ -1787,6 +1808,24 @@ const char* kOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17",
                           // No packed FP32 instructions: plain float code compiles to scalar VALU.
                           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
 
+// The store's bound in bytes: TEMPEST_HIP_CACHE_CAPACITY (bytes, or with a
+// K, M or G suffix), 512 MiB by default; 0 keeps nothing (nothing is read or
+// written).  As JULIA_OBJCACHE_CAPACITY bounds the reference's store
+// (src/Compiler/runtime/cache.jl:43-45).
+long long cache_capacity() {
+  const char* e = std::getenv("TEMPEST_HIP_CACHE_CAPACITY");
+  if (!e || !*e) return 512LL << 20;
+  char* end = nullptr;
+  long long v = std::strtoll(e, &end, 10);
+  if (end && (*end == 'K' || *end == 'k')) v <<= 10;
+  else if (end && (*end == 'M' || *end == 'm')) v <<= 20;
+  else if (end && (*end == 'G' || *end == 'g')) v <<= 30;
+  return std::max(0LL, v);
+}
+
+// Code objects loaded from the store and compiled, in this process.
+int64_t g_loaded = 0, g_compiled = 0;
+
 std::string cache_dir() {
   std::string dir;
   if (const char* e = std::getenv("TEMPEST_HIP_CACHE"); e && *e) dir = e;
@@ -1809,14 +1848,55 @@ struct Compiled {
 
 std::mutex g_mutex;
 
-// Code object for `source`: from the cache on disk, else hiprtc.
+// Remove the entries used least recently (the oldest modification time; a
+// load touches its entry) until the store holds at most `capacity` bytes,
+// keeping `keep`, the entry just written.
+void trim(const std::string& dir, long long capacity, const std::string& keep) {
+  struct Entry {
+    std::string path;
+    long long bytes;
+    struct timespec used;
+  };
+  std::vector<Entry> entries;
+  long long total = 0;
+  if (DIR* dp = opendir(dir.c_str())) {
+    while (struct dirent* de = readdir(dp)) {
+      std::string name = de->d_name;
+      if (name.rfind("floor-", 0) != 0 || name.size() < 6 || name.substr(name.size() - 6) != ".hsaco") continue;
+      std::string path = dir + "/" + name;
+      struct stat st;
+      if (stat(path.c_str(), &st) != 0) continue;
+      entries.push_back({path, (long long)st.st_size, st.st_mtim});
+      total += st.st_size;
+    }
+    closedir(dp);
+  }
+  if (total <= capacity) return;
+  std::sort(entries.begin(), entries.end(), [](const Entry& a, const Entry& b) {
+    return a.used.tv_sec != b.used.tv_sec ? a.used.tv_sec < b.used.tv_sec : a.used.tv_nsec < b.used.tv_nsec;
+  });
+  for (const Entry& e : entries) {
+    if (total <= capacity) break;
+    if (e.path == keep) continue;
+    if (std::remove(e.path.c_str()) == 0) total -= e.bytes;
+  }
+}
+
+// Code object for `source`: from the store on disk, else hiprtc (then kept
+// in the store, which is trimmed to its capacity).
 int code_object(const std::string& source, const std::string& key, std::vector<char>& code) {
-  std::string path = cache_dir() + "/floor-" + key + ".hsaco";
-  {
+  const long long capacity = cache_capacity();
+  const std::string dir = capacity > 0 ? cache_dir() : std::string();
+  std::string path = dir + "/floor-" + key + ".hsaco";
+  if (capacity > 0) {
     std::ifstream in(path, std::ios::binary);
     if (in) {
       code.assign(std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>());
-      if (!code.empty()) return TH_OK;
+      if (!code.empty()) {
+        (void)utimensat(AT_FDCWD, path.c_str(), nullptr, 0);  // used now
+        ++g_loaded;
+        return TH_OK;
+      }
     }
   }
   hiprtcProgram prog;
@@ -1838,13 +1918,17 @@ int code_object(const std::string& source, const std::string& key, std::vector<c
   code.resize(n);
   hiprtcGetCode(prog, code.data());
   hiprtcDestroyProgram(&prog);
-  // Keep it: written beside, then renamed into place.
+  ++g_compiled;
+  if (capacity <= 0) return TH_OK;
+  // Keep it: written beside, then renamed into place (a lost write only
+  // compiles again).
   std::string tmp = path + ".tmp" + std::to_string((long)getpid());
   {
     std::ofstream out(tmp, std::ios::binary);
     out.write(code.data(), (std::streamsize)code.size());
   }
   if (std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
+  trim(dir, capacity, path);
   return TH_OK;
 }
 
@@ -1894,6 +1978,14 @@ int th_floor_source(const th_floor_desc* desc, char* out, size_t capacity, size_
   return TH_OK;
 }
 
+int th_floor_cache_counts(int64_t* loaded, int64_t* compiled) {
+  TH_REQUIRE(loaded && compiled, "th_floor_cache_counts: null output");
+  std::lock_guard<std::mutex> lock(g_mutex);
+  *loaded = g_loaded;
+  *compiled = g_compiled;
+  return TH_OK;
+}
+
 int th_floor_compile(const th_floor_desc* desc) {
   Plan pl;
   Compiled c;
@@ -1919,7 +2011,7 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
       hipError_t e = hipModuleLoadData(&m->module, c.code.data());
       if (e != hipSuccess) {
         // A damaged cache file: compile afresh once.
-        std::remove((cache_dir() + "/floor-" + c.key + ".hsaco").c_str());
+        if (cache_capacity() > 0) std::remove((cache_dir() + "/floor-" + c.key + ".hsaco").c_str());
         if (int r = code_object(c.source, c.key, c.code)) return r;
         TH_HIP(hipModuleLoadData(&m->module, c.code.data()));
       }

@@ -67,9 +67,11 @@ int launch_kernel(const Kernel& k, hipStream_t s) {
 }  // namespace th
 
 namespace th {
-// Timing helpers (below): the cache-clearing buffer, and what a replay adds.
+// Timing helpers (below): the cache-clearing buffer, what a replay adds, and
+// the rate of reads the caches serve.
 static int ensure_clearing();
 static int replay_overhead(double* out);
+static int cached_rate(double* out);
 }  // namespace th
 
 using namespace th;
@@ -88,15 +90,16 @@ struct ClearArgs {
   const u32x4* a;
   uint32_t* sink;
   uint64_t n;
+  int passes;  // reads of the n words, one after another
 };
 __global__ __launch_bounds__(256) void th_clear_kernel(ClearArgs c) {
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   uint32_t s = 0;
-  for (; i < c.n; i += stride) {
-    u32x4 v = c.a[i];
-    s ^= v[0] ^ v[1] ^ v[2] ^ v[3];
-  }
+  for (int p = 0; p < c.passes; ++p)
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < c.n; i += stride) {
+      u32x4 v = c.a[i];
+      s ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+    }
   if (s == 0xffffffffu) c.sink[0] = s;
 }
 
@@ -163,16 +166,19 @@ int th_device_rates(th_rates* out) {
   double bandwidth = 4.0 * 1.0e3 * clock_khz * bus_bits / 8.0;
   // CDNA4 has 256 MiB of MALL (Infinity Cache) behind the XCDs' L2.
   double cache = (double)p.l2CacheSize + 256.0 * 1024 * 1024;
-  // The launch gap measured on this device, once per process.
+  // The launch gap and the cached read rate measured on this device, once
+  // per process.
+  double cached = 0;
   {
     std::lock_guard<std::mutex> lock(g_timing);
     if (int r = ensure_clearing()) return r;
     double overhead = 0;
     if (int r = replay_overhead(&overhead)) return r;
+    if (int r = cached_rate(&cached)) return r;
   }
   out->launch = ctx().launch_gap;
   out->bandwidth = bandwidth;
-  out->cached = 2.0 * bandwidth;
+  out->cached = cached;
   out->cache = cache;
   out->blocks = (double)p.multiProcessorCount;
   return TH_OK;
@@ -618,10 +624,45 @@ static int ensure_clearing() {
 
 static int clear_cache() {
   Context& c = ctx();
-  ClearArgs a{static_cast<const u32x4*>(c.clear_buf), c.sink, c.clear_bytes / 16};
+  ClearArgs a{static_cast<const u32x4*>(c.clear_buf), c.sink, c.clear_bytes / 16, 1};
   int blocks = c.prop.multiProcessorCount * 8;
   hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
   TH_HIP(hipGetLastError());
+  return TH_OK;
+}
+
+// Bytes a second read from what the caches hold: 64 MiB (within L2 + MALL)
+// read 16 times over in one launch of the clearing kernel, the best of 5
+// launches after one, once per process.  The reference takes twice the
+// memory's rate for it (ext/CUDAExt.jl:908-921); this is the device's own.
+static int cached_rate(double* out) {
+  Context& c = ctx();
+  if (c.cached_rate < 0) {
+    const uint64_t bytes = std::min<uint64_t>(64ull << 20, c.clear_bytes);
+    const int passes = 16;
+    ClearArgs a{static_cast<const u32x4*>(c.clear_buf), c.sink, bytes / 16, passes};
+    int blocks = c.prop.multiProcessorCount * 8;
+    hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
+    TH_HIP(hipGetLastError());
+    hipEvent_t ev[6];
+    for (auto& e : ev) TH_HIP(hipEventCreate(&e));
+    TH_HIP(hipEventRecord(ev[0], c.stream));
+    for (int i = 0; i < 5; ++i) {
+      hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
+      TH_HIP(hipGetLastError());
+      TH_HIP(hipEventRecord(ev[i + 1], c.stream));
+    }
+    TH_HIP(hipEventSynchronize(ev[5]));
+    float best = 1e30f;
+    for (int i = 0; i < 5; ++i) {
+      float ms = 0;
+      TH_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+      best = std::min(best, ms);
+    }
+    for (auto& e : ev) TH_HIP(hipEventDestroy(e));
+    c.cached_rate = (double)passes * bytes / (best * 1e-3);
+  }
+  *out = c.cached_rate;
   return TH_OK;
 }
 

@@ -46,6 +46,7 @@ struct Context {
   double replay_overhead = -1.0;
   double launch_gap = -1.0;  // seconds a launch takes inside a long replayed graph
   double graph_base = -1.0;  // seconds a replay costs beyond its launches, back to back
+  double cached_rate = -1.0;  // bytes/s read from what L2 + MALL hold
   double direct_gap = -1.0;  // seconds a direct launch of an empty kernel takes, back to back
 };
 

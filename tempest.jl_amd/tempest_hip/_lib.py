@@ -9,10 +9,14 @@ cover catches (src/Compiler/cover/choose.jl:1014-1025).
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import threading
 
-LIBRARY = pathlib.Path(__file__).resolve().parent.parent / "libtempest_hip.so"
+# TEMPEST_HIP_LIBRARY names another build of the same ABI (the host-only
+# sanitized check build); by default the in-tree library.
+LIBRARY = pathlib.Path(os.environ.get("TEMPEST_HIP_LIBRARY") or
+                       pathlib.Path(__file__).resolve().parent.parent / "libtempest_hip.so")
 
 c_void_p = ctypes.c_void_p
 c_int = ctypes.c_int
@@ -164,6 +168,7 @@ SIGNATURES: dict[str, list] = {
     "th_build_floor": [P(FloorDesc), P(c_void_p)],
     "th_floor_source": [P(FloorDesc), c_char_p, c_size, P(c_size)],
     "th_floor_compile": [P(FloorDesc)],
+    "th_floor_cache_counts": [P(c_i64), P(c_i64)],
     "th_build_tanh_layer_grad": [c_i32, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, P(c_void_p)],
 }

@@ -16,7 +16,9 @@ writes them in the same format (a key, a tab, a number per line):
   refold`` is 0: the floor's claims state no steps.
 - ``HIP memory latency / bandwidth``: this library claims no plain column
   fold, so the device's launch and cached rates, as fit_memory! keeps for a
-  package without one.
+  package without one; both are measured (th_device_rates: an empty kernel's
+  share of a long replayed graph, and the read rate of 64 MiB the caches
+  hold).
 - ``HIP BFloat16 latency / rate / split / recompute``: the bf16 product at
   two sizes; the rate is the slope of seconds on flops, the latency the
   smaller's time less its flops at that rate; the products neither split
