@@ -155,6 +155,20 @@ int th_launch_describe(th_launch* launch, char* host_out, size_t capacity);
 
 int th_launch_destroy(th_launch* launch);
 
+/* A launch's workspace: the bytes of device memory its kernels use beyond its
+ * values (partial sums, statistics, stored intermediates such as attention's
+ * dS'), 0 for none.  Builders allocate nothing: a launch without a workspace
+ * given allocates it at its first run or capture and owns it;
+ * th_launch_set_workspace gives it memory of the caller's instead (256-byte
+ * aligned, at least th_launch_workspace bytes, alive while the launch runs),
+ * freeing one it owned.  A graph captured before must be retargeted
+ * (th_graph_retarget).  This lets a planner place workspaces in its arena
+ * beside the slots (`planned`'s allocations, src/Compiler/runtime/runtime.jl:415),
+ * as the reference's floor takes its workspaces from the target
+ * (allocate(target, ...) in build_floor, src/Compiler/runtime/runtime.jl:1326-1327). */
+int th_launch_workspace(th_launch* launch, uint64_t* host_bytes);
+int th_launch_set_workspace(th_launch* launch, void* ptr);
+
 /* ---- graphs ------------------------------------------------------------ */
 
 /* Record `n` launches, in order, as one graph of kernel nodes.
@@ -601,9 +615,10 @@ int th_build_attention_fwd(const th_attention_desc* desc, th_launch** host_out);
  * deterministic (no atomics); the general kernels need lse.  With grouped heads (kv_heads < heads) dk and
  * dv sum over the heads / kv_heads query heads that read each key/value
  * head, swept in turn (test/cuda/attention.jl:132-140).  The dK/dV sweep stores dS
- * (bf16, 2*batch*heads*seq^2 bytes of workspace the launch owns) for the dQ
- * sweep; when that exceeds 16 GiB, or with TH_ATTN_RECOMPUTE_DQ, the dQ sweep
- * recomputes S and dP instead and the workspace is not allocated.
+ * (bf16, 2*batch*heads*seq^2 bytes of the launch's workspace, th_launch_workspace)
+ * for the dQ sweep; when that exceeds 16 GiB, or with TH_ATTN_RECOMPUTE_DQ, the
+ * dQ sweep recomputes S and dP instead and the workspace holds only the row
+ * statistics.
  * Values: 0 q, 1 k, 2 v, 3 o, 4 lse, 5 dout, 6 dq, 7 dk, 8 dv, 9 starts,
  * 10 lengths.  Replaces the
  * cuTile transposed folds of the backward (ext/cuTileExt/transpose.jl:1-213). */
@@ -619,7 +634,9 @@ int th_build_attention_bwd(const th_attention_desc* desc, th_launch** host_out);
  * d + h*strides[0] + t*strides[1] + b*strides[2]; a (the log-gates) and beta,
  * da, dbeta are fp32 (heads, positions, batch) at gate_strides.  dk = dv =
  * 128, chunk 64, seq a multiple of 64.  The gradient is of
- * sum(o .* dout) with respect to q, k, v, a and beta.
+ * sum(o .* dout) with respect to q, k, v, a and beta; there o may be null, and
+ * is then kept in the launch's workspace (laid out at q's strides).  The chunk
+ * intermediates lie in the workspace (th_launch_workspace).
  * Values: 0 q, 1 k, 2 v, 3 a, 4 beta, 5 o, 6 dout, 7 dq, 8 dk, 9 dv, 10 da,
  * 11 dbeta.  Replaces the scan and recurrence sketches (ext/cuTileExt/
  * build.jl:715-839; codegen/scalar.jl:354-440; runtime/stepped.jl). */

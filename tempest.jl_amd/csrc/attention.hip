@@ -1110,23 +1110,14 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   // offsets from a (batch, head) base.
   TH_REQUIRE((double)d->seq * d->q_strides[1] * 2 < 2147483648.0,
              "attention: a sequence of Q or dO must span under 2 GiB (seq x position stride x 2 bytes)");
-  void* delta = nullptr;
   const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
-  // delta ([b][s][h]), then the per-block statistics (2 floats per row).
-  if (int r = th::device_alloc((size_t)rows * 3 * sizeof(float), &delta)) return r;
-  b.own(delta);
-  a.delta = static_cast<float*>(delta);
-  a.stat = a.delta + rows;
-  // dS' is stored for the dQ sweep when it fits the workspace budget
-  // (4 GiB at B8 H16 S4096); beyond it dQ recomputes S and dP instead.
+  // Workspace: delta ([b][s][h]), then the per-block statistics (2 floats
+  // per row); then dS', stored for the dQ sweep when it fits the budget
+  // (4 GiB at B8 H16 S4096; beyond it dQ recomputes S and dP instead).
+  const uint64_t at_delta = b.workspace((uint64_t)rows * 3 * sizeof(float));
   const double ds_bytes = 2.0 * d->batch * d->heads * (double)d->seq * d->seq;
   const bool store = ds_bytes <= kDsBudget && !(d->flags & TH_ATTN_RECOMPUTE_DQ);
-  if (store) {
-    void* ds = nullptr;
-    if (int r = th::device_alloc((size_t)ds_bytes, &ds)) return r;
-    b.own(ds);
-    a.ds = static_cast<uint16_t*>(ds);
-  }
+  const uint64_t at_ds = store ? b.workspace((uint64_t)ds_bytes) : 0;
   const void* dkdv = store ? (const void*)attn_bwd_dkdv<true> : (const void*)attn_bwd_dkdv<false>;
   const void* dqk = store ? (const void*)attn_bwd_dq_ds : (const void*)attn_bwd_dq;
   const size_t dq_lds = store ? kDqDsLds : kDqLds;
@@ -1142,6 +1133,11 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
                           TH_OFFSET(AttnArgs, dq),  TH_OFFSET(AttnArgs, dk), TH_OFFSET(AttnArgs, dv)};
   for (int v = 0; v < 9; ++v)
     for (int kk : {k0, k1, k2}) b.ref(v, kk, offs[v]);
+  for (int kk : {k0, k1, k2}) {
+    b.ws_ref(kk, TH_OFFSET(AttnArgs, delta), at_delta);
+    b.ws_ref(kk, TH_OFFSET(AttnArgs, stat), at_delta + (uint64_t)rows * sizeof(float));
+    if (store) b.ws_ref(kk, TH_OFFSET(AttnArgs, ds), at_ds);
+  }
   for (int v : {0, 1, 2, 3, 5, 6, 7, 8}) b.align(v, 16);
   const double S = d->seq, BH = (double)d->batch * d->heads;
   const double flops = 2.5 * 4.0 * BH * S * S * kD * (d->causal ? 0.5 : 1.0);

@@ -527,10 +527,7 @@ int build_attention_general_bwd(const th_attention_desc* d, th_launch** out) {
   GenArgs a = args_of(d);
   th::Builder b("attention_bwd", 11);
   const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
-  void* delta = nullptr;
-  if (int r = th::device_alloc((size_t)rows * sizeof(float), &delta)) return r;
-  b.own(delta);
-  a.delta = static_cast<float*>(delta);
+  const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));  // delta, [b][s][h]
   const void* f0 = f32 ? (const void*)attn_gen_delta<true> : (const void*)attn_gen_delta<false>;
   const void* f1 = f32 ? dkdv_kernel<true>(dp) : dkdv_kernel<false>(dp);
   const void* f2 = f32 ? dq_kernel<true>(dp) : dq_kernel<false>(dp);
@@ -548,6 +545,7 @@ int build_attention_general_bwd(const th_attention_desc* d, th_launch** out) {
                            TH_OFFSET(GenArgs, starts), TH_OFFSET(GenArgs, lengths)};
   for (int v = 0; v < 11; ++v)
     for (int kk : {k0, k1, k2}) b.ref(v, kk, offs[v]);
+  for (int kk : {k0, k1, k2}) b.ws_ref(kk, TH_OFFSET(GenArgs, delta), at_delta);
   const double S = d->seq, K = a.kv_seq, BH = (double)d->batch * d->heads, e = f32 ? 4.0 : 2.0;
   const double flops = 2.5 * 4.0 * BH * S * K * d->head_dim * (d->causal ? 0.5 : 1.0);
   b.work(e * d->head_dim * (4.0 * BH * S + 4.0 * d->batch * d->kv_heads * K) + 8.0 * BH * S, flops,

@@ -1164,7 +1164,7 @@ int check(const th_deltanet_desc* d, bool backward) {
   TH_REQUIRE(d->chunk == kC, "deltanet: the chunk must be 64");
   TH_REQUIRE(d->seq > 0 && d->seq % kC == 0, "deltanet: the sequence length must be a positive multiple of 64");
   TH_REQUIRE(d->batch > 0 && d->heads > 0, "deltanet: batch and heads must be positive");
-  TH_REQUIRE(d->q && d->k && d->v && d->a && d->beta && d->o, "deltanet: null q, k, v, a, beta or o");
+  TH_REQUIRE(d->q && d->k && d->v && d->a && d->beta && (d->o || backward), "deltanet: null q, k, v, a, beta or o");
   TH_REQUIRE(aligned(d->q, 16) && aligned(d->k, 16) && aligned(d->v, 16) && aligned(d->o, 16),
              "deltanet: q, k, v, o must be 16-byte aligned");
   TH_REQUIRE(d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0 && d->strides[2] % 8 == 0,
@@ -1184,8 +1184,6 @@ int build(const th_deltanet_desc* d, bool backward, th_launch** out) {
   const int64_t chunks = (int64_t)d->batch * d->heads * (d->seq / kC);
   TH_REQUIRE(chunks <= 0x7fffffff, "deltanet: too many chunks");
   const Workspace w = workspace(chunks, backward);
-  void* ws = nullptr;
-  if (int r = th::device_alloc(w.bytes, &ws)) return r;
   DnArgs a{};
   a.q = static_cast<const uint16_t*>(d->q);
   a.k = static_cast<const uint16_t*>(d->k);
@@ -1199,9 +1197,13 @@ int build(const th_deltanet_desc* d, bool backward, th_launch** out) {
   a.dv = static_cast<uint16_t*>(d->dv_out);
   a.da = d->da;
   a.dbeta = d->dbeta;
-  char* base = static_cast<char*>(ws);
-  float** slots[14] = {&a.ca, &a.T, &a.W, &a.Ut, &a.S, &a.U, &a.P, &a.dU, &a.dSn, &a.dQg, &a.dW, &a.dKd, &a.dP, &a.dg};
-  for (int i = 0; i < 14; ++i) *slots[i] = (i < 7 || backward) ? reinterpret_cast<float*>(base + w.offs[i]) : nullptr;
+  // The per-chunk intermediates (ca, T, W, Ut, S, U, P; for the backward dU,
+  // dSn, dQg, dW, dKd, dP, dg) lie in the launch's workspace at w.offs.
+  const size_t slot_args[14] = {TH_OFFSET(DnArgs, ca),  TH_OFFSET(DnArgs, T),   TH_OFFSET(DnArgs, W),
+                                TH_OFFSET(DnArgs, Ut),  TH_OFFSET(DnArgs, S),   TH_OFFSET(DnArgs, U),
+                                TH_OFFSET(DnArgs, P),   TH_OFFSET(DnArgs, dU),  TH_OFFSET(DnArgs, dSn),
+                                TH_OFFSET(DnArgs, dQg), TH_OFFSET(DnArgs, dW),  TH_OFFSET(DnArgs, dKd),
+                                TH_OFFSET(DnArgs, dP),  TH_OFFSET(DnArgs, dg)};
   a.s_h = d->strides[0];
   a.s_t = d->strides[1];
   a.s_b = d->strides[2];
@@ -1217,7 +1219,12 @@ int build(const th_deltanet_desc* d, bool backward, th_launch** out) {
   const size_t ldss[6] = {kPrepLds, kScanLds, kOutLds, kSgLds, kGaLds, kGbLds};
   for (int i = 0; i < 6; ++i) TH_HIP(hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)ldss[i]));
   th::Builder b(backward ? "deltanet_fwd_bwd" : "deltanet_fwd", 12);
-  b.own(ws);
+  const uint64_t at_ws = b.workspace(w.bytes);
+  // A gradient with no o given keeps it in the workspace, at q's strides.
+  const bool own_o = d->o == nullptr;
+  const uint64_t o_bytes = 2 * ((uint64_t)(d->heads - 1) * d->strides[0] + (uint64_t)(d->seq - 1) * d->strides[1] +
+                                (uint64_t)(d->batch - 1) * d->strides[2] + kD);
+  const uint64_t at_o = own_o ? b.workspace(o_bytes) : 0;
   const unsigned nchunks = (unsigned)chunks;
   const unsigned scans = (unsigned)((int64_t)d->batch * d->heads * (kD / kCols));
   int ks[6];
@@ -1234,7 +1241,13 @@ int build(const th_deltanet_desc* d, bool backward, th_launch** out) {
                            TH_OFFSET(DnArgs, beta), TH_OFFSET(DnArgs, o), TH_OFFSET(DnArgs, dout), TH_OFFSET(DnArgs, dq),
                            TH_OFFSET(DnArgs, dk), TH_OFFSET(DnArgs, dv), TH_OFFSET(DnArgs, da),  TH_OFFSET(DnArgs, dbeta)};
   for (int v = 0; v < 12; ++v)
-    for (int i = 0; i < nk; ++i) b.ref(v, ks[i], offs[v]);
+    if (!(own_o && v == 5))
+      for (int i = 0; i < nk; ++i) b.ref(v, ks[i], offs[v]);
+  if (own_o)
+    for (int i = 0; i < nk; ++i) b.ws_ref(ks[i], offs[5], at_o);
+  for (int j = 0; j < 14; ++j)
+    if (j < 7 || backward)
+      for (int i = 0; i < nk; ++i) b.ws_ref(ks[i], slot_args[j], at_ws + w.offs[j]);
   for (int v : {0, 1, 2, 5, 6, 7, 8, 9}) b.align(v, 16);
   // Algorithmic work: per chunk, forward ~ C^2 dk (A) + C^3/3 (T) + 2 C^2 d (W, U~) + C^2 dk (P)
   // + 2 C dk dv (W S, Qg S) + C^2 dv (P U) + C dk dv (Kd' U) multiply-adds; the backward ~2.3x.

@@ -2034,13 +2034,11 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
   Builder b("floor", d->n_values);
   for (int v = 0; v < d->n_values; ++v)
     if (pl.W > 1 && pl.vec_ok[v]) b.align(v, d->values[v].dtype == TH_F32 ? 16 : 8);
-  for (int f = 0; f < nws; ++f) {
-    void* w = nullptr;
-    size_t bytes = (size_t)std::max<int64_t>(pl.items, 1) * pl.P * state_size(d->folds[f].kind) * sizeof(float);
-    if (int r = device_alloc(bytes, &w)) return r;
-    b.own(w);
-    args.p[d->n_values + f] = w;
-  }
+  // Workspace: a split fold's partial states, one piece a fold.
+  std::vector<uint64_t> at_fold(nws);
+  for (int f = 0; f < nws; ++f)
+    at_fold[f] = b.workspace((uint64_t)std::max<int64_t>(pl.items, 1) * pl.P * state_size(d->folds[f].kind) *
+                             sizeof(float));
   const size_t arg_bytes = sizeof(void*) * (d->n_values + (pl.reduction ? d->n_folds : 0));
   if (pl.items > 0) {
     const int64_t blocks = pl.reduction ? (pl.items + pl.S - 1) / pl.S * pl.P : (pl.qn + pl.S - 1) / pl.S;
@@ -2049,6 +2047,7 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
       int k = b.module_kernel(mod->fns.at(s.name), mod->names[&s - &c.stages[0]].c_str(), dim3((unsigned)blocks),
                               dim3(pl.S * pl.L), 0, args, arg_bytes);
       for (int v = 0; v < d->n_values; ++v) b.ref(v, k, sizeof(void*) * v);
+      for (int f = 0; f < nws; ++f) b.ws_ref(k, sizeof(void*) * (d->n_values + f), at_fold[f]);
     }
   }
   // Algorithmic bytes: every value read once, every output written once.

@@ -186,25 +186,22 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   g.c_split = 0;
   g.ksplit = ksplit;
   const int64_t mn = (int64_t)M * N;
+  // Workspace: the fp32 sums of each part of K (staged products), then the
+  // epilogue's per-tile row sums and loss partials.
+  uint64_t at_parts = 0, at_sums = 0;
   if (staged) {
-    void* ws = nullptr;
-    if (int r = th::device_alloc((size_t)batch * splits * mn * sizeof(float), &ws)) return r;
-    b.own(ws);
-    g.c = ws;
+    at_parts = b.workspace((uint64_t)batch * splits * mn * sizeof(float));
+    g.c = nullptr;
     g.ldc = M;
     g.c_batch = (int64_t)splits * mn;
     g.c_split = mn;
   }
   const bool sums = epi == TH_EPI_SQUARE_LOSS || epi == TH_EPI_GELU_BACKWARD;
   const int blocks = tiles_m * tiles_n;
-  if (sums) {
-    void* ws = nullptr;
-    const size_t floats = (size_t)2 * tiles_n * M + (size_t)4 * blocks;
-    if (int r = th::device_alloc(floats * sizeof(float), &ws)) return r;
-    b.own(ws);
-    g.partial = static_cast<float*>(ws);
-  }
+  if (sums) at_sums = b.workspace(((uint64_t)2 * tiles_n * M + (uint64_t)4 * blocks) * sizeof(float));
   int k = b.kernel(fn, name, dim3(blocks, splits, batch), dim3(kThreads), (uint32_t)lds_bytes, g);
+  if (staged) b.ws_ref(k, TH_OFFSET(GemmArgs, c), at_parts);
+  if (sums) b.ws_ref(k, TH_OFFSET(GemmArgs, partial), at_sums);
   b.ref(0, k, TH_OFFSET(GemmArgs, a));
   b.ref(1, k, TH_OFFSET(GemmArgs, b));
   if (!staged) b.ref(2, k, TH_OFFSET(GemmArgs, c));
@@ -214,7 +211,7 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   for (int v : {0, 1, 2}) b.align(v, 16);
   for (int v : {3, 4, 5}) b.align(v, 8);
   if (staged) {
-    ReduceArgs ra{static_cast<const float*>(g.c), d->c, static_cast<const uint16_t*>(d->bias),
+    ReduceArgs ra{nullptr, d->c, static_cast<const uint16_t*>(d->bias),
                   accumulate ? d->d : nullptr, d->c_ld, d->c_batch, d->d_ld ? d->d_ld : d->c_ld,
                   d->d_ld ? d->d_batch : d->c_batch, M, N, splits, d->c_dtype};
     int kr = b.kernel((const void*)sum_splits, "sum_splits", dim3((unsigned)((mn + 255) / 256), batch), dim3(256), 0,
@@ -222,16 +219,19 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
     b.ref(2, kr, TH_OFFSET(ReduceArgs, c));
     b.ref(3, kr, TH_OFFSET(ReduceArgs, bias));
     b.ref(8, kr, TH_OFFSET(ReduceArgs, d));
+    b.ws_ref(kr, TH_OFFSET(ReduceArgs, ws), at_parts);
   }
   if (sums) {
-    RowSumArgs rs{g.partial, static_cast<uint16_t*>(d->row_sums), M, 2 * tiles_n};
+    RowSumArgs rs{nullptr, static_cast<uint16_t*>(d->row_sums), M, 2 * tiles_n};
     int k2 = b.kernel((const void*)sum_parts, "sum_parts", dim3((M + 255) / 256), dim3(256), 0, rs);
     b.ref(6, k2, TH_OFFSET(RowSumArgs, out));
+    b.ws_ref(k2, TH_OFFSET(RowSumArgs, partial), at_sums);
   }
   if (epi == TH_EPI_SQUARE_LOSS) {
-    LossArgs ls{g.partial + (size_t)2 * tiles_n * M, d->loss, 4 * blocks};
+    LossArgs ls{nullptr, d->loss, 4 * blocks};
     int k3 = b.kernel((const void*)sum_loss, "sum_loss", dim3(1), dim3(256), 0, ls);
     b.ref(7, k3, TH_OFFSET(LossArgs, loss));
+    b.ws_ref(k3, TH_OFFSET(LossArgs, partial), at_sums + (uint64_t)2 * tiles_n * M * sizeof(float));
   }
   const double mm = M, nn = N, kk = K, bb = batch;
   const double cbytes = d->c_dtype == TH_F32 ? 4 : 2;
@@ -273,6 +273,13 @@ extern "C" int th_build_gemm_grouped(const th_gemm_desc* descs, int count, th_la
     }
     g->owned.insert(g->owned.end(), l->owned.begin(), l->owned.end());
     l->owned.clear();
+    // Its workspace follows the previous products' in the whole's.
+    for (th::WsRef r : l->ws_refs) {
+      r.kernel += k0;
+      r.at += g->ws_bytes;
+      g->ws_refs.push_back(r);
+    }
+    g->ws_bytes += l->ws_bytes;
     g->work.bytes += l->work.bytes;
     g->work.flops += l->work.flops;
     g->work.blocks += l->work.blocks;

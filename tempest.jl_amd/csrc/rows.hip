@@ -494,12 +494,8 @@ int build_rows(Op op, const char* title, int64_t rows, int32_t n, int64_t ld, fl
     return th::fail(TH_E_UNSUPPORTED, std::string(title) + ": rows longer than 16384 are not built");
   th::Builder b(title, grad ? 4 : 2);
   RowArgs a{x, g, out, nullptr, rows, ld, n, eps};
-  if (grad) {
-    void* partial = nullptr;
-    if (int r = th::device_alloc((size_t)rows * sizeof(float), &partial)) return r;
-    b.own(partial);
-    a.partial = static_cast<float*>(partial);
-  }
+  // Workspace: the rows' loss partials.
+  const uint64_t at_partial = grad ? b.workspace((uint64_t)rows * sizeof(float)) : 0;
   int k = b.kernel(fn, kname, dim3((unsigned)rows), dim3(kThreads), 0, a);
   b.ref(0, k, TH_OFFSET(RowArgs, x));
   const uint32_t need = (n % 4 == 0 && ld % 4 == 0 && aligned) ? 16 : 4;
@@ -512,6 +508,8 @@ int build_rows(Op op, const char* title, int64_t rows, int32_t n, int64_t ld, fl
     SumArgs s{a.partial, loss, rows};
     int k2 = b.kernel((const void*)sum_all, "sum_all", dim3(1), dim3(1024), 0, s);
     b.ref(3, k2, TH_OFFSET(SumArgs, out));
+    b.ws_ref(k, TH_OFFSET(RowArgs, partial), at_partial);
+    b.ws_ref(k2, TH_OFFSET(SumArgs, x), at_partial);
     b.work(3.0 * 4.0 * (double)rows * n, (op == kSoftmaxGrad ? 8.0 : 10.0) * (double)rows * n,
            rows);
   } else {

@@ -54,6 +54,22 @@ int device_alloc(size_t bytes, void** out) {
   return TH_OK;
 }
 
+// Write the workspace's address into every kernel argument that points into it.
+void point_workspace(th_launch* l) {
+  for (const WsRef& r : l->ws_refs) {
+    void* at = static_cast<char*>(l->ws) + r.at;
+    std::memcpy(l->kernels[r.kernel].args + r.offset, &at, sizeof(void*));
+  }
+}
+
+int ensure_workspace(th_launch* l) {
+  if (l->ws_bytes == 0 || l->ws) return TH_OK;
+  if (int r = device_alloc(l->ws_bytes, &l->ws)) return r;
+  l->ws_owned = true;
+  point_workspace(l);
+  return TH_OK;
+}
+
 int launch_kernel(const Kernel& k, hipStream_t s) {
   void* params[1] = {const_cast<unsigned char*>(k.args)};
   hipError_t e = k.module
@@ -461,6 +477,7 @@ int th_pool_destroy(th_pool* p) {
 int th_launch_run(th_launch* l) {
   if (int r = require_ready()) return r;
   TH_REQUIRE(l != nullptr, "th_launch_run: null launch");
+  if (int r = ensure_workspace(l)) return r;
   for (const Kernel& k : l->kernels)
     if (int r = launch_kernel(k, ctx().stream)) return r;
   return TH_OK;
@@ -497,10 +514,32 @@ int th_launch_describe(th_launch* l, char* out, size_t capacity) {
   return TH_OK;
 }
 
+int th_launch_workspace(th_launch* l, uint64_t* bytes) {
+  TH_REQUIRE(l != nullptr && bytes != nullptr, "th_launch_workspace: null argument");
+  *bytes = l->ws_bytes;
+  return TH_OK;
+}
+
+int th_launch_set_workspace(th_launch* l, void* ptr) {
+  TH_REQUIRE(l != nullptr, "th_launch_set_workspace: null launch");
+  TH_REQUIRE(l->ws_bytes > 0, "th_launch_set_workspace: " + l->name + " has no workspace");
+  TH_REQUIRE(ptr != nullptr && reinterpret_cast<uintptr_t>(ptr) % 256 == 0,
+             "th_launch_set_workspace: the workspace must be a 256-byte aligned device address");
+  if (l->ws_owned) {
+    TH_HIP(hipStreamSynchronize(ctx().stream));  // no kernel of this launch still reads the old one
+    TH_HIP(hipFree(l->ws));
+  }
+  l->ws = ptr;
+  l->ws_owned = false;
+  th::point_workspace(l);
+  return TH_OK;
+}
+
 int th_launch_destroy(th_launch* l) {
   if (!l) return TH_OK;
   for (void* p : l->owned)
     if (p) TH_HIP(hipFree(p));
+  if (l->ws_owned && l->ws) TH_HIP(hipFree(l->ws));
   delete l;
   return TH_OK;
 }
@@ -548,6 +587,11 @@ int th_graph_capture(th_launch* const* steps, int n, th_graph** out) {
   hipGraphNode_t last = nullptr;
   for (int i = 0; i < n; ++i) {
     th_launch* l = steps[i];
+    if (int r = ensure_workspace(l)) {
+      (void)hipGraphDestroy(g->graph);
+      delete g;
+      return r;
+    }
     g->steps.push_back(l);
     g->nodes.emplace_back();
     for (Kernel& k : l->kernels) {

@@ -77,6 +77,14 @@ struct Ref {
   uint32_t offset;
 };
 
+// A pointer into the launch's workspace: kernel, byte offset of the pointer
+// in its arguments, byte offset of what it points at in the workspace.
+struct WsRef {
+  int kernel;
+  uint32_t offset;
+  uint64_t at;
+};
+
 }  // namespace th
 
 struct th_launch {
@@ -84,7 +92,14 @@ struct th_launch {
   std::vector<th::Kernel> kernels;
   std::vector<std::vector<th::Ref>> values;  // per value: every place it is read
   std::vector<uint32_t> align;               // per value: the alignment the build assumed
-  std::vector<void*> owned;                  // workspaces the launch owns
+  std::vector<void*> owned;                  // buffers the launch owns
+  // The workspace: device memory its kernels use beyond its values, given by
+  // the caller (th_launch_set_workspace) or allocated at the first run or
+  // capture, then owned.
+  uint64_t ws_bytes = 0;
+  void* ws = nullptr;
+  bool ws_owned = false;
+  std::vector<th::WsRef> ws_refs;
   th_work work{};
 };
 
@@ -122,6 +137,15 @@ class Builder {
   // Value `v` must stay aligned to `bytes` when it is repointed.
   void align(int v, uint32_t bytes) { l_->align[v] = std::max(l_->align[v], bytes); }
   void own(void* p) { l_->owned.push_back(p); }
+  // Reserve `bytes` of the launch's workspace (256-byte aligned pieces, laid
+  // out in order); returns the piece's offset in it.
+  uint64_t workspace(uint64_t bytes) {
+    const uint64_t at = l_->ws_bytes;
+    l_->ws_bytes += (std::max<uint64_t>(bytes, 1) + 255) / 256 * 256;
+    return at;
+  }
+  // The pointer at byte `offset` of kernel `k`'s arguments is workspace + at.
+  void ws_ref(int k, size_t offset, uint64_t at) { l_->ws_refs.push_back(WsRef{k, (uint32_t)offset, at}); }
   // A kernel compiled at run time: `fn` is a module function.
   template <class Args>
   int module_kernel(hipFunction_t fn, const char* name, dim3 grid, dim3 block, uint32_t shmem,
@@ -158,6 +182,10 @@ class Builder {
 #define TH_OFFSET(Args, member) offsetof(Args, member)
 
 int launch_kernel(const Kernel& k, hipStream_t s);
+// Give the launch its workspace if it has none yet (allocated and owned).
+int ensure_workspace(th_launch* l);
+// Write the workspace's address into the kernel arguments that use it.
+void point_workspace(th_launch* l);
 // Find, on `device` (current), the address of the static scratch that
 // th_softmax_grad_noalloc uses; th_init calls it once per device.
 int rows_scratch_setup(int device);

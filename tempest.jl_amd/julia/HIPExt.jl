@@ -96,9 +96,23 @@ mutable struct HIPLaunch
     handle::Ptr{Cvoid}
     buffers::Vector{Any}
     operands::Vector{Tuple{Int, Int, Int, DataType}}
-    function HIPLaunch(h, buffers, operands = Tuple{Int, Int, Int, DataType}[])
+    function HIPLaunch(h, buffers, operands = Tuple{Int, Int, Int, DataType}[], pool::Ptr{Cvoid} = C_NULL)
         l = new(h, buffers, operands)
         finalizer(x -> ccall((:th_launch_destroy, LIB), Cint, (Ptr{Cvoid},), x.handle), l)
+        # Its workspace (partial sums, stored dS', ...) from the target's pool,
+        # beside the slots, as the reference's floor takes its workspaces from
+        # the target (runtime.jl:1326-1327); without a pool, allocated at the first run.
+        if pool != C_NULL
+            n = Ref{UInt64}(0)
+            check(ccall((:th_launch_workspace, LIB), Cint, (Ptr{Cvoid}, Ptr{UInt64}), h, n), "th_launch_workspace")
+            if n[] > 0
+                ws = HIPBuffer{UInt8}(pool, n[])
+                check(ccall((:th_launch_set_workspace, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}), h, ws.ptr),
+                      "th_launch_set_workspace")
+                push!(l.buffers, ws)
+            end
+        end
+        l
     end
 end
 (l::HIPLaunch)() = check(ccall((:th_launch_run, LIB), Cint, (Ptr{Cvoid},), l.handle), "th_launch_run")
@@ -310,11 +324,11 @@ estimate(::HIPProducts, b::Binding, target, g) =
 product_operands(b::Binding) =
     operands_of(((0, b.arrays.A), (1, b.arrays.B), (2, b.arrays.C), (8, get(b.arrays, :D, nothing))))
 
-function build(::HIPProducts, ::HIPTarget, b::Binding, resources)
+function build(::HIPProducts, t::HIPTarget, b::Binding, resources)
     d = Ref(gemm_desc(b))
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_build_gemm, LIB), Cint, (Ptr{GemmDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_gemm")
-    l = HIPLaunch(out[], Any[s.buffer for s in values(b.arrays)], product_operands(b))
+    l = HIPLaunch(out[], Any[s.buffer for s in values(b.arrays)], product_operands(b), t.pool)
     (l, "HIP product $(b.extents.m)×$(b.extents.n) summing $(b.extents.k)" *
         (b.extents.b > 1 ? ", batch $(b.extents.b)" : "") * (b.template == ACCUMULATED ? ", added to a matrix" : "") *
         ": " * describe(l))
@@ -325,14 +339,14 @@ end
 supports(lib::HIPProducts, target::HIPTarget, bs::Vector{Binding}) =
     all(b -> supports(lib, target, b) && b.template != ACCUMULATED, bs)
 
-function build(::HIPProducts, ::HIPTarget, bs::Vector{Binding}, resources)
+function build(::HIPProducts, t::HIPTarget, bs::Vector{Binding}, resources)
     descs = [gemm_desc(b) for b in bs]
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_build_gemm_grouped, LIB), Cint, (Ptr{GemmDesc}, Cint, Ptr{Ptr{Cvoid}}), descs, length(descs), out),
         "th_build_gemm_grouped")
     # Product i's value v is value 9 (i - 1) + v of the grouped launch.
     ops = reduce(vcat, [[(v, 9 * (i - 1) + j, o, T) for (v, j, o, T) in product_operands(b)] for (i, b) in enumerate(bs)])
-    l = HIPLaunch(out[], Any[s.buffer for b in bs for s in values(b.arrays)], ops)
+    l = HIPLaunch(out[], Any[s.buffer for b in bs for s in values(b.arrays)], ops, t.pool)
     (l, "$(length(bs)) HIP products, one launch: " * describe(l))
 end
 
@@ -381,7 +395,7 @@ end
 
 supports(::HIPEpilogues, ::HIPTarget, b::Binding) = epilogue_desc(b; buffers = false) !== nothing
 
-function build(::HIPEpilogues, ::HIPTarget, b::Binding, resources)
+function build(::HIPEpilogues, t::HIPTarget, b::Binding, resources)
     d = Ref(epilogue_desc(b))
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_build_gemm, LIB), Cint, (Ptr{GemmDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_gemm")
@@ -390,7 +404,7 @@ function build(::HIPEpilogues, ::HIPTarget, b::Binding, resources)
     named = b.template == 1 ? ((0, a.W), (1, a.x), (2, a.Z), (3, a.b), (5, a.H)) :
         b.template == 2 ? ((0, a.W), (1, a.x), (2, a.dy), (3, a.b), (6, a.db), (7, a.loss)) :
         ((0, a.W), (1, a.x), (2, a.dz), (4, a.Z), (6, a.db))
-    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named))
+    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named), t.pool)
     (l, ("GELU layer", "square loss", "GELU backward")[b.template] * " fused into a HIP product: " * describe(l))
 end
 
@@ -493,7 +507,7 @@ function estimate(::HIPAttention, b::Binding, target, g)
     [Work(g.bytes; flops = causal(b) ? flops / 2 : flops, factor = b.arrays.q.eltype)]
 end
 
-function build(::HIPAttention, ::HIPTarget, b::Binding, resources)
+function build(::HIPAttention, t::HIPTarget, b::Binding, resources)
     d = Ref(attention_desc(b))
     out = Ref{Ptr{Cvoid}}()
     a = b.arrays
@@ -506,7 +520,7 @@ function build(::HIPAttention, ::HIPTarget, b::Binding, resources)
             "th_build_attention_fwd")
         named = ((0, a.q), (1, a.k), (2, a.v), (3, a.o), (4, get(a, :lse, nothing)))
     end
-    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named))
+    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named), t.pool)
     (l, "HIP attention" * (backward(b) ? " backward" : "") * (causal(b) ? ", causal" : "") * ": " * describe(l))
 end
 
@@ -541,7 +555,7 @@ function supports(::HIPRows, ::HIPTarget, b::Binding)
     b.template <= 2 ? b.arrays.g.strides == x.strides : b.extents.n <= 16384
 end
 
-function build(::HIPRows, ::HIPTarget, b::Binding, resources)
+function build(::HIPRows, t::HIPTarget, b::Binding, resources)
     a, e = b.arrays, b.extents
     out = Ref{Ptr{Cvoid}}()
     if b.template == 1
@@ -564,7 +578,7 @@ function build(::HIPRows, ::HIPTarget, b::Binding, resources)
             e.r, e.n, a.x.strides[2], 1.0f-5, address(a.x), address(a.y), out), "th_build_layernorm_fwd")
         named = ((0, a.x), (1, a.y))
     end
-    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named))
+    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named), t.pool)
     (l, ("softmax gradient", "LayerNorm gradient", "softmax", "LayerNorm")[b.template] * ", rows resident: " * describe(l))
 end
 
@@ -613,7 +627,7 @@ function supports(::HIPDeltaNet, ::HIPTarget, b::Binding)
         all(s -> s.eltype === Float32 && s.strides == a.a.strides, (a.a, a.beta))
 end
 
-function build(::HIPDeltaNet, ::HIPTarget, b::Binding, resources)
+function build(::HIPDeltaNet, t::HIPTarget, b::Binding, resources)
     a, e = b.arrays, b.extents
     grad = b.template == 2
     p(s) = address_or_null(s)
@@ -632,7 +646,7 @@ function build(::HIPDeltaNet, ::HIPTarget, b::Binding, resources)
         check(ccall((:th_build_deltanet_fwd, LIB), Cint, (Ptr{DeltaNetDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_deltanet_fwd")
         named = ((0, a.q), (1, a.k), (2, a.v), (3, a.a), (4, a.beta), (5, a.o))
     end
-    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named))
+    l = HIPLaunch(out[], Any[s.buffer for s in values(a)], operands_of(named), t.pool)
     (l, "chunked gated DeltaNet" * (grad ? " gradient" : "") * ": " * describe(l))
 end
 
@@ -799,13 +813,13 @@ function floor_desc(kind, domain, reduced, flags, vals, terms, folds, outs)
               pointer(vals), pointer(terms), isempty(folds) ? C_NULL : pointer(folds), pointer(outs))
 end
 
-function floor_launch(kind, domain, reduced, flags, vals, terms, folds, outs, keep, operands)
+function floor_launch(kind, domain, reduced, flags, vals, terms, folds, outs, keep, operands, pool = C_NULL)
     out = Ref{Ptr{Cvoid}}()
     GC.@preserve vals terms folds outs begin
         d = Ref(floor_desc(kind, domain, reduced, flags, vals, terms, folds, outs))
         check(ccall((:th_build_floor, LIB), Cint, (Ptr{FloorDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_floor")
     end
-    HIPLaunch(out[], keep, operands)
+    HIPLaunch(out[], keep, operands, pool)
 end
 
 # The group's kinds by name; any other throws, so that the build falls back.
@@ -926,7 +940,7 @@ function build_floor(target::HIPTarget, p, g, buffers)
         folds = [phased; recomputed]
         terms = [t.op == 5 ? CTerm(t.op, t.fn, t.args, t.ref + length(phased), t.observe, t.lit, t.index) : t for t in b.terms]
         push!(launches, floor_launch(kind, g.domain, reduced, flags, floor_values(b, bufs), terms, folds, outs, Any[bufs...],
-                                     operands))
+                                     operands, target.pool))
     end
     run = HIPFloorRun(launches)
     (run, "HIP floor: " * join(map(describe, launches), "; "))

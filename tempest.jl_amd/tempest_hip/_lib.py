@@ -152,6 +152,8 @@ SIGNATURES: dict[str, list] = {
     "th_time_launch": [c_void_p, c_int, P(c_double)],
     "th_time_graph": [c_void_p, c_int, c_int, P(c_double)],
     "th_time_run": [c_void_p, c_int, c_int, P(c_double)],
+    "th_launch_workspace": [c_void_p, P(c_u64)],
+    "th_launch_set_workspace": [c_void_p, c_void_p],
     "th_dispatch_costs": [P(c_double), P(c_double), P(c_double)],
     "th_build_softmax_grad": [c_i64, c_i32, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)],
     "th_softmax_grad_noalloc": [c_i64, c_i32, c_i64, c_void_p, c_void_p, c_void_p, c_void_p],

@@ -39,6 +39,17 @@ class Launch:
         call("th_launch_work", self.handle, ctypes.byref(w))
         return w
 
+    def workspace(self) -> int:
+        """Bytes of device memory the launch's kernels use beyond its values
+        (th_launch_workspace): allocated at the first run unless given."""
+        n = ctypes.c_uint64()
+        call("th_launch_workspace", self.handle, ctypes.byref(n))
+        return n.value
+
+    def set_workspace(self, ptr: int) -> None:
+        """Use the memory at ``ptr`` (256-byte aligned) as the workspace."""
+        call("th_launch_set_workspace", self.handle, ctypes.c_void_p(ptr))
+
     def describe(self) -> str:
         buf = ctypes.create_string_buffer(2048)
         call("th_launch_describe", self.handle, buf, len(buf))

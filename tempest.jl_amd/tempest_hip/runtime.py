@@ -243,8 +243,35 @@ class Executable:
         for name, x in zip(program.inputs, inputs):
             self._take(name, x, point)
         self.launches = [g.build(dict(self.addresses)) for g in program.groups]
+        self._place_workspaces(pool)
         self.graph: Graph | Direct | None = None
         self._moved: set[int] = set()
+
+    def _place_workspaces(self, pool: Pool | None) -> None:
+        """Give each launch's workspace (attention's dS', split sums, ...) a
+        slot beside the program's: the slots and workspaces are laid out
+        again in one arena (or taken from the pool), the launches repointed
+        to it.  The first arena, built before the workspaces were known,
+        goes."""
+        self.workspaces = [l.workspace() for l in self.launches]
+        if not any(self.workspaces):
+            return
+        sizes = list(self.storage.sizes) + [w for w in self.workspaces if w]
+        arena = Arena(sizes) if pool is None else PoolSlots(pool, sizes)
+        for name, v in self.program.values.items():
+            if v.role == "stored":
+                self.addresses[name] = arena.addresses[self.storage.slots[name]]
+        for g, l in zip(self.program.groups, self.launches):
+            for i, v in enumerate(g.values):
+                if v in self.program.values and self.program.values[v].role == "stored":
+                    l.repoint(i, self.addresses[v])
+        j = len(self.storage.sizes)
+        for l, w in zip(self.launches, self.workspaces):
+            if w:
+                l.set_workspace(arena.addresses[j])
+                j += 1
+        self.arena.destroy()
+        self.arena = arena
 
     # -- binding -------------------------------------------------------------
 
@@ -352,8 +379,9 @@ class Executable:
 
     def explain(self) -> str:
         """explain (runtime.jl:1216-1238): each kernel and what runs it."""
+        ws = sum(1 for w in self.workspaces if w)
         lines = [f"{self.program.name}: {len(self.launches)} launches, arena {self.arena.bytes} bytes "
-                 f"in {len(self.storage.sizes)} slots"]
+                 f"in {len(self.storage.sizes)} slots" + (f" and {ws} workspaces" if ws else "")]
         for g, l in zip(self.program.groups, self.launches):
             lines.append(f"  {g.name}: reads {', '.join(g.reads)}; writes {', '.join(g.writes)}; {l.describe()}")
         if self.graph is not None:

@@ -178,10 +178,13 @@ def test_slots_taken_one_by_one_lie_in_one_reservation(target):
             assert torch.equal(a, b)
         else:
             assert a == b
-    first = list(ex.arena.addresses)
+    # The slots and the products' workspaces (the GELU backward's row sums,
+    # the loss partials) were taken again once the workspaces were known; the
+    # first blocks went back to the pool.
+    assert len(ex.arena.addresses) == len(ex.storage.sizes) + sum(1 for w in ex.workspaces if w) > len(ex.storage.sizes)
     ex.arena.destroy()
     again = th.runtime.PoolSlots(pool, ex.storage.sizes)
-    assert again.addresses == first  # the freed blocks, first fit
+    assert again.addresses[0] == base  # every block freed, first fit from the start
     softmax = th.prepare(th.programs.softmax_columns(rows, n), target, x, g, pool=pool)
     softmax.execute()
     torch.cuda.synchronize()
@@ -220,3 +223,102 @@ def test_grouped_products_are_one_launch(target):
         want = (As[i].double() @ Bs[i].double().T).T
         assert relative(c.double().cpu().numpy(), want.cpu().numpy()) < 1e-5
     assert not Cs[1].any()
+
+
+def test_workspaces_lie_in_the_arena(target):
+    """A launch's workspace (attention's statistics and stored dS') is sized by
+    th_launch_workspace and placed in the executable's arena beside the slots;
+    the results are those of the launch that allocates its own at the first
+    run, and of one given a caller's buffer."""
+    import tempest_hip as th
+    import tempest_hip.launch as L
+    announce("workspace in arena")
+    B, H, S = 1, 2, 256
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    q, k, v, g = (torch.randn(B, S, H, 128, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
+    prog = th.programs.attention(B, H, S)
+    ex = th.prepare(prog, target, q, k, v, g)
+    rows = B * S * H
+    ws = [l.workspace() for l in ex.launches]
+    assert ws[0] == 0
+    stats = (rows * 3 * 4 + 255) // 256 * 256
+    assert ws[1] == stats + 2 * B * H * S * S
+    assert "1 workspaces" in ex.explain()
+    lo, hi = min(ex.arena.addresses), max(ex.arena.addresses)
+    assert ex.arena.bytes >= sum(ex.storage.sizes) + ws[1]
+    ex.execute()
+    torch.cuda.synchronize()
+    got = [t.clone() for t in ex.outputs()]
+    # The same backward with its own workspace (allocated at its first run),
+    # then with a workspace of the caller's.
+    o, lse = got[0], torch.empty(H * S * B, device="cuda")
+    fwd = L.attention_fwd(B, H, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr())
+    fwd()
+    outs = [torch.empty_like(q) for _ in range(3)]
+    bwd = L.attention_bwd(B, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                          g.data_ptr(), *(t.data_ptr() for t in outs))
+    bwd()
+    torch.cuda.synchronize()
+    for a, b in zip(outs, got[1:]):
+        assert torch.equal(a, b)
+    buf = torch.empty(bwd.workspace() + 256, dtype=torch.uint8, device="cuda")
+    addr = (buf.data_ptr() + 255) // 256 * 256
+    bwd.set_workspace(addr)
+    for t in outs:
+        t.zero_()
+    bwd()
+    torch.cuda.synchronize()
+    for a, b in zip(outs, got[1:]):
+        assert torch.equal(a, b)
+    from tempest_hip import HIPError
+    with pytest.raises(HIPError, match="256-byte"):
+        bwd.set_workspace(addr + 16)
+    with pytest.raises(HIPError, match="no workspace"):
+        fwd.set_workspace(addr)
+
+
+def test_workspaces_come_from_the_pool(target):
+    """With a pool, the workspaces are blocks of its reserved range too."""
+    import tempest_hip as th
+    announce("workspace in pool")
+    B, H, S = 1, 2, 256
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    q, k, v, g = (torch.randn(B, S, H, 128, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
+    pool = th.Pool(reserve=4 << 30)
+    base, reserved, _ = pool.info()
+    prog = th.programs.attention(B, H, S)
+    ex = th.prepare(prog, target, q, k, v, g, pool=pool)
+    ref = th.prepare(prog, target, q, k, v, g)
+    assert all(base <= a < base + reserved for a in ex.arena.addresses)
+    assert len(ex.arena.addresses) == len(ex.storage.sizes) + 1
+    for e in (ex, ref):
+        e.execute()
+    torch.cuda.synchronize()
+    for a, b in zip(ex.outputs(), ref.outputs()):
+        assert torch.equal(a, b)
+
+
+def test_deltanet_gradient_keeps_o_in_its_workspace(target):
+    """th_build_deltanet with o null keeps o in the workspace: the gradients
+    are those of the build given an o."""
+    import tempest_hip.launch as L
+    announce("deltanet o in workspace")
+    B, H, T = 1, 2, 128
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    q, k, v, dout = (torch.randn(B, T, H, 128, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
+    q = torch.nn.functional.normalize(q.float(), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(k.float(), dim=-1).to(torch.bfloat16)
+    a = -torch.nn.functional.softplus(torch.randn(B, T, H, device="cuda", generator=gen))
+    beta = torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=gen))
+    results = []
+    for give_o in (True, False):
+        o = torch.zeros_like(q)
+        grads = [torch.zeros_like(q) for _ in range(3)] + [torch.zeros_like(a), torch.zeros_like(beta)]
+        l = L.deltanet(B, H, T, q.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(), beta.data_ptr(),
+                       o.data_ptr() if give_o else 0, dout.data_ptr(), *(t.data_ptr() for t in grads))
+        assert l.workspace() > 0
+        l()
+        torch.cuda.synchronize()
+        results.append(grads)
+    for x, y in zip(*results):
+        assert torch.equal(x, y)
