@@ -374,16 +374,17 @@ def config3(target, steps: int = 5, warmup: int = 2):
             "dispatch": graph_vs_direct(target, ex, steps)}
 
 
-def config4(target, steps: int = 3, warmup: int = 1):
+def config4(target, steps: int = 3, warmup: int = 1, recompute_dq: bool = False):
     """Causal attention fwd+bwd, B8 H16 S4096 D128 bf16: 1.924e12 flops a step
-    (forward 4 B H S^2 D / 2, backward 2.5x that)."""
+    (forward 4 B H S^2 D / 2, backward 2.5x that).  recompute_dq: the
+    backward's dQ sweep recomputes S and dP rather than reading stored dS'."""
     import torch
     import tempest_hip as th
 
     B, H, S, D = 8, 16, 4096, 128
     gen = torch.Generator(device="cuda").manual_seed(4)
     q, k, v, g = (torch.randn(B, S, H, D, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
-    comp = th.compile(th.programs.attention(B, H, S), target, q, k, v, g)
+    comp = th.compile(th.programs.attention(B, H, S, recompute_dq=recompute_dq), target, q, k, v, g)
     ex = comp.executable
     fwd, bwd = ex.launches
     f_fwd, f_bwd = fwd.work().flops, bwd.work().flops
@@ -408,7 +409,9 @@ def config4(target, steps: int = 3, warmup: int = 1):
             "frac_of_bf16_peak": total / (t_f + t_b) / BF16_PEAK, "flops_per_step": total,
             "fwd": {"ms": t_f * 1e3, "TFLOP/s": f_fwd / t_f / 1e12},
             "bwd": {"ms": t_b * 1e3, "TFLOP/s": f_bwd / t_b / 1e12,
-                    "note": "FA2 convention, 2.5x forward flops; deterministic: the dK/dV sweep stores dS, a dQ sweep reads it"}}
+                    "note": "FA2 convention, 2.5x forward flops; deterministic: " +
+                            ("the dQ sweep recomputes S and dP" if recompute_dq else
+                             "the dK/dV sweep stores dS, a dQ sweep reads it")}}
 
 
 def config5(target, steps: int = 3, warmup: int = 1):
@@ -453,7 +456,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
-    ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config5"], default=None,
+    ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
+                                       "config5"], default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
@@ -484,7 +488,8 @@ def main() -> int:
         print(json.dumps({a.only: config2_floor(target, x, g, a.steps, a.warmup)}), flush=True)
         return 0
     if a.only:
-        fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5}[a.only]
+        fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5,
+              "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
     c2 = config2(target, a.steps, a.warmup)

@@ -111,12 +111,14 @@ def mlp(batch: int = 4096, d_in: int = 4096, hidden: int = 16384, d_out: int = 4
 
 
 def attention(batch: int = 8, heads: int = 16, seq: int = 4096, head_dim: int = 128, causal: bool = True,
-              kv_heads: int = 0) -> Program:
+              kv_heads: int = 0, recompute_dq: bool = False) -> Program:
     """Config 4: (q, k, v, dout) -> attention(q, k, v; causal) and the gradients
     of sum(attention(q, k, v) .* dout) w.r.t. q, k, v; bf16 (d, heads, positions,
     batch) arrays, fp32 statistics (test/fixtures/operations.jl:21-70).  With
     kv_heads < heads, k, v, dk and dv have kv_heads heads, query head h reading
-    kv head h / (heads / kv_heads) (test/cuda/attention.jl:132-140).
+    kv head h / (heads / kv_heads) (test/cuda/attention.jl:132-140).  With
+    recompute_dq the dQ sweep recomputes S and dP instead of reading the dS'
+    the dK/dV sweep stores.
 
     Plan: the forward's product, softmax and product fold into one online
     sweep over keys (the online-softmax rewrite, plan/rewrites.jl:29-41),
@@ -137,7 +139,8 @@ def attention(batch: int = 8, heads: int = 16, seq: int = 4096, head_dim: int = 
     bwd = Group("dq, dk, dv", ("q", "k", "v", "o", "lse", "dout", "dq", "dk", "dv"),
                 ("q", "k", "v", "o", "lse", "dout"), ("dq", "dk", "dv"),
                 lambda a: L.attention_bwd(batch, heads, seq, a["q"], a["k"], a["v"], a["o"], a["lse"], a["dout"],
-                                          a["dq"], a["dk"], a["dv"], causal=causal, kv_heads=kv_heads))
+                                          a["dq"], a["dk"], a["dv"], causal=causal, kv_heads=kv_heads,
+                                          recompute_dq=recompute_dq))
     return Program("attention", values, [fwd, bwd], ["q", "k", "v", "dout"], ["o", "dq", "dk", "dv"])
 
 
