@@ -103,3 +103,26 @@ def test_capacity_takes_a_suffix(store, monkeypatch):
     assert len(_entries(store)) == 1
     _group(7.0).compile()
     assert len(_entries(store)) == 1
+
+
+def test_concurrent_builds_share_the_store(store):
+    """Claims and builds run side by side on threads (runtime.jl:649-680): the
+    generator and the store are safe to call from several threads at once;
+    each distinct group is compiled once per key and every thread sees the
+    same source."""
+    from concurrent.futures import ThreadPoolExecutor
+    groups = [_group(10.0 + (i % 4)) for i in range(16)]
+    l0, c0 = _counts()
+
+    def work(g):
+        src = g.source()
+        g.compile()
+        return src
+
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        sources = list(ex.map(work, groups))
+    for i, src in enumerate(sources):
+        assert src == sources[i % 4]
+    assert len(_entries(store)) == 4
+    loaded, compiled = _counts()
+    assert compiled - c0 == 4 and loaded - l0 == 12

@@ -322,3 +322,49 @@ def test_deltanet_gradient_keeps_o_in_its_workspace(target):
         results.append(grads)
     for x, y in zip(*results):
         assert torch.equal(x, y)
+
+
+def test_builds_from_several_threads(target):
+    """Builds run as tasks side by side (runtime.jl:649-680): products, floor
+    groups and row programs built from eight threads at once give launches
+    whose results equal those built one at a time."""
+    from concurrent.futures import ThreadPoolExecutor
+    import tempest_hip.launch as L
+    from tempest_hip.floor import FloorGroup
+    announce("threaded builds")
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    m = 256
+    a = torch.randn(m, m, device="cuda", generator=gen).to(torch.bfloat16)
+    bm = torch.randn(m, m, device="cuda", generator=gen).to(torch.bfloat16)
+    x = torch.randn(64, 1000, device="cuda", generator=gen)
+    g = torch.randn_like(x)
+
+    def build(i):
+        kind = i % 3
+        if kind == 0:
+            c = torch.empty(m, m, device="cuda", dtype=torch.float32)
+            return (c,), L.gemm(m, m, m, a.data_ptr(), 1, m, bm.data_ptr(), 1, m, c.data_ptr(), m, c_dtype=L.F32)
+        if kind == 1:
+            fg = FloorGroup("reduction", (1000, 64), reduced=(0,))
+            fg.value("x", "f32", 64000)
+            fg.value("r", "f32", 64)
+            fg.output("r", fg.fold("sum", fg.apply("exp", fg.load("x", [1, 1000])) * (1.0 + i)).value, [0, 1],
+                      full=False)
+            r = torch.empty(64, device="cuda")
+            return (r,), fg.build({"x": x.data_ptr(), "r": r.data_ptr()})
+        # Every buffer a launch writes stays referenced while it runs: a
+        # dropped one goes back to torch's allocator and is handed out again.
+        dx, loss = torch.empty_like(x), torch.empty(1, device="cuda")
+        return (dx, loss), L.softmax_grad(64, 1000, 1000, x.data_ptr(), g.data_ptr(), dx.data_ptr(),
+                                          loss.data_ptr())
+
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        threaded = list(ex.map(build, range(24)))
+    serial = [build(i) for i in range(24)]
+    for (t1, l1), (t2, l2) in zip(threaded, serial):
+        l1()
+        l2()
+    torch.cuda.synchronize()
+    for (t1, _), (t2, _) in zip(threaded, serial):
+        for u, v in zip(t1, t2):
+            assert torch.equal(u, v)
