@@ -93,6 +93,23 @@ __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// c += a b with c held in AGPRs.  This file's products keep their
+// accumulators in VGPRs (the vector ALUs read scores straight from them); an
+// accumulator that only products touch until the end is better off in the
+// AGPRs, leaving the VGPRs to operands and addresses.  Two wait states first,
+// for a vector instruction that has just written a or b; the caller waits
+// before vector instructions read c (agpr_settle).
+__device__ __forceinline__ void mfma_agpr(bf16x8 a, bf16x8 b, f32x16& c) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// 24 wait states before vector instructions read the accumulators: more than
+// the ISA asks for after a 16-pass product writes its result.
+__device__ __forceinline__ void agpr_settle(f32x16 (&x)[4], f32x16 (&y)[4]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+               : "+a"(x[0]), "+a"(x[1]), "+a"(x[2]), "+a"(x[3]), "+a"(y[0]), "+a"(y[1]), "+a"(y[2]), "+a"(y[3]));
+}
+
 // The eight bf16 of registers [8 part, 8 part + 8) of a 32 x 32 accumulator
 // as the B operand of a 16-deep product over the accumulator's rows
 // 16 part .. 16 part + 15.  Lane l holds rows 8 (i / 4) + 4 (l / 32) + i % 4
@@ -521,7 +538,11 @@ constexpr size_t kDsScratch = kBwdStages * kStageBwd;  // 4 waves x 32 rows of k
 constexpr size_t kDkdvLds = kDsScratch + 4 * 32 * kDsRow * sizeof(uint16_t);
 
 // The gradient products of slices ks0, ks0 + 1 (rows 16 ks0 .. 16 ks0 + 31):
-// dv += dO' P, dk += Q' dS, fragments read half a slice ahead.
+// dv += dO' P, dk += Q' dS, fragments read half a slice ahead.  kAgpr: dv and
+// dk live in AGPRs (the stored-dS' sweep: 129 fewer register moves a step,
+// -3 % on config 4's backward; the recompute sweep, whose registers are
+// allocated differently, is left as it was).
+template <bool kAgpr>
 __device__ __forceinline__ void grads_half(const uint16_t* g, const uint16_t* q, int ks0, const bf16x8 (&pf)[4],
                                            const bf16x8 (&sf)[4], f32x16 (&dv)[4], f32x16 (&dk)[4]) {
   // Unit u = (slice ks0 + u / 2, d blocks 2 (u % 2), 2 (u % 2) + 1).
@@ -544,8 +565,13 @@ __device__ __forceinline__ void grads_half(const uint16_t* g, const uint16_t* q,
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int db = 2 * (u % 2) + e;
-      dv[db] = mfma(fg[u % 3][e], pf[ks], dv[db]);
-      dk[db] = mfma(fq[u % 3][e], sf[ks], dk[db]);
+      if constexpr (kAgpr) {
+        mfma_agpr(fg[u % 3][e], pf[ks], dv[db]);
+        mfma_agpr(fq[u % 3][e], sf[ks], dk[db]);
+      } else {
+        dv[db] = mfma(fg[u % 3][e], pf[ks], dv[db]);
+        dk[db] = mfma(fq[u % 3][e], sf[ks], dk[db]);
+      }
     }
     __builtin_amdgcn_sched_barrier(kFence);
   }
@@ -699,9 +725,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
             if (32 + 8 * (i / 4) + i % 4 < lim) s[1][i] = -INFINITY;
         }
         // dV' (128 d x 32 keys) += dO' P;  dK' += Q' dS.
-        grads_half(G, Q, 0, pf, sf, dv, dk);
+        grads_half<kStore>(G, Q, 0, pf, sf, dv, dk);
         weights_rows(s[1], dp[1], c, pf[2], pf[3], sf[2], sf[3]);
-        grads_half(G, Q, 2, pf, sf, dv, dk);
+        grads_half<kStore>(G, Q, 2, pf, sf, dv, dk);
         if constexpr (kStore) {
           // sf[ks] element e is query 16 ks + 8 (e / 4) + 4 lh + e % 4 of this lane's key.
   #pragma unroll
@@ -726,6 +752,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
         store_pending((nq - 1) * kBwdQ);
       }
     }  // query heads of the group
+    if constexpr (kStore) agpr_settle(dk, dv);
     // Lane holds dK'(d, key), dV'(d, key) for d = 32 db + 8 g + 4 lh + (0..3).
     const int64_t out = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)key * p.k_ss;
   #pragma unroll
