@@ -506,13 +506,24 @@ enum { TH_EPI_STORE = 0, TH_EPI_GELU = 1, TH_EPI_SQUARE_LOSS = 2, TH_EPI_GELU_BA
  * product z's operands start a_batch, b_batch, c_batch (d_batch) elements
  * further.  Factors are bf16 unless flags say fp32 or fp16; products
  * accumulate in fp32 and the result is rounded once.
- * Two implementations: bf16 factors with a unit stride on each operand, m, n,
- * k and the other strides multiples of 8 and operands 16-byte aligned run the
- * bf16 tile kernel (256 x 256 tiles, every epilogue, and K split over parts
- * summed by a second launch when the tiles alone would leave the device idle);
- * anything else with TH_EPI_STORE and no bias runs the general kernel (64 x 64
- * tiles on the fp32 matrix cores, any shape and strides, a result of the
- * factors' type or fp32).
+ * Three implementations, by `tile`:
+ *   TH_TILE_256: bf16 factors with a unit stride on each operand, m, n, k and
+ *     the other strides multiples of 8, operands 16-byte aligned: 256 x 256
+ *     tiles, every epilogue;
+ *   TH_TILE_128X128, _128X64, _64X128, _64X64 (rows x columns of C): bf16 or
+ *     fp16 factors with a unit stride on each operand, the other strides
+ *     multiples of 8, operands 16-byte aligned, any m, n, k, TH_EPI_STORE
+ *     (bias allowed), a result of the factors' type or fp32: the output tiles
+ *     the reference's product sketch searches for half factors
+ *     (ext/cuTileExt/contract.jl:36-39);
+ *   TH_TILE_GENERAL: anything with TH_EPI_STORE and no bias: 64 x 64 tiles on
+ *     the fp32 matrix cores, any shape and strides (fp32 factors run only here).
+ * TH_TILE_AUTO chooses: the 256 x 256 kernel where it takes the product and
+ * fills the device (split or not), else the largest middle tile that gives
+ * 256 workgroups (the smallest if none does), else the general kernel.
+ * `splits` parts of K (256 and middle tiles, TH_EPI_STORE) are summed by a
+ * second launch, with the bias and D; 0 chooses (parts when the tiles alone
+ * would leave the device idle), 1 none.  th_gemm_tune measures the choices.
  * Values: 0 a, 1 b, 2 c, 3 bias, 4 aux, 5 aux_out, 6 row_sums, 7 loss, 8 d.
  * Replaces the cuTile product sketch (ext/cuTileExt/contract.jl:32-206) and
  * cuBLASProducts (ext/cuBLASExt.jl:23-36,247-259): its product, widened and
@@ -521,7 +532,7 @@ typedef struct th_gemm_desc {
   int32_t m, n, k;
   int32_t c_dtype;   /* TH_BF16 or TH_F32 (TH_F32 only with TH_EPI_STORE) */
   int32_t epilogue;  /* TH_EPI_* */
-  int32_t reserved;
+  int32_t tile;      /* TH_TILE_*: which kernel and output tile */
   const void* a;
   int64_t a_m, a_k;
   const void* b;
@@ -539,7 +550,7 @@ typedef struct th_gemm_desc {
   int64_t a_batch, b_batch, c_batch;
   const void* d;     /* TH_GEMM_ACCUMULATE: C = D + A*B, D laid out as C, may be C itself */
   int64_t d_ld, d_batch;  /* 0, 0: C's */
-  int32_t splits;    /* parts K is split into on the tile kernel: 0 chosen, 1 none */
+  int32_t splits;    /* parts K is split into: 0 chosen, 1 none */
   int32_t reserved2;
 } th_gemm_desc;
 
@@ -547,7 +558,28 @@ typedef struct th_gemm_desc {
 #define TH_GEMM_F16_FACTORS 2  /* a and b hold fp16 */
 #define TH_GEMM_ACCUMULATE 4   /* C = D + A*B (cuBLASExt.jl:25, `accumulated`) */
 
+#define TH_TILE_AUTO 0
+#define TH_TILE_256 1
+#define TH_TILE_128X128 2
+#define TH_TILE_128X64 3
+#define TH_TILE_64X128 4
+#define TH_TILE_64X64 5
+#define TH_TILE_GENERAL 6
+
 int th_build_gemm(const th_gemm_desc* desc, th_launch** host_out);
+
+/* Measure the product's choices on the device and return the fastest: its
+ * tile (TH_TILE_*), its parts of K and its time (seconds, as
+ * th_time_launch measures).  The search runs in stages as the reference's
+ * cover searches a product's tiles (ext/cuTileExt/contract.jl:12-27,171-200,
+ * tinygrad's beam search at width one): every tile that takes the product at
+ * its chosen split, then the other splits (1, 2, 4, ... 16, each part at
+ * least 256 deep) of the best.  `desc`'s tile and splits are ignored; its
+ * arrays are the ones measured on, and the product's outputs (c, and what
+ * the epilogue writes) are overwritten; D + A B in place (d == c) is refused.
+ * Results are kept for the process, keyed by the product's shape, layouts,
+ * types and epilogue, so a second call measures nothing. */
+int th_gemm_tune(const th_gemm_desc* desc, int32_t* tile_out, int32_t* splits_out, double* seconds_out);
 
 /* Products alike but for where their operands start, as one launch: each of
  * descs[0..count) built as th_build_gemm builds it, run in order.  Value v of

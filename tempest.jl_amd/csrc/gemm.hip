@@ -1,8 +1,18 @@
-// th_build_gemm: the bf16 product's launch (gemm_kernel.h holds the kernel),
-// and the folds its epilogues leave: bias gradients and the loss.
+// th_build_gemm: a product's launch on the kernel its tile names (the
+// 256 x 256 kernel in gemm_kernel.h, the middle tiles in gemm_mid.hip, the
+// general kernel in gemm_general.hip), the parts of K summed, and the folds
+// the epilogues leave: bias gradients and the loss.  th_gemm_tune measures
+// the choices.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+
 #include "gemm_kernel.h"
+#include "gemm_mid.h"
 #include "th_core.h"
 
 namespace thg {
@@ -41,7 +51,8 @@ __global__ __launch_bounds__(256) void sum_loss(LossArgs a) {
 }
 
 // The parts of K summed (in part order), plus the bias and what the product
-// is added to, rounded once to the result's type: C_z = D_z + sum_s W_zs + bias.
+// is added to, rounded once to the result's type (fp32, bf16 or fp16):
+// C_z = D_z + sum_s W_zs + bias.
 struct ReduceArgs {
   const float* ws;       // [batch][splits][m x n], column-major at ld m
   void* c;               // result, column-major at c_ld, product z at c_batch
@@ -65,6 +76,9 @@ __global__ __launch_bounds__(256) void sum_splits(ReduceArgs a) {
   if (a.c_dtype == TH_F32) {
     if (a.d) v += static_cast<const float*>(a.d)[at_d];
     static_cast<float*>(a.c)[at] = v;
+  } else if (a.c_dtype == TH_F16) {
+    if (a.d) v += (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(a.d)[at_d]);
+    static_cast<uint16_t*>(a.c)[at] = __builtin_bit_cast(uint16_t, (_Float16)v);
   } else {
     if (a.d) v += bf16_float(static_cast<const uint16_t*>(a.d)[at_d]);
     static_cast<uint16_t*>(a.c)[at] = bf16_bits(v);
@@ -92,13 +106,66 @@ bool tile_kernel_takes(const th_gemm_desc* d) {
   return aligned(d->a, 16) && aligned(d->b, 16) && aligned(d->c, 16);
 }
 
+// Whether the middle tiles take the descriptor: half factors, a unit stride
+// on each operand, the other strides multiples of 8, 16-byte operands, a
+// plain product with a result of the factors' type or fp32.
+static bool mid_takes(const th_gemm_desc* d) {
+  if (d->flags & TH_GEMM_F32_FACTORS) return false;
+  if (d->epilogue != TH_EPI_STORE) return false;
+  const int factor = (d->flags & TH_GEMM_F16_FACTORS) ? TH_F16 : TH_BF16;
+  if (d->c_dtype != factor && d->c_dtype != TH_F32) return false;
+  if (!(d->a_k == 1 || d->a_m == 1) || !(d->b_k == 1 || d->b_n == 1)) return false;
+  const int64_t sa = d->a_k == 1 ? d->a_m : d->a_k, sb = d->b_k == 1 ? d->b_n : d->b_k;
+  if (sa % 8 || sb % 8 || d->c_ld < d->m) return false;
+  if (d->batch > 1 && (d->a_batch % 8 || d->b_batch % 8)) return false;
+  return aligned(d->a, 16) && aligned(d->b, 16);
+}
+
+static int mid_rows(int tile) { return tile == TH_TILE_64X128 || tile == TH_TILE_64X64 ? 64 : 128; }
+static int mid_cols(int tile) { return tile == TH_TILE_128X64 || tile == TH_TILE_64X64 ? 64 : 128; }
+
+static int64_t tiles_of(const th_gemm_desc* d, int bm, int bn) {
+  return (int64_t)((d->m + bm - 1) / bm) * ((d->n + bn - 1) / bn) * std::max(1, d->batch);
+}
+
+// The parts of K a tile takes when the caller leaves them to the builder:
+// enough for about 256 workgroups where the tiles alone give fewer than 128,
+// each part at least `least` deep (1024 on the 256 x 256 kernel, 512 on the
+// middle tiles).
+static int auto_splits(const th_gemm_desc* d, int tile) {
+  if (d->epilogue != TH_EPI_STORE || tile == TH_TILE_GENERAL) return 1;
+  const bool big = tile == TH_TILE_256;
+  const int64_t tiles = big ? tiles_of(d, kTile, kTile) : tiles_of(d, mid_rows(tile), mid_cols(tile));
+  const int least = big ? 1024 : 512;
+  if (tiles >= 128 || d->k < 2 * least) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / least));
+}
+
+// TH_TILE_AUTO: the 256 x 256 kernel where it takes the product and fills
+// the device (split or not) or nothing else takes it, else the largest middle
+// tile that gives 256 workgroups (the smallest if none does), else the
+// general kernel.
+static int choose_tile(const th_gemm_desc* d) {
+  const bool mid = mid_takes(d);
+  if (tile_kernel_takes(d) &&
+      (!mid || tiles_of(d, kTile, kTile) * auto_splits(d, TH_TILE_256) >= 128))
+    return TH_TILE_256;
+  if (mid) {
+    for (int t : {TH_TILE_128X128, TH_TILE_128X64, TH_TILE_64X128})
+      if (tiles_of(d, mid_rows(t), mid_cols(t)) >= 256) return t;
+    return TH_TILE_64X64;
+  }
+  return TH_TILE_GENERAL;
+}
+
+static int build_tile256(const th_gemm_desc* d, th_launch** out);
+static int build_mid(const th_gemm_desc* d, int tile, th_launch** out);
+
 extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   if (int r = th::require_ready()) return r;
   *out = nullptr;
   TH_REQUIRE(d != nullptr, "th_build_gemm: null descriptor");
-  const int M = d->m, N = d->n, K = d->k;
-  const int batch = d->batch > 0 ? d->batch : 1;
-  TH_REQUIRE(M >= 1 && N >= 1 && K >= 1, "th_build_gemm: m, n, k must be positive");
+  TH_REQUIRE(d->m >= 1 && d->n >= 1 && d->k >= 1, "th_build_gemm: m, n, k must be positive");
   TH_REQUIRE(d->a && d->b && d->c, "th_build_gemm: null operand");
   TH_REQUIRE((d->flags & ~(TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS | TH_GEMM_ACCUMULATE)) == 0 &&
                  (d->flags & (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS)) != (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS),
@@ -107,9 +174,32 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   TH_REQUIRE(!accumulate || d->d, "th_build_gemm: accumulating needs d");
   const int epi = d->epilogue;
   TH_REQUIRE(epi >= TH_EPI_STORE && epi <= TH_EPI_GELU_BACKWARD, "th_build_gemm: unknown epilogue");
-  TH_REQUIRE(epi == TH_EPI_STORE || (batch == 1 && !accumulate),
+  TH_REQUIRE(epi == TH_EPI_STORE || ((d->batch <= 1) && !accumulate),
              "th_build_gemm: fused epilogues take one product and nothing to add");
-  if (!tile_kernel_takes(d)) return th::build_gemm_general(d, out);
+  TH_REQUIRE(d->tile >= TH_TILE_AUTO && d->tile <= TH_TILE_GENERAL, "th_build_gemm: unknown tile");
+  TH_REQUIRE(d->splits >= 0, "th_build_gemm: splits must be >= 0");
+  const int tile = d->tile == TH_TILE_AUTO ? choose_tile(d) : d->tile;
+  if (tile == TH_TILE_GENERAL) {
+    TH_REQUIRE(d->splits <= 1, "th_build_gemm: the general kernel does not split K");
+    return th::build_gemm_general(d, out);
+  }
+  if (tile == TH_TILE_256) {
+    TH_REQUIRE(tile_kernel_takes(d),
+               "th_build_gemm: the 256 x 256 kernel takes bf16 factors with a unit stride on each operand, m, n, k "
+               "and the other strides multiples of 8 and 16-byte aligned operands");
+    return build_tile256(d, out);
+  }
+  TH_REQUIRE(mid_takes(d),
+             "th_build_gemm: the middle tiles take bf16 or fp16 factors with a unit stride on each operand, the other "
+             "strides multiples of 8, 16-byte aligned operands, TH_EPI_STORE and a result of the factors' type or fp32");
+  return build_mid(d, tile, out);
+}
+
+static int build_tile256(const th_gemm_desc* d, th_launch** out) {
+  const int M = d->m, N = d->n, K = d->k;
+  const int batch = d->batch > 0 ? d->batch : 1;
+  const bool accumulate = (d->flags & TH_GEMM_ACCUMULATE) != 0;
+  const int epi = d->epilogue;
   const int la = d->a_k == 1 ? kK : kMN;
   const int lb = d->b_k == 1 ? kK : kMN;
   TH_REQUIRE(d->c_dtype == TH_BF16 || (d->c_dtype == TH_F32 && epi == TH_EPI_STORE),
@@ -125,13 +215,9 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
                "th_build_gemm: the GELU backward needs aux (8-byte aligned, ld >= m, ld % 4 == 0) and row_sums");
 
   const int tiles_m = (M + kTile - 1) / kTile, tiles_n = (N + kTile - 1) / kTile;
-  // K split over parts where the tiles alone would leave most CUs idle: up to
-  // 256 workgroups, each part at least 1024 deep and a multiple of 64.
-  int splits = d->splits > 0 ? d->splits : 1;
-  if (d->splits == 0 && epi == TH_EPI_STORE) {
-    const int tiles = tiles_m * tiles_n * batch;
-    if (tiles < 128 && K >= 2048) splits = std::max(1, std::min((256 + tiles - 1) / tiles, K / 1024));
-  }
+  // K split over parts (each a multiple of 64 deep) where asked, or where the
+  // tiles alone would leave most CUs idle.
+  int splits = d->splits > 0 ? d->splits : auto_splits(d, TH_TILE_256);
   TH_REQUIRE(splits == 1 || epi == TH_EPI_STORE, "th_build_gemm: only a plain product splits K");
   int ksplit = K;
   if (splits > 1) {
@@ -239,6 +325,170 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   if (epi == TH_EPI_GELU || epi == TH_EPI_GELU_BACKWARD) bytes += 2.0 * mm * nn;
   b.work(bytes, 2.0 * bb * mm * nn * kk, (int64_t)blocks * splits * batch);
   *out = b.release();
+  return TH_OK;
+}
+
+// The middle tiles: one launch of the tile kernel, and for parts of K a
+// second that sums them (with the bias and D) into the result.
+static int build_mid(const th_gemm_desc* d, int tile, th_launch** out) {
+  const int M = d->m, N = d->n, K = d->k;
+  const int batch = d->batch > 0 ? d->batch : 1;
+  const bool accumulate = (d->flags & TH_GEMM_ACCUMULATE) != 0;
+  const bool f16 = (d->flags & TH_GEMM_F16_FACTORS) != 0;
+  int bm = 0, bn = 0, lds = 0;
+  const void* fn = mid_kernel(tile, f16, d->a_k == 1, d->b_k == 1, &bm, &bn, &lds);
+  TH_REQUIRE(fn != nullptr, "th_build_gemm: unknown tile");
+  const int64_t tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
+  TH_REQUIRE(tiles_m * tiles_n <= 0x7fffffff, "th_build_gemm: grid too large");
+  int splits = d->splits > 0 ? d->splits : auto_splits(d, tile);
+  int ksplit = K;
+  if (splits > 1) {
+    ksplit = ((K + splits - 1) / splits + 31) / 32 * 32;
+    splits = (K + ksplit - 1) / ksplit;
+  }
+  TH_REQUIRE(splits <= 65535 && batch <= 65535, "th_build_gemm: grid too large");
+  const bool staged = splits > 1;
+  const int64_t mn = (int64_t)M * N;
+  th::Builder b("gemm_mid", 9);
+  MidArgs g{};
+  g.a = static_cast<const uint16_t*>(d->a);
+  g.b = static_cast<const uint16_t*>(d->b);
+  g.a_m = d->a_m, g.a_k = d->a_k, g.a_batch = d->a_batch;
+  g.b_k = d->b_k, g.b_n = d->b_n, g.b_batch = d->b_batch;
+  g.m = M, g.n = N, g.k = K, g.ksplit = ksplit, g.tiles_m = (int32_t)tiles_m;
+  uint64_t at_parts = 0;
+  if (staged) {
+    // Each part's fp32 sums, [batch][part][m x n] column-major at ld m.
+    at_parts = b.workspace((uint64_t)batch * splits * mn * sizeof(float));
+    g.c = nullptr, g.c_ld = M, g.c_batch = (int64_t)splits * mn, g.c_split = mn, g.result = TH_F32;
+  } else {
+    g.c = d->c, g.c_ld = d->c_ld, g.c_batch = d->c_batch, g.c_split = 0, g.result = d->c_dtype;
+    g.d = accumulate ? d->d : nullptr;
+    g.d_ld = d->d_ld ? d->d_ld : d->c_ld;
+    g.d_batch = d->d_ld ? d->d_batch : d->c_batch;
+    g.bias = static_cast<const uint16_t*>(d->bias);
+  }
+  const char* name = staged ? "gemm_mid_parts_f32" : "gemm_mid";
+  int k = b.kernel(fn, name, dim3((unsigned)(tiles_m * tiles_n), splits, batch), dim3(256), (uint32_t)lds, g);
+  b.ref(0, k, TH_OFFSET(MidArgs, a));
+  b.ref(1, k, TH_OFFSET(MidArgs, b));
+  if (staged) {
+    b.ws_ref(k, TH_OFFSET(MidArgs, c), at_parts);
+  } else {
+    b.ref(2, k, TH_OFFSET(MidArgs, c));
+    b.ref(3, k, TH_OFFSET(MidArgs, bias));
+    b.ref(8, k, TH_OFFSET(MidArgs, d));
+  }
+  b.align(0, 16);
+  b.align(1, 16);
+  if (staged) {
+    ReduceArgs ra{nullptr, d->c, static_cast<const uint16_t*>(d->bias),
+                  accumulate ? d->d : nullptr, d->c_ld, d->c_batch, d->d_ld ? d->d_ld : d->c_ld,
+                  d->d_ld ? d->d_batch : d->c_batch, M, N, splits, d->c_dtype};
+    int kr = b.kernel((const void*)sum_splits, "sum_splits", dim3((unsigned)((mn + 255) / 256), batch), dim3(256), 0,
+                      ra);
+    b.ref(2, kr, TH_OFFSET(ReduceArgs, c));
+    b.ref(3, kr, TH_OFFSET(ReduceArgs, bias));
+    b.ref(8, kr, TH_OFFSET(ReduceArgs, d));
+    b.ws_ref(kr, TH_OFFSET(ReduceArgs, ws), at_parts);
+  }
+  const double mm = M, nn = N, kk = K, bb = batch;
+  const double cbytes = d->c_dtype == TH_F32 ? 4 : 2;
+  b.work(bb * (2.0 * (mm * kk + kk * nn) + cbytes * mm * nn * (accumulate ? 2 : 1)), 2.0 * bb * mm * nn * kk,
+         tiles_m * tiles_n * splits * batch);
+  *out = b.release();
+  return TH_OK;
+}
+
+// ---- measuring the choices -------------------------------------------------------
+
+namespace {
+
+struct Tuned {
+  int32_t tile, splits;
+  double seconds;
+};
+
+std::mutex g_tune_mutex;
+std::map<std::string, Tuned> g_tuned;
+
+std::string tune_key(const th_gemm_desc* d) {
+  char buf[512];
+  snprintf(buf, sizeof buf, "%d %d %d %d|%lld %lld %lld %lld %lld|%lld %lld %lld %lld %lld|%d %d %d %d %d|%d %d %d",
+           d->m, d->n, d->k, std::max(1, d->batch), (long long)d->a_m, (long long)d->a_k, (long long)d->b_k,
+           (long long)d->b_n, (long long)d->c_ld, (long long)d->a_batch, (long long)d->b_batch, (long long)d->c_batch,
+           (long long)d->d_ld, (long long)d->d_batch, d->flags, d->c_dtype, d->epilogue, d->bias != nullptr,
+           d->d != nullptr, (int)(reinterpret_cast<uintptr_t>(d->a) % 16 == 0),
+           (int)(reinterpret_cast<uintptr_t>(d->b) % 16 == 0), (int)(reinterpret_cast<uintptr_t>(d->c) % 16 == 0));
+  return buf;
+}
+
+// The splits a build with `splits` asked (0: the builder's choice) ends up
+// with, as the builders round them.
+int splits_used(const th_gemm_desc* d, int tile, int splits) {
+  if (tile == TH_TILE_GENERAL) return 1;
+  int s = splits > 0 ? splits : auto_splits(d, tile);
+  if (s <= 1) return 1;
+  const int step = tile == TH_TILE_256 ? kDepth : 32;
+  const int ks = ((d->k + s - 1) / s + step - 1) / step * step;
+  return (d->k + ks - 1) / ks;
+}
+
+int measure(const th_gemm_desc* base, int tile, int splits, double* seconds) {
+  th_gemm_desc d = *base;
+  d.tile = tile;
+  d.splits = splits;
+  th_launch* l = nullptr;
+  if (int r = th_build_gemm(&d, &l)) return r;
+  const int r = th_time_launch(l, 0, seconds);
+  th_launch_destroy(l);
+  return r;
+}
+
+}  // namespace
+
+extern "C" int th_gemm_tune(const th_gemm_desc* desc, int32_t* tile_out, int32_t* splits_out, double* seconds_out) {
+  if (int r = th::require_ready()) return r;
+  TH_REQUIRE(desc != nullptr && tile_out && splits_out && seconds_out, "th_gemm_tune: null argument");
+  TH_REQUIRE(!((desc->flags & TH_GEMM_ACCUMULATE) && desc->d == desc->c),
+             "th_gemm_tune: D + A B in place would add the product again at every measurement");
+  const std::string key = tune_key(desc);
+  std::lock_guard<std::mutex> lock(g_tune_mutex);
+  auto hit = g_tuned.find(key);
+  if (hit == g_tuned.end()) {
+    th_gemm_desc d = *desc;
+    d.tile = TH_TILE_AUTO;
+    d.splits = 0;
+    std::vector<int> tiles;
+    if (tile_kernel_takes(&d)) tiles.push_back(TH_TILE_256);
+    if (mid_takes(&d))
+      for (int t : {TH_TILE_128X128, TH_TILE_128X64, TH_TILE_64X128, TH_TILE_64X64}) tiles.push_back(t);
+    if (d.epilogue == TH_EPI_STORE && !d.bias) tiles.push_back(TH_TILE_GENERAL);
+    TH_REQUIRE(!tiles.empty(), "th_gemm_tune: no kernel takes the product");
+    // Stage one: every tile at the split the builder would choose.
+    Tuned best{0, 0, 0.0};
+    for (int t : tiles) {
+      double s = 0;
+      if (int r = measure(&d, t, 0, &s)) return r;
+      if (best.tile == 0 || s < best.seconds) best = Tuned{t, splits_used(&d, t, 0), s};
+    }
+    // Stage two: the other splits of the best (plain products on the tile
+    // kernels), each part at least 256 deep.
+    if (best.tile != TH_TILE_GENERAL && d.epilogue == TH_EPI_STORE) {
+      for (int sp : {1, 2, 4, 8, 16}) {
+        if (sp > 1 && d.k / sp < 256) break;
+        const int used = splits_used(&d, best.tile, sp);
+        if (used == best.splits) continue;
+        double s = 0;
+        if (int r = measure(&d, best.tile, sp, &s)) return r;
+        if (s < best.seconds) best = Tuned{best.tile, used, s};
+      }
+    }
+    hit = g_tuned.emplace(key, best).first;
+  }
+  *tile_out = hit->second.tile;
+  *splits_out = hit->second.splits;
+  *seconds_out = hit->second.seconds;
   return TH_OK;
 }
 

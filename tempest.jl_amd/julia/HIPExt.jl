@@ -274,7 +274,7 @@ const WIDENED, ACCUMULATED = 2, 3
 templates(::HIPProducts, ::HIPTarget) = PRODUCTS
 
 struct GemmDesc
-    m::Int32; n::Int32; k::Int32; c_dtype::Int32; epilogue::Int32; reserved::Int32
+    m::Int32; n::Int32; k::Int32; c_dtype::Int32; epilogue::Int32; tile::Int32
     a::Ptr{Cvoid}; a_m::Int64; a_k::Int64
     b::Ptr{Cvoid}; b_k::Int64; b_n::Int64
     c::Ptr{Cvoid}; c_ld::Int64
@@ -294,9 +294,10 @@ factor_flags(T) = T === Float32 ? GEMM_F32_FACTORS : T === Float16 ? GEMM_F16_FA
 # A binding as th_gemm_desc, or nothing: Float32, Float16 or BFloat16
 # factors of one type, a result of theirs or Float32, the result column-major
 # (unit stride along m), and for `accumulated` a matrix added laid out as the
-# result.  Any other strides the library takes (the tile kernel where it can,
-# the general kernel else).  With `buffers = false` the addresses are null
-# (`supports` is asked without storage).
+# result.  Any other strides the library takes (the library chooses the
+# kernel and its tile: the 256 x 256 or a middle tile where it can, the general
+# kernel else).  With `buffers = false` the addresses are null (`supports` is
+# asked without storage).
 function gemm_desc(b::Binding; buffers = true)
     A, B, Cr = b.arrays.A, b.arrays.B, b.arrays.C
     T, R = A.eltype, Cr.eltype
@@ -324,8 +325,28 @@ estimate(::HIPProducts, b::Binding, target, g) =
 product_operands(b::Binding) =
     operands_of(((0, b.arrays.A), (1, b.arrays.B), (2, b.arrays.C), (8, get(b.arrays, :D, nothing))))
 
+# The descriptor with th_gemm_tune's choice of tile and splits.
+function with_choice(d::GemmDesc, tile::Int32, splits::Int32)
+    names = fieldnames(GemmDesc)
+    vals = Any[getfield(d, f) for f in names]
+    vals[findfirst(==(:tile), names)] = tile
+    vals[findfirst(==(:splits), names)] = splits
+    GemmDesc(vals...)
+end
+
+# TEMPEST_HIP_TUNE=1: the product's tile and splits measured on the device as
+# it is built (th_gemm_tune: every tile that takes it, then the splits of the
+# best, as the reference's cover searches its product tiles,
+# ext/cuTileExt/contract.jl:12-27); otherwise the library's choice.  A product
+# added to a matrix in place is not measured (each run would add it again).
 function build(::HIPProducts, t::HIPTarget, b::Binding, resources)
     d = Ref(gemm_desc(b))
+    if get(ENV, "TEMPEST_HIP_TUNE", "") == "1" && b.template != ACCUMULATED
+        tile, splits, secs = Ref{Int32}(0), Ref{Int32}(0), Ref{Float64}(0)
+        check(ccall((:th_gemm_tune, LIB), Cint, (Ptr{GemmDesc}, Ptr{Int32}, Ptr{Int32}, Ptr{Float64}),
+            d, tile, splits, secs), "th_gemm_tune")
+        d[] = with_choice(d[], tile[], splits[])
+    end
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_build_gemm, LIB), Cint, (Ptr{GemmDesc}, Ptr{Ptr{Cvoid}}), d, out), "th_build_gemm")
     l = HIPLaunch(out[], Any[s.buffer for s in values(b.arrays)], product_operands(b), t.pool)

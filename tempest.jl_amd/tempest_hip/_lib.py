@@ -43,7 +43,7 @@ class Work(ctypes.Structure):
 class GemmDesc(ctypes.Structure):
     """th_gemm_desc (include/tempest_hip.h)."""
     _fields_ = [("m", c_i32), ("n", c_i32), ("k", c_i32), ("c_dtype", c_i32), ("epilogue", c_i32),
-                ("reserved", c_i32), ("a", c_void_p), ("a_m", c_i64), ("a_k", c_i64), ("b", c_void_p),
+                ("tile", c_i32), ("a", c_void_p), ("a_m", c_i64), ("a_k", c_i64), ("b", c_void_p),
                 ("b_k", c_i64), ("b_n", c_i64), ("c", c_void_p), ("c_ld", c_i64), ("bias", c_void_p),
                 ("aux", c_void_p), ("aux_ld", c_i64), ("aux_out", c_void_p), ("row_sums", c_void_p),
                 ("loss", c_void_p), ("batch", c_i32), ("flags", c_i32), ("a_batch", c_i64), ("b_batch", c_i64),
@@ -163,6 +163,7 @@ SIGNATURES: dict[str, list] = {
     "th_build_sum": [c_i64, c_void_p, c_void_p, P(c_void_p)],
     "th_build_gemm": [P(GemmDesc), P(c_void_p)],
     "th_build_gemm_grouped": [P(GemmDesc), c_int, P(c_void_p)],
+    "th_gemm_tune": [P(GemmDesc), P(c_i32), P(c_i32), P(c_double)],
     "th_build_attention_fwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_attention_bwd": [P(AttentionDesc), P(c_void_p)],
     "th_build_deltanet_fwd": [P(DeltaNetDesc), P(c_void_p)],

@@ -30,7 +30,7 @@ def _operand(mat, contiguous_inner: bool):
 LAYOUTS = [("k", "k"), ("k", "mn"), ("mn", "k"), ("mn", "mn")]
 
 
-def _run_gemm(m, n, k, la, lb, c_f32=True, bias=None, ldc=None, seed=0):
+def _run_gemm(m, n, k, la, lb, c_f32=True, bias=None, ldc=None, seed=0, tile=1):
     import tempest_hip.launch as L
     rng = np.random.default_rng(seed)
     A = bf16_round(rng.normal(size=(m, k)).astype(np.float32))
@@ -45,7 +45,9 @@ def _run_gemm(m, n, k, la, lb, c_f32=True, bias=None, ldc=None, seed=0):
     if bias is not None:
         tbias = _bf16(bias)
     l = L.gemm(m, n, k, ta.data_ptr(), a_m, a_k, tb.data_ptr(), b_k, b_n, c.data_ptr(), ldc,
-               c_dtype=L.F32 if c_f32 else L.BF16, bias=tbias.data_ptr() if tbias is not None else 0)
+               c_dtype=L.F32 if c_f32 else L.BF16, bias=tbias.data_ptr() if tbias is not None else 0, tile=tile)
+    if tile == L.TILE_256:
+        assert "gemm_bf16" in l.describe()
     l()
     torch.cuda.synchronize()
     out = c.float().cpu().numpy()[:, :m].T
@@ -57,9 +59,10 @@ def _run_gemm(m, n, k, la, lb, c_f32=True, bias=None, ldc=None, seed=0):
 
 @pytest.mark.parametrize("la,lb", LAYOUTS)
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 768, 320), (72, 136, 40), (8, 8, 8), (1024, 256, 2048)])
-def test_product_fp32_result_is_exact_to_accumulation(target, m, n, k, la, lb):
-    announce("gemm f32", m, n, k, la, lb)
-    out, ref, _ = _run_gemm(m, n, k, la, lb, c_f32=True)
+@pytest.mark.parametrize("tile", [1, 0])  # the 256 x 256 kernel; the library's choice
+def test_product_fp32_result_is_exact_to_accumulation(target, m, n, k, la, lb, tile):
+    announce("gemm f32", m, n, k, la, lb, tile)
+    out, ref, _ = _run_gemm(m, n, k, la, lb, c_f32=True, tile=tile)
     assert relative(out, ref) < 1e-5
 
 
@@ -74,17 +77,25 @@ def test_product_bf16_result_with_bias_and_ldc(target, la, lb):
 
 
 def test_shapes_route_to_the_kernel_that_takes_them(target):
-    """Plain products the tile kernel cannot take (m not a multiple of 8, no
-    unit stride) run on the general kernel; a fused epilogue there is refused."""
+    """The library's choice: a product too small to fill the device with
+    256 x 256 tiles runs on a middle tile, also at m not a multiple of 8; one
+    with no unit stride on the general kernel; a fused epilogue there is
+    refused; a tile named that does not take the product is refused."""
     import tempest_hip.launch as L
     from tempest_hip import HIPError
     t = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
     p = t.data_ptr()
-    assert "gemm_bf16_store" in L.gemm(64, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
-    assert "gemm_general" in L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
+    assert "gemm_mid" in L.gemm(64, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
+    assert "gemm_bf16_store" in L.gemm(64, 64, 64, p, 64, 1, p, 1, 64, p, 64, tile=L.TILE_256).describe()
+    assert "gemm_mid" in L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64).describe()
+    assert "gemm_general" in L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64, tile=L.TILE_GENERAL).describe()
     assert "gemm_general" in L.gemm(64, 64, 32, p, 64, 2, p, 1, 64, p, 64).describe()
     with pytest.raises(HIPError, match="fused epilogues"):
         L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64, epilogue=L.GELU, bias=p, aux_out=p)
+    with pytest.raises(HIPError, match="256 x 256 kernel takes"):
+        L.gemm(60, 64, 64, p, 64, 1, p, 1, 64, p, 64, tile=L.TILE_256)
+    with pytest.raises(HIPError, match="middle tiles take"):
+        L.gemm(64, 64, 32, p, 64, 2, p, 1, 64, p, 64, tile=L.TILE_64X64)
 
 
 def _mlp_inputs(batch, d_in, hidden, d_out, seed):

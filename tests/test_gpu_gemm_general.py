@@ -169,7 +169,7 @@ def test_tile_kernel_batch(target):
     B = _bf16((3, 384, 256), gen)   # B_z(l, j) at z*384*256 + l*256 + j: n-contiguous
     C = torch.zeros(3, 256, 512, dtype=torch.bfloat16, device="cuda")  # column-major m x n
     l = L.gemm(512, 256, 384, A.data_ptr(), 384, 1, B.data_ptr(), 256, 1, C.data_ptr(), 512, batch=3,
-               a_batch=512 * 384, b_batch=384 * 256, c_batch=512 * 256, splits=1)
+               a_batch=512 * 384, b_batch=384 * 256, c_batch=512 * 256, splits=1, tile=L.TILE_256)
     assert "gemm_bf16_store" in l.describe() and "gemm_general" not in l.describe()
     l()
     torch.cuda.synchronize()
@@ -212,14 +212,14 @@ def test_tile_kernel_accumulates(target):
     C = torch.zeros(512, 512, device="cuda")
     prod = (A.double() @ B.double().T).T
     l = L.gemm(512, 512, 1024, A.data_ptr(), 1024, 1, B.data_ptr(), 1, 1024, C.data_ptr(), 512, c_dtype=L.F32,
-               d=D.data_ptr(), splits=2)
+               d=D.data_ptr(), splits=2, tile=L.TILE_256)
     l()
     torch.cuda.synchronize()
     assert relative(C.double().cpu().numpy(), (prod + D.double()).cpu().numpy()) < 1e-5
     Cb = D.to(torch.bfloat16)
     start = Cb.double().clone()
     l2 = L.gemm(512, 512, 1024, A.data_ptr(), 1024, 1, B.data_ptr(), 1, 1024, Cb.data_ptr(), 512, c_dtype=L.BF16,
-                d=Cb.data_ptr(), splits=1)
+                d=Cb.data_ptr(), splits=1, tile=L.TILE_256)
     l2()
     torch.cuda.synchronize()
     assert relative(Cb.double().cpu().numpy(), (prod + start).cpu().numpy()) < 1e-2
