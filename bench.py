@@ -414,6 +414,42 @@ def config4(target, steps: int = 3, warmup: int = 1, recompute_dq: bool = False)
                              "the dK/dV sweep stores dS, a dQ sweep reads it")}}
 
 
+def gemm_tiles(target, runs: int = 20):
+    """The product's tile choices (not a config of its own): for each shape,
+    every kernel that takes it at the split the library would choose, timed as
+    claims are (th_time_launch), then run `runs` times back to back so a
+    kernel trace or counter run sees each variant by its kernel's name; and
+    what th_gemm_tune chose.  bf16 factors, A k-contiguous, B n-contiguous,
+    an fp32 result."""
+    import torch
+    import tempest_hip.launch as L
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    out = {}
+    for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 1024), (256, 256, 8192), (4096, 4096, 4096)):
+        a = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)  # A(i, l) at i k + l
+        b = torch.randn(k, n, device="cuda", generator=gen).to(torch.bfloat16)  # B(l, j) at l n + j
+        c = torch.empty(n, m, device="cuda")
+        args = (m, n, k, a.data_ptr(), k, 1, b.data_ptr(), n, 1, c.data_ptr(), m)
+        flops = 2.0 * m * n * k
+        row = {}
+        for tile in (L.TILE_256, L.TILE_128X128, L.TILE_128X64, L.TILE_64X128, L.TILE_64X64, L.TILE_GENERAL):
+            try:
+                launch = L.gemm(*args, c_dtype=L.F32, tile=tile)
+            except Exception:  # the kernel does not take the shape
+                continue
+            t = target.time_launch(launch)
+            for _ in range(runs):
+                launch()
+            torch.cuda.synchronize()
+            row[L.TILE_NAMES[tile]] = {"us": t * 1e6, "TFLOP/s": flops / t / 1e12,
+                                       "workgroups": launch.work().blocks, "kernels": launch.describe()}
+        tile, splits, t = L.gemm_tune(*args, c_dtype=L.F32)
+        row["chosen"] = {"tile": L.TILE_NAMES[tile], "splits": splits, "us": t * 1e6, "TFLOP/s": flops / t / 1e12}
+        out[f"{m}x{n}x{k}"] = row
+        log(f"gemm tiles {m}x{n}x{k}:", json.dumps(row["chosen"]))
+    return out
+
+
 def config5(target, steps: int = 3, warmup: int = 1):
     """Chunked gated DeltaNet forward + gradient, B4 H16 T8192, d 128, chunk 64."""
     import torch
@@ -457,7 +493,7 @@ def main() -> int:
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
-                                       "config5"], default=None,
+                                       "config5", "gemm_tiles"], default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
@@ -488,7 +524,7 @@ def main() -> int:
         print(json.dumps({a.only: config2_floor(target, x, g, a.steps, a.warmup)}), flush=True)
         return 0
     if a.only:
-        fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5,
+        fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
