@@ -10,6 +10,7 @@ include/tempest_hip.h, one per op class and sketch.
 from __future__ import annotations
 
 import ctypes
+import os
 
 from . import _lib
 from ._lib import call
@@ -138,9 +139,16 @@ def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b
     each of `batch` products; A(i, l) at a[i*a_m + l*a_k], B(l, j) at
     b[l*b_k + j*b_n], product z's operands *_batch elements further; factors
     BF16, F32 or F16; tile: TILE_* (the kernel and its output tile, TILE_AUTO
-    chosen); splits: parts of K (0 chosen, 1 none)."""
+    chosen); splits: parts of K (0 chosen, 1 none).  With TEMPEST_HIP_TUNE=1
+    in the environment a product left to the library (TILE_AUTO, splits 0)
+    takes th_gemm_tune's measured choice instead, as the Julia binding's build
+    does (not D + A B in place, which each measurement would add again)."""
     desc = _gemm_desc(m, n, k, a, a_m, a_k, b, b_k, b_n, c, c_ld, c_dtype, epilogue, bias, aux, aux_ld, aux_out,
                       row_sums, loss, batch, a_batch, b_batch, c_batch, factors, d, d_ld, d_batch, splits, tile)
+    if tile == TILE_AUTO and splits == 0 and os.environ.get("TEMPEST_HIP_TUNE") == "1" and not (d and d == c):
+        t, sp, sec = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_double()
+        call("th_gemm_tune", ctypes.byref(desc), ctypes.byref(t), ctypes.byref(sp), ctypes.byref(sec))
+        desc.tile, desc.splits = t.value, sp.value
     return _built("th_build_gemm", ("a", "b", "c", "bias", "aux", "aux_out", "row_sums", "loss", "d"),
                   ctypes.byref(desc))
 

@@ -200,3 +200,22 @@ def test_every_tile_agrees_on_one_product(target):
                512, c_dtype=L.F32, tile=tile)()
         torch.cuda.synchronize()
         assert relative(c.double().cpu().numpy().T, want) < TOL_F32, L.TILE_NAMES[tile]
+
+
+def test_environment_asks_for_measured_choices(target, monkeypatch):
+    """TEMPEST_HIP_TUNE=1: a product left to the library takes the tuner's
+    tile and split, and still computes the product."""
+    import tempest_hip.launch as L
+    announce("gemm tune env")
+    A, B, ta, tb, st = _case(768, 640, 1536, False, True, True, 31)
+    c = torch.zeros(640, 768, dtype=torch.float32, device="cuda")
+    args = (768, 640, 1536, ta.data_ptr(), st["a_m"], st["a_k"], tb.data_ptr(), st["b_k"], st["b_n"], c.data_ptr(),
+            768)
+    tile, splits, _ = L.gemm_tune(*args, c_dtype=L.F32, factors=L.F16)
+    monkeypatch.setenv("TEMPEST_HIP_TUNE", "1")
+    l = L.gemm(*args, c_dtype=L.F32, factors=L.F16)
+    kernel = {L.TILE_256: "gemm_bf16", L.TILE_GENERAL: "gemm_general"}.get(tile, "gemm_mid")
+    assert kernel in l.describe() and (splits > 1) == ("sum_splits" in l.describe())
+    l()
+    torch.cuda.synchronize()
+    assert relative(c.double().cpu().numpy().T, interpret.product(A[0], B[0])) < TOL_F32
