@@ -848,27 +848,10 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
 // order, so the result does not depend on timing.
 
 // dW, dU~ and T are read straight from memory by the products that use them,
-// and dQK = dP o Gamma (lower) is formed as its operands are read, so LDS
-// holds Q, K, M and N only and two workgroups share a CU.
+// so LDS holds Q, K, M and N only and two workgroups share a CU; dQK = dP o
+// Gamma (lower) takes N once N's own last use is past.
 constexpr size_t kGbLds = 2 * kC * kLdH * sizeof(uint16_t) + 2 * kC * kLdC * sizeof(float) +
                           (2 * kC + 5 * 4 * kC + 2 * kC) * sizeof(float);
-
-// dQK(i, j) = dP(i, j) e^(ca_i - ca_j) for i >= j, 0 above: along its rows
-// (quad(i, j) = dQK(i, j .. j + 3)) or, when kT, along its columns.
-template <bool kT>
-struct DqkReader {
-  const float* dP;  // [64][64] in memory
-  const float* ca;  // [64] in LDS
-  __device__ f32x4v quad(int x, int k) const {
-    f32x4v v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = kT ? k + e : x, j = kT ? x : k + e;
-      v[e] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
-    }
-    return v;
-  }
-};
 
 __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   extern __shared__ float lds[];
@@ -1009,13 +992,20 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
     M[i * kLdC + j] = N[i * kLdC + j] + N[j * kLdC + i];
   }
   __syncthreads();
+  // dQK = dP o Gamma (lower), read by two of the products below along its rows
+  // and its columns: formed once into N (free now), not at every read.
+  for (int e = t; e < kC * kC; e += 256) {
+    const int i = e / kC, j = e % kC;
+    N[i * kLdC + j] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
+  }
+  __syncthreads();
   // dQ = e^ca dQg + dQK K;  dV = beta T' dU~;  dK = dQK' Q + (dG + dG') K +
   // beta e^ca dX + e^(last - ca) dKd with dX = T' dW.  Wave w: columns
   // 32 w .. 32 w + 31, one output at a time (two accumulator sets live).
   {
     const int d0 = 32 * w;
-    const DqkReader<false> Rr{dP, ca};
-    const DqkReader<true> Rc{dP, ca};
+    const RowF32 Rr{N, kLdC};  // dQK along its rows
+    const ColF32 Rc{N, kLdC};  // and along its columns
     {
       f32x4v dq[4][2];
       clear(dq);
