@@ -858,7 +858,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   uint16_t* Qh = reinterpret_cast<uint16_t*>(lds);       // [64][kLdH]
   uint16_t* Kh = Qh + kC * kLdH;                          // [64][kLdH]
   float* M = reinterpret_cast<float*>(Kh + kC * kLdH);   // [64][kLdC]: dT, then dA, then dG + dG'
-  float* N = M + kC * kLdC;        // [64][kLdC]: T' dT, then dG
+  float* N = M + kC * kLdC;        // [64][kLdC]: T' dT, then dG, then dQK
   float* wrow = N + kC * kLdC;     // [64]: sum_j w_ij
   float* brow = wrow + kC;         // [64]: sum_j dA Gamma G
   float* wcol = brow + kC;         // [4][64]: sum_i w_ij by wave
