@@ -12,8 +12,8 @@
 //   P = lower (Gamma_ij q_i.k_j),  Qg = diag(e^ca) Q,  Kd = diag(e^(ca_63 - ca)) K,  g = e^ca_63;
 // across chunks:  U = U~ - W S,  O = Qg S + P U,  S <- g S + Kd' U.
 //
-// Kernels (fp32 arithmetic, every product on the matrix cores as
-// v_mfma_f32_16x16x4_f32; inputs bf16 q, k, v and fp32 a, beta):
+// Kernels (fp32 arithmetic, every product on the bf16 matrix cores with each
+// fp32 operand split into two bf16 halves; inputs bf16 q, k, v and fp32 a, beta):
 //   dn_chunk_prep   one workgroup per chunk: ca, A, T (forward substitution,
 //                   one lane per column), W, U~.
 //   dn_state_scan   one workgroup per (sequence, 32 columns of S): the
@@ -104,18 +104,21 @@ __device__ __forceinline__ void cumulative_gates(float* ca, const DnArgs& p, con
   }
 }
 
-// ---- fp32 products on the matrix cores ----------------------------------------------
-// v_mfma_f32_16x16x4_f32 multiplies fp32 exactly and accumulates in fp32, as
-// the per-thread FMA tiles do (only the order of the additions differs).
+// ---- fp32 products on the bf16 matrix cores -----------------------------------------
+// Each fp32 operand x is split as hi = bf16(x), lo = bf16(x - hi); a b is
+// summed in fp32 as hi hi + hi lo + lo hi on v_mfma_f32_16x16x32_bf16 (the
+// lo lo term and lo's rounding leave about 2^-16 of each product; operands
+// that are bf16 values, Q K V, have no lo).  Three bf16 products cost less
+// than half of the one fp32 product v_mfma_f32_16x16x4_f32 would.
 // Operands sit in LDS as fp32 rows of kLd floats: a row's 16-byte quads land
 // on distinct bank quads for 16 consecutive rows (kLd / 4 odd), and a column
 // read by 16 consecutive rows x 4 row groups hits 64 distinct banks
 // (kLd = 4 mod 16).
 //
-// Lane l = 16 g + r of a 16 x 16 block over 16 consecutive k takes the four
-// k = 16 kb + 4 g + (0..3): one ds_read_b128 per operand when k runs along
-// its rows, four products, each pairing A(i0 + r, k) with B(k, j0 + r); the
-// products' k slot g then holds the same k in both operands.  The block
+// Lane l = 16 g + r of a 16 x 16 block over 32 consecutive k takes the eight
+// k = kb + 8 g + (0..7): two quads per operand when k runs along its rows,
+// split to bf16, each pairing A(i0 + r, k) with B(k, j0 + r); the products'
+// k slot g then holds the same k in both operands.  The block
 // C(i0 + 4 g + v, j0 + r) sits in register v of lane l.
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -132,10 +135,43 @@ __device__ __forceinline__ f32x4v column_quad(const float* x, int ld, int k0, in
   return f32x4v{x[k0 * ld + c], x[(k0 + 1) * ld + c], x[(k0 + 2) * ld + c], x[(k0 + 3) * ld + c]};
 }
 
-__device__ __forceinline__ f32x4v mma4(f32x4v a, f32x4v b, f32x4v c) {
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+// Two fp32 as a pair of bf16 (nearest even), a in the low half.
+__device__ __forceinline__ uint32_t pk2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2v));
+}
+
+// A product operand's eight k (two quads of one row) as bf16 halves: hi the
+// nearest bf16, lo the nearest bf16 to the remainder x - hi (exact in fp32),
+// so hi + lo holds x to about 2^-16 of it.  kExact: x is a bf16 value, lo is 0.
+struct Split8 {
+  bf16x8v hi, lo;
+};
+template <bool kExact>
+__device__ __forceinline__ Split8 split8(f32x4v q0, f32x4v q1) {
+  const float x[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+  u32x4v h, l = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
-  return c;
+  for (int e = 0; e < 4; ++e) h[e] = pk2(x[2 * e], x[2 * e + 1]);
+  if constexpr (!kExact) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      l[e] = pk2(x[2 * e] - __uint_as_float(h[e] << 16), x[2 * e + 1] - __uint_as_float(h[e] & 0xffff0000u));
+  }
+  return Split8{__builtin_bit_cast(bf16x8v, h), __builtin_bit_cast(bf16x8v, l)};
+}
+
+// c += a b over 32 k on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16,
+// fp32 sums): hi hi + hi lo + lo hi, the lo lo term (about 2^-16 of the
+// product) dropped, and the terms of an operand exact in bf16 skipped.
+template <bool kExactA, bool kExactB>
+__device__ __forceinline__ f32x4v mma_split(const Split8& a, const Split8& b, f32x4v c) {
+  if constexpr (!kExactB) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, c, 0, 0, 0);
+  if constexpr (!kExactA) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, c, 0, 0, 0);
 }
 
 // acc[bi][bj] += X(i0 + 16 bi .., k) Y(j0 + 16 bj .., k) over k in [0, K):
@@ -143,16 +179,22 @@ __device__ __forceinline__ f32x4v mma4(f32x4v a, f32x4v b, f32x4v c) {
 template <int BI, int BJ>
 __device__ __forceinline__ void mm_nt(f32x4v (&acc)[BI][BJ], const float* X, int i0, const float* Y, int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
-  for (int kb = 0; kb < K; kb += 16) {
-    f32x4v a[BI], b[BJ];
+  for (int kb = 0; kb < K; kb += 32) {
+    Split8 a[BI], b[BJ];
 #pragma unroll
-    for (int bi = 0; bi < BI; ++bi) a[bi] = quad(X + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
+    for (int bi = 0; bi < BI; ++bi) {
+      const float* row = X + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
+      a[bi] = split8<false>(quad(row), quad(row + 4));
+    }
 #pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) b[bj] = quad(Y + (j0 + 16 * bj + r) * kLd + kb + 4 * g);
+    for (int bj = 0; bj < BJ; ++bj) {
+      const float* row = Y + (j0 + 16 * bj + r) * kLd + kb + 8 * g;
+      b[bj] = split8<false>(quad(row), quad(row + 4));
+    }
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi)
 #pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma_split<false, false>(a[bi], b[bj], acc[bi][bj]);
   }
 }
 
@@ -164,19 +206,19 @@ template <bool XT, bool YT, int BI, int BJ>
 __device__ __forceinline__ void mm_gen(f32x4v (&acc)[BI][BJ], const float* X, int ldx, int i0, const float* Y, int ldy,
                                        int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
-  for (int kb = 0; kb < K; kb += 16) {
-    const int k0 = kb + 4 * g;
-    f32x4v a[BI], b[BJ];
+  auto xq = [&](int k0, int i) { return XT ? column_quad(X, ldx, k0, i) : quad(X + i * ldx + k0); };
+  auto yq = [&](int k0, int j) { return YT ? column_quad(Y, ldy, k0, j) : quad(Y + j * ldy + k0); };
+  for (int kb = 0; kb < K; kb += 32) {
+    const int k0 = kb + 8 * g;
+    Split8 a[BI], b[BJ];
+#pragma unroll
+    for (int bi = 0; bi < BI; ++bi) a[bi] = split8<false>(xq(k0, i0 + 16 * bi + r), xq(k0 + 4, i0 + 16 * bi + r));
+#pragma unroll
+    for (int bj = 0; bj < BJ; ++bj) b[bj] = split8<false>(yq(k0, j0 + 16 * bj + r), yq(k0 + 4, j0 + 16 * bj + r));
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi)
-      a[bi] = XT ? column_quad(X, ldx, k0, i0 + 16 * bi + r) : quad(X + (i0 + 16 * bi + r) * ldx + k0);
 #pragma unroll
-    for (int bj = 0; bj < BJ; ++bj)
-      b[bj] = YT ? column_quad(Y, ldy, k0, j0 + 16 * bj + r) : quad(Y + (j0 + 16 * bj + r) * ldy + k0);
-#pragma unroll
-    for (int bi = 0; bi < BI; ++bi)
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma_split<false, false>(a[bi], b[bj], acc[bi][bj]);
   }
 }
 
@@ -224,16 +266,19 @@ __device__ __forceinline__ void store_blocks(float* out, int ld, const f32x4v (&
 
 // Operand readers for mm_by: quad(x, k) is this lane's (x, k .. k + 3).
 struct RowF32 {  // (x, k) at p[x * ld + k]
+  static constexpr bool kExact = false;
   const float* p;
   int ld;
   __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
 };
 struct ColF32 {  // (x, k) at p[k * ld + x]
+  static constexpr bool kExact = false;
   const float* p;
   int ld;
   __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
 };
 struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
+  static constexpr bool kExact = true;
   const uint16_t* p;
   int64_t ld;
   __device__ f32x4v quad(int x, int k) const {
@@ -242,6 +287,7 @@ struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
   }
 };
 struct ColBf16 {  // (x, k) at bf16 p[k * ld + x]
+  static constexpr bool kExact = true;
   const uint16_t* p;
   int ld;
   __device__ f32x4v quad(int x, int k) const {
@@ -253,16 +299,19 @@ struct ColBf16 {  // (x, k) at bf16 p[k * ld + x]
 template <int BI, int BJ, class XR, class YR>
 __device__ __forceinline__ void mm_by(f32x4v (&acc)[BI][BJ], const XR& X, int i0, const YR& Y, int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
-  for (int kb = 0; kb < K; kb += 16) {
-    f32x4v a[BI], b[BJ];
+  for (int kb = 0; kb < K; kb += 32) {
+    const int k0 = kb + 8 * g;
+    Split8 b[BJ];
 #pragma unroll
-    for (int bi = 0; bi < BI; ++bi) a[bi] = X.quad(i0 + 16 * bi + r, kb + 4 * g);
+    for (int bj = 0; bj < BJ; ++bj)
+      b[bj] = split8<YR::kExact>(Y.quad(j0 + 16 * bj + r, k0), Y.quad(j0 + 16 * bj + r, k0 + 4));
+    // The rows of X one block at a time: only one of its split blocks live.
 #pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) b[bj] = Y.quad(j0 + 16 * bj + r, kb + 4 * g);
+    for (int bi = 0; bi < BI; ++bi) {
+      const Split8 a = split8<XR::kExact>(X.quad(i0 + 16 * bi + r, k0), X.quad(i0 + 16 * bi + r, k0 + 4));
 #pragma unroll
-    for (int bi = 0; bi < BI; ++bi)
-#pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma4(a[bi], b[bj], acc[bi][bj]);
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma_split<XR::kExact, YR::kExact>(a, b[bj], acc[bi][bj]);
+    }
   }
 }
 
@@ -278,7 +327,7 @@ constexpr int kLdH = kD + 8;  // bf16 LDS row of Q, K
 // ---- forward: the chunk's WY form -------------------------------------------------
 // ca, A = strict lower (beta_i Gamma_ij k_i.k_j), T = (I + A)^-1 (forward
 // substitution, one lane per column), W = T diag(beta e^ca) K and
-// U~ = T diag(beta) V; the products on the matrix cores in fp32, K and V in
+// U~ = T diag(beta) V; the products on the matrix cores (split bf16), K and V in
 // LDS as bf16.
 
 __device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* src, int64_t s_t) {
@@ -367,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
 
 // ---- forward: the recurrence across chunks, 32 columns of S per workgroup ---------
 // Per chunk: the starting state is stored, U = U~ - W S, S <- g S + Kd' U,
-// the products on the matrix cores in fp32.  While a chunk's products run,
+// the products on the matrix cores (split bf16).  While a chunk's products run,
 // the next chunk's W, U~ columns, K and ca are loaded into registers.
 
 struct ScanInputs {  // one chunk's inputs as this thread loads them
@@ -510,7 +559,7 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
 
 // ---- forward: outputs ----------------------------------------------------------------
 // P = lower(Gamma o Q K'), O = diag(e^ca) Q S + P U; the products on the
-// matrix cores in fp32, Q and K in LDS as bf16.
+// matrix cores (split bf16), Q and K in LDS as bf16.
 
 // S and U are read by columns straight from memory (each wave's 32 columns
 // once), so only Q, K and P live in LDS and several workgroups share a CU.
@@ -571,7 +620,7 @@ __global__ __launch_bounds__(256, 2) void dn_output(DnArgs p) {
 // ---- backward: the state gradient swept back over chunks -------------------------------
 // One workgroup per (sequence, 32 columns of dS), chunks in reverse:
 //   dSn_n = dS;  dU = P' dO + diag(e^(last - ca)) K dS;  dS <- Qg' dO + g dS - W' dU,
-// the products on the matrix cores in fp32.  While a chunk's products run,
+// the products on the matrix cores (split bf16).  While a chunk's products run,
 // the previous chunk's inputs (P, the dO columns, Q, K, W, ca) are loaded
 // into registers; they go to LDS once the chunk is done with its own.
 
@@ -743,7 +792,7 @@ __global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
 
 // ---- backward: the chunk's products (part a) ---------------------------------------
 // dQg = dO S', dW = -dU S', dKd = U dSn', dP = lower(dO U'), dg = <S, dSn>,
-// every product on the matrix cores in fp32.  Two phases through LDS: dO, dU
+// every product on the matrix cores (split bf16).  Two phases through LDS: dO, dU
 // and S, then U and dSn (dO stays).  Wave w computes columns 32 w .. 32 w + 31
 // of the 64 x 128 results and row block w of dP.
 
@@ -758,21 +807,26 @@ template <int BI, int BJ>
 __device__ __forceinline__ void mm_nt2(f32x4v (&acc1)[BI][BJ], const float* X1, f32x4v (&acc2)[BI][BJ], const float* X2,
                                        int i0, const float* Y, int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
-  for (int kb = 0; kb < K; kb += 16) {
-    f32x4v a1[BI], a2[BI], b[BJ];
+  for (int kb = 0; kb < K; kb += 32) {
+    Split8 a1[BI], a2[BI], b[BJ];
 #pragma unroll
-    for (int bj = 0; bj < BJ; ++bj) b[bj] = quad(Y + (j0 + 16 * bj + r) * kD + kb + 4 * g);
+    for (int bj = 0; bj < BJ; ++bj) {
+      const float* row = Y + (j0 + 16 * bj + r) * kD + kb + 8 * g;
+      b[bj] = split8<false>(quad(row), quad(row + 4));
+    }
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi) {
-      a1[bi] = quad(X1 + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
-      a2[bi] = quad(X2 + (i0 + 16 * bi + r) * kLd + kb + 4 * g);
+      const float* r1 = X1 + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
+      const float* r2 = X2 + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
+      a1[bi] = split8<false>(quad(r1), quad(r1 + 4));
+      a2[bi] = split8<false>(quad(r2), quad(r2 + 4));
     }
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi)
 #pragma unroll
       for (int bj = 0; bj < BJ; ++bj) {
-        acc1[bi][bj] = mma4(a1[bi], b[bj], acc1[bi][bj]);
-        acc2[bi][bj] = mma4(a2[bi], b[bj], acc2[bi][bj]);
+        acc1[bi][bj] = mma_split<false, false>(a1[bi], b[bj], acc1[bi][bj]);
+        acc2[bi][bj] = mma_split<false, false>(a2[bi], b[bj], acc2[bi][bj]);
       }
   }
 }
@@ -839,7 +893,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
 }
 
 // ---- backward: the chunk's WY form, decays and gates (part b) -----------------------
-// Every product on the matrix cores in fp32 (mm_by below); Q and K sit in LDS
+// Every product on the matrix cores, split bf16 (mm_by below); Q and K sit in LDS
 // as bf16 (their exact values) and are widened as they are read, V is read
 // from global where it is needed, and dW, dU~ take turns in one fp32 buffer.
 // The row sums of the gate gradients are complete within a wave (each wave
@@ -1067,12 +1121,11 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
       }
     }
     {
-      f32x4v dk[4][2], dx[4][2];
-      clear(dk);
-      clear(dx);
-      mm_by(dk, Rc, 0, Qc, d0, kC);
-      mm_by(dk, RowF32{M, kLdC}, 0, Kc, d0, kC);
-      mm_by(dx, ColF32{Tc, kC}, 0, ColF32{dW, kD}, d0, kC);
+      // dX first; its terms of dK (beta e^ca dX + e^(last - ca) dKd) then
+      // seed dK's accumulator, so one accumulator set is live at a time.
+      f32x4v acc[4][2];
+      clear(acc);
+      mm_by(acc, ColF32{Tc, kC}, 0, ColF32{dW, kD}, d0, kC);
 #pragma unroll
       for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
@@ -1084,15 +1137,26 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
           for (int bj = 0; bj < 2; ++bj) {
             const int d = d0 + 16 * bj + r;
             const float gk = dKd[i * kD + d], kv = bf(Kh[i * kLdH + d]);
-            const float xv = dx[bi][bj][v];
+            const float xv = acc[bi][bj][v];
             sx = fmaf(kv, xv, sx);
             sk = fmaf(kv, gk, sk);
-            p.dk[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(dk[bi][bj][v] + be[i] * e * xv + ed * gk);
+            acc[bi][bj][v] = be[i] * e * xv + ed * gk;
           }
           sx = row_group_sum(sx);
           sk = row_group_sum(sk);
           if (r == 0) kx[w * kC + i] = sx, kk[w * kC + i] = sk;
         }
+      mm_by(acc, Rc, 0, Qc, d0, kC);
+      mm_by(acc, RowF32{M, kLdC}, 0, Kc, d0, kC);
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj) {
+            const int i = 16 * bi + 4 * g + v, d = d0 + 16 * bj + r;
+            p.dk[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(acc[bi][bj][v]);
+          }
     }
   }
   __syncthreads();
