@@ -16,11 +16,11 @@
 // fp32 operand split into two bf16 halves; inputs bf16 q, k, v and fp32 a, beta):
 //   dn_chunk_prep   one workgroup per chunk: ca, A, T (forward substitution,
 //                   one lane per column), W, U~.
-//   dn_state_scan   one workgroup per (sequence, 32 columns of S): the
-//                   sequential recurrence, each column block independent;
+//   dn_state_scan   one eight-wave workgroup per (sequence, 32 columns of S):
+//                   the sequential recurrence, each column block independent;
 //                   stores each chunk's starting state and U.
 //   dn_output       one workgroup per chunk: P, O.
-//   dn_state_grad   one workgroup per (sequence, 32 columns): the state
+//   dn_state_grad   one eight-wave workgroup per (sequence, 32 columns): the state
 //                   gradient swept back over chunks; stores dU and dS_{n+1}.
 //   dn_grad_a/b     one workgroup per chunk: the chunk's products' gradients,
 //                   the inverse's (dA = -T' dT T'), the decays', a's.
@@ -419,10 +419,14 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
 // the products on the matrix cores (split bf16).  While a chunk's products run,
 // the next chunk's W, U~ columns, K and ca are loaded into registers.
 
+// Eight waves, two on each SIMD: one workgroup per CU (its LDS), and a
+// chunk's serial chain (stage, product, product, update) split eight ways.
+constexpr int kScanThreads = 512;
+
 struct ScanInputs {  // one chunk's inputs as this thread loads them
-  f32x4v w[8];       // W: 8 x 16 bytes
-  f32x4v u[2];       // U~ columns col0 .. col0 + 31: 2 x 16 bytes
-  u32x4v k[4];       // K: 4 x 16 bytes (bf16)
+  f32x4v w[4];       // W: 4 x 16 bytes
+  f32x4v u;          // U~ columns col0 .. col0 + 31: 16 bytes
+  u32x4v k[2];       // K: 2 x 16 bytes (bf16)
   float ca;
 };
 
@@ -431,15 +435,14 @@ __device__ __forceinline__ void scan_load(ScanInputs& in, const DnArgs& p, const
   const float* Wc = p.W + ck.c * kC * kD;
   const float* Uc = p.Ut + ck.c * kC * kD;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + 256 * e];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
-    in.u[e] = *reinterpret_cast<const f32x4v*>(Uc + r * kD + col0 + c);
+  for (int e = 0; e < 4; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + kScanThreads * e];
+  {
+    const int r = t / 8, c = 4 * (t % 8);
+    in.u = *reinterpret_cast<const f32x4v*>(Uc + r * kD + col0 + c);
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + kScanThreads * e, r = x / 16, c = 8 * (x % 16);
     in.k[e] = *reinterpret_cast<const u32x4v*>(p.k + ck.row0 + (int64_t)r * p.s_t + c);
   }
   in.ca = t < kC ? p.ca[ck.c * kC + t] : 0.0f;
@@ -449,19 +452,15 @@ __device__ __forceinline__ void scan_load(ScanInputs& in, const DnArgs& p, const
 __device__ __forceinline__ void scan_store(const ScanInputs& in, float* W, float* Ut, float* Kd, const float* ca) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int x = t + 256 * e, r = x / 32, c = 4 * (x % 32);
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + kScanThreads * e, r = x / 32, c = 4 * (x % 32);
     *reinterpret_cast<f32x4v*>(W + r * kLd + c) = in.w[e];
   }
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
-    *reinterpret_cast<f32x4v*>(Ut + r * kLdS + c) = in.u[e];
-  }
+  *reinterpret_cast<f32x4v*>(Ut + (t / 8) * kLdS + 4 * (t % 8)) = in.u;
   const float last = ca[kC - 1];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + kScanThreads * e, r = x / 16, c = 8 * (x % 16);
     const float ed = expf(last - ca[r]);
     const u32x4v uk = in.k[e];
 #pragma unroll
@@ -474,7 +473,7 @@ __device__ __forceinline__ void scan_store(const ScanInputs& in, float* W, float
 
 constexpr size_t kScanLds = (2 * kC * kLd + kC * kLdS + kD * kLdS + kC * kLdS + kC) * sizeof(float);
 
-__global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
+__global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
   extern __shared__ float lds[];
   float* W = lds;                 // [64][kLd]
   float* Kd = W + kC * kLd;       // [64][kLd]: diag(e^(ca_63 - ca)) K
@@ -486,7 +485,7 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
   const int r = t % 16, g = (t % 64) / 16;
   const int64_t seq = blockIdx.x / (kD / kCols);
   const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
-  for (int e = t; e < kD * kLdS; e += 256) S[e] = 0.0f;
+  for (int e = t; e < kD * kLdS; e += kScanThreads) S[e] = 0.0f;
   ScanInputs in;
   scan_load(in, p, chunk_of(p, seq * p.chunks), col0);
   if (t < kC) ca[t] = in.ca;
@@ -499,55 +498,48 @@ __global__ __launch_bounds__(256, 1) void dn_state_scan(DnArgs p) {
     const float gl = expf(ca[kC - 1]);
     // The chunk's starting state, stored for the output and the backward.
     float* Sc = p.S + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols / 4; e += 256) {
+    for (int e = t; e < kD * kCols / 4; e += kScanThreads) {
       const int row = e / 8, c = 4 * (e % 8);
       *reinterpret_cast<f32x4v*>(Sc + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(S + row * kLdS + c);
     }
-    // U = U~ - W S (64 x 32): wave w takes rows 16 w .. 16 w + 15.
+    // U = U~ - W S (64 x 32): wave w takes the 16 x 16 block at rows
+    // 16 (w mod 4), columns 16 (w / 4).
     {
-      f32x4v ws[1][2];
+      f32x4v ws[1][1];
       clear(ws);
-      mm_gen<false, true>(ws, W, kLd, 16 * w, S, kLdS, 0, kD);
+      const int i0 = 16 * (w % 4), j0 = 16 * (w / 4);
+      mm_gen<false, true>(ws, W, kLd, i0, S, kLdS, j0, kD);
 #pragma unroll
-      for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
-          U[i * kLdS + j] = Ut[i * kLdS + j] - ws[0][bj][v];
-        }
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 4 * g + v, j = j0 + r;
+        U[i * kLdS + j] = Ut[i * kLdS + j] - ws[0][0][v];
+      }
     }
     __syncthreads();
     // U to memory from LDS in 16-byte pieces, beside the products below.
     {
       float* Uo = p.U + ck.c * kC * kD;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int x = t + 256 * e, row = x / 8, c = 4 * (x % 8);
-        *reinterpret_cast<f32x4v*>(Uo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(U + row * kLdS + c);
-      }
+      const int row = t / 8, c = 4 * (t % 8);
+      *reinterpret_cast<f32x4v*>(Uo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(U + row * kLdS + c);
     }
-    // S <- g S + Kd' U (128 x 32): wave w takes rows 32 w .. 32 w + 31.
+    // S <- g S + Kd' U (128 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
-      f32x4v ku[2][2];
+      f32x4v ku[1][2];
       clear(ku);
-      mm_gen<true, true>(ku, Kd, kLd, 32 * w, U, kLdS, 0, kC);
-      float nw[2][2][4];
+      mm_gen<true, true>(ku, Kd, kLd, 16 * w, U, kLdS, 0, kC);
+      float nw[2][4];
 #pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
+      for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int i = 32 * w + 16 * bi + 4 * g + v, j = 16 * bj + r;
-            nw[bi][bj][v] = gl * S[i * kLdS + j] + ku[bi][bj][v];
-          }
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
+          nw[bj][v] = gl * S[i * kLdS + j] + ku[0][bj][v];
+        }
       __syncthreads();  // every wave has read S, U and this chunk's inputs
 #pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
+      for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) S[(32 * w + 16 * bi + 4 * g + v) * kLdS + 16 * bj + r] = nw[bi][bj][v];
+        for (int v = 0; v < 4; ++v) S[(16 * w + 4 * g + v) * kLdS + 16 * bj + r] = nw[bj][v];
     }
     if (n + 1 < p.chunks) {
       if (t < kC) ca[t] = in.ca;
@@ -630,10 +622,10 @@ constexpr size_t kSgLds =
 // One chunk's inputs as this thread loads them (plain vector types, so the
 // whole set stays in registers).
 struct SgInputs {
-  f32x4v p[4];     // P: 4 x 16 bytes
-  u32x2v d[2];     // dO columns col0 .. col0 + 31: 2 x 8 bytes (bf16)
-  u32x4v q[4], k[4];  // Q, K: 4 x 16 bytes each (bf16)
-  f32x4v w[8];
+  f32x4v p[2];     // P: 2 x 16 bytes
+  u32x2v d;        // dO columns col0 .. col0 + 31: 8 bytes (bf16)
+  u32x4v q[2], k[2];  // Q, K: 2 x 16 bytes each (bf16)
+  f32x4v w[4];
   float ca;
 };
 
@@ -642,20 +634,16 @@ __device__ __forceinline__ void sg_load(SgInputs& in, const DnArgs& p, const Chu
   const float* Pc = p.P + ck.c * kC * kC;
   const float* Wc = p.W + ck.c * kC * kD;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) in.p[e] = reinterpret_cast<const f32x4v*>(Pc)[t + 256 * e];
+  for (int e = 0; e < 2; ++e) in.p[e] = reinterpret_cast<const f32x4v*>(Pc)[t + kScanThreads * e];
+  in.d = *reinterpret_cast<const u32x2v*>(p.dout + ck.row0 + (int64_t)(t / 8) * p.s_t + col0 + 4 * (t % 8));
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
-    in.d[e] = *reinterpret_cast<const u32x2v*>(p.dout + ck.row0 + (int64_t)r * p.s_t + col0 + c);
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    const int x = t + kScanThreads * e, r = x / 16, c = 8 * (x % 16);
     in.q[e] = *reinterpret_cast<const u32x4v*>(p.q + ck.row0 + (int64_t)r * p.s_t + c);
     in.k[e] = *reinterpret_cast<const u32x4v*>(p.k + ck.row0 + (int64_t)r * p.s_t + c);
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + 256 * e];
+  for (int e = 0; e < 4; ++e) in.w[e] = reinterpret_cast<const f32x4v*>(Wc)[t + kScanThreads * e];
   in.ca = t < kC ? p.ca[ck.c * kC + t] : 0.0f;
 }
 
@@ -664,20 +652,15 @@ __device__ __forceinline__ void sg_store(const SgInputs& in, float* P, float* dO
                                          const float* ca) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int x = t + 256 * e, r = x / 16, c = 4 * (x % 16);
+  for (int e = 0; e < 2; ++e) {
+    const int x = t + kScanThreads * e, r = x / 16, c = 4 * (x % 16);
     *reinterpret_cast<f32x4v*>(P + r * kLdC + c) = in.p[e];
   }
+  *reinterpret_cast<f32x4v*>(dO + (t / 8) * kLdS + 4 * (t % 8)) =
+      f32x4v{bf((uint16_t)in.d[0]), bf((uint16_t)(in.d[0] >> 16)), bf((uint16_t)in.d[1]), bf((uint16_t)(in.d[1] >> 16))};
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int x = t + 256 * e, r = x / 8, c = 4 * (x % 8);
-    *reinterpret_cast<f32x4v*>(dO + r * kLdS + c) =
-        f32x4v{bf((uint16_t)in.d[e][0]), bf((uint16_t)(in.d[e][0] >> 16)), bf((uint16_t)in.d[e][1]),
-               bf((uint16_t)(in.d[e][1] >> 16))};
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int x = t + 256 * e, r = x / 16, c = 8 * (x % 16);
+    const int x = t + kScanThreads * e, r = x / 16, c = 8 * (x % 16);
     const float eq = expf(ca[r]);
     const u32x4v uq = in.q[e], uk = in.k[e];
 #pragma unroll
@@ -691,13 +674,13 @@ __device__ __forceinline__ void sg_store(const SgInputs& in, float* P, float* dO
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int x = t + 256 * e, r = x / 32, c = 4 * (x % 32);
+  for (int e = 0; e < 4; ++e) {
+    const int x = t + kScanThreads * e, r = x / 32, c = 4 * (x % 32);
     *reinterpret_cast<f32x4v*>(W + r * kLd + c) = in.w[e];
   }
 }
 
-__global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
+__global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
   extern __shared__ float lds[];
   float* P = lds;                  // [64][kLdC]
   float* dO = P + kC * kLdC;       // [64][kLdS]: columns col0 .. col0 + 31 of dO
@@ -711,7 +694,7 @@ __global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
   const int r = t % 16, g = (t % 64) / 16;
   const int64_t seq = blockIdx.x / (kD / kCols);
   const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
-  for (int e = t; e < kD * kLdS; e += 256) dS[e] = 0.0f;
+  for (int e = t; e < kD * kLdS; e += kScanThreads) dS[e] = 0.0f;
   SgInputs in;
   {
     const Chunk ck = chunk_of(p, seq * p.chunks + p.chunks - 1);
@@ -727,60 +710,53 @@ __global__ __launch_bounds__(256, 1) void dn_state_grad(DnArgs p) {
     const float last = ca[kC - 1];
     // The gradient at the chunk's end state.
     float* dSc = p.dSn + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols / 4; e += 256) {
+    for (int e = t; e < kD * kCols / 4; e += kScanThreads) {
       const int row = e / 8, c = 4 * (e % 8);
       *reinterpret_cast<float4*>(dSc + row * kD + col0 + c) = *reinterpret_cast<const float4*>(dS + row * kLdS + c);
     }
-    // dU (64 x 32): wave w takes rows 16 w .. 16 w + 15.
+    // dU (64 x 32): wave w takes the 16 x 16 block at rows 16 (w mod 4),
+    // columns 16 (w / 4).
     {
-      f32x4v pd[1][2], kd[1][2];
+      f32x4v pd[1][1], kd[1][1];
       clear(pd);
       clear(kd);
-      mm_gen<true, true>(pd, P, kLdC, 16 * w, dO, kLdS, 0, kC);
-      mm_gen<false, true>(kd, K, kLd, 16 * w, dS, kLdS, 0, kD);
+      const int i0 = 16 * (w % 4), j0 = 16 * (w / 4);
+      mm_gen<true, true>(pd, P, kLdC, i0, dO, kLdS, j0, kC);
+      mm_gen<false, true>(kd, K, kLd, i0, dS, kLdS, j0, kD);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int i = 16 * w + 4 * g + v;
-        const float e = expf(last - ca[i]);
-#pragma unroll
-        for (int bj = 0; bj < 2; ++bj) dU[i * kLdS + 16 * bj + r] = pd[0][bj][v] + e * kd[0][bj][v];
+        const int i = i0 + 4 * g + v;
+        dU[i * kLdS + j0 + r] = pd[0][0][v] + expf(last - ca[i]) * kd[0][0][v];
       }
     }
     __syncthreads();
     // dU to memory from LDS in 16-byte pieces, beside the products below.
     {
       float* dUo = p.dU + ck.c * kC * kD;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int x = t + 256 * e, row = x / 8, c = 4 * (x % 8);
-        *reinterpret_cast<f32x4v*>(dUo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(dU + row * kLdS + c);
-      }
+      const int row = t / 8, c = 4 * (t % 8);
+      *reinterpret_cast<f32x4v*>(dUo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(dU + row * kLdS + c);
     }
-    // dS <- Qg' dO + g dS - W' dU (128 x 32): wave w takes rows 32 w .. 32 w + 31.
+    // dS <- Qg' dO + g dS - W' dU (128 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
-      f32x4v qd[2][2], wu[2][2];
+      f32x4v qd[1][2], wu[1][2];
       clear(qd);
       clear(wu);
-      mm_gen<true, true>(qd, Qg, kLd, 32 * w, dO, kLdS, 0, kC);
-      mm_gen<true, true>(wu, W, kLd, 32 * w, dU, kLdS, 0, kC);
+      mm_gen<true, true>(qd, Qg, kLd, 16 * w, dO, kLdS, 0, kC);
+      mm_gen<true, true>(wu, W, kLd, 16 * w, dU, kLdS, 0, kC);
       const float gl = expf(last);
-      float nw[2][2][4];
+      float nw[2][4];
 #pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
+      for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int i = 32 * w + 16 * bi + 4 * g + v, j = 16 * bj + r;
-            nw[bi][bj][v] = qd[bi][bj][v] + gl * dS[i * kLdS + j] - wu[bi][bj][v];
-          }
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * w + 4 * g + v, j = 16 * bj + r;
+          nw[bj][v] = qd[0][bj][v] + gl * dS[i * kLdS + j] - wu[0][bj][v];
+        }
       __syncthreads();  // every wave has read dS, dU and this chunk's inputs
 #pragma unroll
-      for (int bi = 0; bi < 2; ++bi)
+      for (int bj = 0; bj < 2; ++bj)
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) dS[(32 * w + 16 * bi + 4 * g + v) * kLdS + 16 * bj + r] = nw[bi][bj][v];
+        for (int v = 0; v < 4; ++v) dS[(16 * w + 4 * g + v) * kLdS + 16 * bj + r] = nw[bj][v];
     }
     if (n > 0) {
       if (t < kC) ca[t] = in.ca;
@@ -1284,10 +1260,10 @@ int build(const th_deltanet_desc* d, bool backward, th_launch** out) {
   int ks[6];
   int nk = 0;
   ks[nk++] = b.kernel(fns[0], "dn_chunk_prep", dim3(nchunks), dim3(256), (uint32_t)kPrepLds, a);
-  ks[nk++] = b.kernel(fns[1], "dn_state_scan", dim3(scans), dim3(256), (uint32_t)kScanLds, a);
+  ks[nk++] = b.kernel(fns[1], "dn_state_scan", dim3(scans), dim3(kScanThreads), (uint32_t)kScanLds, a);
   ks[nk++] = b.kernel(fns[2], "dn_output", dim3(nchunks), dim3(256), (uint32_t)kOutLds, a);
   if (backward) {
-    ks[nk++] = b.kernel(fns[3], "dn_state_grad", dim3(scans), dim3(256), (uint32_t)kSgLds, a);
+    ks[nk++] = b.kernel(fns[3], "dn_state_grad", dim3(scans), dim3(kScanThreads), (uint32_t)kSgLds, a);
     ks[nk++] = b.kernel(fns[4], "dn_grad_a", dim3(nchunks), dim3(256), (uint32_t)kGaLds, a);
     ks[nk++] = b.kernel(fns[5], "dn_grad_b", dim3(nchunks), dim3(256), (uint32_t)kGbLds, a);
   }
