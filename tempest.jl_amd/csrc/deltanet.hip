@@ -967,6 +967,12 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   // dbeta_i gets sum_j dA Gamma G; w = (dA beta_i G + dP QK) o Gamma gives
   // dca_i += sum_j w_ij - sum_j w_ji.
   {
+    // This lane's dP values, loaded under the products below.
+    float dpv[4][4];
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dpv[bj][v] = dP[(i0 + 4 * g + v) * kC + 16 * bj + r];
     f32x4v gk[1][4], qk[1][4];
     clear(gk);
     clear(qk);
@@ -994,7 +1000,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
         const float gg = bj <= w ? gk[0][bj][v] : 0.0f, q = bj <= w ? qk[0][bj][v] : 0.0f;
         N[i * kLdC + j] = dA * be[i] * gam;
         rowb[v] += dA * gam * gg;
-        const float wv = i >= j ? (dA * be[i] * gg + dP[i * kC + j] * q) * gam : 0.0f;
+        const float wv = i >= j ? (dA * be[i] * gg + dpv[bj][v] * q) * gam : 0.0f;
         roww[v] += wv;
         colw[bj] += wv;
       }
@@ -1024,9 +1030,15 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   __syncthreads();
   // dQK = dP o Gamma (lower), read by two of the products below along its rows
   // and its columns: formed once into N (free now), not at every read.
-  for (int e = t; e < kC * kC; e += 256) {
-    const int i = e / kC, j = e % kC;
-    N[i * kLdC + j] = i >= j ? dP[i * kC + j] * expf(ca[i] - ca[j]) : 0.0f;
+  {
+    float x[kC * kC / 256];
+#pragma unroll
+    for (int u = 0; u < kC * kC / 256; ++u) x[u] = dP[t + 256 * u];
+#pragma unroll
+    for (int u = 0; u < kC * kC / 256; ++u) {
+      const int e = t + 256 * u, i = e / kC, j = e % kC;
+      N[i * kLdC + j] = i >= j ? x[u] * expf(ca[i] - ca[j]) : 0.0f;
+    }
   }
   __syncthreads();
   // dQ = e^ca dQg + dQK K;  dV = beta T' dU~;  dK = dQK' Q + (dG + dG') K +
@@ -1037,6 +1049,13 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
     const RowF32 Rr{N, kLdC};  // dQK along its rows
     const ColF32 Rc{N, kLdC};  // and along its columns
     {
+      float gqv[4][4][2];  // this lane's dQg, loaded under the product
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj) gqv[bi][v][bj] = dQg[(16 * bi + 4 * g + v) * kD + d0 + 16 * bj + r];
       f32x4v dq[4][2];
       clear(dq);
       mm_by(dq, Rr, 0, Kc, d0, kC);
@@ -1050,7 +1069,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
 #pragma unroll
           for (int bj = 0; bj < 2; ++bj) {
             const int d = d0 + 16 * bj + r;
-            const float gq = dQg[i * kD + d], qv = bf(Qh[i * kLdH + d]);
+            const float gq = gqv[bi][v][bj], qv = bf(Qh[i * kLdH + d]);
             sq = fmaf(qv, gq, sq);
             p.dq[ck.row0 + (int64_t)i * p.s_t + d] = to_bf(e * gq + dq[bi][bj][v]);
           }
@@ -1099,6 +1118,13 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
     {
       // dX first; its terms of dK (beta e^ca dX + e^(last - ca) dKd) then
       // seed dK's accumulator, so one accumulator set is live at a time.
+      float gkv[4][4][2];  // this lane's dKd, loaded under the product
+#pragma unroll
+      for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int bj = 0; bj < 2; ++bj) gkv[bi][v][bj] = dKd[(16 * bi + 4 * g + v) * kD + d0 + 16 * bj + r];
       f32x4v acc[4][2];
       clear(acc);
       mm_by(acc, ColF32{Tc, kC}, 0, ColF32{dW, kD}, d0, kC);
@@ -1112,7 +1138,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
 #pragma unroll
           for (int bj = 0; bj < 2; ++bj) {
             const int d = d0 + 16 * bj + r;
-            const float gk = dKd[i * kD + d], kv = bf(Kh[i * kLdH + d]);
+            const float gk = gkv[bi][v][bj], kv = bf(Kh[i * kLdH + d]);
             const float xv = acc[bi][bj][v];
             sx = fmaf(kv, xv, sx);
             sk = fmaf(kv, gk, sk);
