@@ -231,18 +231,37 @@ __device__ __forceinline__ void clear(f32x4v (&acc)[BI][BJ]) {
 }
 
 // rows x 128 fp32 from global (row stride 128) into LDS rows of kLd, 16-byte pieces.
-__device__ __forceinline__ void stage_f32(float* dst, const float* src, int rows) {
-  for (int e = threadIdx.x; e < rows * 32; e += 256) {
-    const int r = e / 32, c = 4 * (e % 32);
-    *reinterpret_cast<float4*>(dst + r * kLd + c) = *reinterpret_cast<const float4*>(src + r * kD + c);
+// Each staging helper issues all of a thread's loads before its first LDS
+// store, so their latencies overlap instead of adding up.
+__device__ __forceinline__ void stage_f32(float* dst, const float* src) {
+  constexpr int n = kC * 32 / 256;
+  float4 x[n];
+#pragma unroll
+  for (int u = 0; u < n; ++u) {
+    const int e = threadIdx.x + 256 * u;
+    x[u] = *reinterpret_cast<const float4*>(src + (e / 32) * kD + 4 * (e % 32));
+  }
+#pragma unroll
+  for (int u = 0; u < n; ++u) {
+    const int e = threadIdx.x + 256 * u;
+    *reinterpret_cast<float4*>(dst + (e / 32) * kLd + 4 * (e % 32)) = x[u];
   }
 }
 
 // 64 x 128 bf16 of a (d, heads, positions, batch) array into LDS as fp32 rows of kLd.
 __device__ __forceinline__ void stage_bf16(float* dst, const uint16_t* src, int64_t s_t) {
-  for (int e = threadIdx.x; e < kC * 16; e += 256) {
+  constexpr int n = kC * 16 / 256;
+  uint4 x[n];
+#pragma unroll
+  for (int q = 0; q < n; ++q) {
+    const int e = threadIdx.x + 256 * q;
+    x[q] = *reinterpret_cast<const uint4*>(src + (e / 16) * s_t + 8 * (e % 16));
+  }
+#pragma unroll
+  for (int q = 0; q < n; ++q) {
+    const int e = threadIdx.x + 256 * q;
     const int r = e / 16, c8 = 8 * (e % 16);
-    const uint4 w = *reinterpret_cast<const uint4*>(src + r * s_t + c8);
+    const uint4 w = x[q];
     const uint32_t u[4] = {w.x, w.y, w.z, w.w};
     float f[8];
 #pragma unroll
@@ -330,10 +349,23 @@ constexpr int kLdH = kD + 8;  // bf16 LDS row of Q, K
 // U~ = T diag(beta) V; the products on the matrix cores (split bf16), K and V in
 // LDS as bf16.
 
-__device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* src, int64_t s_t) {
-  for (int e = threadIdx.x; e < kC * (kD / 8); e += 256) {
-    const int row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
-    *reinterpret_cast<uint4*>(dst + row * kLdH + c8) = *reinterpret_cast<const uint4*>(src + row * s_t + c8);
+// Two 64 x 128 bf16 arrays of rows at s_t into LDS rows of kLdH, every load
+// issued before the first store.
+__device__ __forceinline__ void stage_rows_bf16(uint16_t* dst1, const uint16_t* src1, uint16_t* dst2,
+                                                const uint16_t* src2, int64_t s_t) {
+  constexpr int n = kC * (kD / 8) / 256;
+  uint4 x1[n], x2[n];
+#pragma unroll
+  for (int u = 0; u < n; ++u) {
+    const int e = threadIdx.x + 256 * u, row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
+    x1[u] = *reinterpret_cast<const uint4*>(src1 + row * s_t + c8);
+    x2[u] = *reinterpret_cast<const uint4*>(src2 + row * s_t + c8);
+  }
+#pragma unroll
+  for (int u = 0; u < n; ++u) {
+    const int e = threadIdx.x + 256 * u, row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
+    *reinterpret_cast<uint4*>(dst1 + row * kLdH + c8) = x1[u];
+    *reinterpret_cast<uint4*>(dst2 + row * kLdH + c8) = x2[u];
   }
 }
 
@@ -353,8 +385,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
   const Chunk ck = chunk_of(p, blockIdx.x);
   const int t = threadIdx.x, w = t / 64;
   const int r = t % 16, g = (t % 64) / 16;
-  stage_rows_bf16(Kh, p.k + ck.row0, p.s_t);
-  stage_rows_bf16(Vh, p.v + ck.row0, p.s_t);
+  stage_rows_bf16(Kh, p.k + ck.row0, Vh, p.v + ck.row0, p.s_t);
   cumulative_gates(ca, p, ck);
   if (t < 64) be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
   __syncthreads();
@@ -568,8 +599,7 @@ __global__ __launch_bounds__(256, 2) void dn_output(DnArgs p) {
   const int r = t % 16, g = (t % 64) / 16;
   const float* S = p.S + ck.c * kD * kD;  // [128][128]
   const float* U = p.U + ck.c * kC * kD;  // [64][128]
-  stage_rows_bf16(Qh, p.q + ck.row0, p.s_t);
-  stage_rows_bf16(Kh, p.k + ck.row0, p.s_t);
+  stage_rows_bf16(Qh, p.q + ck.row0, Kh, p.k + ck.row0, p.s_t);
   if (t < 64) ca[t] = p.ca[ck.c * kC + t];
   __syncthreads();
   const RowBf16 Qr{Qh, kLdH};
@@ -817,7 +847,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
   const float* Sc = p.S + ck.c * kD * kD;
   const float* dSc = p.dSn + ck.c * kD * kD;
   stage_bf16(dO, p.dout + ck.row0, p.s_t);
-  stage_f32(X, p.dU + ck.c * kC * kD, kC);
+  stage_f32(X, p.dU + ck.c * kC * kD);
   __syncthreads();
   {
     f32x4v q[4][2], wq[4][2];
@@ -828,7 +858,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
     store_blocks(p.dW + ck.c * kC * kD, kD, wq, 0, 32 * w, -1.0f);
   }
   __syncthreads();
-  stage_f32(X, p.U + ck.c * kC * kD, kC);
+  stage_f32(X, p.U + ck.c * kC * kD);
   __syncthreads();
   {
     f32x4v kd[4][2];
@@ -853,6 +883,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
   }
   // dg = <S, dSn>, both from memory, a fixed tree.
   float sum = 0.0f;
+#pragma unroll 4
   for (int e = t; e < kD * kD / 4; e += 256) {
     const int r = e / 32, c = 4 * (e % 32);
     const float4 sv = *reinterpret_cast<const float4*>(Sc + r * kD + c);
@@ -904,11 +935,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   const uint16_t* qg = p.q + ck.row0;
   const uint16_t* kg = p.k + ck.row0;
   const uint16_t* vg = p.v + ck.row0;
-  for (int e = t; e < kC * (kD / 8); e += 256) {
-    const int row = e / (kD / 8), c8 = (e % (kD / 8)) * 8;
-    *reinterpret_cast<uint4*>(Qh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(qg + row * p.s_t + c8);
-    *reinterpret_cast<uint4*>(Kh + row * kLdH + c8) = *reinterpret_cast<const uint4*>(kg + row * p.s_t + c8);
-  }
+  stage_rows_bf16(Qh, qg, Kh, kg, p.s_t);
   const float* Tc = p.T + ck.c * kC * kC;  // [64][64]
   const float* dW = p.dW + ck.c * kC * kD;
   const float* dUt = p.dU + ck.c * kC * kD;
