@@ -405,21 +405,31 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
     }
   }
   __syncthreads();
-  // T = (I + A)^-1 by forward substitution, lane j owning column j:
-  // T_ij = -sum_{l<i} A_il T_lj for i > j, T_jj = 1.
-  if (t < 64) {
-    const int j = t;
-    float col[kC];
+  // T = (I + A)^-1 by forward substitution: T_ij = -sum_{l<i} A_il T_lj for
+  // i > j, T_jj = 1.  Column j = 16 w + (lane / 4) belongs to the four lanes
+  // q = lane mod 4 of a quad of wave w: lane q sums the terms l = 4 m + q
+  // and keeps T_lj for those l (c[m]), the quad adds its four partial sums
+  // ((q0 + q1) + (q2 + q3) in every lane), so all four waves share the
+  // 2080 fmas of the sweep.  A_il is 0 for l >= i, so the terms of rows not
+  // yet solved (c[m] still 0) add nothing.
+  {
+    const int q = t % 4, j = 16 * w + (t % 64) / 4;
+    float c[kC / 4];
+#pragma unroll
+    for (int m = 0; m < kC / 4; ++m) c[m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < kC; ++i) {
-      float sum = 0.0f;
+      float part = 0.0f;
 #pragma unroll
-      for (int l = 0; l < i; ++l) sum = fmaf(AT[i * kLdC + l], col[l], sum);
-      col[i] = i == j ? 1.0f : (i < j ? 0.0f : -sum);
+      for (int m = 0; m < (i + 3) / 4; ++m) part = fmaf(AT[i * kLdC + 4 * m + q], c[m], part);
+      part += __shfl_xor(part, 1, 64);
+      part += __shfl_xor(part, 2, 64);
+      const float ti = i == j ? 1.0f : (i < j ? 0.0f : -part);
+      if (q == i % 4) c[i / 4] = ti;
     }
-    // One wave: its LDS reads of A above complete before its writes of T below.
+    __syncthreads();  // every wave's reads of A precede the writes of T
 #pragma unroll
-    for (int i = 0; i < kC; ++i) AT[i * kLdC + j] = col[i];
+    for (int m = 0; m < kC / 4; ++m) AT[(4 * m + q) * kLdC + j] = c[m];
   }
   __syncthreads();
   {
