@@ -537,11 +537,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
     __syncthreads();
     if (n + 1 < p.chunks) scan_load(in, p, chunk_of(p, seq * p.chunks + n + 1), col0);
     const float gl = expf(ca[kC - 1]);
-    // The chunk's starting state, stored for the output and the backward.
+    // The chunk's starting state, stored for the output and the backward: read
+    // now, written to memory at the chunk's end (and U with it), after the
+    // next chunk's inputs are in LDS, whose wait for their loads would also
+    // wait for every store issued before it.
     float* Sc = p.S + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols / 4; e += kScanThreads) {
-      const int row = e / 8, c = 4 * (e % 8);
-      *reinterpret_cast<f32x4v*>(Sc + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(S + row * kLdS + c);
+    f32x4v s_out[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = t + kScanThreads * u, row = e / 8, c = 4 * (e % 8);
+      s_out[u] = *reinterpret_cast<const f32x4v*>(S + row * kLdS + c);
     }
     // U = U~ - W S (64 x 32): wave w takes the 16 x 16 block at rows
     // 16 (w mod 4), columns 16 (w / 4).
@@ -557,12 +562,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
       }
     }
     __syncthreads();
-    // U to memory from LDS in 16-byte pieces, beside the products below.
-    {
-      float* Uo = p.U + ck.c * kC * kD;
-      const int row = t / 8, c = 4 * (t % 8);
-      *reinterpret_cast<f32x4v*>(Uo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(U + row * kLdS + c);
-    }
+    // U for memory, 16 bytes a thread.
+    const f32x4v u_out = *reinterpret_cast<const f32x4v*>(U + (t / 8) * kLdS + 4 * (t % 8));
     // S <- g S + Kd' U (128 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
       f32x4v ku[1][2];
@@ -587,6 +588,13 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
       __syncthreads();
       scan_store(in, W, Ut, Kd, ca);
     }
+    // S and U of this chunk to memory.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = t + kScanThreads * u, row = e / 8, c = 4 * (e % 8);
+      *reinterpret_cast<f32x4v*>(Sc + row * kD + col0 + c) = s_out[u];
+    }
+    *reinterpret_cast<f32x4v*>(p.U + ck.c * kC * kD + (t / 8) * kD + col0 + 4 * (t % 8)) = u_out;
   }
 }
 
@@ -748,11 +756,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
     __syncthreads();
     if (n > 0) sg_load(in, p, chunk_of(p, seq * p.chunks + n - 1), col0);
     const float last = ca[kC - 1];
-    // The gradient at the chunk's end state.
+    // The gradient at the chunk's end state: read now, written to memory at
+    // the chunk's end (and dU with it), after the previous chunk's inputs are
+    // in LDS, whose wait for their loads would also wait for every store
+    // issued before it.
     float* dSc = p.dSn + ck.c * kD * kD;
-    for (int e = t; e < kD * kCols / 4; e += kScanThreads) {
-      const int row = e / 8, c = 4 * (e % 8);
-      *reinterpret_cast<float4*>(dSc + row * kD + col0 + c) = *reinterpret_cast<const float4*>(dS + row * kLdS + c);
+    f32x4v ds_out[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = t + kScanThreads * u, row = e / 8, c = 4 * (e % 8);
+      ds_out[u] = *reinterpret_cast<const f32x4v*>(dS + row * kLdS + c);
     }
     // dU (64 x 32): wave w takes the 16 x 16 block at rows 16 (w mod 4),
     // columns 16 (w / 4).
@@ -770,12 +783,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       }
     }
     __syncthreads();
-    // dU to memory from LDS in 16-byte pieces, beside the products below.
-    {
-      float* dUo = p.dU + ck.c * kC * kD;
-      const int row = t / 8, c = 4 * (t % 8);
-      *reinterpret_cast<f32x4v*>(dUo + row * kD + col0 + c) = *reinterpret_cast<const f32x4v*>(dU + row * kLdS + c);
-    }
+    // dU for memory, 16 bytes a thread.
+    const f32x4v du_out = *reinterpret_cast<const f32x4v*>(dU + (t / 8) * kLdS + 4 * (t % 8));
     // dS <- Qg' dO + g dS - W' dU (128 x 32): wave w takes rows 16 w .. 16 w + 15.
     {
       f32x4v qd[1][2], wu[1][2];
@@ -803,6 +812,13 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       __syncthreads();
       sg_store(in, P, dO, Qg, K, W, ca);
     }
+    // dSn and dU of this chunk to memory.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = t + kScanThreads * u, row = e / 8, c = 4 * (e % 8);
+      *reinterpret_cast<f32x4v*>(dSc + row * kD + col0 + c) = ds_out[u];
+    }
+    *reinterpret_cast<f32x4v*>(p.dU + ck.c * kC * kD + (t / 8) * kD + col0 + 4 * (t % 8)) = du_out;
   }
 }
 
