@@ -479,7 +479,7 @@ def config5(target, steps: int = 3, warmup: int = 1):
     s = e0.elapsed_time(e1) * 1e-3 / steps
     return {"ms_per_step": s * 1e3, "TFLOP/s": w.flops / s / 1e12, "GB/s": w.bytes / s / 1e9,
             "flops_per_step": w.flops, "bytes_per_step": w.bytes,
-            "note": "fp32 products on the matrix cores (chunk prep, column-split state scan, outputs, reverse "
+            "note": "fp32 products as split bf16 on the matrix cores (chunk prep, column-split state scan, outputs, reverse "
                     "state-gradient scan, chunk-local backward); flops/bytes are the algorithmic estimates of "
                     "th_launch_work"}
 
