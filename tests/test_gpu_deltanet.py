@@ -30,7 +30,9 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (1, 256, 2), (2, 192, 3)])
+# (1, 8192, 2): config 5's sequence length, 128 chunks of state hand-off
+# through the split-bf16 products.
+@pytest.mark.parametrize("B,T,H", [(1, 64, 1), (1, 256, 2), (2, 192, 3), (1, 8192, 2)])
 def test_forward_and_gradient_match_oracle(target, B, T, H):
     import tempest_hip as th
     announce("deltanet", B, T, H)
