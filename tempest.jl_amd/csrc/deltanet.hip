@@ -512,6 +512,27 @@ __device__ __forceinline__ void scan_store(const ScanInputs& in, float* W, float
   }
 }
 
+// Scan workgroup b -> (sequence, first column of its slice of S).  The chip
+// hands workgroups to its 8 XCDs in turn (b mod 8), each XCD with its own L2;
+// the slices of one sequence read the same chunk inputs (W, K, Q, P), so they
+// go to one XCD, whose L2 then serves all but the first read: slice j of
+// sequence s is workgroup 32 (s / 8) + 8 j + s mod 8 for the sequences in
+// whole groups of eight, the rest in order after them.
+struct ScanSlot {
+  int64_t seq;
+  int col0;
+};
+__device__ __forceinline__ ScanSlot scan_slot() {
+  constexpr int kSlices = kD / kCols;
+  const int b = blockIdx.x, nseq = gridDim.x / kSlices, whole = nseq / 8 * 8;
+  if (b < whole * kSlices) {
+    const int q = b / 8;
+    return ScanSlot{(int64_t)(q / kSlices) * 8 + b % 8, (q % kSlices) * kCols};
+  }
+  const int x = b - whole * kSlices;
+  return ScanSlot{(int64_t)whole + x / kSlices, (x % kSlices) * kCols};
+}
+
 constexpr size_t kScanLds = (2 * kC * kLd + kC * kLdS + kD * kLdS + kC * kLdS + kC) * sizeof(float);
 
 __global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
@@ -524,8 +545,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_scan(DnArgs p) {
   float* ca = U + kC * kLdS;      // [64]
   const int t = threadIdx.x, w = t / 64;
   const int r = t % 16, g = (t % 64) / 16;
-  const int64_t seq = blockIdx.x / (kD / kCols);
-  const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
+  const ScanSlot slot = scan_slot();
+  const int64_t seq = slot.seq;
+  const int col0 = slot.col0;
   for (int e = t; e < kD * kLdS; e += kScanThreads) S[e] = 0.0f;
   ScanInputs in;
   scan_load(in, p, chunk_of(p, seq * p.chunks), col0);
@@ -740,8 +762,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
   float* ca = dU + kC * kLdS;      // [64]
   const int t = threadIdx.x, w = t / 64;
   const int r = t % 16, g = (t % 64) / 16;
-  const int64_t seq = blockIdx.x / (kD / kCols);
-  const int col0 = (blockIdx.x % (kD / kCols)) * kCols;
+  const ScanSlot slot = scan_slot();
+  const int64_t seq = slot.seq;
+  const int col0 = slot.col0;
   for (int e = t; e < kD * kLdS; e += kScanThreads) dS[e] = 0.0f;
   SgInputs in;
   {
