@@ -984,10 +984,30 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   const uint16_t* qg = p.q + ck.row0;
   const uint16_t* kg = p.k + ck.row0;
   const uint16_t* vg = p.v + ck.row0;
-  stage_rows_bf16(Qh, qg, Kh, kg, p.s_t);
   const float* Tc = p.T + ck.c * kC * kC;  // [64][64]
   const float* dW = p.dW + ck.c * kC * kD;
   const float* dUt = p.dU + ck.c * kC * kD;
+  const int i0 = 16 * w;  // this wave's rows of the 64 x 64 work
+  // The first products' operands from memory (this wave's rows of dW and
+  // dU~, its lanes' V), requested before the staging so that their latency
+  // overlaps it: lane (r, g) takes k = 32 kb + 8 g + (0..7).
+  f32x4v dwq[8], duq[8];
+  uint2 vq[4][8];
+  {
+    const float* dWr = dW + (i0 + r) * kD + 8 * g;
+    const float* dUr = dUt + (i0 + r) * kD + 8 * g;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      dwq[h] = quad(dWr + 32 * (h / 2) + 4 * (h % 2));
+      duq[h] = quad(dUr + 32 * (h / 2) + 4 * (h % 2));
+    }
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+        vq[bj][h] = *reinterpret_cast<const uint2*>(vg + (int64_t)(16 * bj + r) * p.s_t + 32 * (h / 2) + 8 * g + 4 * (h % 2));
+  }
+  stage_rows_bf16(Qh, qg, Kh, kg, p.s_t);
   const float* dQg = p.dQg + ck.c * kC * kD;
   const float* dKd = p.dKd + ck.c * kC * kD;
   const float* dP = p.dP + ck.c * kC * kC;
@@ -999,14 +1019,26 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   const RowBf16 Kr{Kh, kLdH}, Qr{Qh, kLdH};
   const ColBf16 Kc{Kh, kLdH}, Qc{Qh, kLdH};
   const float last = ca[kC - 1];
-  const int i0 = 16 * w;  // this wave's rows of the 64 x 64 work
   // dT = dW X' + dU~ Y',  X = diag(beta e^ca) K, Y = diag(beta) V.
   {
     f32x4v xk[1][4], yv[1][4];
     clear(xk);
     clear(yv);
-    mm_by(xk, RowF32{dW, kD}, i0, Kr, 0, kD);
-    mm_by(yv, RowF32{dUt, kD}, i0, RowBf16{vg, p.s_t}, 0, kD);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const Split8 aw = split8<false>(dwq[2 * kb], dwq[2 * kb + 1]);
+      const Split8 au = split8<false>(duq[2 * kb], duq[2 * kb + 1]);
+#pragma unroll
+      for (int bj = 0; bj < 4; ++bj) {
+        const int x = 16 * bj + r, k0 = 32 * kb + 8 * g;
+        const Split8 bk = split8<true>(Kr.quad(x, k0), Kr.quad(x, k0 + 4));
+        xk[0][bj] = mma_split<false, true>(aw, bk, xk[0][bj]);
+        const uint2 v0 = vq[bj][2 * kb], v1 = vq[bj][2 * kb + 1];
+        const Split8 bv{__builtin_bit_cast(bf16x8v, u32x4v{v0.x, v0.y, v1.x, v1.y}),
+                        __builtin_bit_cast(bf16x8v, u32x4v{0u, 0u, 0u, 0u})};
+        yv[0][bj] = mma_split<false, true>(au, bv, yv[0][bj]);
+      }
+    }
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj)
 #pragma unroll
