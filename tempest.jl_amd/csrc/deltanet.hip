@@ -108,8 +108,9 @@ __device__ __forceinline__ void cumulative_gates(float* ca, const DnArgs& p, con
 // Each fp32 operand x is split as hi = bf16(x), lo = bf16(x - hi); a b is
 // summed in fp32 as hi hi + hi lo + lo hi on v_mfma_f32_16x16x32_bf16 (the
 // lo lo term and lo's rounding leave about 2^-16 of each product; operands
-// that are bf16 values, Q K V, have no lo).  Three bf16 products cost less
-// than half of the one fp32 product v_mfma_f32_16x16x4_f32 would.
+// that are bf16 values, Q K V, have no lo).  The three bf16 products of 32 k
+// take 48 matrix-core cycles, the eight fp32 ones (v_mfma_f32_16x16x4_f32)
+// for the same k would take 256.
 // Operands sit in LDS as fp32 rows of kLd floats: a row's 16-byte quads land
 // on distinct bank quads for 16 consecutive rows (kLd / 4 odd), and a column
 // read by 16 consecutive rows x 4 row groups hits 64 distinct banks
