@@ -63,7 +63,7 @@ struct DnArgs {
   float* dW;    // [c][64][128]
   float* dKd;   // [c][64][128]
   float* dP;    // [c][64][64]
-  float* dg;    // [c]
+  float* dg;    // [c][kDgParts]: <S, dSn> by (column slice, wave) of the state gradient
   int64_t s_h, s_t, s_b;  // strides (elements) of q, k, v, o, dout, dq, dk, dv along head, position, batch
   int64_t g_h, g_t, g_b;  // strides of a, beta, da, dbeta
   int32_t batch, heads, seq, chunks;
@@ -464,6 +464,9 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(DnArgs p) {
 // Eight waves, two on each SIMD: one workgroup per CU (its LDS), and a
 // chunk's serial chain (stage, product, product, update) split eight ways.
 constexpr int kScanThreads = 512;
+// dg = <S, dSn> of a chunk in partial sums, one per wave of each column
+// slice's state-gradient workgroup, folded in a fixed order by their reader.
+constexpr int kDgParts = (kD / kCols) * (kScanThreads / 64);
 
 struct ScanInputs {  // one chunk's inputs as this thread loads them
   f32x4v w[4];       // W: 4 x 16 bytes
@@ -778,6 +781,14 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
   for (int n = p.chunks - 1; n >= 0; --n) {
     const Chunk ck = chunk_of(p, seq * p.chunks + n);
     __syncthreads();
+    // This chunk's starting state, where this thread's dS values below sit:
+    // dg's partial sums take it at the chunk's end.
+    f32x4v s_in[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = t + kScanThreads * u, row = e / 8, c = 4 * (e % 8);
+      s_in[u] = *reinterpret_cast<const f32x4v*>(p.S + ck.c * kD * kD + row * kD + col0 + c);
+    }
     if (n > 0) sg_load(in, p, chunk_of(p, seq * p.chunks + n - 1), col0);
     const float last = ca[kC - 1];
     // The gradient at the chunk's end state: read now, written to memory at
@@ -843,11 +854,19 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       *reinterpret_cast<f32x4v*>(dSc + row * kD + col0 + c) = ds_out[u];
     }
     *reinterpret_cast<f32x4v*>(p.dU + ck.c * kC * kD + (t / 8) * kD + col0 + 4 * (t % 8)) = du_out;
+    // This wave's part of dg = <S, dSn>.
+    float dot = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dot = fmaf(s_in[u][e], ds_out[u][e], dot);
+    dot = thd::wave_sum(dot);
+    if (t % 64 == 0) p.dg[ck.c * kDgParts + (col0 / kCols) * (kScanThreads / 64) + w] = dot;
   }
 }
 
 // ---- backward: the chunk's products (part a) ---------------------------------------
-// dQg = dO S', dW = -dU S', dKd = U dSn', dP = lower(dO U'), dg = <S, dSn>,
+// dQg = dO S', dW = -dU S', dKd = U dSn', dP = lower(dO U'),
 // every product on the matrix cores (split bf16).  Two phases through LDS: dO, dU
 // and S, then U and dSn (dO stays).  Wave w computes columns 32 w .. 32 w + 31
 // of the 64 x 128 results and row block w of dP.
@@ -855,7 +874,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
 // S and dSn are read by rows straight from memory (each wave's 32 rows, for
 // both products that use them at once), so only dO and one 64-row operand
 // live in LDS and two workgroups share a CU.
-constexpr size_t kGaLds = 2 * kC * kLd * sizeof(float) + 4 * sizeof(float);
+constexpr size_t kGaLds = 2 * kC * kLd * sizeof(float);
 
 // acc1 += X1 Y', acc2 += X2 Y' over k in [0, K): X1, X2 rows i0 .. of LDS
 // (stride kLd), Y rows j0 + 16 bj .. of memory (stride kD), each Y quad read once.
@@ -891,7 +910,6 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
   extern __shared__ float lds[];
   float* dO = lds;              // [64][kLd]
   float* X = dO + kC * kLd;     // [64][kLd]: dU, then U
-  float* red = X + kC * kLd;    // [4]
   const Chunk ck = chunk_of(p, blockIdx.x);
   const int t = threadIdx.x, w = t / 64;
   const float* Sc = p.S + ck.c * kD * kD;
@@ -931,22 +949,6 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
       }
     }
   }
-  // dg = <S, dSn>, both from memory, a fixed tree.
-  float sum = 0.0f;
-#pragma unroll 4
-  for (int e = t; e < kD * kD / 4; e += 256) {
-    const int r = e / 32, c = 4 * (e % 32);
-    const float4 sv = *reinterpret_cast<const float4*>(Sc + r * kD + c);
-    const float4 dv = *reinterpret_cast<const float4*>(dSc + r * kD + c);
-    sum = fmaf(sv.x, dv.x, sum);
-    sum = fmaf(sv.y, dv.y, sum);
-    sum = fmaf(sv.z, dv.z, sum);
-    sum = fmaf(sv.w, dv.w, sum);
-  }
-  sum = thd::wave_sum(sum);
-  if (t % 64 == 0) red[t / 64] = sum;
-  __syncthreads();
-  if (t == 0) p.dg[ck.c] = red[0] + red[1] + red[2] + red[3];
 }
 
 // ---- backward: the chunk's WY form, decays and gates (part b) -----------------------
@@ -1012,6 +1014,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
   const float* dQg = p.dQg + ck.c * kC * kD;
   const float* dKd = p.dKd + ck.c * kC * kD;
   const float* dP = p.dP + ck.c * kC * kC;
+  const float dg_part = t < kDgParts ? p.dg[ck.c * kDgParts + t] : 0.0f;
   if (t < 64) {
     ca[t] = p.ca[ck.c * kC + t];
     be[t] = p.beta[ck.grow0 + (int64_t)t * p.g_t];
@@ -1290,7 +1293,11 @@ __global__ __launch_bounds__(256, 2) void dn_grad_b(DnArgs p) {
     float kd_all = kd;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) kd_all += __shfl_xor(kd_all, o, 64);
-    if (i == kC - 1) dca += kd_all + p.dg[ck.c] * expf(last);
+    // dg: its kDgParts partial sums, lane q holding part q, a fixed tree.
+    float dg = i < kDgParts ? dg_part : 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) dg += __shfl_xor(dg, o, 64);
+    if (i == kC - 1) dca += kd_all + dg * expf(last);
     float x = dca;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -1312,7 +1319,7 @@ struct Workspace {
 Workspace workspace(int64_t chunks, bool backward) {
   const size_t sizes[14] = {(size_t)kC, (size_t)kC * kC, (size_t)kC * kD, (size_t)kC * kD, (size_t)kD * kD,
                             (size_t)kC * kD, (size_t)kC * kC, (size_t)kC * kD, (size_t)kD * kD, (size_t)kC * kD,
-                            (size_t)kC * kD, (size_t)kC * kD, (size_t)kC * kC, 1};
+                            (size_t)kC * kD, (size_t)kC * kD, (size_t)kC * kC, (size_t)kDgParts};
   Workspace w{};
   size_t at = 0;
   for (int i = 0; i < 14; ++i) {
