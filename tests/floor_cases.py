@@ -1053,6 +1053,307 @@ def reverse_recurrence():
                 ["H", "Y"], closed)
 
 
+# ---- more of the fixture programs (test/fixtures/programs.jl:60-146) -----------------
+
+def log_sum_exp_written_out():
+    """sum(written_logsumexp(x; dims = 1) .* data(1, 6)), m + log(sum(exp(x - m))) by columns."""
+    x, w = data(8, 6), data(1, 6)
+
+    def row(g):
+        xx = g.load("x", (1, 8))
+        m = g.fold("max", xx).value
+        s = g.fold("sum", g.apply("exp", xx - m), phase=2).value
+        g.output("r", (m + g.apply("log", s)) * g.load("w", (0, 1)), (0, 1), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        m = X.max(axis=0)
+        r = (m + np.log(np.exp(X - m).sum(axis=0))) * v["w"]
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("log-sum-exp written out", (8, 6), (0,), row, {"x": F(x), "w": F(w)}, closed, 6)
+
+
+def softmax_by_the_maximum_read():
+    """m = maximum(x; dims = 1); e = exp.(x .- m); sum(e ./ sum(e; dims = 1) .* t) + sum(m):
+    three phases by columns, the maximum also an output term."""
+    x, t = data(8, 6), data(8, 6, scale=0.7)
+
+    def row(g):
+        xx, tt = g.load("x", (1, 8)), g.load("t", (1, 8))
+        m = g.fold("max", xx).value
+        s = g.fold("sum", g.apply("exp", xx - m), phase=2).value
+        y = g.fold("sum", g.apply("exp", xx - m) / s * tt, phase=3).value
+        g.output("r", y + m, (0, 1), full=False)
+
+    def closed(v):
+        X, T = v["x"].reshape(8, 6, order="F"), v["t"].reshape(8, 6, order="F")
+        m = X.max(axis=0)
+        e = np.exp(X - m)
+        r = (e / e.sum(axis=0) * T).sum(axis=0) + m
+        return {"r": r, "loss": [r.sum()]}
+    return _column_then_sum("softmax by the maximum, the maximum read", (8, 6), (0,), row,
+                            {"x": F(x), "t": F(t)}, closed, 6)
+
+
+def scalar_input():
+    """(x, s) -> sum(abs2, x .* s .+ s^2) with s = 0.7, a scalar argument."""
+    x = data(8, 6)
+
+    def build(g):
+        sv = g.load("s", (0, 0))
+        return g.fold("sum", g.apply("abs2", g.load("x", (1, 8)) * sv + sv * sv)).value
+    return _whole("scalar input", (8, 6), build, {"x": F(x), "s": np.array([0.7])},
+                  lambda v: {"loss": [np.sum((v["x"] * v["s"][0] + v["s"][0] ** 2) ** 2)]})
+
+
+def _column_sums_squared(name):
+    """sum(abs2, y) for y the column sums of x (8 x 6): a column group, then
+    the fold of the six sums' squares."""
+    x = data(8, 6)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0,), name="column sums")
+    g1.value("x", "f32", 48)
+    g1.value("r", "f32", 6)
+    g1.output("r", g1.fold("sum", g1.load("x", (1, 8))).value, (0, 1), full=False)
+    g2 = FloorGroup("reduction", (6,), reduced=(0,), name="sum(abs2, r)")
+    g2.value("r", "f32", 6)
+    g2.value("loss", "f32", 1)
+    g2.output("loss", g2.fold("sum", g2.apply("abs2", g2.load("r", (1,)))).value, full=False)
+
+    def closed(v):
+        r = v["x"].reshape(8, 6, order="F").sum(axis=0)
+        return {"r": r, "loss": [np.sum(r ** 2)]}
+    return Case(name, [g1, g2], {"x": F(x)}, {"r": 6, "loss": 1}, ["r", "loss"], closed)
+
+
+def vec_and_dropdims():
+    """sum(abs2, vec(dropdims(sum(x; dims = 1); dims = 1)))."""
+    return _column_sums_squared("vec and dropdims")
+
+
+def scalar_writes_in_a_loop():
+    """y = similar(x, 6); for i in 1:6; y[i] = sum(x[:, i]); end; sum(abs2, y)."""
+    return _column_sums_squared("scalar writes in a loop")
+
+
+def opaque_leaky_with_a_rule():
+    """sum(abs2, leaky.(x)), leaky(x) = x > 0 ? x : 0.01 x."""
+    x = data(8, 6)
+
+    def build(g):
+        t = g.load("x", (1, 8))
+        return g.fold("sum", g.apply("abs2", g.apply("ifelse", g.apply(">", t, 0.0), t, t * 0.01))).value
+    return _whole("opaque leaky with a rule", (8, 6), build, {"x": F(x)},
+                  lambda v: {"loss": [np.sum(np.where(v["x"] > 0, v["x"], 0.01 * v["x"]) ** 2)]})
+
+
+def norms_and_a_normalized_vector():
+    """norm(x) + norm(x, 1) + norm(x, 3) + sum(normalize(u) .* data(8; scale = 0.3)):
+    three folds over x, then u's dot and norm."""
+    x, u, w = data(8, 6), data(8, scale=0.5), data(8, scale=0.3)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="norms of x")
+    g1.value("x", "f32", 48)
+    g1.value("nx", "f32", 1)
+    t = g1.load("x", (1, 8))
+    a = g1.apply("abs", t)
+    n2 = g1.fold("sum", g1.apply("abs2", t)).value
+    n1 = g1.fold("sum", a).value
+    n3 = g1.fold("sum", a * a * a).value
+    g1.output("nx", g1.apply("sqrt", n2) + n1 + n3 ** (1.0 / 3.0), full=False)
+    g2 = FloorGroup("reduction", (8,), reduced=(0,), name="sum(normalize(u) .* w)")
+    for k, n in (("u", 8), ("w", 8), ("nx", 1), ("loss", 1)):
+        g2.value(k, "f32", n)
+    uu = g2.load("u", (1,))
+    dot = g2.fold("sum", uu * g2.load("w", (1,))).value
+    nu = g2.fold("sum", g2.apply("abs2", uu)).value
+    g2.output("loss", dot / g2.apply("sqrt", nu) + g2.load("nx", (0,)), full=False)
+
+    def closed(v):
+        X = v["x"]
+        nx = np.sqrt(np.sum(X ** 2)) + np.sum(np.abs(X)) + np.sum(np.abs(X) ** 3) ** (1 / 3)
+        return {"nx": [nx], "loss": [nx + np.sum(v["u"] / np.linalg.norm(v["u"]) * v["w"])]}
+    return Case("norms and a normalized vector", [g1, g2], {"x": F(x), "u": F(u), "w": F(w)},
+                {"nx": 1, "loss": 1}, ["nx", "loss"], closed)
+
+
+def cartesian_diagonal_and_dot():
+    """sum(abs2, diag(x)) + x[CartesianIndex(2, 3)] + dot(x, tanh.(x)), x 6 x 6:
+    the diagonal as a load of stride 7, the element at its constant offset."""
+    x = data(6, 6)
+    g1 = FloorGroup("reduction", (6,), reduced=(0,), name="sum(abs2, diag(x)) + x[2, 3]")
+    g1.value("x", "f32", 36)
+    g1.value("d", "f32", 1)
+    g1.output("d", g1.fold("sum", g1.apply("abs2", g1.load("x", (7,)))).value + g1.load("x", (0,), constant=13),
+              full=False)
+    g2 = FloorGroup("reduction", (6, 6), reduced=(0, 1), name="dot(x, tanh.(x))")
+    for k, n in (("x", 36), ("d", 1), ("loss", 1)):
+        g2.value(k, "f32", n)
+    t = g2.load("x", (1, 6))
+    g2.output("loss", g2.fold("sum", t * g2.apply("tanh", t)).value + g2.load("d", (0, 0)), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(6, 6, order="F")
+        d = np.sum(np.diag(X) ** 2) + X[1, 2]
+        return {"d": [d], "loss": [d + np.sum(X * np.tanh(X))]}
+    return Case("Cartesian indices, the diagonal and dot", [g1, g2], {"x": F(x)}, {"d": 1, "loss": 1},
+                ["d", "loss"], closed)
+
+
+def a_scalar_written_into_place():
+    """y = copy(x); y[3, 2] = s * 2; sum(abs2, y), s = 0.7."""
+    x = data(8, 6)
+    w = FloorGroup("pointwise", (1,), name="y[3, 2] = s * 2")
+    w.value("s", "f32", 1)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("s", (0,)) * 2.0, (0,), constant=2 + 8 * 1)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        Y[2, 1] = val["s"][0] * 2
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(Y ** 2)]}
+    return Case("a scalar written into place", [_copy("x", "y", (8, 6)), w,
+                                                _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", y))],
+                {"x": F(x), "s": np.array([0.7])}, {"y": 48, "loss": 1}, ["y", "loss"], closed)
+
+
+def rotation_by_a_constant_permutation():
+    """sum(abs2, x .* c .+ x[[3, 4, 1, 2], :] .* s), x 4 x 6, c and s 4 x 1: the
+    permutation [3, 4, 1, 2] is i -> (i + 2) mod 4, a load at a rotated row."""
+    x, c, sn = data(4, 6), data(4, 1), data(4, 1, scale=0.3)
+    g = FloorGroup("reduction", (2, 2, 6), reduced=(0, 1, 2), name="x .* c .+ x[[3, 4, 1, 2], :] .* s")
+    for k, n in (("x", 24), ("c", 4), ("s", 4), ("loss", 1)):
+        g.value(k, "f32", n)
+    # Row i = i0 + 2 i1 (i0, i1 in 0..1); its partner row (i + 2) mod 4 = i0 + 2 (1 - i1).
+    xi = g.load("x", (1, 2, 4))
+    xp = g.load("x", (1, -2, 4), constant=2)
+    y = xi * g.load("c", (1, 2, 0)) + xp * g.load("s", (1, 2, 0))
+    g.output("loss", g.fold("sum", g.apply("abs2", y)).value, full=False)
+
+    def closed(v):
+        X = v["x"].reshape(4, 6, order="F")
+        Y = X * v["c"][:, None] + X[[2, 3, 0, 1], :] * v["s"][:, None]
+        return {"loss": [np.sum(Y ** 2)]}
+    return Case("rotation by a constant permutation", [g], {"x": F(x), "c": F(c), "s": F(sn)}, {"loss": 1},
+                ["loss"], closed)
+
+
+def concatenations():
+    """sum(abs2, vcat(x, v) .* data(11, 6)) + sum(hcat(x, x) .* 2), x 8 x 6, v 3 x 6:
+    vcat as two loads of the 11 x 6 domain split by rows, hcat's sum as twice x's."""
+    x, v, d = data(8, 6), data(3, 6, scale=0.3), data(11, 6)
+    gx = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="x rows of vcat, and hcat(x, x)")
+    for k, n in (("x", 48), ("d", 66), ("a", 1)):
+        gx.value(k, "f32", n)
+    t = gx.load("x", (1, 8))
+    gx.output("a", gx.fold("sum", gx.apply("abs2", t * gx.load("d", (1, 11)))).value
+              + gx.fold("sum", t * 2.0 + t * 2.0).value, full=False)
+    gv = FloorGroup("reduction", (3, 6), reduced=(0, 1), name="v rows of vcat")
+    for k, n in (("v", 18), ("d", 66), ("a", 1), ("loss", 1)):
+        gv.value(k, "f32", n)
+    gv.output("loss", gv.fold("sum", gv.apply("abs2", gv.load("v", (1, 3)) * gv.load("d", (1, 11), constant=8))).value
+              + gv.load("a", (0, 0)), full=False)
+
+    def closed(val):
+        X, V, D = (val["x"].reshape(8, 6, order="F"), val["v"].reshape(3, 6, order="F"),
+                   val["d"].reshape(11, 6, order="F"))
+        a = np.sum((X * D[:8]) ** 2) + np.sum(np.hstack([X, X]) * 2)
+        return {"a": [a], "loss": [a + np.sum((V * D[8:]) ** 2)]}
+    return Case("concatenations", [gx, gv], {"x": F(x), "v": F(v), "d": F(d)}, {"a": 1, "loss": 1},
+                ["a", "loss"], closed)
+
+
+def a_write_at_index_arrays():
+    """y = copy(x); y[:, [5, 2, 6]] = v; sum(abs2, tanh.(y)): the index list a
+    gather on the written position."""
+    x, v, cols = data(8, 6), data(8, 3, scale=0.3), _idx([5, 2, 6])
+    w = FloorGroup("pointwise", (8, 3), name="y[:, [5, 2, 6]] = v")
+    w.value("v", "f32", 24)
+    w.value("cols", "i32", 3)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("v", (1, 8)), (1, 0), constant=-8, gather=w.load("cols", (0, 1)), gather_coeff=8)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        Y[:, [4, 1, 5]] = val["v"].reshape(8, 3, order="F")
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.tanh(Y) ** 2)]}
+    return Case("a write at index arrays", [_copy("x", "y", (8, 6)), w,
+                                            _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("tanh", y)))],
+                {"x": F(x), "v": F(v), "cols": cols}, {"y": 48, "loss": 1}, ["y", "loss"], closed,
+                dtypes={"cols": "i32"})
+
+
+def gather_by_a_traced_vector():
+    """(x, i) -> sum(abs2, x[:, i] .* 2), i = [3, 1, 3, 6] an argument."""
+    x, i = data(8, 6), _idx([3, 1, 3, 6])
+    g = FloorGroup("reduction", (8, 4), reduced=(0, 1), name="x[:, i] .* 2")
+    g.value("x", "f32", 48)
+    g.value("i", "i64", 4)
+    g.value("loss", "f32", 1)
+    col = g.load("i", (0, 1))
+    g.output("loss", g.fold("sum", g.apply("abs2", g.load("x", (1, 0), constant=-8, gather=col, gather_coeff=8) * 2.0)).value,
+             full=False)
+    return Case("gather by a traced vector", [g], {"x": F(x), "i": i}, {"loss": 1}, ["loss"],
+                lambda v: {"loss": [np.sum((2 * v["x"].reshape(8, 6, order="F")[:, [2, 0, 2, 5]]) ** 2)]},
+                dtypes={"i": "i64"})
+
+
+def _renamed(make, name):
+    case = make()
+    case.name = name
+    return case
+
+
+def linear_recurrence_named_with_generic_fold():
+    """accumulate(RECURRENCE, tuple.(a, b)): the same combine named with
+    GenericFold, which claims it associates; planned as the same scan."""
+    return _renamed(linear_recurrence, "a linear recurrence named with GenericFold")
+
+
+def welford_variance_as_base_spells_it():
+    """mapreduce(welford_lift, welford, x; dims = 1) observed s[3] / s[1]:
+    Welford's fold as Base spells it, planned as the square fold."""
+    return _renamed(welford_variance, "Welford's variance as Base spells it")
+
+
+def welford_variance_named_with_generic_fold():
+    """reduce(VARIANCE, x; dims = 1): the same fold named with GenericFold."""
+    return _renamed(welford_variance, "Welford's variance named with GenericFold")
+
+
+def circular_shifts_rotations_and_repeats():
+    """sum(abs2, circshift(x, (1, -2)) .* data(8, 6)) + sum(rotr90(x) .* data(6, 8)) +
+    sum(abs2, repeat(x; inner = (1, 2), outer = (2, 1)) .* data(16, 12)), x 8 x 6:
+    the shift as two Mod atoms, the rotation as a reversed affine load, the
+    repeat as a Mod and a Div atom."""
+    x, d1, d2, d3 = data(8, 6), data(8, 6), data(6, 8), data(16, 12)
+    g1 = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="circshift(x, (1, -2)) .* d1")
+    for k, n in (("x", 48), ("d1", 48), ("a", 1)):
+        g1.value(k, "f32", n)
+    shifted = g1.load("x", (0, 0), parts=[("mod", (1, 0), 8, 1, -1), ("mod", (0, 1), 6, 8, 2)])
+    g1.output("a", g1.fold("sum", g1.apply("abs2", shifted * g1.load("d1", (1, 8)))).value, full=False)
+    g2 = FloorGroup("reduction", (6, 8), reduced=(0, 1), name="rotr90(x) .* d2")
+    for k, n in (("x", 48), ("d2", 48), ("a", 1), ("b", 1)):
+        g2.value(k, "f32", n)
+    g2.output("b", g2.fold("sum", g2.load("x", (8, -1), constant=7) * g2.load("d2", (1, 6))).value
+              + g2.load("a", (0, 0)), full=False)
+    g3 = FloorGroup("reduction", (16, 12), reduced=(0, 1), name="repeat(x; inner = (1, 2), outer = (2, 1)) .* d3")
+    for k, n in (("x", 48), ("d3", 192), ("b", 1), ("loss", 1)):
+        g3.value(k, "f32", n)
+    rep = g3.load("x", (0, 0), parts=[("mod", (1, 0), 8, 1), ("div", (0, 1), 2, 8)])
+    g3.output("loss", g3.fold("sum", g3.apply("abs2", rep * g3.load("d3", (1, 16)))).value
+              + g3.load("b", (0, 0)), full=False)
+
+    def closed(v):
+        X = v["x"].reshape(8, 6, order="F")
+        D1, D2, D3 = (v["d1"].reshape(8, 6, order="F"), v["d2"].reshape(6, 8, order="F"),
+                      v["d3"].reshape(16, 12, order="F"))
+        a = np.sum((np.roll(X, (1, -2), axis=(0, 1)) * D1) ** 2)
+        b = a + np.sum(np.rot90(X, -1) * D2)
+        return {"a": [a], "b": [b], "loss": [b + np.sum((np.tile(np.repeat(X, 2, axis=1), (2, 1)) * D3) ** 2)]}
+    return Case("circular shifts, rotations and repeats", [g1, g2, g3],
+                {"x": F(x), "d1": F(d1), "d2": F(d2), "d3": F(d3)}, {"a": 1, "b": 1, "loss": 1},
+                ["a", "b", "loss"], closed)
+
+
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
@@ -1064,7 +1365,13 @@ CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, mi
          gather_by_linear_and_scalar_indices, embedding_and_layer_norm, scatter_add_gradient,
          extremes_and_where_they_are, extremes_of_a_vector, mean_recomputed, recurrence_with_recomputed_sums,
          reverse_recurrence, write_of_a_slice, padding_by_a_write, writes_through_views, strided_and_reversed_writes,
-         write_at_traced_positions, mean_divided_in_place, permutedims_and_copyto]
+         write_at_traced_positions, mean_divided_in_place, permutedims_and_copyto,
+         log_sum_exp_written_out, softmax_by_the_maximum_read, scalar_input, vec_and_dropdims,
+         scalar_writes_in_a_loop, opaque_leaky_with_a_rule, norms_and_a_normalized_vector,
+         cartesian_diagonal_and_dot, a_scalar_written_into_place, rotation_by_a_constant_permutation,
+         concatenations, a_write_at_index_arrays, gather_by_a_traced_vector,
+         linear_recurrence_named_with_generic_fold, welford_variance_as_base_spells_it,
+         welford_variance_named_with_generic_fold, circular_shifts_rotations_and_repeats]
 
 
 def run_oracle(case: Case) -> dict:

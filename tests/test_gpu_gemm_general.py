@@ -64,12 +64,14 @@ def test_products_of_the_fixture_programs(target):
         ("MLP w1 * x", data(7, 6, scale=0.1), data(6, 10), False, False, None),
         ("MLP w2 * h", data(6, 7, scale=0.2), np.tanh(data(7, 10)), False, False, None),
         ("adjoint product a' * b", data(6, 4), data(6, 5, scale=0.3), True, False, None),
-        ("spelled product", data(5, 7, scale=0.3), data(7, 6), False, False, None),
+        ("product spelled as a broadcast sum", data(5, 7, scale=0.3), data(7, 6), False, False, None),
         ("linear w * x", data(9, 7, scale=0.2), data(7, 10), False, False, None),
-        ("residual w * x .+ x", data(7, 7, scale=0.2), data(7, 10), False, False, data(7, 10)),
+        ("residual epilogue w * x .+ x", data(7, 7, scale=0.2), data(7, 10), False, False, data(7, 10)),
+        ("scaling prologue w * (x .* 0.5)", data(9, 7, scale=0.2), data(7, 10) * 0.5, False, False, None),
         ("products of transposes a' * b'", data(7, 5, scale=0.2), data(6, 7), True, True, None),
         ("matrix vector", data(5, 4), data(4, 1, scale=0.5), False, False, None),
         ("a constant times x", data(5, 4, scale=0.2), data(4, 3), False, False, None),
+        ("a constant times a vector", data(5, 4, scale=0.2), data(4, 1, scale=0.5), False, False, None),
         ("x' times a constant", data(5, 3), data(5, 4, scale=0.2), True, False, None),
     ]
     for name, a, b, ta, tb, d in cases:
@@ -89,6 +91,15 @@ def test_batched_products(target):
     c = data(3, 5, 2)
     got, _ = _product(data(3, 5, 2) * 0 + c, b.transpose(1, 0, 2).copy(), (3, 5), (5, 4), batch=2)
     assert relative(got, interpret.product(c, b.transpose(1, 0, 2))) < TOL_F32
+    # "batched product with a constant" and "constant batched product": the
+    # closed-over BATCH = data(4, 3, 2; scale = 0.3) as either factor.
+    const = data(4, 3, 2, scale=0.3)
+    a3 = data(3, 4, 2)
+    got, _ = _product(a3, const, (3, 4), (4, 3), batch=2)
+    assert relative(got, interpret.product(a3, const)) < TOL_F32
+    b3 = data(3, 5, 2)
+    got, _ = _product(const, b3, (4, 3), (3, 5), batch=2)
+    assert relative(got, interpret.product(const, b3)) < TOL_F32
 
 
 @pytest.mark.parametrize("factors,result", [("bf16", "bf16"), ("bf16", "f32"), ("f16", "f16"), ("f16", "f32")])
