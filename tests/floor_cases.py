@@ -1374,6 +1374,58 @@ CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, mi
          welford_variance_named_with_generic_fold, circular_shifts_rotations_and_repeats]
 
 
+# ---- writes where several elements land at one position ---------------------------
+# REPEATED_WRITES (test/fixtures/programs.jl:148-155): the interpreters and
+# the CPU's floor take the colliding writes in order, the last landing; a
+# device lands any one of them, so, as in the reference, these are checked on
+# the CPU only (the oracle's groups against the closed form).
+
+def a_write_at_repeated_positions():
+    """y = copy(x); y[[2, 7, 2], :] .= v; sum(abs2, sin.(y)): rows 2 and 7 of y
+    get rows 3 and 2 of v (the later write to row 2 lands)."""
+    x, v, rows = data(8, 6), data(3, 6, scale=0.3), _idx([2, 7, 2])
+    w = FloorGroup("pointwise", (3, 6), name="y[[2, 7, 2], :] .= v")
+    w.value("v", "f32", 18)
+    w.value("rows", "i64", 3)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("v", (1, 3)), (0, 8), constant=-1, gather=w.load("rows", (1, 0)), gather_coeff=1)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        V = val["v"].reshape(3, 6, order="F")
+        for k, r in enumerate([1, 6, 1]):
+            Y[r, :] = V[k, :]
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.sin(Y) ** 2)]}
+    return Case("a write at repeated positions", [_copy("x", "y", (8, 6)), w,
+                                                  _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("sin", y)))],
+                {"x": F(x), "v": F(v), "rows": rows}, {"y": 48, "loss": 1}, ["y", "loss"], closed,
+                dtypes={"rows": "i64"})
+
+
+def a_write_at_repeated_traced_positions():
+    """y = copy(x); y[:, i] .= v; sum(abs2, tanh.(y)), i = Int32[4, 1, 4]:
+    column 4 takes v's third column."""
+    x, v, i = data(8, 6), data(8, 3, scale=0.3), _idx([4, 1, 4])
+    w = FloorGroup("pointwise", (8, 3), name="y[:, i] .= v")
+    w.value("v", "f32", 24)
+    w.value("i", "i32", 3)
+    w.value("y", "f32", 48)
+    w.output("y", w.load("v", (1, 8)), (1, 0), constant=-8, gather=w.load("i", (0, 1)), gather_coeff=8)
+
+    def closed(val):
+        Y = val["x"].reshape(8, 6, order="F").copy()
+        V = val["v"].reshape(8, 3, order="F")
+        for k, c in enumerate([3, 0, 3]):
+            Y[:, c] = V[:, k]
+        return {"y": Y.ravel(order="F"), "loss": [np.sum(np.tanh(Y) ** 2)]}
+    return Case("a write at repeated traced positions", [_copy("x", "y", (8, 6)), w,
+                                                         _loss((8, 6), ["y"], lambda g, y: g.apply("abs2", g.apply("tanh", y)))],
+                {"x": F(x), "v": F(v), "i": i}, {"y": 48, "loss": 1}, ["y", "loss"], closed, dtypes={"i": "i32"})
+
+
+CPU_ONLY = [a_write_at_repeated_positions, a_write_at_repeated_traced_positions]
+
+
 def run_oracle(case: Case) -> dict:
     """Every value after the case's groups, by the oracle, in order."""
     from oracle.floor_groups import evaluate

@@ -27,6 +27,17 @@ def test_oracle_matches_closed_form(name):
         assert relative(vals[k], np.asarray(want[k], dtype=np.float64)) < tol, (name, k)
 
 
+@pytest.mark.parametrize("make", FC.CPU_ONLY, ids=[c.__name__ for c in FC.CPU_ONLY])
+def test_repeated_writes_land_in_order(make):
+    """The reference's REPEATED_WRITES, checked on the CPU as it checks them:
+    the oracle takes colliding writes in order, the last landing."""
+    case = make()
+    vals = FC.run_oracle(case)
+    want = case.closed(_cast_inputs(case))
+    for k in case.results:
+        assert relative(vals[k], np.asarray(want[k], dtype=np.float64)) < 1e-6, (case.name, k)
+
+
 def test_kat_sum_of_squares_exact():
     # src/Compiler/runtime/compile.jl:35-40: exactly 30.
     assert FC.run_oracle(FC.kat_sum_abs2())["loss"][0] == 30.0
