@@ -323,6 +323,9 @@ enum {
   TH_FN_IFELSE, TH_FN_ROUND, TH_FN_FLOOR, TH_FN_CEIL, TH_FN_SIGN, TH_FN_CLAMP, TH_FN_FMA,
   TH_FN_INV,
   TH_FN_BFLOAT16, /* x rounded to bfloat16 (nearest, ties to even) and widened back: Cast{BFloat16} */
+  TH_FN_DROPOUT,  /* (key, position, rate): the dropout fixture's keep scale, 1 / (1 - rate) or 0, from
+                     a wrapping 32-bit hash of the key and the 1-based position (stream 0);
+                     test/fixtures/operations.jl:88-103 */
   TH_FN_COUNT
 };
 

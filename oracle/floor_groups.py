@@ -53,7 +53,31 @@ def _ternary(fn, a, b, c):
         return np.where(a > c, c, np.where(a < b, b, a))
     if fn == "fma":
         return a * b + c
+    if fn == "dropout":
+        return dropout_scale(a, b, c)
     raise ValueError(fn)
+
+
+def dropout_scale(key, pos, rate):
+    """The dropout fixture's keep scale (test/fixtures/operations.jl:88-103,
+    stream 0): Int32 products of the key and the 1-based position with the
+    fixture's constants, wrapping, xor-folded; logical shifts; the top 24
+    bits as a Float32 fraction u; 1 / (1 - rate) in Float32 when u >= rate.
+    Computed in Python integers masked to 32 bits."""
+    key, pos, rate = np.broadcast_arrays(np.asarray(key), np.asarray(pos), np.asarray(rate))
+    out = np.empty(key.shape)
+    m = 0xFFFFFFFF
+    for idx in np.ndindex(key.shape):
+        h = ((int(key[idx]) * -1640531535) & m) ^ ((int(pos[idx]) * -1028477387) & m)
+        h ^= h >> 16
+        h = (h * 2146121005) & m
+        h ^= h >> 15
+        h = (h * -2073254261) & m
+        h ^= h >> 16
+        u = np.float32(h >> 8) * np.float32(2.0 ** -24)
+        r = np.float32(rate[idx])
+        out[idx] = np.float32(1) / (np.float32(1) - r) if u >= r else 0.0
+    return out
 
 
 def fold_reduce(kind: str, y: np.ndarray, g, axes: tuple):

@@ -60,7 +60,7 @@ int arity(int fn) {
     case TH_FN_MAX: case TH_FN_MIN: case TH_FN_LT: case TH_FN_LE: case TH_FN_GT:
     case TH_FN_GE: case TH_FN_EQ: case TH_FN_NE:
       return 2;
-    case TH_FN_IFELSE: case TH_FN_CLAMP: case TH_FN_FMA:
+    case TH_FN_IFELSE: case TH_FN_CLAMP: case TH_FN_FMA: case TH_FN_DROPOUT:
       return 3;
     default:
       return fn >= 0 && fn < TH_FN_COUNT ? 1 : -1;
@@ -72,7 +72,7 @@ const char* fn_name(int fn) {
       "", "", "", "", "", "th_abs", "th_abs2", "th_sqrt", "th_exp", "th_log", "th_tanh", "th_sin",
       "th_cos", "th_log1p", "th_expm1", "th_pow", "th_max", "th_min", "th_lt", "th_le", "th_gt",
       "th_ge", "th_eq", "th_ne", "th_ifelse", "th_round", "th_floor", "th_ceil", "th_sign",
-      "th_clamp", "th_fma", "th_inv", "th_rbf"};
+      "th_clamp", "th_fma", "th_inv", "th_rbf", "th_dropout"};
   return names[fn];
 }
 
@@ -681,6 +681,11 @@ __device__ __forceinline__ float th_ld(const float* p, long i) { return p[i]; }
 __device__ __forceinline__ float th_ld(const th_bf16* p, long i) { return th_bf(p[i]); }
 __device__ __forceinline__ float th_ld(float* p, long i) { return p[i]; }
 __device__ __forceinline__ float th_ld(th_bf16* p, long i) { return th_bf(p[i]); }
+// An integer value read as a term (a seed, a count): its fp32 value.
+__device__ __forceinline__ float th_ld(const int* p, long i) { return (float)p[i]; }
+__device__ __forceinline__ float th_ld(const long* p, long i) { return (float)p[i]; }
+__device__ __forceinline__ float th_ld(int* p, long i) { return (float)p[i]; }
+__device__ __forceinline__ float th_ld(long* p, long i) { return (float)p[i]; }
 __device__ __forceinline__ float th_ldn(const float* p, long i) { return __builtin_nontemporal_load(p + i); }
 __device__ __forceinline__ float th_ldn(const th_bf16* p, long i) { return th_bf(__builtin_nontemporal_load(p + i)); }
 __device__ __forceinline__ float th_ldn(float* p, long i) { return th_ldn((const float*)p, i); }
@@ -735,6 +740,20 @@ __device__ __forceinline__ float th_fma(float a, float b, float c) { return fmaf
 __device__ __forceinline__ float th_inv(float x) { return 1.0f / x; }
 // Cast{BFloat16}: rounded to bfloat16, then widened back to fp32.
 __device__ __forceinline__ float th_rbf(float x) { return th_bf(th_tobf(x)); }
+// The dropout fixture's keep scale (test/fixtures/operations.jl:88-103,
+// stream 0): the key and the 1-based position (integers held exactly in
+// fp32) hashed in wrapping 32-bit arithmetic with logical shifts; the top 24
+// bits as a fraction u, kept at scale 1 / (1 - rate) when u >= rate.
+__device__ __forceinline__ float th_dropout(float key, float pos, float rate) {
+  unsigned h = (unsigned)(int)key * 0x9e3779b1u ^ (unsigned)(int)pos * 0xc2b2ae35u;
+  h ^= h >> 16;
+  h *= 0x7feb352du;
+  h ^= h >> 15;
+  h *= 0x846ca68bu;
+  h ^= h >> 16;
+  const float u = (float)(h >> 8) * 0x1p-24f;
+  return u >= rate ? 1.0f / (1.0f - rate) : 0.0f;
+}
 // lse_shift (src/Compiler/IR/folds.jl:194): the maximum when finite, else 0.
 __device__ __forceinline__ float th_shift(float m) { return __builtin_isfinite(m) ? m : 0.0f; }
 // Relative{Exponential}: state (m, s), s the weighted sum of exp(y - shift(m)).
@@ -834,7 +853,7 @@ TH_V1(th_cos) TH_V1(th_log1p) TH_V1(th_expm1) TH_V1(th_round) TH_V1(th_floor) TH
 TH_V1(th_sign) TH_V1(th_inv) TH_V1(th_rbf)
 TH_V2(th_pow) TH_V2(th_max) TH_V2(th_min) TH_V2(th_lt) TH_V2(th_le) TH_V2(th_gt) TH_V2(th_ge)
 TH_V2(th_eq) TH_V2(th_ne)
-TH_V3(th_ifelse) TH_V3(th_clamp) TH_V3(th_fma)
+TH_V3(th_ifelse) TH_V3(th_clamp) TH_V3(th_fma) TH_V3(th_dropout)
 __device__ __forceinline__ void th_exp_step(th_v& m, th_v& s, th_v y, th_v g) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) { float a = m[j], b = s[j]; th_exp_step(a, b, y[j], g[j]); m[j] = a; s[j] = b; }

@@ -39,9 +39,9 @@ STEP = {"each": 0, "first": 1, "last": 2, "carry": 3}  # a recurrence output's r
 FN = {name: k for k, name in enumerate([
     "+", "-", "*", "/", "neg", "abs", "abs2", "sqrt", "exp", "log", "tanh", "sin", "cos", "log1p", "expm1", "^",
     "max", "min", "<", "<=", ">", ">=", "==", "!=", "ifelse", "round", "floor", "ceil", "sign", "clamp", "fma",
-    "inv", "bfloat16"])}
+    "inv", "bfloat16", "dropout"])}
 ARITY = {name: (2 if name in ("+", "-", "*", "/", "^", "max", "min", "<", "<=", ">", ">=", "==", "!=") else
-                3 if name in ("ifelse", "clamp", "fma") else 1) for name in FN}
+                3 if name in ("ifelse", "clamp", "fma", "dropout") else 1) for name in FN}
 FOLD = {"sum": 0, "prod": 1, "max": 2, "min": 3, "exp": 4, "square": 5, "linear": 6, "argmax": 7, "argmin": 8}
 SCAN = {None: 0, "inclusive": 1, "exclusive": 2}
 OBSERVE = {"value": 0, "statistic": 1, "sum": 2, "logsumexp": 3}

@@ -1354,6 +1354,39 @@ def circular_shifts_rotations_and_repeats():
                 ["a", "b", "loss"], closed)
 
 
+def dropout():
+    """(x, s) -> sum(abs2, Ops.dropout(x, s; rate = 0.25) .* 2), s = Int32[7]: the
+    keep scale of position i (1-based, column-major) a hash of the seed's
+    first element and i (test/fixtures/operations.jl:88-119)."""
+    x, s = data(8, 6), _idx([7])
+
+    def build(g):
+        pos = g.index((1, 8)) + 1.0
+        keep = g.apply("dropout", g.load("s", (0, 0)), pos, 0.25)
+        return g.fold("sum", g.apply("abs2", g.load("x", (1, 8)) * keep * 2.0)).value
+
+    def closed(v):
+        # The hash restated with numpy's wrapping uint32 arithmetic (the oracle
+        # uses Python integers masked to 32 bits).
+        i = np.arange(1, 49, dtype=np.uint32)
+        with np.errstate(over="ignore"):
+            h = (np.uint32(int(v["s"][0])) * np.uint32(0x9E3779B1)) ^ (i * np.uint32(0xC2B2AE35))
+            h ^= h >> np.uint32(16)
+            h *= np.uint32(0x7FEB352D)
+            h ^= h >> np.uint32(15)
+            h *= np.uint32(0x846CA68B)
+            h ^= h >> np.uint32(16)
+        u = (h >> np.uint32(8)).astype(np.float32) * np.float32(2.0 ** -24)
+        keep = np.where(u >= np.float32(0.25), np.float32(1) / np.float32(0.75), np.float32(0))
+        return {"loss": [np.sum((v["x"] * keep * 2) ** 2)]}
+    g = FloorGroup("reduction", (8, 6), reduced=(0, 1), name="dropout")
+    g.value("x", "f32", 48)
+    g.value("s", "i32", 1)
+    g.value("loss", "f32", 1)
+    g.output("loss", build(g), full=False)
+    return Case("dropout", [g], {"x": F(x), "s": s}, {"loss": 1}, ["loss"], closed, dtypes={"s": "i32"})
+
+
 CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, minus_mean, swish, powers,
          clamp_and_max, strided_view_and_index, rounded_counted_tested, column_maxima, row_minima, products,
          softmax_columns, softmax_rows, rank3_softmax, rmsnorm, layer_norm, layer_norm_welford, welford_variance,
@@ -1371,7 +1404,7 @@ CASES = [dot_product, sum_abs2_tanh, full_logsumexp, maximum_and_shifted_sum, mi
          cartesian_diagonal_and_dot, a_scalar_written_into_place, rotation_by_a_constant_permutation,
          concatenations, a_write_at_index_arrays, gather_by_a_traced_vector,
          linear_recurrence_named_with_generic_fold, welford_variance_as_base_spells_it,
-         welford_variance_named_with_generic_fold, circular_shifts_rotations_and_repeats]
+         welford_variance_named_with_generic_fold, circular_shifts_rotations_and_repeats, dropout]
 
 
 # ---- writes where several elements land at one position ---------------------------

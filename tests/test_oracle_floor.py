@@ -38,6 +38,21 @@ def test_repeated_writes_land_in_order(make):
         assert relative(vals[k], np.asarray(want[k], dtype=np.float64)) < 1e-6, (case.name, k)
 
 
+def test_dropout_scale_keeps_its_rate():
+    """The dropout hash's keep scale over 20000 positions: 1 / (1 - rate) or 0,
+    kept with frequency 1 - rate (a flipped comparison keeps `rate`), the
+    same positions for the same seed and different ones for another."""
+    pos = np.arange(1, 20001)
+    for rate in (0.25, 0.5, 0.9):
+        k = FG.dropout_scale(np.full(pos.shape, 7), pos, np.full(pos.shape, rate))
+        assert set(np.unique(k)) <= {0.0, float(np.float32(1) / (np.float32(1) - np.float32(rate)))}
+        assert abs((k > 0).mean() - (1 - rate)) < 0.015, rate
+    a = FG.dropout_scale(np.full(pos.shape, 7), pos, np.full(pos.shape, 0.5))
+    b = FG.dropout_scale(np.full(pos.shape, 8), pos, np.full(pos.shape, 0.5))
+    assert np.array_equal(a, FG.dropout_scale(np.full(pos.shape, 7), pos, np.full(pos.shape, 0.5)))
+    assert 0.4 < ((a > 0) != (b > 0)).mean() < 0.6
+
+
 def test_kat_sum_of_squares_exact():
     # src/Compiler/runtime/compile.jl:35-40: exactly 30.
     assert FC.run_oracle(FC.kat_sum_abs2())["loss"][0] == 30.0
