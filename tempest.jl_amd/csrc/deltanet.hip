@@ -176,8 +176,9 @@ __device__ __forceinline__ f32x4v mma_split(const Split8& a, const Split8& b, f3
 }
 
 // acc[bi][bj] += X(i0 + 16 bi .., k) Y(j0 + 16 bj .., k) over k in [0, K):
-// both operands with k along their rows (row-major in LDS, stride kLd).
-template <int BI, int BJ>
+// both operands with k along their rows (row-major in LDS, stride kLd);
+// kExactX: X's fp32 values are bf16 values (no lo part).
+template <int BI, int BJ, bool kExactX = false>
 __device__ __forceinline__ void mm_nt(f32x4v (&acc)[BI][BJ], const float* X, int i0, const float* Y, int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
   for (int kb = 0; kb < K; kb += 32) {
@@ -185,7 +186,7 @@ __device__ __forceinline__ void mm_nt(f32x4v (&acc)[BI][BJ], const float* X, int
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi) {
       const float* row = X + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
-      a[bi] = split8<false>(quad(row), quad(row + 4));
+      a[bi] = split8<kExactX>(quad(row), quad(row + 4));
     }
 #pragma unroll
     for (int bj = 0; bj < BJ; ++bj) {
@@ -195,7 +196,7 @@ __device__ __forceinline__ void mm_nt(f32x4v (&acc)[BI][BJ], const float* X, int
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi)
 #pragma unroll
-      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma_split<false, false>(a[bi], b[bj], acc[bi][bj]);
+      for (int bj = 0; bj < BJ; ++bj) acc[bi][bj] = mma_split<kExactX, false>(a[bi], b[bj], acc[bi][bj]);
   }
 }
 
@@ -296,6 +297,12 @@ struct ColF32 {  // (x, k) at p[k * ld + x]
   const float* p;
   int ld;
   __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
+};
+struct RowF32Bf {  // (x, k) at p[x * ld + k], fp32 holding bf16 values
+  static constexpr bool kExact = true;
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
 };
 struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
   static constexpr bool kExact = true;
@@ -810,7 +817,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       clear(kd);
       const int i0 = 16 * (w % 4), j0 = 16 * (w / 4);
       mm_gen<true, true>(pd, P, kLdC, i0, dO, kLdS, j0, kC);
-      mm_gen<false, true>(kd, K, kLd, i0, dS, kLdS, j0, kD);
+      mm_by(kd, RowF32Bf{K, kLd}, i0, ColF32{dS, kLdS}, j0, kD);  // K: bf16 values
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = i0 + 4 * g + v;
@@ -877,8 +884,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
 constexpr size_t kGaLds = 2 * kC * kLd * sizeof(float);
 
 // acc1 += X1 Y', acc2 += X2 Y' over k in [0, K): X1, X2 rows i0 .. of LDS
-// (stride kLd), Y rows j0 + 16 bj .. of memory (stride kD), each Y quad read once.
-template <int BI, int BJ>
+// (stride kLd), Y rows j0 + 16 bj .. of memory (stride kD), each Y quad read once;
+// kExact1: X1's fp32 values are bf16 values.
+template <int BI, int BJ, bool kExact1 = false>
 __device__ __forceinline__ void mm_nt2(f32x4v (&acc1)[BI][BJ], const float* X1, f32x4v (&acc2)[BI][BJ], const float* X2,
                                        int i0, const float* Y, int j0, int K) {
   const int r = threadIdx.x % 16, g = (threadIdx.x % 64) / 16;
@@ -893,14 +901,14 @@ __device__ __forceinline__ void mm_nt2(f32x4v (&acc1)[BI][BJ], const float* X1, 
     for (int bi = 0; bi < BI; ++bi) {
       const float* r1 = X1 + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
       const float* r2 = X2 + (i0 + 16 * bi + r) * kLd + kb + 8 * g;
-      a1[bi] = split8<false>(quad(r1), quad(r1 + 4));
+      a1[bi] = split8<kExact1>(quad(r1), quad(r1 + 4));
       a2[bi] = split8<false>(quad(r2), quad(r2 + 4));
     }
 #pragma unroll
     for (int bi = 0; bi < BI; ++bi)
 #pragma unroll
       for (int bj = 0; bj < BJ; ++bj) {
-        acc1[bi][bj] = mma_split<false, false>(a1[bi], b[bj], acc1[bi][bj]);
+        acc1[bi][bj] = mma_split<kExact1, false>(a1[bi], b[bj], acc1[bi][bj]);
         acc2[bi][bj] = mma_split<false, false>(a2[bi], b[bj], acc2[bi][bj]);
       }
   }
@@ -921,7 +929,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
     f32x4v q[4][2], wq[4][2];
     clear(q);
     clear(wq);
-    mm_nt2(q, dO, wq, X, 0, Sc, 32 * w, kD);
+    mm_nt2<4, 2, true>(q, dO, wq, X, 0, Sc, 32 * w, kD);  // dO: bf16 values
     store_blocks(p.dQg + ck.c * kC * kD, kD, q, 0, 32 * w, 1.0f);
     store_blocks(p.dW + ck.c * kC * kD, kD, wq, 0, 32 * w, -1.0f);
   }
@@ -941,7 +949,7 @@ __global__ __launch_bounds__(256, 2) void dn_grad_a(DnArgs p) {
     for (int jb = 0; jb < 4; ++jb) {
       f32x4v acc[1][1];
       clear(acc);
-      if (jb <= w) mm_nt(acc, dO, 16 * w, X, 16 * jb, kD);
+      if (jb <= w) mm_nt<1, 1, true>(acc, dO, 16 * w, X, 16 * jb, kD);  // dO: bf16 values
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = 16 * w + 4 * g + v, j = 16 * jb + r;
