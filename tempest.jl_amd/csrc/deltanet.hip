@@ -304,6 +304,12 @@ struct RowF32Bf {  // (x, k) at p[x * ld + k], fp32 holding bf16 values
   int ld;
   __device__ f32x4v quad(int x, int k) const { return *reinterpret_cast<const f32x4v*>(p + x * ld + k); }
 };
+struct ColF32Bf {  // (x, k) at p[k * ld + x], fp32 holding bf16 values
+  static constexpr bool kExact = true;
+  const float* p;
+  int ld;
+  __device__ f32x4v quad(int x, int k) const { return column_quad(p, ld, k, x); }
+};
 struct RowBf16 {  // (x, k) at bf16 p[x * ld + k]
   static constexpr bool kExact = true;
   const uint16_t* p;
@@ -816,7 +822,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       clear(pd);
       clear(kd);
       const int i0 = 16 * (w % 4), j0 = 16 * (w / 4);
-      mm_gen<true, true>(pd, P, kLdC, i0, dO, kLdS, j0, kC);
+      mm_by(pd, ColF32{P, kLdC}, i0, ColF32Bf{dO, kLdS}, j0, kC);  // dO: bf16 values
       mm_by(kd, RowF32Bf{K, kLd}, i0, ColF32{dS, kLdS}, j0, kD);  // K: bf16 values
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -832,7 +838,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_state_grad(DnArgs p) {
       f32x4v qd[1][2], wu[1][2];
       clear(qd);
       clear(wu);
-      mm_gen<true, true>(qd, Qg, kLd, 16 * w, dO, kLdS, 0, kC);
+      mm_by(qd, ColF32{Qg, kLd}, 16 * w, ColF32Bf{dO, kLdS}, 0, kC);
       mm_gen<true, true>(wu, W, kLd, 16 * w, dU, kLdS, 0, kC);
       const float gl = expf(last);
       float nw[2][4];
