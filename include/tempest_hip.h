@@ -107,6 +107,13 @@ int th_upload(void* dst, const void* host_src, size_t bytes);
 int th_download(void* host_dst, const void* src, size_t bytes);
 int th_copy(void* dst, const void* src, size_t bytes);
 
+/* A device-to-device copy of `bytes` bytes as a launch: run it, record it in
+ * a graph and repoint it as any other (values: 0 dst, 1 src; any alignment).
+ * Replaces the `Copy` step (src/Compiler/runtime/runtime.jl:47-64) where a
+ * target records its steps as one graph (capture, ext/CUDAExt.jl:515-572,
+ * records a copy node for it). */
+int th_build_copy(void* dst, const void* src, uint64_t bytes, th_launch** host_out);
+
 /* The slot arena: `n` slots of `sizes[i]` bytes laid out in one hipMalloc
  * slab, each at a multiple of `align` (>= 256, a power of two).  Replaces the
  * per-slot allocate of `planned`, src/Compiler/runtime/runtime.jl:415, fed by
@@ -125,7 +132,11 @@ int th_arena_destroy(th_arena* arena);
  * as `planned` does (src/Compiler/runtime/runtime.jl:415, allocate(t, T, n)
  * per slot), land in one range.  Replaces allocate(::CUDATarget, T, n),
  * ext/CUDAExt.jl:23, for the slots of an executable.  th_pool_destroy waits
- * for the device and unmaps everything. */
+ * for the device and unmaps everything — at once when no block is taken,
+ * else when th_pool_free returns the last one (no block may be taken after
+ * it), so a host whose collector frees the pool before its buffers (Julia
+ * finalizes objects that die together in no set order) frees no memory
+ * still in use.  The pool calls are safe from several threads. */
 typedef struct th_pool th_pool;
 int th_pool_create(uint64_t reserve, th_pool** host_out);
 int th_pool_alloc(th_pool* pool, uint64_t bytes, uint64_t align, void** host_out);
@@ -285,6 +296,12 @@ int th_build_sum(int64_t count, const float* x, float* out, th_launch** host_out
  * the once outputs after the sweep (scan_kernel, codegen/scalar.jl:350-398). */
 enum { TH_GROUP_POINTWISE = 0, TH_GROUP_REDUCTION = 1, TH_GROUP_SCAN = 2, TH_GROUP_RECURRENCE = 3 };
 #define TH_FLOOR_REVERSE 1
+/* A pointwise group whose items run one after another, in order, on one
+ * thread: a fold by key's elements (accumulating outputs) then add without
+ * atomics, in the items' order, so every run rounds alike (the CPU floor's
+ * order, src/Compiler/codegen/scalar.jl:496-522).  What a deterministic target
+ * (src/Compiler/runtime/target.jl:229-231) asks of a fold by key. */
+#define TH_FLOOR_ORDERED (1 << 16)
 
 /* A recurrence group (recurrence_kernel, codegen/scalar.jl:402-440) steps
  * along one axis, named by the flags (TH_FLOOR_STEP(axis)), a thread per

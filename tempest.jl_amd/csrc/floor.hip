@@ -109,6 +109,7 @@ struct Plan {
   int step = -1;                 // the recurrence's step axis
   bool scan = false;             // a scan group: one thread per item, in order
   bool reverse = false;
+  bool ordered = false;           // one thread takes the items in order (TH_FLOOR_ORDERED)
   std::vector<int> order;        // a scan group's folds in (phase, index) order
   int rank = 1;
   int64_t E[kRank] = {1, 1, 1, 1};
@@ -192,8 +193,9 @@ int validate(const th_floor_desc* d) {
              "th_build_floor: unknown group kind");
   const bool rec = d->kind == TH_GROUP_RECURRENCE;
   TH_REQUIRE(d->flags == 0 || (d->kind == TH_GROUP_SCAN && d->flags == TH_FLOOR_REVERSE) ||
-                 (rec && (d->flags & ~(TH_FLOOR_REVERSE | TH_FLOOR_STEP(7))) == 0),
-             "th_build_floor: only a scan or a recurrence group runs in reverse");
+                 (rec && (d->flags & ~(TH_FLOOR_REVERSE | TH_FLOOR_STEP(7))) == 0) ||
+                 (d->kind == TH_GROUP_POINTWISE && d->flags == TH_FLOOR_ORDERED),
+             "th_build_floor: only a scan or a recurrence group runs in reverse, only a pointwise one in order");
   TH_REQUIRE(d->rank >= 1 && d->rank <= kRank, "th_build_floor: rank must be 1..4");
   for (int k = 0; k < d->rank; ++k) TH_REQUIRE(d->extents[k] >= 0, "th_build_floor: negative extent");
   const uint32_t all = (1u << d->rank) - 1;
@@ -437,7 +439,8 @@ int plan(const th_floor_desc* d, Plan& pl) {
   pl.recurrence = d->kind == TH_GROUP_RECURRENCE;
   pl.step = pl.recurrence ? step_axis(d) : -1;
   pl.scan = d->kind == TH_GROUP_SCAN;
-  pl.reverse = (d->flags & TH_FLOOR_REVERSE) != 0;
+  pl.reverse = (d->flags & TH_FLOOR_REVERSE) != 0 && d->kind != TH_GROUP_POINTWISE;
+  pl.ordered = d->kind == TH_GROUP_POINTWISE && (d->flags & TH_FLOOR_ORDERED) != 0;
   pl.rank = d->rank;
   for (int k = 0; k < d->rank; ++k) pl.E[k] = d->extents[k];
   for (int k = 0; k < d->rank; ++k) ((pl.reduction && (d->reduced >> k & 1)) ? pl.swept : pl.kept).push_back(k);
@@ -615,10 +618,11 @@ int plan(const th_floor_desc* d, Plan& pl) {
     for (int k = 0; k < pl.rank; ++k) pl.kept.push_back(k);
     pl.items = 1;
     for (int k = 0; k < pl.rank; ++k) pl.items *= pl.E[k];
-    pl.W = (pl.E[0] % 4 == 0 && pl.E[0] >= 4 && !pl.gathers) ? 4 : 1;
+    pl.W = (pl.E[0] % 4 == 0 && pl.E[0] >= 4 && !pl.gathers && !pl.ordered) ? 4 : 1;
     pl.vax = pl.W > 1 ? 0 : -1;
     pl.qn = pl.items / pl.W;
-    pl.S = 256;
+    // In order: one wave whose first lane takes every item in turn.
+    pl.S = pl.ordered ? 64 : 256;
     pl.L = 1;
   }
   // Vector accesses: aligned pointer, and every other coefficient and the
@@ -702,6 +706,8 @@ __device__ __forceinline__ long th_clampi(long i, long n) { return i < 0 ? 0 : (
 __device__ __forceinline__ long th_fld(long x, long d) { return x >= 0 ? x / d : -((-x + d - 1) / d); }
 __device__ __forceinline__ long th_fmod(long x, long d) { return x - d * th_fld(x, d); }
 __device__ __forceinline__ void th_add(float* p, long i, float v) { atomicAdd(p + i, v); }
+// In order (one thread): the elements add in the items' order, every run alike.
+__device__ __forceinline__ void th_add_ordered(float* p, long i, float v) { p[i] = p[i] + v; }
 __device__ __forceinline__ float th_abs(float x) { return fabsf(x); }
 __device__ __forceinline__ float th_abs2(float x) { return x * x; }
 __device__ __forceinline__ float th_sqrt(float x) { return sqrtf(x); }
@@ -1458,7 +1464,7 @@ class Writer {
   void store(const std::string& ind, const th_output& x, const std::string& val, bool vec) {
     std::string p = vname(x.value), at = addr(x.index, x.value);
     if (x.accumulate) {  // a fold by key: positions may repeat
-      o_ << ind << "th_add(" << p << ", " << at << ", " << val << ");\n";
+      o_ << ind << (pl_.ordered ? "th_add_ordered(" : "th_add(") << p << ", " << at << ", " << val << ");\n";
       return;
     }
     // Full outputs are written once and not read again here: non-temporal.
@@ -1794,8 +1800,13 @@ class Writer {
   void pointwise(const std::string& name) {
     std::ostringstream& o = o_;
     header(name);
-    o << "  const long lin = (long)blockIdx.x * " << pl_.S << " + threadIdx.x;\n";
-    o << "  if (lin >= " << pl_.qn << "L) return;\n";
+    if (pl_.ordered) {
+      o << "  if (blockIdx.x != 0 || threadIdx.x != 0) return;\n";
+      o << "  for (long lin = 0; lin < " << pl_.qn << "L; ++lin) {\n";
+    } else {
+      o << "  const long lin = (long)blockIdx.x * " << pl_.S << " + threadIdx.x;\n";
+      o << "  if (lin >= " << pl_.qn << "L) return;\n";
+    }
     o << "  {\n    long r = lin;\n";
     for (int k = 0; k < pl_.rank; ++k) {
       int64_t e = k == 0 ? pl_.E[0] / pl_.W : pl_.E[k];
@@ -1809,6 +1820,7 @@ class Writer {
     std::map<int, std::string> names;
     emit("  ", reach(d_, roots), pl_.W > 1, false, names, nullptr);
     for (int x = 0; x < d_->n_outputs; ++x) store("  ", d_->outputs[x], names.at(d_->outputs[x].term), true);
+    if (pl_.ordered) o << "  }\n";
     o << "}\n";
   }
 };
@@ -2060,7 +2072,7 @@ int th_build_floor(const th_floor_desc* desc, th_launch** out) {
                              sizeof(float));
   const size_t arg_bytes = sizeof(void*) * (d->n_values + (pl.reduction ? d->n_folds : 0));
   if (pl.items > 0) {
-    const int64_t blocks = pl.reduction ? (pl.items + pl.S - 1) / pl.S * pl.P : (pl.qn + pl.S - 1) / pl.S;
+    const int64_t blocks = pl.ordered ? 1 : pl.reduction ? (pl.items + pl.S - 1) / pl.S * pl.P : (pl.qn + pl.S - 1) / pl.S;
     TH_REQUIRE(blocks < (int64_t)1 << 31, "th_build_floor: domain too large for one grid");
     for (const Stage& s : c.stages) {
       int k = b.module_kernel(mod->fns.at(s.name), mod->names[&s - &c.stages[0]].c_str(), dim3((unsigned)blocks),

@@ -119,6 +119,29 @@ __global__ __launch_bounds__(256) void th_clear_kernel(ClearArgs c) {
   if (s == 0xffffffffu) c.sink[0] = s;
 }
 
+
+// A copy of `bytes` bytes as a kernel, so that a graph records it beside the
+// launches and retargets it as one (the reference's `Copy` step,
+// src/Compiler/runtime/runtime.jl:47-64).  16-byte words where both ends and
+// the length allow, bytes otherwise: the choice is made per launch from the
+// addresses it holds, so any repointing keeps it correct.
+struct CopyArgs {
+  unsigned char* dst;
+  const unsigned char* src;
+  uint64_t bytes;
+};
+__global__ __launch_bounds__(256) void th_copy_kernel(CopyArgs c) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if ((((uintptr_t)c.dst | (uintptr_t)c.src | c.bytes) & 15) == 0) {
+    u32x4* d = reinterpret_cast<u32x4*>(c.dst);
+    const u32x4* s = reinterpret_cast<const u32x4*>(c.src);
+    for (uint64_t i = t; i < c.bytes / 16; i += stride) d[i] = __builtin_nontemporal_load(s + i);
+  } else {
+    for (uint64_t i = t; i < c.bytes; i += stride) c.dst[i] = c.src[i];
+  }
+}
+
 extern "C" {
 
 const char* th_last_error(void) { return g_error.c_str(); }
@@ -255,6 +278,23 @@ int th_copy(void* dst, const void* src, size_t bytes) {
   return TH_OK;
 }
 
+int th_build_copy(void* dst, const void* src, uint64_t bytes, th_launch** out) {
+  *out = nullptr;
+  TH_REQUIRE(bytes < (uint64_t(1) << 48), "th_build_copy: too many bytes");
+  Builder b("copy", 2);
+  CopyArgs a{static_cast<unsigned char*>(dst), static_cast<const unsigned char*>(src), bytes};
+  const uint64_t words = (bytes + 15) / 16;
+  const unsigned blocks = (unsigned)std::max<uint64_t>(1, std::min<uint64_t>((words + 255) / 256, 4096));
+  int k = b.kernel((const void*)th_copy_kernel, "th_copy_kernel", dim3(blocks), dim3(256), 0, a);
+  b.ref(0, k, TH_OFFSET(CopyArgs, dst));
+  b.ref(1, k, TH_OFFSET(CopyArgs, src));
+  b.align(0, 1);
+  b.align(1, 1);
+  b.work(2.0 * (double)bytes, 0.0, blocks);
+  *out = b.release();
+  return TH_OK;
+}
+
 }  // extern "C"
 
 struct th_arena {
@@ -275,7 +315,31 @@ struct th_pool {
   uint64_t top = 0;          // the end of the highest block taken
   std::vector<std::pair<hipMemGenericAllocationHandle_t, uint64_t>> chunks;
   std::map<uint64_t, uint64_t> free, used;  // offset -> bytes
+  // Destroyed while blocks were still taken: the range is released when the
+  // last of them is freed (a host's collector may free a pool before its
+  // blocks).  Hosts may free from finalizer threads, hence the lock.
+  bool closing = false;
+  std::mutex mu;
 };
+
+// Unmap and free the pool's range, and the pool: once nothing is taken from it.
+static int pool_release(th_pool* p) {
+  // Nothing may still read the pool's memory.
+  TH_HIP(hipDeviceSynchronize());
+  if (p->vmm) {
+    uint64_t off = 0;
+    for (const auto& c : p->chunks) {
+      TH_HIP(hipMemUnmap(static_cast<char*>(p->base) + off, c.second));
+      TH_HIP(hipMemRelease(c.first));
+      off += c.second;
+    }
+    if (p->base) TH_HIP(hipMemAddressFree(p->base, p->reserved));
+  } else if (p->base) {
+    TH_HIP(hipFree(p->base));
+  }
+  delete p;
+  return TH_OK;
+}
 
 extern "C" {
 
@@ -397,6 +461,8 @@ int th_pool_alloc(th_pool* p, uint64_t bytes, uint64_t align, void** out) {
   if (int r = require_ready()) return r;
   TH_REQUIRE(p != nullptr, "th_pool_alloc: null pool");
   *out = nullptr;
+  std::lock_guard<std::mutex> hold(p->mu);
+  TH_REQUIRE(!p->closing, "th_pool_alloc: the pool was destroyed");
   if (align < 256) align = 256;
   TH_REQUIRE((align & (align - 1)) == 0, "th_pool_alloc: alignment must be a power of two");
   bytes = std::max<uint64_t>((bytes + 255) / 256 * 256, 256);
@@ -427,22 +493,27 @@ int th_pool_alloc(th_pool* p, uint64_t bytes, uint64_t align, void** out) {
 int th_pool_free(th_pool* p, void* ptr) {
   TH_REQUIRE(p != nullptr, "th_pool_free: null pool");
   if (!ptr) return TH_OK;
-  const uint64_t at = static_cast<uint64_t>(static_cast<char*>(ptr) - static_cast<char*>(p->base));
-  auto it = p->used.find(at);
-  TH_REQUIRE(ptr >= p->base && it != p->used.end(), "th_pool_free: not a block of this pool");
-  uint64_t lo = at, hi = at + it->second;
-  p->used.erase(it);
-  // Coalesce with the free neighbours; a free block at the top lowers it.
-  auto next = p->free.find(hi);
-  if (next != p->free.end()) hi += next->second, p->free.erase(next);
-  auto prev = p->free.lower_bound(lo);
-  if (prev != p->free.begin()) {
-    --prev;
-    if (prev->first + prev->second == lo) lo = prev->first, p->free.erase(prev);
+  bool last = false;
+  {
+    std::lock_guard<std::mutex> hold(p->mu);
+    const uint64_t at = static_cast<uint64_t>(static_cast<char*>(ptr) - static_cast<char*>(p->base));
+    auto it = p->used.find(at);
+    TH_REQUIRE(ptr >= p->base && it != p->used.end(), "th_pool_free: not a block of this pool");
+    uint64_t lo = at, hi = at + it->second;
+    p->used.erase(it);
+    // Coalesce with the free neighbours; a free block at the top lowers it.
+    auto next = p->free.find(hi);
+    if (next != p->free.end()) hi += next->second, p->free.erase(next);
+    auto prev = p->free.lower_bound(lo);
+    if (prev != p->free.begin()) {
+      --prev;
+      if (prev->first + prev->second == lo) lo = prev->first, p->free.erase(prev);
+    }
+    if (hi == p->top) p->top = lo;
+    else p->free[lo] = hi - lo;
+    last = p->closing && p->used.empty();
   }
-  if (hi == p->top) p->top = lo;
-  else p->free[lo] = hi - lo;
-  return TH_OK;
+  return last ? pool_release(p) : TH_OK;
 }
 
 int th_pool_info(th_pool* p, void** base, uint64_t* reserved, uint64_t* mapped) {
@@ -455,21 +526,14 @@ int th_pool_info(th_pool* p, void** base, uint64_t* reserved, uint64_t* mapped) 
 
 int th_pool_destroy(th_pool* p) {
   if (!p) return TH_OK;
-  // Nothing may still read the pool's memory.
-  TH_HIP(hipDeviceSynchronize());
-  if (p->vmm) {
-    uint64_t off = 0;
-    for (const auto& c : p->chunks) {
-      TH_HIP(hipMemUnmap(static_cast<char*>(p->base) + off, c.second));
-      TH_HIP(hipMemRelease(c.first));
-      off += c.second;
-    }
-    if (p->base) TH_HIP(hipMemAddressFree(p->base, p->reserved));
-  } else if (p->base) {
-    TH_HIP(hipFree(p->base));
+  {
+    std::lock_guard<std::mutex> hold(p->mu);
+    if (p->closing) return TH_OK;
+    p->closing = true;
+    // Blocks still taken keep the range: the last th_pool_free releases it.
+    if (!p->used.empty()) return TH_OK;
   }
-  delete p;
-  return TH_OK;
+  return pool_release(p);
 }
 
 // ---- launches --------------------------------------------------------------

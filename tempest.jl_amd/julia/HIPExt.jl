@@ -14,16 +14,23 @@
 #
 # No Julia toolchain exists where this backend was built, so this file has not
 # been run; tests/test_julia_binding.py checks every `ccall` against the
-# header (symbol, argument count, C types) and every struct mirror against
-# gcc's layout of the header's struct, and the same calls, argument for
-# argument, are exercised by the Python host in tempest.jl_amd/tempest_hip.
+# header (symbol, argument count, C types), every struct mirror against gcc's
+# layout of the header's struct, every method that extends one of Tempest's
+# functions against the reference's methods of it (no ambiguity, not shadowed),
+# the Target protocol against what CUDATarget specialises, and the calls the
+# runtime makes on a slot's storage against the methods here; the same calls,
+# argument for argument, are exercised by the Python host in tempest.jl_amd/tempest_hip.
 module HIPExt
 
 using Tempest
 import Tempest.Compiler: allocate, upload, upload!, download!, bindable, pointable, capture, recapture, retarget!,
-    replay, release, device_name, toolchain, measurable, time_launch, device_rates, quiesce, build_floor
+    replay, release, device_name, toolchain, measurable, time_launch, device_rates, quiesce, build_floor,
+    implementations, numerics, permits_rewrites, rounded_backward, deterministic, product_class,
+    target_for, device_of, default_device, on_device, task_stream
 using Tempest.Compiler.Implement: Library, Template, Binding, Strided, Work
-import Tempest.Compiler.Implement: templates, supports, build, estimate, repoints, repoint!, loaded, in_place
+import Tempest.Compiler.Implement: templates, supports, build, estimate, repoints, repoint!, loaded, in_place, package_of
+
+const C = Tempest.Compiler
 
 const LIB = get(ENV, "TEMPEST_HIP_LIBRARY", joinpath(@__DIR__, "..", "libtempest_hip.so"))
 
@@ -33,58 +40,219 @@ function check(status::Cint, what)
     throw(ErrorException("$what failed ($status): $msg"))
 end
 
+# ---- device storage -----------------------------------------------------------------
+
+"""
+    HIPPool(device, reserve)
+
+One reserved range of `reserve` bytes of device addresses (th_pool_create):
+`planned` allocates a slot at a time (runtime.jl:415), and every slot of
+every executable lands in that range.  Every buffer taken from it holds it;
+the library releases the range when the pool is destroyed and its last block
+is freed, in whichever order the collector finalizes them.
+"""
+mutable struct HIPPool
+    handle::Ptr{Cvoid}
+    device::Int
+    function HIPPool(device::Integer, reserve::Integer)
+        check(ccall((:th_init, LIB), Cint, (Cint,), device), "th_init")
+        out = Ref{Ptr{Cvoid}}()
+        check(ccall((:th_pool_create, LIB), Cint, (UInt64, Ptr{Ptr{Cvoid}}), reserve, out), "th_pool_create")
+        finalizer(p -> ccall((:th_pool_destroy, LIB), Cint, (Ptr{Cvoid},), p.handle), new(out[], Int(device)))
+    end
+end
+
+"""
+    HIPBuffer{T}(pool, n)
+
+`n` elements of `T` on the device, a block of `pool`: a dense vector whose
+`pointer` is the device address, as `planned` makes a slot (`allocate`) and
+views it (`slot_view(slot, T, n) = reinterpret(T, view(slot, 1:n*sizeof(T)))`,
+runtime.jl:605).  Elements read and written one at a time are copied one at a
+time; `copyto!` between device arrays, and between them and `Array`s, copies
+in one piece.
+"""
+mutable struct HIPBuffer{T} <: DenseVector{T}
+    ptr::Ptr{T}
+    n::Int
+    pool::HIPPool
+    function HIPBuffer{T}(pool::HIPPool, n::Integer) where {T}
+        isbitstype(T) && sizeof(T) > 0 || throw(ArgumentError("a device buffer holds bits types, not $T"))
+        out = Ref{Ptr{Cvoid}}()
+        check(ccall((:th_pool_alloc, LIB), Cint, (Ptr{Cvoid}, UInt64, UInt64, Ptr{Ptr{Cvoid}}),
+            pool.handle, max(n, 1) * sizeof(T), 256, out), "th_pool_alloc")
+        b = new{T}(Ptr{T}(out[]), Int(n), pool)
+        finalizer(x -> ccall((:th_pool_free, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}), x.pool.handle, x.ptr), b)
+    end
+end
+
+Base.size(b::HIPBuffer) = (b.n,)
+Base.length(b::HIPBuffer) = b.n
+Base.IndexStyle(::Type{<:HIPBuffer}) = IndexLinear()
+Base.elsize(::Type{<:HIPBuffer{T}}) where {T} = sizeof(T)
+Base.sizeof(b::HIPBuffer{T}) where {T} = b.n * sizeof(T)
+Base.pointer(b::HIPBuffer) = b.ptr
+Base.pointer(b::HIPBuffer{T}, i::Integer) where {T} = b.ptr + (i - 1) * sizeof(T)
+Base.unsafe_convert(::Type{Ptr{T}}, b::HIPBuffer{T}) where {T} = b.ptr
+Base.similar(b::HIPBuffer, ::Type{T}, dims::Dims) where {T} =
+    length(dims) == 1 ? HIPBuffer{T}(b.pool, dims[1]) : reshape(HIPBuffer{T}(b.pool, prod(dims)), dims)
+
+function Base.getindex(b::HIPBuffer{T}, i::Int) where {T}
+    @boundscheck checkbounds(b, i)
+    x = Ref{T}()
+    check(ccall((:th_download, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t), x, pointer(b, i), sizeof(T)), "th_download")
+    x[]
+end
+
+function Base.setindex!(b::HIPBuffer{T}, v, i::Int) where {T}
+    @boundscheck checkbounds(b, i)
+    x = Ref{T}(convert(T, v))
+    check(ccall((:th_upload, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t), pointer(b, i), x, sizeof(T)), "th_upload")
+    b
+end
+
+# The forms a slot's storage takes in Tempest's runtime, each contiguous on
+# the device: a buffer, a range of one, a reinterpretation of either (a slot's
+# value, runtime.jl:605), and any of those reshaped (a result, runtime.jl:524).
+const HIPSub{T} = SubArray{T, 1, <:HIPBuffer, <:Tuple{AbstractUnitRange}, true}
+const HIPSlot{T} = Union{HIPBuffer{T}, HIPSub{T}, Base.ReinterpretArray{T, 1, <:Any, <:Union{HIPBuffer, HIPSub}}}
+const HIPDense{T} = Union{HIPSlot{T}, Base.ReshapedArray{T, <:Any, <:HIPSlot}}
+
+Base.pointer(x::HIPSub{T}) where {T} = pointer(parent(x)) + (first(only(parentindices(x))) - 1) * sizeof(T)
+Base.pointer(x::Base.ReinterpretArray{T, 1, <:Any, <:Union{HIPBuffer, HIPSub}}) where {T} = Ptr{T}(pointer(parent(x)))
+Base.pointer(x::Base.ReshapedArray{T, <:Any, <:HIPSlot}) where {T} = Ptr{T}(pointer(parent(x)))
+
+# The pool a device array's storage was taken from.
+pool_of(b::HIPBuffer) = b.pool
+pool_of(x::HIPDense) = pool_of(parent(x))
+
+device_address(x) = Ptr{Cvoid}(pointer(x))
+bytes_of(x) = length(x) * sizeof(eltype(x))
+
+function device_copy!(to::Ptr{Cvoid}, from::Ptr{Cvoid}, bytes)
+    check(ccall((:th_copy, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t), to, from, bytes), "th_copy")
+end
+
+# Element ranges checked as Base's copyto! checks them; the copies run on the
+# library's stream, in order with its launches (th_copy, th_upload, th_download).
+function copy_span(dest, doff, src, soff, n)
+    n >= 0 || throw(ArgumentError("tried to copy n=$n elements, but n should be nonnegative"))
+    n == 0 && return false
+    checkbounds(dest, doff:(doff + n - 1))
+    checkbounds(src, soff:(soff + n - 1))
+    true
+end
+
+function Base.copyto!(dest::HIPDense{T}, doff::Integer, src::HIPDense{T}, soff::Integer, n::Integer) where {T}
+    copy_span(dest, doff, src, soff, n) &&
+        device_copy!(device_address(dest) + (doff - 1) * sizeof(T), device_address(src) + (soff - 1) * sizeof(T), n * sizeof(T))
+    dest
+end
+
+function Base.copyto!(dest::Array{T}, doff::Integer, src::HIPDense{T}, soff::Integer, n::Integer) where {T}
+    copy_span(dest, doff, src, soff, n) &&
+        check(ccall((:th_download, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
+            pointer(dest, doff), device_address(src) + (soff - 1) * sizeof(T), n * sizeof(T)), "th_download")
+    dest
+end
+
+function Base.copyto!(dest::HIPDense{T}, doff::Integer, src::Array{T}, soff::Integer, n::Integer) where {T}
+    copy_span(dest, doff, src, soff, n) &&
+        check(ccall((:th_upload, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t),
+            device_address(dest) + (doff - 1) * sizeof(T), pointer(src, soff), n * sizeof(T)), "th_upload")
+    dest
+end
+
+function whole(dest, src)
+    length(dest) >= length(src) || throw(BoundsError(dest, eachindex(src)))
+    length(src)
+end
+Base.copyto!(dest::HIPDense{T}, src::HIPDense{T}) where {T} = copyto!(dest, 1, src, 1, whole(dest, src))
+Base.copyto!(dest::Array{T}, src::HIPDense{T}) where {T} = copyto!(dest, 1, src, 1, whole(dest, src))
+Base.copyto!(dest::HIPDense{T}, src::Array{T}) where {T} = copyto!(dest, 1, src, 1, whole(dest, src))
+
 # ---- the target ---------------------------------------------------------------------
 
 """
-    HIPTarget(implementations...; device = 0, reserve = 64 << 30, deterministic = true)
+    HIPTarget(implementations...; device = 0, reserve = 64 << 30, deterministic = false)
 
 One MI355X.  Its slots come from one reserved range of `reserve` bytes of
-device addresses (th_pool_create): `planned` allocates a slot at a time
-(runtime.jl:415), and every slot of every executable lands in that range.
-`deterministic = false` is the reference's default (runtime/target.jl:31);
-every kernel here is deterministic either way.
+device addresses (`HIPPool`).  `implementations` are the libraries it offers
+the cover, tried in order beside the floor; by default all of this
+extension's.  `deterministic = true` keeps every sum's rounding independent
+of the order blocks run in (target.jl:229-231): the floor's folds by key then
+add their elements one at a time in the order of the items instead of by
+atomics, the one place this backend's sums depend on that order; every other
+kernel here folds in a fixed order either way.  `false` is the reference's
+default (target.jl:31).
 """
-mutable struct HIPTarget <: Tempest.Compiler.Target
+mutable struct HIPTarget <: C.Target
     implementations::Tuple
     device::Int
-    pool::Ptr{Cvoid}
+    pool::HIPPool
     deterministic::Bool
+    # The one inner constructor, so that Julia makes no field-by-field ones
+    # that a call with four implementations would reach.
+    HIPTarget(::Val{:fields}, implementations::Tuple, device::Int, pool::HIPPool, deterministic::Bool) =
+        new(implementations, device, pool, deterministic)
 end
 
-function HIPTarget(implementations...; device::Integer = 0, reserve::Integer = 64 << 30, deterministic::Bool = true)
-    check(ccall((:th_init, LIB), Cint, (Cint,), device), "th_init")
-    pool = Ref{Ptr{Cvoid}}()
-    check(ccall((:th_pool_create, LIB), Cint, (UInt64, Ptr{Ptr{Cvoid}}), reserve, pool), "th_pool_create")
-    t = HIPTarget(implementations, device, pool[], deterministic)
-    finalizer(x -> ccall((:th_pool_destroy, LIB), Cint, (Ptr{Cvoid},), x.pool), t)
-end
+HIPTarget(implementations...; device::Integer = 0, reserve::Integer = 64 << 30, deterministic::Bool = false) =
+    HIPTarget(Val(:fields), isempty(implementations) ? default_implementations() : implementations, Int(device),
+        HIPPool(device, reserve), deterministic)
 
-"A block of the target's pool: its address and elements, given back when collected."
-mutable struct HIPBuffer{T}
-    ptr::Ptr{Cvoid}
-    n::Int
-    pool::Ptr{Cvoid}
-    function HIPBuffer{T}(pool::Ptr{Cvoid}, n::Integer) where {T}
-        out = Ref{Ptr{Cvoid}}()
-        check(ccall((:th_pool_alloc, LIB), Cint, (Ptr{Cvoid}, UInt64, UInt64, Ptr{Ptr{Cvoid}}), pool, n * sizeof(T), 256, out),
-            "th_pool_alloc")
-        b = new{T}(out[], n, pool)
-        finalizer(x -> ccall((:th_pool_free, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}), x.pool, x.ptr), b)
-    end
+# A target over an existing pool: what `target_for` gives for its buffers.
+HIPTarget(pool::HIPPool; deterministic::Bool = false) =
+    HIPTarget(Val(:fields), default_implementations(), pool.device, pool, deterministic)
+
+default_implementations() = (HIPProducts(), HIPEpilogues(), HIPAttention(), HIPRows(), HIPDeltaNet())
+
+Base.show(io::IO, t::HIPTarget) = print(io, "HIPTarget(", join(map(repr, t.implementations), ", "), "; device = ", t.device,
+    t.deterministic ? ", deterministic = true" : "", ")")
+
+# The options the compiler reads (target.jl:79-83,216-231; cover/cost.jl:132).
+implementations(t::HIPTarget) = t.implementations
+numerics(t::HIPTarget) = t.deterministic ? Symbol("full-deterministic") : :full
+# The row kernels and attention fold exponentials online, as the rewrite does.
+permits_rewrites(::HIPTarget) = true
+# The attention backward reads the forward's output as it was rounded to bf16.
+rounded_backward(::HIPTarget) = true
+deterministic(t::HIPTarget) = t.deterministic
+# Half-precision products run as themselves, Float32 ones in full precision.
+product_class(::HIPTarget, T) = T === Float16 || T === Tempest.BFloat16 ? nameof(T) : :full
+
+# Arrays and devices (target.jl:94-124,129-175).  One device per process: the
+# library drives the device its first `th_init` named.
+target_for(x::HIPDense) = HIPTarget(pool_of(x))
+device_of(x::HIPDense) = pool_of(x).device
+device_of(t::HIPTarget) = t.device
+default_device(t::HIPTarget) = t.device
+function on_device(f, t::HIPTarget, device::Int)
+    device == t.device || throw(ArgumentError("libtempest_hip drives device $(t.device), not $device"))
+    f()
 end
-Base.length(b::HIPBuffer) = b.n
-Base.eltype(::HIPBuffer{T}) where {T} = T
-Base.pointer(b::HIPBuffer) = b.ptr
 
 allocate(t::HIPTarget, T, n) = HIPBuffer{T}(t.pool, n)
-upload(t::HIPTarget, x::Array) = upload!(t, allocate(t, eltype(x), length(x)), x)
-upload!(::HIPTarget, b::HIPBuffer, x::Array) =
-    (check(ccall((:th_upload, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t), b.ptr, x, sizeof(x)), "th_upload"); b)
-download!(::HIPTarget, x::Array, b::HIPBuffer) =
-    (check(ccall((:th_download, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, Csize_t), x, b.ptr, sizeof(x)), "th_download"); x)
-bindable(::HIPTarget, x) = x isa HIPBuffer
-pointable(::HIPTarget, x, at) = x isa HIPBuffer && at % 16 == 0
+upload(t::HIPTarget, x) = upload!(t, allocate(t, eltype(x), length(x)), x)
+# An array on the host other than an `Array` goes through one (as CUDA's
+# target does, ext/CUDAExt.jl:33-36).
+upload!(::HIPTarget, buffer, x) = copyto!(buffer, x isa Union{Array, HIPDense} ? vec(x) : vec(Array(x)))
+download!(::HIPTarget, x, buffer) =
+    x isa Union{Array, HIPDense} ? copyto!(x, buffer) : copyto!(x, reshape(copyto!(Array{eltype(buffer)}(undef, length(buffer)), buffer), size(x)))
+bindable(::HIPTarget, x) = x isa HIPDense
+# Kernels assume at most 16-byte alignment of what they are built on (th_launch_repoint checks it).
+pointable(::HIPTarget, x, at) = x isa HIPDense && at % 16 == 0
 quiesce(::HIPTarget) = check(ccall((:th_quiesce, LIB), Cint, ()), "th_quiesce")
+# Every launch, copy and replay of the library goes to one stream: a task's
+# stream is that one (ext/CUDAExt.jl:331-345 keeps CUDA's task streams).
+function task_stream(::HIPTarget)
+    s = Ref{Ptr{Cvoid}}()
+    check(ccall((:th_get_stream, LIB), Cint, (Ptr{Ptr{Cvoid}},), s), "th_get_stream")
+    s[]
+end
+quiesce(t::HIPTarget, ::Ptr{Cvoid}) = quiesce(t)
+
+# ---- launches -----------------------------------------------------------------------
 
 """
 One claim's launch: a th_launch*, the buffers it reads (kept alive), and
@@ -96,18 +264,18 @@ mutable struct HIPLaunch
     handle::Ptr{Cvoid}
     buffers::Vector{Any}
     operands::Vector{Tuple{Int, Int, Int, DataType}}
-    function HIPLaunch(h, buffers, operands = Tuple{Int, Int, Int, DataType}[], pool::Ptr{Cvoid} = C_NULL)
+    function HIPLaunch(h, buffers, operands = Tuple{Int, Int, Int, DataType}[], pool::Union{Nothing, HIPPool} = nothing)
         l = new(h, buffers, operands)
         finalizer(x -> ccall((:th_launch_destroy, LIB), Cint, (Ptr{Cvoid},), x.handle), l)
         # Its workspace (partial sums, stored dS', ...) from the target's pool,
         # beside the slots, as the reference's floor takes its workspaces from
         # the target (runtime.jl:1326-1327); without a pool, allocated at the first run.
-        if pool != C_NULL
+        if pool !== nothing
             n = Ref{UInt64}(0)
             check(ccall((:th_launch_workspace, LIB), Cint, (Ptr{Cvoid}, Ptr{UInt64}), h, n), "th_launch_workspace")
             if n[] > 0
                 ws = HIPBuffer{UInt8}(pool, n[])
-                check(ccall((:th_launch_set_workspace, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}), h, ws.ptr),
+                check(ccall((:th_launch_set_workspace, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}), h, pointer(ws)),
                       "th_launch_set_workspace")
                 push!(l.buffers, ws)
             end
@@ -117,11 +285,13 @@ mutable struct HIPLaunch
 end
 (l::HIPLaunch)() = check(ccall((:th_launch_run, LIB), Cint, (Ptr{Cvoid},), l.handle), "th_launch_run")
 repoints(::HIPLaunch) = true
-function repoint!(l::HIPLaunch, value, buffer::HIPBuffer)
+# `buffer` is any storage the runtime hands over: a buffer, a slot's view of
+# one, the caller's array (runtime.jl:1091-1092,1130-1131).
+function repoint!(l::HIPLaunch, value, buffer)
     for (v, i, offset, T) in l.operands
         v == value || continue
-        check(ccall((:th_launch_repoint, LIB), Cint, (Ptr{Cvoid}, Cint, Ptr{Cvoid}), l.handle, i, buffer.ptr + offset * sizeof(T)),
-            "th_launch_repoint")
+        check(ccall((:th_launch_repoint, LIB), Cint, (Ptr{Cvoid}, Cint, Ptr{Cvoid}), l.handle, i,
+            device_address(buffer) + offset * sizeof(T)), "th_launch_repoint")
     end
     l
 end
@@ -138,24 +308,61 @@ struct HIPFloorRun
 end
 (r::HIPFloorRun)() = foreach(l -> l(), r.launches)
 repoints(::HIPFloorRun) = true
-repoint!(r::HIPFloorRun, value, buffer::HIPBuffer) = (foreach(l -> repoint!(l, value, buffer), r.launches); r)
+repoint!(r::HIPFloorRun, value, buffer) = (foreach(l -> repoint!(l, value, buffer), r.launches); r)
 
-"A captured run of steps: a th_graph* and the launches it keeps."
+# ---- graphs -------------------------------------------------------------------------
+
+"""
+The copy a `Copy` step makes (runtime.jl:47-64), as a launch a graph records:
+`length(c.to)` elements from `c.from` after its first `c.offset`.  Pointed
+again at wherever the step's buffers are now, after the runtime repoints the
+step (`point_copy!`).
+"""
+function copy_launch(c::C.Copy)
+    out = Ref{Ptr{Cvoid}}()
+    check(ccall((:th_build_copy, LIB), Cint, (Ptr{Cvoid}, Ptr{Cvoid}, UInt64, Ptr{Ptr{Cvoid}}),
+        device_address(c.to), device_address(c.from) + c.offset * sizeof(eltype(c.from)), bytes_of(c.to), out), "th_build_copy")
+    HIPLaunch(out[], Any[c.to, c.from])
+end
+
+function point_copy!(l::HIPLaunch, c::C.Copy)
+    check(ccall((:th_launch_repoint, LIB), Cint, (Ptr{Cvoid}, Cint, Ptr{Cvoid}), l.handle, 0, device_address(c.to)),
+        "th_launch_repoint")
+    check(ccall((:th_launch_repoint, LIB), Cint, (Ptr{Cvoid}, Cint, Ptr{Cvoid}), l.handle, 1,
+        device_address(c.from) + c.offset * sizeof(eltype(c.from))), "th_launch_repoint")
+    l.buffers = Any[c.to, c.from]
+    l
+end
+
+# The launches a step's run records as graph nodes, in order; nothing for a
+# run this target cannot record (a recurrence stepped, runtime/stepped.jl),
+# whose capture then replays the runs themselves.
+recorded(run::HIPLaunch) = HIPLaunch[run]
+recorded(run::HIPFloorRun) = run.launches
+recorded(run::C.Copy) = bytes_of(run.to) > 0 ? HIPLaunch[copy_launch(run)] : HIPLaunch[]
+recorded(run) = nothing
+
+"""
+A captured run of steps: a th_graph*, each step's run as captured, its
+launches in the graph and where they start among the graph's (th_graph_retarget
+numbers launches from 0, in capture order), and what the graph keeps alive.
+"""
 mutable struct HIPGraph
     handle::Ptr{Cvoid}
+    runs::Vector{Any}
+    launches::Vector{Vector{HIPLaunch}}
+    first::Vector{Int}
     keep::Any
 end
 
-launches_of(run::HIPLaunch) = (run,)
-launches_of(run::HIPFloorRun) = run.launches
-
 """
-Steps that replay faster launched one by one than as one graph: a recording
-of the launches themselves, which carry their own repointed arguments (as the
-reference's target records a run of crossings, ext/CUDAExt.jl:561-566).
+Steps that replay faster launched one by one than as one graph, or that this
+target cannot record: the steps' runs themselves, in order, each reading
+where its launches read (as the reference's target records a run of
+crossings, ext/CUDAExt.jl:561-566).
 """
 struct HIPDirect
-    launches::Vector{HIPLaunch}
+    runs::Vector{Any}
     keep::Any
 end
 
@@ -168,34 +375,48 @@ function graph_pays(kernels)
     base[] + kernels * gap[] < kernels * direct[]
 end
 
+# `steps` are `Scheduled` steps of one stream (schedule.jl:120-126): on one
+# device their waits and signals order nothing beyond the stream's own order.
 function capture(::HIPTarget, steps, keep)
-    launches = HIPLaunch[l for s in steps for l in launches_of(s.step.run)]
-    graph_pays(sum(l -> launch_work(l).kernels, launches; init = 0)) || return HIPDirect(launches, keep)
-    handles = Ptr{Cvoid}[l.handle for l in launches]
+    runs = Any[s.step.run for s in steps]
+    launches = map(recorded, runs)
+    any(isnothing, launches) && return HIPDirect(runs, keep)
+    all_launches = reduce(vcat, launches; init = HIPLaunch[])
+    graph_pays(sum(l -> launch_work(l).kernels, all_launches; init = 0)) || return HIPDirect(runs, keep)
+    handles = Ptr{Cvoid}[l.handle for l in all_launches]
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_graph_capture, LIB), Cint, (Ptr{Ptr{Cvoid}}, Cint, Ptr{Ptr{Cvoid}}), handles, length(handles), out),
         "th_graph_capture")
-    HIPGraph(out[], keep)
+    first = cumsum([0; length.(launches)])[1:end - 1]
+    HIPGraph(out[], runs, launches, first, keep)
 end
 recapture(t::HIPTarget, g::Union{HIPGraph, HIPDirect}, steps, keep) = (release(t, g); capture(t, steps, keep))
 replay(::HIPTarget, g::HIPGraph) = check(ccall((:th_graph_replay, LIB), Cint, (Ptr{Cvoid},), g.handle), "th_graph_replay")
-replay(::HIPTarget, d::HIPDirect) = foreach(l -> l(), d.launches)
+replay(::HIPTarget, d::HIPDirect) = foreach(run -> run(), d.runs)
 release(::HIPTarget, g::HIPGraph) =
     (g.handle == C_NULL || ccall((:th_graph_release, LIB), Cint, (Ptr{Cvoid},), g.handle); g.handle = C_NULL; nothing)
 release(::HIPTarget, ::HIPDirect) = nothing
 
-# Our kernels' argument layouts are known: the launches are repointed, then
-# their graph nodes take their arguments in place; nothing is learned or
-# re-recorded (ext/CUDAExt.jl:604-668 learns them).
+# `steps` are the moved steps' positions among those `capture` took
+# (runtime.jl:1127: `[last(r.at[j]) for j in at]`).  Our kernels' argument
+# layouts are known: the launches are repointed, then exactly their graph
+# nodes take their arguments in place; nothing is learned or re-recorded
+# (ext/CUDAExt.jl:614-668 learns them).  A recording of the runs reads where
+# its runs read: true (target.jl:526-528).
 retarget!(::HIPTarget, ::HIPDirect, steps, moves, repoint) = (repoint(); true)
 function retarget!(::HIPTarget, g::HIPGraph, steps, moves, repoint)
     repoint()
-    n = sum(s -> length(launches_of(s.step.run)), steps; init = 0)
-    for i in 1:n
-        check(ccall((:th_graph_retarget, LIB), Cint, (Ptr{Cvoid}, Cint), g.handle, i - 1), "th_graph_retarget")
+    for s in steps
+        run = g.runs[s]
+        run isa C.Copy && foreach(l -> point_copy!(l, run), g.launches[s])
+        for j in 0:(length(g.launches[s]) - 1)
+            check(ccall((:th_graph_retarget, LIB), Cint, (Ptr{Cvoid}, Cint), g.handle, g.first[s] + j), "th_graph_retarget")
+        end
     end
     true
 end
+
+# ---- measuring ----------------------------------------------------------------------
 
 function device_name(::HIPTarget)
     buf = Vector{UInt8}(undef, 512)
@@ -254,7 +475,7 @@ function describe(l::HIPLaunch)
     unsafe_string(pointer(buf))
 end
 
-address(s::Strided) = pointer(s.buffer) + s.offset * sizeof(s.eltype)
+address(s::Strided) = device_address(s.buffer) + s.offset * sizeof(s.eltype)
 address_or_null(s) = s === nothing ? C_NULL : address(s)
 
 # ---- products (the templates of cuBLASProducts, ext/cuBLASExt.jl:23-36) ----------------
@@ -262,7 +483,6 @@ address_or_null(s) = s === nothing ? C_NULL : address(s)
 struct HIPProducts <: Library end
 loaded(::Type{HIPProducts}) = true
 
-const C = Tempest.Compiler
 product(A, B) = C.contract(A, B, (1, 3, 4), (3, 2, 4), (1, 2, 4))
 widened(A, B) = product(Float32.(A), Float32.(B))
 accumulated(A, B, D) = D .+ product(A, B)
@@ -415,6 +635,9 @@ function epilogue_desc(b::Binding; buffers = true)
 end
 
 supports(::HIPEpilogues, ::HIPTarget, b::Binding) = epilogue_desc(b; buffers = false) !== nothing
+
+estimate(::HIPEpilogues, b::Binding, target, g) =
+    [Work(g.bytes; flops = 2.0 * b.extents.m * b.extents.n * b.extents.k, factor = b.arrays.W.eltype)]
 
 function build(::HIPEpilogues, t::HIPTarget, b::Binding, resources)
     d = Ref(epilogue_desc(b))
@@ -648,6 +871,14 @@ function supports(::HIPDeltaNet, ::HIPTarget, b::Binding)
         all(s -> s.eltype === Float32 && s.strides == a.a.strides, (a.a, a.beta))
 end
 
+# The chunked form's products (examples/deltanet.jl:58-86), chunk 64, d = 128:
+# per chunk about 12.9 Mflop forward, three times that with the gradient.
+function estimate(::HIPDeltaNet, b::Binding, target, g)
+    e = b.extents
+    chunks = e.h * e.b * (e.t ÷ 64)
+    [Work(g.bytes; flops = chunks * 12.9e6 * (b.template == 2 ? 3.0 : 1.0), factor = Float32)]
+end
+
 function build(::HIPDeltaNet, t::HIPTarget, b::Binding, resources)
     a, e = b.arrays, b.extents
     grad = b.template == 2
@@ -704,6 +935,7 @@ end
 
 const GROUP_POINTWISE, GROUP_REDUCTION, GROUP_SCAN, GROUP_RECURRENCE = Int32(0), Int32(1), Int32(2), Int32(3)
 const STEP_EACH, STEP_FIRST, STEP_LAST, STEP_CARRY = Int32(0), Int32(1), Int32(2), Int32(3)
+const FLOOR_ORDERED = Int32(1 << 16)
 
 const FLOOR_FN = IdDict{Any, Int32}(+ => 0, - => 1, * => 2, / => 3, abs => 5, abs2 => 6, sqrt => 7, exp => 8,
     log => 9, tanh => 10, sin => 11, cos => 12, log1p => 13, expm1 => 14, (^) => 15, max => 16, min => 17,
@@ -825,7 +1057,7 @@ value_code(T) = T === Float32 ? 0 : T === Tempest.BFloat16 ? 1 : T === Int32 ? 2
 function floor_values(b::FloorBuilder, buffers)
     C_ = Tempest.Compiler
     [FloorValue(value_code(b.graph.values[v].eltype), 0, C_.storage_length(b.graph.values[v]),
-                pointer(buffers[i])) for (i, v) in enumerate(b.slots)]
+                device_address(buffers[i])) for (i, v) in enumerate(b.slots)]
 end
 
 function floor_desc(kind, domain, reduced, flags, vals, terms, folds, outs)
@@ -834,7 +1066,7 @@ function floor_desc(kind, domain, reduced, flags, vals, terms, folds, outs)
               pointer(vals), pointer(terms), isempty(folds) ? C_NULL : pointer(folds), pointer(outs))
 end
 
-function floor_launch(kind, domain, reduced, flags, vals, terms, folds, outs, keep, operands, pool = C_NULL)
+function floor_launch(kind, domain, reduced, flags, vals, terms, folds, outs, keep, operands, pool = nothing)
     out = Ref{Ptr{Cvoid}}()
     GC.@preserve vals terms folds outs begin
         d = Ref(floor_desc(kind, domain, reduced, flags, vals, terms, folds, outs))
@@ -890,8 +1122,10 @@ end
 # A fold by key's two launches (keyed_kernels, codegen/scalar.jl:496-522):
 # its storage set to the contents it starts from or the fold's initial state
 # (unless `held` already), then each element added (SumFold, by atomics) or
-# written (Overwrite) at the position its key names.
-function keyed_launches(graph, g, r, held, slots, buffers, operands)
+# written (Overwrite) at the position its key names.  `ordered`, for a
+# deterministic target, takes the elements one after another in the items'
+# order (TH_FLOOR_ORDERED): no atomics, every run rounds alike.
+function keyed_launches(graph, g, r, held, slots, buffers, operands, ordered, pool)
     C_, IR = Tempest.Compiler, Tempest.Compiler.IR
     val = graph.values[r]
     d = val.definition
@@ -905,29 +1139,42 @@ function keyed_launches(graph, g, r, held, slots, buffers, operands)
         start = d.into === nothing ? add!(b0, IR.Lit(0.0f0)) : add!(b0, C_.stored_term(d.into))
         outs = [COutput(slot(b0, r), start, 1, 0, caffine(C_.address(val, C_.identity_index(val.dims), C_.Domain(val.dims)), gathered0))]
         push!(launches, floor_launch(GROUP_POINTWISE, val.dims, UInt32(0), Int32(0), floor_values(b0, buffers), b0.terms,
-                                     b0.folds, outs, keep, operands))
+                                     b0.folds, outs, keep, operands, pool))
     end
     b = FloorBuilder(graph, g, slots, g.domain)
     gathered(a) = add!(b, IR.Load(a.value, a.index))
     t = add!(b, C_.stored_statistics(g.terms[r], graph, g))
     at = caffine(C_.address(val, C_.placement(graph, g, r), C_.Domain(g.domain)), gathered)
     outs = [COutput(slot(b, r), t, 1, fold isa IR.SumFold ? 1 : 0, at)]
-    push!(launches, floor_launch(GROUP_POINTWISE, g.domain, UInt32(0), Int32(0), floor_values(b, buffers), b.terms, b.folds,
-                                 outs, keep, operands))
+    push!(launches, floor_launch(GROUP_POINTWISE, g.domain, UInt32(0), ordered ? FLOOR_ORDERED : Int32(0),
+                                 floor_values(b, buffers), b.terms, b.folds, outs, keep, operands, pool))
     launches
 end
 
-function build_floor(target::HIPTarget, p, g, buffers)
+# The floor for a group on this target, in place of the generic one
+# (runtime.jl:1323-1335), whose kernels are Julia functions: the group's
+# terms go to the library, which writes and compiles the kernel.  What the
+# floor stores that the plan does not is kept in storage of its own, taken
+# from the target's pool and held by the run, as the generic floor keeps it.
+function build_floor(target::HIPTarget, p::C.Plan, g::C.Group, buffers)
     C_, IR = Tempest.Compiler, Tempest.Compiler.IR
     graph = p.graph
     stored = C_.floor_stored(p, g)
     slots = C_.kernel_slots(p, g, stored)
-    bufs = [buffers[v] for v in slots]
+    own = Any[]
+    function buffer(v)
+        (buffers[v] !== nothing || p.stored[v]) && return buffers[v]
+        b = allocate(target, graph.values[v].eltype, C_.storage_length(graph.values[v]))
+        push!(own, b)
+        b
+    end
+    bufs = Any[buffer(v) for v in slots]
     operands = Tuple{Int, Int, Int, DataType}[(v, i - 1, 0, UInt8) for (i, v) in enumerate(slots)]
     launches = HIPLaunch[]
     keyed = filter(r -> C_.keyed(graph, r), g.reductions)
     for r in keyed
-        append!(launches, keyed_launches(graph, g, r, C_.starts_in_place(graph, r, buffers), slots, bufs, operands))
+        append!(launches, keyed_launches(graph, g, r, C_.starts_in_place(graph, r, buffers), slots, bufs, operands,
+                                         deterministic(target), target.pool))
     end
     folds_in_place = [r for r in g.reductions if !(r in keyed)]
     if !isempty(folds_in_place) || g.kind isa C_.PointwiseKind || g.kind isa C_.RecurrenceKind
@@ -963,8 +1210,16 @@ function build_floor(target::HIPTarget, p, g, buffers)
         push!(launches, floor_launch(kind, g.domain, reduced, flags, floor_values(b, bufs), terms, folds, outs, Any[bufs...],
                                      operands, target.pool))
     end
+    foreach(l -> append!(l.buffers, own), launches)
     run = HIPFloorRun(launches)
     (run, "HIP floor: " * join(map(describe, launches), "; "))
 end
+
+# The package the rates file keeps these libraries' lines under
+# (tempest.jl_amd/rates/AMD_Instinct_MI355X.cold.rates.tsv: `HIP ...`), as
+# Tempest's own libraries name theirs (Implement/packages.jl:42-44); by
+# default it would be this module's name.
+const HIPLibrary = Union{HIPProducts, HIPEpilogues, HIPAttention, HIPRows, HIPDeltaNet}
+package_of(::HIPLibrary) = :HIP
 
 end # module

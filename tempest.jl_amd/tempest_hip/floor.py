@@ -161,6 +161,7 @@ class FloorGroup:
     name: str = "floor group"
     reverse: bool = False                           # a scan or recurrence group from its last position
     step: int = -1                                  # a recurrence group's step axis (one of `reduced`)
+    ordered: bool = False                           # a pointwise group's items one after another (TH_FLOOR_ORDERED)
     values: dict = field(default_factory=dict)      # name -> (dtype, length), in value order
     terms: list = field(default_factory=list)       # (op, fn, args, ref, observe, lit, affine)
     folds: list = field(default_factory=list)       # (kind, phase, body, weight, scan, inner extents)
@@ -289,7 +290,8 @@ class FloorGroup:
         d.extents[:] = list(self.extents) + [1] * (RANK - len(self.extents))
         d.reduced = sum(1 << k for k in self.reduced)
         d.n_values, d.n_terms, d.n_folds, d.n_outputs = nv, nt, nf, no
-        d.flags = (1 if self.reverse else 0) | ((self.step << 8) if self.kind == "recurrence" else 0)
+        d.flags = ((1 if self.reverse else 0) | ((self.step << 8) if self.kind == "recurrence" else 0) |
+                   ((1 << 16) if self.ordered else 0))
         d.values, d.terms, d.folds, d.outputs = values, terms, folds, outs
         return d, (values, terms, folds, outs)
 

@@ -159,6 +159,7 @@ class Pool:
 
     def __init__(self, reserve: int = 64 << 30):
         self._h = ctypes.c_void_p()
+        self._closed = False
         call("th_pool_create", ctypes.c_uint64(reserve), ctypes.byref(self._h))
 
     def alloc(self, nbytes: int, align: int = 256) -> int:
@@ -176,9 +177,11 @@ class Pool:
         return b.value, r.value, m.value
 
     def destroy(self) -> None:
-        if self._h is not None:
+        """Give the range back; blocks still taken keep it until the last of
+        them is freed (th_pool_destroy), so the handle stays for their frees."""
+        if not self._closed:
+            self._closed = True
             call("th_pool_destroy", self._h)
-            self._h = None
 
     def __del__(self):
         try:

@@ -269,6 +269,37 @@ def test_embedding_gather_and_scatter_add_at_size(target):
     assert relative(ts["dE"].cpu().numpy().reshape(vocab, d), want) < TOL
 
 
+def test_scatter_add_in_order_is_deterministic(target):
+    """TH_FLOOR_ORDERED (what a deterministic target asks of a fold by key):
+    dE[:, t[j]] += dy[:, j] with the tokens taken one after another adds in
+    the items' order, so two runs agree bit for bit and equal a float32
+    accumulation in token order (numpy's add.at in float32), where the
+    atomic path's sums may differ in their last bits."""
+    from tempest_hip.floor import FloorGroup
+    announce("floor scatter add in order")
+    d, vocab, n = 64, 300, 2000
+    rng = np.random.default_rng(22)
+    tok = rng.integers(1, 40, n).astype(np.int32)  # heavily repeated
+    dy = rng.standard_normal(d * n).astype(np.float32)
+    g = FloorGroup("pointwise", (d, n), name="dE[:, t] .+= dy, in order", ordered=True)
+    g.value("dy", "f32", d * n)
+    g.value("t", "i32", n)
+    g.value("dE", "f32", d * vocab)
+    g.output("dE", g.load("dy", (1, d)), (1, 0), constant=-d, gather=g.load("t", (0, 1)), gather_coeff=d,
+             accumulate=True)
+    dyt, tt = torch.from_numpy(dy).cuda(), torch.from_numpy(tok).cuda()
+    runs = []
+    for _ in range(2):
+        dE = torch.zeros(d * vocab, device="cuda")
+        g.build({"dy": dyt.data_ptr(), "t": tt.data_ptr(), "dE": dE.data_ptr()})()
+        torch.cuda.synchronize()
+        runs.append(dE.cpu().numpy())
+    want = np.zeros((vocab, d), dtype=np.float32)
+    np.add.at(want, tok - 1, dy.reshape(n, d))
+    assert np.array_equal(runs[0], runs[1])
+    assert np.array_equal(runs[0].reshape(vocab, d), want)
+
+
 @pytest.mark.parametrize("n,m,reverse", [(4096, 37, False), (100000, 1, False), (5003, 6, True), (64, 900, False)])
 def test_parallel_scans(target, n, m, reverse):
     """Scans along the contiguous axis by a workgroup per item: an inclusive

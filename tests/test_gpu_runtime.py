@@ -368,3 +368,61 @@ def test_builds_from_several_threads(target):
     for (t1, _), (t2, _) in zip(threaded, serial):
         for u, v in zip(t1, t2):
             assert torch.equal(u, v)
+
+
+def test_copy_launch_records_and_retargets(target):
+    """th_build_copy, the `Copy` step as a launch (runtime.jl:47-64): run
+    directly, replayed in a graph, and retargeted to other buffers in place;
+    16-byte words where the ends and the length allow, bytes otherwise."""
+    import ctypes
+    from tempest_hip import _lib
+    announce("copy launch")
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    for nbytes, off in ((4 << 20, 0), (1000003, 0), (4096, 3)):
+        src = torch.randint(0, 256, (nbytes + 16,), dtype=torch.uint8, device="cuda", generator=gen)
+        dst = torch.zeros(nbytes + 16, dtype=torch.uint8, device="cuda")
+        h = ctypes.c_void_p()
+        _lib.call("th_build_copy", dst.data_ptr() + off, src.data_ptr() + off, ctypes.c_uint64(nbytes), ctypes.byref(h))
+        g = ctypes.c_void_p()
+        try:
+            _lib.call("th_launch_run", h)
+            _lib.call("th_quiesce")
+            assert torch.equal(dst[off:off + nbytes], src[off:off + nbytes])
+            assert not dst[off + nbytes:].any() and not dst[:off].any()
+            handles = (ctypes.c_void_p * 1)(h.value)
+            _lib.call("th_graph_capture", handles, 1, ctypes.byref(g))
+            src2 = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=gen)
+            dst2 = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+            _lib.call("th_launch_repoint", h, 0, ctypes.c_void_p(dst2.data_ptr()))
+            _lib.call("th_launch_repoint", h, 1, ctypes.c_void_p(src2.data_ptr()))
+            _lib.call("th_graph_retarget", g, 0)
+            _lib.call("th_graph_replay", g)
+            _lib.call("th_quiesce")
+            assert torch.equal(dst2, src2)
+        finally:
+            if g.value:
+                _lib.call("th_graph_release", g)
+            _lib.call("th_launch_destroy", h)
+
+
+def test_pool_destroyed_before_its_blocks(target):
+    """A pool destroyed while a block is taken keeps its range until that
+    block is freed (a host's collector may finalize the pool first), and
+    takes no new block meanwhile."""
+    import ctypes
+    from tempest_hip import HIPError, _lib
+    announce("pool destroyed before its blocks")
+    p = ctypes.c_void_p()
+    _lib.call("th_pool_create", ctypes.c_uint64(1 << 30), ctypes.byref(p))
+    a = ctypes.c_void_p()
+    _lib.call("th_pool_alloc", p, ctypes.c_uint64(1 << 20), ctypes.c_uint64(256), ctypes.byref(a))
+    _lib.call("th_pool_destroy", p)
+    host = np.arange(1 << 18, dtype=np.float32)
+    back = np.zeros_like(host)
+    _lib.call("th_upload", a, host.ctypes.data, ctypes.c_size_t(host.nbytes))
+    _lib.call("th_download", back.ctypes.data, a, ctypes.c_size_t(back.nbytes))
+    assert np.array_equal(host, back)
+    b = ctypes.c_void_p()
+    with pytest.raises(HIPError, match="destroyed"):
+        _lib.call("th_pool_alloc", p, ctypes.c_uint64(256), ctypes.c_uint64(256), ctypes.byref(b))
+    _lib.call("th_pool_free", p, a)
