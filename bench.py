@@ -202,6 +202,20 @@ def cpu_baseline(x, g, budget_s: float = 10.0):
             "seconds_full_step": step_s}
 
 
+def host_info() -> dict:
+    """The GPU box's host as the CPU baselines ran on it: logical CPUs the
+    process may use (nproc), those the machine has, and the CPU model."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": len(os.sched_getaffinity(0)), "cpus_online": os.cpu_count(), "cpu_model": model}
+
+
 def _one_thread():
     from threadpoolctl import threadpool_limits
     return threadpool_limits(1)
@@ -405,7 +419,8 @@ def config4(target, steps: int = 3, warmup: int = 1, recompute_dq: bool = False)
     t_f /= steps
     t_b /= steps
     total = f_fwd + f_bwd
-    return {"ms_per_step": (t_f + t_b) * 1e3, "TFLOP/s": total / (t_f + t_b) / 1e12,
+    dispatch = graph_vs_direct(target, ex, reps=3, warmup=1)
+    return {"ms_per_step": (t_f + t_b) * 1e3, "TFLOP/s": total / (t_f + t_b) / 1e12, "dispatch": dispatch,
             "frac_of_bf16_peak": total / (t_f + t_b) / BF16_PEAK, "flops_per_step": total,
             "fwd": {"ms": t_f * 1e3, "TFLOP/s": f_fwd / t_f / 1e12},
             "bwd": {"ms": t_b * 1e3, "TFLOP/s": f_bwd / t_b / 1e12,
@@ -447,6 +462,40 @@ def gemm_tiles(target, runs: int = 20):
         row["chosen"] = {"tile": L.TILE_NAMES[tile], "splits": splits, "us": t * 1e6, "TFLOP/s": flops / t / 1e12}
         out[f"{m}x{n}x{k}"] = row
         log(f"gemm tiles {m}x{n}x{k}:", json.dumps(row["chosen"]))
+    out["fp32"] = gemm_f32_rows(target, runs)
+    return out
+
+
+def gemm_f32_rows(target, runs: int = 20):
+    """fp32 factors: in full precision on the fp32 matrix cores (the 128 x 128
+    kernel, K split where the tiles alone do not fill the device) and as split
+    bf16 (bf16x3) on the bf16 tile kernels; each timed as claims are
+    (th_time_launch), then run `runs` times for a kernel trace.  A k-contiguous,
+    B n-contiguous, an fp32 result.  TFLOP/s counts the fp32 product's 2mnk."""
+    import torch
+    import tempest_hip.launch as L
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    out = {}
+    for m, n, k in ((4096, 4096, 4096), (256, 256, 8192), (1024, 1024, 1024)):
+        a = torch.randn(m, k, device="cuda", generator=gen)
+        b = torch.randn(k, n, device="cuda", generator=gen)
+        c = torch.empty(n, m, device="cuda")
+        args = (m, n, k, a.data_ptr(), k, 1, b.data_ptr(), n, 1, c.data_ptr(), m)
+        flops = 2.0 * m * n * k
+        row = {}
+        for name, kw in (("full", {}), ("bf16x3", {"bf16x3": True})):
+            launch = L.gemm(*args, c_dtype=L.F32, factors=L.F32, **kw)
+            t = target.time_launch(launch)
+            for _ in range(runs):
+                launch()
+            torch.cuda.synchronize()
+            row[name] = {"us": t * 1e6, "TFLOP/s": flops / t / 1e12, "workgroups": launch.work().blocks,
+                         "kernels": launch.describe()}
+            # Norm-wise error against the float64 product (torch's, as the checker).
+            want = (a.double() @ b.double()).T
+            row[name]["rel_err_vs_f64"] = float((c.double() - want).norm() / want.norm())
+        out[f"{m}x{n}x{k}"] = row
+        log(f"gemm fp32 {m}x{n}x{k}:", json.dumps({kk: v["TFLOP/s"] for kk, v in row.items()}))
     return out
 
 
@@ -477,11 +526,62 @@ def config5(target, steps: int = 3, warmup: int = 1):
     e1.record()
     torch.cuda.synchronize()
     s = e0.elapsed_time(e1) * 1e-3 / steps
-    return {"ms_per_step": s * 1e3, "TFLOP/s": w.flops / s / 1e12, "GB/s": w.bytes / s / 1e9,
+    dispatch = graph_vs_direct(target, ex, reps=3, warmup=1)
+    return {"ms_per_step": s * 1e3, "TFLOP/s": w.flops / s / 1e12, "GB/s": w.bytes / s / 1e9, "dispatch": dispatch,
             "flops_per_step": w.flops, "bytes_per_step": w.bytes,
             "note": "fp32 products as split bf16 on the matrix cores (chunk prep, column-split state scan, outputs, reverse "
                     "state-gradient scan, chunk-local backward); flops/bytes are the algorithmic estimates of "
                     "th_launch_work"}
+
+
+def dispatch_costs(target, reps: int = 2000):
+    """Where a graph replay's time goes on this device: graphs of 1, 9 and 40
+    near-empty launches (16-byte copies, th_build_copy), replayed back to back
+    (device time per replay from events) with the host time of each
+    th_graph_replay (hipGraphLaunch) call, against the same launches run
+    directly (th_launch_run)."""
+    import ctypes
+    import torch
+    from tempest_hip import _lib
+    buf = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    out = {}
+    for nodes in (1, 9, 40):
+        hs = []
+        for _ in range(nodes):
+            h = ctypes.c_void_p()
+            _lib.call("th_build_copy", buf.data_ptr() + 32, buf.data_ptr(), ctypes.c_uint64(16), ctypes.byref(h))
+            hs.append(h)
+        g = ctypes.c_void_p()
+        _lib.call("th_graph_capture", (ctypes.c_void_p * nodes)(*[h.value for h in hs]), nodes, ctypes.byref(g))
+        try:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            row = {}
+            for how in ("graph", "direct"):
+                for _ in range(50):
+                    if how == "graph":
+                        _lib.call("th_graph_replay", g)
+                    else:
+                        for h in hs:
+                            _lib.call("th_launch_run", h)
+                torch.cuda.synchronize()
+                e0.record()
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    if how == "graph":
+                        _lib.call("th_graph_replay", g)
+                    else:
+                        for h in hs:
+                            _lib.call("th_launch_run", h)
+                host = (time.perf_counter() - t0) / reps
+                e1.record()
+                torch.cuda.synchronize()
+                row[how] = {"us_device_per_step": e0.elapsed_time(e1) * 1e3 / reps, "us_host_per_step": host * 1e6}
+            out[f"{nodes}_launches"] = row
+        finally:
+            _lib.call("th_graph_release", g)
+            for h in hs:
+                _lib.call("th_launch_destroy", h)
+    return out
 
 
 def main() -> int:
@@ -493,7 +593,7 @@ def main() -> int:
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
-                                       "config5", "gemm_tiles"], default=None,
+                                       "config5", "gemm_tiles", "gemm_f32", "dispatch"], default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
@@ -525,6 +625,7 @@ def main() -> int:
         return 0
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
+              "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
@@ -577,6 +678,8 @@ def main() -> int:
             cpu = cpu_baseline(c2["x"], c2["g"])
         except Exception as err:
             cpu = {"error": repr(err)}
+        if isinstance(cpu, dict):
+            cpu.update(host_info())
         log("cpu_baseline:", json.dumps(cpu))
         # The other configs' CPU paths, each beside its own figures.
         for key, fn in (("config1_tanh_layer", cpu_config1), ("config3_mlp", cpu_config3),
@@ -585,6 +688,8 @@ def main() -> int:
                 r = fn()
             except Exception as err:
                 r = {"error": repr(err)}
+            if isinstance(r, dict):
+                r.update(host_info())
             if isinstance(configs.get(key), dict):
                 configs[key]["cpu_baseline"] = r
             log(key, "cpu:", json.dumps(r))

@@ -536,8 +536,11 @@ enum { TH_EPI_STORE = 0, TH_EPI_GELU = 1, TH_EPI_SQUARE_LOSS = 2, TH_EPI_GELU_BA
  *     (bias allowed), a result of the factors' type or fp32: the output tiles
  *     the reference's product sketch searches for half factors
  *     (ext/cuTileExt/contract.jl:36-39);
- *   TH_TILE_GENERAL: anything with TH_EPI_STORE and no bias: 64 x 64 tiles on
- *     the fp32 matrix cores, any shape and strides (fp32 factors run only here).
+ *   TH_TILE_GENERAL: anything with TH_EPI_STORE and no bias, on the fp32
+ *     matrix cores, any shape and strides: fp32 factors with an fp32 result on
+ *     128 x 128 tiles (16-byte loads along a unit stride, K split like the
+ *     others), half factors or a half result on 64 x 64 tiles (unsplit).
+ *     fp32 factors run only here unless TH_GEMM_BF16X3.
  * TH_TILE_AUTO chooses: the 256 x 256 kernel where it takes the product and
  * fills the device (split or not), else the largest middle tile that gives
  * 256 workgroups (the smallest if none does), else the general kernel.
@@ -577,6 +580,15 @@ typedef struct th_gemm_desc {
 #define TH_GEMM_F32_FACTORS 1  /* a and b hold fp32 */
 #define TH_GEMM_F16_FACTORS 2  /* a and b hold fp16 */
 #define TH_GEMM_ACCUMULATE 4   /* C = D + A*B (cuBLASExt.jl:25, `accumulated`) */
+/* With TH_GEMM_F32_FACTORS: each fp32 factor split x = hi + lo in bf16
+ * (hi = bf16(x), lo = bf16(x - hi)) and the product run on the bf16 tile
+ * kernels as A_hi B_hi + A_hi B_lo + A_lo B_hi, summed in fp32 (one product
+ * over K tripled; the tripled operands in the launch's workspace): about 16
+ * of fp32's 24 significant bits, on matrix cores 16x faster than fp32's.
+ * The MI355X counterpart of the reference's precision = :tf32x3
+ * (src/Compiler/runtime/target.jl:42-44, ext/cuBLASExt.jl:61-65).  An fp32
+ * result, no epilogue or bias; tile AUTO or one of the bf16 tiles. */
+#define TH_GEMM_BF16X3 8
 
 #define TH_TILE_AUTO 0
 #define TH_TILE_256 1

@@ -87,6 +87,40 @@ __global__ __launch_bounds__(256) void sum_splits(ReduceArgs a) {
 
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
+// An fp32 factor as three bf16 copies along K, for the bf16x3 products:
+// x = hi + lo + (below lo), hi = bf16(x), lo = bf16(x - hi); A's copies are
+// (hi, hi, lo) and B's (hi, lo, hi), so that the product of the two tripled
+// operands is A_hi B_hi + A_hi B_lo + A_lo B_hi.  Each copy is k8 deep (k
+// rounded up to 8, zeros past k); rows past `rows` (up to the destination's
+// padded count) are zeros.
+struct SplitArgs {
+  const float* src;
+  uint16_t* dst;
+  int64_t s_r, s_k, s_batch;  // source strides along the rows (m or n), along k, between products
+  int64_t d_r, d_k, d_batch;  // destination strides
+  int64_t total;              // destination elements of one copy of one product: rows_pad x k8
+  int32_t rows, rows_pad, k, k8;
+  int32_t order;   // 0: (hi, hi, lo), 1: (hi, lo, hi)
+  int32_t k_fast;  // 1: k is the destination's contiguous axis
+};
+
+__global__ __launch_bounds__(256) void split_bf16x3(SplitArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.total) return;
+  const int64_t z = blockIdx.y;
+  int64_t r, l;
+  if (a.k_fast) r = e / a.k8, l = e % a.k8;
+  else r = e % a.rows_pad, l = e / a.rows_pad;
+  const float x = (r < a.rows && l < a.k) ? a.src[z * a.s_batch + r * a.s_r + l * a.s_k] : 0.0f;
+  const uint16_t hi = bf16_bits(x);
+  const uint16_t lo = bf16_bits(x - bf16_float(hi));
+  uint16_t* d = a.dst + z * a.d_batch + r * a.d_r + l * a.d_k;
+  const int64_t step = (int64_t)a.k8 * a.d_k;
+  d[0] = hi;
+  d[step] = a.order == 0 ? hi : lo;
+  d[2 * step] = a.order == 0 ? lo : hi;
+}
+
 }  // namespace
 }  // namespace thg
 
@@ -133,7 +167,14 @@ static int64_t tiles_of(const th_gemm_desc* d, int bm, int bn) {
 // each part at least `least` deep (1024 on the 256 x 256 kernel, 512 on the
 // middle tiles).
 static int auto_splits(const th_gemm_desc* d, int tile) {
-  if (d->epilogue != TH_EPI_STORE || tile == TH_TILE_GENERAL) return 1;
+  if (d->epilogue != TH_EPI_STORE) return 1;
+  if (tile == TH_TILE_GENERAL) {
+    // fp32 factors on 128 x 128 tiles split as the others; half factors do not.
+    if (!(d->flags & TH_GEMM_F32_FACTORS) || d->c_dtype != TH_F32 || d->bias) return 1;
+    const int64_t tiles = tiles_of(d, 128, 128);
+    if (tiles >= 128 || d->k < 256) return 1;
+    return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / 128));
+  }
   const bool big = tile == TH_TILE_256;
   const int64_t tiles = big ? tiles_of(d, kTile, kTile) : tiles_of(d, mid_rows(tile), mid_cols(tile));
   const int least = big ? 1024 : 512;
@@ -160,6 +201,7 @@ static int choose_tile(const th_gemm_desc* d) {
 
 static int build_tile256(const th_gemm_desc* d, th_launch** out);
 static int build_mid(const th_gemm_desc* d, int tile, th_launch** out);
+static int build_bf16x3(const th_gemm_desc* d, th_launch** out);
 
 extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   if (int r = th::require_ready()) return r;
@@ -167,7 +209,7 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
   TH_REQUIRE(d != nullptr, "th_build_gemm: null descriptor");
   TH_REQUIRE(d->m >= 1 && d->n >= 1 && d->k >= 1, "th_build_gemm: m, n, k must be positive");
   TH_REQUIRE(d->a && d->b && d->c, "th_build_gemm: null operand");
-  TH_REQUIRE((d->flags & ~(TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS | TH_GEMM_ACCUMULATE)) == 0 &&
+  TH_REQUIRE((d->flags & ~(TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS | TH_GEMM_ACCUMULATE | TH_GEMM_BF16X3)) == 0 &&
                  (d->flags & (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS)) != (TH_GEMM_F32_FACTORS | TH_GEMM_F16_FACTORS),
              "th_build_gemm: unknown flags");
   const bool accumulate = (d->flags & TH_GEMM_ACCUMULATE) != 0;
@@ -178,11 +220,9 @@ extern "C" int th_build_gemm(const th_gemm_desc* d, th_launch** out) {
              "th_build_gemm: fused epilogues take one product and nothing to add");
   TH_REQUIRE(d->tile >= TH_TILE_AUTO && d->tile <= TH_TILE_GENERAL, "th_build_gemm: unknown tile");
   TH_REQUIRE(d->splits >= 0, "th_build_gemm: splits must be >= 0");
+  if (d->flags & TH_GEMM_BF16X3) return build_bf16x3(d, out);
   const int tile = d->tile == TH_TILE_AUTO ? choose_tile(d) : d->tile;
-  if (tile == TH_TILE_GENERAL) {
-    TH_REQUIRE(d->splits <= 1, "th_build_gemm: the general kernel does not split K");
-    return th::build_gemm_general(d, out);
-  }
+  if (tile == TH_TILE_GENERAL) return th::build_gemm_general(d, out);
   if (tile == TH_TILE_256) {
     TH_REQUIRE(tile_kernel_takes(d),
                "th_build_gemm: the 256 x 256 kernel takes bf16 factors with a unit stride on each operand, m, n, k "
@@ -400,6 +440,86 @@ static int build_mid(const th_gemm_desc* d, int tile, th_launch** out) {
   return TH_OK;
 }
 
+// fp32 factors as split bf16 on the bf16 tile kernels (TH_GEMM_BF16X3): each
+// factor becomes three bf16 copies along K (split_bf16x3) in the launch's
+// workspace, and one product over 3 k8 sums A_hi B_hi + A_hi B_lo + A_lo B_hi
+// in fp32 — the MI355X counterpart of the reference's :tf32x3
+// (src/Compiler/runtime/target.jl:42-44, ext/cuBLASExt.jl:61-65).  The
+// launch is the two split kernels followed by the inner product's kernels;
+// the inner product's operands point into the workspace.
+static int build_bf16x3(const th_gemm_desc* d, th_launch** out) {
+  TH_REQUIRE(d->flags & TH_GEMM_F32_FACTORS, "th_build_gemm: TH_GEMM_BF16X3 splits fp32 factors");
+  TH_REQUIRE(d->epilogue == TH_EPI_STORE && !d->bias && d->c_dtype == TH_F32,
+             "th_build_gemm: a bf16x3 product stores an fp32 result, with no epilogue or bias");
+  TH_REQUIRE(d->tile == TH_TILE_AUTO || (d->tile >= TH_TILE_256 && d->tile <= TH_TILE_64X64),
+             "th_build_gemm: a bf16x3 product runs on the bf16 tile kernels");
+  const int batch = d->batch > 0 ? d->batch : 1;
+  const int M = d->m, N = d->n, K = d->k;
+  const int k8 = (K + 7) / 8 * 8, m8 = (M + 7) / 8 * 8, n8 = (N + 7) / 8 * 8;
+  TH_REQUIRE((int64_t)3 * k8 <= 0x7fffffff, "th_build_gemm: K too large");
+  // The tripled operands, dense, with the fp32 operand's unit-stride axis kept.
+  th_gemm_desc in = *d;
+  in.flags = d->flags & TH_GEMM_ACCUMULATE;
+  in.k = 3 * k8;
+  const bool a_kfast = d->a_k == 1 && d->a_m != 1;
+  const bool b_kfast = d->b_k == 1 && d->b_n != 1;
+  SplitArgs sa{}, sb{};
+  sa.rows = M, sa.k = K, sa.k8 = k8, sa.order = 0, sa.k_fast = a_kfast;
+  sa.s_r = d->a_m, sa.s_k = d->a_k, sa.s_batch = d->a_batch;
+  if (a_kfast) sa.rows_pad = M, sa.d_r = 3 * k8, sa.d_k = 1, in.a_m = 3 * k8, in.a_k = 1;
+  else sa.rows_pad = m8, sa.d_r = 1, sa.d_k = m8, in.a_m = 1, in.a_k = m8;
+  sa.total = (int64_t)sa.rows_pad * k8;
+  sa.d_batch = 3 * sa.total;
+  sb.rows = N, sb.k = K, sb.k8 = k8, sb.order = 1, sb.k_fast = b_kfast;
+  sb.s_r = d->b_n, sb.s_k = d->b_k, sb.s_batch = d->b_batch;
+  if (b_kfast) sb.rows_pad = N, sb.d_r = 3 * k8, sb.d_k = 1, in.b_n = 3 * k8, in.b_k = 1;
+  else sb.rows_pad = n8, sb.d_r = 1, sb.d_k = n8, in.b_n = 1, in.b_k = n8;
+  sb.total = (int64_t)sb.rows_pad * k8;
+  sb.d_batch = 3 * sb.total;
+  in.a_batch = sa.d_batch, in.b_batch = sb.d_batch;
+  // Stand-ins the inner build checks for alignment; the workspace replaces them.
+  in.a = reinterpret_cast<const void*>(uintptr_t(256));
+  in.b = reinterpret_cast<const void*>(uintptr_t(256));
+  th_launch* inner = nullptr;
+  if (int r = th_build_gemm(&in, &inner)) return r;
+  const uint64_t a_bytes = (uint64_t)batch * sa.d_batch * 2, b_bytes = (uint64_t)batch * sb.d_batch * 2;
+  th::Builder bl("gemm_bf16x3", 9);
+  const uint64_t at_a = bl.workspace(a_bytes), at_b = bl.workspace(b_bytes);
+  const uint64_t at_inner = bl.workspace(inner->ws_bytes);
+  sa.src = static_cast<const float*>(d->a), sb.src = static_cast<const float*>(d->b);
+  const int ka = bl.kernel((const void*)split_bf16x3, "split_bf16x3_a", dim3((unsigned)((sa.total + 255) / 256), batch),
+                           dim3(256), 0, sa);
+  const int kb = bl.kernel((const void*)split_bf16x3, "split_bf16x3_b", dim3((unsigned)((sb.total + 255) / 256), batch),
+                           dim3(256), 0, sb);
+  bl.ref(0, ka, TH_OFFSET(SplitArgs, src));
+  bl.ref(1, kb, TH_OFFSET(SplitArgs, src));
+  bl.ws_ref(ka, TH_OFFSET(SplitArgs, dst), at_a);
+  bl.ws_ref(kb, TH_OFFSET(SplitArgs, dst), at_b);
+  th_launch* l = bl.release();
+  // The inner product's kernels after the splits: its operands a and b
+  // become the tripled copies in the workspace, its other values ours.
+  const int base = (int)l->kernels.size();
+  for (const th::Kernel& k : inner->kernels) l->kernels.push_back(k);
+  for (int v = 0; v < (int)inner->values.size() && v < (int)l->values.size(); ++v)
+    for (const th::Ref& r : inner->values[v]) {
+      if (v == 0) l->ws_refs.push_back(th::WsRef{base + r.kernel, r.offset, at_a});
+      else if (v == 1) l->ws_refs.push_back(th::WsRef{base + r.kernel, r.offset, at_b});
+      else l->values[v].push_back(th::Ref{base + r.kernel, r.offset});
+    }
+  for (const th::WsRef& w : inner->ws_refs) l->ws_refs.push_back(th::WsRef{base + w.kernel, w.offset, at_inner + w.at});
+  for (int v = 2; v < (int)inner->align.size() && v < (int)l->align.size(); ++v) l->align[v] = inner->align[v];
+  l->work.kernels = (int32_t)l->kernels.size();
+  l->work.flops = 2.0 * batch * (double)M * N * K;
+  l->work.bytes = batch * (4.0 * ((double)M * K + (double)K * N) + 4.0 * (double)M * N *
+                          ((d->flags & TH_GEMM_ACCUMULATE) ? 2 : 1));
+  l->work.blocks = inner->work.blocks;
+  l->name = "gemm_bf16x3 (fp32 factors as hi + lo bf16, K tripled): " + inner->name;
+  inner->kernels.clear();
+  th_launch_destroy(inner);
+  *out = l;
+  return TH_OK;
+}
+
 // ---- measuring the choices -------------------------------------------------------
 
 namespace {
@@ -460,21 +580,32 @@ extern "C" int th_gemm_tune(const th_gemm_desc* desc, int32_t* tile_out, int32_t
     d.tile = TH_TILE_AUTO;
     d.splits = 0;
     std::vector<int> tiles;
-    if (tile_kernel_takes(&d)) tiles.push_back(TH_TILE_256);
-    if (mid_takes(&d))
-      for (int t : {TH_TILE_128X128, TH_TILE_128X64, TH_TILE_64X128, TH_TILE_64X64}) tiles.push_back(t);
-    if (d.epilogue == TH_EPI_STORE && !d.bias) tiles.push_back(TH_TILE_GENERAL);
+    const bool x3 = (d.flags & TH_GEMM_BF16X3) != 0;
+    if (x3) {
+      // The bf16 tiles the tripled product may run on: those that build.
+      for (int t : {TH_TILE_256, TH_TILE_128X128, TH_TILE_128X64, TH_TILE_64X128, TH_TILE_64X64}) tiles.push_back(t);
+    } else {
+      if (tile_kernel_takes(&d)) tiles.push_back(TH_TILE_256);
+      if (mid_takes(&d))
+        for (int t : {TH_TILE_128X128, TH_TILE_128X64, TH_TILE_64X128, TH_TILE_64X64}) tiles.push_back(t);
+      if (d.epilogue == TH_EPI_STORE && !d.bias) tiles.push_back(TH_TILE_GENERAL);
+    }
     TH_REQUIRE(!tiles.empty(), "th_gemm_tune: no kernel takes the product");
     // Stage one: every tile at the split the builder would choose.
     Tuned best{0, 0, 0.0};
     for (int t : tiles) {
       double s = 0;
-      if (int r = measure(&d, t, 0, &s)) return r;
+      if (int r = measure(&d, t, 0, &s)) {
+        if (x3) continue;  // a tile the tripled product does not fit
+        return r;
+      }
       if (best.tile == 0 || s < best.seconds) best = Tuned{t, splits_used(&d, t, 0), s};
     }
+    TH_REQUIRE(best.tile != 0, "th_gemm_tune: no kernel takes the product");
     // Stage two: the other splits of the best (plain products on the tile
-    // kernels), each part at least 256 deep.
-    if (best.tile != TH_TILE_GENERAL && d.epilogue == TH_EPI_STORE) {
+    // kernels, and fp32 ones on the general kernel), each part at least 256 deep.
+    const bool general_splits = d.flags & TH_GEMM_F32_FACTORS && d.c_dtype == TH_F32 && !d.bias;
+    if ((best.tile != TH_TILE_GENERAL || general_splits) && d.epilogue == TH_EPI_STORE) {
       for (int sp : {1, 2, 4, 8, 16}) {
         if (sp > 1 && d.k / sp < 256) break;
         const int used = splits_used(&d, best.tile, sp);

@@ -112,7 +112,7 @@ def tanh_layer_grad(d: int, h: int, c: int, w: int, b: int, x: int, loss: int, d
 
 F32, BF16, F16 = 0, 1, 4
 STORE, GELU, SQUARE_LOSS, GELU_BACKWARD = 0, 1, 2, 3
-F32_FACTORS, F16_FACTORS, ACCUMULATE = 1, 2, 4  # TH_GEMM_*
+F32_FACTORS, F16_FACTORS, ACCUMULATE, BF16X3 = 1, 2, 4, 8  # TH_GEMM_*
 # TH_TILE_*: which kernel and output tile a product runs on.
 TILE_AUTO, TILE_256, TILE_128X128, TILE_128X64, TILE_64X128, TILE_64X64, TILE_GENERAL = range(7)
 TILE_NAMES = {TILE_256: "256x256", TILE_128X128: "128x128", TILE_128X64: "128x64", TILE_64X128: "64x128",
@@ -121,8 +121,8 @@ TILE_NAMES = {TILE_256: "256x256", TILE_128X128: "128x128", TILE_128X64: "128x64
 
 def _gemm_desc(m, n, k, a, a_m, a_k, b, b_k, b_n, c, c_ld, c_dtype=BF16, epilogue=STORE, bias=0, aux=0, aux_ld=0,
                aux_out=0, row_sums=0, loss=0, batch=1, a_batch=0, b_batch=0, c_batch=0, factors=BF16, d=0, d_ld=0,
-               d_batch=0, splits=0, tile=TILE_AUTO):
-    flags = {BF16: 0, F32: F32_FACTORS, F16: F16_FACTORS}[factors] | (ACCUMULATE if d else 0)
+               d_batch=0, splits=0, tile=TILE_AUTO, bf16x3=False):
+    flags = {BF16: 0, F32: F32_FACTORS, F16: F16_FACTORS}[factors] | (ACCUMULATE if d else 0) | (BF16X3 if bf16x3 else 0)
     return _lib.GemmDesc(m=m, n=n, k=k, c_dtype=c_dtype, epilogue=epilogue, tile=tile, a=a, a_m=a_m, a_k=a_k, b=b,
                          b_k=b_k, b_n=b_n, c=c, c_ld=c_ld, bias=bias or None, aux=aux or None, aux_ld=aux_ld,
                          aux_out=aux_out or None, row_sums=row_sums or None, loss=loss or None, batch=batch,
@@ -134,17 +134,19 @@ def gemm(m: int, n: int, k: int, a: int, a_m: int, a_k: int, b: int, b_k: int, b
          c_dtype: int = BF16, epilogue: int = STORE, bias: int = 0, aux: int = 0, aux_ld: int = 0,
          aux_out: int = 0, row_sums: int = 0, loss: int = 0, batch: int = 1, a_batch: int = 0, b_batch: int = 0,
          c_batch: int = 0, factors: int = BF16, d: int = 0, d_ld: int = 0, d_batch: int = 0,
-         splits: int = 0, tile: int = TILE_AUTO) -> Launch:
+         splits: int = 0, tile: int = TILE_AUTO, bf16x3: bool = False) -> Launch:
     """C (m x n, column-major at c_ld) = A (m x k) * B (k x n) (+ D with d), for
     each of `batch` products; A(i, l) at a[i*a_m + l*a_k], B(l, j) at
     b[l*b_k + j*b_n], product z's operands *_batch elements further; factors
     BF16, F32 or F16; tile: TILE_* (the kernel and its output tile, TILE_AUTO
-    chosen); splits: parts of K (0 chosen, 1 none).  With TEMPEST_HIP_TUNE=1
+    chosen); splits: parts of K (0 chosen, 1 none); bf16x3: fp32 factors as
+    hi + lo bf16 on the bf16 tile kernels (TH_GEMM_BF16X3).  With TEMPEST_HIP_TUNE=1
     in the environment a product left to the library (TILE_AUTO, splits 0)
     takes th_gemm_tune's measured choice instead, as the Julia binding's build
     does (not D + A B in place, which each measurement would add again)."""
     desc = _gemm_desc(m, n, k, a, a_m, a_k, b, b_k, b_n, c, c_ld, c_dtype, epilogue, bias, aux, aux_ld, aux_out,
-                      row_sums, loss, batch, a_batch, b_batch, c_batch, factors, d, d_ld, d_batch, splits, tile)
+                      row_sums, loss, batch, a_batch, b_batch, c_batch, factors, d, d_ld, d_batch, splits, tile,
+                      bf16x3)
     if tile == TILE_AUTO and splits == 0 and os.environ.get("TEMPEST_HIP_TUNE") == "1" and not (d and d == c):
         t, sp, sec = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_double()
         call("th_gemm_tune", ctypes.byref(desc), ctypes.byref(t), ctypes.byref(sp), ctypes.byref(sec))

@@ -1,5 +1,7 @@
 """Products beyond the bf16 tile kernel's shapes, and the tile kernel's batch,
-split K and accumulate.  The general kernel: every product of the reference's
+split K and accumulate.  fp32 factors on their own 128 x 128 kernel (vector
+loads along a unit stride, edges element by element, K split into parts) and
+as split bf16 (bf16x3) on the bf16 tile kernels, at sizes, against float64.  The general kernel: every product of the reference's
 fixture programs at its own shape (test/fixtures/programs.jl:79-96), fp32
 factors, transposed operands through strides, a batch axis, D + A B, and bf16
 or fp16 factors at shapes that are not multiples of 8.  A whole fixture
@@ -77,7 +79,7 @@ def test_products_of_the_fixture_programs(target):
     for name, a, b, ta, tb, d in cases:
         announce("general product", name)
         got, l = _product(a, b, a.shape, b.shape, ta, tb, d=d)
-        assert "gemm_general" in l.describe(), name
+        assert "gemm_f32" in l.describe(), name
         want = interpret.product(a.T if ta else a, b.T if tb else b, d)
         assert relative(got, want) < TOL_F32, (name, relative(got, want))
 
@@ -234,3 +236,136 @@ def test_tile_kernel_accumulates(target):
     l2()
     torch.cuda.synchronize()
     assert relative(Cb.double().cpu().numpy(), (prod + start).cpu().numpy()) < 1e-2
+
+
+def _f32_operands(m, n, k, a_kfast, b_kfast, seed, batch=1):
+    """fp32 A (m x k) and B (k x n) for each of `batch` products, on the
+    device in the layout asked: A k-contiguous (A(i, l) at i k + l) or
+    m-contiguous (l m + i); B k-contiguous (j k + l) or n-contiguous (l n + j).
+    Returns the float64 values, the tensors and the strides."""
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((batch, m, k)).astype(np.float32)
+    B = rng.standard_normal((batch, k, n)).astype(np.float32)
+    ta = torch.from_numpy(np.ascontiguousarray(A if a_kfast else A.transpose(0, 2, 1))).cuda()
+    tb = torch.from_numpy(np.ascontiguousarray(B.transpose(0, 2, 1) if b_kfast else B)).cuda()
+    st = {"a_m": k if a_kfast else 1, "a_k": 1 if a_kfast else m, "b_k": 1 if b_kfast else n, "b_n": k if b_kfast else 1,
+          "a_batch": m * k, "b_batch": k * n}
+    return A.astype(np.float64), B.astype(np.float64), ta, tb, st
+
+
+def _run_f32(m, n, k, ta, tb, st, batch=1, d=None, bf16x3=False, splits=0, tile=0):
+    import tempest_hip.launch as L
+    c = torch.zeros(batch, n, m, device="cuda")  # column-major m x n per product
+    l = L.gemm(m, n, k, ta.data_ptr(), st["a_m"], st["a_k"], tb.data_ptr(), st["b_k"], st["b_n"], c.data_ptr(), m,
+               c_dtype=L.F32, factors=L.F32, batch=batch, a_batch=st["a_batch"], b_batch=st["b_batch"],
+               c_batch=m * n, d=(d.data_ptr() if d is not None else 0), bf16x3=bf16x3, splits=splits, tile=tile)
+    l()
+    torch.cuda.synchronize()
+    return c.double().cpu().numpy().transpose(0, 2, 1), l
+
+
+@pytest.mark.parametrize("m,n,k,a_kfast,b_kfast", [
+    (512, 384, 1024, True, True), (512, 384, 1024, False, False), (512, 384, 1024, True, False),
+    (512, 384, 1024, False, True), (1000, 700, 333, True, False), (129, 257, 17, False, True),
+    (2048, 1024, 1536, False, False), (1, 300, 5, True, True)])
+def test_f32_kernel_at_size(target, m, n, k, a_kfast, b_kfast):
+    """fp32 factors on the 128 x 128 kernel, every operand layout, interior
+    tiles (16-byte loads) and ragged edges (element loads, bounds-checked)."""
+    announce("fp32 kernel", m, n, k, a_kfast, b_kfast)
+    A, B, ta, tb, st = _f32_operands(m, n, k, a_kfast, b_kfast, m + n + k)
+    got, l = _run_f32(m, n, k, ta, tb, st)
+    assert "gemm_f32" in l.describe()
+    assert relative(got[0], A[0] @ B[0]) < TOL_F32
+
+
+def test_f32_kernel_splits_k_batches_and_adds(target):
+    """256 x 256 x 8192 (four tiles alone) split into parts summed in order;
+    a batch of three with D + A B; D + A B in place (D = C)."""
+    announce("fp32 kernel split k")
+    A, B, ta, tb, st = _f32_operands(256, 256, 8192, True, False, 11)
+    got, l = _run_f32(256, 256, 8192, ta, tb, st)
+    assert "gemm_f32_sum_parts" in l.describe() and l.work().blocks >= 256, l.describe()
+    assert relative(got[0], A[0] @ B[0]) < 3e-5  # fp32 sums of 8192 terms
+    A, B, ta, tb, st = _f32_operands(384, 200, 640, False, True, 12, batch=3)
+    D = torch.randn(3, 200, 384, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
+    got, _ = _run_f32(384, 200, 640, ta, tb, st, batch=3, d=D)
+    want = A @ B + D.double().cpu().numpy().transpose(0, 2, 1)
+    assert relative(got, want) < TOL_F32
+    # In place: C starts as D and the product is added to it.
+    import tempest_hip.launch as L
+    c = D.clone()
+    start = c.double().cpu().numpy().transpose(0, 2, 1)
+    L.gemm(384, 200, 640, ta.data_ptr(), st["a_m"], st["a_k"], tb.data_ptr(), st["b_k"], st["b_n"], c.data_ptr(), 384,
+           c_dtype=L.F32, factors=L.F32, batch=3, a_batch=st["a_batch"], b_batch=st["b_batch"], c_batch=384 * 200,
+           d=c.data_ptr(), splits=2)()
+    torch.cuda.synchronize()
+    assert relative(c.double().cpu().numpy().transpose(0, 2, 1), A @ B + start) < TOL_F32
+
+
+# bf16x3: each fp32 factor hi + lo with hi = bf16(x), lo = bf16(x - hi), and
+# C = A_hi B_hi + A_hi B_lo + A_lo B_hi summed in fp32.  What it leaves out
+# per product a b: a_lo b_lo (|a_lo| <= 2^-9 |a|, so <= 2^-18 |a b|) and the
+# rounding of x - hi to lo (<= 2^-9 |x - hi| <= 2^-17 |x|), about 2^-16 of
+# |a b| at worst; random signs keep the norm-wise error of a sum of such
+# terms near that, well inside the 2e-4 the reference's fp32 product tests
+# hold (test/cuda/products.jl) and ~100x below bf16 factors' error.
+TOL_BF16X3 = 2e-4
+
+
+@pytest.mark.parametrize("m,n,k,a_kfast,b_kfast", [
+    (1024, 768, 2048, True, True), (1024, 768, 2048, False, False), (1024, 768, 2048, True, False),
+    (1024, 768, 2048, False, True), (1000, 700, 333, False, True), (37, 29, 53, True, False)])
+def test_bf16x3_products(target, m, n, k, a_kfast, b_kfast):
+    """fp32 factors as split bf16 on the bf16 tile kernels: within the fp32
+    products' tolerance, and far closer than bf16 factors."""
+    from oracle.data import bf16_round
+    announce("bf16x3", m, n, k, a_kfast, b_kfast)
+    A, B, ta, tb, st = _f32_operands(m, n, k, a_kfast, b_kfast, 7 * m + k)
+    got, l = _run_f32(m, n, k, ta, tb, st, bf16x3=True)
+    desc = l.describe()
+    assert "split_bf16x3" in desc and ("gemm_bf16" in desc or "gemm_mid" in desc) and "gemm_f32" not in desc, desc
+    want = A[0] @ B[0]
+    err = relative(got[0], want)
+    plain = relative(bf16_round(A[0].astype(np.float32)).astype(np.float64) @
+                     bf16_round(B[0].astype(np.float32)).astype(np.float64), want)
+    assert err < TOL_BF16X3, err
+    assert err < plain / 30, (err, plain)
+
+
+def test_bf16x3_batch_split_and_in_place(target):
+    """A batch of two with D + A B, K split, and D + A B in place."""
+    import tempest_hip.launch as L
+    announce("bf16x3 batch")
+    A, B, ta, tb, st = _f32_operands(512, 512, 4096, True, False, 13, batch=2)
+    D = torch.randn(2, 512, 512, device="cuda", generator=torch.Generator(device="cuda").manual_seed(4))
+    got, l = _run_f32(512, 512, 4096, ta, tb, st, batch=2, d=D, bf16x3=True, splits=4)
+    assert "sum_splits" in l.describe()
+    want = A @ B + D.double().cpu().numpy().transpose(0, 2, 1)
+    assert relative(got, want) < TOL_BF16X3
+    c = D.clone()
+    start = c.double().cpu().numpy().transpose(0, 2, 1)
+    L.gemm(512, 512, 4096, ta.data_ptr(), st["a_m"], st["a_k"], tb.data_ptr(), st["b_k"], st["b_n"], c.data_ptr(), 512,
+           c_dtype=L.F32, factors=L.F32, batch=2, a_batch=st["a_batch"], b_batch=st["b_batch"], c_batch=512 * 512,
+           d=c.data_ptr(), bf16x3=True)()
+    torch.cuda.synchronize()
+    assert relative(c.double().cpu().numpy().transpose(0, 2, 1), A @ B + start) < TOL_BF16X3
+
+
+def test_bf16x3_tuned_and_refusals(target):
+    """th_gemm_tune measures the bf16 tiles for a bf16x3 product; an epilogue,
+    a bias or a half result is refused."""
+    import tempest_hip.launch as L
+    from tempest_hip import HIPError
+    announce("bf16x3 tune")
+    A, B, ta, tb, st = _f32_operands(768, 640, 1536, True, True, 14)
+    c = torch.zeros(640, 768, device="cuda")
+    args = (768, 640, 1536, ta.data_ptr(), st["a_m"], st["a_k"], tb.data_ptr(), st["b_k"], st["b_n"], c.data_ptr(), 768)
+    tile, splits, sec = L.gemm_tune(*args, c_dtype=L.F32, factors=L.F32, bf16x3=True)
+    assert tile in (L.TILE_256, L.TILE_128X128, L.TILE_128X64, L.TILE_64X128, L.TILE_64X64) and sec > 0
+    L.gemm(*args, c_dtype=L.F32, factors=L.F32, bf16x3=True, tile=tile, splits=splits)()
+    torch.cuda.synchronize()
+    assert relative(c.double().cpu().numpy().T, A[0] @ B[0]) < TOL_BF16X3
+    with pytest.raises(HIPError, match="bf16x3"):
+        L.gemm(*args, c_dtype=L.BF16, factors=L.F32, bf16x3=True)
+    with pytest.raises(HIPError, match="bf16x3"):
+        L.gemm(*args, c_dtype=L.F32, factors=L.F32, bf16x3=True, tile=L.TILE_GENERAL)
