@@ -174,52 +174,66 @@ Base.copyto!(dest::HIPDense{T}, src::Array{T}) where {T} = copyto!(dest, 1, src,
 # ---- the target ---------------------------------------------------------------------
 
 """
-    HIPTarget(implementations...; device = 0, reserve = 64 << 30, deterministic = false)
+    HIPTarget(implementations...; device = 0, reserve = 64 << 30, precision = :full, deterministic = false)
 
 One MI355X.  Its slots come from one reserved range of `reserve` bytes of
 device addresses (`HIPPool`).  `implementations` are the libraries it offers
 the cover, tried in order beside the floor; by default all of this
-extension's.  `deterministic = true` keeps every sum's rounding independent
-of the order blocks run in (target.jl:229-231): the floor's folds by key then
-add their elements one at a time in the order of the items instead of by
-atomics, the one place this backend's sums depend on that order; every other
-kernel here folds in a fixed order either way.  `false` is the reference's
-default (target.jl:31).
+extension's.
+
+- `precision`: the numerics policy for products of Float32 factors (as
+  CUDATarget's, target.jl:42-44): `:full` keeps them in Float32 on the fp32
+  matrix cores; `:bf16x3` splits each factor into two BFloat16 parts,
+  `x = hi + lo`, and sums three bf16 products in Float32
+  (`A_hi B_hi + A_hi B_lo + A_lo B_hi`, about 16 of Float32's 24 significant
+  bits), on matrix cores sixteen times faster: the MI355X counterpart of
+  `:tf32x3`, which this device has no TF32 for.
+- `deterministic = true` keeps every sum's rounding independent of the order
+  blocks run in (target.jl:229-231): the floor's folds by key then add their
+  elements one at a time in the order of the items instead of by atomics,
+  the one place this backend's sums depend on that order; every other kernel
+  here folds in a fixed order either way.  `false` is the reference's default
+  (target.jl:31).
 """
 mutable struct HIPTarget <: C.Target
     implementations::Tuple
     device::Int
     pool::HIPPool
+    precision::Symbol
     deterministic::Bool
     # The one inner constructor, so that Julia makes no field-by-field ones
-    # that a call with four implementations would reach.
-    HIPTarget(::Val{:fields}, implementations::Tuple, device::Int, pool::HIPPool, deterministic::Bool) =
-        new(implementations, device, pool, deterministic)
+    # that a call with five implementations would reach.
+    function HIPTarget(::Val{:fields}, implementations::Tuple, device::Int, pool::HIPPool, precision::Symbol,
+                       deterministic::Bool)
+        precision in (:full, :bf16x3) || throw(ArgumentError("precision must be :full or :bf16x3, got $precision"))
+        new(implementations, device, pool, precision, deterministic)
+    end
 end
 
-HIPTarget(implementations...; device::Integer = 0, reserve::Integer = 64 << 30, deterministic::Bool = false) =
+HIPTarget(implementations...; device::Integer = 0, reserve::Integer = 64 << 30, precision::Symbol = :full,
+    deterministic::Bool = false) =
     HIPTarget(Val(:fields), isempty(implementations) ? default_implementations() : implementations, Int(device),
-        HIPPool(device, reserve), deterministic)
+        HIPPool(device, reserve), precision, deterministic)
 
 # A target over an existing pool: what `target_for` gives for its buffers.
-HIPTarget(pool::HIPPool; deterministic::Bool = false) =
-    HIPTarget(Val(:fields), default_implementations(), pool.device, pool, deterministic)
+HIPTarget(pool::HIPPool; precision::Symbol = :full, deterministic::Bool = false) =
+    HIPTarget(Val(:fields), default_implementations(), pool.device, pool, precision, deterministic)
 
 default_implementations() = (HIPProducts(), HIPEpilogues(), HIPAttention(), HIPRows(), HIPDeltaNet())
 
 Base.show(io::IO, t::HIPTarget) = print(io, "HIPTarget(", join(map(repr, t.implementations), ", "), "; device = ", t.device,
-    t.deterministic ? ", deterministic = true" : "", ")")
+    ", precision = :", t.precision, t.deterministic ? ", deterministic = true" : "", ")")
 
 # The options the compiler reads (target.jl:79-83,216-231; cover/cost.jl:132).
 implementations(t::HIPTarget) = t.implementations
-numerics(t::HIPTarget) = t.deterministic ? Symbol("full-deterministic") : :full
+numerics(t::HIPTarget) = Symbol(t.precision, t.deterministic ? "-deterministic" : "")
 # The row kernels and attention fold exponentials online, as the rewrite does.
 permits_rewrites(::HIPTarget) = true
 # The attention backward reads the forward's output as it was rounded to bf16.
 rounded_backward(::HIPTarget) = true
 deterministic(t::HIPTarget) = t.deterministic
-# Half-precision products run as themselves, Float32 ones in full precision.
-product_class(::HIPTarget, T) = T === Float16 || T === Tempest.BFloat16 ? nameof(T) : :full
+# Half-precision products run as themselves, Float32 ones in the target's precision.
+product_class(t::HIPTarget, T) = T === Float16 || T === Tempest.BFloat16 ? nameof(T) : t.precision
 
 # Arrays and devices (target.jl:94-124,129-175).  One device per process: the
 # library drives the device its first `th_init` named.
@@ -506,7 +520,7 @@ struct GemmDesc
 end
 
 const TH_F32, TH_BF16, TH_F16 = Int32(0), Int32(1), Int32(4)
-const GEMM_F32_FACTORS, GEMM_F16_FACTORS, GEMM_ACCUMULATE = Int32(1), Int32(2), Int32(4)
+const GEMM_F32_FACTORS, GEMM_F16_FACTORS, GEMM_ACCUMULATE, GEMM_BF16X3 = Int32(1), Int32(2), Int32(4), Int32(8)
 dtype_code(T) = T === Float32 ? TH_F32 : T === Tempest.BFloat16 ? TH_BF16 : T === Float16 ? TH_F16 :
     throw(ArgumentError("libtempest_hip has no $T arrays"))
 factor_flags(T) = T === Float32 ? GEMM_F32_FACTORS : T === Float16 ? GEMM_F16_FACTORS : Int32(0)
@@ -517,8 +531,9 @@ factor_flags(T) = T === Float32 ? GEMM_F32_FACTORS : T === Float16 ? GEMM_F16_FA
 # result.  Any other strides the library takes (the library chooses the
 # kernel and its tile: the 256 x 256 or a middle tile where it can, the general
 # kernel else).  With `buffers = false` the addresses are null (`supports` is
-# asked without storage).
-function gemm_desc(b::Binding; buffers = true)
+# asked without storage).  `precision = :bf16x3` runs Float32 factors with a
+# Float32 result as split bf16 (TH_GEMM_BF16X3).
+function gemm_desc(b::Binding; buffers = true, precision = :full)
     A, B, Cr = b.arrays.A, b.arrays.B, b.arrays.C
     T, R = A.eltype, Cr.eltype
     T in (Float32, Float16, Tempest.BFloat16) && B.eltype === T && (R === T || R === Float32) || return nothing
@@ -529,9 +544,10 @@ function gemm_desc(b::Binding; buffers = true)
     D = accumulate ? b.arrays.D : nothing
     accumulate && !(D.eltype === R && D.strides == Cr.strides) && return nothing
     p(s) = buffers ? address_or_null(s) : C_NULL
+    x3 = precision === :bf16x3 && T === Float32 && R === Float32 ? GEMM_BF16X3 : Int32(0)
     GemmDesc(e.m, e.n, e.k, dtype_code(R), 0, 0, p(A), A.strides[1], A.strides[2], p(B), B.strides[1], B.strides[2],
         p(Cr), Cr.strides[2], C_NULL, C_NULL, 0, C_NULL, C_NULL, C_NULL,
-        e.b, factor_flags(T) | (accumulate ? GEMM_ACCUMULATE : Int32(0)), A.strides[3], B.strides[3], Cr.strides[3],
+        e.b, factor_flags(T) | (accumulate ? GEMM_ACCUMULATE : Int32(0)) | x3, A.strides[3], B.strides[3], Cr.strides[3],
         p(D), accumulate ? D.strides[2] : 0, accumulate ? D.strides[3] : 0, 0, 0)
 end
 
@@ -560,7 +576,7 @@ end
 # ext/cuTileExt/contract.jl:12-27); otherwise the library's choice.  A product
 # added to a matrix in place is not measured (each run would add it again).
 function build(::HIPProducts, t::HIPTarget, b::Binding, resources)
-    d = Ref(gemm_desc(b))
+    d = Ref(gemm_desc(b; precision = t.precision))
     if get(ENV, "TEMPEST_HIP_TUNE", "") == "1" && b.template != ACCUMULATED
         tile, splits, secs = Ref{Int32}(0), Ref{Int32}(0), Ref{Float64}(0)
         check(ccall((:th_gemm_tune, LIB), Cint, (Ptr{GemmDesc}, Ptr{Int32}, Ptr{Int32}, Ptr{Float64}),
@@ -581,7 +597,7 @@ supports(lib::HIPProducts, target::HIPTarget, bs::Vector{Binding}) =
     all(b -> supports(lib, target, b) && b.template != ACCUMULATED, bs)
 
 function build(::HIPProducts, t::HIPTarget, bs::Vector{Binding}, resources)
-    descs = [gemm_desc(b) for b in bs]
+    descs = [gemm_desc(b; precision = t.precision) for b in bs]
     out = Ref{Ptr{Cvoid}}()
     check(ccall((:th_build_gemm_grouped, LIB), Cint, (Ptr{GemmDesc}, Cint, Ptr{Ptr{Cvoid}}), descs, length(descs), out),
         "th_build_gemm_grouped")

@@ -78,17 +78,20 @@ _initialised: int | None = None
 class HIPTarget:
     """Run on one MI355X (gfx950) through libtempest_hip.
 
-    Options as CUDATarget's (target.jl:30-75): ``precision`` for products
-    (``:full`` here means fp32 stays fp32; bf16 products accumulate in fp32),
-    ``online`` (permits the online softmax), ``rounded_backward``,
-    ``deterministic`` (every kernel of this library is: no atomics whose order
-    changes a sum, fixed reduction trees).
+    Options as CUDATarget's (target.jl:30-75): ``precision`` for products of
+    fp32 factors, ``"full"`` (fp32 on the fp32 matrix cores) or ``"bf16x3"``
+    (each factor split hi + lo in bf16 and three bf16 products summed in
+    fp32, TH_GEMM_BF16X3: the counterpart of CUDA's ``:tf32x3``); half
+    factors always accumulate in fp32.  ``online`` (permits the online
+    softmax), ``rounded_backward``, ``deterministic`` (every kernel here folds
+    in a fixed order but the floor's folds by key, which add by atomics unless
+    their groups run in order, FloorGroup(ordered=True)).
     """
 
     def __init__(self, implementations: Sequence = (), device: int = 0, precision: str = "full",
-                 online: bool = True, rounded_backward: bool = True, deterministic: bool = True):
-        if precision not in ("full",):
-            raise ValueError(f"precision must be 'full' on this target, got {precision!r}")
+                 online: bool = True, rounded_backward: bool = True, deterministic: bool = False):
+        if precision not in ("full", "bf16x3"):
+            raise ValueError(f"precision must be 'full' or 'bf16x3' on this target, got {precision!r}")
         self.implementations = tuple(implementations)
         self.device = device
         self.precision = precision
@@ -142,6 +145,14 @@ class HIPTarget:
 
     def deterministic(self) -> bool:
         return self.deterministic_
+
+    def product_class(self, dtype: torch.dtype) -> str:  # cover/cost.jl:132
+        """Half factors by their type; fp32 ones by the precision they run in."""
+        return {torch.bfloat16: "BFloat16", torch.float16: "Float16"}.get(dtype, self.precision)
+
+    def product_options(self, dtype: torch.dtype) -> dict:
+        """The gemm keywords this target's precision gives a product of `dtype` factors."""
+        return {"bf16x3": True} if dtype == torch.float32 and self.precision == "bf16x3" else {}
 
     # -- storage ------------------------------------------------------------------
 

@@ -588,3 +588,19 @@ def test_checks_catch_planted_defects():
     # No package_of: the rates file's `HIP` lines would be looked up as `HIPExt`.
     planted = _plant("package_of(::HIPLibrary) = :HIP\n", "")
     assert any(p.startswith("package_of:") for p in library_problems(planted))
+
+
+def test_gemm_flags_match_the_header():
+    """The product flags the binding sets are the header's TH_GEMM_* values,
+    and HIPTarget's precision reaches the descriptor (bf16x3 for Float32
+    factors with a Float32 result only)."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER, flags=re.S)
+    want = {n: int(v) for n, v in re.findall(r"#define TH_GEMM_(\w+) (\d+)", text)}
+    got = re.search(r"const GEMM_F32_FACTORS, GEMM_F16_FACTORS, GEMM_ACCUMULATE, GEMM_BF16X3 = "
+                    r"Int32\((\d+)\), Int32\((\d+)\), Int32\((\d+)\), Int32\((\d+)\)", JL)
+    assert got, "GEMM flag constants"
+    assert [int(x) for x in got.groups()] == [want["F32_FACTORS"], want["F16_FACTORS"], want["ACCUMULATE"],
+                                               want["BF16X3"]]
+    assert "x3 = precision === :bf16x3 && T === Float32 && R === Float32 ? GEMM_BF16X3 : Int32(0)" in JL
+    assert JL.count("gemm_desc(b; precision = t.precision)") == 2
+    assert "precision in (:full, :bf16x3) ||" in JL
