@@ -429,6 +429,50 @@ def config4(target, steps: int = 3, warmup: int = 1, recompute_dq: bool = False)
                              "the dK/dV sweep stores dS, a dQ sweep reads it")}}
 
 
+def attention_head_dims(target, steps: int = 3, warmup: int = 1):
+    """Causal attention forward + backward at B8 H16 S4096 with head dims 64
+    and 256 (the matrix-core kernels for head dims other than the tuned
+    128), bf16, and 128 at S4095, a length the tuned kernels do not take.
+    TFLOP/s counts the FA2 flops of the visible (query, key) pairs:
+    forward 4 D pairs per (batch, head), backward 2.5x that."""
+    import torch
+    import tempest_hip.launch as L
+    out = {}
+    for D, S in ((64, 4096), (256, 4096), (128, 4095)):
+        B, H = 8, 16
+        gen = torch.Generator(device="cuda").manual_seed(40 + D)
+        q, k, v, g = (torch.randn(B, S, H, D, device="cuda", generator=gen).to(torch.bfloat16) for _ in range(4))
+        o, lse = torch.empty_like(q), torch.empty(B, S, H, device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        fwd = L.attention_fwd(B, H, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              causal=True, head_dim=D)
+        bwd = L.attention_bwd(B, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              g.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), causal=True, head_dim=D)
+        for _ in range(warmup):
+            fwd()
+            bwd()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        t_f = t_b = 0.0
+        for _ in range(steps):
+            ev[0].record()
+            fwd()
+            ev[1].record()
+            bwd()
+            ev[2].record()
+            torch.cuda.synchronize()
+            t_f += ev[0].elapsed_time(ev[1]) * 1e-3 / steps
+            t_b += ev[1].elapsed_time(ev[2]) * 1e-3 / steps
+        ff, fb = fwd.work().flops, bwd.work().flops
+        out[f"B{B}_H{H}_S{S}_d{D}_causal"] = {
+            "fwd": {"ms": t_f * 1e3, "TFLOP/s": ff / t_f / 1e12}, "bwd": {"ms": t_b * 1e3, "TFLOP/s": fb / t_b / 1e12},
+            "ms_per_step": (t_f + t_b) * 1e3, "TFLOP/s": (ff + fb) / (t_f + t_b) / 1e12,
+            "frac_of_bf16_peak": (ff + fb) / (t_f + t_b) / BF16_PEAK, "kernels": [fwd.describe(), bwd.describe()]}
+        log(f"attention d{D} S{S}:", json.dumps({kk: out[f"B{B}_H{H}_S{S}_d{D}_causal"][kk]
+                                                 for kk in ("ms_per_step", "TFLOP/s")}))
+    return out
+
+
 def gemm_tiles(target, runs: int = 20):
     """The product's tile choices (not a config of its own): for each shape,
     every kernel that takes it at the split the library would choose, timed as
@@ -593,7 +637,8 @@ def main() -> int:
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
-                                       "config5", "gemm_tiles", "gemm_f32", "dispatch"], default=None,
+                                       "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims"],
+                    default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy, 10 times: the known-size kernel that "
@@ -625,7 +670,7 @@ def main() -> int:
         return 0
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
-              "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows,
+              "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows, "attention_head_dims": attention_head_dims,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
@@ -667,6 +712,10 @@ def main() -> int:
         except Exception as err:
             configs["config4_attention"] = {"error": repr(err)}
         log("config4:", json.dumps(configs["config4_attention"]))
+        try:
+            configs["attention_head_dims"] = attention_head_dims(target)
+        except Exception as err:
+            configs["attention_head_dims"] = {"error": repr(err)}
         try:
             configs["config5_deltanet"] = config5(target)
         except Exception as err:

@@ -1,0 +1,629 @@
+// Op class (c) on the matrix cores at head dims 64, 128 and 256 and any
+// lengths: what the tuned kernels of attention.hip (head dim 128, lengths in
+// 128s) do not take, short of fp32 arrays and device-held masks, which stay
+// on attention_generic.hip.  The reference's cuDNN claim takes half
+// precision d <= 256 on tensor cores (ext/cuDNNExt.jl:90-100) and its cuTile
+// sweep any tile (ext/cuTileExt/build.jl:326-493); d = 64 and d = 256 are
+// the head dims models use beside 128.
+//
+// bf16 operands, v_mfma_f32_32x32x16_bf16, fp32 statistics; the forms of the
+// tuned kernels, simpler: tiles of 64 positions x D in LDS as plain rows of
+// D + 8 bf16 (16-byte reads along a row, ds_read_b64_tr_b16 down a column),
+// staged through registers one step ahead (zeros past the sequence), one
+// barrier a step.
+//   forward: a workgroup of four waves per 128 queries, 32 a wave; S' = K Q'
+//     (keys on registers, queries on lanes), online softmax in exp2 units,
+//     O' += V' P' with P rounded to bf16 (folds.jl:186-222), lse = m + log(l);
+//   backward (FA2's formulas, deterministic, no workspace beyond delta):
+//     dK, dV: a workgroup per 128 keys (32 a wave, K and V rows in registers)
+//     sweeping the query tiles of each query head of its group, S = Q K',
+//     dP = dO V', P = exp(S - lse), dS = P (dP - delta), dV' += dO' P,
+//     dK' += Q' dS; at d = 256 each workgroup keeps half of dK' and dV'
+//     (grid twice as wide, the scores computed by both halves) so that its
+//     accumulators fit one wave's registers;
+//     dQ: a workgroup per 128 queries sweeping key tiles, S' and dP'
+//     recomputed, dQ' += K' dS'.
+// Masks: keys past the keys' length and, causal, keys after the query
+// (key <= query, positions from 0) weigh 0; queries past the sequence are
+// computed on zeros and not stored.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "th_core.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct MArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;  // natural log, [b][s][h]
+  const uint16_t* dout;
+  float* delta;  // backward workspace: rowsum(dO .* O), [b][s][h]
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t q_sh, q_ss, q_sb;  // strides (elements) of q, o, dout, dq
+  int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
+  int32_t seq, kv_seq, heads, kv_heads, batch, causal;
+  float scale;
+};
+
+__device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+// The value lane l ^ 32 holds.
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(threadIdx.x % 64 < 32 ? r[1] : r[0]);
+}
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// A operand from a tile (rows of D + 8 bf16), M along its rows: rows
+// r0 + lane % 32, k = columns 16 ks + 8 (lane / 32) + (0..7).
+template <int D>
+__device__ __forceinline__ bf16x8 frag_rows(const uint16_t* t, int r0, int ks) {
+  const int lane = threadIdx.x % 64;
+  return *reinterpret_cast<const bf16x8*>(t + (r0 + lane % 32) * (D + 8) + 16 * ks + 8 * (lane / 32));
+}
+
+// A operand from a tile, M along its columns: m = column d0 + lane % 32, k
+// = the 16 rows of step ks in the order the accumulator's registers give the
+// B operand (k-slot 8 h + e <-> row 16 ks + 8 (e / 4) + 4 h + e % 4, h =
+// lane / 32).  ds_read_b64_tr_b16 hands lane i of each 16 element i % 4 of
+// the 8-byte pieces addressed by lanes 4 k + i / 4; lane j here addresses row
+// base + j / 4, columns dgrp + 4 (j % 4) + (0..3), so lane i receives rows
+// base + (0..3) of column dgrp + i; two reads cover the eight rows.
+template <int D>
+__device__ __forceinline__ bf16x8 frag_tr(const uint16_t* t, int d0, int ks) {
+  const int lane = threadIdx.x % 64, j = lane % 16;
+  const int col = d0 + 16 * ((lane / 16) % 2) + 4 * (j % 4);
+  const int row = 16 * ks + 4 * (lane / 32) + j / 4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + row * (D + 8) + col));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + (row + 8) * (D + 8) + col));
+  const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// A row of a (position-major) operand as the B operand of a product over d:
+// d = 16 ks + 8 (lane / 32) + (0..7); zeros for a position past the end.
+template <int D>
+__device__ __forceinline__ void row_operand(const uint16_t* row, bool live, bf16x8 (&f)[D / 16]) {
+  const int lane = threadIdx.x % 64;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    f[ks] = live ? *reinterpret_cast<const bf16x8*>(row + 16 * ks + 8 * (lane / 32)) : bf16x8{};
+}
+
+// A 64-position tile of an operand staged through registers: thread t holds
+// the 16-byte chunks t + 256 i; rows past `limit` read as zeros.
+template <int D>
+struct Stage {
+  static constexpr int kChunks = D / 8;          // per row
+  static constexpr int kPer = 64 * kChunks / 256;  // per thread
+  u32x4 r[kPer];
+  __device__ void load(const uint16_t* base, int64_t ss, int row0, int limit) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i, row = c / kChunks, col = c % kChunks;
+      r[i] = row0 + row < limit ? *reinterpret_cast<const u32x4*>(base + (int64_t)(row0 + row) * ss + 8 * col)
+                                : u32x4{0, 0, 0, 0};
+    }
+  }
+  __device__ void store(uint16_t* t) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i, row = c / kChunks, col = c % kChunks;
+      *reinterpret_cast<u32x4*>(t + row * (D + 8) + 8 * col) = r[i];
+    }
+  }
+};
+
+template <int D>
+constexpr int kTile = 64 * (D + 8);  // bf16 elements of a tile in LDS
+
+// ---- forward ---------------------------------------------------------------------
+
+template <int D>
+__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void mfma_attn_fwd(MArgs p) {
+  constexpr int NS = D / 16, NB = D / 32;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.heads / p.kv_heads);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
+  const int q0 = qb * 128 + wave * 32, query = q0 + lr;
+  const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  bf16x8 qf[NS];
+  row_operand<D>(qbase + (int64_t)query * p.q_ss, query < p.seq, qf);
+  f32x16 o[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) o[i] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+  const float c = p.scale * kLog2e;
+  const int qlast = min(qb * 128 + 127, p.seq - 1);
+  const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
+  const int nsteps = (kend + 63) / 64;
+  Stage<D> sk, sv;
+  auto K = [&](int s) { return lds + 2 * s * kTile<D>; };
+  auto V = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
+  if (nsteps > 0) {
+    sk.load(kbase, p.k_ss, 0, p.kv_seq);
+    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.store(K(0));
+    sv.store(V(0));
+  }
+  __syncthreads();
+  for (int j = 0; j < nsteps; ++j) {
+    const int cur = j & 1, k0 = 64 * j;
+    if (j + 1 < nsteps) {
+      sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
+      sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
+    }
+    // S' (64 keys x 32 queries): keys 32 kb + 8 (i / 4) + 4 lh + i % 4 in register i.
+    f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) s[kb] = mfma(frag_rows<D>(K(cur), 32 * kb, ks), qf[ks], s[kb]);
+    if (k0 + 64 > p.kv_seq || (p.causal && k0 + 64 > q0)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * lh + i % 4;
+          if (key >= p.kv_seq || (p.causal && key > query)) s[kb][i] = -INFINITY;
+        }
+    }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[kb][i]);
+    mb = fmaxf(mb, other_half(mb)) * c;
+    const float mn = fmaxf(m, mb);
+    const float shift = isfinite(mn) ? mn : 0.0f;  // lse_shift (folds.jl:194)
+    const float alpha = __builtin_amdgcn_exp2f(m - shift);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) o[i] *= alpha;
+    m = mn;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float w0 = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * part + 2 * e], c, -shift));
+          const float w1 = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * part + 2 * e + 1], c, -shift));
+          l += w0 + w1;
+          w[e] = pack2(w0, w1);
+        }
+        pf[2 * kb + part] = (bf16x8)w;
+      }
+    // O' (D x 32 queries) += V' P', the weights rounded to bf16.
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < NB; ++db) o[db] = mfma(frag_tr<D>(V(cur), 32 * db, ks), pf[ks], o[db]);
+    if (j + 1 < nsteps) {
+      // The other stage was last read in step j - 1, before the barrier that ended it.
+      sk.store(K(cur ^ 1));
+      sv.store(V(cur ^ 1));
+    }
+    __syncthreads();
+  }
+  l += other_half(l);
+  if (query >= p.seq) return;
+  const float inv = 1.0f / l;
+  uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
+#pragma unroll
+  for (int db = 0; db < NB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * lh;
+      *reinterpret_cast<u32x2*>(obase + d) =
+          u32x2{pack2(o[db][4 * g] * inv, o[db][4 * g + 1] * inv), pack2(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv)};
+    }
+  if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
+}
+
+// ---- backward: delta = rowsum(dO .* O) ---------------------------------------------
+
+struct DeltaArgs {
+  MArgs p;  // first: its members sit at MArgs' offsets
+  int32_t d;
+};
+
+__global__ __launch_bounds__(256) void mfma_attn_delta(DeltaArgs a) {
+  const MArgs& p = a.p;
+  const int d = a.d;
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;  // [b][s][h]
+  const int64_t total = (int64_t)p.batch * p.seq * p.heads;
+  if (row >= total) return;
+  const int h = (int)(row % p.heads);
+  const int64_t s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
+  const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss;
+  float v = 0.0f;
+  for (int c = threadIdx.x % 64; c < d; c += 64) v += bf16_float(p.o[at + c]) * bf16_float(p.dout[at + c]);
+  v = thd::wave_sum(v);
+  if (threadIdx.x % 64 == 0) p.delta[row] = v;
+}
+
+// ---- backward: dK, dV ----------------------------------------------------------------
+// A workgroup takes 128 keys (32 a wave) and DO of the D features of dK and
+// dV (D, or half of 256).  Per query tile of 64: S (64 queries x 32 keys)
+// with queries on the registers and keys on the lanes, so that P and dS feed
+// the products over queries straight from the accumulators.
+
+template <int D, int DO>
+__global__ __launch_bounds__(256, 1) void mfma_attn_dkdv(MArgs p) {
+  constexpr int NS = D / 16, NBO = DO / 32, halves = D / DO;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  float* stats = reinterpret_cast<float*>(lds + 4 * kTile<D>);  // [stage][lse * log2e (64) | delta (64)]
+  const int kblk = blockIdx.x / halves, dh = blockIdx.x % halves;
+  const int hk = blockIdx.y, b = blockIdx.z;
+  const int group = p.heads / p.kv_heads;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
+  const int kw0 = kblk * 128, key = kw0 + wave * 32 + lr;
+  const int64_t koff = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  bf16x8 kf[NS], vf[NS];
+  row_operand<D>(p.k + koff + (int64_t)key * p.k_ss, key < p.kv_seq, kf);
+  row_operand<D>(p.v + koff + (int64_t)key * p.k_ss, key < p.kv_seq, vf);
+  f32x16 dk[NBO], dv[NBO];
+#pragma unroll
+  for (int i = 0; i < NBO; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
+  const float c = p.scale * kLog2e;
+  auto Q = [&](int s) { return lds + 2 * s * kTile<D>; };
+  auto G = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
+  auto Ls = [&](int s) { return stats + 128 * s; };
+  const int qstart = p.causal ? kw0 / 64 * 64 : 0;
+  const int nsteps = qstart < p.seq ? (p.seq - qstart + 63) / 64 : 0;
+  Stage<D> sq, sg;
+  float st = 0.0f;  // threads 0..127: a query's lse * log2e or delta
+  auto load = [&](const uint16_t* qbase, const uint16_t* gbase, int h, int q0) {
+    sq.load(qbase, p.q_ss, q0, p.seq);
+    sg.load(gbase, p.q_ss, q0, p.seq);
+    if (threadIdx.x < 128) {
+      const int j = q0 + threadIdx.x % 64;
+      const int64_t row = ((int64_t)b * p.seq + j) * p.heads + h;
+      st = j < p.seq ? (threadIdx.x < 64 ? p.lse[row] * kLog2e : p.delta[row]) : 0.0f;
+    }
+  };
+  auto store = [&](int s) {
+    sq.store(Q(s));
+    sg.store(G(s));
+    if (threadIdx.x < 128) Ls(s)[threadIdx.x] = st;
+  };
+  for (int h = hk * group; h < (hk + 1) * group; ++h) {
+    const uint16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const uint16_t* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    if (nsteps > 0) {
+      load(qbase, gbase, h, qstart);
+      store(0);
+    }
+    __syncthreads();
+    for (int j = 0; j < nsteps; ++j) {
+      const int cur = j & 1, qq0 = qstart + 64 * j;
+      if (j + 1 < nsteps) load(qbase, gbase, h, qq0 + 64);
+      const uint16_t *Qt = Q(cur), *Gt = G(cur);
+      const float* L = Ls(cur);
+      // S = Q K', dP = dO V' (64 queries x 32 keys): query 32 jj + 8 (i / 4) + 4 lh + i % 4 in register i.
+      f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+      for (int ks = 0; ks < NS; ++ks)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          s[jj] = mfma(frag_rows<D>(Qt, 32 * jj, ks), kf[ks], s[jj]);
+          dp[jj] = mfma(frag_rows<D>(Gt, 32 * jj, ks), vf[ks], dp[jj]);
+        }
+      bf16x8 pf[4], sf[4];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          u32x4 wp, wd;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float w[2], x[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int i = 8 * part + 2 * e + u;
+              const int qi = 32 * jj + 8 * (i / 4) + 4 * lh + i % 4, query = qq0 + qi;
+              const bool seen = query < p.seq && key < p.kv_seq && (!p.causal || key <= query);
+              w[u] = seen ? __builtin_amdgcn_exp2f(fmaf(s[jj][i], c, -L[qi])) : 0.0f;
+              x[u] = w[u] * (dp[jj][i] - L[64 + qi]);
+            }
+            wp[e] = pack2(w[0], w[1]);
+            wd[e] = pack2(x[0], x[1]);
+          }
+          pf[2 * jj + part] = (bf16x8)wp;
+          sf[2 * jj + part] = (bf16x8)wd;
+        }
+      // dV' (DO features x 32 keys) += dO' P;  dK' += Q' dS.
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int db = 0; db < NBO; ++db) {
+          dv[db] = mfma(frag_tr<D>(Gt, DO * dh + 32 * db, ks), pf[ks], dv[db]);
+          dk[db] = mfma(frag_tr<D>(Qt, DO * dh + 32 * db, ks), sf[ks], dk[db]);
+        }
+      if (j + 1 < nsteps) store(cur ^ 1);
+      __syncthreads();
+    }
+  }
+  if (key >= p.kv_seq) return;
+  const int64_t out = koff + (int64_t)key * p.k_ss;
+#pragma unroll
+  for (int db = 0; db < NBO; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = DO * dh + 32 * db + 8 * g + 4 * lh;
+      const float sc = p.scale;
+      *reinterpret_cast<u32x2*>(p.dk + out + d) =
+          u32x2{pack2(dk[db][4 * g] * sc, dk[db][4 * g + 1] * sc), pack2(dk[db][4 * g + 2] * sc, dk[db][4 * g + 3] * sc)};
+      *reinterpret_cast<u32x2*>(p.dv + out + d) =
+          u32x2{pack2(dv[db][4 * g], dv[db][4 * g + 1]), pack2(dv[db][4 * g + 2], dv[db][4 * g + 3])};
+    }
+}
+
+// ---- backward: dQ ----------------------------------------------------------------------
+// A workgroup takes 128 queries (32 a wave) and sweeps key tiles of 64:
+// S' = K Q', dP' = V dO' (keys on the registers, queries on the lanes),
+// dS' = P' (dP' - delta), dQ' (D x 32 queries) += K' dS'.
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void mfma_attn_dq(MArgs p) {
+  constexpr int NS = D / 16, NB = D / 32;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.heads / p.kv_heads);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
+  const int q0 = qb * 128 + wave * 32, query = q0 + lr;
+  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
+  const bool live = query < p.seq;
+  bf16x8 qf[NS], gf[NS];
+  row_operand<D>(p.q + qoff, live, qf);
+  row_operand<D>(p.dout + qoff, live, gf);
+  const int64_t srow = ((int64_t)b * p.seq + query) * p.heads + h;
+  const float l2 = live ? p.lse[srow] * kLog2e : 0.0f;
+  const float dl = live ? p.delta[srow] : 0.0f;
+  const float c = p.scale * kLog2e;
+  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  f32x16 dq[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) dq[i] = f32x16{};
+  const int qlast = min(qb * 128 + 127, p.seq - 1);
+  const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
+  const int nsteps = (kend + 63) / 64;
+  Stage<D> sk, sv;
+  auto K = [&](int s) { return lds + 2 * s * kTile<D>; };
+  auto V = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
+  if (nsteps > 0) {
+    sk.load(kbase, p.k_ss, 0, p.kv_seq);
+    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.store(K(0));
+    sv.store(V(0));
+  }
+  __syncthreads();
+  for (int j = 0; j < nsteps; ++j) {
+    const int cur = j & 1, k0 = 64 * j;
+    if (j + 1 < nsteps) {
+      sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
+      sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
+    }
+    f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int ks = 0; ks < NS; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        s[kb] = mfma(frag_rows<D>(K(cur), 32 * kb, ks), qf[ks], s[kb]);
+        dp[kb] = mfma(frag_rows<D>(V(cur), 32 * kb, ks), gf[ks], dp[kb]);
+      }
+    bf16x8 sf[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int i = 8 * part + 2 * e + u;
+            const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * lh + i % 4;
+            const bool seen = key < p.kv_seq && (!p.causal || key <= query);
+            const float pw = seen ? __builtin_amdgcn_exp2f(fmaf(s[kb][i], c, -l2)) : 0.0f;
+            x[u] = pw * (dp[kb][i] - dl);
+          }
+          w[e] = pack2(x[0], x[1]);
+        }
+        sf[2 * kb + part] = (bf16x8)w;
+      }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < NB; ++db) dq[db] = mfma(frag_tr<D>(K(cur), 32 * db, ks), sf[ks], dq[db]);
+    if (j + 1 < nsteps) {
+      sk.store(K(cur ^ 1));
+      sv.store(V(cur ^ 1));
+    }
+    __syncthreads();
+  }
+  if (!live) return;
+  uint16_t* out = p.dq + qoff;
+#pragma unroll
+  for (int db = 0; db < NB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * lh;
+      const float sc = p.scale;
+      *reinterpret_cast<u32x2*>(out + d) =
+          u32x2{pack2(dq[db][4 * g] * sc, dq[db][4 * g + 1] * sc), pack2(dq[db][4 * g + 2] * sc, dq[db][4 * g + 3] * sc)};
+    }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+MArgs margs_of(const th_attention_desc* d) {
+  MArgs a{};
+  a.q = static_cast<const uint16_t*>(d->q);
+  a.k = static_cast<const uint16_t*>(d->k);
+  a.v = static_cast<const uint16_t*>(d->v);
+  a.o = static_cast<uint16_t*>(d->o);
+  a.lse = d->lse;
+  a.dout = static_cast<const uint16_t*>(d->dout);
+  a.dq = static_cast<uint16_t*>(d->dq);
+  a.dk = static_cast<uint16_t*>(d->dk);
+  a.dv = static_cast<uint16_t*>(d->dv);
+  a.q_sh = d->q_strides[0], a.q_ss = d->q_strides[1], a.q_sb = d->q_strides[2];
+  a.k_sh = d->k_strides[0], a.k_ss = d->k_strides[1], a.k_sb = d->k_strides[2];
+  a.seq = d->seq;
+  a.kv_seq = d->kv_seq > 0 ? d->kv_seq : d->seq;
+  a.heads = d->heads, a.kv_heads = d->kv_heads, a.batch = d->batch, a.causal = d->causal;
+  a.scale = d->scale > 0 ? d->scale : 1.0f / sqrtf((float)d->head_dim);
+  return a;
+}
+
+// (query, key) pairs the mask leaves: the algorithmic work's count.
+double visible_pairs(const MArgs& a) {
+  const double S = a.seq, K = a.kv_seq;
+  if (!a.causal) return S * K;
+  // sum over queries q of min(q + 1, K)
+  const double full = std::min(S, K);
+  return full * (full + 1) / 2 + std::max(0.0, S - K) * K;
+}
+
+template <int D>
+int fwd_launch(const th_attention_desc* d, th_launch** out) {
+  const size_t lds = 4 * (size_t)kTile<D> * sizeof(uint16_t);
+  TH_HIP(hipFuncSetAttribute((const void*)mfma_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  MArgs a = margs_of(d);
+  th::Builder b("attention_fwd_mfma", 7);
+  const dim3 grid((unsigned)((d->seq + 127) / 128), d->heads, d->batch);
+  int k = b.kernel((const void*)mfma_attn_fwd<D>, D == 64 ? "mfma_attn_fwd_d64" : D == 128 ? "mfma_attn_fwd_d128"
+                                                                                          : "mfma_attn_fwd_d256",
+                   grid, dim3(256), (uint32_t)lds, a);
+  b.ref(0, k, TH_OFFSET(MArgs, q));
+  b.ref(1, k, TH_OFFSET(MArgs, k));
+  b.ref(2, k, TH_OFFSET(MArgs, v));
+  b.ref(3, k, TH_OFFSET(MArgs, o));
+  b.ref(4, k, TH_OFFSET(MArgs, lse));
+  for (int v = 0; v < 4; ++v) b.align(v, 16);
+  const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
+  b.work(2.0 * BH * a.seq * D * 2 + 2.0 * BHk * a.kv_seq * D * 2 + 4.0 * BH * a.seq, 4.0 * BH * D * visible_pairs(a),
+         (int64_t)grid.x * grid.y * grid.z);
+  *out = b.release();
+  return TH_OK;
+}
+
+template <int D>
+int bwd_launch(const th_attention_desc* d, th_launch** out) {
+  constexpr int DO = D == 256 ? 128 : D;
+  const size_t lds_kv = 4 * (size_t)kTile<D> * sizeof(uint16_t);
+  const size_t lds_dkdv = lds_kv + 2 * 128 * sizeof(float);
+  TH_HIP(hipFuncSetAttribute((const void*)mfma_attn_dkdv<D, DO>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)lds_dkdv));
+  TH_HIP(hipFuncSetAttribute((const void*)mfma_attn_dq<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_kv));
+  MArgs a = margs_of(d);
+  th::Builder b("attention_bwd_mfma", 11);
+  const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+  const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));
+  int k0 = b.kernel((const void*)mfma_attn_delta, "mfma_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                    DeltaArgs{a, D});
+  const dim3 gkv((unsigned)((a.kv_seq + 127) / 128 * (D / DO)), d->kv_heads, d->batch);
+  const dim3 gq((unsigned)((d->seq + 127) / 128), d->heads, d->batch);
+  int k1 = b.kernel((const void*)mfma_attn_dkdv<D, DO>, D == 64 ? "mfma_attn_dkdv_d64" : D == 128 ? "mfma_attn_dkdv_d128"
+                                                                                               : "mfma_attn_dkdv_d256",
+                    gkv, dim3(256), (uint32_t)lds_dkdv, a);
+  int k2 = b.kernel((const void*)mfma_attn_dq<D>, D == 64 ? "mfma_attn_dq_d64" : D == 128 ? "mfma_attn_dq_d128"
+                                                                                       : "mfma_attn_dq_d256",
+                    gq, dim3(256), (uint32_t)lds_kv, a);
+  const size_t offs[9] = {TH_OFFSET(MArgs, q),  TH_OFFSET(MArgs, k),  TH_OFFSET(MArgs, v),
+                          TH_OFFSET(MArgs, o),  TH_OFFSET(MArgs, lse), TH_OFFSET(MArgs, dout),
+                          TH_OFFSET(MArgs, dq), TH_OFFSET(MArgs, dk),  TH_OFFSET(MArgs, dv)};
+  // The delta kernel's arguments are MArgs followed by d: the same offsets.
+  for (int v = 0; v < 9; ++v)
+    for (int kk : {k0, k1, k2}) b.ref(v, kk, offs[v]);
+  for (int kk : {k0, k1, k2}) b.ws_ref(kk, TH_OFFSET(MArgs, delta), at_delta);
+  for (int v : {0, 1, 2, 3, 5, 6, 7, 8}) b.align(v, 16);
+  const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
+  b.work(2.0 * BH * a.seq * D * 4 + 2.0 * BHk * a.kv_seq * D * 4 + 8.0 * BH * a.seq,
+         2.5 * 4.0 * BH * D * visible_pairs(a), (int64_t)gkv.x * gkv.y * gkv.z);
+  *out = b.release();
+  return TH_OK;
+}
+
+int check_mfma(const th_attention_desc* d, bool backward) {
+  TH_REQUIRE(d->q && d->k && d->v && d->o, "attention: null q, k, v or o");
+  TH_REQUIRE(aligned16(d->q) && aligned16(d->k) && aligned16(d->v) && aligned16(d->o),
+             "attention: q, k, v, o must be 16-byte aligned");
+  if (backward) {
+    TH_REQUIRE(d->lse && d->dout && d->dq && d->dk && d->dv, "attention backward: null lse, dout, dq, dk or dv");
+    TH_REQUIRE(aligned16(d->dout) && aligned16(d->dq) && aligned16(d->dk) && aligned16(d->dv),
+               "attention backward: dout, dq, dk, dv must be 16-byte aligned");
+  }
+  return TH_OK;
+}
+
+}  // namespace
+
+namespace th {
+
+// bf16 arrays, head dim 64, 128 or 256, any positive lengths, no
+// device-held masks, 16-byte rows, operands and strides.
+bool mfma_attention_takes(const th_attention_desc* d) {
+  if (!d || (d->flags & TH_ATTN_F32) || d->starts || d->lengths) return false;
+  if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return false;
+  if (d->seq < 1 || d->kv_seq < 0 || d->batch < 1 || d->heads < 1 || d->kv_heads < 1 || d->heads % d->kv_heads)
+    return false;
+  for (int64_t s : {d->q_strides[0], d->q_strides[1], d->q_strides[2], d->k_strides[0], d->k_strides[1], d->k_strides[2]})
+    if (s <= 0 || s % 8) return false;
+  const int64_t kv = d->kv_seq > 0 ? d->kv_seq : d->seq;
+  return (d->seq + 127) / 128 <= 0x7fffffff && (kv + 127) / 128 * 2 <= 0x7fffffff && d->heads <= 65535 &&
+         d->batch <= 65535;
+}
+
+int build_attention_mfma_fwd(const th_attention_desc* d, th_launch** out) {
+  if (int r = check_mfma(d, false)) return r;
+  switch (d->head_dim) {
+    case 64: return fwd_launch<64>(d, out);
+    case 128: return fwd_launch<128>(d, out);
+    default: return fwd_launch<256>(d, out);
+  }
+}
+
+int build_attention_mfma_bwd(const th_attention_desc* d, th_launch** out) {
+  if (int r = check_mfma(d, true)) return r;
+  switch (d->head_dim) {
+    case 64: return bwd_launch<64>(d, out);
+    case 128: return bwd_launch<128>(d, out);
+    default: return bwd_launch<256>(d, out);
+  }
+}
+
+}  // namespace th

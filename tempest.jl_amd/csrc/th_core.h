@@ -194,6 +194,11 @@ int device_alloc(size_t bytes, void** out);
 // Attention for what the matrix-core kernels do not take (attention_generic.hip).
 int build_attention_general_fwd(const th_attention_desc* d, th_launch** out);
 int build_attention_general_bwd(const th_attention_desc* d, th_launch** out);
+// Attention on the matrix cores at head dims 64, 128 and 256 and any lengths
+// (attention_mfma.hip): what the tuned kernels do not take, bf16, no masks.
+bool mfma_attention_takes(const th_attention_desc* d);
+int build_attention_mfma_fwd(const th_attention_desc* d, th_launch** out);
+int build_attention_mfma_bwd(const th_attention_desc* d, th_launch** out);
 // Products the bf16 tile kernel does not take (gemm_general.hip).
 int build_gemm_general(const th_gemm_desc* d, th_launch** out);
 
