@@ -141,13 +141,22 @@ struct Stage {
 template <int D>
 constexpr int kTile = 64 * (D + 8);  // bf16 elements of a tile in LDS
 
+// Causal sweeps do less work for earlier query blocks (and later key
+// blocks): workgroup x takes blocks x and nb - 1 - x, so every workgroup
+// sweeps about the same number of tiles.
+template <class F>
+__device__ __forceinline__ void mirrored(bool causal, int x, int nb, F&& f) {
+  f(x);
+  if (causal && 2 * x + 1 != nb) f(nb - 1 - x);
+}
+
 // ---- forward ---------------------------------------------------------------------
 
 template <int D>
-__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void mfma_attn_fwd(MArgs p) {
+__device__ __forceinline__ void fwd_block(const MArgs& p, const int qb) {
   constexpr int NS = D / 16, NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lr;
@@ -250,6 +259,11 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void mfma_attn_fwd(MArgs p) 
   if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
 }
 
+template <int D>
+__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void mfma_attn_fwd(MArgs p) {
+  mirrored(p.causal, blockIdx.x, (p.seq + 127) / 128, [&](int qb) { fwd_block<D>(p, qb); });
+}
+
 // ---- backward: delta = rowsum(dO .* O) ---------------------------------------------
 
 struct DeltaArgs {
@@ -279,11 +293,10 @@ __global__ __launch_bounds__(256) void mfma_attn_delta(DeltaArgs a) {
 // the products over queries straight from the accumulators.
 
 template <int D, int DO>
-__global__ __launch_bounds__(256, 1) void mfma_attn_dkdv(MArgs p) {
-  constexpr int NS = D / 16, NBO = DO / 32, halves = D / DO;
+__device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const int dh) {
+  constexpr int NS = D / 16, NBO = DO / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   float* stats = reinterpret_cast<float*>(lds + 4 * kTile<D>);  // [stage][lse * log2e (64) | delta (64)]
-  const int kblk = blockIdx.x / halves, dh = blockIdx.x % halves;
   const int hk = blockIdx.y, b = blockIdx.z;
   const int group = p.heads / p.kv_heads;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
@@ -389,16 +402,24 @@ __global__ __launch_bounds__(256, 1) void mfma_attn_dkdv(MArgs p) {
     }
 }
 
+template <int D, int DO>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void mfma_attn_dkdv(MArgs p) {
+  constexpr int halves = D / DO;
+  const int kv = p.kv_seq;
+  mirrored(p.causal, blockIdx.x / halves, (kv + 127) / 128,
+           [&](int kblk) { dkdv_block<D, DO>(p, kblk, blockIdx.x % halves); });
+}
+
 // ---- backward: dQ ----------------------------------------------------------------------
 // A workgroup takes 128 queries (32 a wave) and sweeps key tiles of 64:
 // S' = K Q', dP' = V dO' (keys on the registers, queries on the lanes),
 // dS' = P' (dP' - delta), dQ' (D x 32 queries) += K' dS'.
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void mfma_attn_dq(MArgs p) {
+__device__ __forceinline__ void dq_block(const MArgs& p, const int qb) {
   constexpr int NS = D / 16, NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lr;
@@ -487,7 +508,19 @@ __global__ __launch_bounds__(256, 1) void mfma_attn_dq(MArgs p) {
     }
 }
 
+template <int D>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void mfma_attn_dq(MArgs p) {
+  mirrored(p.causal, blockIdx.x, (p.seq + 127) / 128, [&](int qb) { dq_block<D>(p, qb); });
+}
+
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Workgroups along a sequence of n positions in blocks of 128: causal ones
+// take a block and its mirror.
+unsigned blocks_of(int n, int causal) {
+  const unsigned nb = (unsigned)((n + 127) / 128);
+  return causal ? (nb + 1) / 2 : nb;
+}
 
 MArgs margs_of(const th_attention_desc* d) {
   MArgs a{};
@@ -524,7 +557,7 @@ int fwd_launch(const th_attention_desc* d, th_launch** out) {
   TH_HIP(hipFuncSetAttribute((const void*)mfma_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   MArgs a = margs_of(d);
   th::Builder b("attention_fwd_mfma", 7);
-  const dim3 grid((unsigned)((d->seq + 127) / 128), d->heads, d->batch);
+  const dim3 grid(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k = b.kernel((const void*)mfma_attn_fwd<D>, D == 64 ? "mfma_attn_fwd_d64" : D == 128 ? "mfma_attn_fwd_d128"
                                                                                           : "mfma_attn_fwd_d256",
                    grid, dim3(256), (uint32_t)lds, a);
@@ -555,8 +588,8 @@ int bwd_launch(const th_attention_desc* d, th_launch** out) {
   const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));
   int k0 = b.kernel((const void*)mfma_attn_delta, "mfma_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                     DeltaArgs{a, D});
-  const dim3 gkv((unsigned)((a.kv_seq + 127) / 128 * (D / DO)), d->kv_heads, d->batch);
-  const dim3 gq((unsigned)((d->seq + 127) / 128), d->heads, d->batch);
+  const dim3 gkv(blocks_of(a.kv_seq, d->causal) * (D / DO), d->kv_heads, d->batch);
+  const dim3 gq(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k1 = b.kernel((const void*)mfma_attn_dkdv<D, DO>, D == 64 ? "mfma_attn_dkdv_d64" : D == 128 ? "mfma_attn_dkdv_d128"
                                                                                                : "mfma_attn_dkdv_d256",
                     gkv, dim3(256), (uint32_t)lds_dkdv, a);
