@@ -578,6 +578,22 @@ def config5(target, steps: int = 3, warmup: int = 1):
                     "th_launch_work"}
 
 
+def matrix_rate(target) -> dict:
+    """The matrix cores' sustained bf16 rate on this device (th_matrix_rate):
+    register-only products on every SIMD, with one operand pair throughout
+    and with random operands changing every product, and the shader clock
+    the waves ran at.  The ceiling a product kernel's data meets here."""
+    import ctypes
+    from tempest_hip import _lib
+    out = {}
+    for name, vary in (("constant_operands", 0), ("random_operands", 1)):
+        f, c = ctypes.c_double(), ctypes.c_double()
+        _lib.call("th_matrix_rate", vary, ctypes.byref(f), ctypes.byref(c))
+        out[name] = {"PFLOP/s": f.value / 1e15, "frac_of_bf16_peak": f.value / BF16_PEAK, "clock_GHz": c.value / 1e9}
+    log("matrix rate:", json.dumps(out))
+    return out
+
+
 def dispatch_costs(target, reps: int = 2000):
     """Where a graph replay's time goes on this device: graphs of 1, 9 and 40
     near-empty launches (16-byte copies, th_build_copy), replayed back to back
@@ -637,7 +653,8 @@ def main() -> int:
     ap.add_argument("--only-config2", action="store_true",
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
-                                       "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims"],
+                                       "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims",
+                                       "matrix_rate"],
                     default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -671,6 +688,7 @@ def main() -> int:
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
               "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows, "attention_head_dims": attention_head_dims,
+              "matrix_rate": matrix_rate,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
@@ -706,6 +724,10 @@ def main() -> int:
             configs["config3_mlp"] = config3(target)
         except Exception as err:
             configs["config3_mlp"] = {"error": repr(err)}
+        try:
+            configs["config3_mlp"]["matrix_rate"] = matrix_rate(target)
+        except Exception as err:
+            configs["config3_mlp"]["matrix_rate"] = {"error": repr(err)}
         log("config3:", json.dumps(configs["config3_mlp"]))
         try:
             configs["config4_attention"] = config4(target)

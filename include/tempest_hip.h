@@ -226,6 +226,17 @@ int th_time_run(th_launch* launch, int warmup, int reps, double* host_seconds);
  * always records a graph (capture(::CUDATarget, ...), ext/CUDAExt.jl:565). */
 int th_dispatch_costs(double* graph_base, double* in_graph, double* direct);
 
+/* The matrix cores' sustained bf16 rate on this device, measured: every SIMD
+ * runs two waves of back-to-back v_mfma_f32_32x32x16_bf16 on register
+ * operands, one operand pair throughout (vary = 0) or eight pairs of random
+ * bits cycled so that each product's operands differ (vary = 1, as real
+ * data's do); flop/s over the run, and the shader clock the waves ran at
+ * (their clock counter against the 100 MHz real-time counter).  The ceiling
+ * any product kernel meets on this device, beside the data-sheet peak.  No
+ * reference counterpart: the reference fits product rates from products
+ * (cover/calibrate.jl). */
+int th_matrix_rate(int vary, double* host_flops_per_s, double* host_clock_hz);
+
 /* ---- op class (a): fused pointwise + reductions -------------------------- */
 
 /* Softmax over each contiguous run of n (a column of the reference's n x rows

@@ -142,6 +142,63 @@ __global__ __launch_bounds__(256) void th_copy_kernel(CopyArgs c) {
   }
 }
 
+
+// ---- the matrix cores' sustained rate ---------------------------------------------------
+// Every SIMD of the device runs two waves of back-to-back
+// v_mfma_f32_32x32x16_bf16 on operands held in registers (four independent
+// accumulators a wave): with one operand pair throughout, or with eight
+// pairs of random bits cycled so that every product's operands differ from
+// the last one's, as a real product's do.  Each wave reads the shader clock
+// counter and the 100 MHz real-time counter at its start and end, so the run
+// reports the clock the matrix cores actually ran at.
+typedef __bf16 th_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float th_f32x16 __attribute__((ext_vector_type(16)));
+
+struct RateArgs {
+  const u32x4* seed;   // 8 operand pairs' bits per lane
+  float* sink;         // written only if the sums come out as a value they never do
+  uint64_t* stamps;    // per workgroup: clock start, end, real-time start, end
+  int32_t iters;
+  int32_t vary;
+};
+
+__global__ __launch_bounds__(256, 2) void th_matrix_rate_kernel(RateArgs a) {
+  const int lane = threadIdx.x % 64;
+  th_bf16x8 A[8], B[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    A[s] = __builtin_bit_cast(th_bf16x8, a.seed[(2 * s) * 64 + lane]);
+    B[s] = __builtin_bit_cast(th_bf16x8, a.seed[(2 * s + 1) * 64 + lane]);
+  }
+  th_f32x16 acc[4] = {th_f32x16{}, th_f32x16{}, th_f32x16{}, th_f32x16{}};
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < a.iters; ++it) {
+    if (a.vary) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[s], B[(s + j) % 8], acc[j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], B[0], acc[j], 0, 0, 0);
+    }
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  float x = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x += acc[j][0] + acc[j][15];
+  if (x == 1234.5f) a.sink[blockIdx.x] = x;
+  if (threadIdx.x == 0) {
+    a.stamps[4 * blockIdx.x + 0] = t0;
+    a.stamps[4 * blockIdx.x + 1] = t1;
+    a.stamps[4 * blockIdx.x + 2] = r0;
+    a.stamps[4 * blockIdx.x + 3] = r1;
+  }
+}
+
 extern "C" {
 
 const char* th_last_error(void) { return g_error.c_str(); }
@@ -678,6 +735,16 @@ int th_graph_capture(th_launch* const* steps, int n, th_graph** out) {
     delete g;
     return hip_fail(e, "hipGraphInstantiate");
   }
+  // The graph's work descriptions to the device now rather than at the first
+  // replay.  (A replay's fixed cost is the host's hipGraphLaunch call, about
+  // 15 us for one node plus ~1 us a node here; uploading does not change it.)
+  e = hipGraphUpload(g->exec, ctx().stream);
+  if (e != hipSuccess) {
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return hip_fail(e, "hipGraphUpload");
+  }
   *out = g;
   return TH_OK;
 }
@@ -927,6 +994,65 @@ int th_dispatch_costs(double* graph_base, double* in_graph, double* direct) {
   *in_graph = c.launch_gap;
   *direct = c.direct_gap;
   return TH_OK;
+}
+
+int th_matrix_rate(int vary, double* flops_per_s, double* clock_hz) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(flops_per_s && clock_hz, "th_matrix_rate: null output");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  const int blocks = 2 * c.prop.multiProcessorCount;
+  // Random operand bits: bf16 in [1, 2) with random signs and mantissas.
+  std::vector<uint32_t> host(16 * 64 * 4);
+  uint64_t z = 0x9e3779b97f4a7c15ull;
+  for (uint32_t& w : host) {
+    z = z * 6364136223846793005ull + 1442695040888963407ull;
+    const uint32_t r = (uint32_t)(z >> 32);
+    w = (0x3f803f80u) | (r & 0x807f807fu);
+  }
+  void* seed = nullptr;
+  void* sink = nullptr;
+  void* stamps = nullptr;
+  if (int r = device_alloc(host.size() * 4, &seed)) return r;
+  int rc = device_alloc(blocks * sizeof(float), &sink);
+  if (!rc) rc = device_alloc(blocks * 4 * sizeof(uint64_t), &stamps);
+  if (rc) {
+    (void)hipFree(seed);
+    if (sink) (void)hipFree(sink);
+    return rc;
+  }
+  auto done = [&](int r) {
+    (void)hipStreamSynchronize(c.stream);
+    (void)hipFree(seed);
+    (void)hipFree(sink);
+    (void)hipFree(stamps);
+    return r;
+  };
+  if (hipMemcpy(seed, host.data(), host.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_matrix_rate: seed upload failed"));
+  const int iters = 20000;
+  RateArgs a{static_cast<const u32x4*>(seed), static_cast<float*>(sink), static_cast<uint64_t*>(stamps), iters,
+             vary ? 1 : 0};
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_matrix_rate: events"));
+  hipLaunchKernelGGL(th_matrix_rate_kernel, dim3(blocks), dim3(256), 0, c.stream, a);  // warm up the clocks
+  (void)hipEventRecord(e0, c.stream);
+  hipLaunchKernelGGL(th_matrix_rate_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
+  (void)hipEventRecord(e1, c.stream);
+  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_matrix_rate: run failed"));
+  float ms = 0;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  std::vector<uint64_t> st(blocks * 4);
+  if (hipMemcpy(st.data(), stamps, st.size() * 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_matrix_rate: stamps"));
+  double clock = 0;
+  for (int i = 0; i < blocks; ++i) clock += (double)(st[4 * i + 1] - st[4 * i]) / (double)(st[4 * i + 3] - st[4 * i + 2]);
+  *clock_hz = clock / blocks * 100e6;  // the real-time counter runs at 100 MHz
+  *flops_per_s = (double)blocks * 4 * iters * 32 * 32768.0 / (ms * 1e-3);
+  return done(TH_OK);
 }
 
 int th_time_graph(th_graph* g, int warmup, int reps, double* seconds) {
