@@ -124,15 +124,20 @@ def test_backward_both_dq_paths(target, S, causal, recompute):
 
 
 def test_head_dims_route_to_the_kernels_that_take_them(target):
-    """d 128 at a multiple of 128 takes the matrix-core kernel; d 64 and a
-    length of 100 take the general kernels; d beyond 256 is refused."""
+    """d 128 at a multiple of 128 takes the tuned matrix-core kernel; d 64,
+    d 256 and d 128 at a length of 100 the other matrix-core kernels; d 100
+    and fp32 the general kernels; d beyond 256 is refused."""
     import tempest_hip.launch as L
     from tempest_hip import HIPError
     t = torch.zeros(1, 128, 1, 300, dtype=torch.bfloat16, device="cuda")
     p = t.data_ptr()
-    assert "attn_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p).describe()
-    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=64).describe()
-    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 100, p, p, p, p).describe()
+    tuned = L.attention_fwd(1, 1, 1, 128, p, p, p, p).describe()
+    assert "attn_fwd" in tuned and "mfma_attn" not in tuned
+    assert "mfma_attn_fwd_d64" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=64).describe()
+    assert "mfma_attn_fwd_d256" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=256).describe()
+    assert "mfma_attn_fwd_d128" in L.attention_fwd(1, 1, 1, 100, p, p, p, p).describe()
+    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=100).describe()
+    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, f32=True).describe()
     with pytest.raises(HIPError, match="head_dim must be 1..256"):
         L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=300)
 
