@@ -594,6 +594,28 @@ def matrix_rate(target) -> dict:
     return out
 
 
+def lds_rate(target) -> dict:
+    """The LDS read rate on this device (th_lds_rate): ds_read_b128 and
+    ds_read_b64_tr_b16 at one and two workgroups of four waves a CU, alone
+    and with one product per 1 KB read (32 flops a byte, the attention
+    sweeps' ratio), in bytes a clock a CU at the clock the waves ran at."""
+    import ctypes
+    from tempest_hip import _lib
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = {}
+    for mode, name in ((0, "b128"), (1, "tr_b64_pairs"), (2, "b128_with_products"), (3, "tr_b64_pairs_with_products")):
+        for per_cu in (1, 2):
+            b, f, c = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+            _lib.call("th_lds_rate", mode, per_cu, ctypes.byref(b), ctypes.byref(f), ctypes.byref(c))
+            row = {"TB/s": b.value / 1e12, "B/clk/CU": b.value / c.value / cus, "clock_GHz": c.value / 1e9}
+            if mode >= 2:
+                row["PFLOP/s"] = f.value / 1e15
+            out[f"{name}_{per_cu}wg"] = row
+    log("lds rate:", json.dumps(out))
+    return out
+
+
 def dispatch_costs(target, reps: int = 2000):
     """Where a graph replay's time goes on this device: graphs of 1, 9 and 40
     near-empty launches (16-byte copies, th_build_copy), replayed back to back
@@ -654,7 +676,7 @@ def main() -> int:
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
                                        "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims",
-                                       "matrix_rate"],
+                                       "matrix_rate", "lds_rate"],
                     default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -688,7 +710,7 @@ def main() -> int:
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
               "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows, "attention_head_dims": attention_head_dims,
-              "matrix_rate": matrix_rate,
+              "matrix_rate": matrix_rate, "lds_rate": lds_rate,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
@@ -733,6 +755,10 @@ def main() -> int:
             configs["config4_attention"] = config4(target)
         except Exception as err:
             configs["config4_attention"] = {"error": repr(err)}
+        try:
+            configs["config4_attention"]["lds_rate"] = lds_rate(target)
+        except Exception as err:
+            configs["config4_attention"]["lds_rate"] = {"error": repr(err)}
         log("config4:", json.dumps(configs["config4_attention"]))
         try:
             configs["attention_head_dims"] = attention_head_dims(target)

@@ -237,6 +237,15 @@ int th_dispatch_costs(double* graph_base, double* in_graph, double* direct);
  * (cover/calibrate.jl). */
 int th_matrix_rate(int vary, double* host_flops_per_s, double* host_clock_hz);
 
+/* The LDS read rate on this device, measured: workgroups of four waves (one
+ * or two a CU, per_cu) read 64 KB of LDS in a loop, eight 1 KB wave reads in
+ * flight, by ds_read_b128 (mode 0) or pairs of ds_read_b64_tr_b16 (mode 1);
+ * modes 2 and 3 issue one v_mfma_f32_32x32x16_bf16 on each read as well (32
+ * flops a byte, the attention sweeps' ratio).  Bytes/s and flop/s over the
+ * run, and the shader clock the waves ran at.  The LDS ceiling the attention
+ * kernels meet.  No reference counterpart: a device measurement. */
+int th_lds_rate(int mode, int per_cu, double* host_bytes_per_s, double* host_flops_per_s, double* host_clock_hz);
+
 /* ---- op class (a): fused pointwise + reductions -------------------------- */
 
 /* Softmax over each contiguous run of n (a column of the reference's n x rows

@@ -199,6 +199,63 @@ __global__ __launch_bounds__(256, 2) void th_matrix_rate_kernel(RateArgs a) {
   }
 }
 
+// ---- the LDS read rate --------------------------------------------------------------
+// Workgroups of four waves read a 64 KB LDS array in a loop, eight reads in
+// flight a wave, at conflict-free addresses (each wave a different 8 KB
+// block per read): ds_read_b128 (modes 0 and 2) or pairs of
+// ds_read_b64_tr_b16 (modes 1 and 3), 16 bytes a lane either way.  Modes 2
+// and 3 also issue one v_mfma_f32_32x32x16_bf16 on each 1 KB read, 32 flops
+// a byte: the ratio of the attention sweeps' products to their fragment
+// reads.  Clock and real-time stamps as in the matrix-rate kernel.
+typedef short th_s16x4 __attribute__((ext_vector_type(4)));
+typedef short th_s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) th_s16x4 th_lds_s16x4;
+
+struct LdsRateArgs {
+  uint32_t* sink;     // written only if the reads fold to a value they never do
+  uint64_t* stamps;   // per workgroup: clock start, end, real-time start, end
+  int32_t iters;
+};
+
+template <int kMode>
+__global__ __launch_bounds__(256, 2) void th_lds_rate_kernel(LdsRateArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[32768];
+  for (int i = threadIdx.x; i < 32768; i += 256) lds[i] = (uint16_t)(i * 7 + 1);
+  __syncthreads();
+  const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+  u32x4 x = {0, 0, 0, 0};
+  th_f32x16 acc[2] = {th_f32x16{}, th_f32x16{}};
+  const th_bf16x8 b = __builtin_bit_cast(th_bf16x8, u32x4{0x3f803f80u ^ (uint32_t)lane, 0x3f803f81u, 0x3f803f82u, 0x3f803f83u});
+  const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < a.iters; ++it) {
+    asm volatile("" ::: "memory");  // read the array again every iteration
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int base = ((u + 2 * w) & 7) * 4096;
+      u32x4 r;
+      if constexpr (kMode == 0 || kMode == 2) {
+        r = *reinterpret_cast<const u32x4*>(lds + base + 8 * lane);
+      } else {
+        const th_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((th_lds_s16x4*)(lds + base + 4 * lane));
+        const th_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((th_lds_s16x4*)(lds + base + 256 + 4 * lane));
+        r = __builtin_bit_cast(u32x4, th_s16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+      }
+      x ^= r;
+      if constexpr (kMode >= 2)
+        acc[u & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(th_bf16x8, r), b, acc[u & 1], 0, 0, 0);
+    }
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  const uint32_t y = x[0] ^ x[1] ^ x[2] ^ x[3] ^ __float_as_uint(acc[0][0] + acc[1][3]);
+  if (y == 0x12345678u) a.sink[blockIdx.x] = y;
+  if (threadIdx.x == 0) {
+    a.stamps[4 * blockIdx.x + 0] = t0;
+    a.stamps[4 * blockIdx.x + 1] = t1;
+    a.stamps[4 * blockIdx.x + 2] = r0;
+    a.stamps[4 * blockIdx.x + 3] = r1;
+  }
+}
+
 extern "C" {
 
 const char* th_last_error(void) { return g_error.c_str(); }
@@ -1052,6 +1109,60 @@ int th_matrix_rate(int vary, double* flops_per_s, double* clock_hz) {
   for (int i = 0; i < blocks; ++i) clock += (double)(st[4 * i + 1] - st[4 * i]) / (double)(st[4 * i + 3] - st[4 * i + 2]);
   *clock_hz = clock / blocks * 100e6;  // the real-time counter runs at 100 MHz
   *flops_per_s = (double)blocks * 4 * iters * 32 * 32768.0 / (ms * 1e-3);
+  return done(TH_OK);
+}
+
+int th_lds_rate(int mode, int per_cu, double* bytes_per_s, double* flops_per_s, double* clock_hz) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(bytes_per_s && flops_per_s && clock_hz, "th_lds_rate: null output");
+  TH_REQUIRE(mode >= 0 && mode <= 3, "th_lds_rate: mode must be 0 (b128), 1 (tr), 2 (b128 + products) or 3 (tr + products)");
+  TH_REQUIRE(per_cu == 1 || per_cu == 2, "th_lds_rate: one or two workgroups a CU");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  const int blocks = per_cu * c.prop.multiProcessorCount;
+  void* sink = nullptr;
+  void* stamps = nullptr;
+  if (int r = device_alloc(blocks * sizeof(uint32_t), &sink)) return r;
+  if (int r = device_alloc(blocks * 4 * sizeof(uint64_t), &stamps)) {
+    (void)hipFree(sink);
+    return r;
+  }
+  auto done = [&](int r) {
+    (void)hipStreamSynchronize(c.stream);
+    (void)hipFree(sink);
+    (void)hipFree(stamps);
+    return r;
+  };
+  const int iters = 4000;
+  LdsRateArgs a{static_cast<uint32_t*>(sink), static_cast<uint64_t*>(stamps), iters};
+  const void* k = mode == 0 ? (const void*)th_lds_rate_kernel<0>
+                : mode == 1 ? (const void*)th_lds_rate_kernel<1>
+                : mode == 2 ? (const void*)th_lds_rate_kernel<2>
+                            : (const void*)th_lds_rate_kernel<3>;
+  void* params[] = {&a};
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_lds_rate: events"));
+  // Warm up the clocks, then time the second launch.
+  if (hipLaunchKernel(k, dim3(blocks), dim3(256), params, 0, c.stream) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_lds_rate: launch failed"));
+  (void)hipEventRecord(e0, c.stream);
+  (void)hipLaunchKernel(k, dim3(blocks), dim3(256), params, 0, c.stream);
+  (void)hipEventRecord(e1, c.stream);
+  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_lds_rate: run failed"));
+  float ms = 0;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  std::vector<uint64_t> st(blocks * 4);
+  if (hipMemcpy(st.data(), stamps, st.size() * 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_lds_rate: stamps"));
+  double clock = 0;
+  for (int i = 0; i < blocks; ++i) clock += (double)(st[4 * i + 1] - st[4 * i]) / (double)(st[4 * i + 3] - st[4 * i + 2]);
+  *clock_hz = clock / blocks * 100e6;
+  const double reads = (double)blocks * 4 * 8 * iters;  // wave reads of 1 KB
+  *bytes_per_s = reads * 1024.0 / (ms * 1e-3);
+  *flops_per_s = mode >= 2 ? reads * 32768.0 / (ms * 1e-3) : 0.0;
   return done(TH_OK);
 }
 

@@ -150,6 +150,28 @@ def test_timing_and_rates(target):
     assert w.bytes == 3 * 4 * 1024 * 4096 and w.kernels == 2
 
 
+def test_lds_rate_measures_reads_and_products(target):
+    import ctypes
+    from tempest_hip import _lib
+    announce("lds rate")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    got = {}
+    for mode in range(4):
+        b, f, c = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        _lib.call("th_lds_rate", mode, 2, ctypes.byref(b), ctypes.byref(f), ctypes.byref(c))
+        assert 0.5e9 < c.value < 3.0e9, c.value
+        per_clk = b.value / c.value / cus
+        # Between a tenth of a bank pass and the 256 bytes a clock the 64 banks give.
+        assert 10 < per_clk <= 300, (mode, per_clk)
+        assert (f.value > 0) == (mode >= 2)
+        got[mode] = per_clk
+    print("LDS B/clk/CU", got, flush=True)
+    for bad in ((4, 1), (-1, 1), (0, 3), (0, 0)):
+        with pytest.raises(_lib.HIPError):
+            _lib.call("th_lds_rate", bad[0], bad[1], ctypes.byref(ctypes.c_double()), ctypes.byref(ctypes.c_double()),
+                      ctypes.byref(ctypes.c_double()))
+
+
 def test_slots_taken_one_by_one_lie_in_one_reservation(target):
     """A pool's reserved range (th_pool_*): the config-3 MLP program's slots
     and a second executable's, allocated one at a time as `planned` does
