@@ -616,6 +616,188 @@ def lds_rate(target) -> dict:
     return out
 
 
+# The reference's own recorded times (NVIDIA GB10, µs) for the programs
+# reference_benchmarks runs: TRIALS.md:2155-2158 (bf16 attention forward and
+# training step, the later of its records), :2183-2187 (TF32), and
+# test/bench/coverage-NVIDIA_GB10.tsv (the coverage compositions of
+# test/fixtures/compositions.jl).
+REFERENCE_US = {
+    "attention_bf16_D64_H8_B2_S1024_causal": {"fwd": 36.2, "step": 191.0},
+    "attention_bf16_D64_H8_B2_S2048_causal": {"fwd": 123.7, "step": 597.0},
+    "attention_f32_D64_H8_B2_S1024_causal": {"fwd": 95.0, "step": 410.0},
+    "attention_f32_D64_H8_B2_S2048_causal": {"fwd": 330.0, "step": 1408.0},
+    "attention_f32_D64_H4_S256_B2_causal": {"fwd": 123.61, "step": 195.41},
+    "softmax_through_logsumexp_512x1024": {"fwd": 5.56},
+    "layer_norm_two_passes_512x1024": {"fwd": 10.07},
+    "rmsnorm_divided_by_the_root_512x1024": {"fwd": 9.89},
+    "linear_bias_gelu_256x384x512_f32": {"fwd": 13.44},
+}
+
+
+def _graph_step_us(launches, samples: int = 15, milliseconds: float = 4.0) -> float:
+    """Device microseconds of one step of `launches`, as the reference's coverage
+    bench takes it (test/bench/coverage.jl:21-28): the step captured enough times
+    into one graph to run a few milliseconds, the minimum over samples of one
+    replay's device time over the repetitions."""
+    import ctypes
+    from tempest_hip import _lib
+    for l in launches:
+        l()  # workspaces are taken at the first run
+    def timed(reps: int, warm: int, n: int) -> list[float]:
+        hs = [l.handle.value for l in launches] * reps
+        g = ctypes.c_void_p()
+        _lib.call("th_graph_capture", (ctypes.c_void_p * len(hs))(*hs), len(hs), ctypes.byref(g))
+        try:
+            out = []
+            for i in range(n):
+                sec = ctypes.c_double()
+                _lib.call("th_time_graph", g, warm if i == 0 else 0, 1, ctypes.byref(sec))
+                out.append(sec.value / reps)
+            return out
+        finally:
+            _lib.call("th_graph_release", g)
+    once = min(timed(1, 3, 3))
+    reps = max(1, min(200, round(milliseconds * 1e-3 / once)))
+    return min(timed(reps, 1, samples)) * 1e6
+
+
+def reference_benchmarks(target) -> dict:
+    """This path's programs at the shapes the reference itself times, beside
+    the reference's recorded times on its GB10 (REFERENCE_US): causal attention
+    (64 features, one key head per query head) forward and training step
+    (loss = sum(abs2, o): o, the loss and dO = 2o by one floor group, then the
+    backward) in bf16 and fp32 (the reference's numbers at fp32 are TF32), the
+    coverage suite's attention (64 x 4 heads x 256 positions x 2, fp32) and its
+    column programs over a 512 x 1024 fp32 matrix (softmax through logsumexp,
+    the two-pass layer norm and RMSNorm with a weight, and linear, bias, GELU at
+    256 x 384 x 512 in fp32, test/fixtures/compositions.jl:41-138).  Inputs are
+    the reference's sample(dims; scale) = 2 sin(scale (1:prod(dims)))
+    (compositions.jl:36).  Each result is checked against float64 torch:
+    rel_err = |ours - exact| / |exact| over the output (attention: o, dq, dk, dv)."""
+    import torch
+    import tempest_hip.launch as L
+    from tempest_hip.floor import FloorGroup
+
+    def sample(n, scale, dtype):
+        return (2.0 * torch.sin(scale * torch.arange(1, n + 1, device="cuda", dtype=torch.float64))).to(dtype)
+
+    def rel(a, b):
+        a, b = a.detach().double(), b.detach().double()
+        return float((a - b).norm() / b.norm())
+
+    out = {}
+    # ---- attention
+    shapes = [("bf16", 64, 8, 2, 1024, (0.1, 0.2, 0.3)), ("bf16", 64, 8, 2, 2048, (0.1, 0.2, 0.3)),
+              ("f32", 64, 8, 2, 1024, (0.1, 0.2, 0.3)), ("f32", 64, 8, 2, 2048, (0.1, 0.2, 0.3)),
+              ("f32", 64, 4, 2, 256, (0.1, 0.2, 0.3))]
+    for dt, D, H, B, S, scales in shapes:
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+        n = D * H * S * B
+        q, k, v = (sample(n, sc, tdt).view(B, S, H, D) for sc in scales)  # (d, heads, positions, batch)
+        o, g = torch.empty_like(q), torch.empty_like(q)
+        lse = torch.empty(B, S, H, device="cuda")
+        loss = torch.zeros(1, device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        f32 = dt == "f32"
+        fwd = L.attention_fwd(B, H, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              causal=True, head_dim=D, f32=f32)
+        lg = FloorGroup("reduction", (n,), reduced=(0,), name="loss = sum(abs2, o), dO = 2o")
+        lg.value("o", dt, n)
+        lg.value("g", dt, n)
+        lg.value("loss", "f32", 1)
+        oo = lg.load("o", (1,))
+        lg.output("g", oo * 2.0, (1,))
+        lg.output("loss", lg.fold("sum", lg.apply("abs2", oo)).value, full=False)
+        lossl = lg.build({"o": o.data_ptr(), "g": g.data_ptr(), "loss": loss.data_ptr()})
+        bwd = L.attention_bwd(B, H, S, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              g.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), causal=True, head_dim=D,
+                              f32=f32)
+        t_fwd = _graph_step_us([fwd])
+        t_step = _graph_step_us([fwd, lossl, bwd])
+        fwd(), lossl(), bwd()
+        torch.cuda.synchronize()
+        # float64 reference: loss = sum(abs2, attention(q, k, v)) and its gradients.
+        qq, kk, vv = (t.double().permute(0, 2, 1, 3).contiguous().requires_grad_(True) for t in (q, k, v))
+        sc = qq @ kk.transpose(-1, -2).contiguous() / D ** 0.5
+        mask = torch.ones(S, S, device="cuda", dtype=torch.bool).triu(1)
+        p = torch.softmax(sc.masked_fill(mask, float("-inf")), dim=-1)
+        oref = p @ vv
+        (oref * oref).sum().backward()
+        back = lambda t: t.permute(0, 2, 1, 3)  # noqa: E731
+        name = f"attention_{dt}_D{D}_H{H}_B{B}_S{S}_causal" if H == 8 else f"attention_{dt}_D{D}_H{H}_S{S}_B{B}_causal"
+        ref = REFERENCE_US[name]
+        out[name] = {"us_fwd": t_fwd, "us_step": t_step, "reference_us_gb10": ref,
+                     "speedup_fwd": ref["fwd"] / t_fwd, "speedup_step": ref["step"] / t_step,
+                     "rel_err": {"o": rel(o, back(oref)), "dq": rel(dq, back(qq.grad)), "dk": rel(dk, back(kk.grad)),
+                                 "dv": rel(dv, back(vv.grad))},
+                     "kernels": [fwd.describe(), bwd.describe()]}
+        for l in (fwd, lossl, bwd):
+            l.destroy()
+        del qq, kk, vv, sc, p, oref
+        log(name, json.dumps({kk_: out[name][kk_] for kk_ in ("us_fwd", "us_step", "speedup_fwd", "speedup_step")}))
+    # ---- column programs over X (512 x 1024), w (512)
+    N, M = 512, 1024
+    x = sample(N * M, 0.3, torch.float32)
+    w = sample(N, 0.1, torch.float32)
+    y = torch.empty_like(x)
+    X, Wt = x.double().view(M, N).T, w.double()  # Julia's N x M, column-major
+    def col_group(name):
+        g = FloorGroup("reduction", (N, M), reduced=(0,), name=name)
+        g.value("x", "f32", N * M)
+        g.value("w", "f32", N)
+        g.value("y", "f32", N * M)
+        return g, g.load("x", (1, N)), g.load("w", (1, 0))
+    progs = {}
+    g, xx, ww = col_group("softmax through logsumexp")
+    g.output("y", g.apply("exp", xx - g.fold("exp", xx).logsumexp), (1, N))
+    progs["softmax_through_logsumexp_512x1024"] = (g, torch.softmax(X, dim=0))
+    g, xx, ww = col_group("layer norm, two passes")
+    m = g.fold("sum", xx).value / float(N)
+    var = g.fold("sum", g.apply("abs2", xx - m), phase=2).value / float(N)
+    g.output("y", (xx - m) / g.apply("sqrt", var + 1e-5) * ww, (1, N))
+    mu = X.mean(dim=0, keepdim=True)
+    progs["layer_norm_two_passes_512x1024"] = (
+        g, (X - mu) / torch.sqrt(((X - mu) ** 2).mean(dim=0, keepdim=True) + 1e-5) * Wt[:, None])
+    g, xx, ww = col_group("RMSNorm, divided by the root")
+    g.output("y", xx / g.apply("sqrt", g.fold("sum", g.apply("abs2", xx)).value / float(N) + 1e-5) * ww, (1, N))
+    progs["rmsnorm_divided_by_the_root_512x1024"] = (
+        g, X / torch.sqrt((X ** 2).sum(dim=0, keepdim=True) / N + 1e-5) * Wt[:, None])
+    for name, (g, exact) in progs.items():
+        l = g.build({"x": x.data_ptr(), "w": w.data_ptr(), "y": y.data_ptr()})
+        t = _graph_step_us([l])
+        l()
+        torch.cuda.synchronize()
+        out[name] = {"us_fwd": t, "reference_us_gb10": REFERENCE_US[name], "speedup_fwd": REFERENCE_US[name]["fwd"] / t,
+                     "rel_err": rel(y.view(M, N).T, exact)}
+        l.destroy()
+        log(name, json.dumps({kk_: out[name][kk_] for kk_ in ("us_fwd", "speedup_fwd", "rel_err")}))
+    # ---- linear, bias, GELU: gelu.(W * Z .+ b), W 256 x 384, Z 384 x 512, b 256, fp32
+    m_, k_, n_ = 256, 384, 512
+    Wm, Zm, bv = sample(m_ * k_, 0.01, torch.float32), sample(k_ * n_, 0.2, torch.float32), sample(m_, 0.3, torch.float32)
+    c = torch.empty(m_ * n_, device="cuda")
+    yo = torch.empty_like(c)
+    prod = L.gemm(m_, n_, k_, Wm.data_ptr(), 1, m_, Zm.data_ptr(), 1, k_, c.data_ptr(), m_, c_dtype=L.F32,
+                  factors=L.F32)
+    eg = FloorGroup("pointwise", (m_, n_), name="gelu.(c .+ b)")
+    eg.value("c", "f32", m_ * n_)
+    eg.value("b", "f32", m_)
+    eg.value("y", "f32", m_ * n_)
+    z = eg.load("c", (1, m_)) + eg.load("b", (1, 0))
+    eg.output("y", z / 2.0 * (1.0 + eg.apply("tanh", 0.7978846 * (z + 0.044715 * z * z * z))), (1, m_))
+    epi = eg.build({"c": c.data_ptr(), "b": bv.data_ptr(), "y": yo.data_ptr()})
+    t = _graph_step_us([prod, epi])
+    prod(), epi()
+    torch.cuda.synchronize()
+    Zd = (Wm.double().view(k_, m_).T @ Zm.double().view(n_, k_).T) + bv.double()[:, None]
+    exact = Zd / 2 * (1 + torch.tanh(0.7978846 * (Zd + 0.044715 * Zd ** 3)))
+    name = "linear_bias_gelu_256x384x512_f32"
+    out[name] = {"us_fwd": t, "reference_us_gb10": REFERENCE_US[name], "speedup_fwd": REFERENCE_US[name]["fwd"] / t,
+                 "rel_err": rel(yo.view(n_, m_).T, exact), "kernels": [prod.describe(), epi.describe()]}
+    prod.destroy(), epi.destroy()
+    log(name, json.dumps({kk_: out[name][kk_] for kk_ in ("us_fwd", "speedup_fwd", "rel_err")}))
+    return out
+
+
 def dispatch_costs(target, reps: int = 2000):
     """Where a graph replay's time goes on this device: graphs of 1, 9 and 40
     near-empty launches (16-byte copies, th_build_copy), replayed back to back
@@ -676,7 +858,7 @@ def main() -> int:
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
                                        "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims",
-                                       "matrix_rate", "lds_rate"],
+                                       "matrix_rate", "lds_rate", "reference_benchmarks"],
                     default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -710,7 +892,7 @@ def main() -> int:
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
               "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows, "attention_head_dims": attention_head_dims,
-              "matrix_rate": matrix_rate, "lds_rate": lds_rate,
+              "matrix_rate": matrix_rate, "lds_rate": lds_rate, "reference_benchmarks": reference_benchmarks,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0

@@ -172,8 +172,8 @@ static int auto_splits(const th_gemm_desc* d, int tile) {
     // fp32 factors on 128 x 128 tiles split as the others; half factors do not.
     if (!(d->flags & TH_GEMM_F32_FACTORS) || d->c_dtype != TH_F32 || d->bias) return 1;
     const int64_t tiles = tiles_of(d, 128, 128);
-    if (tiles >= 128 || d->k < 256) return 1;
-    return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / 128));
+    if (tiles >= 128 || d->k < 64) return 1;
+    return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / 32));
   }
   const bool big = tile == TH_TILE_256;
   const int64_t tiles = big ? tiles_of(d, kTile, kTile) : tiles_of(d, mid_rows(tile), mid_cols(tile));

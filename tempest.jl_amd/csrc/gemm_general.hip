@@ -377,6 +377,82 @@ __global__ __launch_bounds__(256, 2) void gemm_f32(F32GemmArgs p) {
     }
 }
 
+// ---- fp32 factors, small products: 32 x 32 blocks ---------------------------------
+// A product whose 128 x 128 tiles would leave most of the device idle, with
+// K short enough not to need parts: a workgroup of four waves per 32 x 32
+// block of C, wave w taking a quarter of K (in pairs) with
+// v_mfma_f32_32x32x2_f32 on operands loaded from memory straight into
+// registers, eight products' worth at a time (the operands of such a
+// product sit in L2).  The three other waves' partial blocks go through LDS
+// and wave 0 adds them in wave order, so the result does not depend on
+// timing, then D, and stores.  Every load and store is bounds-checked.
+
+constexpr int kSB = 32;  // C block
+constexpr int kSU = 8;   // products per batch of loads
+
+__global__ __launch_bounds__(256) void gemm_f32_small(F32GemmArgs p) {
+  __shared__ float part[3][16 * 64];  // waves 1..3's blocks, [register][lane]
+  const int tiles_m = (p.m + kSB - 1) / kSB;
+  const int m0 = (blockIdx.x % tiles_m) * kSB, n0 = (blockIdx.x / tiles_m) * kSB;
+  const int z = blockIdx.z;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int pairs = (p.k + 1) / 2, per = (pairs + 3) / 4;
+  const int kb = 2 * min(pairs, wave * per), ke = min(p.k, 2 * min(pairs, (wave + 1) * per));
+  const int mi = m0 + lane % 32, nj = n0 + lane % 32, kh = lane / 32;
+  const bool m_in = mi < p.m, n_in = nj < p.n;
+  const float* ap = p.a + z * p.a_batch + (int64_t)(m_in ? mi : 0) * p.a_m;
+  const float* bp = p.b + z * p.b_batch + (int64_t)(n_in ? nj : 0) * p.b_n;
+  f32x16g acc = {};
+  // Lane l gives A(row l % 32, k l / 32) and B(k l / 32, column l % 32); the
+  // next batch's loads are issued before this batch's products.
+  float ra[2][kSU], rb[2][kSU];
+  auto load = [&](int k0, float (&xa)[kSU], float (&xb)[kSU]) {
+#pragma unroll
+    for (int u = 0; u < kSU; ++u) {
+      const int k = k0 + 2 * u + kh;
+      const bool k_in = k < ke;
+      xa[u] = (m_in && k_in) ? ap[(int64_t)k * p.a_k] : 0.0f;
+      xb[u] = (n_in && k_in) ? bp[(int64_t)k * p.b_k] : 0.0f;
+    }
+  };
+  auto multiply = [&](const float (&xa)[kSU], const float (&xb)[kSU]) {
+#pragma unroll
+    for (int u = 0; u < kSU; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[u], xb[u], acc, 0, 0, 0);
+  };
+  constexpr int kStep = 2 * kSU;
+  if (kb < ke) load(kb, ra[0], rb[0]);
+  for (int k0 = kb; k0 < ke; k0 += 2 * kStep) {
+    if (k0 + kStep < ke) load(k0 + kStep, ra[1], rb[1]);
+    multiply(ra[0], rb[0]);
+    if (k0 + kStep >= ke) break;
+    if (k0 + 2 * kStep < ke) load(k0 + 2 * kStep, ra[0], rb[0]);
+    multiply(ra[1], rb[1]);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[wave - 1][r * 64 + lane] = acc[r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += part[w][r * 64 + lane];
+  // Lane l holds C(rows 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32).
+  if (!n_in) return;
+  float* c = p.c + z * p.c_batch;
+  const float* d = p.d ? p.d + z * p.d_batch : nullptr;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + 8 * (r / 4) + 4 * kh + r % 4;
+    if (m < p.m) {
+      float v = acc[r];
+      if (d) v += d[(int64_t)m + (int64_t)nj * p.d_ld];
+      c[(int64_t)m + (int64_t)nj * p.c_ld] = v;
+    }
+  }
+}
+
 // C_z = D_z + the parts' sums in part order (fp32).
 struct F32SumArgs {
   const float* ws;  // [batch][parts][m x n], ld m
@@ -446,11 +522,12 @@ int build_gemm_general(const th_gemm_desc* d, th_launch** out) {
 
 // The parts of K an fp32 product takes when the caller leaves them: enough
 // for about 256 workgroups where the tiles alone give fewer than 128, each
-// part at least 128 deep (eight steps: 256 x 256 x 8192 takes 64 parts).
+// part at least 32 deep (two steps: 256 x 256 x 8192 takes 64 parts, 256 x
+// 512 x 384 twelve).
 static int f32_splits(const th_gemm_desc* d) {
   const int64_t tiles = (int64_t)((d->m + kFT - 1) / kFT) * ((d->n + kFT - 1) / kFT) * std::max(1, d->batch);
-  if (tiles >= 128 || d->k < 256) return 1;
-  return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / 128));
+  if (tiles >= 128 || d->k < 64) return 1;
+  return (int)std::max<int64_t>(1, std::min<int64_t>((256 + tiles - 1) / tiles, d->k / 32));
 }
 
 static bool f32_vector(const void* base, int64_t unit_other, int64_t other, int64_t batch_stride, int n_batch) {
@@ -458,7 +535,18 @@ static bool f32_vector(const void* base, int64_t unit_other, int64_t other, int6
          unit_other == 1;
 }
 
+static int build_gemm_f32_small(const th_gemm_desc* d, th_launch** out);
+
+// Whether an fp32 product takes the 32 x 32 kernel: the parts left to the
+// library, its 128 x 128 tiles fewer than 64 (a quarter of the device), K
+// at most 2048 (a wave's quarter of it at most 512 deep).
+static bool f32_small(const th_gemm_desc* d) {
+  const int64_t tiles = (int64_t)((d->m + kFT - 1) / kFT) * ((d->n + kFT - 1) / kFT) * std::max(1, d->batch);
+  return d->splits == 0 && tiles < 64 && d->k <= 2048;
+}
+
 static int build_gemm_f32(const th_gemm_desc* d, th_launch** out) {
+  if (f32_small(d)) return build_gemm_f32_small(d, out);
   const int batch = d->batch > 0 ? d->batch : 1;
   const int64_t tiles = (int64_t)((d->m + kFT - 1) / kFT) * ((d->n + kFT - 1) / kFT);
   TH_REQUIRE(tiles <= 0x7fffffff && batch <= 65535, "th_build_gemm: grid too large");
@@ -513,6 +601,32 @@ static int build_gemm_f32(const th_gemm_desc* d, th_launch** out) {
   const double mm = d->m, nn = d->n, kk = d->k, bb = batch;
   b.work(bb * (4.0 * (mm * kk + kk * nn) + 4.0 * mm * nn * (acc ? 2 : 1)), 2.0 * bb * mm * nn * kk,
          tiles * splits * batch);
+  *out = b.release();
+  return TH_OK;
+}
+
+static int build_gemm_f32_small(const th_gemm_desc* d, th_launch** out) {
+  const int batch = d->batch > 0 ? d->batch : 1;
+  const int64_t blocks = (int64_t)((d->m + kSB - 1) / kSB) * ((d->n + kSB - 1) / kSB);
+  TH_REQUIRE(blocks <= 0x7fffffff && batch <= 65535, "th_build_gemm: grid too large");
+  const bool acc = (d->flags & TH_GEMM_ACCUMULATE) != 0;
+  TH_REQUIRE(!acc || d->d, "th_build_gemm: accumulating needs d");
+  F32GemmArgs a{};
+  a.a = static_cast<const float*>(d->a), a.b = static_cast<const float*>(d->b);
+  a.a_m = d->a_m, a.a_k = d->a_k, a.a_batch = d->a_batch;
+  a.b_k = d->b_k, a.b_n = d->b_n, a.b_batch = d->b_batch;
+  a.m = d->m, a.n = d->n, a.k = d->k, a.ksplit = d->k;
+  a.c = static_cast<float*>(d->c), a.c_ld = d->c_ld, a.c_batch = d->c_batch, a.c_part = 0;
+  a.d = acc ? static_cast<const float*>(d->d) : nullptr;
+  a.d_ld = d->d_ld ? d->d_ld : d->c_ld, a.d_batch = d->d_ld ? d->d_batch : d->c_batch;
+  th::Builder b("gemm_f32", 9);
+  int k = b.kernel((const void*)gemm_f32_small, "gemm_f32_32x32", dim3((unsigned)blocks, 1, batch), dim3(256), 0, a);
+  b.ref(0, k, TH_OFFSET(F32GemmArgs, a));
+  b.ref(1, k, TH_OFFSET(F32GemmArgs, b));
+  b.ref(2, k, TH_OFFSET(F32GemmArgs, c));
+  b.ref(8, k, TH_OFFSET(F32GemmArgs, d));
+  const double mm = d->m, nn = d->n, kk = d->k, bb = batch;
+  b.work(bb * (4.0 * (mm * kk + kk * nn) + 4.0 * mm * nn * (acc ? 2 : 1)), 2.0 * bb * mm * nn * kk, blocks * batch);
   *out = b.release();
   return TH_OK;
 }

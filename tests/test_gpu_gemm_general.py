@@ -1,7 +1,8 @@
 """Products beyond the bf16 tile kernel's shapes, and the tile kernel's batch,
 split K and accumulate.  fp32 factors on their own 128 x 128 kernel (vector
-loads along a unit stride, edges element by element, K split into parts) and
-as split bf16 (bf16x3) on the bf16 tile kernels, at sizes, against float64.  The general kernel: every product of the reference's
+loads along a unit stride, edges element by element, K split into parts), on
+the 32 x 32 kernel for small products, and as split bf16 (bf16x3) on the bf16
+tile kernels, at sizes, against float64.  The general kernel: every product of the reference's
 fixture programs at its own shape (test/fixtures/programs.jl:79-96), fp32
 factors, transposed operands through strides, a batch axis, D + A B, and bf16
 or fp16 factors at shapes that are not multiples of 8.  A whole fixture
@@ -268,13 +269,17 @@ def _run_f32(m, n, k, ta, tb, st, batch=1, d=None, bf16x3=False, splits=0, tile=
     (512, 384, 1024, True, True), (512, 384, 1024, False, False), (512, 384, 1024, True, False),
     (512, 384, 1024, False, True), (1000, 700, 333, True, False), (129, 257, 17, False, True),
     (2048, 1024, 1536, False, False), (1, 300, 5, True, True)])
-def test_f32_kernel_at_size(target, m, n, k, a_kfast, b_kfast):
-    """fp32 factors on the 128 x 128 kernel, every operand layout, interior
-    tiles (16-byte loads) and ragged edges (element loads, bounds-checked)."""
-    announce("fp32 kernel", m, n, k, a_kfast, b_kfast)
+@pytest.mark.parametrize("splits", [0, 1])
+def test_f32_kernel_at_size(target, m, n, k, a_kfast, b_kfast, splits):
+    """fp32 factors, every operand layout, interior tiles (16-byte loads) and
+    ragged edges (element loads, bounds-checked): with the parts left to the
+    library (the 32 x 32 kernel for products under 64 tiles of 128 x 128 and
+    K <= 2048, else the 128 x 128 one) and in one part (the 128 x 128 kernel)."""
+    announce("fp32 kernel", m, n, k, a_kfast, b_kfast, splits)
     A, B, ta, tb, st = _f32_operands(m, n, k, a_kfast, b_kfast, m + n + k)
-    got, l = _run_f32(m, n, k, ta, tb, st)
-    assert "gemm_f32" in l.describe()
+    got, l = _run_f32(m, n, k, ta, tb, st, splits=splits)
+    small = splits == 0 and ((m + 127) // 128) * ((n + 127) // 128) < 64 and k <= 2048
+    assert ("gemm_f32_32x32" if small else "gemm_f32_128x128") in l.describe(), l.describe()
     assert relative(got[0], A[0] @ B[0]) < TOL_F32
 
 
@@ -286,6 +291,16 @@ def test_f32_kernel_splits_k_batches_and_adds(target):
     got, l = _run_f32(256, 256, 8192, ta, tb, st)
     assert "gemm_f32_sum_parts" in l.describe() and l.work().blocks >= 256, l.describe()
     assert relative(got[0], A[0] @ B[0]) < 3e-5  # fp32 sums of 8192 terms
+    # Eight tiles over a short K ("linear, bias, GELU" of the reference's
+    # coverage suite, 256 x 384 x 512): 128 blocks of 32 x 32, no parts; and
+    # the same asked for in parts of at least 32 (twelve, 96 workgroups).
+    A, B, ta, tb, st = _f32_operands(256, 512, 384, False, False, 13)
+    got, l = _run_f32(256, 512, 384, ta, tb, st)
+    assert "gemm_f32_32x32" in l.describe() and l.work().blocks == 128, l.describe()
+    assert relative(got[0], A[0] @ B[0]) < TOL_F32
+    got, l = _run_f32(256, 512, 384, ta, tb, st, splits=12)
+    assert "gemm_f32_sum_parts" in l.describe() and l.work().blocks == 96, l.describe()
+    assert relative(got[0], A[0] @ B[0]) < TOL_F32
     A, B, ta, tb, st = _f32_operands(384, 200, 640, False, True, 12, batch=3)
     D = torch.randn(3, 200, 384, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
     got, _ = _run_f32(384, 200, 640, ta, tb, st, batch=3, d=D)
