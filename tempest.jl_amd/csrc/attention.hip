@@ -1102,7 +1102,9 @@ extern "C" int th_build_attention_fwd(const th_attention_desc* d, th_launch** ou
   *out = nullptr;
   TH_REQUIRE(d != nullptr, "attention: null descriptor");
   if (!matrix_cores_take(d, false))
-    return th::mfma_attention_takes(d) ? th::build_attention_mfma_fwd(d, out) : th::build_attention_general_fwd(d, out);
+    return th::mfma_attention_takes(d)  ? th::build_attention_mfma_fwd(d, out)
+           : th::f32_attention_takes(d) ? th::build_attention_f32_fwd(d, out)
+                                        : th::build_attention_general_fwd(d, out);
   if (int r = check_desc(d, false)) return r;
   // The forward's direct loads address a (batch, head) sequence of K and V
   // from one base with 32-bit byte offsets.
@@ -1131,7 +1133,9 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   *out = nullptr;
   TH_REQUIRE(d != nullptr, "attention: null descriptor");
   if (!matrix_cores_take(d, true))
-    return th::mfma_attention_takes(d) ? th::build_attention_mfma_bwd(d, out) : th::build_attention_general_bwd(d, out);
+    return th::mfma_attention_takes(d)  ? th::build_attention_mfma_bwd(d, out)
+           : th::f32_attention_takes(d) ? th::build_attention_f32_bwd(d, out)
+                                        : th::build_attention_general_bwd(d, out);
   if (int r = check_desc(d, true)) return r;
   AttnArgs a = args_of(d);
   th::Builder b("attention_bwd", 11);  // values 9, 10 (the masks) are read only by the general kernels

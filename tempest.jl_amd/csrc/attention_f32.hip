@@ -1,0 +1,612 @@
+// Op class (c) for fp32 arrays on the matrix cores: v_mfma_f32_32x32x2_f32
+// (exact fp32 products, fp32 sums) at head dims 64 and 128, any lengths,
+// grouped heads, causal or not.  fp32 attention with device-held masks, and
+// other head dims, stay on attention_generic.hip.  The reference's cuTile
+// sweep takes fp32 arrays (its TF32 mode rounds the factors to 10 bits,
+// ext/cuTileExt/build.jl:326-532; TRIALS.md:2187); here the products are
+// exact, as its default precision asks (src/Compiler/runtime/target.jl:42-44).
+//
+// The forms of the bf16 kernels of attention_mfma.hip, for one product of
+// depth 2 instead of 16:
+//   - products over d (S' = K Q', S = Q K', dP = dO V'): lane half h takes d
+//     in [h D/2, (h + 1) D/2), step s the d h D/2 + s, so a lane's operand
+//     of four steps is one 16-byte read of a tile row (rows of D + 4 floats:
+//     16 lanes reading 16 rows start on 16 distinct bank quads), the other
+//     operand (a position's row) in registers;
+//   - products over positions (O' += V' P', dV' += dO' P, dK' += Q' dS,
+//     dQ' += K' dS'): the score accumulator's register i is the B operand
+//     of step i as it stands (lanes 0..31 holding position 8 (i / 4) + i % 4
+//     of the block, lanes 32..63 the position 4 further), and the output's
+//     row m of block b holds d = NB m + b (NB = D / 32 blocks), so that a
+//     lane's A operands of the NB blocks are NB adjacent floats of one tile
+//     row, one 8- or 16-byte read.
+// Everything else as there: tiles of 64 positions staged through registers a
+// step ahead (zeros past the sequence), one barrier a step, the online
+// softmax in exp2 units (folds.jl:186-222), P in fp32, lse = m + log(l);
+// the backward FA2's, deterministic: delta = rowsum(dO .* O); dK, dV per 128
+// keys sweeping the query tiles of each query head of the group; dQ per 128
+// queries sweeping the key tiles.  Keys past the keys' length and, causal,
+// keys after the query weigh 0; queries past the sequence are computed on
+// zeros and not stored.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "th_core.h"
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct FArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  float* lse;  // natural log, [b][s][h]
+  const float* dout;
+  float* delta;  // backward workspace: rowsum(dO .* O), [b][s][h]
+  float* dq;
+  float* dk;
+  float* dv;
+  int64_t q_sh, q_ss, q_sb;  // strides (elements) of q, o, dout, dq
+  int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
+  int32_t seq, kv_seq, heads, kv_heads, batch, causal;
+  float scale;
+};
+
+__device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// The value lane l ^ 32 holds.
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(threadIdx.x % 64 < 32 ? r[1] : r[0]);
+}
+
+template <int D>
+constexpr int kLd = D + 4;  // LDS row of a tile (floats)
+template <int D>
+constexpr int kTileF = 64 * kLd<D>;
+
+// A position's row as the B operand of a product over d: f[s] = row[h D/2 + s].
+template <int D>
+__device__ __forceinline__ void row_half(const float* row, bool live, float (&f)[D / 2]) {
+  const int h = (threadIdx.x % 64) / 32;
+#pragma unroll
+  for (int u = 0; u < D / 8; ++u) {
+    const f32x4 x = live ? *reinterpret_cast<const f32x4*>(row + h * (D / 2) + 4 * u) : f32x4{};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[4 * u + e] = x[e];
+  }
+}
+
+// acc += T[rows r0 + lane % 32] x f over d (D / 2 steps, four a read).
+template <int D>
+__device__ __forceinline__ void over_d(const float* t, int r0, const float (&f)[D / 2], f32x16& acc) {
+  const int lane = threadIdx.x % 64;
+  const float* row = t + (r0 + lane % 32) * kLd<D> + (lane / 32) * (D / 2);
+#pragma unroll
+  for (int u = 0; u < D / 8; ++u) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(row + 4 * u);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = mfma2(a[e], f[4 * u + e], acc);
+  }
+}
+
+// The NB adjacent floats of tile row `r` this lane gives the NB output
+// blocks of a product over positions: columns NB (lane % 32) + (0..NB-1).
+template <int D>
+struct Cols {
+  float x[D / 32];
+};
+template <int D>
+__device__ __forceinline__ Cols<D> cols_of(const float* t, int r) {
+  constexpr int NB = D / 32;
+  const float* at = t + r * kLd<D> + NB * (threadIdx.x % 32);
+  Cols<D> c;
+  if constexpr (NB == 2) {
+    const f32x2 x = *reinterpret_cast<const f32x2*>(at);
+    c.x[0] = x[0], c.x[1] = x[1];
+  } else {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(at);
+#pragma unroll
+    for (int e = 0; e < NB; ++e) c.x[e] = x[e];
+  }
+  return c;
+}
+
+// out[db] += T'(d, positions of block pb) P over the block's 32 positions:
+// step i pairs position 8 (i / 4) + i % 4 (lanes 0..31) with the one 4
+// further (lanes 32..63), as register i of the score accumulator holds them.
+template <int D>
+__device__ __forceinline__ void over_positions(const float* t, int p0, const f32x16& pw, f32x16 (&out)[D / 32]) {
+  const int lh = (threadIdx.x % 64) / 32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const Cols<D> c = cols_of<D>(t, p0 + 8 * (i / 4) + 4 * lh + i % 4);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) out[db] = mfma2(c.x[db], pw[i], out[db]);
+  }
+}
+
+// Store an output block set: block db's register i holds d = NB (8 (i / 4) +
+// 4 lh + i % 4) + db, for the lane's position; scaled by sc.
+template <int D>
+__device__ __forceinline__ void store_rows(float* row, const f32x16 (&x)[D / 32], float sc) {
+  constexpr int NB = D / 32;
+  const int lh = (threadIdx.x % 64) / 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // d = NB (8 q + 4 lh) + (0 .. 4 NB - 1): register 4 q + e of block db at NB e + db.
+    float* at = row + NB * (8 * q + 4 * lh);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (NB == 2) {
+        *reinterpret_cast<f32x2*>(at + 2 * e) = f32x2{x[0][4 * q + e] * sc, x[1][4 * q + e] * sc};
+      } else {
+        *reinterpret_cast<f32x4*>(at + 4 * e) =
+            f32x4{x[0][4 * q + e] * sc, x[1][4 * q + e] * sc, x[2][4 * q + e] * sc, x[3][4 * q + e] * sc};
+      }
+    }
+  }
+}
+
+// A 64-position tile staged through registers: thread t holds the 16-byte
+// chunks t + 256 i; rows past `limit` read as zeros.
+template <int D>
+struct StageF {
+  static constexpr int kChunks = D / 4;
+  static constexpr int kPer = 64 * kChunks / 256;
+  f32x4 r[kPer];
+  __device__ void load(const float* base, int64_t ss, int row0, int limit) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i, row = c / kChunks, col = c % kChunks;
+      r[i] = row0 + row < limit ? *reinterpret_cast<const f32x4*>(base + (int64_t)(row0 + row) * ss + 4 * col)
+                                : f32x4{};
+    }
+  }
+  __device__ void store(float* t) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i, row = c / kChunks, col = c % kChunks;
+      *reinterpret_cast<f32x4*>(t + row * kLd<D> + 4 * col) = r[i];
+    }
+  }
+};
+
+// Causal sweeps do less work for earlier query blocks (and later key
+// blocks): workgroup x takes blocks x and nb - 1 - x (one pass each), so
+// every workgroup sweeps about the same number of tiles.
+__device__ __forceinline__ int passes(bool causal, int x, int nb) { return causal && 2 * x + 1 != nb ? 2 : 1; }
+__device__ __forceinline__ int block_of(int pass, int x, int nb) { return pass == 0 ? x : nb - 1 - x; }
+
+// ---- forward ---------------------------------------------------------------------
+
+template <int D>
+__device__ __forceinline__ void fwd_block(const FArgs& p, const int qb) {
+  constexpr int NB = D / 32;
+  extern __shared__ __attribute__((aligned(16))) float flds[];
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.heads / p.kv_heads);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
+  const int q0 = qb * 128 + wave * 32, query = q0 + lr;
+  const float* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+  const float* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const float* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  float qf[D / 2];
+  row_half<D>(qbase + (int64_t)query * p.q_ss, query < p.seq, qf);
+  f32x16 o[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) o[i] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+  const float c = p.scale * kLog2e;
+  const int qlast = min(qb * 128 + 127, p.seq - 1);
+  const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
+  const int nsteps = (kend + 63) / 64;
+  StageF<D> sk, sv;
+  auto K = [&](int s) { return flds + 2 * s * kTileF<D>; };
+  auto V = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
+  if (nsteps > 0) {
+    sk.load(kbase, p.k_ss, 0, p.kv_seq);
+    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.store(K(0));
+    sv.store(V(0));
+  }
+  __syncthreads();
+  for (int j = 0; j < nsteps; ++j) {
+    const int cur = j & 1, k0 = 64 * j;
+    if (j + 1 < nsteps) {
+      sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
+      sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
+    }
+    // S' (64 keys x 32 queries): key 32 kb + 8 (i / 4) + 4 lh + i % 4 in register i.
+    f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) over_d<D>(K(cur), 32 * kb, qf, s[kb]);
+    if (k0 + 64 > p.kv_seq || (p.causal && k0 + 64 > q0)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * lh + i % 4;
+          if (key >= p.kv_seq || (p.causal && key > query)) s[kb][i] = -INFINITY;
+        }
+    }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mb = fmaxf(mb, s[kb][i]);
+    mb = fmaxf(mb, other_half(mb)) * c;
+    const float mn = fmaxf(m, mb);
+    const float shift = isfinite(mn) ? mn : 0.0f;  // lse_shift (folds.jl:194)
+    const float alpha = __builtin_amdgcn_exp2f(m - shift);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) o[i] *= alpha;
+    m = mn;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float w = __builtin_amdgcn_exp2f(fmaf(s[kb][i], c, -shift));
+        l += w;
+        s[kb][i] = w;
+      }
+    // O' (D x 32 queries) += V' P'.
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) over_positions<D>(V(cur), 32 * kb, s[kb], o);
+    if (j + 1 < nsteps) {
+      // The other stage was last read in step j - 1, before the barrier that ended it.
+      sk.store(K(cur ^ 1));
+      sv.store(V(cur ^ 1));
+    }
+    __syncthreads();
+  }
+  l += other_half(l);
+  if (query >= p.seq) return;
+  store_rows<D>(p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss, o, 1.0f / l);
+  if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
+}
+
+template <int D>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void f32_attn_fwd(FArgs p) {
+  const int nb = (p.seq + 127) / 128;
+  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+    if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
+    fwd_block<D>(p, block_of(pass, blockIdx.x, nb));
+  }
+}
+
+// ---- backward: delta = rowsum(dO .* O) ---------------------------------------------
+
+struct FDeltaArgs {
+  FArgs p;  // first: its members sit at FArgs' offsets
+  int32_t d;
+};
+
+__global__ __launch_bounds__(256) void f32_attn_delta(FDeltaArgs a) {
+  const FArgs& p = a.p;
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;  // [b][s][h]
+  const int64_t total = (int64_t)p.batch * p.seq * p.heads;
+  if (row >= total) return;
+  const int h = (int)(row % p.heads);
+  const int64_t s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
+  const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss;
+  float v = 0.0f;
+  for (int c = threadIdx.x % 64; c < a.d; c += 64) v += p.o[at + c] * p.dout[at + c];
+  v = thd::wave_sum(v);
+  if (threadIdx.x % 64 == 0) p.delta[row] = v;
+}
+
+// ---- backward: dK, dV ----------------------------------------------------------------
+// A workgroup takes 128 keys (32 a wave).  Per query tile of 64: S (64
+// queries x 32 keys) with queries on the registers and keys on the lanes, so
+// that P and dS feed the products over queries straight from the
+// accumulators.
+
+template <int D>
+__device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk) {
+  constexpr int NB = D / 32;
+  extern __shared__ __attribute__((aligned(16))) float flds[];
+  float* stats = flds + 4 * kTileF<D>;  // [stage][lse * log2e (64) | delta (64)]
+  const int hk = blockIdx.y, b = blockIdx.z;
+  const int group = p.heads / p.kv_heads;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lh = lane / 32;
+  const int kw0 = kblk * 128, key = kw0 + wave * 32 + lane % 32;
+  const int64_t koff = (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  float kf[D / 2], vf[D / 2];
+  row_half<D>(p.k + koff + (int64_t)key * p.k_ss, key < p.kv_seq, kf);
+  row_half<D>(p.v + koff + (int64_t)key * p.k_ss, key < p.kv_seq, vf);
+  f32x16 dk[NB], dv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) dk[i] = f32x16{}, dv[i] = f32x16{};
+  const float c = p.scale * kLog2e;
+  auto Q = [&](int s) { return flds + 2 * s * kTileF<D>; };
+  auto G = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
+  auto Ls = [&](int s) { return stats + 128 * s; };
+  const int qstart = p.causal ? kw0 / 64 * 64 : 0;
+  const int nsteps = qstart < p.seq ? (p.seq - qstart + 63) / 64 : 0;
+  StageF<D> sq, sg;
+  float st = 0.0f;  // threads 0..127: a query's lse * log2e or delta
+  auto load = [&](const float* qbase, const float* gbase, int h, int q0) {
+    sq.load(qbase, p.q_ss, q0, p.seq);
+    sg.load(gbase, p.q_ss, q0, p.seq);
+    if (threadIdx.x < 128) {
+      const int j = q0 + threadIdx.x % 64;
+      const int64_t row = ((int64_t)b * p.seq + j) * p.heads + h;
+      st = j < p.seq ? (threadIdx.x < 64 ? p.lse[row] * kLog2e : p.delta[row]) : 0.0f;
+    }
+  };
+  auto store = [&](int s) {
+    sq.store(Q(s));
+    sg.store(G(s));
+    if (threadIdx.x < 128) Ls(s)[threadIdx.x] = st;
+  };
+  for (int h = hk * group; h < (hk + 1) * group; ++h) {
+    const float* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const float* gbase = p.dout + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    if (nsteps > 0) {
+      load(qbase, gbase, h, qstart);
+      store(0);
+    }
+    __syncthreads();
+    for (int j = 0; j < nsteps; ++j) {
+      const int cur = j & 1, qq0 = qstart + 64 * j;
+      if (j + 1 < nsteps) load(qbase, gbase, h, qq0 + 64);
+      const float *Qt = Q(cur), *Gt = G(cur);
+      const float* L = Ls(cur);
+      // The tile's two halves of 32 queries in turn (half the score
+      // accumulators live at once); the next tile goes to LDS after the first.
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        // S = Q K', dP = dO V' (32 queries x 32 keys): query 32 jj + 8 (i / 4) + 4 lh + i % 4 in register i.
+        f32x16 s = {}, dp = {};
+        over_d<D>(Qt, 32 * jj, kf, s);
+        over_d<D>(Gt, 32 * jj, vf, dp);
+        // P into s, dS into dp.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int qi = 32 * jj + 8 * (i / 4) + 4 * lh + i % 4, query = qq0 + qi;
+          const bool seen = query < p.seq && key < p.kv_seq && (!p.causal || key <= query);
+          const float w = seen ? __builtin_amdgcn_exp2f(fmaf(s[i], c, -L[qi])) : 0.0f;
+          s[i] = w;
+          dp[i] = w * (dp[i] - L[64 + qi]);
+        }
+        // dV' (D x 32 keys) += dO' P;  dK' += Q' dS.
+        over_positions<D>(Gt, 32 * jj, s, dv);
+        over_positions<D>(Qt, 32 * jj, dp, dk);
+        // The other stage was last read in step j - 1, before the barrier that ended it.
+        if (jj == 0 && j + 1 < nsteps) store(cur ^ 1);
+      }
+      __syncthreads();
+    }
+  }
+  if (key >= p.kv_seq) return;
+  const int64_t out = koff + (int64_t)key * p.k_ss;
+  store_rows<D>(p.dk + out, dk, p.scale);
+  store_rows<D>(p.dv + out, dv, 1.0f);
+}
+
+template <int D>
+// One wave a SIMD: K and V of the wave's keys, dK' and dV' take D + D registers.
+__global__ __launch_bounds__(256, 1) void f32_attn_dkdv(FArgs p) {
+  const int nb = (p.kv_seq + 127) / 128;
+  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+    if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
+    dkdv_block<D>(p, block_of(pass, blockIdx.x, nb));
+  }
+}
+
+// ---- backward: dQ ----------------------------------------------------------------------
+// A workgroup takes 128 queries (32 a wave) and sweeps key tiles of 64:
+// S' = K Q', dP' = V dO' (keys on the registers, queries on the lanes),
+// dS' = P' (dP' - delta), dQ' (D x 32 queries) += K' dS'.
+
+template <int D>
+__device__ __forceinline__ void dq_block(const FArgs& p, const int qb) {
+  constexpr int NB = D / 32;
+  extern __shared__ __attribute__((aligned(16))) float flds[];
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (p.heads / p.kv_heads);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lh = lane / 32;
+  const int q0 = qb * 128 + wave * 32, query = q0 + lane % 32;
+  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
+  const bool live = query < p.seq;
+  float qf[D / 2], gf[D / 2];
+  row_half<D>(p.q + qoff, live, qf);
+  row_half<D>(p.dout + qoff, live, gf);
+  const int64_t srow = ((int64_t)b * p.seq + query) * p.heads + h;
+  const float l2 = live ? p.lse[srow] * kLog2e : 0.0f;
+  const float dl = live ? p.delta[srow] : 0.0f;
+  const float c = p.scale * kLog2e;
+  const float* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const float* vbase = p.v + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  f32x16 dq[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) dq[i] = f32x16{};
+  const int qlast = min(qb * 128 + 127, p.seq - 1);
+  const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
+  const int nsteps = (kend + 63) / 64;
+  StageF<D> sk, sv;
+  auto K = [&](int s) { return flds + 2 * s * kTileF<D>; };
+  auto V = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
+  if (nsteps > 0) {
+    sk.load(kbase, p.k_ss, 0, p.kv_seq);
+    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.store(K(0));
+    sv.store(V(0));
+  }
+  __syncthreads();
+  for (int j = 0; j < nsteps; ++j) {
+    const int cur = j & 1, k0 = 64 * j;
+    if (j + 1 < nsteps) {
+      sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
+      sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
+    }
+    // The tile's two halves of 32 keys in turn; the next tile goes to LDS after the first.
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 sc = {}, dp = {};
+      over_d<D>(K(cur), 32 * kb, qf, sc);
+      over_d<D>(V(cur), 32 * kb, gf, dp);
+      // dS' into sc.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * lh + i % 4;
+        const bool seen = key < p.kv_seq && (!p.causal || key <= query);
+        const float pw = seen ? __builtin_amdgcn_exp2f(fmaf(sc[i], c, -l2)) : 0.0f;
+        sc[i] = pw * (dp[i] - dl);
+      }
+      over_positions<D>(K(cur), 32 * kb, sc, dq);
+      if (kb == 0 && j + 1 < nsteps) {
+        sk.store(K(cur ^ 1));
+        sv.store(V(cur ^ 1));
+      }
+    }
+    __syncthreads();
+  }
+  if (!live) return;
+  store_rows<D>(p.dq + qoff, dq, p.scale);
+}
+
+template <int D>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void f32_attn_dq(FArgs p) {
+  const int nb = (p.seq + 127) / 128;
+  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+    if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
+    dq_block<D>(p, block_of(pass, blockIdx.x, nb));
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+unsigned blocks_of(int n, int causal) {
+  const unsigned nb = (unsigned)((n + 127) / 128);
+  return causal ? (nb + 1) / 2 : nb;
+}
+
+FArgs fargs_of(const th_attention_desc* d) {
+  FArgs a{};
+  a.q = static_cast<const float*>(d->q);
+  a.k = static_cast<const float*>(d->k);
+  a.v = static_cast<const float*>(d->v);
+  a.o = static_cast<float*>(d->o);
+  a.lse = d->lse;
+  a.dout = static_cast<const float*>(d->dout);
+  a.dq = static_cast<float*>(d->dq);
+  a.dk = static_cast<float*>(d->dk);
+  a.dv = static_cast<float*>(d->dv);
+  a.q_sh = d->q_strides[0], a.q_ss = d->q_strides[1], a.q_sb = d->q_strides[2];
+  a.k_sh = d->k_strides[0], a.k_ss = d->k_strides[1], a.k_sb = d->k_strides[2];
+  a.seq = d->seq;
+  a.kv_seq = d->kv_seq > 0 ? d->kv_seq : d->seq;
+  a.heads = d->heads, a.kv_heads = d->kv_heads, a.batch = d->batch, a.causal = d->causal;
+  a.scale = d->scale > 0 ? d->scale : 1.0f / sqrtf((float)d->head_dim);
+  return a;
+}
+
+double visible_pairs(const FArgs& a) {
+  const double S = a.seq, K = a.kv_seq;
+  if (!a.causal) return S * K;
+  const double full = std::min(S, K);
+  return full * (full + 1) / 2 + std::max(0.0, S - K) * K;
+}
+
+template <int D>
+int fwd_launch(const th_attention_desc* d, th_launch** out) {
+  const size_t lds = 4 * (size_t)kTileF<D> * sizeof(float);
+  TH_HIP(hipFuncSetAttribute((const void*)f32_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  FArgs a = fargs_of(d);
+  th::Builder b("attention_fwd_f32mfma", 7);
+  const dim3 grid(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  int k = b.kernel((const void*)f32_attn_fwd<D>, D == 64 ? "f32_attn_fwd_d64" : "f32_attn_fwd_d128", grid, dim3(256),
+                   (uint32_t)lds, a);
+  b.ref(0, k, TH_OFFSET(FArgs, q));
+  b.ref(1, k, TH_OFFSET(FArgs, k));
+  b.ref(2, k, TH_OFFSET(FArgs, v));
+  b.ref(3, k, TH_OFFSET(FArgs, o));
+  b.ref(4, k, TH_OFFSET(FArgs, lse));
+  for (int v = 0; v < 4; ++v) b.align(v, 16);
+  const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
+  b.work(2.0 * BH * a.seq * D * 4 + 2.0 * BHk * a.kv_seq * D * 4 + 4.0 * BH * a.seq, 4.0 * BH * D * visible_pairs(a),
+         (int64_t)grid.x * grid.y * grid.z);
+  *out = b.release();
+  return TH_OK;
+}
+
+template <int D>
+int bwd_launch(const th_attention_desc* d, th_launch** out) {
+  const size_t lds_kv = 4 * (size_t)kTileF<D> * sizeof(float);
+  const size_t lds_dkdv = lds_kv + 2 * 128 * sizeof(float);
+  TH_HIP(hipFuncSetAttribute((const void*)f32_attn_dkdv<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)lds_dkdv));
+  TH_HIP(hipFuncSetAttribute((const void*)f32_attn_dq<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_kv));
+  FArgs a = fargs_of(d);
+  th::Builder b("attention_bwd_f32mfma", 11);
+  const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+  const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));
+  int k0 = b.kernel((const void*)f32_attn_delta, "f32_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                    FDeltaArgs{a, D});
+  const dim3 gkv(blocks_of(a.kv_seq, d->causal), d->kv_heads, d->batch);
+  const dim3 gq(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  int k1 = b.kernel((const void*)f32_attn_dkdv<D>, D == 64 ? "f32_attn_dkdv_d64" : "f32_attn_dkdv_d128", gkv,
+                    dim3(256), (uint32_t)lds_dkdv, a);
+  int k2 = b.kernel((const void*)f32_attn_dq<D>, D == 64 ? "f32_attn_dq_d64" : "f32_attn_dq_d128", gq, dim3(256),
+                    (uint32_t)lds_kv, a);
+  const size_t offs[9] = {TH_OFFSET(FArgs, q),  TH_OFFSET(FArgs, k),  TH_OFFSET(FArgs, v),
+                          TH_OFFSET(FArgs, o),  TH_OFFSET(FArgs, lse), TH_OFFSET(FArgs, dout),
+                          TH_OFFSET(FArgs, dq), TH_OFFSET(FArgs, dk),  TH_OFFSET(FArgs, dv)};
+  // The delta kernel's arguments are FArgs followed by d: the same offsets.
+  for (int v = 0; v < 9; ++v)
+    for (int kk : {k0, k1, k2}) b.ref(v, kk, offs[v]);
+  for (int kk : {k0, k1, k2}) b.ws_ref(kk, TH_OFFSET(FArgs, delta), at_delta);
+  for (int v : {0, 1, 2, 3, 5, 6, 7, 8}) b.align(v, 16);
+  const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
+  b.work(2.0 * BH * a.seq * D * 8 + 2.0 * BHk * a.kv_seq * D * 8 + 8.0 * BH * a.seq,
+         2.5 * 4.0 * BH * D * visible_pairs(a), (int64_t)gkv.x * gkv.y * gkv.z);
+  *out = b.release();
+  return TH_OK;
+}
+
+}  // namespace
+
+namespace th {
+
+// fp32 arrays, head dim 64 or 128, positive lengths, no device-held masks,
+// 16-byte aligned operands and rows (strides multiples of 4 floats).
+bool f32_attention_takes(const th_attention_desc* d) {
+  if (!d || !(d->flags & TH_ATTN_F32) || d->starts || d->lengths) return false;
+  if (d->head_dim != 64 && d->head_dim != 128) return false;
+  if (d->seq < 1 || d->kv_seq < 0 || d->batch < 1 || d->heads < 1 || d->kv_heads < 1 || d->heads % d->kv_heads)
+    return false;
+  for (int64_t s : {d->q_strides[0], d->q_strides[1], d->q_strides[2], d->k_strides[0], d->k_strides[1], d->k_strides[2]})
+    if (s <= 0 || s % 4) return false;
+  for (const void* ptr : {(const void*)d->q, (const void*)d->k, (const void*)d->v, (const void*)d->o,
+                          (const void*)d->dout, (const void*)d->dq, (const void*)d->dk, (const void*)d->dv})
+    if (!aligned16(ptr)) return false;
+  const int64_t kv = d->kv_seq > 0 ? d->kv_seq : d->seq;
+  return (d->seq + 127) / 128 <= 0x7fffffff && (kv + 127) / 128 <= 0x7fffffff && d->heads <= 65535 &&
+         d->batch <= 65535;
+}
+
+int build_attention_f32_fwd(const th_attention_desc* d, th_launch** out) {
+  TH_REQUIRE(d->q && d->k && d->v && d->o, "attention: null q, k, v or o");
+  return d->head_dim == 64 ? fwd_launch<64>(d, out) : fwd_launch<128>(d, out);
+}
+
+int build_attention_f32_bwd(const th_attention_desc* d, th_launch** out) {
+  TH_REQUIRE(d->q && d->k && d->v && d->o, "attention: null q, k, v or o");
+  TH_REQUIRE(d->lse && d->dout && d->dq && d->dk && d->dv, "attention backward: null lse, dout, dq, dk or dv");
+  return d->head_dim == 64 ? bwd_launch<64>(d, out) : bwd_launch<128>(d, out);
+}
+
+}  // namespace th

@@ -199,6 +199,11 @@ int build_attention_general_bwd(const th_attention_desc* d, th_launch** out);
 bool mfma_attention_takes(const th_attention_desc* d);
 int build_attention_mfma_fwd(const th_attention_desc* d, th_launch** out);
 int build_attention_mfma_bwd(const th_attention_desc* d, th_launch** out);
+// fp32 arrays on the matrix cores (attention_f32.hip): head dims 64 and 128,
+// no device-held masks.
+bool f32_attention_takes(const th_attention_desc* d);
+int build_attention_f32_fwd(const th_attention_desc* d, th_launch** out);
+int build_attention_f32_bwd(const th_attention_desc* d, th_launch** out);
 // Products the bf16 tile kernel does not take (gemm_general.hip).
 int build_gemm_general(const th_gemm_desc* d, th_launch** out);
 
