@@ -58,6 +58,12 @@ struct FArgs {
   int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
   int32_t seq, kv_seq, heads, kv_heads, batch, causal;
   float scale;
+  // A sweep split into parts (small grids): nsplit parts of `span`
+  // positions (a multiple of 64), partial results in `part`
+  // ([part][b][position][head][d]) and the forward's (m, l) in `part_ml`.
+  int32_t nsplit, span;
+  float* part;
+  float* part_ml;
 };
 
 __device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
@@ -190,11 +196,13 @@ __device__ __forceinline__ int block_of(int pass, int x, int nb) { return pass =
 
 // ---- forward ---------------------------------------------------------------------
 
+// Keys [k_lo, k_hi) of query block qb: all (split < 0) or part `split`,
+// which leaves its unnormalised O' and (m, l) for the combining kernel.
 template <int D>
-__device__ __forceinline__ void fwd_block(const FArgs& p, const int qb) {
+__device__ __forceinline__ void fwd_block(const FArgs& p, const int qb, const int b, const int split) {
   constexpr int NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) float flds[];
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lr;
@@ -210,19 +218,20 @@ __device__ __forceinline__ void fwd_block(const FArgs& p, const int qb) {
   const float c = p.scale * kLog2e;
   const int qlast = min(qb * 128 + 127, p.seq - 1);
   const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
-  const int nsteps = (kend + 63) / 64;
+  const int k_lo = split < 0 ? 0 : split * p.span, k_hi = split < 0 ? kend : min(kend, k_lo + p.span);
+  const int nsteps = k_hi > k_lo ? (k_hi - k_lo + 63) / 64 : 0;
   StageF<D> sk, sv;
   auto K = [&](int s) { return flds + 2 * s * kTileF<D>; };
   auto V = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
   if (nsteps > 0) {
-    sk.load(kbase, p.k_ss, 0, p.kv_seq);
-    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.load(kbase, p.k_ss, k_lo, p.kv_seq);
+    sv.load(vbase, p.k_ss, k_lo, p.kv_seq);
     sk.store(K(0));
     sv.store(V(0));
   }
   __syncthreads();
   for (int j = 0; j < nsteps; ++j) {
-    const int cur = j & 1, k0 = 64 * j;
+    const int cur = j & 1, k0 = k_lo + 64 * j;
     if (j + 1 < nsteps) {
       sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
       sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
@@ -273,17 +282,86 @@ __device__ __forceinline__ void fwd_block(const FArgs& p, const int qb) {
   }
   l += other_half(l);
   if (query >= p.seq) return;
+  if (split >= 0) {
+    // This part's unnormalised O' and (m, l) (m = -inf, l = 0 where it saw no key).
+    const int64_t row = (((int64_t)split * p.batch + b) * p.seq + query) * p.heads + h;
+    store_rows<D>(p.part + row * D, o, 1.0f);
+    if (lh == 0) reinterpret_cast<f32x2*>(p.part_ml)[row] = f32x2{m, l};
+    return;
+  }
   store_rows<D>(p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss, o, 1.0f / l);
   if (lh == 0 && p.lse) p.lse[((int64_t)b * p.seq + query) * p.heads + h] = (m + log2f(l)) * kLn2;
 }
 
 template <int D>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void f32_attn_fwd(FArgs p) {
+  // Split: one part of one block; else a block and, causal, its mirror (one call site).
+  const bool split = p.nsplit > 1;
   const int nb = (p.seq + 127) / 128;
-  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+  const int npass = split ? 1 : passes(p.causal, blockIdx.x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
     if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
-    fwd_block<D>(p, block_of(pass, blockIdx.x, nb));
+    fwd_block<D>(p, split ? blockIdx.x : block_of(pass, blockIdx.x, nb), split ? blockIdx.z / p.nsplit : blockIdx.z,
+                 split ? blockIdx.z % p.nsplit : -1);
   }
+}
+
+// The parts of a split forward combined: per (b, query, head) row, M = max
+// m_s, L = sum l_s 2^(m_s - M), O = sum O_s 2^(m_s - M) / L in part order;
+// lse = (M + log2 L) ln 2.  A thread per four features of a row.
+struct FCombineArgs {
+  FArgs p;  // first: its members sit at FArgs' offsets
+  int32_t d;
+};
+
+__global__ __launch_bounds__(256) void f32_attn_combine(FCombineArgs a) {
+  const FArgs& p = a.p;
+  const int quads = a.d / 4;
+  const int64_t rows = (int64_t)p.batch * p.seq * p.heads;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * quads) return;
+  const int64_t row = t / quads;
+  const int c = 4 * (int)(t % quads);
+  const f32x2* ml = reinterpret_cast<const f32x2*>(p.part_ml);
+  float mx = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, ml[s * rows + row][0]);
+  const float shift = isfinite(mx) ? mx : 0.0f;
+  float l = 0.0f;
+  f32x4 acc = {};
+  for (int s = 0; s < p.nsplit; ++s) {
+    const f32x2 x = ml[s * rows + row];
+    const float w = __builtin_amdgcn_exp2f(x[0] - shift);
+    l += w * x[1];
+    acc += w * *reinterpret_cast<const f32x4*>(p.part + (s * rows + row) * a.d + c);
+  }
+  const int h = (int)(row % p.heads);
+  const int64_t pos = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
+  *reinterpret_cast<f32x4*>(p.o + b * p.q_sb + h * p.q_sh + pos * p.q_ss + c) = acc * (1.0f / l);
+  if (c == 0 && p.lse) p.lse[row] = (mx + log2f(l)) * kLn2;
+}
+
+// dQ, dK or dV from a split sweep's parts: out = scale * sum_s part_s in
+// part order; rows [b][position][head] of `d` features.
+struct FSumArgs {
+  const float* part;
+  float* out;
+  int64_t sh, ss, sb;
+  int32_t positions, heads, batch, d, nsplit;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void f32_attn_sum(FSumArgs a) {
+  const int quads = a.d / 4;
+  const int64_t rows = (int64_t)a.batch * a.positions * a.heads;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * quads) return;
+  const int64_t row = t / quads;
+  const int c = 4 * (int)(t % quads);
+  f32x4 acc = {};
+  for (int s = 0; s < a.nsplit; ++s) acc += *reinterpret_cast<const f32x4*>(a.part + (s * rows + row) * a.d + c);
+  const int h = (int)(row % a.heads);
+  const int64_t pos = (row / a.heads) % a.positions, b = row / ((int64_t)a.heads * a.positions);
+  *reinterpret_cast<f32x4*>(a.out + b * a.sb + h * a.sh + pos * a.ss + c) = acc * a.scale;
 }
 
 // ---- backward: delta = rowsum(dO .* O) ---------------------------------------------
@@ -313,12 +391,14 @@ __global__ __launch_bounds__(256) void f32_attn_delta(FDeltaArgs a) {
 // that P and dS feed the products over queries straight from the
 // accumulators.
 
+// Query tiles [qstart, qstop) for the keys of kblk: all (split < 0) or part
+// `split`, which leaves its unscaled dK', dV'.
 template <int D>
-__device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk) {
+__device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk, const int b, const int split) {
   constexpr int NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) float flds[];
   float* stats = flds + 4 * kTileF<D>;  // [stage][lse * log2e (64) | delta (64)]
-  const int hk = blockIdx.y, b = blockIdx.z;
+  const int hk = blockIdx.y;
   const int group = p.heads / p.kv_heads;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lh = lane / 32;
   const int kw0 = kblk * 128, key = kw0 + wave * 32 + lane % 32;
@@ -333,8 +413,10 @@ __device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk) {
   auto Q = [&](int s) { return flds + 2 * s * kTileF<D>; };
   auto G = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
   auto Ls = [&](int s) { return stats + 128 * s; };
-  const int qstart = p.causal ? kw0 / 64 * 64 : 0;
-  const int nsteps = qstart < p.seq ? (p.seq - qstart + 63) / 64 : 0;
+  const int qfirst = p.causal ? kw0 / 64 * 64 : 0;
+  const int qstart = split < 0 ? qfirst : qfirst + split * p.span;
+  const int qstop = split < 0 ? p.seq : min(p.seq, qstart + p.span);
+  const int nsteps = qstart < qstop ? (qstop - qstart + 63) / 64 : 0;
   StageF<D> sq, sg;
   float st = 0.0f;  // threads 0..127: a query's lse * log2e or delta
   auto load = [&](const float* qbase, const float* gbase, int h, int q0) {
@@ -391,6 +473,13 @@ __device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk) {
     }
   }
   if (key >= p.kv_seq) return;
+  if (split >= 0) {
+    const int64_t rows = (int64_t)p.batch * p.kv_seq * p.kv_heads;
+    const int64_t row = (((int64_t)split * p.batch + b) * p.kv_seq + key) * p.kv_heads + hk;
+    store_rows<D>(p.part + row * D, dk, 1.0f);
+    store_rows<D>(p.part + ((int64_t)p.nsplit * rows + row) * D, dv, 1.0f);
+    return;
+  }
   const int64_t out = koff + (int64_t)key * p.k_ss;
   store_rows<D>(p.dk + out, dk, p.scale);
   store_rows<D>(p.dv + out, dv, 1.0f);
@@ -399,10 +488,13 @@ __device__ __forceinline__ void dkdv_block(const FArgs& p, const int kblk) {
 template <int D>
 // One wave a SIMD: K and V of the wave's keys, dK' and dV' take D + D registers.
 __global__ __launch_bounds__(256, 1) void f32_attn_dkdv(FArgs p) {
+  const bool split = p.nsplit > 1;
   const int nb = (p.kv_seq + 127) / 128;
-  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+  const int npass = split ? 1 : passes(p.causal, blockIdx.x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
     if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
-    dkdv_block<D>(p, block_of(pass, blockIdx.x, nb));
+    dkdv_block<D>(p, split ? blockIdx.x : block_of(pass, blockIdx.x, nb), split ? blockIdx.z / p.nsplit : blockIdx.z,
+                  split ? blockIdx.z % p.nsplit : -1);
   }
 }
 
@@ -411,11 +503,13 @@ __global__ __launch_bounds__(256, 1) void f32_attn_dkdv(FArgs p) {
 // S' = K Q', dP' = V dO' (keys on the registers, queries on the lanes),
 // dS' = P' (dP' - delta), dQ' (D x 32 queries) += K' dS'.
 
+// Keys [k_lo, k_hi) for query block qb: all (split < 0) or part `split`,
+// which leaves its unscaled dQ'.
 template <int D>
-__device__ __forceinline__ void dq_block(const FArgs& p, const int qb) {
+__device__ __forceinline__ void dq_block(const FArgs& p, const int qb, const int b, const int split) {
   constexpr int NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) float flds[];
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lane % 32;
@@ -435,19 +529,20 @@ __device__ __forceinline__ void dq_block(const FArgs& p, const int qb) {
   for (int i = 0; i < NB; ++i) dq[i] = f32x16{};
   const int qlast = min(qb * 128 + 127, p.seq - 1);
   const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
-  const int nsteps = (kend + 63) / 64;
+  const int k_lo = split < 0 ? 0 : split * p.span, k_hi = split < 0 ? kend : min(kend, k_lo + p.span);
+  const int nsteps = k_hi > k_lo ? (k_hi - k_lo + 63) / 64 : 0;
   StageF<D> sk, sv;
   auto K = [&](int s) { return flds + 2 * s * kTileF<D>; };
   auto V = [&](int s) { return flds + (2 * s + 1) * kTileF<D>; };
   if (nsteps > 0) {
-    sk.load(kbase, p.k_ss, 0, p.kv_seq);
-    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.load(kbase, p.k_ss, k_lo, p.kv_seq);
+    sv.load(vbase, p.k_ss, k_lo, p.kv_seq);
     sk.store(K(0));
     sv.store(V(0));
   }
   __syncthreads();
   for (int j = 0; j < nsteps; ++j) {
-    const int cur = j & 1, k0 = 64 * j;
+    const int cur = j & 1, k0 = k_lo + 64 * j;
     if (j + 1 < nsteps) {
       sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
       sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
@@ -475,15 +570,22 @@ __device__ __forceinline__ void dq_block(const FArgs& p, const int qb) {
     __syncthreads();
   }
   if (!live) return;
+  if (split >= 0) {
+    store_rows<D>(p.part + ((((int64_t)split * p.batch + b) * p.seq + query) * p.heads + h) * D, dq, 1.0f);
+    return;
+  }
   store_rows<D>(p.dq + qoff, dq, p.scale);
 }
 
 template <int D>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void f32_attn_dq(FArgs p) {
+  const bool split = p.nsplit > 1;
   const int nb = (p.seq + 127) / 128;
-  for (int pass = 0; pass < passes(p.causal, blockIdx.x, nb); ++pass) {
+  const int npass = split ? 1 : passes(p.causal, blockIdx.x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
     if (pass > 0) __syncthreads();  // the first pass's last LDS reads are done
-    dq_block<D>(p, block_of(pass, blockIdx.x, nb));
+    dq_block<D>(p, split ? blockIdx.x : block_of(pass, blockIdx.x, nb), split ? blockIdx.z / p.nsplit : blockIdx.z,
+                split ? blockIdx.z % p.nsplit : -1);
   }
 }
 
@@ -526,8 +628,12 @@ int fwd_launch(const th_attention_desc* d, th_launch** out) {
   const size_t lds = 4 * (size_t)kTileF<D> * sizeof(float);
   TH_HIP(hipFuncSetAttribute((const void*)f32_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   FArgs a = fargs_of(d);
+  const int nqb = (d->seq + 127) / 128;
+  const th::Split sp = th::split_of((int64_t)nqb * d->heads * d->batch, a.kv_seq);
+  a.nsplit = sp.n, a.span = sp.span;
+  TH_REQUIRE((int64_t)d->batch * sp.n <= 65535, "attention: grid too large");
   th::Builder b("attention_fwd_f32mfma", 7);
-  const dim3 grid(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  const dim3 grid = sp.n > 1 ? dim3(nqb, d->heads, d->batch * sp.n) : dim3(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k = b.kernel((const void*)f32_attn_fwd<D>, D == 64 ? "f32_attn_fwd_d64" : "f32_attn_fwd_d128", grid, dim3(256),
                    (uint32_t)lds, a);
   b.ref(0, k, TH_OFFSET(FArgs, q));
@@ -535,6 +641,19 @@ int fwd_launch(const th_attention_desc* d, th_launch** out) {
   b.ref(2, k, TH_OFFSET(FArgs, v));
   b.ref(3, k, TH_OFFSET(FArgs, o));
   b.ref(4, k, TH_OFFSET(FArgs, lse));
+  if (sp.n > 1) {
+    const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+    const uint64_t at_o = b.workspace((uint64_t)sp.n * rows * D * sizeof(float));
+    const uint64_t at_ml = b.workspace((uint64_t)sp.n * rows * 2 * sizeof(float));
+    int kc = b.kernel((const void*)f32_attn_combine, "f32_attn_combine", dim3((unsigned)((rows * (D / 4) + 255) / 256)),
+                      dim3(256), 0, FCombineArgs{a, D});
+    for (int kk : {k, kc}) {
+      b.ws_ref(kk, TH_OFFSET(FArgs, part), at_o);
+      b.ws_ref(kk, TH_OFFSET(FArgs, part_ml), at_ml);
+    }
+    b.ref(3, kc, TH_OFFSET(FArgs, o));
+    b.ref(4, kc, TH_OFFSET(FArgs, lse));
+  }
   for (int v = 0; v < 4; ++v) b.align(v, 16);
   const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
   b.work(2.0 * BH * a.seq * D * 4 + 2.0 * BHk * a.kv_seq * D * 4 + 4.0 * BH * a.seq, 4.0 * BH * D * visible_pairs(a),
@@ -553,15 +672,50 @@ int bwd_launch(const th_attention_desc* d, th_launch** out) {
   FArgs a = fargs_of(d);
   th::Builder b("attention_bwd_f32mfma", 11);
   const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+  const int64_t rows_k = (int64_t)d->batch * a.kv_seq * d->kv_heads;
   const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));
+  // Small grids split the dK/dV sweep over queries and the dQ sweep over keys.
+  const int nkb = (a.kv_seq + 127) / 128, nqb = (d->seq + 127) / 128;
+  const th::Split skv = th::split_of((int64_t)nkb * d->kv_heads * d->batch, d->seq);
+  const th::Split sq = th::split_of((int64_t)nqb * d->heads * d->batch, a.kv_seq);
+  TH_REQUIRE((int64_t)d->batch * std::max(skv.n, sq.n) <= 65535, "attention: grid too large");
+  FArgs akv = a, aq = a;
+  akv.nsplit = skv.n, akv.span = skv.span;
+  aq.nsplit = sq.n, aq.span = sq.span;
   int k0 = b.kernel((const void*)f32_attn_delta, "f32_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                     FDeltaArgs{a, D});
-  const dim3 gkv(blocks_of(a.kv_seq, d->causal), d->kv_heads, d->batch);
-  const dim3 gq(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  const dim3 gkv = skv.n > 1 ? dim3(nkb, d->kv_heads, d->batch * skv.n) : dim3(blocks_of(a.kv_seq, d->causal), d->kv_heads, d->batch);
+  const dim3 gq = sq.n > 1 ? dim3(nqb, d->heads, d->batch * sq.n) : dim3(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k1 = b.kernel((const void*)f32_attn_dkdv<D>, D == 64 ? "f32_attn_dkdv_d64" : "f32_attn_dkdv_d128", gkv,
-                    dim3(256), (uint32_t)lds_dkdv, a);
+                    dim3(256), (uint32_t)lds_dkdv, akv);
+  if (skv.n > 1) {
+    const uint64_t at_kv = b.workspace((uint64_t)2 * skv.n * rows_k * D * sizeof(float));
+    b.ws_ref(k1, TH_OFFSET(FArgs, part), at_kv);
+    const unsigned g = (unsigned)((rows_k * (D / 4) + 255) / 256);
+    // The outputs' pointers start as the descriptor's (repointing rewrites them with the others).
+    FSumArgs sk{nullptr, static_cast<float*>(d->dk), d->k_strides[0], d->k_strides[1], d->k_strides[2], a.kv_seq,
+                d->kv_heads, d->batch, D, skv.n, a.scale};
+    FSumArgs sv = sk;
+    sv.out = static_cast<float*>(d->dv), sv.scale = 1.0f;
+    const int ks = b.kernel((const void*)f32_attn_sum, "f32_attn_sum_dk", dim3(g), dim3(256), 0, sk);
+    const int kv = b.kernel((const void*)f32_attn_sum, "f32_attn_sum_dv", dim3(g), dim3(256), 0, sv);
+    b.ws_ref(ks, TH_OFFSET(FSumArgs, part), at_kv);
+    b.ws_ref(kv, TH_OFFSET(FSumArgs, part), at_kv + (uint64_t)skv.n * rows_k * D * sizeof(float));
+    b.ref(7, ks, TH_OFFSET(FSumArgs, out));
+    b.ref(8, kv, TH_OFFSET(FSumArgs, out));
+  }
   int k2 = b.kernel((const void*)f32_attn_dq<D>, D == 64 ? "f32_attn_dq_d64" : "f32_attn_dq_d128", gq, dim3(256),
-                    (uint32_t)lds_kv, a);
+                    (uint32_t)lds_kv, aq);
+  if (sq.n > 1) {
+    const uint64_t at_q = b.workspace((uint64_t)sq.n * rows * D * sizeof(float));
+    b.ws_ref(k2, TH_OFFSET(FArgs, part), at_q);
+    FSumArgs s1{nullptr, static_cast<float*>(d->dq), d->q_strides[0], d->q_strides[1], d->q_strides[2], d->seq,
+                d->heads, d->batch, D, sq.n, a.scale};
+    const int kq = b.kernel((const void*)f32_attn_sum, "f32_attn_sum_dq", dim3((unsigned)((rows * (D / 4) + 255) / 256)),
+                            dim3(256), 0, s1);
+    b.ws_ref(kq, TH_OFFSET(FSumArgs, part), at_q);
+    b.ref(6, kq, TH_OFFSET(FSumArgs, out));
+  }
   const size_t offs[9] = {TH_OFFSET(FArgs, q),  TH_OFFSET(FArgs, k),  TH_OFFSET(FArgs, v),
                           TH_OFFSET(FArgs, o),  TH_OFFSET(FArgs, lse), TH_OFFSET(FArgs, dout),
                           TH_OFFSET(FArgs, dq), TH_OFFSET(FArgs, dk),  TH_OFFSET(FArgs, dv)};

@@ -63,6 +63,13 @@ struct MArgs {
   int64_t k_sh, k_ss, k_sb;  // strides of k, v, dk, dv
   int32_t seq, kv_seq, heads, kv_heads, batch, causal;
   float scale;
+  // A sweep split into parts (small grids): nsplit parts of `span`
+  // positions (a multiple of 64) each, fp32 partial results in `part`
+  // ([part][b][position][head][d]) and, for the forward, (m, l) in
+  // `part_ml`; nsplit <= 1: no split.
+  int32_t nsplit, span;
+  float* part;
+  float* part_ml;
 };
 
 __device__ __forceinline__ float bf16_float(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
@@ -144,19 +151,19 @@ constexpr int kTile = 64 * (D + 8);  // bf16 elements of a tile in LDS
 // Causal sweeps do less work for earlier query blocks (and later key
 // blocks): workgroup x takes blocks x and nb - 1 - x, so every workgroup
 // sweeps about the same number of tiles.
-template <class F>
-__device__ __forceinline__ void mirrored(bool causal, int x, int nb, F&& f) {
-  f(x);
-  if (causal && 2 * x + 1 != nb) f(nb - 1 - x);
-}
+__device__ __forceinline__ int passes(bool causal, int x, int nb) { return causal && 2 * x + 1 != nb ? 2 : 1; }
+__device__ __forceinline__ int block_of(int pass, int x, int nb) { return pass == 0 ? x : nb - 1 - x; }
 
 // ---- forward ---------------------------------------------------------------------
 
+// Keys [k_lo, k_hi) of query block qb: all of them (split < 0), or part
+// `split` of the sweep, which leaves its unnormalised O' and (m, l) for the
+// combining kernel.
 template <int D>
-__device__ __forceinline__ void fwd_block(const MArgs& p, const int qb) {
+__device__ __forceinline__ void fwd_block(const MArgs& p, const int qb, const int b, const int split) {
   constexpr int NS = D / 16, NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lr;
@@ -172,19 +179,20 @@ __device__ __forceinline__ void fwd_block(const MArgs& p, const int qb) {
   const float c = p.scale * kLog2e;
   const int qlast = min(qb * 128 + 127, p.seq - 1);
   const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
-  const int nsteps = (kend + 63) / 64;
+  const int k_lo = split < 0 ? 0 : split * p.span, k_hi = split < 0 ? kend : min(kend, k_lo + p.span);
+  const int nsteps = k_hi > k_lo ? (k_hi - k_lo + 63) / 64 : 0;
   Stage<D> sk, sv;
   auto K = [&](int s) { return lds + 2 * s * kTile<D>; };
   auto V = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
   if (nsteps > 0) {
-    sk.load(kbase, p.k_ss, 0, p.kv_seq);
-    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.load(kbase, p.k_ss, k_lo, p.kv_seq);
+    sv.load(vbase, p.k_ss, k_lo, p.kv_seq);
     sk.store(K(0));
     sv.store(V(0));
   }
   __syncthreads();
   for (int j = 0; j < nsteps; ++j) {
-    const int cur = j & 1, k0 = 64 * j;
+    const int cur = j & 1, k0 = k_lo + 64 * j;
     if (j + 1 < nsteps) {
       sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
       sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
@@ -246,6 +254,19 @@ __device__ __forceinline__ void fwd_block(const MArgs& p, const int qb) {
   }
   l += other_half(l);
   if (query >= p.seq) return;
+  if (split >= 0) {
+    // This part's unnormalised O' and (m, l) (m = -inf, l = 0 where it saw no key).
+    const int64_t row = (((int64_t)split * p.batch + b) * p.seq + query) * p.heads + h;
+    float* po = p.part + row * D;
+#pragma unroll
+    for (int db = 0; db < NB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(po + 32 * db + 8 * g + 4 * lh) =
+            f32x4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+    if (lh == 0) reinterpret_cast<f32x2*>(p.part_ml)[row] = f32x2{m, l};
+    return;
+  }
   const float inv = 1.0f / l;
   uint16_t* obase = p.o + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)query * p.q_ss;
 #pragma unroll
@@ -261,7 +282,77 @@ __device__ __forceinline__ void fwd_block(const MArgs& p, const int qb) {
 
 template <int D>
 __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void mfma_attn_fwd(MArgs p) {
-  mirrored(p.causal, blockIdx.x, (p.seq + 127) / 128, [&](int qb) { fwd_block<D>(p, qb); });
+  // Split: one part of one block; else a block and, causal, its mirror (one call site, inlined once).
+  const bool split = p.nsplit > 1;
+  const int nb = (p.seq + 127) / 128;
+  const int npass = split ? 1 : passes(p.causal, blockIdx.x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
+    if (pass > 0) __syncthreads();
+    fwd_block<D>(p, split ? blockIdx.x : block_of(pass, blockIdx.x, nb), split ? blockIdx.z / p.nsplit : blockIdx.z,
+                 split ? blockIdx.z % p.nsplit : -1);
+  }
+}
+
+// The parts of a split forward combined: per (b, query, head) row, M = max
+// m_s, L = sum l_s 2^(m_s - M), O = sum O_s 2^(m_s - M) / L in part order;
+// lse = (M + log2 L) ln 2.  A thread per four features of a row.
+struct CombineArgs {
+  MArgs p;  // first: its members sit at MArgs' offsets
+  int32_t d;
+};
+
+__global__ __launch_bounds__(256) void mfma_attn_combine(CombineArgs a) {
+  const MArgs& p = a.p;
+  const int quads = a.d / 4;
+  const int64_t rows = (int64_t)p.batch * p.seq * p.heads;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * quads) return;
+  const int64_t row = t / quads;
+  const int c = 4 * (int)(t % quads);
+  const f32x2* ml = reinterpret_cast<const f32x2*>(p.part_ml);
+  float mx = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, ml[s * rows + row][0]);
+  const float shift = isfinite(mx) ? mx : 0.0f;
+  float l = 0.0f;
+  f32x4 acc = {};
+  for (int s = 0; s < p.nsplit; ++s) {
+    const f32x2 x = ml[s * rows + row];
+    const float w = __builtin_amdgcn_exp2f(x[0] - shift);
+    l += w * x[1];
+    acc += w * *reinterpret_cast<const f32x4*>(p.part + (s * rows + row) * a.d + c);
+  }
+  const int h = (int)(row % p.heads);
+  const int64_t pos = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
+  const float inv = 1.0f / l;
+  *reinterpret_cast<u32x2*>(p.o + b * p.q_sb + h * p.q_sh + pos * p.q_ss + c) =
+      u32x2{pack2(acc[0] * inv, acc[1] * inv), pack2(acc[2] * inv, acc[3] * inv)};
+  if (c == 0 && p.lse) p.lse[row] = (mx + log2f(l)) * kLn2;
+}
+
+// dQ, dK or dV from a split sweep's parts: out = scale * sum_s part_s in
+// part order, rounded to bf16; rows [b][position][head] of `d` features.
+struct SumArgs {
+  const float* part;
+  uint16_t* out;
+  int64_t sh, ss, sb;
+  int32_t positions, heads, batch, d, nsplit;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void mfma_attn_sum(SumArgs a) {
+  const int quads = a.d / 4;
+  const int64_t rows = (int64_t)a.batch * a.positions * a.heads;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * quads) return;
+  const int64_t row = t / quads;
+  const int c = 4 * (int)(t % quads);
+  f32x4 acc = {};
+  for (int s = 0; s < a.nsplit; ++s) acc += *reinterpret_cast<const f32x4*>(a.part + (s * rows + row) * a.d + c);
+  acc *= a.scale;
+  const int h = (int)(row % a.heads);
+  const int64_t pos = (row / a.heads) % a.positions, b = row / ((int64_t)a.heads * a.positions);
+  *reinterpret_cast<u32x2*>(a.out + b * a.sb + h * a.sh + pos * a.ss + c) =
+      u32x2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
 }
 
 // ---- backward: delta = rowsum(dO .* O) ---------------------------------------------
@@ -292,12 +383,15 @@ __global__ __launch_bounds__(256) void mfma_attn_delta(DeltaArgs a) {
 // with queries on the registers and keys on the lanes, so that P and dS feed
 // the products over queries straight from the accumulators.
 
+// Query tiles [qstart, qstop) for the keys of kblk: all of them (split <
+// 0), or part `split` of the sweep, which leaves its unscaled fp32 dK', dV'.
 template <int D, int DO>
-__device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const int dh) {
+__device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const int dh, const int b,
+                                           const int split) {
   constexpr int NS = D / 16, NBO = DO / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   float* stats = reinterpret_cast<float*>(lds + 4 * kTile<D>);  // [stage][lse * log2e (64) | delta (64)]
-  const int hk = blockIdx.y, b = blockIdx.z;
+  const int hk = blockIdx.y;
   const int group = p.heads / p.kv_heads;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int kw0 = kblk * 128, key = kw0 + wave * 32 + lr;
@@ -312,8 +406,10 @@ __device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const
   auto Q = [&](int s) { return lds + 2 * s * kTile<D>; };
   auto G = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
   auto Ls = [&](int s) { return stats + 128 * s; };
-  const int qstart = p.causal ? kw0 / 64 * 64 : 0;
-  const int nsteps = qstart < p.seq ? (p.seq - qstart + 63) / 64 : 0;
+  const int qfirst = p.causal ? kw0 / 64 * 64 : 0;
+  const int qstart = split < 0 ? qfirst : qfirst + split * p.span;
+  const int qstop = split < 0 ? p.seq : min(p.seq, qstart + p.span);
+  const int nsteps = qstart < qstop ? (qstop - qstart + 63) / 64 : 0;
   Stage<D> sq, sg;
   float st = 0.0f;  // threads 0..127: a query's lse * log2e or delta
   auto load = [&](const uint16_t* qbase, const uint16_t* gbase, int h, int q0) {
@@ -388,6 +484,21 @@ __device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const
     }
   }
   if (key >= p.kv_seq) return;
+  if (split >= 0) {
+    const int64_t rows = (int64_t)p.batch * p.kv_seq * p.kv_heads;
+    const int64_t row = (((int64_t)split * p.batch + b) * p.kv_seq + key) * p.kv_heads + hk;
+    float* pk = p.part + row * D;
+    float* pv = p.part + ((int64_t)p.nsplit * rows + row) * D;
+#pragma unroll
+    for (int db = 0; db < NBO; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = DO * dh + 32 * db + 8 * g + 4 * lh;
+        *reinterpret_cast<f32x4*>(pk + d) = f32x4{dk[db][4 * g], dk[db][4 * g + 1], dk[db][4 * g + 2], dk[db][4 * g + 3]};
+        *reinterpret_cast<f32x4*>(pv + d) = f32x4{dv[db][4 * g], dv[db][4 * g + 1], dv[db][4 * g + 2], dv[db][4 * g + 3]};
+      }
+    return;
+  }
   const int64_t out = koff + (int64_t)key * p.k_ss;
 #pragma unroll
   for (int db = 0; db < NBO; ++db)
@@ -405,9 +516,14 @@ __device__ __forceinline__ void dkdv_block(const MArgs& p, const int kblk, const
 template <int D, int DO>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void mfma_attn_dkdv(MArgs p) {
   constexpr int halves = D / DO;
-  const int kv = p.kv_seq;
-  mirrored(p.causal, blockIdx.x / halves, (kv + 127) / 128,
-           [&](int kblk) { dkdv_block<D, DO>(p, kblk, blockIdx.x % halves); });
+  const bool split = p.nsplit > 1;
+  const int nb = (p.kv_seq + 127) / 128, x = blockIdx.x / halves;
+  const int npass = split ? 1 : passes(p.causal, x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
+    if (pass > 0) __syncthreads();
+    dkdv_block<D, DO>(p, split ? x : block_of(pass, x, nb), blockIdx.x % halves, split ? blockIdx.z / p.nsplit : blockIdx.z,
+                      split ? blockIdx.z % p.nsplit : -1);
+  }
 }
 
 // ---- backward: dQ ----------------------------------------------------------------------
@@ -415,11 +531,13 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void mfma_attn_dkdv(MArgs p) 
 // S' = K Q', dP' = V dO' (keys on the registers, queries on the lanes),
 // dS' = P' (dP' - delta), dQ' (D x 32 queries) += K' dS'.
 
+// Keys [k_lo, k_hi) for query block qb: all of them (split < 0), or part
+// `split` of the sweep, which leaves its unscaled fp32 dQ'.
 template <int D>
-__device__ __forceinline__ void dq_block(const MArgs& p, const int qb) {
+__device__ __forceinline__ void dq_block(const MArgs& p, const int qb, const int b, const int split) {
   constexpr int NS = D / 16, NB = D / 32;
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y;
   const int hk = h / (p.heads / p.kv_heads);
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
   const int q0 = qb * 128 + wave * 32, query = q0 + lr;
@@ -439,19 +557,20 @@ __device__ __forceinline__ void dq_block(const MArgs& p, const int qb) {
   for (int i = 0; i < NB; ++i) dq[i] = f32x16{};
   const int qlast = min(qb * 128 + 127, p.seq - 1);
   const int kend = p.causal ? min(p.kv_seq, qlast + 1) : p.kv_seq;
-  const int nsteps = (kend + 63) / 64;
+  const int k_lo = split < 0 ? 0 : split * p.span, k_hi = split < 0 ? kend : min(kend, k_lo + p.span);
+  const int nsteps = k_hi > k_lo ? (k_hi - k_lo + 63) / 64 : 0;
   Stage<D> sk, sv;
   auto K = [&](int s) { return lds + 2 * s * kTile<D>; };
   auto V = [&](int s) { return lds + (2 * s + 1) * kTile<D>; };
   if (nsteps > 0) {
-    sk.load(kbase, p.k_ss, 0, p.kv_seq);
-    sv.load(vbase, p.k_ss, 0, p.kv_seq);
+    sk.load(kbase, p.k_ss, k_lo, p.kv_seq);
+    sv.load(vbase, p.k_ss, k_lo, p.kv_seq);
     sk.store(K(0));
     sv.store(V(0));
   }
   __syncthreads();
   for (int j = 0; j < nsteps; ++j) {
-    const int cur = j & 1, k0 = 64 * j;
+    const int cur = j & 1, k0 = k_lo + 64 * j;
     if (j + 1 < nsteps) {
       sk.load(kbase, p.k_ss, k0 + 64, p.kv_seq);
       sv.load(vbase, p.k_ss, k0 + 64, p.kv_seq);
@@ -496,6 +615,17 @@ __device__ __forceinline__ void dq_block(const MArgs& p, const int qb) {
     __syncthreads();
   }
   if (!live) return;
+  if (split >= 0) {
+    const int64_t row = (((int64_t)split * p.batch + b) * p.seq + query) * p.heads + h;
+    float* pq = p.part + row * D;
+#pragma unroll
+    for (int db = 0; db < NB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(pq + 32 * db + 8 * g + 4 * lh) =
+            f32x4{dq[db][4 * g], dq[db][4 * g + 1], dq[db][4 * g + 2], dq[db][4 * g + 3]};
+    return;
+  }
   uint16_t* out = p.dq + qoff;
 #pragma unroll
   for (int db = 0; db < NB; ++db)
@@ -510,7 +640,14 @@ __device__ __forceinline__ void dq_block(const MArgs& p, const int qb) {
 
 template <int D>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void mfma_attn_dq(MArgs p) {
-  mirrored(p.causal, blockIdx.x, (p.seq + 127) / 128, [&](int qb) { dq_block<D>(p, qb); });
+  const bool split = p.nsplit > 1;
+  const int nb = (p.seq + 127) / 128;
+  const int npass = split ? 1 : passes(p.causal, blockIdx.x, nb);
+  for (int pass = 0; pass < npass; ++pass) {
+    if (pass > 0) __syncthreads();
+    dq_block<D>(p, split ? blockIdx.x : block_of(pass, blockIdx.x, nb), split ? blockIdx.z / p.nsplit : blockIdx.z,
+                split ? blockIdx.z % p.nsplit : -1);
+  }
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -556,8 +693,12 @@ int fwd_launch(const th_attention_desc* d, th_launch** out) {
   const size_t lds = 4 * (size_t)kTile<D> * sizeof(uint16_t);
   TH_HIP(hipFuncSetAttribute((const void*)mfma_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   MArgs a = margs_of(d);
+  const int nqb = (d->seq + 127) / 128;
+  const th::Split sp = th::split_of((int64_t)nqb * d->heads * d->batch, a.kv_seq);
+  a.nsplit = sp.n, a.span = sp.span;
+  TH_REQUIRE((int64_t)d->batch * sp.n <= 65535, "attention: grid too large");
   th::Builder b("attention_fwd_mfma", 7);
-  const dim3 grid(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  const dim3 grid = sp.n > 1 ? dim3(nqb, d->heads, d->batch * sp.n) : dim3(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k = b.kernel((const void*)mfma_attn_fwd<D>, D == 64 ? "mfma_attn_fwd_d64" : D == 128 ? "mfma_attn_fwd_d128"
                                                                                           : "mfma_attn_fwd_d256",
                    grid, dim3(256), (uint32_t)lds, a);
@@ -566,6 +707,19 @@ int fwd_launch(const th_attention_desc* d, th_launch** out) {
   b.ref(2, k, TH_OFFSET(MArgs, v));
   b.ref(3, k, TH_OFFSET(MArgs, o));
   b.ref(4, k, TH_OFFSET(MArgs, lse));
+  if (sp.n > 1) {
+    const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+    const uint64_t at_o = b.workspace((uint64_t)sp.n * rows * D * sizeof(float));
+    const uint64_t at_ml = b.workspace((uint64_t)sp.n * rows * 2 * sizeof(float));
+    int kc = b.kernel((const void*)mfma_attn_combine, "mfma_attn_combine", dim3((unsigned)((rows * (D / 4) + 255) / 256)),
+                      dim3(256), 0, CombineArgs{a, D});
+    for (int kk : {k, kc}) {
+      b.ws_ref(kk, TH_OFFSET(MArgs, part), at_o);
+      b.ws_ref(kk, TH_OFFSET(MArgs, part_ml), at_ml);
+    }
+    b.ref(3, kc, TH_OFFSET(MArgs, o));
+    b.ref(4, kc, TH_OFFSET(MArgs, lse));
+  }
   for (int v = 0; v < 4; ++v) b.align(v, 16);
   const double BH = (double)d->batch * d->heads, BHk = (double)d->batch * d->kv_heads;
   b.work(2.0 * BH * a.seq * D * 2 + 2.0 * BHk * a.kv_seq * D * 2 + 4.0 * BH * a.seq, 4.0 * BH * D * visible_pairs(a),
@@ -585,17 +739,53 @@ int bwd_launch(const th_attention_desc* d, th_launch** out) {
   MArgs a = margs_of(d);
   th::Builder b("attention_bwd_mfma", 11);
   const int64_t rows = (int64_t)d->batch * d->seq * d->heads;
+  const int64_t rows_k = (int64_t)d->batch * a.kv_seq * d->kv_heads;
   const uint64_t at_delta = b.workspace((uint64_t)rows * sizeof(float));
+  // Small grids split the dK/dV sweep over queries and the dQ sweep over keys.
+  const int nkb = (a.kv_seq + 127) / 128, nqb = (d->seq + 127) / 128;
+  const th::Split skv = th::split_of((int64_t)nkb * (D / DO) * d->kv_heads * d->batch, d->seq);
+  const th::Split sq = th::split_of((int64_t)nqb * d->heads * d->batch, a.kv_seq);
+  TH_REQUIRE((int64_t)d->batch * std::max(skv.n, sq.n) <= 65535, "attention: grid too large");
+  MArgs akv = a, aq = a;
+  akv.nsplit = skv.n, akv.span = skv.span;
+  aq.nsplit = sq.n, aq.span = sq.span;
   int k0 = b.kernel((const void*)mfma_attn_delta, "mfma_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                     DeltaArgs{a, D});
-  const dim3 gkv(blocks_of(a.kv_seq, d->causal) * (D / DO), d->kv_heads, d->batch);
-  const dim3 gq(blocks_of(d->seq, d->causal), d->heads, d->batch);
+  const dim3 gkv = skv.n > 1 ? dim3(nkb * (D / DO), d->kv_heads, d->batch * skv.n)
+                             : dim3(blocks_of(a.kv_seq, d->causal) * (D / DO), d->kv_heads, d->batch);
+  const dim3 gq = sq.n > 1 ? dim3(nqb, d->heads, d->batch * sq.n) : dim3(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k1 = b.kernel((const void*)mfma_attn_dkdv<D, DO>, D == 64 ? "mfma_attn_dkdv_d64" : D == 128 ? "mfma_attn_dkdv_d128"
                                                                                                : "mfma_attn_dkdv_d256",
-                    gkv, dim3(256), (uint32_t)lds_dkdv, a);
+                    gkv, dim3(256), (uint32_t)lds_dkdv, akv);
+  if (skv.n > 1) {
+    const uint64_t at_kv = b.workspace((uint64_t)2 * skv.n * rows_k * D * sizeof(float));
+    b.ws_ref(k1, TH_OFFSET(MArgs, part), at_kv);
+    const unsigned g = (unsigned)((rows_k * (D / 4) + 255) / 256);
+    // The outputs' pointers start as the descriptor's (repointing rewrites them with the others).
+    SumArgs sk{nullptr, static_cast<uint16_t*>(d->dk), d->k_strides[0], d->k_strides[1], d->k_strides[2], a.kv_seq,
+               d->kv_heads, d->batch, D, skv.n, a.scale};
+    SumArgs sv = sk;
+    sv.out = static_cast<uint16_t*>(d->dv), sv.scale = 1.0f;
+    const int ks = b.kernel((const void*)mfma_attn_sum, "mfma_attn_sum_dk", dim3(g), dim3(256), 0, sk);
+    const int kv = b.kernel((const void*)mfma_attn_sum, "mfma_attn_sum_dv", dim3(g), dim3(256), 0, sv);
+    b.ws_ref(ks, TH_OFFSET(SumArgs, part), at_kv);
+    b.ws_ref(kv, TH_OFFSET(SumArgs, part), at_kv + (uint64_t)skv.n * rows_k * D * sizeof(float));
+    b.ref(7, ks, TH_OFFSET(SumArgs, out));
+    b.ref(8, kv, TH_OFFSET(SumArgs, out));
+  }
   int k2 = b.kernel((const void*)mfma_attn_dq<D>, D == 64 ? "mfma_attn_dq_d64" : D == 128 ? "mfma_attn_dq_d128"
                                                                                        : "mfma_attn_dq_d256",
-                    gq, dim3(256), (uint32_t)lds_kv, a);
+                    gq, dim3(256), (uint32_t)lds_kv, aq);
+  if (sq.n > 1) {
+    const uint64_t at_q = b.workspace((uint64_t)sq.n * rows * D * sizeof(float));
+    b.ws_ref(k2, TH_OFFSET(MArgs, part), at_q);
+    SumArgs s1{nullptr, static_cast<uint16_t*>(d->dq), d->q_strides[0], d->q_strides[1], d->q_strides[2], d->seq,
+               d->heads, d->batch, D, sq.n, a.scale};
+    const int kq = b.kernel((const void*)mfma_attn_sum, "mfma_attn_sum_dq", dim3((unsigned)((rows * (D / 4) + 255) / 256)),
+                            dim3(256), 0, s1);
+    b.ws_ref(kq, TH_OFFSET(SumArgs, part), at_q);
+    b.ref(6, kq, TH_OFFSET(SumArgs, out));
+  }
   const size_t offs[9] = {TH_OFFSET(MArgs, q),  TH_OFFSET(MArgs, k),  TH_OFFSET(MArgs, v),
                           TH_OFFSET(MArgs, o),  TH_OFFSET(MArgs, lse), TH_OFFSET(MArgs, dout),
                           TH_OFFSET(MArgs, dq), TH_OFFSET(MArgs, dk),  TH_OFFSET(MArgs, dv)};

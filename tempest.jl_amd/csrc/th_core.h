@@ -191,6 +191,24 @@ void point_workspace(th_launch* l);
 int rows_scratch_setup(int device);
 int device_alloc(size_t bytes, void** out);
 
+// The parts an attention sweep of `length` positions takes when `groups`
+// workgroups (unsplit, unpaired) would leave the device idle: enough for
+// about 512 workgroups where they are fewer than 256 (one a CU), at most 8,
+// each at least 128 positions (span, a multiple of 64).  Each wave's sweep
+// bounds a small grid; parts share it among more waves, at the cost of
+// fp32 partial results and a launch that adds them.
+struct Split {
+  int n, span;
+};
+inline Split split_of(int64_t groups, int length) {
+  if (groups >= 256 || length <= 128) return {1, 0};
+  int n = (int)std::min<int64_t>(8, (512 + groups - 1) / groups);
+  n = std::min(n, (length + 127) / 128);
+  if (n <= 1) return {1, 0};
+  const int span = ((length + n - 1) / n + 63) / 64 * 64;
+  return {(length + span - 1) / span, span};
+}
+
 // Attention for what the matrix-core kernels do not take (attention_generic.hip).
 int build_attention_general_fwd(const th_attention_desc* d, th_launch** out);
 int build_attention_general_bwd(const th_attention_desc* d, th_launch** out);

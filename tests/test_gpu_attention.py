@@ -125,8 +125,9 @@ def test_backward_both_dq_paths(target, S, causal, recompute):
 
 def test_head_dims_route_to_the_kernels_that_take_them(target):
     """d 128 at a multiple of 128 takes the tuned matrix-core kernel; d 64,
-    d 256 and d 128 at a length of 100 the other matrix-core kernels; d 100
-    and fp32 the general kernels; d beyond 256 is refused."""
+    d 256 and d 128 at a length of 100 the other matrix-core kernels; fp32 at
+    d 64 and 128 the fp32 matrix-core kernels; d 100 (bf16 or fp32) the
+    general kernels; d beyond 256 is refused."""
     import tempest_hip.launch as L
     from tempest_hip import HIPError
     t = torch.zeros(1, 128, 1, 300, dtype=torch.bfloat16, device="cuda")
@@ -137,7 +138,9 @@ def test_head_dims_route_to_the_kernels_that_take_them(target):
     assert "mfma_attn_fwd_d256" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=256).describe()
     assert "mfma_attn_fwd_d128" in L.attention_fwd(1, 1, 1, 100, p, p, p, p).describe()
     assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=100).describe()
-    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, f32=True).describe()
+    assert "f32_attn_fwd_d128" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, f32=True).describe()
+    assert "f32_attn_fwd_d64" in L.attention_fwd(1, 1, 1, 100, p, p, p, p, f32=True, head_dim=64).describe()
+    assert "attn_gen_fwd" in L.attention_fwd(1, 1, 1, 128, p, p, p, p, f32=True, head_dim=100).describe()
     with pytest.raises(HIPError, match="head_dim must be 1..256"):
         L.attention_fwd(1, 1, 1, 128, p, p, p, p, head_dim=300)
 

@@ -43,3 +43,21 @@ def test_fp32_attention_replays_bitwise(target):
     torch.cuda.synchronize()
     for a, b in zip(first, (o, lse, dq, dk, dv)):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D,B,H,KV,S,causal,split", [
+    (64, 1, 2, 2, 700, True, True), (128, 1, 2, 1, 300, False, True), (64, 4, 16, 16, 512, True, False)])
+def test_fp32_split_and_whole_sweeps(target, D, B, H, KV, S, causal, split):
+    """A grid under one workgroup a CU splits each sweep into parts (partial
+    results combined or summed in part order); a grid that fills the device
+    sweeps whole.  Both against the float64 oracle."""
+    announce("attn fp32 mfma split", D, B, H, KV, S, causal, split)
+    gen = torch.Generator(device="cuda").manual_seed(17 * D + S + H)
+    q = torch.randn(B, S, H, D, device="cuda", generator=gen) * 0.5
+    k = torch.randn(B, S, KV, D, device="cuda", generator=gen) * 0.5
+    v = torch.randn(B, S, KV, D, device="cuda", generator=gen)
+    g = torch.randn(B, S, H, D, device="cuda", generator=gen)
+    outs, (fwd, bwd) = _run(q, k, v, g, causal, True)
+    assert ("f32_attn_combine" in fwd.describe()) == split, fwd.describe()
+    assert ("f32_attn_sum_dk" in bwd.describe() and "f32_attn_sum_dq" in bwd.describe()) == split, bwd.describe()
+    _check(outs, q, k, v, g, causal, TOL_F32)

@@ -87,3 +87,22 @@ def test_matrix_core_attention_at_size_sampled_heads(target, D):
     assert np.max(np.abs(_np(lse[sl]) - rl)) < 1e-3 * max(1.0, np.abs(rl).max())
     for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         assert relative(_np(got[sl]), ref) < TOL_BF16, (name, relative(_np(got[sl]), ref))
+
+
+@pytest.mark.parametrize("D,B,H,KV,S,causal,split", [
+    (64, 1, 2, 2, 700, True, True), (256, 1, 2, 1, 300, False, True), (64, 4, 16, 16, 512, True, False)])
+def test_split_and_whole_sweeps(target, D, B, H, KV, S, causal, split):
+    """A grid under one workgroup a CU splits each sweep into parts (fp32
+    partial results combined or summed in part order by launches of their
+    own); a grid that fills the device sweeps whole.  Both against the
+    float64 oracle."""
+    import tempest_hip.launch as L
+    announce("attn mfma split", D, B, H, KV, S, causal, split)
+    q, k, v, g = _inputs(B, S, S, H, KV, D, 31 * D + S + H)
+    outs = _run(q, k, v, g, causal)
+    p = q.data_ptr()
+    fwd = L.attention_fwd(B, H, KV, S, p, p, p, p, p, causal=causal, head_dim=D).describe()
+    bwd = L.attention_bwd(B, H, S, p, p, p, p, p, p, p, p, p, causal=causal, kv_heads=KV, head_dim=D).describe()
+    assert ("mfma_attn_combine" in fwd) == split, fwd
+    assert ("mfma_attn_sum_dk" in bwd and "mfma_attn_sum_dq" in bwd) == split, bwd
+    _check(outs, q, k, v, g, causal)
