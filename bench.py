@@ -947,6 +947,10 @@ def main() -> int:
         except Exception as err:
             configs["attention_head_dims"] = {"error": repr(err)}
         try:
+            configs["reference_benchmarks"] = reference_benchmarks(target)
+        except Exception as err:
+            configs["reference_benchmarks"] = {"error": repr(err)}
+        try:
             configs["config5_deltanet"] = config5(target)
         except Exception as err:
             configs["config5_deltanet"] = {"error": repr(err)}
