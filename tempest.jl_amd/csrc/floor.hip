@@ -576,9 +576,11 @@ int plan(const th_floor_desc* d, Plan& pl) {
       pl.qn = pl.count / pl.W;
       pl.L = (int)std::min<int64_t>(256, std::max<int64_t>(64, nextpow2(pl.qn)));
       // Split an item's positions among workgroups only when few items leave
-      // the device idle and each lane would otherwise sweep 256+ steps: a
-      // shorter fold costs less than the extra launch and merge.
-      if (pl.items < 8 * kCUs && pl.qn >= (int64_t)pl.L * 256) {
+      // the device idle and each lane would otherwise sweep 64+ steps: a
+      // shorter fold costs less than the extra launch and merge (one
+      // workgroup's 128 dependent steps over 128 K floats take ~32 us, the
+      // same fold in 16 parts and a merge a few).
+      if (pl.items < 8 * kCUs && pl.qn >= (int64_t)pl.L * 64) {
         int64_t want = (8 * kCUs + pl.items - 1) / std::max<int64_t>(pl.items, 1);
         want = std::min<int64_t>(want, pl.qn / ((int64_t)pl.L * 8));
         pl.P = (int)std::max<int64_t>(1, std::min<int64_t>(want, 1024));
