@@ -63,6 +63,27 @@ def graph_vs_direct(target, ex, reps: int, warmup: int = 2) -> dict:
             "chosen": "graph" if ex.graphed else "direct"}
 
 
+def rows_grad_exact(name: str, x, g):
+    """Float64 gradient of sum(f(x) .* g) over each row of x (the reference's
+    columns): f = softmax, dx = y .* (g .- sum(y .* g)); f = LayerNorm (weight
+    1, bias 0, eps 1e-5), dx = (g .- mean(g) .- y .* mean(g .* y)) ./ sigma.
+    The bench's own parity check on sampled rows (torch, not the oracle)."""
+    import torch
+    x, g = x.double(), g.double()
+    if name == "softmax":
+        y = torch.softmax(x, dim=1)
+        return y * (g - (y * g).sum(dim=1, keepdim=True))
+    mu = x.mean(dim=1, keepdim=True)
+    sigma = torch.sqrt(((x - mu) ** 2).mean(dim=1, keepdim=True) + 1e-5)
+    y = (x - mu) / sigma
+    return (g - g.mean(dim=1, keepdim=True) - y * (g * y).mean(dim=1, keepdim=True)) / sigma
+
+
+def _relative(a, b) -> float:
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm())
+
+
 def config2(target, steps: int, warmup: int):
     import torch
     import tempest_hip as th
@@ -98,13 +119,11 @@ def config2(target, steps: int, warmup: int):
     # A quick parity check on sampled rows (outside the timed region).
     parity = {}
     try:
-        from oracle import interpret
-        from oracle.data import relative
         idx = torch.tensor([0, 777, 16384, ROWS - 1], device="cuda")
-        xs, gs = x.index_select(0, idx).cpu().numpy(), g.index_select(0, idx).cpu().numpy()
-        for name, ex, f in (("softmax", es, interpret.softmax_grad), ("layernorm", el, interpret.layernorm_grad)):
+        xs, gs = x.index_select(0, idx), g.index_select(0, idx)
+        for name, ex in (("softmax", es), ("layernorm", el)):
             _, dx = ex.outputs()
-            parity[name] = relative(dx.index_select(0, idx).cpu().numpy(), f(xs, gs)[1])
+            parity[name] = _relative(dx.index_select(0, idx), rows_grad_exact(name, xs, gs))
     except Exception as err:  # the bench's number stands without it
         parity["error"] = repr(err)
     dispatch = {"softmax": graph_vs_direct(target, es, steps), "layernorm": graph_vs_direct(target, el, steps)}
@@ -137,12 +156,9 @@ def config2_floor(target, x, g, steps: int = 10, warmup: int = 3):
         entry = {"us": s * 1e6, "GB/s": alg / s / 1e9, "frac_of_hbm_peak": alg / s / HBM_PEAK,
                  "plan": ex.explain().splitlines()[1].strip()[:400]}
         try:
-            from oracle import interpret
-            from oracle.data import relative
             idx = torch.tensor([0, 777, 16384, ROWS - 1], device="cuda")
-            xs, gs = x.index_select(0, idx).cpu().numpy(), g.index_select(0, idx).cpu().numpy()
-            f = interpret.softmax_grad if name == "softmax" else interpret.layernorm_grad
-            entry["parity_rel"] = relative(ex.outputs()[1].index_select(0, idx).cpu().numpy(), f(xs, gs)[1])
+            entry["parity_rel"] = _relative(ex.outputs()[1].index_select(0, idx),
+                                            rows_grad_exact(name, x.index_select(0, idx), g.index_select(0, idx)))
         except Exception as err:
             entry["parity_rel"] = repr(err)
         out[name] = entry
@@ -630,6 +646,11 @@ REFERENCE_US = {
     "softmax_through_logsumexp_512x1024": {"fwd": 5.56},
     "layer_norm_two_passes_512x1024": {"fwd": 10.07},
     "rmsnorm_divided_by_the_root_512x1024": {"fwd": 9.89},
+    "rmsnorm_times_the_inverse_root_512x1024": {"fwd": 9.78},
+    "layer_norm_from_the_mean_of_squares_512x1024": {"fwd": 9.99},
+    "softmax_shifted_by_the_maximum_512x1024": {"fwd": 5.69},
+    "softmax_exp_computed_once_512x1024": {"fwd": 4.94},
+    "rmsnorm_training_step_512x1024": {"step": 13.88},
     "linear_bias_gelu_256x384x512_f32": {"fwd": 13.44},
 }
 
@@ -762,6 +783,25 @@ def reference_benchmarks(target) -> dict:
     g.output("y", xx / g.apply("sqrt", g.fold("sum", g.apply("abs2", xx)).value / float(N) + 1e-5) * ww, (1, N))
     progs["rmsnorm_divided_by_the_root_512x1024"] = (
         g, X / torch.sqrt((X ** 2).sum(dim=0, keepdim=True) / N + 1e-5) * Wt[:, None])
+    g, xx, ww = col_group("RMSNorm, times the inverse root")
+    g.output("y", ww * xx * g.apply("inv", g.apply("sqrt", g.fold("sum", xx * xx).value * (1.0 / N) + 1e-5)), (1, N))
+    progs["rmsnorm_times_the_inverse_root_512x1024"] = (
+        g, X / torch.sqrt((X ** 2).sum(dim=0, keepdim=True) / N + 1e-5) * Wt[:, None])
+    g, xx, ww = col_group("layer norm, from the mean of squares")
+    m = g.fold("sum", xx).value / float(N)
+    var = g.fold("sum", xx * xx).value / float(N) - m * m  # x .^ 2: Julia's literal power is x * x
+    g.output("y", ww * (xx - m) / g.apply("sqrt", var + 1e-5), (1, N))
+    progs["layer_norm_from_the_mean_of_squares_512x1024"] = (
+        g, (X - mu) / torch.sqrt(((X - mu) ** 2).mean(dim=0, keepdim=True) + 1e-5) * Wt[:, None])
+    g, xx, ww = col_group("softmax shifted by the maximum")
+    mx = g.fold("max", xx).value
+    e = g.apply("exp", xx - mx)
+    g.output("y", e / g.fold("sum", e, phase=2).value, (1, N))
+    progs["softmax_shifted_by_the_maximum_512x1024"] = (g, torch.softmax(X, dim=0))
+    g, xx, ww = col_group("softmax, exp computed once")
+    e = g.apply("exp", xx)
+    g.output("y", e / g.fold("sum", e).value, (1, N))
+    progs["softmax_exp_computed_once_512x1024"] = (g, torch.softmax(X, dim=0))
     for name, (g, exact) in progs.items():
         l = g.build({"x": x.data_ptr(), "w": w.data_ptr(), "y": y.data_ptr()})
         t = _graph_step_us([l])
@@ -771,6 +811,49 @@ def reference_benchmarks(target) -> dict:
                      "rel_err": rel(y.view(M, N).T, exact)}
         l.destroy()
         log(name, json.dumps({kk_: out[name][kk_] for kk_ in ("us_fwd", "speedup_fwd", "rel_err")}))
+    # ---- RMSNorm, a training step: loss = sum(abs2, rmsnorm(x, w)) and (dx, dw).  Per column c,
+    # r = (sum(x^2)/N + eps)^(-1/2), y = x r w, L_c = sum(y^2), dx = 2 r w y - 2 r^2 L_c x / N;
+    # dw = sum over columns of 2 x^2 r^2 w; loss = sum L_c.  Three groups: the columns, the rows, the loss.
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    rcol, lcol, loss1 = torch.empty(M, device="cuda"), torch.empty(M, device="cuda"), torch.empty(1, device="cuda")
+    g1 = FloorGroup("reduction", (N, M), reduced=(0,), name="RMSNorm's columns: y, L_c, dx")
+    for v_, n_ in (("x", N * M), ("w", N), ("dx", N * M), ("r", M), ("L", M)):
+        g1.value(v_, "f32", n_)
+    xx, ww = g1.load("x", (1, N)), g1.load("w", (1, 0))
+    r = g1.apply("inv", g1.apply("sqrt", g1.fold("sum", g1.apply("abs2", xx)).value / float(N) + 1e-5))
+    yv = xx * r * ww
+    lc = g1.fold("sum", g1.apply("abs2", yv), phase=2).value
+    g1.output("dx", 2.0 * r * ww * yv - 2.0 * r * r * lc * xx / float(N), (1, N))
+    g1.output("r", r, (0, 1), full=False)
+    g1.output("L", lc, (0, 1), full=False)
+    g2 = FloorGroup("reduction", (N, M), reduced=(1,), name="RMSNorm's rows: dw")
+    for v_, n_ in (("x", N * M), ("w", N), ("r", M), ("dw", N)):
+        g2.value(v_, "f32", n_)
+    xx, rr, ww = g2.load("x", (1, N)), g2.load("r", (0, 1)), g2.load("w", (1, 0))
+    g2.output("dw", g2.fold("sum", 2.0 * xx * xx * rr * rr * ww).value, (1, 0), full=False)
+    g3 = FloorGroup("reduction", (M,), reduced=(0,), name="RMSNorm's loss")
+    g3.value("L", "f32", M)
+    g3.value("loss", "f32", 1)
+    g3.output("loss", g3.fold("sum", g3.load("L", (1,))).value, full=False)
+    ptr = {"x": x.data_ptr(), "w": w.data_ptr(), "dx": dx.data_ptr(), "dw": dw.data_ptr(), "r": rcol.data_ptr(),
+           "L": lcol.data_ptr(), "loss": loss1.data_ptr()}
+    ls = [gg.build({k_: ptr[k_] for k_ in gg.values}) for gg in (g1, g2, g3)]
+    t = _graph_step_us(ls)
+    for l in ls:
+        l()
+    torch.cuda.synchronize()
+    Xg, Wg = X.clone().requires_grad_(True), Wt.clone().requires_grad_(True)
+    yr = Xg / torch.sqrt((Xg ** 2).sum(dim=0, keepdim=True) / N + 1e-5) * Wg[:, None]
+    lr_ = (yr ** 2).sum()
+    lr_.backward()
+    name = "rmsnorm_training_step_512x1024"
+    out[name] = {"us_step": t, "us_fwd": t, "reference_us_gb10": REFERENCE_US[name],
+                 "speedup_step": REFERENCE_US[name]["step"] / t,
+                 "rel_err": {"loss": rel(loss1, lr_.reshape(1)), "dx": rel(dx.view(M, N).T, Xg.grad),
+                             "dw": rel(dw, Wg.grad)}}
+    for l in ls:
+        l.destroy()
+    log(name, json.dumps({kk_: out[name][kk_] for kk_ in ("us_step", "speedup_step", "rel_err")}))
     # ---- linear, bias, GELU: gelu.(W * Z .+ b), W 256 x 384, Z 384 x 512, b 256, fp32
     m_, k_, n_ = 256, 384, 512
     Wm, Zm, bv = sample(m_ * k_, 0.01, torch.float32), sample(k_ * n_, 0.2, torch.float32), sample(m_, 0.3, torch.float32)

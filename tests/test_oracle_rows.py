@@ -104,3 +104,20 @@ def test_floor_float32_is_close_to_float64(which, rows, n):
     assert relative(d32, d64) < 2e-5
     assert relative(y32, y64) < 2e-5
     assert abs(l32 - l64) < 1e-4 * max(1.0, np.abs(d64).sum() / rows)
+
+
+def test_bench_parity_reference_matches_the_oracle():
+    """bench.py checks config 2's sampled rows against its own float64 torch
+    gradient (it leaves the oracle to its CPU baseline): that gradient is
+    the oracle's, to rounding."""
+    import numpy as np
+    import torch
+
+    import bench
+    from oracle import interpret
+    from oracle.data import relative
+    rng = np.random.default_rng(11)
+    x, g = rng.standard_normal((4, 300)) * 2, rng.standard_normal((4, 300))
+    for name, f in (("softmax", interpret.softmax_grad), ("layernorm", interpret.layernorm_grad)):
+        got = bench.rows_grad_exact(name, torch.from_numpy(x), torch.from_numpy(g)).numpy()
+        assert relative(got, f(x, g)[1]) < 1e-12, name
