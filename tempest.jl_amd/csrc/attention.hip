@@ -62,8 +62,10 @@ struct AttnArgs {
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
-  // backward workspace: dS' as bf16 in contiguous 16 KB tiles, [b][h][query
-  // block of 128][key block of 64][key][query] (64 x 128 per tile), or null.
+  // backward workspace: dS' as bf16 in the dQ product's operand order,
+  // [b][h][query block of 64][key slice of 16][query half][lane][8] (two 1 KB
+  // fragments per block and slice; lane l holds query 32 half + l % 32 and keys
+  // 8 (e / 4) + 4 (l / 32) + e % 4 of the slice in element e), or null.
   uint16_t* ds;
   // backward workspace: per (b, h) and 64-query block qb, 128 floats: the 64
   // queries' -lse / scale, then their -delta ([b][h][qb][2][64]).
@@ -533,9 +535,17 @@ constexpr int kBwdK = 128;  // keys per workgroup
 constexpr int kBwdQ = 64;   // queries per step
 constexpr size_t kStageBwd = 2 * kTileElems * sizeof(uint16_t) + 2 * 64 * sizeof(float);
 constexpr int kBwdStages = 3;  // query blocks in LDS: one read, two loading
-constexpr int kDsRow = 72;     // LDS row (bf16) of a wave's dS' transpose scratch: 64 queries + 8
-constexpr size_t kDsScratch = kBwdStages * kStageBwd;  // 4 waves x 32 rows of kDsRow
-constexpr size_t kDkdvLds = kDsScratch + 4 * 32 * kDsRow * sizeof(uint16_t);
+constexpr size_t kDsScratch = kBwdStages * kStageBwd;  // then 4 waves x 32 rows of 64 bf16
+constexpr size_t kDkdvLds = kDsScratch + 4 * 32 * 64 * sizeof(uint16_t);
+
+// A wave's dS' transpose scratch: 32 key rows of 64 queries (128 bytes), the
+// sixteen 8-byte chunks of row r stored at c ^ sw(r), sw(r) = 8 ((r / 2) % 2)
+// + r / 4.  The rows' writes (32 lanes, one chunk of 32 rows) fill the 64
+// banks once: rows of one parity share a half of the banks and sw is a
+// bijection on them.  The transposed reads (32 lanes, rows 4 n .. 4 n + 3
+// by eight aligned chunks) do too: rows 4 n and 4 n + 2 (and 4 n + 1, 4 n + 3)
+// land in opposite aligned eights.
+__device__ __forceinline__ int ds_at(int r, int c8) { return r * 64 + 4 * (c8 ^ (8 * ((r / 2) % 2) + r / 4)); }
 
 // The gradient products of slices ks0, ks0 + 1 (rows 16 ks0 .. 16 ks0 + 31):
 // dv += dO' P, dk += Q' dS, fragments read half a slice ahead.  kAgpr: dv and
@@ -662,25 +672,34 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
       // key rows) so that it leaves as whole 128-byte lines.  It is written
       // there at the end of its step and stored during the next one (or after
       // the sweep), beside that step's products.
-      uint16_t* const scratch = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * kDsRow;
+      uint16_t* const scratch = lds + kDsScratch / sizeof(uint16_t) + wave * 32 * 64;
+      // The four product fragments of the scratch's 32 keys x 64 queries, read
+      // transposed (two ds_read_b64_tr_b16 each, as frag_tr): fragment 2 kk + f
+      // is keys 16 kk .. + 15 by queries 32 f .. + 31, lane l holding query
+      // 32 f + l % 32 and keys 16 kk + 8 (e / 4) + 4 (l / 32) + e % 4 in element e.
       u32x4 pend[4];
       auto scratch_read = [&]() {
+        const int g = lane / 16, i = lane % 16;
   #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = lane / 8 + 8 * i, cc = lane % 8;
-          pend[i] = *reinterpret_cast<const u32x4*>(scratch + r * kDsRow + 8 * cc);
-        }
+        for (int kk = 0; kk < 2; ++kk)
+  #pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const int row = 16 * kk + 4 * (g / 2) + i / 4, c8 = 8 * f + 4 * (g % 2) + i % 4;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(scratch + ds_at(row, c8)));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(scratch + ds_at(row + 8, c8)));
+            const u32x2 a = __builtin_bit_cast(u32x2, lo), c = __builtin_bit_cast(u32x2, hi);
+            pend[2 * kk + f] = u32x4{a[0], a[1], c[0], c[1]};
+          }
       };
-      // This wave's 32 keys are rows 32 (wave % 2) .. + 31 of key block k0 / 64;
-      // queries qq0 .. qq0 + 63 are one half of the rows of query block qq0 / 128.
+      // dS' leaves in the dQ sweep's operand order: for each (batch, head), 64-query
+      // block and 16-key slice, two 1 KB fragments (queries 0..31, 32..63 of the
+      // block), lane l's 16 bytes at 16 l.  This wave's 32 keys and 64 queries
+      // are the four fragments of slices k0 / 16, k0 / 16 + 1: 4 KB in one piece.
       auto store_pending = [&](int qq0) {
-        uint16_t* rows0 = p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq +
-                          ((int64_t)(qq0 / 128) * (p.seq / 64) + k0 / 64) * (64 * 128) + (k0 % 64) * 128 + qq0 % 128;
+        uint16_t* frag0 = p.ds + (((int64_t)b * p.heads + h) * (p.seq / 64) + qq0 / 64) * ((int64_t)p.seq * 64) +
+                          (int64_t)(k0 / 16) * 1024 + 8 * lane;
   #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = lane / 8 + 8 * i, cc = lane % 8;
-          __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(rows0 + r * 128 + 8 * cc));
-        }
+        for (int i = 0; i < 4; ++i) __builtin_nontemporal_store(pend[i], reinterpret_cast<u32x4*>(frag0 + 512 * i));
       };
       // Blocks past the end are a harmless reload of the last one into an idle stage.
       fetch(qstart, 0);
@@ -733,8 +752,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(AttnArgs p) {
   #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
             const u32x4 x = __builtin_bit_cast(u32x4, sf[ks]);
-            *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 4 * lh) = u32x2{x[0], x[1]};
-            *reinterpret_cast<u32x2*>(scratch + lr * kDsRow + 16 * ks + 8 + 4 * lh) = u32x2{x[2], x[3]};
+            *reinterpret_cast<u32x2*>(scratch + ds_at(lr, 4 * ks + lh)) = u32x2{x[0], x[1]};
+            *reinterpret_cast<u32x2*>(scratch + ds_at(lr, 4 * ks + 2 + lh)) = u32x2{x[2], x[3]};
           }
         }
         // Wait for block qb + 1's stage.  After its nine loads this wave has
@@ -897,56 +916,65 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
   }
 }
 
-// ---- backward: dQ from the stored dS' -------------------------------------------------
-// dQ' (128 d x 128 queries per workgroup) += K' dS' over key blocks of 32,
-// both operands read transposed from row-major LDS tiles: K [key][d] and
-// dS' [key][query] (the dK/dV kernel wrote every entry this sweep reads;
-// masked ones are 0).  One product per step instead of three, no exp.  The
-// sweep streams dS' (read once, non-temporal) and is bound by how many bytes
-// are in flight: blocks of 32 keys (8 KB of K and 8 KB of dS' each) in a ring
-// of four stages are issued three blocks ahead, each step waiting only for
-// the next block, in the 64 KB of LDS that leaves two workgroups a CU.  (A
-// ring of 64-key blocks one ahead kept one block in flight and read dS' at
-// ~3.7 TB/s; read in this order with plain loads it streams at 7.1 TB/s.)
-
-constexpr int kDqRows = 32;    // keys per step
-constexpr int kDqStages = 4;   // stages in the ring
-constexpr int kDqAhead = 3;    // blocks in flight beyond the one being read
-constexpr int kDqTileElems = kDqRows * kD;
-constexpr size_t kDqDsLds = 2 * kDqStages * kDqTileElems * sizeof(uint16_t);  // (K, dS') per stage
-
-// Direct global -> LDS loads of a 32-row tile: each wave 8 rows, two 1 KB
-// instructions; rows XOR-permuted as tile_at lays them out.
-struct HalfTileDma {
-  __amdgpu_buffer_rsrc_t rsrc;
-  int32_t off[2];
-  int32_t row_bytes;
-  __device__ HalfTileDma(const uint16_t* base, int64_t rs) {
-    rsrc = th_dev::buffer_of(base);
-    row_bytes = (int32_t)(rs * 2);
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+// ---- stores of 32 rows of 128 through LDS ----------------------------------------
+// Four 32 x 32 accumulators acc[db] holding X'(d, row) (lane l: row l % 32,
+// d = 32 db + 8 g + 4 (l / 32) + i for register 4 g + i), scaled and rounded
+// to bf16, leave as whole 256-byte rows of X (row r at out + r * rs): written
+// to a wave's 8 KB of LDS (stage_rows), row r's 16-byte chunk c at position
+// c ^ (r % 16) (rows of one write are 16 distinct chunks, two rows apart by
+// 16 share one; a row's read back is all 64 banks), then read back 16 lanes a
+// row and stored 4 rows an instruction (flush_rows).  Scattered 8-byte stores
+// of the same rows (two lanes a row, 32 rows an instruction) measured 15 us
+// more for config 4's dQ.
+__device__ __forceinline__ void stage_rows(uint16_t* stage, const f32x16 (&acc)[4], float sc) {
+  const int lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = 8 * w + 4 * i + l / 16;
-      const int c = (l % 16) ^ (4 * (r % 4) + (r / 4) % 4);
-      off[i] = (int32_t)(((int64_t)r * rs + 8 * c) * 2);
-    }
-  }
-  template <bool kStream>
-  __device__ __forceinline__ void load(int row0, const uint16_t* lds) const {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const uint32_t dst = (uint32_t)(uintptr_t)lds + 1024 * 2 * w;
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if constexpr (kStream) th_dev::dma16_nt(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
-      else th_dev::dma16(rsrc, off[i], row0 * row_bytes, dst + 1024 * i);
+    for (int g = 0; g < 4; ++g) {
+      const int c = 4 * db + g;
+      *reinterpret_cast<u32x2*>(stage + lr * kD + 8 * (c ^ (lr % 16)) + 4 * lh) =
+          u32x2{pack2(acc[db][4 * g] * sc, acc[db][4 * g + 1] * sc), pack2(acc[db][4 * g + 2] * sc, acc[db][4 * g + 3] * sc)};
     }
-  }
-};
+}
 
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
+__device__ __forceinline__ void flush_rows(const uint16_t* stage, uint16_t* out, int64_t rs) {
+  const int lane = threadIdx.x % 64;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + lane / 16, c = lane % 16;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * kD + 8 * (c ^ (r % 16)));
+    *reinterpret_cast<u32x4*>(out + r * rs + 8 * c) = v;
+  }
+}
+
+// ---- backward: dQ from dS' in operand order ---------------------------------------
+// dQ' (128 d x 64 queries per wave, 256 queries per workgroup) += K' dS' over
+// key steps of 64.  dS' comes straight from memory into registers: the dK/dV
+// sweep stored it in this product's B-operand order (per 64-query block and
+// 16-key slice, two 1 KB fragments, lane l's 16 bytes at 16 l), so each wave
+// streams its own queries' dS' as whole contiguous kilobytes, read once
+// (non-temporal), one step ahead.  Only K goes through LDS, where the four
+// waves share it: a step's 64 K rows are loaded into registers two steps
+// ahead and written to one of two LDS stages at the end of the step before
+// their own, K' read transposed from there (frag_tr).  Per step a wave
+// issues 32 products against 16 KB of LDS reads (64 B a clock a CU at the
+// matrix cores' rate; the earlier sweep that staged dS' through LDS as well
+// needed three times that).  Every load is an ordinary one that the compiler
+// sees and waits for exactly; sweeps have an even number of steps (seq is a
+// multiple of 128), so the loop runs two steps an iteration, the register
+// sets trading roles, with no early exit.  Causal: waves multiply nothing
+// past their own diagonal (fragments there were never written; their loads
+// re-read the wave's last block) and workgroup x takes query blocks x and its
+// mirror; waves whose queries lie past the sequence load K and compute nothing.
+
+constexpr int kDqfQ = 256;  // queries per workgroup (64 per wave)
+constexpr int kDqfK = 64;   // keys per step
+constexpr size_t kDqfLds = 6 * kTileElems * sizeof(uint16_t);  // two 64-key stages of K, then 4 waves x 16 KB of kept dQ rows
+
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_frag(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int nqb = p.seq / kFwdQ;
+  const int nqb = (p.seq + kDqfQ - 1) / kDqfQ;
   const Block blk = xcd_block();
   const int npass = (p.causal && 2 * blk.x + 1 != nqb) ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
@@ -955,73 +983,104 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds(AttnArgs p) {
     const int hk = h / (p.heads / p.kv_heads);
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int lr = lane % 32, lh = lane / 32;
-    const int qw = qb * kFwdQ;  // the workgroup's first query
-    const HalfTileDma kt(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh, p.k_ss);
-    // The query block's dS' tiles (64 keys x 128 queries, 16 KB each, one per
-    // 64 keys, contiguous): key row r of the sweep is row r of their concatenation.
-    const HalfTileDma dt(p.ds + ((int64_t)b * p.heads + h) * p.seq * p.seq + (int64_t)qb * (p.seq / 64) * (64 * 128), 128);
-    const int nkb = p.causal ? ((qb + 1) * kFwdQ) / kDqRows : p.seq / kDqRows;  // >= 4
-    auto Ks = [&](int s) { return lds + 2 * s * kDqTileElems; };
-    auto Ds = [&](int s) { return lds + (2 * s + 1) * kDqTileElems; };
-    // Block kb into stage kb % kDqStages (blocks past the end: a harmless
-    // reload of the last one into a stage no step reads again).  Four loads a wave.
-    auto fetch = [&](int kb) {
-      const int s = kb % kDqStages, at = min(kb, nkb - 1) * kDqRows;
-      kt.load<false>(at, Ks(s));
-      dt.load<true>(at, Ds(s));
+    const int nq64 = p.seq / 64;
+    const int q64 = qb * 4 + wave;  // this wave's 64-query block
+    const bool live = q64 < nq64;
+    // Steps the workgroup sweeps (even) and steps this wave multiplies.
+    const int nsteps = p.causal ? min(p.seq, (qb + 1) * kDqfQ) / kDqfK : p.seq / kDqfK;
+    const int wsteps = !live ? 0 : p.causal ? q64 + 1 : nsteps;
+    const int last = max(wsteps, 1) - 1;  // dS' loads past a wave's last step re-read it
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const int64_t kstep = (int64_t)kDqfK * p.k_ss;
+    const TileRows rows(p.k_ss);
+    const uint16_t* dsw = p.ds + (((int64_t)b * p.heads + h) * nq64 + min(q64, nq64 - 1)) * ((int64_t)p.seq * 64) +
+                          8 * lane;
+    auto load_ds = [&](int kb, u32x4 (&r)[8]) {
+      const uint16_t* at = dsw + (int64_t)min(kb, last) * (4 * 1024);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(at + 512 * i));
     };
-    // Wave (wi, wj) owns d 64 wi .. + 63 and queries 64 wj .. + 63 of the
-    // workgroup's 128 x 128 dQ': 2 + 2 fragments a 16-key slice instead of 4 + 1
-    // for all d of 32 queries, the transposed LDS reads being what the
-    // sweep's LDS traffic is made of.
-    const int wi = wave % 2, wj = wave / 2;
-    f32x16 dq[2][2];
+    auto load_k = [&](int kb, u32x4 (&r)[4]) { rows.load(kbase + (int64_t)min(kb, nsteps - 1) * kstep, r); };
+    auto Ks = [&](int s) { return lds + s * kTileElems; };
+    f32x16 dq0[4], dq1[4];
 #pragma unroll
-    for (int e = 0; e < 2; ++e)
+    for (int i = 0; i < 4; ++i) dq0[i] = f32x16{}, dq1[i] = f32x16{};
+    u32x4 dsa[8], dsb[8], ka[4], kb4[4];
+
+    // Step kb: dS' of step kb + 1 and K rows of step kb + 2 are loaded, the
+    // products of step kb run (its dS' in `cur`, its K in stage kb % 2), and
+    // step kb + 1's K rows (loaded a step ago, in `kn`) go to stage (kb + 1) % 2.
+    auto step = [&](int kb, u32x4 (&cur)[8], u32x4 (&nxt)[8], u32x4 (&kn)[4], u32x4 (&kl)[4]) {
+      load_ds(kb + 1, nxt);
+      load_k(kb + 2, kl);
+      if (kb < wsteps) {
+        const uint16_t* K = Ks(kb & 1);
+        bf16x8 kf[2][4];
 #pragma unroll
-      for (int f = 0; f < 2; ++f) dq[e][f] = f32x16{};
+        for (int db = 0; db < 4; ++db) kf[0][db] = frag_tr(K, 32 * db, 0);
 #pragma unroll
-    for (int kb = 0; kb < kDqAhead; ++kb) fetch(kb);
-    th_dev::wait_and_meet<4 * (kDqAhead - 1)>();  // block 0 has landed
-    for (int kb = 0; kb < nkb; ++kb) {
-      // Into the stage block kb - 1 used: every wave finished reading it
-      // before the barrier that ended the previous step.
-      fetch(kb + kDqAhead);
-      const int st = kb % kDqStages;
-      bf16x8 bs[2][2], kf[2][2];
+        for (int ks = 0; ks < 4; ++ks) {
+          if (ks + 1 < 4) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+            for (int db = 0; db < 4; ++db) kf[(ks + 1) % 2][db] = frag_tr(K, 32 * db, ks + 1);
+          }
+          const bf16x8 b0 = (bf16x8)cur[2 * ks], b1 = (bf16x8)cur[2 * ks + 1];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          bs[ks][e] = frag_tr(Ds(st), 64 * wj + 32 * e, ks);
-          kf[ks][e] = frag_tr(Ks(st), 64 * wi + 32 * e, ks);
+          for (int db = 0; db < 4; ++db) {
+            mfma_agpr(kf[ks % 2][db], b0, dq0[db]);
+            mfma_agpr(kf[ks % 2][db], b1, dq1[db]);
+          }
         }
-      __builtin_amdgcn_sched_barrier(kFence);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-          for (int f = 0; f < 2; ++f) dq[e][f] = mfma(kf[ks][e], bs[ks][f], dq[e][f]);
-      // Block kb + 1 has landed; blocks kb + 2 .. kb + kDqAhead stay in flight.
-      th_dev::wait_and_meet<4 * (kDqAhead - 1)>();
+      }
+      // Every wave has finished reading stage (kb + 1) % 2 (step kb - 1) before
+      // the barrier that ended the previous step.
+      store_rows(Ks((kb + 1) & 1), kn);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+
+    load_k(0, ka);
+    load_ds(0, dsa);
+    load_k(1, kb4);
+    store_rows(Ks(0), ka);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int kb = 0; kb < nsteps; kb += 2) {
+      step(kb, dsa, dsb, kb4, ka);
+      step(kb + 1, dsb, dsa, ka, kb4);
     }
-    // No load may land in this workgroup's LDS after the sweep.
-    th_dev::wait_and_meet<0>();
-    // Lane holds dQ'(d, query) for query 64 wj + 32 f + lr, d = 64 wi + 32 e + 8 g + 4 lh + (0..3).
+    agpr_settle(dq0, dq1);
+    // dQ leaves as whole rows, and only at the workgroup's end: stores share
+    // the wave's in-order count of memory operations with loads, so a store
+    // before the next pass's loads would hold up every wait in it until the
+    // write is acknowledged (about 70 us over config 4's dQ).  A first pass
+    // keeps its rows in this wave's 16 KB of LDS past the K stages; the last
+    // stages each half (32 queries) in its 8 KB of the K stages, free after
+    // the sweep's last barrier, and stores it and the kept rows.
+    uint16_t* const keep = lds + 2 * kTileElems + wave * (64 * kD);
+    if (live) {
+      if (pass + 1 < npass) {
+        stage_rows(keep, dq0, p.scale);
+        stage_rows(keep + 32 * kD, dq1, p.scale);
+      } else {
+        uint16_t* const stage = lds + wave * (32 * kD);
+        const int64_t row0 = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      uint16_t* out = p.dq + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(qw + 64 * wj + 32 * f + lr) * p.q_ss;
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = 64 * wi + 32 * e + 8 * g + 4 * lh;
-          const float sc = p.scale;
-          *reinterpret_cast<u32x2*>(out + d) = u32x2{pack2(dq[e][f][4 * g] * sc, dq[e][f][4 * g + 1] * sc),
-                                                     pack2(dq[e][f][4 * g + 2] * sc, dq[e][f][4 * g + 3] * sc)};
+        for (int f = 0; f < 2; ++f) {
+          stage_rows(stage, f == 0 ? dq0 : dq1, p.scale);
+          flush_rows(stage, p.dq + row0 + (int64_t)(64 * q64 + 32 * f) * p.q_ss, p.q_ss);
         }
+      }
     }
+    if (pass == 1) {
+      // The first pass's rows: query block blk.x.
+      const int k64 = blk.x * 4 + wave;
+      if (k64 < nq64) {
+        const int64_t row0 = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) flush_rows(keep + 32 * kD * f, p.dq + row0 + (int64_t)(64 * k64 + 32 * f) * p.q_ss, p.q_ss);
+      }
+    }
+    // The next pass refills stage 0 only after every wave is done with it.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }
 
@@ -1152,15 +1211,16 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   const bool store = ds_bytes <= kDsBudget && !(d->flags & TH_ATTN_RECOMPUTE_DQ);
   const uint64_t at_ds = store ? b.workspace((uint64_t)ds_bytes) : 0;
   const void* dkdv = store ? (const void*)attn_bwd_dkdv<true> : (const void*)attn_bwd_dkdv<false>;
-  const void* dqk = store ? (const void*)attn_bwd_dq_ds : (const void*)attn_bwd_dq;
-  const size_t dq_lds = store ? kDqDsLds : kDqLds;
+  const void* dqk = store ? (const void*)attn_bwd_dq_frag : (const void*)attn_bwd_dq;
+  const size_t dq_lds = store ? kDqfLds : kDqLds;
   TH_HIP(hipFuncSetAttribute(dkdv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDkdvLds));
   TH_HIP(hipFuncSetAttribute(dqk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds));
   int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, a);
   int k1 = b.kernel(dkdv, store ? "attn_bwd_dkdv_store" : "attn_bwd_dkdv",
                     dim3(blocks_x(d->seq / kBwdK, d->causal), d->kv_heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
-  int k2 = b.kernel(dqk, store ? "attn_bwd_dq_ds" : "attn_bwd_dq",
-                    dim3(blocks_x(d->seq / kFwdQ, d->causal), d->heads, d->batch), dim3(256), (uint32_t)dq_lds, a);
+  const unsigned dq_blocks = store ? blocks_x((d->seq + kDqfQ - 1) / kDqfQ, d->causal) : blocks_x(d->seq / kFwdQ, d->causal);
+  int k2 = b.kernel(dqk, store ? "attn_bwd_dq_frag" : "attn_bwd_dq", dim3(dq_blocks, d->heads, d->batch), dim3(256),
+                    (uint32_t)dq_lds, a);
   const size_t offs[9] = {TH_OFFSET(AttnArgs, q),   TH_OFFSET(AttnArgs, k),  TH_OFFSET(AttnArgs, v),
                           TH_OFFSET(AttnArgs, o),   TH_OFFSET(AttnArgs, lse), TH_OFFSET(AttnArgs, dout),
                           TH_OFFSET(AttnArgs, dq),  TH_OFFSET(AttnArgs, dk), TH_OFFSET(AttnArgs, dv)};

@@ -114,7 +114,7 @@ def test_backward_both_dq_paths(target, S, causal, recompute):
     fwd = L.attention_fwd(B, H, H, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), causal=causal)
     bwd = L.attention_bwd(B, H, S, ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), ptr(g), ptr(dq), ptr(dk), ptr(dv),
                           causal=causal, recompute_dq=recompute)
-    assert ("attn_bwd_dq<" if recompute else "attn_bwd_dq_ds<") in bwd.describe()
+    assert ("attn_bwd_dq<" if recompute else "attn_bwd_dq_frag<") in bwd.describe()
     fwd()
     bwd()
     torch.cuda.synchronize()
