@@ -632,6 +632,21 @@ def lds_rate(target) -> dict:
     return out
 
 
+def read_rate(target) -> dict:
+    """The HBM read rate on this device (th_read_rate): one workgroup of four
+    waves a CU, eight 1 KB loads in flight a wave, over a 2 MB stream a wave
+    and over the attention dQ sweep's dS' reads at config 4's shape."""
+    import ctypes
+    from tempest_hip import _lib
+    out = {}
+    for mode, name in ((0, "stream_2MB_a_wave"), (1, "dq_sweep_dS_reads")):
+        b = ctypes.c_double()
+        _lib.call("th_read_rate", mode, ctypes.byref(b))
+        out[name] = {"TB/s": b.value / 1e12}
+    log("read rate:", json.dumps(out))
+    return out
+
+
 # The reference's own recorded times (NVIDIA GB10, µs) for the programs
 # reference_benchmarks runs: TRIALS.md:2155-2158 (bf16 attention forward and
 # training step, the later of its records), :2183-2187 (TF32), and
@@ -941,7 +956,7 @@ def main() -> int:
                     help="config 2 alone, no CPU baseline (for counter runs)")
     ap.add_argument("--only", choices=["config1", "config2_floor", "config3", "config4", "config4_recompute",
                                        "config5", "gemm_tiles", "gemm_f32", "dispatch", "attention_head_dims",
-                                       "matrix_rate", "lds_rate", "reference_benchmarks"],
+                                       "matrix_rate", "lds_rate", "read_rate", "reference_benchmarks"],
                     default=None,
                     help="run one other config alone and print its figures (for kernel traces and counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -975,7 +990,8 @@ def main() -> int:
     if a.only:
         fn = {"config1": config1, "config3": config3, "config4": config4, "config5": config5, "gemm_tiles": gemm_tiles,
               "dispatch": dispatch_costs, "gemm_f32": gemm_f32_rows, "attention_head_dims": attention_head_dims,
-              "matrix_rate": matrix_rate, "lds_rate": lds_rate, "reference_benchmarks": reference_benchmarks,
+              "matrix_rate": matrix_rate, "lds_rate": lds_rate, "read_rate": read_rate,
+              "reference_benchmarks": reference_benchmarks,
               "config4_recompute": lambda t: config4(t, recompute_dq=True)}[a.only]
         print(json.dumps({a.only: fn(target)}), flush=True)
         return 0
@@ -1024,6 +1040,10 @@ def main() -> int:
             configs["config4_attention"]["lds_rate"] = lds_rate(target)
         except Exception as err:
             configs["config4_attention"]["lds_rate"] = {"error": repr(err)}
+        try:
+            configs["config4_attention"]["read_rate"] = read_rate(target)
+        except Exception as err:
+            configs["config4_attention"]["read_rate"] = {"error": repr(err)}
         log("config4:", json.dumps(configs["config4_attention"]))
         try:
             configs["attention_head_dims"] = attention_head_dims(target)

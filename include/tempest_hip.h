@@ -246,6 +246,14 @@ int th_matrix_rate(int vary, double* host_flops_per_s, double* host_clock_hz);
  * kernels meet.  No reference counterpart: a device measurement. */
 int th_lds_rate(int mode, int per_cu, double* host_bytes_per_s, double* host_flops_per_s, double* host_clock_hz);
 
+/* The HBM read rate on this device, measured: one workgroup of four waves a
+ * CU, each wave keeping eight 1 KB loads (non-temporal) in flight, over a
+ * 2 MB stream of its own (mode 0) or over the attention dQ sweep's dS' reads
+ * at B 8, H 16, S 4096 (mode 1: causal streams of 8 KB steps, two query
+ * blocks a workgroup).  Bytes/s over five launches.  The ceiling of the dQ
+ * sweep's stream.  No reference counterpart: a device measurement. */
+int th_read_rate(int mode, double* host_bytes_per_s);
+
 /* ---- op class (a): fused pointwise + reductions -------------------------- */
 
 /* Softmax over each contiguous run of n (a column of the reference's n x rows

@@ -256,6 +256,52 @@ __global__ __launch_bounds__(256, 2) void th_lds_rate_kernel(LdsRateArgs a) {
   }
 }
 
+// ---- the HBM read rate -------------------------------------------------------------
+// Waves stream 1 KB wave loads (16 bytes a lane, non-temporal) from a device
+// buffer, eight in flight, one workgroup of four waves a CU (96 KB of LDS
+// requested and unused to hold it there).  Mode 0: each of 4 waves x CUs
+// streams its own contiguous 2 MB.  Mode 1: the attention dQ sweep's dS'
+// reads at B 8, H 16, S 4096 (a 4 GiB array): per (batch, head) 64 streams of
+// 512 KB (64-query blocks); workgroup x of a (head, batch) takes 256-query
+// blocks x and 15 - x, wave w streaming block 4 qb + w over steps 0 ..
+// 4 qb + 3 of 8 KB, clamped to its own diagonal (step q64), the workgroups in
+// XCD-contiguous order.  Every address lies inside the array.
+struct ReadRateArgs {
+  const u32x4* src;
+  uint32_t* sink;  // written only if the reads fold to a value they never do
+  int32_t mode;
+};
+
+__global__ __launch_bounds__(256) void th_read_rate_kernel(ReadRateArgs a) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  uint32_t x = 0;
+  auto consume = [&](const u32x4* q) {
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(q + 64 * u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  };
+  if (a.mode == 0) {
+    const int64_t per = (int64_t)2 * 1024 * 1024 / 16;  // 16-byte units a wave
+    const u32x4* q = a.src + ((int64_t)blockIdx.x * 4 + wave) * per + lane;
+    for (int64_t i = 0; i < per; i += 512) consume(q + i);
+  } else {
+    const int S = 4096, H = 16, nq64 = S / 64, nqb = S / 256;
+    int t = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int total = gridDim.x * gridDim.y * gridDim.z;
+    t = (t % 8) * (total / 8) + t / 8;
+    const int bx = t % gridDim.x, h = (t / gridDim.x) % gridDim.y, b = t / (gridDim.x * gridDim.y);
+    for (int pass = 0; pass < 2; ++pass) {
+      const int qb = pass == 0 ? bx : nqb - 1 - bx;
+      const int q64 = 4 * qb + wave;
+      const u32x4* q = a.src + (((int64_t)b * H + h) * nq64 + q64) * ((int64_t)S * 64 * 2 / 16) + lane;
+      for (int kb = 0; kb < 4 * qb + 4; ++kb) consume(q + (int64_t)min(kb, q64) * 512);
+    }
+  }
+  if (x == 0x12345678u) a.sink[blockIdx.x] = x;
+}
+
 extern "C" {
 
 const char* th_last_error(void) { return g_error.c_str(); }
@@ -1163,6 +1209,58 @@ int th_lds_rate(int mode, int per_cu, double* bytes_per_s, double* flops_per_s, 
   const double reads = (double)blocks * 4 * 8 * iters;  // wave reads of 1 KB
   *bytes_per_s = reads * 1024.0 / (ms * 1e-3);
   *flops_per_s = mode >= 2 ? reads * 32768.0 / (ms * 1e-3) : 0.0;
+  return done(TH_OK);
+}
+
+int th_read_rate(int mode, double* bytes_per_s) {
+  if (int r = require_ready()) return r;
+  TH_REQUIRE(bytes_per_s, "th_read_rate: null output");
+  TH_REQUIRE(mode == 0 || mode == 1, "th_read_rate: mode must be 0 (a 2 MB stream a wave) or 1 (the dQ sweep's dS' reads)");
+  std::lock_guard<std::mutex> lock(g_timing);
+  Context& c = ctx();
+  const int cus = c.prop.multiProcessorCount;
+  // Mode 1's array is B 8 x H 16 x S^2 bf16 (4 GiB); mode 0's one 2 MB stream a wave.
+  const size_t bytes = mode == 1 ? (size_t)8 * 16 * 4096 * 4096 * 2 : (size_t)cus * 4 * 2 * 1024 * 1024;
+  void* src = nullptr;
+  void* sink = nullptr;
+  if (int r = device_alloc(bytes, &src)) return r;
+  if (int r = device_alloc(4096 * sizeof(uint32_t), &sink)) {
+    (void)hipFree(src);
+    return r;
+  }
+  auto done = [&](int r) {
+    (void)hipStreamSynchronize(c.stream);
+    (void)hipFree(src);
+    (void)hipFree(sink);
+    return r;
+  };
+  ReadRateArgs a{static_cast<const u32x4*>(src), static_cast<uint32_t*>(sink), mode};
+  const dim3 grid = mode == 1 ? dim3(8, 16, 8) : dim3(cus);
+  const size_t lds = 96 * 1024;  // one workgroup a CU
+  TH_HIP(hipFuncSetAttribute((const void*)th_read_rate_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  // Bytes read: mode 0 the whole array; mode 1, per (batch, head), four waves
+  // of each workgroup x read (4 x + 4) + (4 (15 - x) + 4) steps of 8 KB.
+  double read = (double)bytes;
+  if (mode == 1) {
+    read = 0;
+    for (int x = 0; x < 8; ++x) read += 4.0 * ((4 * x + 4) + (4 * (15 - x) + 4)) * 8192;
+    read *= 8 * 16;
+  }
+  void* params[] = {&a};
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_read_rate: events"));
+  if (hipLaunchKernel((const void*)th_read_rate_kernel, grid, dim3(256), params, lds, c.stream) != hipSuccess)
+    return done(fail(TH_E_STATE, "th_read_rate: launch failed"));
+  (void)hipEventRecord(e0, c.stream);
+  for (int r = 0; r < 5; ++r) (void)hipLaunchKernel((const void*)th_read_rate_kernel, grid, dim3(256), params, lds, c.stream);
+  (void)hipEventRecord(e1, c.stream);
+  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_read_rate: run failed"));
+  float ms = 0;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *bytes_per_s = 5.0 * read / (ms * 1e-3);
   return done(TH_OK);
 }
 

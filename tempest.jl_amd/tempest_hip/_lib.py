@@ -134,6 +134,7 @@ SIGNATURES: dict[str, list] = {
     "th_build_copy": [c_void_p, c_void_p, c_u64, P(c_void_p)],
     "th_matrix_rate": [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_double)],
     "th_lds_rate": [ctypes.c_int, ctypes.c_int, P(ctypes.c_double), P(ctypes.c_double), P(ctypes.c_double)],
+    "th_read_rate": [ctypes.c_int, P(ctypes.c_double)],
     "th_arena_create": [P(c_u64), c_int, c_u64, P(c_void_p)],
     "th_arena_slot": [c_void_p, c_int, P(c_void_p)],
     "th_arena_bytes": [c_void_p, P(c_u64)],

@@ -150,6 +150,20 @@ def test_timing_and_rates(target):
     assert w.bytes == 3 * 4 * 1024 * 4096 and w.kernels == 2
 
 
+def test_read_rate_measures_streams(target):
+    """th_read_rate: both read patterns stream at a physical rate (between 1 and
+    8.2 TB/s, HBM3E's 8 TB/s with its rounding); a bad mode is refused."""
+    import ctypes
+    from tempest_hip import _lib
+    announce("read rate")
+    for mode in (0, 1):
+        b = ctypes.c_double()
+        _lib.call("th_read_rate", mode, ctypes.byref(b))
+        assert 1e12 < b.value < 8.2e12, (mode, b.value)
+    with pytest.raises(_lib.HIPError):
+        _lib.call("th_read_rate", 2, ctypes.byref(ctypes.c_double()))
+
+
 def test_lds_rate_measures_reads_and_products(target):
     import ctypes
     from tempest_hip import _lib
