@@ -361,7 +361,7 @@ def config1(target):
                     "compiled call: host wall time of c(w, b, x) incl. result copies and the loss read"}
 
 
-def config3(target, steps: int = 5, warmup: int = 2):
+def config3(target, steps: int = 20, warmup: int = 10):
     """The 2-layer MLP's gradient at 4096 / 16384 / 4096, batch 4096, bf16:
     six products, 3.299e12 flops a step."""
     import torch
@@ -404,7 +404,7 @@ def config3(target, steps: int = 5, warmup: int = 2):
             "dispatch": graph_vs_direct(target, ex, steps)}
 
 
-def config4(target, steps: int = 3, warmup: int = 1, recompute_dq: bool = False):
+def config4(target, steps: int = 10, warmup: int = 5, recompute_dq: bool = False):
     """Causal attention fwd+bwd, B8 H16 S4096 D128 bf16: 1.924e12 flops a step
     (forward 4 B H S^2 D / 2, backward 2.5x that).  recompute_dq: the
     backward's dQ sweep recomputes S and dP rather than reading stored dS'."""
@@ -559,7 +559,7 @@ def gemm_f32_rows(target, runs: int = 20):
     return out
 
 
-def config5(target, steps: int = 3, warmup: int = 1):
+def config5(target, steps: int = 10, warmup: int = 5):
     """Chunked gated DeltaNet forward + gradient, B4 H16 T8192, d 128, chunk 64."""
     import torch
     import tempest_hip as th
