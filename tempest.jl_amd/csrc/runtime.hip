@@ -913,6 +913,31 @@ static int clear_cache() {
 // read 16 times over in one launch of the clearing kernel, the best of 5
 // launches after one, once per process.  The reference takes twice the
 // memory's rate for it (ext/CUDAExt.jl:908-921); this is the device's own.
+// Timing events, destroyed with the scope, so that every early return
+// (TH_HIP's included) releases them; an event still pending on the stream
+// is released by HIP once it completes.
+struct Events {
+  std::vector<hipEvent_t> e;
+  explicit Events(size_t n) : e(n, nullptr) {}
+  hipError_t create() {
+    for (auto& x : e) {
+      const hipError_t r = hipEventCreate(&x);
+      if (r != hipSuccess) {
+        x = nullptr;
+        return r;
+      }
+    }
+    return hipSuccess;
+  }
+  ~Events() {
+    for (hipEvent_t x : e)
+      if (x) (void)hipEventDestroy(x);
+  }
+  hipEvent_t operator[](size_t i) const { return e[i]; }
+  Events(const Events&) = delete;
+  Events& operator=(const Events&) = delete;
+};
+
 static int cached_rate(double* out) {
   Context& c = ctx();
   if (c.cached_rate < 0) {
@@ -922,8 +947,8 @@ static int cached_rate(double* out) {
     int blocks = c.prop.multiProcessorCount * 8;
     hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
     TH_HIP(hipGetLastError());
-    hipEvent_t ev[6];
-    for (auto& e : ev) TH_HIP(hipEventCreate(&e));
+    Events ev(6);
+    TH_HIP(ev.create());
     TH_HIP(hipEventRecord(ev[0], c.stream));
     for (int i = 0; i < 5; ++i) {
       hipLaunchKernelGGL(th_clear_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
@@ -937,7 +962,6 @@ static int cached_rate(double* out) {
       TH_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
       best = std::min(best, ms);
     }
-    for (auto& e : ev) TH_HIP(hipEventDestroy(e));
     c.cached_rate = (double)passes * bytes / (best * 1e-3);
   }
   *out = c.cached_rate;
@@ -948,22 +972,21 @@ static int cached_rate(double* out) {
 // (cleared, ext/CUDAExt.jl:821-833).
 static int cleared(th_graph* g, int samples, double* out) {
   Context& c = ctx();
-  std::vector<hipEvent_t> ev(2 * samples);
-  for (auto& e : ev) TH_HIP(hipEventCreate(&e));
+  Events ev(2 * samples);
+  TH_HIP(ev.create());
   for (int i = 0; i < samples; ++i) {
     if (int r = clear_cache()) return r;
     TH_HIP(hipEventRecord(ev[2 * i], c.stream));
     TH_HIP(hipGraphLaunch(g->exec, c.stream));
     TH_HIP(hipEventRecord(ev[2 * i + 1], c.stream));
   }
-  TH_HIP(hipEventSynchronize(ev.back()));
+  TH_HIP(hipEventSynchronize(ev[2 * samples - 1]));
   float best = 1e30f;
   for (int i = 0; i < samples; ++i) {
     float ms = 0;
     TH_HIP(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
     best = std::min(best, ms);
   }
-  for (auto& e : ev) TH_HIP(hipEventDestroy(e));
   *out = best * 1e-3;
   return TH_OK;
 }
@@ -971,17 +994,15 @@ static int cleared(th_graph* g, int samples, double* out) {
 static int mean_replay(th_graph* g, int warmup, int reps, double* out) {
   Context& c = ctx();
   for (int i = 0; i < warmup; ++i) TH_HIP(hipGraphLaunch(g->exec, c.stream));
-  hipEvent_t a, b;
-  TH_HIP(hipEventCreate(&a));
-  TH_HIP(hipEventCreate(&b));
+  Events ab(2);
+  TH_HIP(ab.create());
+  const hipEvent_t a = ab[0], b = ab[1];
   TH_HIP(hipEventRecord(a, c.stream));
   for (int i = 0; i < reps; ++i) TH_HIP(hipGraphLaunch(g->exec, c.stream));
   TH_HIP(hipEventRecord(b, c.stream));
   TH_HIP(hipEventSynchronize(b));
   float ms = 0;
   TH_HIP(hipEventElapsedTime(&ms, a, b));
-  TH_HIP(hipEventDestroy(a));
-  TH_HIP(hipEventDestroy(b));
   *out = ms * 1e-3 / std::max(reps, 1);
   return TH_OK;
 }
@@ -1033,9 +1054,9 @@ static int replay_overhead(double* out) {
   c.graph_base = std::max(0.0, t_one - c.launch_gap);
   for (int i = 0; i < 5; ++i)
     if ((r = launch_kernel(blank.kernels[0], c.stream))) return r;
-  hipEvent_t a, b;
-  TH_HIP(hipEventCreate(&a));
-  TH_HIP(hipEventCreate(&b));
+  Events ab(2);
+  TH_HIP(ab.create());
+  const hipEvent_t a = ab[0], b = ab[1];
   TH_HIP(hipEventRecord(a, c.stream));
   for (int i = 0; i < 200; ++i)
     if ((r = launch_kernel(blank.kernels[0], c.stream))) return r;
@@ -1043,8 +1064,6 @@ static int replay_overhead(double* out) {
   TH_HIP(hipEventSynchronize(b));
   float ms = 0;
   TH_HIP(hipEventElapsedTime(&ms, a, b));
-  TH_HIP(hipEventDestroy(a));
-  TH_HIP(hipEventDestroy(b));
   c.direct_gap = ms * 1e-3 / 200;
   *out = c.replay_overhead;
   return TH_OK;
@@ -1136,18 +1155,15 @@ int th_matrix_rate(int vary, double* flops_per_s, double* clock_hz) {
   const int iters = 20000;
   RateArgs a{static_cast<const u32x4*>(seed), static_cast<float*>(sink), static_cast<uint64_t*>(stamps), iters,
              vary ? 1 : 0};
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
-    return done(fail(TH_E_STATE, "th_matrix_rate: events"));
+  Events ev(2);
+  if (ev.create() != hipSuccess) return done(fail(TH_E_STATE, "th_matrix_rate: events"));
   hipLaunchKernelGGL(th_matrix_rate_kernel, dim3(blocks), dim3(256), 0, c.stream, a);  // warm up the clocks
-  (void)hipEventRecord(e0, c.stream);
+  (void)hipEventRecord(ev[0], c.stream);
   hipLaunchKernelGGL(th_matrix_rate_kernel, dim3(blocks), dim3(256), 0, c.stream, a);
-  (void)hipEventRecord(e1, c.stream);
-  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_matrix_rate: run failed"));
+  (void)hipEventRecord(ev[1], c.stream);
+  if (hipEventSynchronize(ev[1]) != hipSuccess) return done(fail(TH_E_STATE, "th_matrix_rate: run failed"));
   float ms = 0;
-  (void)hipEventElapsedTime(&ms, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  (void)hipEventElapsedTime(&ms, ev[0], ev[1]);
   std::vector<uint64_t> st(blocks * 4);
   if (hipMemcpy(st.data(), stamps, st.size() * 8, hipMemcpyDeviceToHost) != hipSuccess)
     return done(fail(TH_E_STATE, "th_matrix_rate: stamps"));
@@ -1186,20 +1202,17 @@ int th_lds_rate(int mode, int per_cu, double* bytes_per_s, double* flops_per_s, 
                 : mode == 2 ? (const void*)th_lds_rate_kernel<2>
                             : (const void*)th_lds_rate_kernel<3>;
   void* params[] = {&a};
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
-    return done(fail(TH_E_STATE, "th_lds_rate: events"));
+  Events ev(2);
+  if (ev.create() != hipSuccess) return done(fail(TH_E_STATE, "th_lds_rate: events"));
   // Warm up the clocks, then time the second launch.
   if (hipLaunchKernel(k, dim3(blocks), dim3(256), params, 0, c.stream) != hipSuccess)
     return done(fail(TH_E_STATE, "th_lds_rate: launch failed"));
-  (void)hipEventRecord(e0, c.stream);
+  (void)hipEventRecord(ev[0], c.stream);
   (void)hipLaunchKernel(k, dim3(blocks), dim3(256), params, 0, c.stream);
-  (void)hipEventRecord(e1, c.stream);
-  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_lds_rate: run failed"));
+  (void)hipEventRecord(ev[1], c.stream);
+  if (hipEventSynchronize(ev[1]) != hipSuccess) return done(fail(TH_E_STATE, "th_lds_rate: run failed"));
   float ms = 0;
-  (void)hipEventElapsedTime(&ms, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  (void)hipEventElapsedTime(&ms, ev[0], ev[1]);
   std::vector<uint64_t> st(blocks * 4);
   if (hipMemcpy(st.data(), stamps, st.size() * 8, hipMemcpyDeviceToHost) != hipSuccess)
     return done(fail(TH_E_STATE, "th_lds_rate: stamps"));
@@ -1221,6 +1234,8 @@ int th_read_rate(int mode, double* bytes_per_s) {
   const int cus = c.prop.multiProcessorCount;
   // Mode 1's array is B 8 x H 16 x S^2 bf16 (4 GiB); mode 0's one 2 MB stream a wave.
   const size_t bytes = mode == 1 ? (size_t)8 * 16 * 4096 * 4096 * 2 : (size_t)cus * 4 * 2 * 1024 * 1024;
+  const size_t lds = 96 * 1024;  // one workgroup a CU
+  TH_HIP(hipFuncSetAttribute((const void*)th_read_rate_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   void* src = nullptr;
   void* sink = nullptr;
   if (int r = device_alloc(bytes, &src)) return r;
@@ -1236,8 +1251,6 @@ int th_read_rate(int mode, double* bytes_per_s) {
   };
   ReadRateArgs a{static_cast<const u32x4*>(src), static_cast<uint32_t*>(sink), mode};
   const dim3 grid = mode == 1 ? dim3(8, 16, 8) : dim3(cus);
-  const size_t lds = 96 * 1024;  // one workgroup a CU
-  TH_HIP(hipFuncSetAttribute((const void*)th_read_rate_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   // Bytes read: mode 0 the whole array; mode 1, per (batch, head), four waves
   // of each workgroup x read (4 x + 4) + (4 (15 - x) + 4) steps of 8 KB.
   double read = (double)bytes;
@@ -1247,19 +1260,16 @@ int th_read_rate(int mode, double* bytes_per_s) {
     read *= 8 * 16;
   }
   void* params[] = {&a};
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
-    return done(fail(TH_E_STATE, "th_read_rate: events"));
+  Events ev(2);
+  if (ev.create() != hipSuccess) return done(fail(TH_E_STATE, "th_read_rate: events"));
   if (hipLaunchKernel((const void*)th_read_rate_kernel, grid, dim3(256), params, lds, c.stream) != hipSuccess)
     return done(fail(TH_E_STATE, "th_read_rate: launch failed"));
-  (void)hipEventRecord(e0, c.stream);
+  (void)hipEventRecord(ev[0], c.stream);
   for (int r = 0; r < 5; ++r) (void)hipLaunchKernel((const void*)th_read_rate_kernel, grid, dim3(256), params, lds, c.stream);
-  (void)hipEventRecord(e1, c.stream);
-  if (hipEventSynchronize(e1) != hipSuccess) return done(fail(TH_E_STATE, "th_read_rate: run failed"));
+  (void)hipEventRecord(ev[1], c.stream);
+  if (hipEventSynchronize(ev[1]) != hipSuccess) return done(fail(TH_E_STATE, "th_read_rate: run failed"));
   float ms = 0;
-  (void)hipEventElapsedTime(&ms, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  (void)hipEventElapsedTime(&ms, ev[0], ev[1]);
   *bytes_per_s = 5.0 * read / (ms * 1e-3);
   return done(TH_OK);
 }
@@ -1280,9 +1290,9 @@ int th_time_run(th_launch* l, int warmup, int reps, double* seconds) {
   Context& c = ctx();
   for (int i = 0; i < warmup; ++i)
     if (int r = th_launch_run(l)) return r;
-  hipEvent_t a, b;
-  TH_HIP(hipEventCreate(&a));
-  TH_HIP(hipEventCreate(&b));
+  Events ab(2);
+  TH_HIP(ab.create());
+  const hipEvent_t a = ab[0], b = ab[1];
   TH_HIP(hipEventRecord(a, c.stream));
   for (int i = 0; i < reps; ++i)
     if (int r = th_launch_run(l)) return r;
@@ -1290,8 +1300,6 @@ int th_time_run(th_launch* l, int warmup, int reps, double* seconds) {
   TH_HIP(hipEventSynchronize(b));
   float ms = 0;
   TH_HIP(hipEventElapsedTime(&ms, a, b));
-  TH_HIP(hipEventDestroy(a));
-  TH_HIP(hipEventDestroy(b));
   *seconds = ms * 1e-3 / reps;
   return TH_OK;
 }
