@@ -443,32 +443,58 @@ __global__ __launch_bounds__(256, 2) void attn_fwd(AttnArgs p) {
 
 // ---- backward: delta = rowsum(dO .* O) -------------------------------------------
 
+constexpr int kDeltaRows = 4;  // rows per sixteen lanes
+
 __global__ __launch_bounds__(256) void attn_bwd_delta(AttnArgs p) {
-  // Sixteen lanes per (query, head, batch) row of 128, 16 bytes each; 16 rows per workgroup.
-  const int64_t row = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
-  const int64_t total = (int64_t)p.batch * p.seq * p.heads;
+  // Sixteen lanes per (query, head, batch) row of 128, 16 bytes each; the
+  // sixteen lanes of group g take rows g + 16 i (i < kDeltaRows) of the
+  // workgroup's 64, every load issued before the first product, so that a
+  // wave has 8 KB in flight (with one row each it had 2 KB, and streamed at
+  // 5 TB/s).  Rows are (batch, position, head) with the head fastest, so each
+  // load instruction covers sixteen consecutive rows.  Row numbers fit 32
+  // bits (the builder checks).
+  const uint32_t total = (uint32_t)p.batch * p.seq * p.heads;
   const int part = threadIdx.x % 16;
-  float v = 0.0f;
-  int64_t b = 0, s = 0;
-  int h = 0;
-  if (row < total) {
-    h = (int)(row % p.heads);
-    s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
-    const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss + 8 * part;
-    const u32x4 ow = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.o + at));
-    const u32x4 gw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.dout + at));
+  const uint32_t row0 = blockIdx.x * (16 * kDeltaRows) + threadIdx.x / 16;
+  struct Pos {
+    int64_t b, s;
+    int h;
+  };
+  auto pos = [&](uint32_t row) {
+    const uint32_t bs = row / (uint32_t)p.heads;
+    return Pos{bs / (uint32_t)p.seq, bs % (uint32_t)p.seq, (int)(row - bs * (uint32_t)p.heads)};
+  };
+  u32x4 ow[kDeltaRows], gw[kDeltaRows];
+  float lse[kDeltaRows];
+#pragma unroll
+  for (int i = 0; i < kDeltaRows; ++i) {
+    // Rows past the end re-read the last one; nothing is written for them.
+    const Pos q = pos(min(row0 + 16 * i, total - 1));
+    const int64_t at = q.b * p.q_sb + q.h * p.q_sh + q.s * p.q_ss + 8 * part;
+    ow[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.o + at));
+    gw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.dout + at));
+    lse[i] = p.lse[(q.b * p.seq + q.s) * p.heads + q.h];
+  }
+  // Every load out before any of their data is used (the scheduler would
+  // otherwise start on the first row and wait for it before the next loads).
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kDeltaRows; ++i) {
+    float v = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      v += bf16_float((uint16_t)ow[e]) * bf16_float((uint16_t)gw[e]) +
-           bf16_float((uint16_t)(ow[e] >> 16)) * bf16_float((uint16_t)(gw[e] >> 16));
-  }
+      v += bf16_float((uint16_t)ow[i][e]) * bf16_float((uint16_t)gw[i][e]) +
+           bf16_float((uint16_t)(ow[i][e] >> 16)) * bf16_float((uint16_t)(gw[i][e] >> 16));
 #pragma unroll
-  for (int m = 8; m >= 1; m /= 2) v += __shfl_xor(v, m, 16);
-  if (row < total && part == 0) {
-    p.delta[(b * p.seq + s) * p.heads + h] = v;
-    const int64_t at = (((int64_t)b * p.heads + h) * (p.seq / 64) + s / 64) * 128 + s % 64;
-    p.stat[at] = p.lse[(b * p.seq + s) * p.heads + h] * (-1.0f / p.scale);
-    p.stat[at + 64] = -v;
+    for (int m = 8; m >= 1; m /= 2) v += __shfl_xor(v, m, 16);
+    const uint32_t row = row0 + 16 * i;
+    if (row < total && part == 0) {
+      const Pos q = pos(row);
+      p.delta[(q.b * p.seq + q.s) * p.heads + q.h] = v;
+      const int64_t at = ((q.b * p.heads + q.h) * (p.seq / 64) + q.s / 64) * 128 + q.s % 64;
+      p.stat[at] = lse[i] * (-1.0f / p.scale);
+      p.stat[at + 64] = -v;
+    }
   }
 }
 
@@ -1215,7 +1241,9 @@ extern "C" int th_build_attention_bwd(const th_attention_desc* d, th_launch** ou
   const size_t dq_lds = store ? kDqfLds : kDqLds;
   TH_HIP(hipFuncSetAttribute(dkdv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDkdvLds));
   TH_HIP(hipFuncSetAttribute(dqk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds));
-  int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, a);
+  TH_REQUIRE(rows < 2147483648LL, "attention: batch x seq x heads must be under 2^31");
+  int k0 = b.kernel((const void*)attn_bwd_delta, "attn_bwd_delta", dim3((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows))),
+                    dim3(256), 0, a);
   int k1 = b.kernel(dkdv, store ? "attn_bwd_dkdv_store" : "attn_bwd_dkdv",
                     dim3(blocks_x(d->seq / kBwdK, d->causal), d->kv_heads, d->batch), dim3(256), (uint32_t)kDkdvLds, a);
   const unsigned dq_blocks = store ? blocks_x((d->seq + kDqfQ - 1) / kDqfQ, d->causal) : blocks_x(d->seq / kFwdQ, d->causal);
