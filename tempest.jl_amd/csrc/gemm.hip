@@ -28,9 +28,7 @@ struct RowSumArgs {
 __global__ __launch_bounds__(256) void sum_parts(RowSumArgs a) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= a.m) return;
-  float s = 0.0f;
-  for (int p = 0; p < a.parts; ++p) s += a.partial[(int64_t)p * a.m + i];
-  a.out[i] = bf16_bits(s);
+  a.out[i] = bf16_bits(thd::sum_in_order(a.partial + i, a.m, a.parts));
 }
 
 struct LossArgs {
@@ -68,9 +66,7 @@ __global__ __launch_bounds__(256) void sum_splits(ReduceArgs a) {
   if (e >= mn) return;
   const int64_t z = blockIdx.y;
   const int64_t i = e % a.m, j = e / a.m;
-  const float* w = a.ws + z * a.splits * mn + e;
-  float v = 0.0f;
-  for (int s = 0; s < a.splits; ++s) v += w[s * mn];
+  float v = thd::sum_in_order(a.ws + z * a.splits * mn + e, mn, a.splits);
   if (a.bias) v += bf16_float(a.bias[i]);
   const int64_t at_d = z * a.d_batch + i + j * a.d_ld, at = z * a.c_batch + i + j * a.c_ld;
   if (a.c_dtype == TH_F32) {

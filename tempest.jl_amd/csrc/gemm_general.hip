@@ -468,9 +468,7 @@ __global__ __launch_bounds__(256) void gemm_f32_sum_parts(F32SumArgs a) {
   if (e >= mn) return;
   const int64_t z = blockIdx.y;
   const int64_t i = e % a.m, j = e / a.m;
-  const float* w = a.ws + z * a.parts * mn + e;
-  float v = 0.0f;
-  for (int s = 0; s < a.parts; ++s) v += w[s * mn];
+  float v = thd::sum_in_order(a.ws + z * a.parts * mn + e, mn, a.parts);
   if (a.d) v += a.d[z * a.d_batch + i + j * a.d_ld];
   a.c[z * a.c_batch + i + j * a.c_ld] = v;
 }

@@ -237,6 +237,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// x[0] + x[stride] + ... + x[(n - 1) stride], added in that order, the loads
+// issued eight at a time: a loop of one load and its add waits a memory round
+// trip per term.
+__device__ __forceinline__ float sum_in_order(const float* x, int64_t stride, int n) {
+  float s = 0.0f;
+  int k = 0;
+  for (; k + 8 <= n; k += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x[(int64_t)(k + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; k < n; ++k) s += x[(int64_t)k * stride];
+  return s;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
