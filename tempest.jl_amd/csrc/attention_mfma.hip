@@ -346,8 +346,8 @@ __global__ __launch_bounds__(256) void mfma_attn_sum(SumArgs a) {
   if (t >= rows * quads) return;
   const int64_t row = t / quads;
   const int c = 4 * (int)(t % quads);
-  f32x4 acc = {};
-  for (int s = 0; s < a.nsplit; ++s) acc += *reinterpret_cast<const f32x4*>(a.part + (s * rows + row) * a.d + c);
+  // Part s of this quad at a.part + (s rows + row) d + c: a stride of rows d / 4 quads.
+  f32x4 acc = thd::sum_in_order(reinterpret_cast<const f32x4*>(a.part + row * a.d + c), rows * a.d / 4, a.nsplit);
   acc *= a.scale;
   const int h = (int)(row % a.heads);
   const int64_t pos = (row / a.heads) % a.positions, b = row / ((int64_t)a.heads * a.positions);

@@ -237,14 +237,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// x[0] + x[stride] + ... + x[(n - 1) stride], added in that order, the loads
-// issued eight at a time: a loop of one load and its add waits a memory round
-// trip per term.
-__device__ __forceinline__ float sum_in_order(const float* x, int64_t stride, int n) {
-  float s = 0.0f;
+// x[0] + x[stride] + ... + x[(n - 1) stride] (T a float or a float vector,
+// stride in elements of T), added in that order, the loads issued eight at a
+// time: a loop of one load and its add waits a memory round trip per term.
+template <class T>
+__device__ __forceinline__ T sum_in_order(const T* x, int64_t stride, int n) {
+  T s = {};
   int k = 0;
   for (; k + 8 <= n; k += 8) {
-    float v[8];
+    T v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) v[u] = x[(int64_t)(k + u) * stride];
 #pragma unroll
