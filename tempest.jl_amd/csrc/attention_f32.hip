@@ -371,18 +371,46 @@ struct FDeltaArgs {
   int32_t d;
 };
 
+// D / 4 lanes per (batch, position, head) row, 16 bytes each (the path takes
+// strides in multiples of 4 and 16-byte bases); each lane group takes
+// kDeltaRowsF rows, 64 / (D / 4) apart, every load issued before the first
+// product.  Rows are numbered with the head fastest, so a load instruction
+// covers consecutive rows; row numbers fit 32 bits (the builder checks).
+constexpr int kDeltaRowsF = 4;
+
+template <int D>
 __global__ __launch_bounds__(256) void f32_attn_delta(FDeltaArgs a) {
+  constexpr int G = D / 4;   // lanes a row
+  constexpr int R = 64 / G;  // rows a wave covers at once
   const FArgs& p = a.p;
-  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;  // [b][s][h]
-  const int64_t total = (int64_t)p.batch * p.seq * p.heads;
-  if (row >= total) return;
-  const int h = (int)(row % p.heads);
-  const int64_t s = (row / p.heads) % p.seq, b = row / ((int64_t)p.heads * p.seq);
-  const int64_t at = b * p.q_sb + h * p.q_sh + s * p.q_ss;
-  float v = 0.0f;
-  for (int c = threadIdx.x % 64; c < a.d; c += 64) v += p.o[at + c] * p.dout[at + c];
-  v = thd::wave_sum(v);
-  if (threadIdx.x % 64 == 0) p.delta[row] = v;
+  const uint32_t total = (uint32_t)p.batch * p.seq * p.heads;
+  const int lane = threadIdx.x % 64, part = lane % G;
+  const uint32_t row0 = (blockIdx.x * 4 + threadIdx.x / 64) * (R * kDeltaRowsF) + lane / G;
+  auto at_of = [&](uint32_t row) {
+    const uint32_t bs = row / (uint32_t)p.heads;
+    const int64_t b = bs / (uint32_t)p.seq, s = bs % (uint32_t)p.seq, h = row - bs * (uint32_t)p.heads;
+    return b * p.q_sb + h * p.q_sh + s * p.q_ss + 4 * part;
+  };
+  f32x4 ov[kDeltaRowsF], gv[kDeltaRowsF];
+#pragma unroll
+  for (int i = 0; i < kDeltaRowsF; ++i) {
+    // Rows past the end re-read the last one; nothing is written for them.
+    const int64_t at = at_of(min(row0 + R * i, total - 1));
+    ov[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.o + at));
+    gv[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.dout + at));
+  }
+  // Every load out before any of their data is used.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kDeltaRowsF; ++i) {
+    float v = ov[i][0] * gv[i][0];
+#pragma unroll
+    for (int e = 1; e < 4; ++e) v += ov[i][e] * gv[i][e];
+#pragma unroll
+    for (int m = G / 2; m >= 1; m /= 2) v += __shfl_xor(v, m, G);
+    const uint32_t row = row0 + R * i;
+    if (row < total && part == 0) p.delta[row] = v;
+  }
 }
 
 // ---- backward: dK, dV ----------------------------------------------------------------
@@ -682,8 +710,10 @@ int bwd_launch(const th_attention_desc* d, th_launch** out) {
   FArgs akv = a, aq = a;
   akv.nsplit = skv.n, akv.span = skv.span;
   aq.nsplit = sq.n, aq.span = sq.span;
-  int k0 = b.kernel((const void*)f32_attn_delta, "f32_attn_delta", dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                    FDeltaArgs{a, D});
+  TH_REQUIRE(rows < 2147483648LL, "attention: batch x seq x heads must be under 2^31");
+  constexpr int kDeltaBlockRows = 4 * (64 / (D / 4)) * kDeltaRowsF;  // rows a workgroup
+  int k0 = b.kernel((const void*)f32_attn_delta<D>, "f32_attn_delta",
+                    dim3((unsigned)((rows + kDeltaBlockRows - 1) / kDeltaBlockRows)), dim3(256), 0, FDeltaArgs{a, D});
   const dim3 gkv = skv.n > 1 ? dim3(nkb, d->kv_heads, d->batch * skv.n) : dim3(blocks_of(a.kv_seq, d->causal), d->kv_heads, d->batch);
   const dim3 gq = sq.n > 1 ? dim3(nqb, d->heads, d->batch * sq.n) : dim3(blocks_of(d->seq, d->causal), d->heads, d->batch);
   int k1 = b.kernel((const void*)f32_attn_dkdv<D>, D == 64 ? "f32_attn_dkdv_d64" : "f32_attn_dkdv_d128", gkv,
