@@ -952,8 +952,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(AttnArgs p) {
 // row and stored 4 rows an instruction (flush_rows).  Scattered 8-byte stores
 // of the same rows (two lanes a row, 32 rows an instruction) measured 15 us
 // more for config 4's dQ.
-__device__ __forceinline__ void stage_rows(uint16_t* stage, const f32x16 (&acc)[4], float sc) {
-  const int lane = threadIdx.x % 64, lr = lane % 32, lh = lane / 32;
+// `lane` is threadIdx.x % 64, passed in so that a caller can make it opaque
+// after its sweep (keeping this address arithmetic out of the sweep).
+__device__ __forceinline__ void stage_rows(uint16_t* stage, const f32x16 (&acc)[4], float sc, int lane) {
+  const int lr = lane % 32, lh = lane / 32;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -964,8 +966,7 @@ __device__ __forceinline__ void stage_rows(uint16_t* stage, const f32x16 (&acc)[
     }
 }
 
-__device__ __forceinline__ void flush_rows(const uint16_t* stage, uint16_t* out, int64_t rs) {
-  const int lane = threadIdx.x % 64;
+__device__ __forceinline__ void flush_rows(const uint16_t* stage, uint16_t* out, int64_t rs, int lane) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int r = 4 * i + lane / 16, c = lane % 16;
@@ -1074,6 +1075,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_frag(AttnArgs p) {
       step(kb + 1, dsb, dsa, ka, kb4);
     }
     agpr_settle(dq0, dq1);
+    int el = lane;
+    asm volatile("" : "+v"(el));  // the epilogue's addresses from here, not hoisted above the sweep
     // dQ leaves as whole rows, and only at the workgroup's end: stores share
     // the wave's in-order count of memory operations with loads, so a store
     // before the next pass's loads would hold up every wait in it until the
@@ -1084,15 +1087,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_frag(AttnArgs p) {
     uint16_t* const keep = lds + 2 * kTileElems + wave * (64 * kD);
     if (live) {
       if (pass + 1 < npass) {
-        stage_rows(keep, dq0, p.scale);
-        stage_rows(keep + 32 * kD, dq1, p.scale);
+        stage_rows(keep, dq0, p.scale, el);
+        stage_rows(keep + 32 * kD, dq1, p.scale, el);
       } else {
         uint16_t* const stage = lds + wave * (32 * kD);
         const int64_t row0 = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
 #pragma unroll
         for (int f = 0; f < 2; ++f) {
-          stage_rows(stage, f == 0 ? dq0 : dq1, p.scale);
-          flush_rows(stage, p.dq + row0 + (int64_t)(64 * q64 + 32 * f) * p.q_ss, p.q_ss);
+          stage_rows(stage, f == 0 ? dq0 : dq1, p.scale, el);
+          flush_rows(stage, p.dq + row0 + (int64_t)(64 * q64 + 32 * f) * p.q_ss, p.q_ss, el);
         }
       }
     }
@@ -1102,7 +1105,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_frag(AttnArgs p) {
       if (k64 < nq64) {
         const int64_t row0 = (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
 #pragma unroll
-        for (int f = 0; f < 2; ++f) flush_rows(keep + 32 * kD * f, p.dq + row0 + (int64_t)(64 * k64 + 32 * f) * p.q_ss, p.q_ss);
+        for (int f = 0; f < 2; ++f)
+          flush_rows(keep + 32 * kD * f, p.dq + row0 + (int64_t)(64 * k64 + 32 * f) * p.q_ss, p.q_ss, el);
       }
     }
     // The next pass refills stage 0 only after every wave is done with it.
